@@ -1,0 +1,180 @@
+/*
+ * memfast_hip.h -- C ABI of the MI355X (gfx950) sliced analog matrix engine.
+ *
+ * This library replaces the reference's accelerator backend, memfast/cuda.py
+ * (NVRTC-compiled memfast/kernels.cu loaded through ctypes).  The reference
+ * binds its backend with ctypes from Python; the drop-in binding of these
+ * entry points is memfast_amd/hip.py (also ctypes), see INTEGRATION.md.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise;
+ *     the caller (PyTorch's caching allocator) owns all memory.  Entry points
+ *     never allocate device memory.
+ *   - `stream` is a hipStream_t passed as void* (PyTorch's current stream).
+ *     Launches are asynchronous; nothing synchronizes the device.
+ *   - Return value: 0 on success, otherwise an MF_E_* status.  The message of
+ *     the last failure on the calling thread is available from mf_last_error().
+ *   - All physical constants travel in one POD descriptor, mf_config, built by
+ *     memfast_amd/hip.py from a memfast Config (the reference instead bakes
+ *     them into the CUDA source as #defines, memfast/cuda.py:67-127).
+ */
+#ifndef MEMFAST_HIP_H
+#define MEMFAST_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MF_ABI_VERSION 1
+#define MF_MAX_SLICES 32
+
+enum {
+    MF_OK = 0,
+    MF_E_INVALID = 1,      /* bad argument, shape or descriptor      -> ValueError */
+    MF_E_UNSUPPORTED = 2,  /* configuration not implemented on HIP  -> NotImplementedError */
+    MF_E_RESOURCE = 3,     /* launch exceeds a device/kernel limit   -> ResourceError */
+    MF_E_HIP = 4           /* HIP runtime error                      -> RuntimeError */
+};
+
+enum { MF_READ_SHARED = 0, MF_READ_SLICE_PAIR = 1, MF_READ_OUTPUT = 2 };
+
+/* Physical configuration (memfast/config.py:21-224), derived on the host.
+ * f_* members are the FP32 values the reference's torch CPU ops use (Python
+ * scalars are rounded to FP32 before they meet an FP32 tensor); d_* are the
+ * FP64 values used when precise_currents is set. */
+typedef struct mf_config {
+    int32_t abi_version;          /* MF_ABI_VERSION */
+    int32_t rows, cols;           /* array_size R, C */
+    int32_t read_rows, reads;     /* P = rows_per_read or R; Gr = ceil(R/P) */
+    int32_t activation_bits, weight_bits;
+    int32_t weight_signed;
+    int32_t n_in, n_w;            /* number of input / weight slices (A, W) */
+    int32_t in_shift[MF_MAX_SLICES], in_mask[MF_MAX_SLICES];
+    int64_t in_factor[MF_MAX_SLICES];
+    int32_t w_shift[MF_MAX_SLICES], w_mask[MF_MAX_SLICES];
+    int64_t w_factor[MF_MAX_SLICES];
+    int32_t adc_max[MF_MAX_SLICES];   /* LSB-first ADC maxima 2^bits-1 */
+    int32_t precise;              /* FP64 conductances and currents */
+    int32_t read_mode;            /* MF_READ_* */
+    int32_t has_write, has_read, has_vnoise, has_nonlinear, has_saf, has_drift;
+    /* FP32 constants */
+    float f_high, f_low, f_voltage, f_span;   /* fp32(H), fp32(L), fp32(V), fp32(H-L) */
+    float f_inv_unit;                         /* fp32(1/((H-L)V)) */
+    float f_write, f_read, f_vnoise;          /* noise sigmas */
+    float f_drift;                            /* fp32(drift factor) */
+    float f_saf_low, f_saf_band;              /* fp32(p_low), fp32(p_low+p_high) */
+    float f_out_mean, f_out_var;              /* fp32(expm1(s^2/2)), fp32(exp(s^2)expm1(s^2)) */
+    float f_two_pi;                           /* fp32(2*pi) */
+    float f_alpha_over_max[MF_MAX_SLICES];    /* fp32(alpha / adc_max[w]) */
+    /* FP64 constants (precise currents) */
+    double d_high, d_low, d_voltage, d_span, d_inv_unit, d_drift;
+    double d_alpha_over_max[MF_MAX_SLICES];
+} mf_config;
+
+/* Identity of a device for the tuning-cache key (replaces memfast/cuda.py:376-389). */
+typedef struct mf_identity {
+    char arch[64];                /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    char name[256];
+    int32_t compute_units;
+    int32_t driver_version;
+    int32_t runtime_version;
+    int64_t memory_bytes;
+} mf_identity;
+
+/* Per-kernel resource figures (replaces Program.resources, memfast/cuda.py:239-273). */
+typedef struct mf_resources {
+    int32_t threads;              /* threads per block */
+    int32_t shared_bytes;         /* LDS per block */
+    int32_t registers;            /* VGPRs per thread */
+    int32_t local_bytes;          /* private (spill) bytes per thread */
+    int32_t max_blocks_per_cu;    /* occupancy */
+} mf_resources;
+
+/* ---- library ------------------------------------------------------------ */
+int32_t mf_abi_version(void);
+const char *mf_last_error(void);
+/* Hash of the kernel sources compiled into this library (tuning-cache key;
+ * replaces the source_hash of memfast/simulator.py:48-54 for the native part). */
+const char *mf_source_hash(void);
+int mf_device_identity(int device, mf_identity *out);
+
+/* ---- quantization and programming --------------------------------------- */
+/* Grouped INT quantization of x [rows, cols] (FP32, row stride ld) with
+ * rectangular groups (gr, gc): memfast/quantization.py:9-44 for bits <= 8.
+ * Writes the per-group scale to `scale` [ceil(rows/gr), ceil(cols/gc)].
+ * `work` is caller scratch of the same size (uint32 group maxima). */
+int mf_group_scales(const float *x, int64_t rows, int64_t cols, int64_t ld, int64_t gr,
+                    int64_t gc, int32_t bits, int32_t is_signed, uint32_t *work,
+                    float *scale, void *stream);
+
+/* Input tiles (memfast/quantization.py:115-137): codes q [n, m*R] (uint8, two's
+ * complement masked to activation_bits, zero padded) and per-read scales
+ * xscale [n, m*Gr].  `scale` is either the group-scale grid from
+ * mf_group_scales (fixed == 0) or a [1, k] fixed scale row (fixed == 1). */
+int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
+                   const float *scale, int64_t gr, int64_t gc, int32_t fixed, uint8_t *q,
+                   float *xscale, void *stream);
+
+/* Weight tiles (memfast/quantization.py:82-112): logical [k, o] matrix b (row
+ * stride ld) -> packed [m, p, R, C] uint8 (the reference layout), the same codes
+ * column-major as packed_t [p*C, m*R] for the MFMA kernel, and per-read scales
+ * wscale [m*Gr, p*C].  `scale` is the group grid from mf_group_scales.
+ * packed_t may be NULL. */
+int mf_weight_tiles(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
+                    const float *scale, int64_t gr, int64_t gc, uint8_t *packed,
+                    uint8_t *packed_t, float *wscale, void *stream);
+
+/* packed [m, p, R, C] -> packed_t [p*C, m*R] (for checkpoints loaded from disk). */
+int mf_transpose_packed(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p,
+                        uint8_t *packed_t, void *stream);
+
+/* ---- conductances ------------------------------------------------------- */
+/* Programmed and read conductances (memfast/reference.py:10-51, kernels.cu:43-69)
+ * for tiles [begin, end): g [planes][m][end-begin][W][R][C] in FP32 (FP64 when
+ * cfg->precise), planes = n_in for read_mode slice_pair with read noise, else 1. */
+int mf_restore(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p,
+               int64_t begin, int64_t end, uint32_t seed, uint64_t event, void *g,
+               void *stream);
+
+/* ---- array reads --------------------------------------------------------- */
+/* Reference-compatible partial (memfast/cuda.py:322-373 / memfast/reference.py:63-117):
+ * integer slice totals T [n, m*Gr, end-begin, C] as FP32 (all integer valued).
+ * g: conductances as written by mf_restore for the same [begin, end), or an
+ * injected tensor of that layout.  NULL g means ideal devices (closed form).
+ * codes (optional, may be NULL): per-pair ADC counts int32
+ * [n, m*Gr, n_in, n_w, end-begin, C] for code-level parity. */
+int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
+               const uint8_t *packed, int64_t p, int64_t begin, int64_t end, const void *g,
+               uint32_t seed, uint64_t event, float *totals, int32_t *codes, void *stream);
+
+/* Fused read + scale restore (memfast/simulator.py:561-586 without the bias):
+ * out [n, ldo] FP32 receives columns [0, p*C) of
+ *   sum over reads g in torch's CPU order of (float(T[n,g,o]) * xscale[n,g]) * wscale[g,o].
+ * g as for mf_partial over all tiles (begin=0, end=p); NULL means ideal devices.
+ * For ideal devices with packed_t != NULL the MFMA kernel is used. */
+int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
+          const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
+          const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo,
+          void *stream);
+
+/* Kernel selected by mf_mm for this shape: 0 = general, 1 = MFMA ideal. */
+int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
+                 int32_t *kernel_id);
+
+/* Resource figures of the kernel mf_mm would launch. */
+int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *out);
+
+/* ---- counter-based RNG (memfast/random.py:8-33), for parity tests -------- */
+/* out[i] = uniform(address[i], seed, stream) (FP32) */
+int mf_rng_uniform(const uint64_t *address, int64_t count, uint64_t seed, uint32_t stream,
+                   float *out, void *stream_handle);
+/* out[i] = normal(address[i], seed, stream) (FP32, Box-Muller with OCML) */
+int mf_rng_normal(const uint64_t *address, int64_t count, uint64_t seed, uint32_t stream,
+                  float *out, void *stream_handle);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MEMFAST_HIP_H */

@@ -1,0 +1,497 @@
+// extern "C" entry points of libmemfast_hip.so (declared in include/memfast_hip.h).
+//
+// Host side of the gfx950 engine: argument validation, kernel selection, the
+// ideal-device MFMA plan, launches on the caller's stream and error strings.
+// Nothing here allocates device memory; the caller owns every buffer.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "mf_kernels.h"
+
+#ifndef MF_SOURCE_HASH
+#define MF_SOURCE_HASH "unknown"
+#endif
+
+namespace mf {
+
+__global__ void k_rng(const u64 *address, i64 count, u64 seed, u32 stream, int kind, float two_pi,
+                      float *out) {
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += i64(gridDim.x) * blockDim.x)
+        out[i] = kind ? normal(address[i], seed, stream, two_pi) : uniform(address[i], seed, stream);
+}
+
+// ---------------------------------------------------------------------------
+thread_local char g_error[1024] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(MF_E_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+    return MF_OK;
+}
+
+unsigned grid_for(i64 total, int block = 256) {
+    i64 blocks = (total + block - 1) / block;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 65536 * 8) blocks = 65536 * 8;
+    return unsigned(blocks);
+}
+
+int check_config(const mf_config *cfg) {
+    if (!cfg) return fail(MF_E_INVALID, "config descriptor is NULL");
+    if (cfg->abi_version != MF_ABI_VERSION)
+        return fail(MF_E_INVALID, "config ABI version %d, library expects %d", cfg->abi_version,
+                    MF_ABI_VERSION);
+    if (cfg->rows < 1 || cfg->cols < 4 || cfg->cols % 4 || cfg->read_rows < 1 ||
+        cfg->read_rows > cfg->rows || cfg->reads != (cfg->rows + cfg->read_rows - 1) / cfg->read_rows)
+        return fail(MF_E_INVALID, "invalid array geometry");
+    if (cfg->n_in < 1 || cfg->n_in > MF_MAX_SLICES || cfg->n_w < 1 || cfg->n_w > MF_MAX_SLICES)
+        return fail(MF_E_INVALID, "invalid slice counts");
+    if (cfg->activation_bits > 8 || cfg->weight_bits > 8)
+        return fail(MF_E_UNSUPPORTED,
+                    "precisions above 8 bits (64-bit codes, FP64 restore) are not implemented "
+                    "on the HIP backend yet");
+    return MF_OK;
+}
+
+int ceil_log2_torch(i64 x) {
+    // c10 utils::CeilLog2 as used by the CPU sum kernel.
+    if (x <= 2) return 1;
+    int bits = 0;
+    u64 v = u64(x - 1);
+    while (v) { ++bits; v >>= 1; }
+    return bits;
+}
+
+int level_power(i64 size) {
+    const int lp = ceil_log2_torch(size) / 4;
+    return lp > 4 ? lp : 4;
+}
+
+bool needs_conductances(const mf_config *cfg) {
+    return cfg->has_write || cfg->has_saf ||
+           (cfg->has_read && cfg->read_mode != MF_READ_OUTPUT);
+}
+
+int restore_planes(const mf_config *cfg) {
+    return (cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR) ? cfg->n_in : 1;
+}
+
+// Whether every output column uses the plain cascade of torch's sum.
+bool all_cascade_columns(int C, i64 p) {
+    for (i64 first = 0; first < p; first += 2) {
+        const i64 wc = ((p - first) < 2 ? (p - first) : 2) * C;
+        const i64 span = wc >= 8 ? 32 : 4;
+        if (wc % span) return false;
+    }
+    return true;
+}
+
+int byte_mask(int shift, int mask, bool sign_slice) {
+    int m = (mask << shift) & 0xFF;
+    if (sign_slice) m |= (0xFF << shift) & 0xFF;
+    return m;
+}
+
+u32 replicate(int m) { return u32(m) * 0x01010101u; }
+
+// Ideal-device MFMA eligibility and plan.  Returns false (with reason) when the
+// general kernel must be used.
+bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, int *ks,
+                      const char **why) {
+    if (cfg->has_write || cfg->has_read || cfg->has_vnoise || cfg->has_nonlinear || cfg->has_saf ||
+        cfg->has_drift) {
+        *why = "device effects enabled";
+        return false;
+    }
+    if (!cfg->weight_signed) { *why = "unsigned weights"; return false; }
+    if (cfg->read_rows % 32 || cfg->rows % cfg->read_rows || cfg->read_rows > 64) {
+        *why = "rows_per_read must be 32 or 64 and divide the array rows";
+        return false;
+    }
+    const i64 G = m * cfg->reads;
+    if (G >= 4096) { *why = "more than 4095 reads per output"; return false; }
+    if (!all_cascade_columns(cfg->cols, p)) { *why = "interleaved summation columns"; return false; }
+    const int P = cfg->read_rows;
+    // Closed-form exactness: FP32 (or FP64) current error stays below 1/4 count.
+    const double unit_err = cfg->precise ? std::ldexp(1.0, -53) : std::ldexp(1.0, -24);
+    const double span = cfg->precise ? cfg->d_span : double(cfg->f_span);
+    const double high = cfg->precise ? cfg->d_high : double(cfg->f_high);
+    double bound_abs = 0.0;
+    for (int a = 0; a < cfg->n_in; ++a)
+        for (int w = 0; w < cfg->n_w; ++w) {
+            const double ma = cfg->in_mask[a], mw = cfg->w_mask[w];
+            double zcap = P * ma * mw;
+            if (zcap > cfg->adc_max[w] + 1.0) zcap = cfg->adc_max[w] + 1.0;
+            const double rel = (P + 16.0 + mw * high / span) * unit_err;
+            if (zcap * rel > bound_abs) bound_abs = zcap * rel;
+        }
+    if (bound_abs >= 0.25) { *why = "FP32 currents may move ADC counts"; return false; }
+    // int32 accumulators: the reconstruction bound of the slice totals.
+    double fa_sum = 0.0, fw_sum = 0.0;
+    for (int a = 0; a < cfg->n_in; ++a) fa_sum += std::fabs(double(cfg->in_factor[a]));
+    for (int w = 0; w < cfg->n_w; ++w)
+        fw_sum += std::fabs(double(cfg->w_factor[w])) * cfg->adc_max[w];
+    if (fa_sum * fw_sum >= 2147483647.0) { *why = "slice totals exceed int32"; return false; }
+
+    memset(plan, 0, sizeof(*plan));
+    unsigned free_sets[MF_MAX_SLICES];
+    for (int w = 0; w < cfg->n_w; ++w) {
+        unsigned set = 0;
+        for (int a = 0; a < cfg->n_in; ++a) {
+            const i64 smax = i64(P) * cfg->in_mask[a] * cfg->w_mask[w];
+            if (smax <= cfg->adc_max[w]) set |= 1u << a;
+        }
+        free_sets[w] = set;
+    }
+    bool grouped[MF_MAX_SLICES] = {false};
+    for (int w = 0; w < cfg->n_w; ++w) {
+        if (grouped[w] || free_sets[w] == 0) continue;
+        int amask = 0, bmask = 0;
+        for (int a = 0; a < cfg->n_in; ++a)
+            if (free_sets[w] >> a & 1)
+                amask |= byte_mask(cfg->in_shift[a], cfg->in_mask[a], a == cfg->n_in - 1);
+        for (int v = w; v < cfg->n_w; ++v)
+            if (!grouped[v] && free_sets[v] == free_sets[w]) {
+                grouped[v] = true;
+                bmask |= byte_mask(cfg->w_shift[v], cfg->w_mask[v], v == cfg->n_w - 1);
+            }
+        if (plan->n_lin >= IDEAL_MAX_LIN) { *why = "too many linear terms"; return false; }
+        plan->lin_a[plan->n_lin] = replicate(amask);
+        plan->lin_b[plan->n_lin] = replicate(bmask);
+        ++plan->n_lin;
+    }
+    for (int a = 0; a < cfg->n_in; ++a)
+        for (int w = 0; w < cfg->n_w; ++w) {
+            if (free_sets[w] >> a & 1) continue;
+            if (plan->n_clamp >= IDEAL_MAX_CLAMP) { *why = "too many clamped pairs"; return false; }
+            const int c = plan->n_clamp++;
+            plan->cl_a[c] = replicate(byte_mask(cfg->in_shift[a], cfg->in_mask[a], a == cfg->n_in - 1));
+            plan->cl_b[c] = replicate(byte_mask(cfg->w_shift[w], cfg->w_mask[w], w == cfg->n_w - 1));
+            const i64 f = cfg->in_factor[a] * cfg->w_factor[w];
+            plan->cl_val[c] = int(f * cfg->adc_max[w]);
+            plan->cl_upper[c] = f > 0 ? 1 : 0;
+        }
+    *ks = P / 32;
+    return true;
+}
+
+template <typename Phys>
+int launch_general(const mf_config *cfg, const GeneralArgs &args, int out_kind, hipStream_t s) {
+    const i64 ncols = args.width * cfg->cols;
+    const i64 col_blocks = (ncols + 31) / 32;
+    const i64 vec_blocks = (args.n + 7) / 8;
+    if (col_blocks > 65535) return fail(MF_E_RESOURCE, "too many output columns for one launch");
+    if (vec_blocks > 2147483647) return fail(MF_E_RESOURCE, "too many input vectors");
+    const dim3 grid{unsigned(vec_blocks), unsigned(col_blocks), 1u};
+    const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
+    if (sizeof(Phys) == 4) {
+        if (output_noise)
+            hipLaunchKernelGGL((k_general<float, 2, true>), grid, dim3(256), 0, s, *cfg, args, out_kind);
+        else
+            hipLaunchKernelGGL((k_general<float, 8, false>), grid, dim3(256), 0, s, *cfg, args, out_kind);
+    } else {
+        if (output_noise)
+            hipLaunchKernelGGL((k_general<double, 2, true>), grid, dim3(256), 0, s, *cfg, args, out_kind);
+        else
+            hipLaunchKernelGGL((k_general<double, 4, false>), grid, dim3(256), 0, s, *cfg, args, out_kind);
+    }
+    return check_launch("general read");
+}
+
+}  // namespace mf
+
+using namespace mf;
+
+extern "C" {
+
+int32_t mf_abi_version(void) { return MF_ABI_VERSION; }
+
+const char *mf_last_error(void) { return g_error; }
+
+const char *mf_source_hash(void) { return MF_SOURCE_HASH; }
+
+int mf_device_identity(int device, mf_identity *out) {
+    if (!out) return fail(MF_E_INVALID, "identity output is NULL");
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(MF_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    memset(out, 0, sizeof(*out));
+    snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+    snprintf(out->name, sizeof(out->name), "%s", prop.name);
+    out->compute_units = prop.multiProcessorCount;
+    out->memory_bytes = int64_t(prop.totalGlobalMem);
+    int version = 0;
+    if (hipDriverGetVersion(&version) == hipSuccess) out->driver_version = version;
+    if (hipRuntimeGetVersion(&version) == hipSuccess) out->runtime_version = version;
+    return MF_OK;
+}
+
+int mf_group_scales(const float *x, int64_t rows, int64_t cols, int64_t ld, int64_t gr,
+                    int64_t gc, int32_t bits, int32_t is_signed, uint32_t *work, float *scale,
+                    void *stream) {
+    if (!x || !work || !scale || rows < 1 || cols < 1 || ld < cols || gr < 1 || gc < 1)
+        return fail(MF_E_INVALID, "invalid group-scale arguments");
+    if (bits < 2 || bits > 8) return fail(MF_E_UNSUPPORTED, "group scales support 2..8 bits");
+    gr = gr < rows ? gr : rows;
+    gc = gc < cols ? gc : cols;
+    const i64 nrg = (rows + gr - 1) / gr, ncg = (cols + gc - 1) / gc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
+    hipLaunchKernelGGL(k_group_max, dim3(grid_for(rows * ((cols + 7) / 8))), dim3(256), 0, s, x,
+                       rows, cols, ld, gr, gc, ncg, work);
+    const float upper = float((1 << (bits - (is_signed ? 1 : 0))) - 1);
+    hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg,
+                       upper, scale);
+    return check_launch("group scales");
+}
+
+int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
+                   const float *scale, int64_t gr, int64_t gc, int32_t fixed, uint8_t *q,
+                   float *xscale, void *stream) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k)
+        return fail(MF_E_INVALID, "invalid input-tile arguments");
+    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (k + R - 1) / R;
+    const i64 kp = m * R;
+    gr = gr < n ? gr : n;
+    gc = gc < k ? gc : k;
+    const i64 ncg = (k + gc - 1) / gc;
+    const int bits = cfg->activation_bits;
+    const float upper = float((1 << (bits - 1)) - 1);
+    const u32 mask = (1u << bits) - 1u;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_input_codes, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
+                       scale, gr, gc, ncg, fixed, -upper, upper, mask, q);
+    hipLaunchKernelGGL(k_input_scales, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k, m * Gr,
+                       R, P, Gr, scale, gr, gc, ncg, fixed, xscale);
+    return check_launch("input tiles");
+}
+
+int mf_weight_tiles(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
+                    const float *scale, int64_t gr, int64_t gc, uint8_t *packed,
+                    uint8_t *packed_t, float *wscale, void *stream) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!b || !scale || !packed || !wscale || k < 1 || o < 1 || ld < o)
+        return fail(MF_E_INVALID, "invalid weight-tile arguments");
+    const int R = cfg->rows, C = cfg->cols, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (k + R - 1) / R, p = (o + C - 1) / C;
+    gr = gr < k ? gr : k;
+    gc = gc < o ? gc : o;
+    const i64 ncg = (o + gc - 1) / gc;
+    const int bits = cfg->weight_bits;
+    const float upper = float((1 << (bits - (cfg->weight_signed ? 1 : 0))) - 1);
+    const float lower = cfg->weight_signed ? -upper : 0.0f;
+    const u32 mask = (1u << bits) - 1u;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_weight_codes, dim3(grid_for(m * R * p * C)), dim3(256), 0, s, b, k, o, ld,
+                       R, C, m, p, scale, gr, gc, ncg, lower, upper, mask, packed, packed_t);
+    hipLaunchKernelGGL(k_weight_scales, dim3(grid_for(m * Gr * p * C)), dim3(256), 0, s, k, o,
+                       m * Gr, p * C, R, P, Gr, scale, gr, gc, ncg, wscale);
+    return check_launch("weight tiles");
+}
+
+int mf_transpose_packed(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p,
+                        uint8_t *packed_t, void *stream) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!packed || !packed_t || m < 1 || p < 1) return fail(MF_E_INVALID, "invalid transpose arguments");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_transpose_packed, dim3(grid_for(m * cfg->rows * p * cfg->cols)), dim3(256),
+                       0, s, packed, cfg->rows, cfg->cols, m, p, packed_t);
+    return check_launch("transpose packed");
+}
+
+int mf_restore(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p, int64_t begin,
+               int64_t end, uint32_t seed, uint64_t event, void *g, void *stream) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!packed || !g || m < 1 || p < 1 || begin < 0 || end <= begin || end > p)
+        return fail(MF_E_INVALID, "invalid restore arguments");
+    const int planes = restore_planes(cfg);
+    const i64 total = i64(planes) * m * (end - begin) * cfg->n_w * cfg->rows * cfg->cols;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (cfg->precise)
+        hipLaunchKernelGGL(k_restore<double>, dim3(grid_for(total)), dim3(256), 0, s, *cfg, packed, m,
+                           p, begin, end - begin, seed, event, planes, static_cast<double *>(g));
+    else
+        hipLaunchKernelGGL(k_restore<float>, dim3(grid_for(total)), dim3(256), 0, s, *cfg, packed, m,
+                           p, begin, end - begin, seed, event, planes, static_cast<float *>(g));
+    return check_launch("restore");
+}
+
+int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m, const uint8_t *packed,
+               int64_t p, int64_t begin, int64_t end, const void *g, uint32_t seed,
+               uint64_t event, float *totals, int32_t *codes, void *stream) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!q || !packed || !totals || n < 1 || m < 1 || p < 1 || begin < 0 || end <= begin || end > p)
+        return fail(MF_E_INVALID, "invalid partial arguments");
+    if (cfg->n_in > 8 || cfg->n_w > 8) return fail(MF_E_UNSUPPORTED, "more than 8 slices");
+    if (!g && needs_conductances(cfg))
+        return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
+    GeneralArgs args{};
+    args.q = q;
+    args.packed = packed;
+    args.g = g;
+    args.out = totals;
+    args.codes = codes;
+    args.n = n;
+    args.m = m;
+    args.p = p;
+    args.begin = begin;
+    args.width = end - begin;
+    args.seed = seed;
+    args.event = event;
+    args.planes = g ? restore_planes(cfg) : 1;
+    const i64 G = m * cfg->reads;
+    args.lp_cascade = level_power(G);
+    args.lp_interleaved = level_power(G / 4);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return cfg->precise ? launch_general<double>(cfg, args, OUT_TOTALS, s)
+                        : launch_general<float>(cfg, args, OUT_TOTALS, s);
+}
+
+int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
+                 int32_t *kernel_id) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!kernel_id) return fail(MF_E_INVALID, "kernel_id is NULL");
+    IdealPlan plan;
+    int ks = 0;
+    const char *why = "";
+    *kernel_id = (has_packed_t && build_ideal_plan(cfg, m, p, &plan, &ks, &why)) ? 1 : 0;
+    (void)n;
+    return MF_OK;
+}
+
+int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
+          const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
+          const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo, void *stream) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
+        ldo < p * cfg->cols)
+        return fail(MF_E_INVALID, "invalid mm arguments");
+    if (cfg->n_in > 8 || cfg->n_w > 8) return fail(MF_E_UNSUPPORTED, "more than 8 slices");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const i64 G = m * cfg->reads;
+    IdealPlan plan;
+    int ks = 0;
+    const char *why = "";
+    const bool aligned = (reinterpret_cast<uintptr_t>(q) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(packed_t) % 16 == 0);
+    if (!g && packed_t && aligned && build_ideal_plan(cfg, m, p, &plan, &ks, &why)) {
+        IdealArgs args{};
+        args.q = q;
+        args.wt = packed_t;
+        args.xscale = xscale;
+        args.wscale = wscale;
+        args.out = out;
+        args.n = n;
+        args.kp = m * cfg->rows;
+        args.G = G;
+        args.ldo = ldo;
+        args.ldws = p * cfg->cols;
+        args.ncols = p * cfg->cols;
+        args.Gr = cfg->reads;
+        args.R = cfg->rows;
+        args.P = cfg->read_rows;
+        args.a_bits = cfg->activation_bits;
+        args.w_bits = cfg->weight_bits;
+        constexpr int BM = 64, BN = 128;
+        const i64 gy = (n + BM - 1) / BM, gx = (args.ncols + BN - 1) / BN;
+        if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
+        const dim3 grid{unsigned(gx), unsigned(gy), 1u};
+        if (ks == 1)
+            hipLaunchKernelGGL((k_ideal<1, 2, 1>), grid, dim3(256), 0, s, plan, args);
+        else
+            hipLaunchKernelGGL((k_ideal<1, 2, 2>), grid, dim3(256), 0, s, plan, args);
+        return check_launch("ideal MFMA read");
+    }
+    if (!g && needs_conductances(cfg))
+        return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
+    GeneralArgs args{};
+    args.q = q;
+    args.packed = packed;
+    args.g = g;
+    args.xscale = xscale;
+    args.wscale = wscale;
+    args.out = out;
+    args.n = n;
+    args.m = m;
+    args.p = p;
+    args.begin = 0;
+    args.width = p;
+    args.ldo = ldo;
+    args.ldws = p * cfg->cols;
+    args.seed = seed;
+    args.event = event;
+    args.planes = g ? restore_planes(cfg) : 1;
+    args.lp_cascade = level_power(G);
+    args.lp_interleaved = level_power(G / 4);
+    return cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
+                        : launch_general<float>(cfg, args, OUT_FUSED, s);
+}
+
+int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *out) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!out) return fail(MF_E_INVALID, "resources output is NULL");
+    hipFuncAttributes attr;
+    hipError_t e;
+    if (kernel_id == 1)
+        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_ideal<1, 2, 1>));
+    else if (cfg->precise)
+        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<double, 4, false>));
+    else
+        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<float, 8, false>));
+    if (e != hipSuccess) return fail(MF_E_HIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
+    memset(out, 0, sizeof(*out));
+    out->threads = 256;
+    out->shared_bytes = int32_t(attr.sharedSizeBytes);
+    out->registers = attr.numRegs;
+    out->local_bytes = int32_t(attr.localSizeBytes);
+    int blocks = 0;
+    const void *fn = kernel_id == 1 ? reinterpret_cast<const void *>(&k_ideal<1, 2, 1>)
+                                    : reinterpret_cast<const void *>(&k_general<float, 8, false>);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) == hipSuccess)
+        out->max_blocks_per_cu = blocks;
+    if (out->max_blocks_per_cu < 1 && blocks == 0) return fail(MF_E_RESOURCE, "zero resident blocks");
+    return MF_OK;
+}
+
+int mf_rng_uniform(const uint64_t *address, int64_t count, uint64_t seed, uint32_t stream,
+                   float *out, void *stream_handle) {
+    if (!address || !out || count < 0) return fail(MF_E_INVALID, "invalid rng arguments");
+    if (count == 0) return MF_OK;
+    hipLaunchKernelGGL(k_rng, dim3(grid_for(count)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream_handle), reinterpret_cast<const u64 *>(address),
+                       count, u64(seed), stream, 0, 6.2831854820251465f, out);
+    return check_launch("rng uniform");
+}
+
+int mf_rng_normal(const uint64_t *address, int64_t count, uint64_t seed, uint32_t stream,
+                  float *out, void *stream_handle) {
+    if (!address || !out || count < 0) return fail(MF_E_INVALID, "invalid rng arguments");
+    if (count == 0) return MF_OK;
+    hipLaunchKernelGGL(k_rng, dim3(grid_for(count)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream_handle), reinterpret_cast<const u64 *>(address),
+                       count, u64(seed), stream, 1, 6.2831854820251465f, out);
+    return check_launch("rng normal");
+}
+
+}  // extern "C"

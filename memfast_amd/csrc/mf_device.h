@@ -1,0 +1,128 @@
+// Device-side helpers shared by the gfx950 kernels of the sliced analog engine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/memfast_hip.h"
+
+namespace mf {
+
+typedef uint8_t u8;
+typedef uint32_t u32;
+typedef uint64_t u64;
+typedef int64_t i64;
+
+// ---------------------------------------------------------------------------
+// Counter-based RNG keyed by physical address (memfast/random.py:8-33,
+// memfast/kernels.cu:22-41).  The integer part is exact; the normal uses
+// OCML's logf/cosf/sqrtf (not bit-identical to torch CPU's).
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ u32 mix(u32 x) {
+    x = (x ^ (x >> 16)) * 0x7feb352du;
+    x = (x ^ (x >> 15)) * 0x846ca68bu;
+    return x ^ (x >> 16);
+}
+
+__device__ __forceinline__ float uniform(u64 address, u64 seed, u32 stream) {
+    const u32 key = mix(u32(seed) ^ (stream * 0x9e3779b9u));
+    const u32 hi = u32(address >> 32);
+    u32 fold = mix(hi ^ mix(u32(seed >> 32)));
+    if (hi != 0u) fold ^= mix(hi ^ key);
+    const u32 h = mix(u32(address) ^ fold ^ key);
+    // ((h >> 8) + 0.5) / 2^24 is exact in FP32.
+    return (float(h >> 8) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+__device__ __forceinline__ float normal(u64 address, u64 seed, u32 stream, float two_pi) {
+    const float u = uniform(address, seed, stream);
+    const float v = uniform(address, seed, stream + 1u);
+    // torch: sqrt(-2 * log(u)) * cos((2*pi) * v), all FP32.
+    return sqrtf(-2.0f * logf(u)) * cosf(two_pi * v);
+}
+
+__host__ __device__ __forceinline__ u64 event_seed(u32 seed, u64 event) {
+    return u64(seed ^ mix(u32(event))) | (u64(mix(u32(event >> 32))) << 32);
+}
+
+// ---------------------------------------------------------------------------
+// torch CPU reduction order of `sum` over the read dimension
+// (aten/src/ATen/native/cpu/SumKernel.cpp as shipped in torch 2.x):
+// a 4-level cascade whose level step is 2^lp; each full block of 2^lp values is
+// summed sequentially from zero and pushed up the levels, the tail stays in
+// level 0, and the levels are finally folded low-first.  Columns outside the
+// 4-row-vector chunks use four interleaved cascades (rows k, k+4, ...), then
+// the leftover rows are added to the first one and the four are folded.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Cascade {
+    T acc[4];
+    int count;
+    __device__ __forceinline__ void reset() {
+        acc[0] = acc[1] = acc[2] = acc[3] = T(0);
+        count = 0;
+    }
+    __device__ __forceinline__ void push(T x, int lp) {
+        acc[0] = acc[0] + x;
+        ++count;
+        const int step_mask = (1 << lp) - 1;
+        if ((count & step_mask) == 0) {
+#pragma unroll
+            for (int j = 1; j < 4; ++j) {
+                acc[j] = acc[j] + acc[j - 1];
+                acc[j - 1] = T(0);
+                if ((count & (step_mask << (j * lp))) != 0) break;
+            }
+        }
+    }
+    __device__ __forceinline__ T finish() const {
+        T r = acc[0];
+        r = r + acc[1];
+        r = r + acc[2];
+        r = r + acc[3];
+        return r;
+    }
+};
+
+// Interleaved (ILP 4) variant: values arrive in read order g = 0..total-1.
+template <typename T>
+struct Interleaved {
+    Cascade<T> stream[4];
+    T first;   // finalized stream 0 plus leftover rows
+    int seen;
+    __device__ __forceinline__ void reset() {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) stream[k].reset();
+        first = T(0);
+        seen = 0;
+    }
+    // total: number of values; lp: level power of each stream (size total/4).
+    __device__ __forceinline__ void push(T x, int total, int lp) {
+        const int full = (total / 4) * 4;
+        if (seen < full) {
+            const int k = seen & 3;
+            // Stream k receives its q-th value; dispatch without dynamic indexing.
+            if (k == 0) stream[0].push(x, lp);
+            else if (k == 1) stream[1].push(x, lp);
+            else if (k == 2) stream[2].push(x, lp);
+            else stream[3].push(x, lp);
+            if (seen + 1 == full) first = stream[0].finish();
+        } else {
+            if (full == 0 && seen == 0) first = T(0);
+            first = first + x;
+        }
+        ++seen;
+    }
+    __device__ __forceinline__ T finish(int total) const {
+        const int full = (total / 4) * 4;
+        T r = first;
+        if (full) {
+            r = r + stream[1].finish();
+            r = r + stream[2].finish();
+            r = r + stream[3].finish();
+        }
+        return r;
+    }
+};
+
+}  // namespace mf

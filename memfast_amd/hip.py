@@ -1,0 +1,577 @@
+"""ctypes binding of libmemfast_hip.so, the gfx950 accelerator backend.
+
+Drop-in replacement of the reference's memfast/cuda.py (NVRTC + libcuda via
+ctypes).  The Python-level names the simulator imports are kept:
+``ResourceError`` (cuda.py:15-16), ``cache_root`` (:47-51), ``atomic_write``
+(:54-64), ``program(...).resources(...)`` (:239-273, :313-319), ``partial``
+(:322-373) and ``identity`` (:376-389).  Kernels are built ahead of time
+(memfast_amd/build_native.py); physical constants travel in an ``mf_config``
+descriptor instead of being compiled into the source.
+
+There is no CPU fallback: every entry point raises when the library or a HIP
+device is missing.
+"""
+
+import ctypes as ct
+import math
+import os
+from functools import lru_cache
+from pathlib import Path
+
+import torch
+
+LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
+MAX_SLICES = 32
+ABI_VERSION = 1
+
+OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
+
+# Optional launch timer: when set to a list, ``mm`` appends a (start, end)
+# pair of torch.cuda.Events recorded on the launch stream around the fused
+# read kernel (used by bench.py to time the dominant kernel).
+kernel_timer = None
+READ_MODES = {"shared": 0, "slice_pair": 1, "output": 2}
+
+
+class ResourceError(RuntimeError):
+    """A launch exceeds a compiled kernel or device resource limit."""
+
+
+class BackendError(RuntimeError):
+    """The HIP backend is unavailable or a HIP runtime call failed."""
+
+
+def cache_root():
+    """Root of persistent caches: $MEMFAST_CACHE_DIR or $XDG_CACHE_HOME/memfast."""
+    base = os.environ.get("MEMFAST_CACHE_DIR")
+    if base:
+        return Path(base).expanduser()
+    return Path(os.environ.get("XDG_CACHE_HOME", Path.home() / ".cache")) / "memfast"
+
+
+def atomic_write(path, content):
+    """Write bytes through a temporary file in the same directory and rename."""
+    import tempfile
+
+    path = Path(path)
+    path.parent.mkdir(parents=True, exist_ok=True)
+    with tempfile.NamedTemporaryFile(dir=path.parent, delete=False) as stream:
+        temporary = Path(stream.name)
+        stream.write(content)
+    try:
+        os.replace(temporary, path)
+    finally:
+        temporary.unlink(missing_ok=True)
+
+
+# ---------------------------------------------------------------------------
+# C structures (include/memfast_hip.h)
+# ---------------------------------------------------------------------------
+class MFConfig(ct.Structure):
+    _fields_ = [
+        ("abi_version", ct.c_int32),
+        ("rows", ct.c_int32), ("cols", ct.c_int32),
+        ("read_rows", ct.c_int32), ("reads", ct.c_int32),
+        ("activation_bits", ct.c_int32), ("weight_bits", ct.c_int32),
+        ("weight_signed", ct.c_int32),
+        ("n_in", ct.c_int32), ("n_w", ct.c_int32),
+        ("in_shift", ct.c_int32 * MAX_SLICES), ("in_mask", ct.c_int32 * MAX_SLICES),
+        ("in_factor", ct.c_int64 * MAX_SLICES),
+        ("w_shift", ct.c_int32 * MAX_SLICES), ("w_mask", ct.c_int32 * MAX_SLICES),
+        ("w_factor", ct.c_int64 * MAX_SLICES),
+        ("adc_max", ct.c_int32 * MAX_SLICES),
+        ("precise", ct.c_int32),
+        ("read_mode", ct.c_int32),
+        ("has_write", ct.c_int32), ("has_read", ct.c_int32), ("has_vnoise", ct.c_int32),
+        ("has_nonlinear", ct.c_int32), ("has_saf", ct.c_int32), ("has_drift", ct.c_int32),
+        ("f_high", ct.c_float), ("f_low", ct.c_float), ("f_voltage", ct.c_float),
+        ("f_span", ct.c_float), ("f_inv_unit", ct.c_float),
+        ("f_write", ct.c_float), ("f_read", ct.c_float), ("f_vnoise", ct.c_float),
+        ("f_drift", ct.c_float),
+        ("f_saf_low", ct.c_float), ("f_saf_band", ct.c_float),
+        ("f_out_mean", ct.c_float), ("f_out_var", ct.c_float),
+        ("f_two_pi", ct.c_float),
+        ("f_alpha_over_max", ct.c_float * MAX_SLICES),
+        ("d_high", ct.c_double), ("d_low", ct.c_double), ("d_voltage", ct.c_double),
+        ("d_span", ct.c_double), ("d_inv_unit", ct.c_double), ("d_drift", ct.c_double),
+        ("d_alpha_over_max", ct.c_double * MAX_SLICES),
+    ]
+
+
+class MFIdentity(ct.Structure):
+    _fields_ = [
+        ("arch", ct.c_char * 64),
+        ("name", ct.c_char * 256),
+        ("compute_units", ct.c_int32),
+        ("driver_version", ct.c_int32),
+        ("runtime_version", ct.c_int32),
+        ("memory_bytes", ct.c_int64),
+    ]
+
+
+class MFResources(ct.Structure):
+    _fields_ = [
+        ("threads", ct.c_int32),
+        ("shared_bytes", ct.c_int32),
+        ("registers", ct.c_int32),
+        ("local_bytes", ct.c_int32),
+        ("max_blocks_per_cu", ct.c_int32),
+    ]
+
+
+_P = ct.c_void_p
+_I64 = ct.c_int64
+_I32 = ct.c_int32
+_CFG = ct.POINTER(MFConfig)
+
+SIGNATURES = {
+    "mf_abi_version": ([], _I32),
+    "mf_last_error": ([], ct.c_char_p),
+    "mf_source_hash": ([], ct.c_char_p),
+    "mf_device_identity": ([ct.c_int, ct.POINTER(MFIdentity)], ct.c_int),
+    "mf_group_scales": ([_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P], ct.c_int),
+    "mf_input_tiles": ([_CFG, _P, _I64, _I64, _I64, _P, _I64, _I64, _I32, _P, _P, _P], ct.c_int),
+    "mf_weight_tiles": ([_CFG, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P], ct.c_int),
+    "mf_transpose_packed": ([_CFG, _P, _I64, _I64, _P, _P], ct.c_int),
+    "mf_restore": ([_CFG, _P, _I64, _I64, _I64, _I64, ct.c_uint32, ct.c_uint64, _P, _P],
+                   ct.c_int),
+    "mf_partial": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
+                    _P, _P, _P], ct.c_int),
+    "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
+               _I64, _P], ct.c_int),
+    "mf_mm_kernel": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I32)], ct.c_int),
+    "mf_resources_query": ([_CFG, _I32, ct.POINTER(MFResources)], ct.c_int),
+    "mf_rng_uniform": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
+    "mf_rng_normal": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
+}
+
+
+@lru_cache(None)
+def library():
+    """Load libmemfast_hip.so after torch, so both share one HIP runtime."""
+    if not LIBRARY.is_file():
+        raise BackendError(
+            f"{LIBRARY} is missing; build it with `python -m memfast_amd.build_native` "
+            "(memfast_amd has no CPU fallback)"
+        )
+    lib = ct.CDLL(str(LIBRARY))
+    for name, (args, result) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = result
+    if lib.mf_abi_version() != ABI_VERSION:
+        raise BackendError("libmemfast_hip.so ABI version differs from memfast_amd")
+    return lib
+
+
+def native_source_hash():
+    return library().mf_source_hash().decode()
+
+
+def check(status, operation):
+    if status == OK:
+        return
+    message = library().mf_last_error().decode(errors="replace")
+    text = f"{operation} failed: {message}"
+    if status == E_INVALID:
+        raise ValueError(text)
+    if status == E_UNSUPPORTED:
+        raise NotImplementedError(text)
+    if status == E_RESOURCE:
+        raise ResourceError(text)
+    raise BackendError(f"{text} (HIP status {status})")
+
+
+def _ptr(tensor):
+    return ct.c_void_p(tensor.data_ptr()) if tensor is not None else None
+
+
+def _stream(device):
+    return ct.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_device(tensor):
+    if not tensor.is_cuda:
+        raise BackendError("memfast_amd kernels run on HIP devices only (tensor is on CPU)")
+
+
+# ---------------------------------------------------------------------------
+# Config -> descriptor
+# ---------------------------------------------------------------------------
+@lru_cache(maxsize=512)
+def descriptor(config):
+    """mf_config for a (hashable, frozen) Config."""
+    ni = config.nonidealities
+    d = MFConfig()
+    d.abi_version = ABI_VERSION
+    d.rows, d.cols = config.array_size
+    d.read_rows = config.read_rows
+    d.reads = config.reads_per_array
+    d.activation_bits = config.activation_bits
+    d.weight_bits = config.weight_bits
+    d.weight_signed = int(config.weight_signed)
+    il, wl = config.input_layout, config.weight_layout
+    if len(il) > MAX_SLICES or len(wl) > MAX_SLICES:
+        raise NotImplementedError("more than 32 slices")
+    d.n_in, d.n_w = len(il), len(wl)
+    for index, (shift, mask, factor) in enumerate(il):
+        d.in_shift[index], d.in_mask[index], d.in_factor[index] = shift, mask, factor
+    for index, (shift, mask, factor) in enumerate(wl):
+        d.w_shift[index], d.w_mask[index], d.w_factor[index] = shift, mask, factor
+    maxima = config.adc_maxima
+    for index, value in enumerate(maxima):
+        d.adc_max[index] = value
+        d.f_alpha_over_max[index] = ni.adc_nonlinearity / value
+        d.d_alpha_over_max[index] = ni.adc_nonlinearity / value
+    d.precise = int(config.precise_currents)
+    d.read_mode = READ_MODES[ni.read_mode]
+    drift = ni.drift_factor
+    d.has_write = int(ni.write_variation != 0)
+    d.has_read = int(ni.read_variation != 0)
+    d.has_vnoise = int(ni.voltage_variation != 0)
+    d.has_nonlinear = int(ni.adc_nonlinearity != 0)
+    d.has_saf = int(ni.stuck_at_low + ni.stuck_at_high != 0)
+    d.has_drift = int(drift != 1.0)
+    high, low, volt = config.high_conductance, config.low_conductance, config.read_voltage
+    unit = config.current_unit
+    # ctypes rounds Python floats to FP32 like torch rounds scalars meeting FP32 tensors.
+    d.f_high, d.f_low, d.f_voltage, d.f_span = high, low, volt, high - low
+    d.f_inv_unit = 1 / unit
+    d.f_write, d.f_read, d.f_vnoise = ni.write_variation, ni.read_variation, ni.voltage_variation
+    d.f_drift = drift
+    d.f_saf_low = ni.stuck_at_low
+    d.f_saf_band = ni.stuck_at_low + ni.stuck_at_high
+    sigma = ni.read_variation
+    d.f_out_mean = math.expm1(0.5 * sigma**2)
+    d.f_out_var = math.exp(sigma**2) * math.expm1(sigma**2)
+    d.f_two_pi = 2 * math.pi
+    d.d_high, d.d_low, d.d_voltage, d.d_span = high, low, volt, high - low
+    d.d_inv_unit = 1 / unit
+    d.d_drift = drift
+    return d
+
+
+def needs_conductances(config):
+    ni = config.nonidealities
+    return bool(
+        ni.write_variation
+        or ni.stuck_at_low + ni.stuck_at_high
+        or (ni.read_variation and ni.read_mode != "output")
+    )
+
+
+def restore_planes(config):
+    ni = config.nonidealities
+    if ni.read_variation and ni.read_mode == "slice_pair":
+        return len(config.input_layout)
+    return 1
+
+
+def supported(config):
+    """Raise NotImplementedError for configurations the HIP backend lacks."""
+    if config.wide:
+        raise NotImplementedError(
+            "precisions above 8 bits and BFP (64-bit codes, FP64 restore) are not "
+            "implemented on the HIP backend yet"
+        )
+
+
+# ---------------------------------------------------------------------------
+# Programming and quantization
+# ---------------------------------------------------------------------------
+def _group_dims(shape, granularity):
+    rows, cols = shape
+    gr = rows if granularity[0] is None else min(granularity[0], rows)
+    gc = cols if granularity[1] is None else min(granularity[1], cols)
+    return gr, gc
+
+
+def group_scales(value, bits, granularity, *, signed=True):
+    """Per-group INT scales of a 2-D FP32 device tensor (quantization.py:9-33)."""
+    require_device(value)
+    value = value.contiguous()
+    rows, cols = value.shape
+    gr, gc = _group_dims(value.shape, granularity)
+    nr, nc = math.ceil(rows / gr), math.ceil(cols / gc)
+    work = torch.empty((nr, nc), dtype=torch.int32, device=value.device)
+    scale = torch.empty((nr, nc), dtype=torch.float32, device=value.device)
+    with torch.cuda.device(value.device):
+        check(
+            library().mf_group_scales(
+                _ptr(value), rows, cols, cols, gr, gc, bits, int(signed), _ptr(work),
+                _ptr(scale), _stream(value.device),
+            ),
+            "group scales",
+        )
+    return scale, gr, gc
+
+
+def input_tiles(value, config, fixed_scale=None):
+    """Codes q [N, m, R] (uint8) and per-read scales [N, m*Gr] (quantization.py:115-137)."""
+    supported(config)
+    require_device(value)
+    n, k = value.shape
+    if not torch.isfinite(value).all():
+        raise ValueError("quantized values must be finite")
+    x = value.to(torch.float32).contiguous()
+    r = config.array_size[0]
+    m = math.ceil(k / r)
+    q = torch.empty((n, m, r), dtype=torch.uint8, device=value.device)
+    xscale = torch.empty((n, m * config.reads_per_array), dtype=torch.float32, device=value.device)
+    if fixed_scale is None:
+        scale, gr, gc = group_scales(x, config.activation_bits, config.input_quant_gran)
+        fixed = 0
+    else:
+        scale = fixed_scale.to(device=value.device, dtype=torch.float32).reshape(-1).contiguous()
+        if scale.numel() != k:
+            raise ValueError("fixed input scale must have one entry per input feature")
+        gr, gc, fixed = 1, 1, 1
+    with torch.cuda.device(value.device):
+        check(
+            library().mf_input_tiles(
+                ct.byref(descriptor(config)), _ptr(x), n, k, k, _ptr(scale), gr, gc, fixed,
+                _ptr(q), _ptr(xscale), _stream(value.device),
+            ),
+            "input tiles",
+        )
+    return q, xscale
+
+
+def weight_tiles(weight, config, *, transposed=True):
+    """PyTorch [O,K] weights -> packed [m,p,R,C], packed_t [p*C, m*R], scales [m*Gr,p,C].
+
+    Follows quantization.py:82-112 (weights are quantized in physical [K,O]
+    coordinates).  ``packed_t`` is the column-major copy read by the MFMA kernel.
+    """
+    supported(config)
+    require_device(weight)
+    o, k = weight.shape
+    b = weight.detach().T.to(torch.float32).contiguous()  # [K, O]
+    if not torch.isfinite(b).all():
+        raise ValueError("quantized values must be finite in torch.float32")
+    if not config.weight_signed and (b < 0).any():
+        raise ValueError(
+            "unsigned floating weights must be nonnegative INT values; "
+            "use map_quantized with zero_points for affine weights"
+        )
+    scale, gr, gc = group_scales(b, config.weight_bits, config.weight_quant_gran,
+                                 signed=config.weight_signed)
+    return pack_codes(None, scale, config, k, o, gr, gc, source=b, transposed=transposed)
+
+
+def pack_codes(codes, scale, config, k, o, gr, gc, *, source=None, transposed=True):
+    """Quantize ``source`` [K,O] with group grid ``scale`` into packed tiles."""
+    r, c = config.array_size
+    m, p = math.ceil(k / r), math.ceil(o / c)
+    device = source.device
+    packed = torch.empty((m, p, r, c), dtype=torch.uint8, device=device)
+    packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=device) if transposed else None
+    wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        check(
+            library().mf_weight_tiles(
+                ct.byref(descriptor(config)), _ptr(source), k, o, o, _ptr(scale), gr, gc,
+                _ptr(packed), _ptr(packed_t), _ptr(wscale), _stream(device),
+            ),
+            "weight tiles",
+        )
+    return packed, packed_t, wscale
+
+
+def transpose_packed(packed, config):
+    """packed [m,p,R,C] -> packed_t [p*C, m*R] (for checkpoints and imported codes)."""
+    require_device(packed)
+    m, p, r, c = packed.shape
+    packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=packed.device)
+    src = packed.to(torch.uint8).contiguous()
+    with torch.cuda.device(packed.device):
+        check(
+            library().mf_transpose_packed(
+                ct.byref(descriptor(config)), _ptr(src), m, p, _ptr(packed_t),
+                _stream(packed.device),
+            ),
+            "transpose packed",
+        )
+    return packed_t
+
+
+# ---------------------------------------------------------------------------
+# Conductances, partial totals, fused product
+# ---------------------------------------------------------------------------
+def restore(packed, config, seed, event, begin, end):
+    """Programmed + read conductances g [planes, m, end-begin, W, R, C]."""
+    supported(config)
+    require_device(packed)
+    m, p, r, c = packed.shape
+    planes = restore_planes(config)
+    dtype = torch.float64 if config.precise_currents else torch.float32
+    g = torch.empty((planes, m, end - begin, len(config.weight_layout), r, c), dtype=dtype,
+                    device=packed.device)
+    src = packed.to(torch.uint8).contiguous()
+    with torch.cuda.device(packed.device):
+        check(
+            library().mf_restore(
+                ct.byref(descriptor(config)), _ptr(src), m, p, begin, end, seed, event, _ptr(g),
+                _stream(packed.device),
+            ),
+            "restore",
+        )
+    return g
+
+
+def _checked_conductance(g, config, m, width, r, c):
+    """Validate an injected or restored conductance tensor [planes, m, width, W, R, C]."""
+    expected = (restore_planes(config), m, width, len(config.weight_layout), r, c)
+    if g.dim() == 5:
+        g = g.unsqueeze(0)
+    if tuple(g.shape) != expected:
+        raise ValueError(f"conductance tensor must have shape {expected}, got {tuple(g.shape)}")
+    require_device(g)
+    return g.to(torch.float64 if config.precise_currents else torch.float32).contiguous()
+
+
+def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance=None,
+            codes=False):
+    """Integer slice totals T [N, m*Gr, end-begin, C] (FP32), as memfast/cuda.py:322-373.
+
+    ``conductance`` injects a [planes, m, end-begin, W, R, C] tensor in place of
+    the sampled one; ``codes=True`` also returns per-pair ADC counts
+    [N, m*Gr, A, W, (end-begin)*C] (int32).  ``schedule`` is accepted for
+    interface compatibility; the HIP kernels choose their own tiling.
+    """
+    supported(config)
+    require_device(q)
+    n, m, r = q.shape
+    p, c = packed.shape[1], config.array_size[1]
+    width = end - begin
+    g = conductance
+    if g is None and needs_conductances(config):
+        g = restore(packed, config, seed, event, begin, end)
+    if g is not None:
+        g = _checked_conductance(g, config, m, width, r, c)
+    groups = m * config.reads_per_array
+    totals = torch.empty((n, groups, width, c), dtype=torch.float32, device=q.device)
+    counts = None
+    if codes:
+        counts = torch.empty(
+            (n, groups, len(config.input_layout), len(config.weight_layout), width * c),
+            dtype=torch.int32, device=q.device,
+        )
+    with torch.cuda.device(q.device):
+        check(
+            library().mf_partial(
+                ct.byref(descriptor(config)), _ptr(q.contiguous()), n, m,
+                _ptr(packed.to(torch.uint8).contiguous()), p, begin, end, _ptr(g), seed, event,
+                _ptr(totals), _ptr(counts), _stream(q.device),
+            ),
+            "partial",
+        )
+    return (totals, counts) if codes else totals
+
+
+def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=None, out=None):
+    """Fused read + scale restore: [N, p*C] FP32, summed over reads in torch's order."""
+    supported(config)
+    require_device(q)
+    n, m, r = q.shape
+    p, c = packed.shape[1], config.array_size[1]
+    g = conductance
+    if g is None and needs_conductances(config):
+        g = restore(packed, config, seed, event, 0, p)
+    if g is not None:
+        g = _checked_conductance(g, config, m, p, r, c)
+        packed_t = None
+    if out is None:
+        out = torch.empty((n, p * c), dtype=torch.float32, device=q.device)
+    timer = kernel_timer
+    with torch.cuda.device(q.device):
+        if timer is not None:
+            start = torch.cuda.Event(enable_timing=True)
+            start.record()
+        check(
+            library().mf_mm(
+                ct.byref(descriptor(config)), _ptr(q.contiguous()), _ptr(xscale.contiguous()), n,
+                m, _ptr(packed.contiguous()), _ptr(packed_t), _ptr(wscale.contiguous()), p,
+                _ptr(g), seed, event, _ptr(out), out.stride(0), _stream(q.device),
+            ),
+            "mm",
+        )
+        if timer is not None:
+            end = torch.cuda.Event(enable_timing=True)
+            end.record()
+            timer.append((start, end))
+    return out
+
+
+def mm_kernel(config, n, m, p, has_packed_t=True):
+    """0: general kernel, 1: ideal-device MFMA kernel (what ``mm`` will launch)."""
+    out = ct.c_int32()
+    check(library().mf_mm_kernel(ct.byref(descriptor(config)), n, m, p, int(has_packed_t),
+                                 ct.byref(out)), "kernel selection")
+    return out.value
+
+
+# ---------------------------------------------------------------------------
+# RNG (parity tests)
+# ---------------------------------------------------------------------------
+def rng(address, seed, stream, kind="uniform"):
+    require_device(address)
+    addr = address.to(torch.int64).contiguous()
+    out = torch.empty(addr.shape, dtype=torch.float32, device=addr.device)
+    fn = library().mf_rng_uniform if kind == "uniform" else library().mf_rng_normal
+    with torch.cuda.device(addr.device):
+        check(fn(_ptr(addr), addr.numel(), int(seed) & (2**64 - 1), stream, _ptr(out),
+                 _stream(addr.device)), f"rng {kind}")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Compatibility surface of memfast/cuda.py
+# ---------------------------------------------------------------------------
+class Program:
+    """Resource view of the kernels (replaces the NVRTC Program, cuda.py:130-310)."""
+
+    def __init__(self, config, vectors, columns):
+        self.config = config
+        self.vectors = vectors
+        self.columns = columns
+
+    def resources(self, config, vectors, columns, workers):
+        info = MFResources()
+        kernel = 1 if config.nonidealities.ideal else 0
+        check(library().mf_resources_query(ct.byref(descriptor(config)), kernel, ct.byref(info)),
+              "resources")
+        return dict(threads=info.threads, shared=info.shared_bytes, local_bytes=info.local_bytes,
+                    registers=info.registers)
+
+
+@lru_cache(maxsize=256)
+def program(config, vectors, columns, device):
+    with torch.cuda.device(device):
+        torch.empty(0, device=device)
+        return Program(config, vectors, columns)
+
+
+def identity(device):
+    """Hardware identity hashed into the tuning-cache key."""
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    info = MFIdentity()
+    check(library().mf_device_identity(index, ct.byref(info)), "device identity")
+    return dict(
+        name=info.name.decode(),
+        arch=info.arch.decode(),
+        compute_units=info.compute_units,
+        memory=info.memory_bytes,
+        driver=info.driver_version,
+        runtime=info.runtime_version,
+        torch=torch.__version__,
+        hip=torch.version.hip,
+        kernels=native_source_hash(),
+    )
+
+
+__all__ = [
+    "ResourceError", "BackendError", "cache_root", "atomic_write", "partial", "program",
+    "identity", "mm", "restore", "input_tiles", "weight_tiles", "transpose_packed",
+]

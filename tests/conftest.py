@@ -1,0 +1,30 @@
+"""Shared pytest setup: the `gpu` marker, import paths and golden fixtures."""
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLDEN = ROOT / "tests" / "golden"
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a HIP (MI355X) device")
+
+
+@pytest.fixture(scope="session")
+def reference_vectors():
+    return dict(np.load(GOLDEN / "reference_vectors.npz", allow_pickle=False))
+
+
+@pytest.fixture(scope="session")
+def hip_device():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    return torch.device("cuda", 0)

@@ -1,0 +1,100 @@
+"""The C-ABI library loads on any host and exports every symbol include/memfast_hip.h declares.
+
+No compute call is made here (no GPU in the build container).
+"""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from memfast_amd import hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "memfast_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(mf_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "mf_mm" in names and "mf_partial" in names and len(names) >= 14
+
+
+def test_library_exports_every_declared_symbol():
+    lib = hip.library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(hip.LIBRARY)], capture_output=True,
+                        text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (mf_\w+)", nm))
+    assert set(declared_functions()) <= exported
+
+
+def test_ctypes_signatures_cover_header():
+    assert set(hip.SIGNATURES) == set(declared_functions())
+
+
+def test_abi_version_and_hash():
+    lib = hip.library()
+    assert lib.mf_abi_version() == hip.ABI_VERSION
+    from memfast_amd.build_native import source_hash
+
+    assert hip.native_source_hash() == source_hash(), "library is stale: rebuild it"
+
+
+def test_struct_layout_matches_c(tmp_path):
+    """Offsets of mf_config / sizes of mf_identity and mf_resources agree with gcc's."""
+    fields = [name for name, _ in hip.MFConfig._fields_]
+    probe = tmp_path / "layout.c"
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(){"]
+    lines += [f'printf("%zu\\n", offsetof(mf_config, {name}));' for name in fields]
+    lines += ['printf("%zu\\n%zu\\n%zu\\n", sizeof(mf_config), sizeof(mf_identity), '
+              'sizeof(mf_resources)); return 0;}']
+    probe.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(probe)], check=True)
+    values = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
+                                             check=True).stdout.split()]
+    offsets = [getattr(hip.MFConfig, name).offset for name in fields]
+    assert values[:len(fields)] == offsets
+    assert values[len(fields):] == [ctypes.sizeof(hip.MFConfig), ctypes.sizeof(hip.MFIdentity),
+                                    ctypes.sizeof(hip.MFResources)]
+
+
+def test_error_reporting_without_device():
+    """Invalid descriptors are rejected on the host before any launch."""
+    lib = hip.library()
+    bad = hip.MFConfig()
+    bad.abi_version = 999
+    out = ctypes.c_int32()
+    status = lib.mf_mm_kernel(ctypes.byref(bad), 1, 1, 1, 1, ctypes.byref(out))
+    assert status == hip.E_INVALID
+    assert b"ABI version" in lib.mf_last_error()
+    with pytest.raises(ValueError):
+        hip.check(status, "probe")
+
+
+def test_descriptor_fp32_constants():
+    import math
+    import struct
+
+    from memfast_amd import Config, Nonidealities
+
+    cfg = Config(nonidealities=Nonidealities(read_variation=0.03, adc_nonlinearity=0.1))
+    d = hip.descriptor(cfg)
+
+    def f32(x):
+        return struct.unpack("f", struct.pack("f", x))[0]
+
+    assert d.f_span == f32(cfg.high_conductance - cfg.low_conductance)
+    assert d.f_inv_unit == f32(1 / cfg.current_unit)
+    assert d.f_two_pi == f32(2 * math.pi)
+    assert d.f_out_mean == f32(math.expm1(0.5 * 0.03**2))
+    assert list(d.adc_max)[:len(cfg.adc_maxima)] == list(cfg.adc_maxima)
+    assert d.f_alpha_over_max[0] == f32(0.1 / cfg.adc_maxima[0])

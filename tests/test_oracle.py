@@ -1,0 +1,279 @@
+"""Pins of the CPU oracle (oracle/oracle.py) against reference-held data and mathematics.
+
+* LeNet checkpoints shipped with the reference: INT4 codes, packing, seeds.
+* The DFT notebook known answer (examples/notebooks/03_dft_image_denoising.ipynb:374-386).
+* Vectors written by tests/golden/make_reference_vectors.py from the reference CPU path.
+* A scalar C restatement (oracle/brute.c) of the ideal ADC closed form and the RNG hash.
+"""
+
+import ctypes
+import math
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from memfast_amd import Config, Nonidealities
+from oracle import oracle
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLDEN = ROOT / "tests" / "golden"
+
+
+@pytest.fixture(scope="module")
+def brute():
+    lib_path = ROOT / "oracle" / "libbrute.so"
+    if not lib_path.exists():
+        subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    lib = ctypes.CDLL(str(lib_path))
+    lib.brute_mix.argtypes = [ctypes.c_uint32]
+    lib.brute_mix.restype = ctypes.c_uint32
+    lib.brute_uniform_bits.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]
+    lib.brute_uniform_bits.restype = ctypes.c_uint32
+    lib.brute_event_seed.argtypes = [ctypes.c_uint32, ctypes.c_uint64]
+    lib.brute_event_seed.restype = ctypes.c_uint64
+    return lib
+
+
+def _cfg(case, **extra):
+    base = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                weight_slice=(1, 1, 2, 2, 2), array_size=(32, 16), rows_per_read=16,
+                weight_quant_gran=(16, 1), input_quant_gran=(1, 16), adc_bits=(6, 7, 7, 8, 8))
+    noise = {
+        "ideal": dict(write_variation=0.0),
+        "write": dict(write_variation=0.02),
+        "shared": dict(write_variation=0.02, read_variation=0.01, adc_nonlinearity=0.1),
+        "slice_pair": dict(write_variation=0.02, read_variation=0.02, read_mode="slice_pair"),
+        "output": dict(write_variation=0.02, read_variation=0.02, read_mode="output"),
+        "voltage": dict(write_variation=0.0, voltage_variation=0.05),
+        "saf_drift": dict(write_variation=0.02, stuck_at_low=0.05, stuck_at_high=0.03,
+                          drift_coefficient=0.05, drift_time=100.0),
+        "binary_int4": dict(write_variation=0.02),
+    }[case]
+    if case == "binary_int4":
+        base = dict(activation_bits=8, weight_bits=4, array_size=(64, 64), adc_bits=6)
+    base.update(extra)
+    return Config(**base, nonidealities=Nonidealities(**noise))
+
+
+# ---------------------------------------------------------------------------
+# RNG
+# ---------------------------------------------------------------------------
+def test_rng_matches_reference_vectors(reference_vectors):
+    v = reference_vectors
+    addresses = torch.from_numpy(v["rng_address"])
+    for si, seed in enumerate(v["rng_seeds"].tolist()):
+        for ti, stream in enumerate(v["rng_streams"].tolist()):
+            u = oracle.uniform(addresses, int(seed), int(stream)).numpy()
+            z = oracle.normal(addresses, int(seed), int(stream)).numpy()
+            np.testing.assert_array_equal(u, v["rng_uniform"][si, ti])
+            np.testing.assert_array_equal(z, v["rng_normal"][si, ti])
+
+
+def test_event_seed_and_mix_vectors(reference_vectors, brute):
+    v = reference_vectors
+    for (seed, event), expected in zip(v["event_pairs"].tolist(), v["event_seeds"].tolist()):
+        assert oracle.event_seed(int(seed), int(event)) == expected
+        assert brute.brute_event_seed(int(seed), int(event)) == expected
+    for x, expected in zip(v["mix_in"].tolist(), v["mix_out"].tolist()):
+        assert oracle.mix_int(int(x)) == expected
+        assert brute.brute_mix(int(x)) == expected
+
+
+def test_uniform_c_restatement(reference_vectors, brute):
+    v = reference_vectors
+    for si, seed in enumerate(v["rng_seeds"].tolist()):
+        for ti, stream in enumerate(v["rng_streams"].tolist()):
+            bits = np.array([brute.brute_uniform_bits(int(a) & (2**64 - 1), int(seed), int(stream))
+                             for a in v["rng_address"].tolist()], dtype=np.float64)
+            np.testing.assert_array_equal(((bits + 0.5) / 2**24).astype(np.float32),
+                                          v["rng_uniform"][si, ti])
+
+
+def test_uniform_distribution():
+    """Uniforms are FP32(h + 0.5) / 2^24 for 24-bit h: multiples of 2^-25 in (0,1)."""
+    address = torch.arange(200000, dtype=torch.int64) * 7919 + 2**33
+    u = oracle.uniform(address, 4017293833, 10).double()
+    scaled = u * 2**25
+    assert torch.equal(scaled, scaled.round())
+    assert 0 < u.min() and u.max() < 1
+    assert abs(u.mean().item() - 0.5) < 3e-3
+    counts = torch.histc(u, bins=16, min=0, max=1)
+    expected = len(u) / 16
+    chi2 = ((counts - expected) ** 2 / expected).sum().item()
+    assert chi2 < 40  # 15 dof, p ~ 5e-4
+    z = oracle.normal(address, 4017293833, 10).double()
+    assert abs(z.mean().item()) < 0.01 and abs(z.std().item() - 1) < 0.01
+
+
+def test_seed_names_from_checkpoint():
+    data = np.load(GOLDEN / "lenet_int4.npz", allow_pickle=False)
+    for index in range(int(data["count"])):
+        name = str(data[f"l{index}_name"])
+        assert oracle.name_seed(135, name) == int(data[f"l{index}_seed"])
+    assert oracle.name_seed(135, "matrix.0") == 4017293833
+    assert oracle.name_seed(135, "matrix.1") == 3292730091
+
+
+# ---------------------------------------------------------------------------
+# Quantization / packing
+# ---------------------------------------------------------------------------
+def test_lenet_int4_codes_from_float_checkpoint():
+    data = np.load(GOLDEN / "lenet_int4.npz", allow_pickle=False)
+    cfg = Config(activation_bits=8, weight_bits=4, array_size=(64, 64), adc_bits=6,
+                 input_quant_gran=(1, None), weight_quant_gran=(None, 1))
+    for index in range(int(data["count"])):
+        weight = torch.from_numpy(data[f"l{index}_weight"])
+        packed, scale = oracle.weight_tiles(weight, cfg)
+        np.testing.assert_array_equal(packed.numpy(), data[f"l{index}_packed"])
+        stored = torch.from_numpy(data[f"l{index}_weight_scale"])
+        # The shipped scales came from a CUDA reciprocal multiply; the CPU reference
+        # divides.  They agree to 1 ulp.
+        ulp = torch.nextafter(stored, torch.full_like(stored, math.inf)) - stored
+        assert ((scale - stored).abs() <= ulp).all()
+        peak = weight.abs().amax(1)
+        expected = torch.where(peak > 0, peak, torch.ones_like(peak)) / 7
+        o = weight.shape[0]
+        assert torch.equal(scale.reshape(scale.shape[0], -1)[0, :o], expected)
+
+
+def test_fixed_input_scale_fixture():
+    data = np.load(GOLDEN / "lenet_int4.npz", allow_pickle=False)
+    for index in range(int(data["count"])):
+        maximum = float(data[f"l{index}_maximum"])
+        scale = max(maximum if maximum > 0 else 1.0, torch.finfo(torch.float32).tiny) / 127
+        stored = data[f"l{index}_input_scale"]
+        assert np.all(stored == np.float32(scale))
+
+
+def test_round_half_even_and_clamp():
+    cfg = Config(activation_bits=4, weight_bits=4, array_size=(8, 4), input_quant_gran=(1, None))
+    # max 7 -> scale 1; values at .5 boundaries round to even.
+    x = torch.tensor([[7.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, -7.0]])
+    q, xs = oracle.input_tiles(x, cfg)
+    codes = q.flatten().long()
+    signed = torch.where(codes >= 8, codes - 16, codes)
+    assert signed.tolist() == [7, 0, 2, 2, 0, -2, -2, -7]
+    assert xs.flatten().tolist() == [1.0]
+
+
+def test_read_starts_and_padding():
+    cfg = Config(array_size=(10, 4), rows_per_read=4, input_quant_gran=(1, None),
+                 weight_quant_gran=(None, 1))
+    assert oracle.read_starts(2, cfg).tolist() == [0, 4, 8, 10, 14, 18]
+    x = torch.arange(1, 16, dtype=torch.float32)[None]  # K=15 -> m=2, padded to 20
+    q, xs = oracle.input_tiles(x, cfg)
+    assert q.shape == (1, 2, 10) and xs.shape == (1, 6)
+    assert q.flatten()[15:].tolist() == [0] * 5
+
+
+def test_reference_fixture_tiles(reference_vectors):
+    v = reference_vectors
+    for name in v["case_names"].tolist():
+        cfg = _cfg(name)
+        a = torch.from_numpy(v[f"case_{name}_a"])
+        b = torch.from_numpy(v[f"case_{name}_b"])
+        packed, wscale = oracle.weight_tiles(b.T, cfg)
+        q, xscale = oracle.input_tiles(a, cfg)
+        np.testing.assert_array_equal(packed.numpy(), v[f"case_{name}_packed"])
+        np.testing.assert_array_equal(wscale.numpy(), v[f"case_{name}_wscale"])
+        np.testing.assert_array_equal(q.numpy(), v[f"case_{name}_q"])
+        np.testing.assert_array_equal(xscale.numpy(), v[f"case_{name}_xscale"])
+
+
+# ---------------------------------------------------------------------------
+# Array reads
+# ---------------------------------------------------------------------------
+def test_reference_fixture_reads(reference_vectors):
+    v = reference_vectors
+    for name in v["case_names"].tolist():
+        cfg = _cfg(name)
+        packed = torch.from_numpy(v[f"case_{name}_packed"])
+        q = torch.from_numpy(v[f"case_{name}_q"])
+        seed = int(v[f"case_{name}_seed"])
+        p = packed.shape[1]
+        raw, _, _ = oracle.restored(packed, cfg, seed, 0, 0, p)
+        np.testing.assert_array_equal(raw.numpy(), v[f"case_{name}_restored"])
+        totals = oracle.partial(q, packed, cfg, seed, 0, 0, p)
+        np.testing.assert_array_equal(totals.numpy(), v[f"case_{name}_totals"])
+
+
+def test_reference_fixture_mm(reference_vectors):
+    v = reference_vectors
+    for name in v["case_names"].tolist():
+        cfg = _cfg(name)
+        a = torch.from_numpy(v[f"case_{name}_a"])
+        b = torch.from_numpy(v[f"case_{name}_b"])
+        np.testing.assert_array_equal(oracle.mm(a, b, cfg).numpy(), v[f"case_{name}_out0"])
+        np.testing.assert_array_equal(oracle.mm(a, b, cfg, event=1).numpy(),
+                                      v[f"case_{name}_out1"])
+
+
+def _brute_totals(brute, q, packed, cfg):
+    n, m, r = q.shape
+    p, c = packed.shape[1], cfg.array_size[1]
+    il, wl = oracle.input_layout(cfg), oracle.weight_layout(cfg)
+    gr = oracle.reads_per_array(cfg)
+    out = np.zeros((n, m * gr, p, c), dtype=np.int64)
+    i32 = ctypes.c_int * len(il)
+    w32 = ctypes.c_int * len(wl)
+    i64a = ctypes.c_int64 * len(il)
+    i64w = ctypes.c_int64 * len(wl)
+    qn = np.ascontiguousarray(q.numpy())
+    pn = np.ascontiguousarray(packed.numpy())
+    brute.brute_ideal_totals(
+        qn.ctypes.data_as(ctypes.c_void_p), pn.ctypes.data_as(ctypes.c_void_p), n, m, p, r, c,
+        oracle.read_rows(cfg), len(il), i32(*[e[0] for e in il]), i32(*[e[1] for e in il]),
+        i64a(*[e[2] for e in il]), len(wl), w32(*[e[0] for e in wl]), w32(*[e[1] for e in wl]),
+        i64w(*[e[2] for e in wl]), w32(*oracle.adc_maxima(cfg)),
+        out.ctypes.data_as(ctypes.c_void_p),
+    )
+    return out
+
+
+@pytest.mark.parametrize("kwargs,shape", [
+    (dict(array_size=(32, 16), rows_per_read=16, input_slice=(1, 1, 2, 2, 2),
+          weight_slice=(1, 1, 2, 2, 2), adc_bits=(6, 7, 7, 8, 8)), (5, 70, 40)),
+    (dict(array_size=(20, 8), rows_per_read=7, adc_bits=4), (3, 45, 9)),
+    (dict(activation_bits=6, weight_bits=4, array_size=(16, 8), weight_slice=(1, 3), adc_bits=3),
+     (4, 40, 11)),
+    (dict(weight_bits=4, weight_signed=False, weight_slice=(2, 2), array_size=(16, 4),
+          adc_bits=5), (2, 33, 6)),
+])
+def test_ideal_partial_matches_closed_form_and_brute(brute, kwargs, shape):
+    cfg = Config(**kwargs, nonidealities=Nonidealities(write_variation=0.0))
+    torch.manual_seed(7)
+    n, k, o = shape
+    a = torch.randn(n, k)
+    b = torch.randn(k, o).abs() if not cfg.weight_signed else torch.randn(k, o)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    q, _ = oracle.input_tiles(a, cfg)
+    totals = oracle.partial(q, packed, cfg, 1, 0, 0, packed.shape[1])
+    closed = oracle.ideal_totals_closed_form(q, packed, cfg)
+    assert torch.equal(totals.long(), closed)
+    assert np.array_equal(_brute_totals(brute, q, packed, cfg), closed.numpy())
+
+
+def test_dft_known_answer():
+    """examples/notebooks/03_dft_image_denoising.ipynb:374-386 (recorded max error 9.537e-07)."""
+    size = 256
+    idx = np.arange(size)
+    basis = np.exp(-2j * np.pi * np.outer(idx, idx) / size) / np.sqrt(size)
+    weight = torch.tensor(basis.real, dtype=torch.float32)
+    vectors = torch.linspace(-1, 1, 3 * size).reshape(3, size)
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1,) * 8, weight_slice=(1,) * 8,
+                 array_size=(64, 64), adc_bits=8, input_quant_gran=(1, 64),
+                 weight_quant_gran=(None, 1), seed=135,
+                 nonidealities=Nonidealities(write_variation=0.0))
+    wscale = weight.abs().amax(dim=0, keepdim=True) / 127
+    groups = vectors.reshape(3, size // 64, 64)
+    iscale = (groups.abs().amax(dim=-1, keepdim=True) / 127).expand_as(groups).reshape_as(vectors)
+    dq_w = (weight / wscale).round().clamp(-127, 127) * wscale
+    dq_x = (vectors / iscale).round().clamp(-127, 127) * iscale
+    expected = dq_x @ dq_w
+    actual = oracle.mm(vectors, weight, cfg)
+    # The notebook's own assertion; its recorded 9.537e-07 came from the CUDA path,
+    # whose summation order differs from the CPU reference's.
+    torch.testing.assert_close(actual, expected, rtol=1e-5, atol=2e-5)
