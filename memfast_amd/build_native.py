@@ -27,6 +27,9 @@ FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
+    # No implicit FMA contraction: the CPU reference rounds every product and
+    # sum separately (explicit fma() calls are kept where intended).
+    "-ffp-contract=off",
     # Packed FP32 VALU forms are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
@@ -38,7 +41,7 @@ def source_files():
 
 def source_hash():
     """SHA-256 over every native source and the public header."""
-    digest = hashlib.sha256()
+    digest = hashlib.sha256(" ".join(FLAGS).encode())
     for path in [*sorted(SOURCES.glob("*")), HEADER]:
         if path.is_file() and path.suffix in (".hip", ".h"):
             digest.update(path.name.encode())

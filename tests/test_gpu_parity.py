@@ -26,14 +26,33 @@ def say(*args):
     print("[gpu-parity]", *args, flush=True)
 
 
+class BitsEqual:
+    """Truthy bitwise comparison whose repr explains a mismatch."""
+
+    def __init__(self, a, b):
+        a, b = a.detach().cpu().contiguous(), b.detach().cpu().contiguous().to(a.dtype)
+        assert a.shape == b.shape, (a.shape, b.shape)
+        if a.dtype.is_floating_point:
+            view = torch.int32 if a.dtype == torch.float32 else torch.int64
+            diff = a.view(view) != b.view(view)
+        else:
+            diff = a != b
+        self.ok = not bool(diff.any())
+        self.count = int(diff.sum())
+        self.total = diff.numel()
+        self.max_abs = float((a.double() - b.double()).abs().max()) if self.count else 0.0
+        self.first = diff.nonzero()[:3].tolist() if self.count else []
+
+    def __bool__(self):
+        return self.ok
+
+    def __repr__(self):
+        return (f"BitsEqual({self.count}/{self.total} differ, max |diff| {self.max_abs:.3e}, "
+                f"first at {self.first})")
+
+
 def bits_equal(a, b):
-    a, b = a.detach().cpu().contiguous(), b.detach().cpu().contiguous()
-    assert a.shape == b.shape, (a.shape, b.shape)
-    if a.dtype.is_floating_point:
-        return torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a.view(torch.int64),
-                           b.to(a.dtype).view(torch.int32) if a.dtype == torch.float32
-                           else b.to(a.dtype).view(torch.int64))
-    return torch.equal(a, b.to(a.dtype))
+    return BitsEqual(a, b)
 
 
 def ideal(**kwargs):
