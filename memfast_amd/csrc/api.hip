@@ -105,16 +105,48 @@ int byte_mask(int shift, int mask, bool sign_slice) {
 
 u32 replicate(int m) { return u32(m) * 0x01010101u; }
 
+// Operand masks of one slice: natural (two's complement value = factor*digit,
+// sign-extended for codes narrower than 8 bits) and positive (value =
+// |factor|*digit, halved for the sign bit of an 8-bit code).
+struct SliceForm {
+    u32 nat, pos;
+    int shift;      // positive form shifted right by one (8-bit sign slice)
+    int posval;     // positive operand value per digit unit
+    int sign;       // sign of the factor
+    int scale;      // factor = sign * posval * scale
+};
+
+SliceForm slice_form(int shift, int mask, int64_t factor, bool sign_slice, int bits) {
+    SliceForm f{};
+    f.nat = replicate(byte_mask(shift, mask, sign_slice && bits < 8));
+    f.sign = factor < 0 ? -1 : 1;
+    const int64_t mag = factor < 0 ? -factor : factor;
+    if (sign_slice && shift == 7) {
+        f.pos = replicate(0x80);
+        f.shift = 1;
+        f.posval = 64;
+        f.scale = 2;
+    } else {
+        f.pos = replicate((mask << shift) & 0xFF);
+        f.shift = 0;
+        f.posval = int(mag);
+        f.scale = 1;
+    }
+    if (sign_slice && bits == 8) f.nat = replicate(0x80);
+    return f;
+}
+
 // Ideal-device MFMA eligibility and plan.  Returns false (with reason) when the
 // general kernel must be used.
-bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, int *ks,
-                      const char **why) {
+bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotTests *xtests,
+                      SlotTests *wtests, int *ks, const char **why) {
     if (cfg->has_write || cfg->has_read || cfg->has_vnoise || cfg->has_nonlinear || cfg->has_saf ||
         cfg->has_drift) {
         *why = "device effects enabled";
         return false;
     }
     if (!cfg->weight_signed) { *why = "unsigned weights"; return false; }
+    if (cfg->n_in > IDEAL_MAX_CA || cfg->n_w > IDEAL_MAX_CW) { *why = "too many slices"; return false; }
     if (cfg->read_rows % 32 || cfg->rows % cfg->read_rows || cfg->read_rows > 64) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
         return false;
@@ -137,7 +169,6 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, int *
             if (zcap * rel > bound_abs) bound_abs = zcap * rel;
         }
     if (bound_abs >= 0.25) { *why = "FP32 currents may move ADC counts"; return false; }
-    // int32 accumulators: the reconstruction bound of the slice totals.
     double fa_sum = 0.0, fw_sum = 0.0;
     for (int a = 0; a < cfg->n_in; ++a) fa_sum += std::fabs(double(cfg->in_factor[a]));
     for (int w = 0; w < cfg->n_w; ++w)
@@ -145,45 +176,101 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, int *
     if (fa_sum * fw_sum >= 2147483647.0) { *why = "slice totals exceed int32"; return false; }
 
     memset(plan, 0, sizeof(*plan));
+    bool is_free[MF_MAX_SLICES][MF_MAX_SLICES];
     unsigned free_sets[MF_MAX_SLICES];
     for (int w = 0; w < cfg->n_w; ++w) {
-        unsigned set = 0;
+        free_sets[w] = 0;
         for (int a = 0; a < cfg->n_in; ++a) {
             const i64 smax = i64(P) * cfg->in_mask[a] * cfg->w_mask[w];
-            if (smax <= cfg->adc_max[w]) set |= 1u << a;
+            is_free[a][w] = smax <= cfg->adc_max[w];
+            if (is_free[a][w]) free_sets[w] |= 1u << a;
         }
-        free_sets[w] = set;
     }
+    SliceForm xf[MF_MAX_SLICES], wf[MF_MAX_SLICES];
+    for (int a = 0; a < cfg->n_in; ++a)
+        xf[a] = slice_form(cfg->in_shift[a], cfg->in_mask[a], cfg->in_factor[a],
+                           a == cfg->n_in - 1, cfg->activation_bits);
+    for (int w = 0; w < cfg->n_w; ++w)
+        wf[w] = slice_form(cfg->w_shift[w], cfg->w_mask[w], cfg->w_factor[w],
+                           w == cfg->n_w - 1, cfg->weight_bits);
+    // Static linear terms: weight slices grouped by their clamp-free input sets.
     bool grouped[MF_MAX_SLICES] = {false};
     for (int w = 0; w < cfg->n_w; ++w) {
         if (grouped[w] || free_sets[w] == 0) continue;
-        int amask = 0, bmask = 0;
+        u32 xmask = 0, wmask = 0;
         for (int a = 0; a < cfg->n_in; ++a)
-            if (free_sets[w] >> a & 1)
-                amask |= byte_mask(cfg->in_shift[a], cfg->in_mask[a], a == cfg->n_in - 1);
+            if (free_sets[w] >> a & 1) xmask |= xf[a].nat;
         for (int v = w; v < cfg->n_w; ++v)
             if (!grouped[v] && free_sets[v] == free_sets[w]) {
                 grouped[v] = true;
-                bmask |= byte_mask(cfg->w_shift[v], cfg->w_mask[v], v == cfg->n_w - 1);
+                wmask |= wf[v].nat;
             }
         if (plan->n_lin >= IDEAL_MAX_LIN) { *why = "too many linear terms"; return false; }
-        plan->lin_a[plan->n_lin] = replicate(amask);
-        plan->lin_b[plan->n_lin] = replicate(bmask);
+        plan->lin_w[plan->n_lin] = wmask;
+        plan->lin_x[plan->n_lin] = xmask;
         ++plan->n_lin;
     }
+    // Clamp-candidate grid: slot cw * 8 + ca.
+    int ca_of[MF_MAX_SLICES], cw_of[MF_MAX_SLICES];
+    for (int a = 0; a < cfg->n_in; ++a) {
+        ca_of[a] = -1;
+        for (int w = 0; w < cfg->n_w; ++w)
+            if (!is_free[a][w]) { ca_of[a] = plan->n_ca++; break; }
+        if (ca_of[a] >= 0) {
+            const int ca = ca_of[a];
+            plan->ca_xnat[ca] = xf[a].nat;
+            plan->ca_xpos[ca] = xf[a].pos;
+            plan->ca_posval[ca] = xf[a].posval;
+            plan->ca_msign[ca] = xf[a].sign * xf[a].scale;
+            if (xf[a].shift) plan->xshift_bits |= 1u << ca;
+            if (xf[a].nat == xf[a].pos && !xf[a].shift) plan->same_bits |= 1u << ca;
+        }
+    }
+    for (int w = 0; w < cfg->n_w; ++w) {
+        cw_of[w] = -1;
+        for (int a = 0; a < cfg->n_in; ++a)
+            if (!is_free[a][w]) { cw_of[w] = plan->n_cw++; break; }
+        if (cw_of[w] >= 0) {
+            const int cw = cw_of[w];
+            plan->cw_wnat[cw] = wf[w].nat;
+            plan->cw_wpos[cw] = wf[w].pos;
+            plan->cw_posmax[cw] = wf[w].posval * cfg->adc_max[w];
+            plan->cw_msign[cw] = wf[w].sign * wf[w].scale;
+            if (wf[w].shift) plan->wshift_bits |= 1u << cw;
+        }
+    }
+    memset(xtests, 0, sizeof(*xtests));
+    memset(wtests, 0, sizeof(*wtests));
     for (int a = 0; a < cfg->n_in; ++a)
         for (int w = 0; w < cfg->n_w; ++w) {
-            if (free_sets[w] >> a & 1) continue;
-            if (plan->n_clamp >= IDEAL_MAX_CLAMP) { *why = "too many clamped pairs"; return false; }
-            const int c = plan->n_clamp++;
-            plan->cl_a[c] = replicate(byte_mask(cfg->in_shift[a], cfg->in_mask[a], a == cfg->n_in - 1));
-            plan->cl_b[c] = replicate(byte_mask(cfg->w_shift[w], cfg->w_mask[w], w == cfg->n_w - 1));
-            const i64 f = cfg->in_factor[a] * cfg->w_factor[w];
-            plan->cl_val[c] = int(f * cfg->adc_max[w]);
-            plan->cl_upper[c] = f > 0 ? 1 : 0;
+            if (is_free[a][w]) continue;
+            const int slot = ca_of[a] * 8 + cw_of[w];
+            plan->exists |= uint64_t(1) << slot;
+            // S <= Mw * sum_r da  and  S <= Ma * sum_r dw.
+            xtests->exists |= uint64_t(1) << slot;
+            xtests->slice[slot] = a;
+            xtests->thr[slot] = cfg->adc_max[w] / cfg->w_mask[w];
+            wtests->exists |= uint64_t(1) << slot;
+            wtests->slice[slot] = w;
+            wtests->thr[slot] = cfg->adc_max[w] / cfg->in_mask[a];
         }
     *ks = P / 32;
     return true;
+}
+
+i64 align256(i64 x) { return (x + 255) / 256 * 256; }
+
+void ideal_workspace(const mf_config *cfg, i64 n, i64 m, i64 p, i64 *xbytes, i64 *wbytes) {
+    const i64 G = m * cfg->reads;
+    *xbytes = align256((n + 63) / 64 * G * 8);
+    *wbytes = align256((p * cfg->cols + 31) / 32 * G * 8);
+}
+
+SliceLayout layout_of(const int32_t *shift, const int32_t *mask, int count) {
+    SliceLayout l{};
+    l.count = count;
+    for (int i = 0; i < count; ++i) { l.shift[i] = shift[i]; l.mask[i] = mask[i]; }
+    return l;
 }
 
 template <typename Phys>
@@ -371,16 +458,28 @@ int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t 
     if (status) return status;
     if (!kernel_id) return fail(MF_E_INVALID, "kernel_id is NULL");
     IdealPlan plan;
+    SlotTests xt, wt;
     int ks = 0;
     const char *why = "";
-    *kernel_id = (has_packed_t && build_ideal_plan(cfg, m, p, &plan, &ks, &why)) ? 1 : 0;
+    *kernel_id = (has_packed_t && build_ideal_plan(cfg, m, p, &plan, &xt, &wt, &ks, &why)) ? 1 : 0;
     (void)n;
+    return MF_OK;
+}
+
+int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64_t *bytes) {
+    int status = check_config(cfg);
+    if (status) return status;
+    if (!bytes || n < 1 || m < 1 || p < 1) return fail(MF_E_INVALID, "invalid workspace query");
+    i64 xb, wb;
+    ideal_workspace(cfg, n, m, p, &xb, &wb);
+    *bytes = xb + wb;
     return MF_OK;
 }
 
 int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
-          const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo, void *stream) {
+          const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo, void *workspace,
+          int64_t workspace_bytes, void *stream) {
     int status = check_config(cfg);
     if (status) return status;
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
@@ -393,33 +492,55 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
     int ks = 0;
     const char *why = "";
     const bool aligned = (reinterpret_cast<uintptr_t>(q) % 16 == 0) &&
-                         (reinterpret_cast<uintptr_t>(packed_t) % 16 == 0);
-    if (!g && packed_t && aligned && build_ideal_plan(cfg, m, p, &plan, &ks, &why)) {
+                         (reinterpret_cast<uintptr_t>(packed_t) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(out) % 16 == 0) && ldo % 4 == 0;
+    i64 xbytes = 0, wbytes = 0;
+    ideal_workspace(cfg, n, m, p, &xbytes, &wbytes);
+    const bool room = workspace && workspace_bytes >= xbytes + wbytes;
+    SlotTests xtests, wtests;
+    if (!g && packed_t && aligned && room &&
+        build_ideal_plan(cfg, m, p, &plan, &xtests, &wtests, &ks, &why)) {
+        uint64_t *xbits = static_cast<uint64_t *>(workspace);
+        uint64_t *wbits = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) + xbytes);
+        const i64 kp = m * cfg->rows, ncols = p * cfg->cols;
+        const SliceLayout xl = layout_of(cfg->in_shift, cfg->in_mask, cfg->n_in);
+        const SliceLayout wl = layout_of(cfg->w_shift, cfg->w_mask, cfg->n_w);
+        hipLaunchKernelGGL(k_digit_bits, dim3(grid_for(G * ((n + 63) / 64 * 64))), dim3(256), 0, s,
+                           q, n, kp, G, cfg->reads, cfg->rows, cfg->read_rows, xl, 64, xtests, xbits);
+        hipLaunchKernelGGL(k_digit_bits, dim3(grid_for(G * ((ncols + 63) / 64 * 64))), dim3(256), 0,
+                           s, packed_t, ncols, kp, G, cfg->reads, cfg->rows, cfg->read_rows, wl, 32,
+                           wtests, wbits);
         IdealArgs args{};
         args.q = q;
         args.wt = packed_t;
         args.xscale = xscale;
         args.wscale = wscale;
+        args.xbits = xbits;
+        args.wbits = wbits;
         args.out = out;
         args.n = n;
-        args.kp = m * cfg->rows;
+        args.kp = kp;
         args.G = G;
         args.ldo = ldo;
-        args.ldws = p * cfg->cols;
-        args.ncols = p * cfg->cols;
+        args.ldws = ncols;
+        args.ncols = ncols;
         args.Gr = cfg->reads;
         args.R = cfg->rows;
         args.P = cfg->read_rows;
         args.a_bits = cfg->activation_bits;
         args.w_bits = cfg->weight_bits;
-        constexpr int BM = 64, BN = 128;
-        const i64 gy = (n + BM - 1) / BM, gx = (args.ncols + BN - 1) / BN;
+        const int tn = ks == 1 ? 2 : 1;
+        const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (ncols + 63) / 64;
         if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
         const dim3 grid{unsigned(gx), unsigned(gy), 1u};
-        if (ks == 1)
-            hipLaunchKernelGGL((k_ideal<1, 2, 1>), grid, dim3(256), 0, s, plan, args);
-        else
-            hipLaunchKernelGGL((k_ideal<1, 2, 2>), grid, dim3(256), 0, s, plan, args);
+        const bool small = plan.n_ca <= 4 && plan.n_cw <= 4;
+        if (ks == 1) {
+            if (small) hipLaunchKernelGGL((k_ideal<2, 1, 4, 4>), grid, dim3(256), 0, s, plan, args);
+            else hipLaunchKernelGGL((k_ideal<2, 1, 8, 8>), grid, dim3(256), 0, s, plan, args);
+        } else {
+            if (small) hipLaunchKernelGGL((k_ideal<1, 2, 4, 4>), grid, dim3(256), 0, s, plan, args);
+            else hipLaunchKernelGGL((k_ideal<1, 2, 8, 8>), grid, dim3(256), 0, s, plan, args);
+        }
         return check_launch("ideal MFMA read");
     }
     if (!g && needs_conductances(cfg))
@@ -454,7 +575,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     hipFuncAttributes attr;
     hipError_t e;
     if (kernel_id == 1)
-        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_ideal<1, 2, 1>));
+        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_ideal<2, 1, 4, 4>));
     else if (cfg->precise)
         e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<double, 4, false>));
     else
@@ -466,7 +587,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     out->registers = attr.numRegs;
     out->local_bytes = int32_t(attr.localSizeBytes);
     int blocks = 0;
-    const void *fn = kernel_id == 1 ? reinterpret_cast<const void *>(&k_ideal<1, 2, 1>)
+    const void *fn = kernel_id == 1 ? reinterpret_cast<const void *>(&k_ideal<2, 1, 4, 4>)
                                     : reinterpret_cast<const void *>(&k_general<float, 8, false>);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) == hipSuccess)
         out->max_blocks_per_cu = blocks;

@@ -1,24 +1,28 @@
 // Ideal-device sliced array read on gfx950 int8 MFMA, fused with the scale
 // restore and torch's read-order summation.  Only `out` is written to HBM.
 //
-// With every device effect off the ADC count of a slice pair is the closed form
-//   code(a,w) = min(S_aw, max_w),  S_aw = sum_r da[n,r] * dw[r,c]
-// (memfast/reference.py:63-117 with ideal conductances; exact because FP32
-// current errors stay far below half a count, checked on the host).  The host
-// splits the A*W slice pairs into
-//   * linear terms: pairs whose S can never exceed max_w.  Their sum
-//     sum fa*fw*S is an int8 x int8 product of masked two's complement codes
-//     (the masked byte's value is exactly sum_{slices in mask} f*d), chained
-//     into one int32 accumulator with no VALU work;
-//   * clamped pairs: one MFMA each on masked codes (X = fa*fw*S), clamped to
-//     fa*fw*max_w (min for positive factors, max for negative), then added.
-// T is then restored as (float(T) * xs[n,g]) * ws[g,c] and accumulated over
-// reads in torch's CPU cascade order (level step 16).
+// With every device effect off the ADC count of slice pair (a, w) is the closed
+// form code = min(S_aw, max_w), S_aw = sum_r da[n,r] * dw[r,c] (memfast/
+// reference.py:63-117 with ideal conductances; exact because FP32 current
+// errors stay far below half a count, checked on the host).  Per read:
+//   * static linear terms: pairs that can never exceed max_w.  Their signed sum
+//     is an int8 x int8 MFMA of masked two's complement codes (a masked byte's
+//     int8 value is exactly sum factor*digit over the slices in the mask);
+//   * for the remaining pairs, a per-read, per-wave test on precomputed digit
+//     sums proves most of them clamp-free (S <= Mw*max_n sum_r da, or
+//     S <= Ma*max_c sum_r dw); those merge into one natural-form MFMA per input
+//     slice, again with no VALU work;
+//   * pairs still at risk get their own MFMA on positive operand forms, one
+//     v_min and one v_mad_i32_i24 per output.
+// T is restored as (float(T) * xs[n,g]) * ws[g,c] and summed over reads in
+// torch's CPU cascade order (level step 16; level 2 kept in `out`).
 //
-// Block: 4 waves (2 x 2), each wave TM x TN tiles of 32x32 outputs.  Per read
-// the block stages A codes [BM x 32*KS] and B codes [BN x 32*KS] in LDS
-// (double buffered).  Roofline: int8 MFMA for the pair products, with the VALU
-// epilogue (clamp, add, 4-op scale restore per output and read) as co-bound.
+// Orientation: the MFMA A operand is the weight codes (tile rows = output
+// columns c), the B operand the input codes (tile columns = vectors n), so the
+// per-weight-slice masks are built once per wave and shared by TN vector tiles.
+// Block = 4 waves: 2 (columns) x 2 (vectors); wave tile 32 columns x 32*TN
+// vectors; LDS holds codes [64 x 32*KS] and [64*TN x 32*KS] per read, double
+// buffered.  Roofline: int8 MFMA, with the VALU epilogue as co-bound.
 #include "mf_kernels.h"
 
 namespace mf {
@@ -27,7 +31,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Sign-extend each byte holding a `bits`-wide two's complement code.
 __device__ __forceinline__ u32 sext_bytes(u32 x, int bits) {
     const u32 sign = (x >> (bits - 1)) & 0x01010101u;
     const u32 ext = (0xFFu << bits) & 0xFFu;
@@ -35,12 +38,8 @@ __device__ __forceinline__ u32 sext_bytes(u32 x, int bits) {
 }
 
 __device__ __forceinline__ v4i sext4(v4i x, int bits) {
-    v4i r;
-    r.x = int(sext_bytes(u32(x.x), bits));
-    r.y = int(sext_bytes(u32(x.y), bits));
-    r.z = int(sext_bytes(u32(x.z), bits));
-    r.w = int(sext_bytes(u32(x.w), bits));
-    return r;
+    return v4i{int(sext_bytes(u32(x.x), bits)), int(sext_bytes(u32(x.y), bits)),
+               int(sext_bytes(u32(x.z), bits)), int(sext_bytes(u32(x.w), bits))};
 }
 
 __device__ __forceinline__ v4i and4(v4i x, u32 m) {
@@ -48,91 +47,150 @@ __device__ __forceinline__ v4i and4(v4i x, u32 m) {
     return v4i{x.x & mi, x.y & mi, x.z & mi, x.w & mi};
 }
 
-template <int TM, int TN, int KS>
-__global__ __launch_bounds__(256) void k_ideal(const IdealPlan plan, const IdealArgs args) {
-    constexpr int BM = 2 * TM * 32, BN = 2 * TN * 32;
-    constexpr int KB = 32 * KS;           // code bytes per row and read
-    constexpr int STRIDE = KB + 16;       // LDS row stride (conflict-free b128 reads)
-    constexpr int CHUNKS = KB / 16;       // 16-byte chunks per row
-    constexpr int A_LOADS = (BM * CHUNKS + 255) / 256;
-    constexpr int B_LOADS = (BN * CHUNKS + 255) / 256;
-    __shared__ __align__(16) u8 sA[2][BM * STRIDE];
-    __shared__ __align__(16) u8 sB[2][BN * STRIDE];
-    __shared__ __align__(16) float sX[2][BM];
-    __shared__ __align__(16) float sW[2][BN];
+// Positive operand form: masked bytes, halved for an 8-bit sign slice (bit 7).
+__device__ __forceinline__ v4i pos4(v4i x, u32 m, int shift) {
+    v4i r = and4(x, m);
+    if (shift) {
+        r.x = int(u32(r.x) >> 1);
+        r.y = int(u32(r.y) >> 1);
+        r.z = int(u32(r.z) >> 1);
+        r.w = int(u32(r.w) >> 1);
+    }
+    return r;
+}
+
+__device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// Per-read digit sums, maximized over blocks of `block` (32 or 64) rows, then
+// tested against the slot thresholds: out[rb][g] = mask of proven slots.
+__global__ __launch_bounds__(256) void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G,
+                                                    int Gr, int R, int P,
+                                                    const SliceLayout layout, int block,
+                                                    const SlotTests tests, uint64_t *out) {
+    const i64 rows_pad = ((rows + 63) / 64) * 64;
+    const i64 total = G * rows_pad;
+    const int S = layout.count;
+    for (i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += i64(gridDim.x) * blockDim.x) {
+        const i64 g = t / rows_pad, row = t % rows_pad;
+        const i64 kofs = (g / Gr) * R + (g % Gr) * P;
+        int sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (row < rows) {
+            const u8 *src = codes + row * kp + kofs;
+            for (int b = 0; b < P; ++b) {
+                const int code = src[b];
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+                    if (s < S) sums[s] += (code >> layout.shift[s]) & layout.mask[s];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            if (s >= S) break;
+            int v = sums[s];
+            for (int off = 1; off < block; off <<= 1) v = max(v, __shfl_xor(v, off, 64));
+            sums[s] = v;
+        }
+        if ((row % block) == 0 && row < rows) {
+            uint64_t bits = 0;
+            for (int slot = 0; slot < 64; ++slot) {
+                if (!((tests.exists >> slot) & 1)) continue;
+                int v = 0;
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+                    if (s == tests.slice[slot]) v = sums[s];
+                if (v <= tests.thr[slot]) bits |= uint64_t(1) << slot;
+            }
+            out[(row / block) * G + g] = bits;
+        }
+    }
+}
+
+template <int TN, int KS, int MAXCW, int MAXCA>
+__global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const IdealArgs args) {
+    constexpr int BC = 64;                 // output columns per block
+    constexpr int BV = 2 * TN * 32;        // vectors per block
+    constexpr int KB = 32 * KS;            // code bytes per row and read
+    constexpr int STRIDE = KB + 16;        // LDS row stride (conflict-free b128 reads)
+    constexpr int CHUNKS = KB / 16;
+    constexpr int W_LOADS = (BC * CHUNKS + 255) / 256;
+    constexpr int X_LOADS = (BV * CHUNKS + 255) / 256;
+    __shared__ __align__(16) u8 sW[2][BC * STRIDE];
+    __shared__ __align__(16) u8 sX[2][BV * STRIDE];
+    __shared__ __align__(16) float sWS[2][BC];
+    __shared__ __align__(16) float sXS[2][BV];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const i64 row0 = i64(blockIdx.y) * BM;
-    const i64 col0 = i64(blockIdx.x) * BN;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wc = wave & 1, wv = wave >> 1;
+    const i64 c0 = i64(blockIdx.x) * BC;
+    const i64 v0 = i64(blockIdx.y) * BV;
     const i64 G = args.G;
+    const i64 cblock = (c0 + wc * 32) / 32;          // weight digit-max block (32 columns)
+    const i64 vblock = (v0 + wv * TN * 32) / 64;     // input digit-max block (64 vectors)
+    const int lrow = lane & 31, lhalf = lane >> 5;
 
-    v4i ra[A_LOADS], rb[B_LOADS];
-    float rx = 0.0f, rw = 0.0f;
+    v4i rw[W_LOADS], rx[X_LOADS];
+    float rscale = 0.0f;
 
     auto fetch = [&](i64 g) {
         const i64 kofs = (g / args.Gr) * args.R + (g % args.Gr) * args.P;
 #pragma unroll
-        for (int e = 0; e < A_LOADS; ++e) {
+        for (int e = 0; e < W_LOADS; ++e) {
             const int c = tid + e * 256;
             const int row = c / CHUNKS, part = c % CHUNKS;
             v4i v = v4i{0, 0, 0, 0};
-            if (c < BM * CHUNKS && row0 + row < args.n)
-                v = *reinterpret_cast<const v4i *>(args.q + (row0 + row) * args.kp + kofs + part * 16);
-            ra[e] = v;
+            if (c < BC * CHUNKS && c0 + row < args.ncols)
+                v = *reinterpret_cast<const v4i *>(args.wt + (c0 + row) * args.kp + kofs + part * 16);
+            rw[e] = v;
         }
 #pragma unroll
-        for (int e = 0; e < B_LOADS; ++e) {
+        for (int e = 0; e < X_LOADS; ++e) {
             const int c = tid + e * 256;
-            const int col = c / CHUNKS, part = c % CHUNKS;
+            const int row = c / CHUNKS, part = c % CHUNKS;
             v4i v = v4i{0, 0, 0, 0};
-            if (c < BN * CHUNKS && col0 + col < args.ncols)
-                v = *reinterpret_cast<const v4i *>(args.wt + (col0 + col) * args.kp + kofs + part * 16);
-            rb[e] = v;
+            if (c < BV * CHUNKS && v0 + row < args.n)
+                v = *reinterpret_cast<const v4i *>(args.q + (v0 + row) * args.kp + kofs + part * 16);
+            rx[e] = v;
         }
-        if (tid < BM) rx = row0 + tid < args.n ? args.xscale[(row0 + tid) * G + g] : 0.0f;
-        if (tid >= 256 - BN) {
-            const int col = tid - (256 - BN);
-            rw = col0 + col < args.ncols ? args.wscale[g * args.ldws + col0 + col] : 0.0f;
+        if (tid < BC) {
+            rscale = c0 + tid < args.ncols ? args.wscale[g * args.ldws + c0 + tid] : 0.0f;
+        } else if (tid < BC + BV) {
+            const int v = tid - BC;
+            rscale = v0 + v < args.n ? args.xscale[(v0 + v) * G + g] : 0.0f;
         }
     };
     auto stash = [&](int buf) {
 #pragma unroll
-        for (int e = 0; e < A_LOADS; ++e) {
+        for (int e = 0; e < W_LOADS; ++e) {
             const int c = tid + e * 256;
-            if (c < BM * CHUNKS) {
-                v4i v = ra[e];
-                if (args.a_bits < 8) v = sext4(v, args.a_bits);
-                *reinterpret_cast<v4i *>(&sA[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
+            if (c < BC * CHUNKS) {
+                v4i v = rw[e];
+                if (args.w_bits < 8) v = sext4(v, args.w_bits);
+                *reinterpret_cast<v4i *>(&sW[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
             }
         }
 #pragma unroll
-        for (int e = 0; e < B_LOADS; ++e) {
+        for (int e = 0; e < X_LOADS; ++e) {
             const int c = tid + e * 256;
-            if (c < BN * CHUNKS) {
-                v4i v = rb[e];
-                if (args.w_bits < 8) v = sext4(v, args.w_bits);
-                *reinterpret_cast<v4i *>(&sB[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
+            if (c < BV * CHUNKS) {
+                v4i v = rx[e];
+                if (args.a_bits < 8) v = sext4(v, args.a_bits);
+                *reinterpret_cast<v4i *>(&sX[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
             }
         }
-        if (tid < BM) sX[buf][tid] = rx;
-        if (tid >= 256 - BN) sW[buf][tid - (256 - BN)] = rw;
+        if (tid < BC) sWS[buf][tid] = rscale;
+        else if (tid < BC + BV) sXS[buf][tid - BC] = rscale;
     };
 
-    // Cascade accumulators of torch's sum (levels 0 and 1 in registers,
-    // level 2 in `out`, written from zero at its first flush).
-    float acc0[TM][TN][16], acc1[TM][TN][16];
+    float acc0[TN][16], acc1[TN][16];
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
+    for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) { acc0[tm][tn][r] = 0.0f; acc1[tm][tn][r] = 0.0f; }
-
-    const int lrow = lane & 31;
-    const int lhalf = lane >> 5;
+        for (int r = 0; r < 16; ++r) { acc0[tn][r] = 0.0f; acc1[tn][r] = 0.0f; }
 
     fetch(0);
     stash(0);
@@ -142,128 +200,122 @@ __global__ __launch_bounds__(256) void k_ideal(const IdealPlan plan, const Ideal
         const int cur = int(g & 1);
         if (g + 1 < G) fetch(g + 1);
 
-        v4i A[TM][KS], B[TN][KS];
+        v4i Wr[KS], Xr[TN][KS];
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
+        for (int ks = 0; ks < KS; ++ks) {
+            Wr[ks] = *reinterpret_cast<const v4i *>(
+                &sW[cur][(wc * 32 + lrow) * STRIDE + ks * 32 + lhalf * 16]);
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                A[tm][ks] = *reinterpret_cast<const v4i *>(
-                    &sA[cur][(wm * TM * 32 + tm * 32 + lrow) * STRIDE + ks * 32 + lhalf * 16]);
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                B[tn][ks] = *reinterpret_cast<const v4i *>(
-                    &sB[cur][(wn * TN * 32 + tn * 32 + lrow) * STRIDE + ks * 32 + lhalf * 16]);
+            for (int tn = 0; tn < TN; ++tn)
+                Xr[tn][ks] = *reinterpret_cast<const v4i *>(
+                    &sX[cur][(wv * TN * 32 + tn * 32 + lrow) * STRIDE + ks * 32 + lhalf * 16]);
+        }
 
-        v16i T[TM][TN];
+        v16i T[TN];
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn) T[tm][tn] = v16i{};
+        for (int tn = 0; tn < TN; ++tn) T[tn] = v16i{};
 
+        // Static linear terms.
         for (int t = 0; t < plan.n_lin; ++t) {
-            const u32 ma = plan.lin_a[t], mb = plan.lin_b[t];
-            v4i Am[TM][KS], Bm[TN][KS];
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
+            for (int ks = 0; ks < KS; ++ks) {
+                const v4i wm = and4(Wr[ks], plan.lin_w[t]);
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) Am[tm][ks] = and4(A[tm][ks], ma);
+                for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, and4(Xr[tn][ks], plan.lin_x[t]), T[tn]);
+            }
+        }
+
+        // Per-read decisions: slots (ca * 8 + cw) proven clamp-free on either
+        // side merge into one natural-form MFMA per input slice; the others get
+        // their own MFMA, a min and a signed multiply-add.  Scalar control only.
+        const uint64_t proven = args.xbits[vblock * G + g] | args.wbits[cblock * G + g];
+        const uint64_t fail = plan.exists & ~proven;
+        const uint64_t safe = plan.exists & proven;
+        for (int ca = 0; ca < plan.n_ca; ++ca) {
+            const u32 safe_w = u32(safe >> (ca * 8)) & 0xFFu;
+            u32 fail_w = u32(fail >> (ca * 8)) & 0xFFu;
+            v4i Xp[TN][KS];
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) Bm[tn][ks] = and4(B[tn][ks], mb);
+                for (int ks = 0; ks < KS; ++ks)
+                    Xp[tn][ks] = pos4(Xr[tn][ks], plan.ca_xpos[ca], (plan.xshift_bits >> ca) & 1);
+            if (safe_w) {
+                u32 merged = 0;
+                for (u32 bits = safe_w; bits; bits &= bits - 1)
+                    merged |= plan.cw_wnat[__builtin_ctz(bits)];
+                const bool same = (plan.same_bits >> ca) & 1;
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
+                for (int ks = 0; ks < KS; ++ks) {
+                    const v4i wm = and4(Wr[ks], merged);
+#pragma unroll
+                    for (int tn = 0; tn < TN; ++tn) {
+                        const v4i xn = same ? Xp[tn][ks] : and4(Xr[tn][ks], plan.ca_xnat[ca]);
+                        T[tn] = mfma(wm, xn, T[tn]);
+                    }
+                }
+            }
+            for (; fail_w; fail_w &= fail_w - 1) {
+                const int cw = __builtin_ctz(fail_w);
+                v4i Wp[KS];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    Wp[ks] = pos4(Wr[ks], plan.cw_wpos[cw], (plan.wshift_bits >> cw) & 1);
+                v16i y[TN];
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) {
+                    y[tn] = v16i{};
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) y[tn] = mfma(Wp[ks], Xp[tn][ks], y[tn]);
+                }
+                const int lim = plan.ca_posval[ca] * plan.cw_posmax[cw];
+                const int mul = plan.ca_msign[ca] * plan.cw_msign[cw];
 #pragma unroll
                 for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-                    for (int ks = 0; ks < KS; ++ks)
-                        T[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am[tm][ks], Bm[tn][ks],
-                                                                          T[tm][tn], 0, 0, 0);
-        }
-
-#pragma unroll 2
-        for (int c = 0; c < plan.n_clamp; ++c) {
-            const u32 ma = plan.cl_a[c], mb = plan.cl_b[c];
-            const int lim = plan.cl_val[c];
-            const bool upper = plan.cl_upper[c] != 0;
-            v4i Am[TM][KS], Bm[TN][KS];
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) Am[tm][ks] = and4(A[tm][ks], ma);
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) Bm[tn][ks] = and4(B[tn][ks], mb);
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) {
-                    v16i X = v16i{};
-#pragma unroll
-                    for (int ks = 0; ks < KS; ++ks)
-                        X = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am[tm][ks], Bm[tn][ks], X, 0, 0, 0);
-                    if (upper) {
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) T[tm][tn][r] += min(X[r], lim);
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) T[tm][tn][r] += max(X[r], lim);
-                    }
-                }
+                    for (int r = 0; r < 16; ++r) T[tn][r] += __mul24(min(y[tn][r], lim), mul);
+            }
         }
 
         // Scale restore (float(T) * xs) * ws and cascade accumulation.
-        v4f xs[TM][4];
+        v4f ws4[4];
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
+        for (int qd = 0; qd < 4; ++qd)
+            ws4[qd] = *reinterpret_cast<const v4f *>(&sWS[cur][wc * 32 + qd * 8 + lhalf * 4]);
 #pragma unroll
-            for (int qd = 0; qd < 4; ++qd)
-                xs[tm][qd] = *reinterpret_cast<const v4f *>(
-                    &sX[cur][wm * TM * 32 + tm * 32 + qd * 8 + lhalf * 4]);
-        float ws[TN];
+        for (int tn = 0; tn < TN; ++tn) {
+            const float xs = sXS[cur][wv * TN * 32 + tn * 32 + lrow];
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) ws[tn] = sW[cur][wn * TN * 32 + tn * 32 + lrow];
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
+            for (int r = 0; r < 16; ++r) {
+                float v = float(T[tn][r]) * xs;
+                v = v * ws4[r >> 2][r & 3];
+                acc0[tn][r] = acc0[tn][r] + v;
+            }
+        }
+        const i64 count = g + 1;
+        if ((count & 15) == 0) {
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float v = float(T[tm][tn][r]) * xs[tm][r >> 2][r & 3];
-                    v = v * ws[tn];
-                    acc0[tm][tn][r] = acc0[tm][tn][r] + v;
+                    acc1[tn][r] = acc1[tn][r] + acc0[tn][r];
+                    acc0[tn][r] = 0.0f;
                 }
-        const i64 count = g + 1;
-        if ((count & 15) == 0) {
+            if ((count & 255) == 0) {
+                // Level 2 of the cascade lives in `out` (more than 255 reads).
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn)
+                for (int tn = 0; tn < TN; ++tn) {
+                    const i64 n = v0 + wv * TN * 32 + tn * 32 + lrow;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        acc1[tm][tn][r] = acc1[tm][tn][r] + acc0[tm][tn][r];
-                        acc0[tm][tn][r] = 0.0f;
-                    }
-            if ((count & 255) == 0) {
-                // Level 2 lives in `out` (rare: more than 255 reads).
-#pragma unroll
-                for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-                    for (int tn = 0; tn < TN; ++tn) {
-                        const i64 col = col0 + wn * TN * 32 + tn * 32 + lrow;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const i64 row = row0 + wm * TM * 32 + tm * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-                            if (row < args.n && col < args.ncols) {
-                                float *dst = args.out + row * args.ldo + col;
-                                *dst = count == 256 ? acc1[tm][tn][r] : *dst + acc1[tm][tn][r];
-                            }
-                            acc1[tm][tn][r] = 0.0f;
+                        const i64 c = c0 + wc * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+                        if (n < args.n && c < args.ncols) {
+                            float *dst = args.out + n * args.ldo + c;
+                            *dst = count == 256 ? acc1[tn][r] : *dst + acc1[tn][r];
                         }
+                        acc1[tn][r] = 0.0f;
                     }
+                }
             }
         }
 
@@ -272,28 +324,36 @@ __global__ __launch_bounds__(256) void k_ideal(const IdealPlan plan, const Ideal
     }
 
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
+    for (int tn = 0; tn < TN; ++tn) {
+        const i64 n = v0 + wv * TN * 32 + tn * 32 + lrow;
+        if (n >= args.n) continue;
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-            const i64 col = col0 + wn * TN * 32 + tn * 32 + lrow;
+        for (int qd = 0; qd < 4; ++qd) {
+            const i64 c = c0 + wc * 32 + qd * 8 + lhalf * 4;
+            float *dst = args.out + n * args.ldo + c;
+            v4f v;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const i64 row = row0 + wm * TM * 32 + tm * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-                if (row < args.n && col < args.ncols) {
-                    float *dst = args.out + row * args.ldo + col;
-                    float v = acc0[tm][tn][r] + acc1[tm][tn][r];
-                    if (G >= 256) v = v + *dst;
-                    *dst = v;
-                }
+            for (int e = 0; e < 4; ++e) {
+                float s = acc0[tn][qd * 4 + e] + acc1[tn][qd * 4 + e];
+                if (G >= 256 && c + e < args.ncols) s = s + dst[e];
+                v[e] = s;
+            }
+            if (c + 3 < args.ncols) {
+                *reinterpret_cast<v4f *>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c + e < args.ncols) dst[e] = v[e];
             }
         }
+    }
 }
 
-#define MF_IDEAL_INST(TM, TN, KS) \
-    template __global__ void k_ideal<TM, TN, KS>(const IdealPlan, const IdealArgs);
-MF_IDEAL_INST(2, 2, 1)
-MF_IDEAL_INST(2, 2, 2)
-MF_IDEAL_INST(1, 2, 1)
-MF_IDEAL_INST(1, 2, 2)
+#define MF_IDEAL_INST(TN, KS, MAXCW, MAXCA) \
+    template __global__ void k_ideal<TN, KS, MAXCW, MAXCA>(const IdealPlan, const IdealArgs);
+MF_IDEAL_INST(2, 1, 4, 4)
+MF_IDEAL_INST(2, 1, 8, 8)
+MF_IDEAL_INST(1, 2, 4, 4)
+MF_IDEAL_INST(1, 2, 8, 8)
 
 }  // namespace mf

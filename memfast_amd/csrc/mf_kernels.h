@@ -28,30 +28,66 @@ template <typename Phys, int WG, bool OUTPUT_NOISE>
 __global__ void k_general(const mf_config cfg, const GeneralArgs args, int out_kind);
 
 // ---- ideal MFMA read (ideal_mfma.hip) -------------------------------------
-constexpr int IDEAL_MAX_LIN = 16;
-constexpr int IDEAL_MAX_CLAMP = 64;
+constexpr int IDEAL_MAX_LIN = 16;   // static linear terms
+constexpr int IDEAL_MAX_CA = 8;     // input slices with at least one clamped pair
+constexpr int IDEAL_MAX_CW = 8;     // weight slices with at least one clamped pair
 
+// Slice pairs that can exceed their ADC limit form a (clamp-a x clamp-w) grid of
+// slots s = ca * 8 + cw.  Per read and wave a slot is *proven clamp-free* (and
+// merged into a linear MFMA, exactly) when a digit-sum bound shows S <= max:
+// max_n sum_r da <= floor(max_w / Mw) (input side) or max_c sum_r dw <=
+// floor(max_w / Ma) (weight side).  The pre-pass k_digit_bits evaluates these
+// tests and stores one 64-bit slot mask per (block, read).
+// Operand "natural" forms are masked two's complement bytes whose int8 value is
+// factor*digit; "positive" forms are masked (and, for an 8-bit sign slice,
+// halved) bytes whose value is posval*digit with factor = msign*posval.
 struct IdealPlan {
-    int n_lin, n_clamp;
-    u32 lin_a[IDEAL_MAX_LIN], lin_b[IDEAL_MAX_LIN];
-    u32 cl_a[IDEAL_MAX_CLAMP], cl_b[IDEAL_MAX_CLAMP];
-    int cl_val[IDEAL_MAX_CLAMP];
-    int cl_upper[IDEAL_MAX_CLAMP];   // 1: min(X, val); 0: max(X, val)
+    int n_lin;
+    u32 lin_w[IDEAL_MAX_LIN], lin_x[IDEAL_MAX_LIN];   // natural masks, weight / input side
+    int n_ca, n_cw;
+    u32 ca_xnat[IDEAL_MAX_CA], ca_xpos[IDEAL_MAX_CA];
+    int ca_posval[IDEAL_MAX_CA], ca_msign[IDEAL_MAX_CA];
+    u32 cw_wnat[IDEAL_MAX_CW], cw_wpos[IDEAL_MAX_CW];
+    int cw_posmax[IDEAL_MAX_CW], cw_msign[IDEAL_MAX_CW];   // posval_w * max_w
+    u32 xshift_bits, wshift_bits, same_bits;  // per ca / cw / ca (natural == positive form)
+    uint64_t exists;                          // slots holding a clamp-candidate pair
+};
+
+// Tests evaluated by k_digit_bits for one side: slot s passes when the block's
+// maximum digit sum of slice[s] is at most thr[s].
+struct SlotTests {
+    uint64_t exists;
+    int slice[64];
+    int thr[64];
 };
 
 struct IdealArgs {
-    const u8 *q;          // [n, kp] input codes
-    const u8 *wt;         // [ncols, kp] weight codes, column-major (packed_t)
-    const float *xscale;  // [n, G]
-    const float *wscale;  // [G, ldws]
-    float *out;           // [n, ldo]
+    const u8 *q;            // [n, kp] input codes
+    const u8 *wt;           // [ncols, kp] weight codes, column-major (packed_t)
+    const float *xscale;    // [n, G]
+    const float *wscale;    // [G, ldws]
+    const uint64_t *xbits;  // [ceil(n/64), G] input-side proven slots per 64 vectors
+    const uint64_t *wbits;  // [ceil(ncols/32), G] weight-side proven slots per 32 columns
+    float *out;             // [n, ldo]
     i64 n, kp, G, ldo, ldws, ncols;
     int Gr, R, P;
-    int a_bits, w_bits;   // code widths (< 8: sign-extend bytes on load)
+    int a_bits, w_bits;     // code widths (< 8: sign-extend bytes on load)
 };
 
-template <int TM, int TN, int KS>
+template <int TN, int KS, int MAXCW, int MAXCA>
 __global__ void k_ideal(const IdealPlan plan, const IdealArgs args);
+
+struct SliceLayout {
+    int count;
+    int shift[MF_MAX_SLICES];
+    int mask[MF_MAX_SLICES];
+};
+
+// Per-read digit sums of every slice, maximized over blocks of `block` rows,
+// turned into the slot mask of `tests`: out[rb][g].
+__global__ void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int Gr, int R, int P,
+                             const SliceLayout layout, int block, const SlotTests tests,
+                             uint64_t *out);
 
 // ---- conductances (restore.hip) -------------------------------------------
 template <typename Phys>

@@ -138,7 +138,8 @@ SIGNATURES = {
     "mf_partial": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
                     _P, _P, _P], ct.c_int),
     "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
-               _I64, _P], ct.c_int),
+               _I64, _P, _I64, _P], ct.c_int),
+    "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, ct.POINTER(_I64)], ct.c_int),
     "mf_mm_kernel": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I32)], ct.c_int),
     "mf_resources_query": ([_CFG, _I32, ct.POINTER(MFResources)], ct.c_int),
     "mf_rng_uniform": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
@@ -483,6 +484,12 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
         packed_t = None
     if out is None:
         out = torch.empty((n, p * c), dtype=torch.float32, device=q.device)
+    workspace = None
+    if packed_t is not None:
+        size = ct.c_int64()
+        check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
+              "workspace size")
+        workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
     timer = kernel_timer
     with torch.cuda.device(q.device):
         if timer is not None:
@@ -492,7 +499,8 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
             library().mf_mm(
                 ct.byref(descriptor(config)), _ptr(q.contiguous()), _ptr(xscale.contiguous()), n,
                 m, _ptr(packed.contiguous()), _ptr(packed_t), _ptr(wscale.contiguous()), p,
-                _ptr(g), seed, event, _ptr(out), out.stride(0), _stream(q.device),
+                _ptr(g), seed, event, _ptr(out), out.stride(0), _ptr(workspace),
+                0 if workspace is None else workspace.numel(), _stream(q.device),
             ),
             "mm",
         )
