@@ -154,11 +154,13 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
  *   sum over reads g in torch's CPU order of (float(T[n,g,o]) * xscale[n,g]) * wscale[g,o].
  * g as for mf_partial over all tiles (begin=0, end=p); NULL means ideal devices.
  * For ideal devices with packed_t != NULL and a workspace of at least
- * mf_mm_workspace() bytes (256-byte aligned) the MFMA kernel is used. */
+ * mf_mm_workspace() bytes (256-byte aligned) the MFMA kernel is used;
+ * `variant` picks its tiling (0 default, 1: 64 vectors per wave, 2: 32 vectors
+ * per wave; the tuned mode's schedule grid).  Results do not depend on it. */
 int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
           const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo,
-          void *workspace, int64_t workspace_bytes, void *stream);
+          void *workspace, int64_t workspace_bytes, int32_t variant, void *stream);
 
 /* Workspace bytes mf_mm needs for the MFMA kernel (per-read digit-sum maxima). */
 int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64_t *bytes);

@@ -105,34 +105,15 @@ int byte_mask(int shift, int mask, bool sign_slice) {
 
 u32 replicate(int m) { return u32(m) * 0x01010101u; }
 
-// Operand masks of one slice: natural (two's complement value = factor*digit,
-// sign-extended for codes narrower than 8 bits) and positive (value =
-// |factor|*digit, halved for the sign bit of an 8-bit code).
+// Natural operand mask of one slice: masked two's complement bytes whose int8
+// value is factor*digit (sign-extended bits included for codes narrower than 8).
 struct SliceForm {
-    u32 nat, pos;
-    int shift;      // positive form shifted right by one (8-bit sign slice)
-    int posval;     // positive operand value per digit unit
-    int sign;       // sign of the factor
-    int scale;      // factor = sign * posval * scale
+    u32 nat;
 };
 
-SliceForm slice_form(int shift, int mask, int64_t factor, bool sign_slice, int bits) {
+SliceForm slice_form(int shift, int mask, bool sign_slice, int bits) {
     SliceForm f{};
     f.nat = replicate(byte_mask(shift, mask, sign_slice && bits < 8));
-    f.sign = factor < 0 ? -1 : 1;
-    const int64_t mag = factor < 0 ? -factor : factor;
-    if (sign_slice && shift == 7) {
-        f.pos = replicate(0x80);
-        f.shift = 1;
-        f.posval = 64;
-        f.scale = 2;
-    } else {
-        f.pos = replicate((mask << shift) & 0xFF);
-        f.shift = 0;
-        f.posval = int(mag);
-        f.scale = 1;
-    }
-    if (sign_slice && bits == 8) f.nat = replicate(0x80);
     return f;
 }
 
@@ -188,11 +169,11 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
     }
     SliceForm xf[MF_MAX_SLICES], wf[MF_MAX_SLICES];
     for (int a = 0; a < cfg->n_in; ++a)
-        xf[a] = slice_form(cfg->in_shift[a], cfg->in_mask[a], cfg->in_factor[a],
-                           a == cfg->n_in - 1, cfg->activation_bits);
+        xf[a] = slice_form(cfg->in_shift[a], cfg->in_mask[a], a == cfg->n_in - 1,
+                           cfg->activation_bits);
     for (int w = 0; w < cfg->n_w; ++w)
-        wf[w] = slice_form(cfg->w_shift[w], cfg->w_mask[w], cfg->w_factor[w],
-                           w == cfg->n_w - 1, cfg->weight_bits);
+        wf[w] = slice_form(cfg->w_shift[w], cfg->w_mask[w], w == cfg->n_w - 1,
+                           cfg->weight_bits);
     // Static linear terms: weight slices grouped by their clamp-free input sets.
     bool grouped[MF_MAX_SLICES] = {false};
     for (int w = 0; w < cfg->n_w; ++w) {
@@ -210,20 +191,15 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
         plan->lin_x[plan->n_lin] = xmask;
         ++plan->n_lin;
     }
-    // Clamp-candidate grid: slot cw * 8 + ca.
+    // Clamp-candidate grid: slot ca * 8 + cw.
     int ca_of[MF_MAX_SLICES], cw_of[MF_MAX_SLICES];
     for (int a = 0; a < cfg->n_in; ++a) {
         ca_of[a] = -1;
         for (int w = 0; w < cfg->n_w; ++w)
             if (!is_free[a][w]) { ca_of[a] = plan->n_ca++; break; }
         if (ca_of[a] >= 0) {
-            const int ca = ca_of[a];
-            plan->ca_xnat[ca] = xf[a].nat;
-            plan->ca_xpos[ca] = xf[a].pos;
-            plan->ca_posval[ca] = xf[a].posval;
-            plan->ca_msign[ca] = xf[a].sign * xf[a].scale;
-            if (xf[a].shift) plan->xshift_bits |= 1u << ca;
-            if (xf[a].nat == xf[a].pos && !xf[a].shift) plan->same_bits |= 1u << ca;
+            plan->ca_xnat[ca_of[a]] = xf[a].nat;
+            plan->ca_factor[ca_of[a]] = int(cfg->in_factor[a]);
         }
     }
     for (int w = 0; w < cfg->n_w; ++w) {
@@ -231,12 +207,9 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
         for (int a = 0; a < cfg->n_in; ++a)
             if (!is_free[a][w]) { cw_of[w] = plan->n_cw++; break; }
         if (cw_of[w] >= 0) {
-            const int cw = cw_of[w];
-            plan->cw_wnat[cw] = wf[w].nat;
-            plan->cw_wpos[cw] = wf[w].pos;
-            plan->cw_posmax[cw] = wf[w].posval * cfg->adc_max[w];
-            plan->cw_msign[cw] = wf[w].sign * wf[w].scale;
-            if (wf[w].shift) plan->wshift_bits |= 1u << cw;
+            plan->cw_wnat[cw_of[w]] = wf[w].nat;
+            plan->cw_limit[cw_of[w]] = int(cfg->w_factor[w] * cfg->adc_max[w]);
+            if (cfg->w_factor[w] < 0) plan->cw_negative |= 1u << cw_of[w];
         }
     }
     memset(xtests, 0, sizeof(*xtests));
@@ -452,6 +425,15 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m, con
                         : launch_general<float>(cfg, args, OUT_TOTALS, s);
 }
 
+// Extents the MFMA kernel addresses with 32-bit buffer offsets (a block's code
+// slab of up to 128 rows and the whole per-read weight-scale table) and its grid.
+static bool ideal_extent_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
+    const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
+    const i64 limit = 0x7FFFFFFF;
+    return 128 * kp <= limit && G * ncols * 4 <= limit && 128 * G * 4 <= limit &&
+           (n + 63) / 64 <= 65535;
+}
+
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
                  int32_t *kernel_id) {
     int status = check_config(cfg);
@@ -461,8 +443,8 @@ int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t 
     SlotTests xt, wt;
     int ks = 0;
     const char *why = "";
-    *kernel_id = (has_packed_t && build_ideal_plan(cfg, m, p, &plan, &xt, &wt, &ks, &why)) ? 1 : 0;
-    (void)n;
+    *kernel_id = (has_packed_t && ideal_extent_ok(cfg, n, m, p) &&
+                  build_ideal_plan(cfg, m, p, &plan, &xt, &wt, &ks, &why)) ? 1 : 0;
     return MF_OK;
 }
 
@@ -479,7 +461,7 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64
 int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
           const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo, void *workspace,
-          int64_t workspace_bytes, void *stream) {
+          int64_t workspace_bytes, int32_t variant, void *stream) {
     int status = check_config(cfg);
     if (status) return status;
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
@@ -498,7 +480,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
     ideal_workspace(cfg, n, m, p, &xbytes, &wbytes);
     const bool room = workspace && workspace_bytes >= xbytes + wbytes;
     SlotTests xtests, wtests;
-    if (!g && packed_t && aligned && room &&
+    if (!g && packed_t && aligned && room && ideal_extent_ok(cfg, n, m, p) &&
         build_ideal_plan(cfg, m, p, &plan, &xtests, &wtests, &ks, &why)) {
         uint64_t *xbits = static_cast<uint64_t *>(workspace);
         uint64_t *wbits = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) + xbytes);
@@ -529,18 +511,16 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         args.P = cfg->read_rows;
         args.a_bits = cfg->activation_bits;
         args.w_bits = cfg->weight_bits;
-        const int tn = ks == 1 ? 2 : 1;
+        // Tile variants: 0 default (32 vectors per wave), 1 = 64 vectors per wave,
+        // 2 = 32 vectors per wave.
+        if (variant < 0 || variant > 2) return fail(MF_E_INVALID, "unknown kernel variant %d", variant);
+        const int tn = (ks == 1 && variant == 1) ? 2 : 1;
         const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (ncols + 63) / 64;
         if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
         const dim3 grid{unsigned(gx), unsigned(gy), 1u};
-        const bool small = plan.n_ca <= 4 && plan.n_cw <= 4;
-        if (ks == 1) {
-            if (small) hipLaunchKernelGGL((k_ideal<2, 1, 4, 4>), grid, dim3(256), 0, s, plan, args);
-            else hipLaunchKernelGGL((k_ideal<2, 1, 8, 8>), grid, dim3(256), 0, s, plan, args);
-        } else {
-            if (small) hipLaunchKernelGGL((k_ideal<1, 2, 4, 4>), grid, dim3(256), 0, s, plan, args);
-            else hipLaunchKernelGGL((k_ideal<1, 2, 8, 8>), grid, dim3(256), 0, s, plan, args);
-        }
+        if (ks == 1 && tn == 2) hipLaunchKernelGGL((k_ideal<2, 1>), grid, dim3(256), 0, s, plan, args);
+        else if (ks == 1) hipLaunchKernelGGL((k_ideal<1, 1>), grid, dim3(256), 0, s, plan, args);
+        else hipLaunchKernelGGL((k_ideal<1, 2>), grid, dim3(256), 0, s, plan, args);
         return check_launch("ideal MFMA read");
     }
     if (!g && needs_conductances(cfg))
@@ -575,7 +555,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     hipFuncAttributes attr;
     hipError_t e;
     if (kernel_id == 1)
-        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_ideal<2, 1, 4, 4>));
+        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_ideal<2, 1>));
     else if (cfg->precise)
         e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<double, 4, false>));
     else
@@ -587,7 +567,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     out->registers = attr.numRegs;
     out->local_bytes = int32_t(attr.localSizeBytes);
     int blocks = 0;
-    const void *fn = kernel_id == 1 ? reinterpret_cast<const void *>(&k_ideal<2, 1, 4, 4>)
+    const void *fn = kernel_id == 1 ? reinterpret_cast<const void *>(&k_ideal<2, 1>)
                                     : reinterpret_cast<const void *>(&k_general<float, 8, false>);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) == hipSuccess)
         out->max_blocks_per_cu = blocks;

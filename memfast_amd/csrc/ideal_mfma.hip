@@ -23,6 +23,8 @@
 // Block = 4 waves: 2 (columns) x 2 (vectors); wave tile 32 columns x 32*TN
 // vectors; LDS holds codes [64 x 32*KS] and [64*TN x 32*KS] per read, double
 // buffered.  Roofline: int8 MFMA, with the VALU epilogue as co-bound.
+#include <type_traits>
+
 #include "mf_kernels.h"
 
 namespace mf {
@@ -45,18 +47,6 @@ __device__ __forceinline__ v4i sext4(v4i x, int bits) {
 __device__ __forceinline__ v4i and4(v4i x, u32 m) {
     const int mi = int(m);
     return v4i{x.x & mi, x.y & mi, x.z & mi, x.w & mi};
-}
-
-// Positive operand form: masked bytes, halved for an 8-bit sign slice (bit 7).
-__device__ __forceinline__ v4i pos4(v4i x, u32 m, int shift) {
-    v4i r = and4(x, m);
-    if (shift) {
-        r.x = int(u32(r.x) >> 1);
-        r.y = int(u32(r.y) >> 1);
-        r.z = int(u32(r.z) >> 1);
-        r.w = int(u32(r.w) >> 1);
-    }
-    return r;
 }
 
 __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
@@ -108,11 +98,18 @@ __global__ __launch_bounds__(256) void k_digit_bits(const u8 *codes, i64 rows, i
     }
 }
 
-template <int TN, int KS, int MAXCW, int MAXCA>
+// Buffer resource over [base, base + bytes): loads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, i64 bytes) {
+    const int records = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : int(bytes < 0 ? 0 : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), short(0), records,
+                                             0x00020000);
+}
+
+template <int TN, int KS>
 __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const IdealArgs args) {
     constexpr int BC = 64;                 // output columns per block
     constexpr int BV = 2 * TN * 32;        // vectors per block
-    constexpr int KB = 32 * KS;            // code bytes per row and read
+    constexpr int KB = 32 * KS;            // code bytes per row and read (= P)
     constexpr int STRIDE = KB + 16;        // LDS row stride (conflict-free b128 reads)
     constexpr int CHUNKS = KB / 16;
     constexpr int W_LOADS = (BC * CHUNKS + 255) / 256;
@@ -128,46 +125,59 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
     const int wc = wave & 1, wv = wave >> 1;
     const i64 c0 = i64(blockIdx.x) * BC;
     const i64 v0 = i64(blockIdx.y) * BV;
-    const i64 G = args.G;
-    const i64 cblock = (c0 + wc * 32) / 32;          // weight digit-max block (32 columns)
-    const i64 vblock = (v0 + wv * TN * 32) / 64;     // input digit-max block (64 vectors)
+    const int G = int(args.G);
+    const i64 cblock = (c0 + wc * 32) / 32;          // weight digit-bits block (32 columns)
+    const i64 vblock = (v0 + wv * TN * 32) / 64;     // input digit-bits block (64 vectors)
     const int lrow = lane & 31, lhalf = lane >> 5;
+    const i64 kp = args.kp;
+
+    // Block-local buffers: rows past n / ncols read as zero.
+    const i64 wrows = (args.ncols - c0) < BC ? (args.ncols - c0) : BC;
+    const i64 vrows = (args.n - v0) < BV ? (args.n - v0) : BV;
+    const __amdgpu_buffer_rsrc_t wbuf = buffer_of(args.wt + c0 * kp, wrows * kp);
+    const __amdgpu_buffer_rsrc_t xbuf = buffer_of(args.q + v0 * kp, vrows * kp);
+    const __amdgpu_buffer_rsrc_t wsbuf =
+        buffer_of(args.wscale + c0, (i64(G) * args.ldws - c0) * 4);
+    const __amdgpu_buffer_rsrc_t xsbuf = buffer_of(args.xscale + v0 * G, vrows * G * 4);
+
+    // Per-thread load slots (fixed across reads; the read adds g * P bytes).
+    int w_off[W_LOADS], x_off[X_LOADS];
+#pragma unroll
+    for (int e = 0; e < W_LOADS; ++e) {
+        const int c = tid + e * 256;
+        w_off[e] = (c / CHUNKS) * int(kp) + (c % CHUNKS) * 16;
+    }
+#pragma unroll
+    for (int e = 0; e < X_LOADS; ++e) {
+        const int c = tid + e * 256;
+        x_off[e] = (c / CHUNKS) * int(kp) + (c % CHUNKS) * 16;
+    }
+    const bool scale_w = tid < BC;
+    const bool scale_x = tid >= BC && tid < BC + BV;
+    const int scale_off = scale_w ? tid * 4 : (tid - BC) * G * 4;
 
     v4i rw[W_LOADS], rx[X_LOADS];
     float rscale = 0.0f;
-
-    auto fetch = [&](i64 g) {
-        const i64 kofs = (g / args.Gr) * args.R + (g % args.Gr) * args.P;
+    auto fetch = [&](int g) {
+        const int kofs = g * KB;
 #pragma unroll
-        for (int e = 0; e < W_LOADS; ++e) {
-            const int c = tid + e * 256;
-            const int row = c / CHUNKS, part = c % CHUNKS;
-            v4i v = v4i{0, 0, 0, 0};
-            if (c < BC * CHUNKS && c0 + row < args.ncols)
-                v = *reinterpret_cast<const v4i *>(args.wt + (c0 + row) * args.kp + kofs + part * 16);
-            rw[e] = v;
-        }
+        for (int e = 0; e < W_LOADS; ++e)
+            rw[e] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, w_off[e] + kofs, 0, 0);
 #pragma unroll
-        for (int e = 0; e < X_LOADS; ++e) {
-            const int c = tid + e * 256;
-            const int row = c / CHUNKS, part = c % CHUNKS;
-            v4i v = v4i{0, 0, 0, 0};
-            if (c < BV * CHUNKS && v0 + row < args.n)
-                v = *reinterpret_cast<const v4i *>(args.q + (v0 + row) * args.kp + kofs + part * 16);
-            rx[e] = v;
-        }
-        if (tid < BC) {
-            rscale = c0 + tid < args.ncols ? args.wscale[g * args.ldws + c0 + tid] : 0.0f;
-        } else if (tid < BC + BV) {
-            const int v = tid - BC;
-            rscale = v0 + v < args.n ? args.xscale[(v0 + v) * G + g] : 0.0f;
-        }
+        for (int e = 0; e < X_LOADS; ++e)
+            rx[e] = __builtin_amdgcn_raw_buffer_load_b128(xbuf, x_off[e] + kofs, 0, 0);
+        if (scale_w)
+            rscale = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                wsbuf, scale_off + g * int(args.ldws) * 4, 0, 0));
+        else if (scale_x)
+            rscale = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                xsbuf, scale_off + g * 4, 0, 0));
     };
     auto stash = [&](int buf) {
 #pragma unroll
         for (int e = 0; e < W_LOADS; ++e) {
             const int c = tid + e * 256;
-            if (c < BC * CHUNKS) {
+            if (W_LOADS * 256 == BC * CHUNKS || c < BC * CHUNKS) {
                 v4i v = rw[e];
                 if (args.w_bits < 8) v = sext4(v, args.w_bits);
                 *reinterpret_cast<v4i *>(&sW[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
@@ -176,14 +186,14 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
 #pragma unroll
         for (int e = 0; e < X_LOADS; ++e) {
             const int c = tid + e * 256;
-            if (c < BV * CHUNKS) {
+            if (X_LOADS * 256 == BV * CHUNKS || c < BV * CHUNKS) {
                 v4i v = rx[e];
                 if (args.a_bits < 8) v = sext4(v, args.a_bits);
                 *reinterpret_cast<v4i *>(&sX[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
             }
         }
-        if (tid < BC) sWS[buf][tid] = rscale;
-        else if (tid < BC + BV) sXS[buf][tid - BC] = rscale;
+        if (scale_w) sWS[buf][tid] = rscale;
+        else if (scale_x) sXS[buf][tid - BC] = rscale;
     };
 
     float acc0[TN][16], acc1[TN][16];
@@ -196,8 +206,10 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
     stash(0);
     __syncthreads();
 
-    for (i64 g = 0; g < G; ++g) {
-        const int cur = int(g & 1);
+    const uint64_t *xbits = args.xbits + vblock * G;
+    const uint64_t *wbits = args.wbits + cblock * G;
+    for (int g = 0; g < G; ++g) {
+        const int cur = g & 1;
         if (g + 1 < G) fetch(g + 1);
 
         v4i Wr[KS], Xr[TN][KS];
@@ -211,70 +223,79 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
                     &sX[cur][(wv * TN * 32 + tn * 32 + lrow) * STRIDE + ks * 32 + lhalf * 16]);
         }
 
+        // Static linear terms (the first one starts the accumulator from zero).
         v16i T[TN];
+        {
+            const u32 mw = plan.lin_w[0], mx = plan.lin_x[0];
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) T[tn] = v16i{};
-
-        // Static linear terms.
-        for (int t = 0; t < plan.n_lin; ++t) {
+            for (int tn = 0; tn < TN; ++tn) {
+                T[tn] = mfma(and4(Wr[0], mw), and4(Xr[tn][0], mx), v16i{});
+#pragma unroll
+                for (int ks = 1; ks < KS; ++ks)
+                    T[tn] = mfma(and4(Wr[ks], mw), and4(Xr[tn][ks], mx), T[tn]);
+            }
+        }
+        for (int t = 1; t < plan.n_lin; ++t) {
+            const u32 mw = plan.lin_w[t], mx = plan.lin_x[t];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const v4i wm = and4(Wr[ks], plan.lin_w[t]);
+                const v4i wm = and4(Wr[ks], mw);
 #pragma unroll
-                for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, and4(Xr[tn][ks], plan.lin_x[t]), T[tn]);
+                for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, and4(Xr[tn][ks], mx), T[tn]);
             }
         }
 
-        // Per-read decisions: slots (ca * 8 + cw) proven clamp-free on either
-        // side merge into one natural-form MFMA per input slice; the others get
-        // their own MFMA, a min and a signed multiply-add.  Scalar control only.
-        const uint64_t proven = args.xbits[vblock * G + g] | args.wbits[cblock * G + g];
+        // Slots (ca * 8 + cw) proven clamp-free on either side merge into one
+        // MFMA per input slice; the others get their own MFMA and a clamp.
+        const uint64_t proven = xbits[g] | wbits[g];
         const uint64_t fail = plan.exists & ~proven;
         const uint64_t safe = plan.exists & proven;
         for (int ca = 0; ca < plan.n_ca; ++ca) {
             const u32 safe_w = u32(safe >> (ca * 8)) & 0xFFu;
             u32 fail_w = u32(fail >> (ca * 8)) & 0xFFu;
-            v4i Xp[TN][KS];
+            if (!(safe_w | fail_w)) continue;
+            v4i Xn[TN][KS];
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    Xp[tn][ks] = pos4(Xr[tn][ks], plan.ca_xpos[ca], (plan.xshift_bits >> ca) & 1);
+                for (int ks = 0; ks < KS; ++ks) Xn[tn][ks] = and4(Xr[tn][ks], plan.ca_xnat[ca]);
             if (safe_w) {
                 u32 merged = 0;
                 for (u32 bits = safe_w; bits; bits &= bits - 1)
                     merged |= plan.cw_wnat[__builtin_ctz(bits)];
-                const bool same = (plan.same_bits >> ca) & 1;
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     const v4i wm = and4(Wr[ks], merged);
 #pragma unroll
+                    for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, Xn[tn][ks], T[tn]);
+                }
+            }
+            // A clamped pair's product Y = fa*fw*S has the sign of its limit
+            // lim = fa*fw*max: min() clamps positive pairs, max() negative ones.
+            const int fa = plan.ca_factor[ca];
+            const u32 neg_w = fail_w & (fa < 0 ? ~plan.cw_negative : plan.cw_negative);
+            auto clamped = [&](u32 bits, auto negative) {
+                for (; bits; bits &= bits - 1) {
+                    const int cw = __builtin_ctz(bits);
+                    v4i Wn[KS];
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) Wn[ks] = and4(Wr[ks], plan.cw_wnat[cw]);
+                    const int lim = fa * plan.cw_limit[cw];
+#pragma unroll
                     for (int tn = 0; tn < TN; ++tn) {
-                        const v4i xn = same ? Xp[tn][ks] : and4(Xr[tn][ks], plan.ca_xnat[ca]);
-                        T[tn] = mfma(wm, xn, T[tn]);
+                        v16i y = mfma(Wn[0], Xn[tn][0], v16i{});
+#pragma unroll
+                        for (int ks = 1; ks < KS; ++ks) y = mfma(Wn[ks], Xn[tn][ks], y);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            if constexpr (decltype(negative)::value) T[tn][r] += max(y[r], lim);
+                            else T[tn][r] += min(y[r], lim);
+                        }
                     }
                 }
-            }
-            for (; fail_w; fail_w &= fail_w - 1) {
-                const int cw = __builtin_ctz(fail_w);
-                v4i Wp[KS];
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    Wp[ks] = pos4(Wr[ks], plan.cw_wpos[cw], (plan.wshift_bits >> cw) & 1);
-                v16i y[TN];
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) {
-                    y[tn] = v16i{};
-#pragma unroll
-                    for (int ks = 0; ks < KS; ++ks) y[tn] = mfma(Wp[ks], Xp[tn][ks], y[tn]);
-                }
-                const int lim = plan.ca_posval[ca] * plan.cw_posmax[cw];
-                const int mul = plan.ca_msign[ca] * plan.cw_msign[cw];
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) T[tn][r] += __mul24(min(y[tn][r], lim), mul);
-            }
+            };
+            clamped(fail_w & ~neg_w, std::false_type{});
+            clamped(neg_w, std::true_type{});
         }
 
         // Scale restore (float(T) * xs) * ws and cascade accumulation.
@@ -292,7 +313,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
                 acc0[tn][r] = acc0[tn][r] + v;
             }
         }
-        const i64 count = g + 1;
+        const int count = g + 1;
         if ((count & 15) == 0) {
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
@@ -349,11 +370,9 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
     }
 }
 
-#define MF_IDEAL_INST(TN, KS, MAXCW, MAXCA) \
-    template __global__ void k_ideal<TN, KS, MAXCW, MAXCA>(const IdealPlan, const IdealArgs);
-MF_IDEAL_INST(2, 1, 4, 4)
-MF_IDEAL_INST(2, 1, 8, 8)
-MF_IDEAL_INST(1, 2, 4, 4)
-MF_IDEAL_INST(1, 2, 8, 8)
+#define MF_IDEAL_INST(TN, KS) template __global__ void k_ideal<TN, KS>(const IdealPlan, const IdealArgs);
+MF_IDEAL_INST(2, 1)
+MF_IDEAL_INST(1, 1)
+MF_IDEAL_INST(1, 2)
 
 }  // namespace mf

@@ -38,19 +38,20 @@ constexpr int IDEAL_MAX_CW = 8;     // weight slices with at least one clamped p
 // max_n sum_r da <= floor(max_w / Mw) (input side) or max_c sum_r dw <=
 // floor(max_w / Ma) (weight side).  The pre-pass k_digit_bits evaluates these
 // tests and stores one 64-bit slot mask per (block, read).
-// Operand "natural" forms are masked two's complement bytes whose int8 value is
-// factor*digit; "positive" forms are masked (and, for an 8-bit sign slice,
-// halved) bytes whose value is posval*digit with factor = msign*posval.
+// Operands are "natural" forms: masked two's complement bytes whose int8 value
+// is the sum of factor*digit over the slices in the mask.  A clamped pair's
+// product Y = fa*fw*S is clamped to fa*fw*max_w (min for positive pairs,
+// max for negative ones).
 struct IdealPlan {
     int n_lin;
-    u32 lin_w[IDEAL_MAX_LIN], lin_x[IDEAL_MAX_LIN];   // natural masks, weight / input side
+    u32 lin_w[IDEAL_MAX_LIN], lin_x[IDEAL_MAX_LIN];   // weight / input side masks
     int n_ca, n_cw;
-    u32 ca_xnat[IDEAL_MAX_CA], ca_xpos[IDEAL_MAX_CA];
-    int ca_posval[IDEAL_MAX_CA], ca_msign[IDEAL_MAX_CA];
-    u32 cw_wnat[IDEAL_MAX_CW], cw_wpos[IDEAL_MAX_CW];
-    int cw_posmax[IDEAL_MAX_CW], cw_msign[IDEAL_MAX_CW];   // posval_w * max_w
-    u32 xshift_bits, wshift_bits, same_bits;  // per ca / cw / ca (natural == positive form)
-    uint64_t exists;                          // slots holding a clamp-candidate pair
+    u32 ca_xnat[IDEAL_MAX_CA];
+    int ca_factor[IDEAL_MAX_CA];                      // fa
+    u32 cw_wnat[IDEAL_MAX_CW];
+    int cw_limit[IDEAL_MAX_CW];                       // fw * max_w
+    u32 cw_negative;                                  // bit cw: fw < 0
+    uint64_t exists;                                  // slots holding a clamp candidate
 };
 
 // Tests evaluated by k_digit_bits for one side: slot s passes when the block's
@@ -74,7 +75,7 @@ struct IdealArgs {
     int a_bits, w_bits;     // code widths (< 8: sign-extend bytes on load)
 };
 
-template <int TN, int KS, int MAXCW, int MAXCA>
+template <int TN, int KS>
 __global__ void k_ideal(const IdealPlan plan, const IdealArgs args);
 
 struct SliceLayout {

@@ -138,7 +138,7 @@ SIGNATURES = {
     "mf_partial": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
                     _P, _P, _P], ct.c_int),
     "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
-               _I64, _P, _I64, _P], ct.c_int),
+               _I64, _P, _I64, _I32, _P], ct.c_int),
     "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, ct.POINTER(_I64)], ct.c_int),
     "mf_mm_kernel": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I32)], ct.c_int),
     "mf_resources_query": ([_CFG, _I32, ct.POINTER(MFResources)], ct.c_int),
@@ -470,7 +470,8 @@ def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance
     return (totals, counts) if codes else totals
 
 
-def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=None, out=None):
+def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=None, out=None,
+       variant=0):
     """Fused read + scale restore: [N, p*C] FP32, summed over reads in torch's order."""
     supported(config)
     require_device(q)
@@ -500,7 +501,7 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
                 ct.byref(descriptor(config)), _ptr(q.contiguous()), _ptr(xscale.contiguous()), n,
                 m, _ptr(packed.contiguous()), _ptr(packed_t), _ptr(wscale.contiguous()), p,
                 _ptr(g), seed, event, _ptr(out), out.stride(0), _ptr(workspace),
-                0 if workspace is None else workspace.numel(), _stream(q.device),
+                0 if workspace is None else workspace.numel(), variant, _stream(q.device),
             ),
             "mm",
         )
