@@ -50,15 +50,16 @@ def time_steps(fn, steps, warmup):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    hip.kernel_timer = []
+    hip.collect_kernel_times()
+    hip.profile_kernels(True)
     start = time.perf_counter()
     for _ in range(steps):
         fn()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
-    timer, hip.kernel_timer = hip.kernel_timer, None
-    kernel_ms = sum(s.elapsed_time(e) for s, e in timer) / max(1, len(timer))
-    return elapsed / steps * 1e3, kernel_ms
+    hip.profile_kernels(False)
+    launches, total_ms = hip.collect_kernel_times()
+    return elapsed / steps * 1e3, total_ms / max(1, launches)
 
 
 def main():

@@ -40,6 +40,16 @@ enum {
 
 enum { MF_READ_SHARED = 0, MF_READ_SLICE_PAIR = 1, MF_READ_OUTPUT = 2 };
 
+/* Bits kernels OR into a caller-owned device status word (uint32) instead of
+ * synchronizing: the caller reads it once per product and raises the matching
+ * error (memfast/functional.py:49-53, quantization.py:25-26,
+ * simulator.py:614-615 and :643-644 check the same conditions on the host). */
+enum {
+    MF_STATUS_INPUT = 1,   /* non-finite activation value */
+    MF_STATUS_WEIGHT = 2,  /* non-finite weight value */
+    MF_STATUS_OUTPUT = 4   /* non-finite FP32 output of mf_mm */
+};
+
 /* Physical configuration (memfast/config.py:21-224), derived on the host.
  * f_* members are the FP32 values the reference's torch CPU ops use (Python
  * scalars are rounded to FP32 before they meet an FP32 tensor); d_* are the
@@ -101,30 +111,30 @@ const char *mf_source_hash(void);
 int mf_device_identity(int device, mf_identity *out);
 
 /* ---- quantization and programming --------------------------------------- */
-/* Grouped INT quantization of x [rows, cols] (FP32, row stride ld) with
- * rectangular groups (gr, gc): memfast/quantization.py:9-44 for bits <= 8.
- * Writes the per-group scale to `scale` [ceil(rows/gr), ceil(cols/gc)].
- * `work` is caller scratch of the same size (uint32 group maxima). */
-int mf_group_scales(const float *x, int64_t rows, int64_t cols, int64_t ld, int64_t gr,
-                    int64_t gc, int32_t bits, int32_t is_signed, uint32_t *work,
-                    float *scale, void *stream);
-
-/* Input tiles (memfast/quantization.py:115-137): codes q [n, m*R] (uint8, two's
- * complement masked to activation_bits, zero padded) and per-read scales
- * xscale [n, m*Gr].  `scale` is either the group-scale grid from
- * mf_group_scales (fixed == 0) or a [1, k] fixed scale row (fixed == 1). */
+/* Fixed-scale input tiles (memfast/quantization.py:115-137 with fixed_scale, the
+ * set_input_scale path): codes q [n, m*R] (uint8, two's complement masked to
+ * activation_bits, zero padded) and per-read scales xscale [n, m*Gr] from a
+ * per-feature scale row `scale` [k]. */
 int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
-                   const float *scale, int64_t gr, int64_t gc, int32_t fixed, uint8_t *q,
-                   float *xscale, void *stream);
+                   const float *scale, uint8_t *q, float *xscale, void *stream);
 
-/* Weight tiles (memfast/quantization.py:82-112): logical [k, o] matrix b (row
- * stride ld) -> packed [m, p, R, C] uint8 (the reference layout), the same codes
- * column-major as packed_t [p*C, m*R] for the MFMA kernel, and per-read scales
- * wscale [m*Gr, p*C].  `scale` is the group grid from mf_group_scales.
- * packed_t may be NULL. */
-int mf_weight_tiles(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
-                    const float *scale, int64_t gr, int64_t gc, uint8_t *packed,
-                    uint8_t *packed_t, float *wscale, void *stream);
+/* Dynamic grouped quantization of activations, whole (memfast/quantization.py:9-44
+ * followed by input_tiles :115-137): group-scale grid scale [ceil(n/gr), ceil(k/gc)],
+ * codes q [n, m*R] and per-read scales xscale [n, m*Gr] in one call.  Row-local
+ * groups (gr == 1) run one fused pass; other shapes need `work` (uint32, grid
+ * sized).  status (may be NULL) receives MF_STATUS_INPUT for a non-finite x. */
+int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
+                       int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *q,
+                       float *xscale, uint32_t *status, void *stream);
+
+/* Dynamic grouped quantization and programming of a logical [k, o] weight
+ * matrix (memfast/quantization.py:9-44 followed by weight_tiles :82-112):
+ * scale grid, packed [m, p, R, C], packed_t [p*C, m*R] (may be NULL) and
+ * wscale [m*Gr, p*C].  Column-local groups (gc == 1, gr <= 256) run one fused
+ * pass; other shapes need `work`.  status receives MF_STATUS_WEIGHT. */
+int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
+                        int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *packed,
+                        uint8_t *packed_t, float *wscale, uint32_t *status, void *stream);
 
 /* packed [m, p, R, C] -> packed_t [p*C, m*R] (for checkpoints loaded from disk). */
 int mf_transpose_packed(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p,
@@ -156,11 +166,30 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
  * For ideal devices with packed_t != NULL and a workspace of at least
  * mf_mm_workspace() bytes (256-byte aligned) the MFMA kernel is used;
  * `variant` picks its tiling (0 default, 1: 64 vectors per wave, 2: 32 vectors
- * per wave; the tuned mode's schedule grid).  Results do not depend on it. */
+ * per wave; the tuned mode's schedule grid).  Results do not depend on it.
+ * status (may be NULL) receives MF_STATUS_OUTPUT when an output is non-finite. */
 int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
           const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo,
-          void *workspace, int64_t workspace_bytes, int32_t variant, void *stream);
+          void *workspace, int64_t workspace_bytes, int32_t variant, uint32_t *status,
+          void *stream);
+
+/* Overflow-safe FP64 restore and read sum of one chunk of `width` tiles
+ * (memfast/simulator.py:57-66 restore_scales and :578-585, the wide/retry path
+ * taken when the FP32 restore is non-finite, :614-615): totals [n, G, width*C]
+ * from mf_partial, xscale [n, G], wscale [G, ldws]; writes the FP64 sums to
+ * out[v * ldo + col0 + c] for c < width*C, in torch's CPU summation order. */
+int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,
+                  const float *xscale, const float *wscale, int64_t ldws, int64_t col0, double *out,
+                  int64_t ldo, void *stream);
+
+/* Benchmark timing of mf_mm's main read kernel (no reference counterpart; the
+ * reference times whole candidate calls with CUDA events, memfast/simulator.py:306-316):
+ * while enabled, each mf_mm call records a HIP event pair on its stream around
+ * the read-kernel launch only.  mf_profile_collect waits for the recorded pairs
+ * and returns their count and summed milliseconds, then forgets them. */
+int mf_profile_kernels(int32_t enable);
+int mf_profile_collect(int64_t *launches, double *milliseconds);
 
 /* Workspace bytes mf_mm needs for the MFMA kernel (per-read digit-sum maxima). */
 int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64_t *bytes);

@@ -7,6 +7,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <utility>
+#include <vector>
 
 #include "mf_kernels.h"
 
@@ -25,6 +27,26 @@ __global__ void k_rng(const u64 *address, i64 count, u64 seed, u32 stream, int k
 
 // ---------------------------------------------------------------------------
 thread_local char g_error[1024] = "";
+
+// Read-kernel timing for benchmarks: event pairs recorded around the main read
+// kernel of each mf_mm call while enabled (single host thread, as torch's).
+struct ProfileState {
+    bool enabled = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending, spare;
+};
+ProfileState g_profile;
+
+std::pair<hipEvent_t, hipEvent_t> profile_pair() {
+    if (!g_profile.spare.empty()) {
+        auto pair = g_profile.spare.back();
+        g_profile.spare.pop_back();
+        return pair;
+    }
+    std::pair<hipEvent_t, hipEvent_t> pair{nullptr, nullptr};
+    if (hipEventCreate(&pair.first) != hipSuccess || hipEventCreate(&pair.second) != hipSuccess)
+        return {nullptr, nullptr};
+    return pair;
+}
 
 int fail(int code, const char *fmt, ...) {
     va_list ap;
@@ -297,28 +319,8 @@ int mf_device_identity(int device, mf_identity *out) {
     return MF_OK;
 }
 
-int mf_group_scales(const float *x, int64_t rows, int64_t cols, int64_t ld, int64_t gr,
-                    int64_t gc, int32_t bits, int32_t is_signed, uint32_t *work, float *scale,
-                    void *stream) {
-    if (!x || !work || !scale || rows < 1 || cols < 1 || ld < cols || gr < 1 || gc < 1)
-        return fail(MF_E_INVALID, "invalid group-scale arguments");
-    if (bits < 2 || bits > 8) return fail(MF_E_UNSUPPORTED, "group scales support 2..8 bits");
-    gr = gr < rows ? gr : rows;
-    gc = gc < cols ? gc : cols;
-    const i64 nrg = (rows + gr - 1) / gr, ncg = (cols + gc - 1) / gc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
-    hipLaunchKernelGGL(k_group_max, dim3(grid_for(rows * ((cols + 7) / 8))), dim3(256), 0, s, x,
-                       rows, cols, ld, gr, gc, ncg, work);
-    const float upper = float((1 << (bits - (is_signed ? 1 : 0))) - 1);
-    hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg,
-                       upper, scale);
-    return check_launch("group scales");
-}
-
 int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
-                   const float *scale, int64_t gr, int64_t gc, int32_t fixed, uint8_t *q,
-                   float *xscale, void *stream) {
+                   const float *scale, uint8_t *q, float *xscale, void *stream) {
     int status = check_config(cfg);
     if (status) return status;
     if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k)
@@ -326,42 +328,103 @@ int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, i
     const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
     const i64 m = (k + R - 1) / R;
     const i64 kp = m * R;
-    gr = gr < n ? gr : n;
-    gc = gc < k ? gc : k;
-    const i64 ncg = (k + gc - 1) / gc;
     const int bits = cfg->activation_bits;
     const float upper = float((1 << (bits - 1)) - 1);
     const u32 mask = (1u << bits) - 1u;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(k_input_codes, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
-                       scale, gr, gc, ncg, fixed, -upper, upper, mask, q);
+                       scale, i64(1), i64(1), k, 1, -upper, upper, mask, q);
     hipLaunchKernelGGL(k_input_scales, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k, m * Gr,
-                       R, P, Gr, scale, gr, gc, ncg, fixed, xscale);
+                       R, P, Gr, scale, i64(1), i64(1), k, 1, xscale);
     return check_launch("input tiles");
 }
 
-int mf_weight_tiles(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
-                    const float *scale, int64_t gr, int64_t gc, uint8_t *packed,
-                    uint8_t *packed_t, float *wscale, void *stream) {
-    int status = check_config(cfg);
-    if (status) return status;
-    if (!b || !scale || !packed || !wscale || k < 1 || o < 1 || ld < o)
-        return fail(MF_E_INVALID, "invalid weight-tile arguments");
+static i64 lcm4(i64 gr) { return gr % 4 == 0 ? gr : (gr % 2 == 0 ? 2 * gr : 4 * gr); }
+
+int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
+                       int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *q,
+                       float *xscale, uint32_t *status, void *stream) {
+    int status_code = check_config(cfg);
+    if (status_code) return status_code;
+    if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k || gr < 1 || gc < 1)
+        return fail(MF_E_INVALID, "invalid input quantization arguments");
+    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (k + R - 1) / R, kp = m * R;
+    gr = gr < n ? gr : n;
+    gc = gc < k ? gc : k;
+    const i64 nrg = (n + gr - 1) / gr, ncg = (k + gc - 1) / gc;
+    const int bits = cfg->activation_bits;
+    const float upper = float((1 << (bits - 1)) - 1);
+    const u32 mask = (1u << bits) - 1u;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (gr == 1 && gc <= 1024) {
+        const bool vec = gc % 4 == 0 && k % 4 == 0 && kp % 4 == 0 && ld % 4 == 0 &&
+                         reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(q) % 4 == 0;
+        if (vec)
+            hipLaunchKernelGGL(k_row_groups<true>, dim3(grid_for(n * ncg)), dim3(256), 0, s, x, n, k,
+                               ld, gc, ncg, kp, -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+        else
+            hipLaunchKernelGGL(k_row_groups<false>, dim3(grid_for(n * ncg)), dim3(256), 0, s, x, n,
+                               k, ld, gc, ncg, kp, -upper, upper, mask, q, scale, status,
+                               u32(MF_STATUS_INPUT));
+    } else {
+        if (!work) return fail(MF_E_INVALID, "grouped input quantization needs a work buffer");
+        hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
+        hipLaunchKernelGGL(k_group_max, dim3(grid_for(n * ((k + 7) / 8))), dim3(256), 0, s, x, n, k,
+                           ld, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT));
+        hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
+                           nrg * ncg, upper, scale);
+        hipLaunchKernelGGL(k_input_codes, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
+                           scale, gr, gc, ncg, 0, -upper, upper, mask, q);
+    }
+    hipLaunchKernelGGL(k_input_scales, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k, m * Gr, R,
+                       P, Gr, scale, gr, gc, ncg, 0, xscale);
+    return check_launch("input quantization");
+}
+
+int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
+                        int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *packed,
+                        uint8_t *packed_t, float *wscale, uint32_t *status, void *stream) {
+    int status_code = check_config(cfg);
+    if (status_code) return status_code;
+    if (!b || !scale || !packed || !wscale || k < 1 || o < 1 || ld < o || gr < 1 || gc < 1)
+        return fail(MF_E_INVALID, "invalid weight quantization arguments");
     const int R = cfg->rows, C = cfg->cols, P = cfg->read_rows, Gr = cfg->reads;
-    const i64 m = (k + R - 1) / R, p = (o + C - 1) / C;
+    const i64 m = (k + R - 1) / R, p = (o + C - 1) / C, kp = m * R, op = p * C;
     gr = gr < k ? gr : k;
     gc = gc < o ? gc : o;
-    const i64 ncg = (o + gc - 1) / gc;
+    const i64 nrg = (k + gr - 1) / gr, ncg = (o + gc - 1) / gc;
     const int bits = cfg->weight_bits;
     const float upper = float((1 << (bits - (cfg->weight_signed ? 1 : 0))) - 1);
     const float lower = cfg->weight_signed ? -upper : 0.0f;
     const u32 mask = (1u << bits) - 1u;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(k_weight_codes, dim3(grid_for(m * R * p * C)), dim3(256), 0, s, b, k, o, ld,
-                       R, C, m, p, scale, gr, gc, ncg, lower, upper, mask, packed, packed_t);
-    hipLaunchKernelGGL(k_weight_scales, dim3(grid_for(m * Gr * p * C)), dim3(256), 0, s, k, o,
-                       m * Gr, p * C, R, P, Gr, scale, gr, gc, ncg, wscale);
-    return check_launch("weight tiles");
+    const i64 unit = lcm4(gr);
+    const i64 span = unit >= 128 ? unit : unit * (128 / unit);
+    if (gc == 1 && gr <= 256 && (kp + span - 1) / span <= 65535) {
+        const dim3 grid{unsigned((op + 255) / 256), unsigned((kp + span - 1) / span), 1u};
+        if (kp % 4 == 0)
+            hipLaunchKernelGGL(k_col_groups<true>, grid, dim3(256), 0, s, b, k, o, ld, gr, span, R, C,
+                               m, p, lower, upper, mask, packed, packed_t, scale, status,
+                               u32(MF_STATUS_WEIGHT));
+        else
+            hipLaunchKernelGGL(k_col_groups<false>, grid, dim3(256), 0, s, b, k, o, ld, gr, span, R,
+                               C, m, p, lower, upper, mask, packed, packed_t, scale, status,
+                               u32(MF_STATUS_WEIGHT));
+    } else {
+        if (!work) return fail(MF_E_INVALID, "grouped weight quantization needs a work buffer");
+        hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
+        hipLaunchKernelGGL(k_group_max, dim3(grid_for(k * ((o + 7) / 8))), dim3(256), 0, s, b, k, o,
+                           ld, gr, gc, ncg, work, status, u32(MF_STATUS_WEIGHT));
+        hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
+                           nrg * ncg, upper, scale);
+        hipLaunchKernelGGL(k_weight_codes, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o, ld, R,
+                           C, m, p, scale, gr, gc, ncg, lower, upper, mask, packed, packed_t);
+    }
+    hipLaunchKernelGGL(k_weight_scales, dim3(grid_for(m * Gr * op)), dim3(256), 0, s, k, o, m * Gr,
+                       op, R, P, Gr, scale, gr, gc, ncg, wscale);
+    return check_launch("weight quantization");
 }
 
 int mf_transpose_packed(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p,
@@ -461,9 +524,9 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64
 int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
           const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo, void *workspace,
-          int64_t workspace_bytes, int32_t variant, void *stream) {
-    int status = check_config(cfg);
-    if (status) return status;
+          int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream) {
+    const int valid = check_config(cfg);
+    if (valid) return valid;
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
         ldo < p * cfg->cols)
         return fail(MF_E_INVALID, "invalid mm arguments");
@@ -500,6 +563,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         args.xbits = xbits;
         args.wbits = wbits;
         args.out = out;
+        args.status = status;
         args.n = n;
         args.kp = kp;
         args.G = G;
@@ -518,9 +582,15 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (ncols + 63) / 64;
         if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
         const dim3 grid{unsigned(gx), unsigned(gy), 1u};
+        std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
         if (ks == 1 && tn == 2) hipLaunchKernelGGL((k_ideal<2, 1>), grid, dim3(256), 0, s, plan, args);
         else if (ks == 1) hipLaunchKernelGGL((k_ideal<1, 1>), grid, dim3(256), 0, s, plan, args);
         else hipLaunchKernelGGL((k_ideal<1, 2>), grid, dim3(256), 0, s, plan, args);
+        if (timing.first) {
+            hipEventRecord(timing.second, s);
+            g_profile.pending.push_back(timing);
+        }
         return check_launch("ideal MFMA read");
     }
     if (!g && needs_conductances(cfg))
@@ -532,6 +602,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
     args.xscale = xscale;
     args.wscale = wscale;
     args.out = out;
+    args.status = status;
     args.n = n;
     args.m = m;
     args.p = p;
@@ -544,8 +615,54 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
     args.planes = g ? restore_planes(cfg) : 1;
     args.lp_cascade = level_power(G);
     args.lp_interleaved = level_power(G / 4);
-    return cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
-                        : launch_general<float>(cfg, args, OUT_FUSED, s);
+    std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+    if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+    const int launched = cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
+                                      : launch_general<float>(cfg, args, OUT_FUSED, s);
+    if (timing.first) {
+        hipEventRecord(timing.second, s);
+        g_profile.pending.push_back(timing);
+    }
+    return launched;
+}
+
+int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,
+                  const float *xscale, const float *wscale, int64_t ldws, int64_t col0, double *out,
+                  int64_t ldo, void *stream) {
+    const int valid = check_config(cfg);
+    if (valid) return valid;
+    const i64 wc = width * cfg->cols;
+    if (!totals || !xscale || !wscale || !out || n < 1 || G < 1 || width < 1 || col0 < 0 ||
+        ldws < col0 + wc || ldo < col0 + wc || G > 0x7FFFFFFF)
+        return fail(MF_E_INVALID, "invalid stable-sum arguments");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_stable_sum, dim3(grid_for(n * wc)), dim3(256), 0, s, totals, n, G, wc,
+                       xscale, wscale, ldws, col0, out, ldo, level_power(G), level_power(G / 4));
+    return check_launch("stable sum");
+}
+
+int mf_profile_kernels(int32_t enable) {
+    g_profile.enabled = enable != 0;
+    return MF_OK;
+}
+
+int mf_profile_collect(int64_t *launches, double *milliseconds) {
+    if (!launches || !milliseconds) return fail(MF_E_INVALID, "profile outputs are NULL");
+    *launches = 0;
+    *milliseconds = 0.0;
+    int status = MF_OK;
+    for (auto &pair : g_profile.pending) {
+        float ms = 0.0f;
+        hipError_t e = hipEventSynchronize(pair.second);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, pair.first, pair.second);
+        if (e != hipSuccess && status == MF_OK)
+            status = fail(MF_E_HIP, "kernel timing failed: %s", hipGetErrorString(e));
+        *milliseconds += ms;
+        ++*launches;
+        g_profile.spare.push_back(pair);
+    }
+    g_profile.pending.clear();
+    return status;
 }
 
 int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *out) {

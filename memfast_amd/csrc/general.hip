@@ -12,6 +12,8 @@
 // Block: 8 vectors x 32 columns, one thread per output.  Per 32-row chunk the
 // block stages voltages (all input slices) and conductances (a group of
 // weight slices) in LDS.  Bound: VALU FMAs, K*A*W per output.
+#include <cfloat>
+
 #include "mf_kernels.h"
 
 namespace mf {
@@ -229,8 +231,9 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
     }
     if (live && out_kind == OUT_FUSED) {
         const i64 o = args.begin * C + col;
-        args.out[vec * args.ldo + o] =
-            use_interleaved ? interleaved.finish(int(G)) : cascade.finish();
+        const float value = use_interleaved ? interleaved.finish(int(G)) : cascade.finish();
+        args.out[vec * args.ldo + o] = value;
+        if (!(fabsf(value) <= FLT_MAX) && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
     }
 }
 

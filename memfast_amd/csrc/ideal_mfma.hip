@@ -23,6 +23,7 @@
 // Block = 4 waves: 2 (columns) x 2 (vectors); wave tile 32 columns x 32*TN
 // vectors; LDS holds codes [64 x 32*KS] and [64*TN x 32*KS] per read, double
 // buffered.  Roofline: int8 MFMA, with the VALU epilogue as co-bound.
+#include <cfloat>
 #include <type_traits>
 
 #include "mf_kernels.h"
@@ -344,6 +345,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
         __syncthreads();
     }
 
+    bool finite = true;
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
         const i64 n = v0 + wv * TN * 32 + tn * 32 + lrow;
@@ -358,6 +360,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
                 float s = acc0[tn][qd * 4 + e] + acc1[tn][qd * 4 + e];
                 if (G >= 256 && c + e < args.ncols) s = s + dst[e];
                 v[e] = s;
+                finite = finite && (c + e >= args.ncols || fabsf(s) <= FLT_MAX);
             }
             if (c + 3 < args.ncols) {
                 *reinterpret_cast<v4f *>(dst) = v;
@@ -368,6 +371,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
             }
         }
     }
+    if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
 #define MF_IDEAL_INST(TN, KS) template __global__ void k_ideal<TN, KS>(const IdealPlan, const IdealArgs);

@@ -17,6 +17,7 @@ struct GeneralArgs {
     const float *wscale;  // [G, ldws]
     float *out;           // fused: [n, ldo]; totals: [n, G, width, C]
     int32_t *codes;       // optional [n, G, A, W, width*C]
+    u32 *status;          // optional: MF_STATUS_OUTPUT for a non-finite fused output
     i64 n, m, p, begin, width, ldo, ldws;
     u32 seed;
     u64 event;
@@ -70,6 +71,7 @@ struct IdealArgs {
     const uint64_t *xbits;  // [ceil(n/64), G] input-side proven slots per 64 vectors
     const uint64_t *wbits;  // [ceil(ncols/32), G] weight-side proven slots per 32 columns
     float *out;             // [n, ldo]
+    u32 *status;            // optional: MF_STATUS_OUTPUT for a non-finite output
     i64 n, kp, G, ldo, ldws, ncols;
     int Gr, R, P;
     int a_bits, w_bits;     // code widths (< 8: sign-extend bytes on load)
@@ -95,10 +97,23 @@ template <typename Phys>
 __global__ void k_restore(const mf_config cfg, const u8 *packed, i64 m, i64 p, i64 begin,
                           i64 width, u32 seed, u64 event, int planes, Phys *g);
 
+// ---- FP64 restore and read sum (stable.hip) --------------------------------
+__global__ void k_stable_sum(const float *totals, i64 n, i64 G, i64 wc, const float *xscale,
+                             const float *wscale, i64 ldws, i64 col0, double *out, i64 ldo,
+                             int lp_cascade, int lp_interleaved);
+
 // ---- quantization (quantize.hip) ------------------------------------------
 __global__ void k_fill_u32(u32 *p, i64 count, u32 value);
 __global__ void k_group_max(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,
-                            u32 *work);
+                            u32 *work, u32 *status, u32 flag);
+template <bool VEC>
+__global__ void k_row_groups(const float *x, i64 n, i64 k, i64 ld, i64 gc, i64 ncg, i64 kp,
+                             float lower, float upper, u32 mask, u8 *q, float *scale,
+                             u32 *status, u32 flag);
+template <bool WORD>
+__global__ void k_col_groups(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 span, int R,
+                             int C, i64 m, i64 p, float lower, float upper, u32 mask,
+                             u8 *packed, u8 *packed_t, float *scale, u32 *status, u32 flag);
 __global__ void k_group_scale(const u32 *work, i64 groups, float upper, float *scale);
 __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
                               i64 gr, i64 gc, i64 ncg, int fixed, float lower, float upper,

@@ -6,6 +6,8 @@
 // correctly rounded FP32 (as torch CPU's true division) and rounding is
 // round-half-even (rintf), so codes and scales are bit-identical to the CPU
 // reference.  All kernels are HBM-bound elementwise passes.
+#include <cfloat>
+
 #include "mf_kernels.h"
 
 namespace mf {
@@ -18,11 +20,13 @@ __global__ void k_fill_u32(u32 *p, i64 count, u32 value) {
 
 // Per-group max |x| via an integer atomicMax on the FP32 bit pattern (|x| >= 0
 // orders like its bits).  Each thread first folds a run of up to 8 elements
-// of one row that lie in the same group, to cut atomic traffic.
+// of one row that lie in the same group, to cut atomic traffic.  A non-finite
+// element ORs `flag` into *status (when status is non-null).
 __global__ void k_group_max(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
-                            i64 ncg, u32 *work) {
+                            i64 ncg, u32 *work, u32 *status, u32 flag) {
     const i64 runs_per_row = (cols + 7) / 8;
     const i64 total = rows * runs_per_row;
+    bool finite = true;
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += i64(gridDim.x) * blockDim.x) {
         const i64 r = i / runs_per_row;
@@ -39,11 +43,14 @@ __global__ void k_group_max(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, 
                 group = g;
                 best = 0;
             }
-            const u32 bits = __float_as_uint(fabsf(row[c]));
+            const float v = fabsf(row[c]);
+            finite = finite && v <= FLT_MAX;
+            const u32 bits = __float_as_uint(v);
             best = bits > best ? bits : best;
         }
         if (group >= 0) atomicMax(&work[(r / gr) * ncg + group], best);
     }
+    if (!finite && status) atomicOr(status, flag);
 }
 
 // scale = (max > 0 ? max : 1) / upper, clamped below by the smallest subnormal.
@@ -65,6 +72,135 @@ __device__ __forceinline__ u8 quantize_code(float x, float s, float lower, float
     c = c > upper ? upper : c;
     return u8(u32(int(c)) & mask);
 }
+
+// scale of one group from its peak |x| (quantization.py:25-31 for INT codes).
+__device__ __forceinline__ float group_scale(float peak, float upper) {
+    float s = (peak > 0.0f ? peak : 1.0f) / upper;
+    const float tiny = __uint_as_float(1u);
+    return s < tiny ? tiny : s;
+}
+
+// Fused grouped quantization of row-local groups (gr == 1, the activation
+// layout): one thread per (row, group of gc columns) computes the group's peak,
+// its scale (stored in the grid scale [n, ncg]) and the codes of q [n, kp]; the
+// thread of a row's last group also writes the zero padding [k, kp).  The
+// second pass over the group re-reads it from cache.  VEC: 16-byte loads and
+// 4-byte code stores (gc, k, kp and ld multiples of 4, x 16-byte aligned).
+template <bool VEC>
+__global__ void k_row_groups(const float *x, i64 n, i64 k, i64 ld, i64 gc, i64 ncg, i64 kp,
+                             float lower, float upper, u32 mask, u8 *q, float *scale,
+                             u32 *status, u32 flag) {
+    const i64 total = n * ncg;
+    bool finite = true;
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += i64(gridDim.x) * blockDim.x) {
+        const i64 row = i / ncg, j = i - row * ncg;
+        const i64 c0 = j * gc, c1 = (c0 + gc) < k ? (c0 + gc) : k;
+        const float *src = x + row * ld;
+        u8 *dst = q + row * kp;
+        float peak = 0.0f;
+        if (VEC) {
+            for (i64 c = c0; c < c1; c += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(src + c);
+                const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
+                finite = finite && a0 <= FLT_MAX && a1 <= FLT_MAX && a2 <= FLT_MAX && a3 <= FLT_MAX;
+                peak = fmaxf(peak, fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+            }
+        } else {
+            for (i64 c = c0; c < c1; ++c) {
+                const float a = fabsf(src[c]);
+                finite = finite && a <= FLT_MAX;
+                peak = fmaxf(peak, a);
+            }
+        }
+        const float s = group_scale(peak, upper);
+        scale[i] = s;
+        if (VEC) {
+            for (i64 c = c0; c < c1; c += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(src + c);
+                const u32 word = u32(quantize_code(v.x, s, lower, upper, mask)) |
+                                 u32(quantize_code(v.y, s, lower, upper, mask)) << 8 |
+                                 u32(quantize_code(v.z, s, lower, upper, mask)) << 16 |
+                                 u32(quantize_code(v.w, s, lower, upper, mask)) << 24;
+                *reinterpret_cast<u32 *>(dst + c) = word;
+            }
+            if (j == ncg - 1)
+                for (i64 c = k; c < kp; c += 4) *reinterpret_cast<u32 *>(dst + c) = 0u;
+        } else {
+            for (i64 c = c0; c < c1; ++c) dst[c] = quantize_code(src[c], s, lower, upper, mask);
+            if (j == ncg - 1)
+                for (i64 c = k; c < kp; ++c) dst[c] = 0;
+        }
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+template __global__ void k_row_groups<true>(const float *, i64, i64, i64, i64, i64, i64, float,
+                                            float, u32, u8 *, float *, u32 *, u32);
+template __global__ void k_row_groups<false>(const float *, i64, i64, i64, i64, i64, i64, float,
+                                             float, u32, u8 *, float *, u32 *, u32);
+
+// Fused grouped quantization of column-local groups (gc == 1, the weight
+// layout of quantization.py:82-112): thread = one physical column `col` of the
+// padded [kp, op] code matrix and one chunk of `span` rows (a multiple of gr,
+// so groups never straddle chunks).  Lanes take consecutive columns, so the
+// FP32 reads, the packed [m, p, R, C] bytes and the scale grid [nrg, o] are
+// coalesced; each thread writes its run of packed_t [op, kp] (column-major)
+// itself, four rows per 4-byte store when WORD (kp and span multiples of 4).
+template <bool WORD>
+__global__ void k_col_groups(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 span, int R,
+                             int C, i64 m, i64 p, float lower, float upper, u32 mask,
+                             u8 *packed, u8 *packed_t, float *scale, u32 *status, u32 flag) {
+    const i64 kp = m * R, op = p * C;
+    const i64 col = i64(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (col >= op) return;
+    const i64 r0 = i64(blockIdx.y) * span;
+    const i64 r1 = (r0 + span) < kp ? (r0 + span) : kp;
+    if (r0 >= r1) return;
+    const i64 t = col / C, c = col - t * C;
+    i64 tile = r0 / R, r = r0 - tile * R;   // packed coordinates of the current row
+    u8 *column_t = packed_t ? packed_t + col * kp : nullptr;
+    u32 word = 0;
+    bool finite = true;
+    auto put = [&](i64 row, u8 code) {
+        packed[((tile * p + t) * R + r) * C + c] = code;
+        if (++r == R) { r = 0; ++tile; }
+        if (column_t) {
+            if (WORD) {
+                word |= u32(code) << (8 * (row & 3));
+                if ((row & 3) == 3) {
+                    *reinterpret_cast<u32 *>(column_t + row - 3) = word;
+                    word = 0;
+                }
+            } else {
+                column_t[row] = code;
+            }
+        }
+    };
+    i64 row = r0;
+    if (col < o) {
+        const i64 live = r1 < k ? r1 : k;
+        while (row < live) {
+            const i64 g_end = (row + gr) < live ? (row + gr) : live;
+            float peak = 0.0f;
+            for (i64 rr = row; rr < g_end; ++rr) {
+                const float a = fabsf(b[rr * ld + col]);
+                finite = finite && a <= FLT_MAX;
+                peak = fmaxf(peak, a);
+            }
+            const float s = group_scale(peak, upper);
+            scale[(row / gr) * o + col] = s;
+            for (; row < g_end; ++row) put(row, quantize_code(b[row * ld + col], s, lower, upper, mask));
+        }
+    }
+    for (; row < r1; ++row) put(row, 0);
+    if (!finite && status) atomicOr(status, flag);
+}
+template __global__ void k_col_groups<true>(const float *, i64, i64, i64, i64, i64, int, int, i64,
+                                            i64, float, float, u32, u8 *, u8 *, float *, u32 *,
+                                            u32);
+template __global__ void k_col_groups<false>(const float *, i64, i64, i64, i64, i64, int, int, i64,
+                                             i64, float, float, u32, u8 *, u8 *, float *, u32 *,
+                                             u32);
 
 // q [n, kp] with kp = m*R; columns >= k are zero padding.
 __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,

@@ -24,8 +24,8 @@ from .simulator import Simulator
 _FLOATING = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
-def _operands(a, b):
-    """Type, device and finiteness checks of functional.py:32-53."""
+def _operands(a, b, *, finite=True):
+    """Type, device and (unless deferred) finiteness checks of functional.py:32-53."""
     for name, value in (("A", a), ("B", b)):
         if not isinstance(value, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor")
@@ -39,9 +39,19 @@ def _operands(a, b):
         raise ValueError("A and B must use the same device")
     if a.device.type not in ("cpu", "cuda"):
         raise ValueError("matrix simulation requires CPU or CUDA operands")
+    if finite:
+        _finite(a, b)
+
+
+def _finite(a, b):
     for name, value in (("A", a), ("B", b)):
         if not torch.isfinite(value).all():
             raise ValueError(f"{name} must be finite")
+
+
+# Operand dtypes whose FP32 quantization preserves finiteness, so the fused
+# product's device-side check raises exactly where the host check would.
+_FUSED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
 def _engine(a, simulator, config, mode, cache_dir):
@@ -111,9 +121,13 @@ def _rhs_view(simulator, owner, rhs, index):
     return record[2][index]
 
 
-def _product(a, b, simulator, cached_rhs=None):
-    matrix = _map_rhs(simulator, b if cached_rhs is None else cached_rhs)
-    analog = matrix(a.detach())
+def _product(a, b, simulator, cached_rhs=None, fused=False):
+    rhs = b if cached_rhs is None else cached_rhs
+    if fused:
+        analog = simulator._product(a.detach(), rhs)
+    else:
+        matrix = _map_rhs(simulator, rhs)
+        analog = matrix(a.detach())
     if not torch.is_grad_enabled() or not (a.requires_grad or b.requires_grad):
         return analog
     surrogate = _quantized_linear(a, b.transpose(0, 1), None, simulator.config)
@@ -121,32 +135,46 @@ def _product(a, b, simulator, cached_rhs=None):
 
 
 def _matmul(a, b, *, simulator, config, mode, cache_dir, out):
-    _operands(a, b)
-    left_vector, right_vector = a.ndim == 1, b.ndim == 1
-    left = a.unsqueeze(0) if left_vector else a
-    right = b.unsqueeze(-1) if right_vector else b
-    if left.shape[-1] != right.shape[-2]:
-        raise ValueError("A and B have incompatible reduction dimensions")
+    # Finiteness is checked on the device inside the fused product when it
+    # applies; every other route (and every error raised before the product)
+    # checks it on the host first, keeping the reference's error order.
+    _operands(a, b, finite=False)
     try:
-        batch = torch.broadcast_shapes(left.shape[:-2], right.shape[:-2])
-    except RuntimeError:
-        raise ValueError("A and B batch dimensions cannot broadcast") from None
-    rows, reduction, columns = left.shape[-2], left.shape[-1], right.shape[-1]
-    shape = batch + (() if left_vector else (rows,)) + (() if right_vector else (columns,))
-    _out(a, b, out, shape)
-    engine = _engine(a, simulator, config, mode, cache_dir)
+        left_vector, right_vector = a.ndim == 1, b.ndim == 1
+        left = a.unsqueeze(0) if left_vector else a
+        right = b.unsqueeze(-1) if right_vector else b
+        if left.shape[-1] != right.shape[-2]:
+            raise ValueError("A and B have incompatible reduction dimensions")
+        try:
+            batch = torch.broadcast_shapes(left.shape[:-2], right.shape[:-2])
+        except RuntimeError:
+            raise ValueError("A and B batch dimensions cannot broadcast") from None
+        rows, reduction, columns = left.shape[-2], left.shape[-1], right.shape[-1]
+        shape = batch + (() if left_vector else (rows,)) + (() if right_vector else (columns,))
+        _out(a, b, out, shape)
+        engine = _engine(a, simulator, config, mode, cache_dir)
+    except Exception:
+        _finite(a, b)
+        raise
+    shared_rhs = all(size == 1 for size in right.shape[:-2])
+    empty = a.numel() == 0 or b.numel() == 0 or 0 in shape
+    fused = (
+        isinstance(engine, Simulator) and a.dtype in _FUSED_DTYPES and shared_rhs and not empty
+    )
+    if not fused:
+        _finite(a, b)
     with torch.autocast(device_type=a.device.type, enabled=False):
-        if a.numel() == 0 or b.numel() == 0 or 0 in shape:
+        if empty:
             result = a.new_zeros(shape)
             if torch.is_grad_enabled() and (a.requires_grad or b.requires_grad):
                 result = _SurrogateGradient.apply(result, torch.matmul(a.float(), b.float()))
         else:
             left = left.expand(batch + (rows, reduction))
             rhs_batch = right.shape[:-2]
-            if all(size == 1 for size in rhs_batch):
+            if shared_rhs:
                 rhs = right if right.ndim == 2 else right.reshape(reduction, columns)
                 cached = None if b.ndim == 2 else _rhs_view(engine, b, rhs, ())
-                result = _product(left, rhs, engine, cached)
+                result = _product(left, rhs, engine, cached, fused)
             else:
                 groups = {}
                 padding = len(batch) - len(rhs_batch)

@@ -26,10 +26,6 @@ ABI_VERSION = 1
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
-# Optional launch timer: when set to a list, ``mm`` appends a (start, end)
-# pair of torch.cuda.Events recorded on the launch stream around the fused
-# read kernel (used by bench.py to time the dominant kernel).
-kernel_timer = None
 READ_MODES = {"shared": 0, "slice_pair": 1, "output": 2}
 
 
@@ -129,16 +125,21 @@ SIGNATURES = {
     "mf_last_error": ([], ct.c_char_p),
     "mf_source_hash": ([], ct.c_char_p),
     "mf_device_identity": ([ct.c_int, ct.POINTER(MFIdentity)], ct.c_int),
-    "mf_group_scales": ([_P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P], ct.c_int),
-    "mf_input_tiles": ([_CFG, _P, _I64, _I64, _I64, _P, _I64, _I64, _I32, _P, _P, _P], ct.c_int),
-    "mf_weight_tiles": ([_CFG, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P], ct.c_int),
+    "mf_input_tiles": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _P, _P], ct.c_int),
+    "mf_quantize_inputs": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P],
+                           ct.c_int),
+    "mf_quantize_weights": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P,
+                             _P], ct.c_int),
     "mf_transpose_packed": ([_CFG, _P, _I64, _I64, _P, _P], ct.c_int),
     "mf_restore": ([_CFG, _P, _I64, _I64, _I64, _I64, ct.c_uint32, ct.c_uint64, _P, _P],
                    ct.c_int),
     "mf_partial": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
                     _P, _P, _P], ct.c_int),
     "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
-               _I64, _P, _I64, _I32, _P], ct.c_int),
+               _I64, _P, _I64, _I32, _P, _P], ct.c_int),
+    "mf_stable_sum": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P], ct.c_int),
+    "mf_profile_kernels": ([_I32], ct.c_int),
+    "mf_profile_collect": ([ct.POINTER(_I64), ct.POINTER(ct.c_double)], ct.c_int),
     "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, ct.POINTER(_I64)], ct.c_int),
     "mf_mm_kernel": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I32)], ct.c_int),
     "mf_resources_query": ([_CFG, _I32, ct.POINTER(MFResources)], ct.c_int),
@@ -287,94 +288,96 @@ def _group_dims(shape, granularity):
     return gr, gc
 
 
-def group_scales(value, bits, granularity, *, signed=True):
-    """Per-group INT scales of a 2-D FP32 device tensor (quantization.py:9-33)."""
-    require_device(value)
-    value = value.contiguous()
-    rows, cols = value.shape
-    gr, gc = _group_dims(value.shape, granularity)
-    nr, nc = math.ceil(rows / gr), math.ceil(cols / gc)
-    work = torch.empty((nr, nc), dtype=torch.int32, device=value.device)
-    scale = torch.empty((nr, nc), dtype=torch.float32, device=value.device)
-    with torch.cuda.device(value.device):
-        check(
-            library().mf_group_scales(
-                _ptr(value), rows, cols, cols, gr, gc, bits, int(signed), _ptr(work),
-                _ptr(scale), _stream(value.device),
-            ),
-            "group scales",
-        )
-    return scale, gr, gc
+STATUS_INPUT, STATUS_WEIGHT, STATUS_OUTPUT = 1, 2, 4
 
 
-def input_tiles(value, config, fixed_scale=None):
-    """Codes q [N, m, R] (uint8) and per-read scales [N, m*Gr] (quantization.py:115-137)."""
+def status_word(device):
+    """Zeroed device status word (int32) that kernels OR their MF_STATUS_* bits into."""
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+def input_tiles(value, config, fixed_scale=None, *, status=None):
+    """Codes q [N, m, R] (uint8) and per-read scales [N, m*Gr] (quantization.py:115-137).
+
+    Without ``status`` a non-finite value raises here (quantization.py:25-26);
+    with a status word the check is deferred: STATUS_INPUT is set on the device.
+    """
     supported(config)
     require_device(value)
     n, k = value.shape
-    if not torch.isfinite(value).all():
+    if status is None and not torch.isfinite(value).all():
         raise ValueError("quantized values must be finite")
     x = value.to(torch.float32).contiguous()
     r = config.array_size[0]
     m = math.ceil(k / r)
     q = torch.empty((n, m, r), dtype=torch.uint8, device=value.device)
     xscale = torch.empty((n, m * config.reads_per_array), dtype=torch.float32, device=value.device)
-    if fixed_scale is None:
-        scale, gr, gc = group_scales(x, config.activation_bits, config.input_quant_gran)
-        fixed = 0
-    else:
+    descr = ct.byref(descriptor(config))
+    with torch.cuda.device(value.device):
+        if fixed_scale is None:
+            gr, gc = _group_dims(x.shape, config.input_quant_gran)
+            grid = (math.ceil(n / gr), math.ceil(k / gc))
+            scale = torch.empty(grid, dtype=torch.float32, device=value.device)
+            work = torch.empty(grid, dtype=torch.int32, device=value.device)
+            check(
+                library().mf_quantize_inputs(
+                    descr, _ptr(x), n, k, k, gr, gc, _ptr(work), _ptr(scale), _ptr(q),
+                    _ptr(xscale), _ptr(status), _stream(value.device),
+                ),
+                "input quantization",
+            )
+            return q, xscale
+        if status is not None:
+            bad = torch.isfinite(x).all().logical_not().to(torch.int32) * STATUS_INPUT
+            status.bitwise_or_(bad)
         scale = fixed_scale.to(device=value.device, dtype=torch.float32).reshape(-1).contiguous()
         if scale.numel() != k:
             raise ValueError("fixed input scale must have one entry per input feature")
-        gr, gc, fixed = 1, 1, 1
-    with torch.cuda.device(value.device):
         check(
             library().mf_input_tiles(
-                ct.byref(descriptor(config)), _ptr(x), n, k, k, _ptr(scale), gr, gc, fixed,
-                _ptr(q), _ptr(xscale), _stream(value.device),
+                descr, _ptr(x), n, k, k, _ptr(scale), _ptr(q), _ptr(xscale), _stream(value.device),
             ),
             "input tiles",
         )
     return q, xscale
 
 
-def weight_tiles(weight, config, *, transposed=True):
+def weight_tiles(weight, config, *, transposed=True, status=None):
     """PyTorch [O,K] weights -> packed [m,p,R,C], packed_t [p*C, m*R], scales [m*Gr,p,C].
 
     Follows quantization.py:82-112 (weights are quantized in physical [K,O]
     coordinates).  ``packed_t`` is the column-major copy read by the MFMA kernel.
+    Without ``status`` a non-finite weight raises here; with a status word the
+    check is deferred (STATUS_WEIGHT on the device).
     """
     supported(config)
     require_device(weight)
     o, k = weight.shape
     b = weight.detach().T.to(torch.float32).contiguous()  # [K, O]
-    if not torch.isfinite(b).all():
+    if status is None and not torch.isfinite(b).all():
         raise ValueError("quantized values must be finite in torch.float32")
     if not config.weight_signed and (b < 0).any():
         raise ValueError(
             "unsigned floating weights must be nonnegative INT values; "
             "use map_quantized with zero_points for affine weights"
         )
-    scale, gr, gc = group_scales(b, config.weight_bits, config.weight_quant_gran,
-                                 signed=config.weight_signed)
-    return pack_codes(None, scale, config, k, o, gr, gc, source=b, transposed=transposed)
-
-
-def pack_codes(codes, scale, config, k, o, gr, gc, *, source=None, transposed=True):
-    """Quantize ``source`` [K,O] with group grid ``scale`` into packed tiles."""
     r, c = config.array_size
     m, p = math.ceil(k / r), math.ceil(o / c)
-    device = source.device
+    device = b.device
+    gr, gc = _group_dims(b.shape, config.weight_quant_gran)
+    grid = (math.ceil(k / gr), math.ceil(o / gc))
+    scale = torch.empty(grid, dtype=torch.float32, device=device)
+    work = torch.empty(grid, dtype=torch.int32, device=device)
     packed = torch.empty((m, p, r, c), dtype=torch.uint8, device=device)
     packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=device) if transposed else None
     wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float32, device=device)
     with torch.cuda.device(device):
         check(
-            library().mf_weight_tiles(
-                ct.byref(descriptor(config)), _ptr(source), k, o, o, _ptr(scale), gr, gc,
-                _ptr(packed), _ptr(packed_t), _ptr(wscale), _stream(device),
+            library().mf_quantize_weights(
+                ct.byref(descriptor(config)), _ptr(b), k, o, o, gr, gc, _ptr(work), _ptr(scale),
+                _ptr(packed), _ptr(packed_t), _ptr(wscale), _ptr(status), _stream(device),
             ),
-            "weight tiles",
+            "weight quantization",
         )
     return packed, packed_t, wscale
 
@@ -471,7 +474,7 @@ def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance
 
 
 def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=None, out=None,
-       variant=0):
+       variant=0, status=None):
     """Fused read + scale restore: [N, p*C] FP32, summed over reads in torch's order."""
     supported(config)
     require_device(q)
@@ -491,25 +494,56 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
         check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
               "workspace size")
         workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
-    timer = kernel_timer
     with torch.cuda.device(q.device):
-        if timer is not None:
-            start = torch.cuda.Event(enable_timing=True)
-            start.record()
         check(
             library().mf_mm(
                 ct.byref(descriptor(config)), _ptr(q.contiguous()), _ptr(xscale.contiguous()), n,
                 m, _ptr(packed.contiguous()), _ptr(packed_t), _ptr(wscale.contiguous()), p,
                 _ptr(g), seed, event, _ptr(out), out.stride(0), _ptr(workspace),
-                0 if workspace is None else workspace.numel(), variant, _stream(q.device),
+                0 if workspace is None else workspace.numel(), variant, _ptr(status),
+                _stream(q.device),
             ),
             "mm",
         )
-        if timer is not None:
-            end = torch.cuda.Event(enable_timing=True)
-            end.record()
-            timer.append((start, end))
     return out
+
+
+def stable_sum(totals, xscale, wscale, config, col0, out):
+    """FP64 overflow-safe restore + read sum of one chunk into ``out`` [N, ldo] (FP64).
+
+    totals [N, G, width, C] from ``partial``; xscale [N, G]; wscale [G, p*C].
+    Same values and order as restore_scales(...).sum(1) on the CPU
+    (memfast/simulator.py:57-66, :578-585).
+    """
+    require_device(totals)
+    n, groups, width, c = totals.shape
+    if out.dtype != torch.float64 or out.stride(1) != 1:
+        raise ValueError("stable sums go to a row-major FP64 output")
+    totals = totals.to(torch.float32).contiguous()
+    xscale = xscale.to(torch.float32).contiguous()
+    wscale = wscale.to(torch.float32).contiguous()
+    with torch.cuda.device(totals.device):
+        check(
+            library().mf_stable_sum(
+                ct.byref(descriptor(config)), _ptr(totals), n, groups, width, _ptr(xscale),
+                _ptr(wscale), wscale.shape[1], col0, _ptr(out), out.stride(0),
+                _stream(totals.device),
+            ),
+            "stable sum",
+        )
+    return out
+
+
+def profile_kernels(enable):
+    """Start (True) or stop recording HIP events around mf_mm's read kernel."""
+    check(library().mf_profile_kernels(int(bool(enable))), "profile")
+
+
+def collect_kernel_times():
+    """(launches, total milliseconds) of the read kernels recorded since the last call."""
+    launches, ms = ct.c_int64(), ct.c_double()
+    check(library().mf_profile_collect(ct.byref(launches), ct.byref(ms)), "profile collect")
+    return launches.value, ms.value
 
 
 def mm_kernel(config, n, m, p, has_packed_t=True):

@@ -73,6 +73,14 @@ IDEAL_CASES = [
                           weight_slice=(1, 3, 4)), 5, 70, 30),
     ("unsigned", ideal(weight_bits=4, weight_signed=False, weight_slice=(2, 2),
                        array_size=(32, 16), adc_bits=5), 4, 40, 20),
+    # Quantization routes: 2-D groups (atomic group maxima) on both operands ...
+    ("grouped_2d", ideal(array_size=(64, 32), rows_per_read=16, adc_bits=8,
+                         input_quant_gran=(2, 16), weight_quant_gran=(32, 4)), 7, 150, 40),
+    # ... scalar loads and byte stores (odd group width, 66-row tiles) ...
+    ("odd_rows", ideal(array_size=(66, 32), adc_bits=8, input_quant_gran=(1, 66),
+                       weight_quant_gran=(66, 1)), 5, 150, 36),
+    # ... and groups too long for one thread (whole rows and whole columns).
+    ("whole_rows", ideal(adc_bits=8), 3, 1500, 20),
 ]
 
 
@@ -325,3 +333,85 @@ def test_config2_full_size_rows(hip_device):
     say("oracle on rows", rows.tolist())
     expected = oracle.mm(a[rows], b, cfg)
     assert bits_equal(out[rows.to(hip_device)], expected)
+
+
+def test_functional_nonfinite_operands_leave_simulator_unchanged(hip_device):
+    """The fused product checks finiteness on the device (functional.py:49-53 order)."""
+    from memfast_amd import Simulator, mm
+
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(5)
+    a = torch.randn(6, 256, generator=gen)
+    b = torch.randn(256, 40, generator=gen)
+    sim = Simulator(cfg, device=hip_device)
+    bad_a, bad_b = a.clone(), b.clone()
+    bad_a[3, 100] = float("nan")
+    bad_b[7, 2] = float("inf")
+    cases = [(bad_a, b, "A must be finite"), (a, bad_b, "B must be finite"),
+             (bad_a, bad_b, "A must be finite")]
+    for left, right, message in cases:
+        with pytest.raises(ValueError, match=message):
+            sim.mm(left.to(hip_device), right.to(hip_device))
+        with pytest.raises(ValueError, match=message):
+            mm(left.to(hip_device).bfloat16(), right.to(hip_device).bfloat16(), config=cfg)
+    assert sim._next_id == 0 and not sim._matrix_cache
+    assert bits_equal(sim.mm(a.to(hip_device), b.to(hip_device)), oracle.mm(a, b, cfg))
+
+
+def test_functional_reprogramming_follows_in_place_edits(hip_device):
+    """Reused RHS programs take new codes in place and keep name and event counter."""
+    from memfast_amd import Simulator
+
+    cfg = Config(**SMALL, nonidealities=Nonidealities(write_variation=0.0, read_variation=0.01))
+    gen = torch.Generator().manual_seed(6)
+    a = torch.randn(5, 256, generator=gen)
+    b = torch.randn(256, 40, generator=gen)
+    sim = Simulator(cfg, device=hip_device)
+    a_dev, b_dev = a.to(hip_device), b.to(hip_device)
+    outputs = [sim.mm(a_dev, b_dev)]
+    program = sim._matrix_cache[id(b_dev)][2]
+    b_dev.mul_(-0.5)
+    outputs.append(sim.mm(a_dev, b_dev))
+    assert sim._matrix_cache[id(b_dev)][2] is program and program._event == 2
+    assert program.name == "matrix.0" and sim._next_id == 1
+    for event, (weights, got) in enumerate(zip((b, b * -0.5), outputs)):
+        expected = oracle.mm(a, weights, cfg, event=event)
+        rel = (got.cpu() - expected).abs() / expected.abs().clamp_min(1e-6)
+        say("  event", event, "elements beyond 1e-5:", (rel > 1e-5).float().mean().item())
+        assert (rel > 1e-5).float().mean().item() <= 0.02
+
+
+def test_fp32_overflow_retries_in_fp64(hip_device):
+    """Non-finite FP32 restores repeat in FP64 (simulator.py:614-615); FP64 operands keep it."""
+    from memfast_amd import Simulator
+
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(7)
+    a = torch.randn(4, 256, generator=gen, dtype=torch.float64) * 1e30
+    b = torch.randn(256, 36, generator=gen, dtype=torch.float64) * 1e30
+    sim = Simulator(cfg, device=hip_device)
+    got = sim.mm(a.to(hip_device), b.to(hip_device))
+    expected = oracle.mm(a, b, cfg)
+    assert got.dtype == torch.float64 and torch.isfinite(got).all()
+    assert bits_equal(got, expected)
+    with pytest.raises(FloatingPointError):
+        sim.mm(a.float().to(hip_device), b.float().to(hip_device))
+
+
+@pytest.mark.parametrize("groups,width,c", [(5, 1, 4), (17, 2, 12), (128, 2, 128), (300, 1, 36),
+                                            (40, 2, 4)])
+def test_stable_sum_matches_cpu_restore(hip_device, groups, width, c):
+    """FP64 restore + read sum equals oracle.restore_scales(...).sum(1) on the CPU, bit for bit."""
+    cfg = ideal(**CONFIG2 | dict(array_size=(128, c)))
+    gen = torch.Generator().manual_seed(groups * 7 + c)
+    n = 3
+    totals = torch.randint(-5000, 5000, (n, groups, width, c), generator=gen).float()
+    xs = torch.exp(15 * torch.randn(n, groups, generator=gen)).float()
+    ws = torch.exp(15 * torch.randn(groups, width * c, generator=gen)).float()
+    expected = oracle.restore_scales(totals, xs[:, :, None, None],
+                                     ws.reshape(groups, width, c)[None]).sum(1).flatten(1)
+    # The chunk sits at columns [8, 8 + width*C) of the output and of the scale rows.
+    out = torch.zeros((n, width * c + 8), dtype=torch.float64, device=hip_device)
+    ws_rows = torch.cat([torch.ones(groups, 8), ws], dim=1)
+    hip.stable_sum(totals.to(hip_device), xs.to(hip_device), ws_rows.to(hip_device), cfg, 8, out)
+    assert bits_equal(out[:, 8:], expected)
