@@ -97,10 +97,16 @@ def main():
     value = macs / (ms_step * 1e-3) / 1e9
     achieved = 2 * slice_macs / (kernel_ms * 1e-3) / 1e12
 
-    noisy_cfg = memfast.Config(**BASE, nonidealities=memfast.Nonidealities(
-        write_variation=0.02, read_variation=0.01, adc_nonlinearity=0.1))
-    noisy_sim = memfast.Simulator(noisy_cfg, device=device)
-    noisy_ms, noisy_kernel_ms = time_steps(lambda: noisy_sim.mm(a, b), args.noisy_steps, 1)
+    noisy = None
+    if args.noisy_steps > 0:
+        noisy_cfg = memfast.Config(**BASE, nonidealities=memfast.Nonidealities(
+            write_variation=0.02, read_variation=0.01, adc_nonlinearity=0.1))
+        noisy_sim = memfast.Simulator(noisy_cfg, device=device)
+        noisy_ms, noisy_kernel_ms = time_steps(lambda: noisy_sim.mm(a, b), args.noisy_steps, 1)
+        noisy = dict(ms_per_step=round(noisy_ms, 3), kernel_ms=round(noisy_kernel_ms, 3),
+                     value=round(macs / (noisy_ms * 1e-3) / 1e9, 3), unit="GMAC/s",
+                     config="write_variation=0.02, read_variation=0.01 shared, "
+                            "adc_nonlinearity=0.1")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -145,9 +151,7 @@ def main():
         roofline=dict(bound="mfma", achieved=round(achieved, 2), peak=INT8_PEAK_TOPS,
                       unit="TFLOP/s", frac=round(achieved / INT8_PEAK_TOPS, 4), traffic=None,
                       note="int8 tera-ops (2 per slice-MAC, 25 pairs) / fused kernel time"),
-        noisy=dict(ms_per_step=round(noisy_ms, 3), kernel_ms=round(noisy_kernel_ms, 3),
-                   value=round(macs / (noisy_ms * 1e-3) / 1e9, 3), unit="GMAC/s",
-                   config="write_variation=0.02, read_variation=0.01 shared, adc_nonlinearity=0.1"),
+        noisy=noisy,
         cpu_baseline=cpu,
         kernels=hip.native_source_hash()[:16],
     )

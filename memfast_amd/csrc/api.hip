@@ -357,10 +357,32 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
     const float upper = float((1 << (bits - 1)) - 1);
     const u32 mask = (1u << bits) - 1u;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (gr == 1 && gc <= 1024) {
-        const bool vec = gc % 4 == 0 && k % 4 == 0 && kp % 4 == 0 && ld % 4 == 0 &&
-                         reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-                         reinterpret_cast<uintptr_t>(q) % 4 == 0;
+    const bool vec = gc % 4 == 0 && k % 4 == 0 && kp % 4 == 0 && ld % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(q) % 4 == 0;
+    const i64 quads = gc / 4;
+    const bool pow2 = quads > 0 && (quads & (quads - 1)) == 0;
+    if (gr == 1 && vec && pow2 && quads <= 64) {
+        const int L = int(quads);
+        hipLaunchKernelGGL(k_row_groups_lanes, dim3(unsigned((n * ncg * L + 255) / 256)), dim3(256),
+                           0, s, x, n, k, ld, L, ncg, kp, -upper, upper, mask, q, scale, status,
+                           u32(MF_STATUS_INPUT));
+    } else if (gr == 1 && vec && pow2 && quads <= 1024) {
+        const dim3 grid{unsigned((n * ncg * 64 + 255) / 256)};
+        const int V = int(quads / 64);
+        if (V == 2)
+            hipLaunchKernelGGL(k_row_groups_wave<2>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+        else if (V == 4)
+            hipLaunchKernelGGL(k_row_groups_wave<4>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+        else if (V == 8)
+            hipLaunchKernelGGL(k_row_groups_wave<8>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+        else
+            hipLaunchKernelGGL(k_row_groups_wave<16>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+    } else if (gr == 1 && gc <= 1024) {
         if (vec)
             hipLaunchKernelGGL(k_row_groups<true>, dim3(grid_for(n * ncg)), dim3(256), 0, s, x, n, k,
                                ld, gc, ncg, kp, -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
@@ -402,7 +424,27 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
     hipStream_t s = static_cast<hipStream_t>(stream);
     const i64 unit = lcm4(gr);
     const i64 span = unit >= 128 ? unit : unit * (128 / unit);
-    if (gc == 1 && gr <= 256 && (kp + span - 1) / span <= 65535) {
+    const bool reg_group = gr == 8 || gr == 16 || gr == 32 || gr == 64;
+    if (gc == 1 && reg_group && (kp + gr - 1) / gr <= 65535) {
+        const dim3 grid{unsigned((op + 255) / 256), unsigned((kp + gr - 1) / gr), 1u};
+        const bool word = kp % 4 == 0;
+#define MF_COL_REG_LAUNCH(GR)                                                                    \
+    if (gr == GR) {                                                                              \
+        if (word)                                                                                \
+            hipLaunchKernelGGL((k_col_groups_reg<GR, true>), grid, dim3(256), 0, s, b, k, o, ld, R, \
+                               C, m, p, lower, upper, mask, packed, packed_t, scale, status,      \
+                               u32(MF_STATUS_WEIGHT));                                           \
+        else                                                                                     \
+            hipLaunchKernelGGL((k_col_groups_reg<GR, false>), grid, dim3(256), 0, s, b, k, o, ld, \
+                               R, C, m, p, lower, upper, mask, packed, packed_t, scale, status,   \
+                               u32(MF_STATUS_WEIGHT));                                           \
+    }
+        MF_COL_REG_LAUNCH(8)
+        MF_COL_REG_LAUNCH(16)
+        MF_COL_REG_LAUNCH(32)
+        MF_COL_REG_LAUNCH(64)
+#undef MF_COL_REG_LAUNCH
+    } else if (gc == 1 && gr <= 256 && (kp + span - 1) / span <= 65535) {
         const dim3 grid{unsigned((op + 255) / 256), unsigned((kp + span - 1) / span), 1u};
         if (kp % 4 == 0)
             hipLaunchKernelGGL(k_col_groups<true>, grid, dim3(256), 0, s, b, k, o, ld, gr, span, R, C,
@@ -494,7 +536,7 @@ static bool ideal_extent_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     const i64 limit = 0x7FFFFFFF;
     return 128 * kp <= limit && G * ncols * 4 <= limit && 128 * G * 4 <= limit &&
-           (n + 63) / 64 <= 65535;
+           (n + 63) / 64 <= 65535 && (ncols + 31) / 32 <= 65535;
 }
 
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
@@ -550,11 +592,11 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         const i64 kp = m * cfg->rows, ncols = p * cfg->cols;
         const SliceLayout xl = layout_of(cfg->in_shift, cfg->in_mask, cfg->n_in);
         const SliceLayout wl = layout_of(cfg->w_shift, cfg->w_mask, cfg->n_w);
-        hipLaunchKernelGGL(k_digit_bits, dim3(grid_for(G * ((n + 63) / 64 * 64))), dim3(256), 0, s,
-                           q, n, kp, G, cfg->reads, cfg->rows, cfg->read_rows, xl, 64, xtests, xbits);
-        hipLaunchKernelGGL(k_digit_bits, dim3(grid_for(G * ((ncols + 63) / 64 * 64))), dim3(256), 0,
-                           s, packed_t, ncols, kp, G, cfg->reads, cfg->rows, cfg->read_rows, wl, 32,
-                           wtests, wbits);
+        const unsigned gblocks = unsigned((G + 63) / 64);
+        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((n + 63) / 64)), dim3(256), 0, s,
+                           q, n, kp, G, cfg->read_rows, xl, 64, xtests, xbits);
+        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((ncols + 31) / 32)), dim3(256), 0,
+                           s, packed_t, ncols, kp, G, cfg->read_rows, wl, 32, wtests, wbits);
         IdealArgs args{};
         args.q = q;
         args.wt = packed_t;

@@ -56,47 +56,73 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 
 // Per-read digit sums, maximized over blocks of `block` (32 or 64) rows, then
 // tested against the slot thresholds: out[rb][g] = mask of proven slots.
-__global__ __launch_bounds__(256) void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G,
-                                                    int Gr, int R, int P,
+// Workgroup = 64 reads (one per lane, so a wave loads 64 consecutive P-byte
+// runs of a row) x 4 waves that split the block's rows; LDS combines the
+// four partial maxima.  Digit sums use SWAR: (word >> shift) & mask per byte,
+// then v_sad_u8 adds the four bytes.  Requires P in {32, 64} and reads that
+// start at g * P (R a multiple of P).
+__global__ __launch_bounds__(256) void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int P,
                                                     const SliceLayout layout, int block,
                                                     const SlotTests tests, uint64_t *out) {
-    const i64 rows_pad = ((rows + 63) / 64) * 64;
-    const i64 total = G * rows_pad;
+    __shared__ int partial[3][8][64];
+    const int lane = threadIdx.x & 63, quarter = threadIdx.x >> 6;
+    const i64 g = i64(blockIdx.x) * 64 + lane;
+    const i64 rb = blockIdx.y;
     const int S = layout.count;
-    for (i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
-         t += i64(gridDim.x) * blockDim.x) {
-        const i64 g = t / rows_pad, row = t % rows_pad;
-        const i64 kofs = (g / Gr) * R + (g % Gr) * P;
-        int sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (row < rows) {
-            const u8 *src = codes + row * kp + kofs;
-            for (int b = 0; b < P; ++b) {
-                const int code = src[b];
+    const int per = block / 4;
+    int best[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    u32 masks[8];
 #pragma unroll
-                for (int s = 0; s < 8; ++s)
-                    if (s < S) sums[s] += (code >> layout.shift[s]) & layout.mask[s];
+    for (int sl = 0; sl < 8; ++sl) masks[sl] = sl < S ? u32(layout.mask[sl]) * 0x01010101u : 0u;
+    if (g < G) {
+        for (int i = 0; i < per; ++i) {
+            const i64 row = rb * block + quarter * per + i;
+            if (row >= rows) break;
+            const uint4 *src = reinterpret_cast<const uint4 *>(codes + row * kp + g * P);
+            uint4 chunk[4];
+            chunk[0] = src[0];
+            chunk[1] = src[1];
+            if (P == 64) {
+                chunk[2] = src[2];
+                chunk[3] = src[3];
             }
-        }
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            if (s >= S) break;
-            int v = sums[s];
-            for (int off = 1; off < block; off <<= 1) v = max(v, __shfl_xor(v, off, 64));
-            sums[s] = v;
-        }
-        if ((row % block) == 0 && row < rows) {
-            uint64_t bits = 0;
-            for (int slot = 0; slot < 64; ++slot) {
-                if (!((tests.exists >> slot) & 1)) continue;
-                int v = 0;
+            for (int sl = 0; sl < 8; ++sl) {
+                if (sl >= S) break;
+                const int sh = layout.shift[sl];
+                const u32 mk = masks[sl];
+                u32 sum = 0;
 #pragma unroll
-                for (int s = 0; s < 8; ++s)
-                    if (s == tests.slice[slot]) v = sums[s];
-                if (v <= tests.thr[slot]) bits |= uint64_t(1) << slot;
+                for (int c = 0; c < 4; ++c) {
+                    if (c >= 2 && P != 64) break;
+                    sum = __builtin_amdgcn_sad_u8((chunk[c].x >> sh) & mk, 0u, sum);
+                    sum = __builtin_amdgcn_sad_u8((chunk[c].y >> sh) & mk, 0u, sum);
+                    sum = __builtin_amdgcn_sad_u8((chunk[c].z >> sh) & mk, 0u, sum);
+                    sum = __builtin_amdgcn_sad_u8((chunk[c].w >> sh) & mk, 0u, sum);
+                }
+                best[sl] = max(best[sl], int(sum));
             }
-            out[(row / block) * G + g] = bits;
         }
     }
+    if (quarter > 0) {
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) partial[quarter - 1][sl][lane] = best[sl];
+    }
+    __syncthreads();
+    if (quarter > 0 || g >= G || rb * block >= rows) return;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl)
+        best[sl] = max(max(best[sl], partial[0][sl][lane]), max(partial[1][sl][lane], partial[2][sl][lane]));
+    uint64_t bits = 0;
+    for (int slot = 0; slot < 64; ++slot) {
+        if (!((tests.exists >> slot) & 1)) continue;
+        int v = 0;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl)
+            if (sl == tests.slice[slot]) v = best[sl];
+        if (v <= tests.thr[slot]) bits |= uint64_t(1) << slot;
+    }
+    out[rb * G + g] = bits;
 }
 
 // Buffer resource over [base, base + bytes): loads past the end return zero.

@@ -88,7 +88,7 @@ struct SliceLayout {
 
 // Per-read digit sums of every slice, maximized over blocks of `block` rows,
 // turned into the slot mask of `tests`: out[rb][g].
-__global__ void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int Gr, int R, int P,
+__global__ void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int P,
                              const SliceLayout layout, int block, const SlotTests tests,
                              uint64_t *out);
 
@@ -110,6 +110,17 @@ template <bool VEC>
 __global__ void k_row_groups(const float *x, i64 n, i64 k, i64 ld, i64 gc, i64 ncg, i64 kp,
                              float lower, float upper, u32 mask, u8 *q, float *scale,
                              u32 *status, u32 flag);
+__global__ void k_row_groups_lanes(const float *x, i64 n, i64 k, i64 ld, int L, i64 ncg, i64 kp,
+                                   float lower, float upper, u32 mask, u8 *q, float *scale,
+                                   u32 *status, u32 flag);
+template <int V>
+__global__ void k_row_groups_wave(const float *x, i64 n, i64 k, i64 ld, i64 ncg, i64 kp,
+                                  float lower, float upper, u32 mask, u8 *q, float *scale,
+                                  u32 *status, u32 flag);
+template <int GR, bool WORD>
+__global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+                                 i64 p, float lower, float upper, u32 mask, u8 *packed,
+                                 u8 *packed_t, float *scale, u32 *status, u32 flag);
 template <bool WORD>
 __global__ void k_col_groups(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 span, int R,
                              int C, i64 m, i64 p, float lower, float upper, u32 mask,

@@ -139,6 +139,161 @@ template __global__ void k_row_groups<true>(const float *, i64, i64, i64, i64, i
 template __global__ void k_row_groups<false>(const float *, i64, i64, i64, i64, i64, i64, float,
                                              float, u32, u8 *, float *, u32 *, u32);
 
+// Cooperative row groups of gc = 4*L floats (L a power of two <= 64): L lanes
+// share a group, each holding one float4, so a wave reads 1 KiB contiguous per
+// load and writes 256 contiguous code bytes.  The group peak is a shuffle
+// reduction over the L lanes.  Requires the VEC conditions of k_row_groups.
+__global__ void k_row_groups_lanes(const float *x, i64 n, i64 k, i64 ld, int L, i64 ncg, i64 kp,
+                                   float lower, float upper, u32 mask, u8 *q, float *scale,
+                                   u32 *status, u32 flag) {
+    const i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x;
+    const i64 total = n * ncg * L;
+    if (t >= total) return;   // whole groups: L divides 64 and total
+    const i64 grp = t / L;
+    const int member = int(t - grp * L);
+    const i64 row = grp / ncg, j = grp - row * ncg;
+    const i64 col = j * 4 * L + member * 4;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (col < k) v = *reinterpret_cast<const float4 *>(x + row * ld + col);
+    const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
+    const bool finite = a0 <= FLT_MAX && a1 <= FLT_MAX && a2 <= FLT_MAX && a3 <= FLT_MAX;
+    float peak = fmaxf(fmaxf(a0, a1), fmaxf(a2, a3));
+    for (int off = 1; off < L; off <<= 1) peak = fmaxf(peak, __shfl_xor(peak, off, 64));
+    const float s = group_scale(peak, upper);
+    if (member == 0) scale[grp] = s;
+    u8 *dst = q + row * kp;
+    if (col < k) {
+        const u32 word = u32(quantize_code(v.x, s, lower, upper, mask)) |
+                         u32(quantize_code(v.y, s, lower, upper, mask)) << 8 |
+                         u32(quantize_code(v.z, s, lower, upper, mask)) << 16 |
+                         u32(quantize_code(v.w, s, lower, upper, mask)) << 24;
+        *reinterpret_cast<u32 *>(dst + col) = word;
+    }
+    if (j == ncg - 1)
+        for (i64 c = k + member * 4; c < kp; c += 4 * L) *reinterpret_cast<u32 *>(dst + c) = 0u;
+    if (!finite && status) atomicOr(status, flag);
+}
+
+// Wave-wide row groups of gc = 256*V floats: one wave per group, V float4 per
+// lane kept in registers (one pass), peak reduced across the wave.
+template <int V>
+__global__ void k_row_groups_wave(const float *x, i64 n, i64 k, i64 ld, i64 ncg, i64 kp,
+                                  float lower, float upper, u32 mask, u8 *q, float *scale,
+                                  u32 *status, u32 flag) {
+    const i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x;
+    const i64 grp = t >> 6;
+    const int lane = int(t & 63);
+    if (grp >= n * ncg) return;   // whole waves
+    const i64 row = grp / ncg, j = grp - row * ncg;
+    const i64 c0 = j * 256 * V;
+    const float *src = x + row * ld;
+    float4 v[V];
+    float peak = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const i64 col = c0 + (i * 64 + lane) * 4;
+        v[i] = col < k ? *reinterpret_cast<const float4 *>(src + col)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float a0 = fabsf(v[i].x), a1 = fabsf(v[i].y), a2 = fabsf(v[i].z), a3 = fabsf(v[i].w);
+        finite = finite && a0 <= FLT_MAX && a1 <= FLT_MAX && a2 <= FLT_MAX && a3 <= FLT_MAX;
+        peak = fmaxf(peak, fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+    }
+    for (int off = 1; off < 64; off <<= 1) peak = fmaxf(peak, __shfl_xor(peak, off, 64));
+    const float s = group_scale(peak, upper);
+    if (lane == 0) scale[grp] = s;
+    u8 *dst = q + row * kp;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const i64 col = c0 + (i * 64 + lane) * 4;
+        if (col < k) {
+            const u32 word = u32(quantize_code(v[i].x, s, lower, upper, mask)) |
+                             u32(quantize_code(v[i].y, s, lower, upper, mask)) << 8 |
+                             u32(quantize_code(v[i].z, s, lower, upper, mask)) << 16 |
+                             u32(quantize_code(v[i].w, s, lower, upper, mask)) << 24;
+            *reinterpret_cast<u32 *>(dst + col) = word;
+        }
+    }
+    if (j == ncg - 1)
+        for (i64 c = k + lane * 4; c < kp; c += 256) *reinterpret_cast<u32 *>(dst + c) = 0u;
+    if (!finite && status) atomicOr(status, flag);
+}
+template __global__ void k_row_groups_wave<2>(const float *, i64, i64, i64, i64, i64, float, float,
+                                              u32, u8 *, float *, u32 *, u32);
+template __global__ void k_row_groups_wave<4>(const float *, i64, i64, i64, i64, i64, float, float,
+                                              u32, u8 *, float *, u32 *, u32);
+template __global__ void k_row_groups_wave<8>(const float *, i64, i64, i64, i64, i64, float, float,
+                                              u32, u8 *, float *, u32 *, u32);
+template __global__ void k_row_groups_wave<16>(const float *, i64, i64, i64, i64, i64, float,
+                                               float, u32, u8 *, float *, u32 *, u32);
+
+// Column groups of GR rows held in registers: thread = (physical column, one
+// row group), so every lane issues its GR coalesced loads at once.  Writes the
+// scale grid, packed [m, p, R, C] (bytes, coalesced across lanes) and the
+// thread's GR contiguous bytes of packed_t (4-byte stores when WORD: kp % 4 == 0).
+template <int GR, bool WORD>
+__global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+                                 i64 p, float lower, float upper, u32 mask, u8 *packed,
+                                 u8 *packed_t, float *scale, u32 *status, u32 flag) {
+    const i64 kp = m * R, op = p * C;
+    const i64 col = i64(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (col >= op) return;
+    const i64 r0 = i64(blockIdx.y) * GR;
+    const bool live = col < o;
+    float v[GR];
+#pragma unroll
+    for (int i = 0; i < GR; ++i) {
+        const i64 row = r0 + i;
+        v[i] = (live && row < k) ? b[row * ld + col] : 0.0f;
+    }
+    float peak = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < GR; ++i) {
+        const float a = fabsf(v[i]);
+        finite = finite && a <= FLT_MAX;
+        peak = fmaxf(peak, a);
+    }
+    const float s = group_scale(peak, upper);
+    if (live && r0 < k) scale[i64(blockIdx.y) * o + col] = s;
+    const i64 t = col / C, c = col - t * C;
+    i64 tile = r0 / R, r = r0 - tile * R;
+    u8 *column_t = packed_t ? packed_t + col * kp : nullptr;
+    u32 word = 0;
+#pragma unroll
+    for (int i = 0; i < GR; ++i) {
+        const i64 row = r0 + i;
+        if (row >= kp) break;
+        const u8 code = (live && row < k) ? quantize_code(v[i], s, lower, upper, mask) : u8(0);
+        packed[((tile * p + t) * R + r) * C + c] = code;
+        if (++r == R) { r = 0; ++tile; }
+        if (column_t) {
+            if (WORD) {
+                word |= u32(code) << (8 * (i & 3));
+                if ((i & 3) == 3) {
+                    *reinterpret_cast<u32 *>(column_t + row - 3) = word;
+                    word = 0;
+                }
+            } else {
+                column_t[row] = code;
+            }
+        }
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+#define MF_COL_REG_INST(GR, WORD)                                                               \
+    template __global__ void k_col_groups_reg<GR, WORD>(const float *, i64, i64, i64, int, int, \
+                                                        i64, i64, float, float, u32, u8 *, u8 *,  \
+                                                        float *, u32 *, u32);
+MF_COL_REG_INST(8, true)
+MF_COL_REG_INST(8, false)
+MF_COL_REG_INST(16, true)
+MF_COL_REG_INST(16, false)
+MF_COL_REG_INST(32, true)
+MF_COL_REG_INST(32, false)
+MF_COL_REG_INST(64, true)
+MF_COL_REG_INST(64, false)
+
 // Fused grouped quantization of column-local groups (gc == 1, the weight
 // layout of quantization.py:82-112): thread = one physical column `col` of the
 // padded [kp, op] code matrix and one chunk of `span` rows (a multiple of gr,

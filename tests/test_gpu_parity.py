@@ -79,8 +79,13 @@ IDEAL_CASES = [
     # ... scalar loads and byte stores (odd group width, 66-row tiles) ...
     ("odd_rows", ideal(array_size=(66, 32), adc_bits=8, input_quant_gran=(1, 66),
                        weight_quant_gran=(66, 1)), 5, 150, 36),
-    # ... and groups too long for one thread (whole rows and whole columns).
+    # ... and groups too long for one thread (whole rows and whole columns),
     ("whole_rows", ideal(adc_bits=8), 3, 1500, 20),
+    # one wave per 1024-float row group,
+    ("row_wave", ideal(adc_bits=8), 3, 1024, 20),
+    # register column groups with byte stores (kp = 54 is not a multiple of 4).
+    ("col_bytes", ideal(array_size=(18, 32), rows_per_read=2, weight_quant_gran=(8, 1),
+                        adc_bits=6), 4, 45, 36),
 ]
 
 
