@@ -31,6 +31,14 @@ BASE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, tera-ops/s
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per launch of the read kernel on this workload, from two rocprofv3
+# --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the
+# same counters read for a 256 MiB device copy (FETCH x1.99974, WRITE x1.0):
+# 225.1 MiB read + 64.0 MiB written.  Summary and commands:
+# profiles/k_ideal_config2_pmc.md.  Only valid for the kernel sources it was
+# measured on (hash prefix below); otherwise the bench reports null.
+MEASURED_TRAFFIC = dict(kernels="ce3a6329d20ce4c8", bytes=303186787)
+
 
 def cpu_model():
     try:
@@ -69,6 +77,9 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--noisy-steps", type=int, default=2)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                        help="first run one device-to-device copy of MIB MiB (a known-size "
+                             "kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the sliced matmul path is built and measured on a "
@@ -87,6 +98,11 @@ def main():
     b_cpu = torch.randn(SIZE, SIZE)
     a = a_cpu.to(device)
     b = b_cpu.to(device)
+    if args.copy_calibration > 0:
+        source = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device=device)
+        torch.empty_like(source).copy_(source)
+        torch.cuda.synchronize()
+        del source
     ideal_cfg = memfast.Config(**BASE, nonidealities=memfast.Nonidealities(write_variation=0.0))
     sim = memfast.Simulator(ideal_cfg, device=device)
     ms_step, kernel_ms = time_steps(lambda: sim.mm(a, b), args.steps, args.warmup)
@@ -128,6 +144,8 @@ def main():
                     f"{threads} threads of {cpu_model()}"),
         )
 
+    kernels = hip.native_source_hash()[:16]
+    traffic = MEASURED_TRAFFIC["bytes"] if MEASURED_TRAFFIC["kernels"] == kernels else None
     line = dict(
         metric="effective GMAC/s, Simulator.mm 4096^3 INT8 (1,1,2,2,2)",
         value=round(value, 3),
@@ -149,11 +167,12 @@ def main():
         slice_mac_per_s=slice_macs / (ms_step * 1e-3),
         kernel_ms=round(kernel_ms, 4),
         roofline=dict(bound="mfma", achieved=round(achieved, 2), peak=INT8_PEAK_TOPS,
-                      unit="TFLOP/s", frac=round(achieved / INT8_PEAK_TOPS, 4), traffic=None,
-                      note="int8 tera-ops (2 per slice-MAC, 25 pairs) / fused kernel time"),
+                      unit="TFLOP/s", frac=round(achieved / INT8_PEAK_TOPS, 4), traffic=traffic,
+                      note="int8 tera-ops (2 per slice-MAC, 25 pairs) / read-kernel time "
+                           "(HIP events on its stream); traffic = HBM bytes per launch"),
         noisy=noisy,
         cpu_baseline=cpu,
-        kernels=hip.native_source_hash()[:16],
+        kernels=kernels,
     )
     print(json.dumps(line), flush=True)
 
