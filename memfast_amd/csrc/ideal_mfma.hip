@@ -12,8 +12,9 @@
 //     sums proves most of them clamp-free (S <= Mw*max_n sum_r da, or
 //     S <= Ma*max_c sum_r dw); those merge into one natural-form MFMA per input
 //     slice, again with no VALU work;
-//   * pairs still at risk get their own MFMA on positive operand forms, one
-//     v_min and one v_mad_i32_i24 per output.
+//   * pairs still at risk get their own natural-form MFMA; its product
+//     Y = fa*fw*S has the sign of fa*fw, so one v_min_i32 (positive pairs) or
+//     v_max_i32 (negative pairs) against fa*fw*max_w and one add per output.
 // T is restored as (float(T) * xs[n,g]) * ws[g,c] and summed over reads in
 // torch's CPU cascade order (level step 16; level 2 kept in `out`).
 //

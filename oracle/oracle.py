@@ -16,8 +16,8 @@ Pinning status (what checks each function beyond this restatement):
     float and static-INT4 checkpoints (codes, layout, padding), IEEE division
     identities, brute-force round-half-even.
   * input_tiles / read_starts: closed-form index tests, fixed-scale fixture.
-  * mix / uniform / event_seed / normal: the published lowbias32 inverse,
-    a C restatement, distribution tests, and vectors written by
+  * mix / uniform / event_seed / normal: a C restatement (oracle/brute.c),
+    distribution tests, and vectors written by
     tests/golden/make_reference_vectors.py.
   * partial / adc (ideal devices): C brute force of the closed form
     code = min(sum_r da*dw, max), the DFT notebook known answer.
