@@ -191,10 +191,23 @@ int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t 
 int mf_profile_kernels(int32_t enable);
 int mf_profile_collect(int64_t *launches, double *milliseconds);
 
-/* Workspace bytes mf_mm needs for the MFMA kernel (per-read digit-sum maxima). */
+/* Workspace bytes mf_mm needs for its MFMA kernels: per-read digit-sum maxima
+ * (ideal devices) or the conductance terms of every column (noisy devices; a
+ * smaller workspace of at least 64 columns' worth makes mf_mm work in column
+ * chunks).  0 when the general kernel is used. */
 int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64_t *bytes);
 
-/* Kernel selected by mf_mm for this shape: 0 = general, 1 = MFMA ideal. */
+/* Integer slice totals T [n, m*Gr, p*C] (FP32) of the noisy-device MFMA read,
+ * the values memfast/cuda.py:322-373 partial returns for tiles [0, p), for
+ * parity tests of that kernel: g NULL restores conductances from packed_t
+ * (seed, event) like mf_restore, or g is an injected FP32 [m][p][W][R][C]
+ * tensor.  MF_E_UNSUPPORTED when mf_mm would not use that kernel. */
+int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
+                 const uint8_t *packed_t, int64_t p, const float *g, uint32_t seed, uint64_t event,
+                 float *totals, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Kernel selected by mf_mm for this shape: 0 = general, 1 = MFMA ideal,
+ * 2 = MFMA noisy (bf16 split conductances). */
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
                  int32_t *kernel_id);
 

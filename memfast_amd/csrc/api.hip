@@ -261,6 +261,107 @@ void ideal_workspace(const mf_config *cfg, i64 n, i64 m, i64 p, i64 *xbytes, i64
     *wbytes = align256((p * cfg->cols + 31) / 32 * G * 8);
 }
 
+// Noisy-device MFMA eligibility and plan (noisy_mfma.hip): FP32 currents,
+// conductances that do not depend on the input slice (no slice_pair read
+// noise), no voltage or output-mode read noise, reads of 32 or 64 rows that
+// tile the array, plain cascade columns, FP32-exact totals.
+bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *ks,
+                      const char **why) {
+    if (cfg->precise) { *why = "FP64 currents"; return false; }
+    if (cfg->has_vnoise) { *why = "voltage variation"; return false; }
+    if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
+    if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
+        *why = "rows_per_read must be 32 or 64 and divide the array rows";
+        return false;
+    }
+    if (cfg->read_rows == 64 && cfg->n_in > 5) { *why = "more than 5 input slices at 64-row reads"; return false; }
+    if (cfg->n_in > 8 || cfg->n_w > 8) { *why = "too many slices"; return false; }
+    const i64 G = m * cfg->reads;
+    if (G >= 4096) { *why = "more than 4095 reads per output"; return false; }
+    if (!all_cascade_columns(cfg->cols, p)) { *why = "interleaved summation columns"; return false; }
+    double fa_sum = 0.0, fw_sum = 0.0;
+    for (int a = 0; a < cfg->n_in; ++a) fa_sum += std::fabs(double(cfg->in_factor[a]));
+    for (int w = 0; w < cfg->n_w; ++w) fw_sum += std::fabs(double(cfg->w_factor[w])) * cfg->adc_max[w];
+    if (fa_sum * fw_sum >= 16777216.0) { *why = "slice totals exceed FP32 integers"; return false; }
+    memset(plan, 0, sizeof(*plan));
+    plan->n_in = cfg->n_in;
+    plan->n_w = cfg->n_w;
+    for (int w = 0; w < cfg->n_w; ++w) {
+        plan->k1[w] = float(cfg->d_voltage * double(cfg->w_mask[w]) * cfg->d_inv_unit);
+        plan->top[w] = float(cfg->adc_max[w]);
+        plan->alpha[w] = cfg->has_nonlinear ? cfg->f_alpha_over_max[w] : 0.0f;
+        plan->fw[w] = float(cfg->w_factor[w]);
+    }
+    for (int a = 0; a < cfg->n_in; ++a) {
+        plan->fa[a] = float(cfg->in_factor[a]);
+        plan->in_shift[a] = cfg->in_shift[a];
+        plan->in_mask4[a] = u32(cfg->in_mask[a]) * 0x01010101u;
+    }
+    *ks = cfg->read_rows / 16;
+    return true;
+}
+
+// Bytes of conductance terms per 32-column block: 3 bf16 terms per cell and slice.
+i64 noisy_block_bytes(const mf_config *cfg, i64 m) { return i64(cfg->n_w) * 32 * m * cfg->rows * 3 * 2; }
+
+bool noisy_extent_ok(i64 n, i64 m, const mf_config *cfg) {
+    const i64 kp = m * cfg->rows;
+    return 64 * kp <= 0x7FFFFFFF && (n + 63) / 64 <= 65535;
+}
+
+// Split conductances and run k_noisy over column chunks that fit `bytes` of
+// workspace (at least 64 columns).  g: optional injected conductances.
+int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *q,
+                 const float *xscale, i64 n, i64 m, const u8 *packed_t, const float *wscale, i64 p,
+                 const float *g, u32 seed, u64 event, float *out, i64 ldo, void *workspace,
+                 i64 bytes, int totals, u32 *status, hipStream_t s) {
+    const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
+    const i64 per_block = noisy_block_bytes(cfg, m);
+    const i64 max_cb = (bytes / per_block) / 2 * 2;
+    if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
+    uint4 *gs = static_cast<uint4 *>(workspace);
+    for (i64 c_begin = 0; c_begin < ncols; c_begin += max_cb * 32) {
+        const i64 cols = (ncols - c_begin) < max_cb * 32 ? (ncols - c_begin) : max_cb * 32;
+        const i64 CB = (cols + 63) / 64 * 2;
+        const i64 threads = i64(cfg->n_w) * CB * G * ks * 64;
+        if (ks == 2)
+            hipLaunchKernelGGL(k_split_conductances<2>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
+                               packed_t, g, m, p, ncols, seed, event, c_begin, CB, gs);
+        else
+            hipLaunchKernelGGL(k_split_conductances<4>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
+                               packed_t, g, m, p, ncols, seed, event, c_begin, CB, gs);
+        NoisyArgs args{};
+        args.q = q;
+        args.gs = gs;
+        args.xscale = xscale;
+        args.wscale = wscale;
+        args.out = out;
+        args.status = status;
+        args.n = n;
+        args.kp = kp;
+        args.G = G;
+        args.ldo = ldo;
+        args.ldws = ncols;
+        args.ncols = ncols;
+        args.c_begin = c_begin;
+        args.CB = CB;
+        args.totals = totals;
+        const dim3 grid{unsigned(CB / 2), unsigned((n + 63) / 64), 1u};
+        const bool nl = cfg->has_nonlinear != 0;
+        if (ks == 4) {
+            if (nl) hipLaunchKernelGGL((k_noisy<4, 5, true>), grid, dim3(256), 0, s, plan, args);
+            else hipLaunchKernelGGL((k_noisy<4, 5, false>), grid, dim3(256), 0, s, plan, args);
+        } else if (cfg->n_in <= 5) {
+            if (nl) hipLaunchKernelGGL((k_noisy<2, 5, true>), grid, dim3(256), 0, s, plan, args);
+            else hipLaunchKernelGGL((k_noisy<2, 5, false>), grid, dim3(256), 0, s, plan, args);
+        } else {
+            if (nl) hipLaunchKernelGGL((k_noisy<2, 8, true>), grid, dim3(256), 0, s, plan, args);
+            else hipLaunchKernelGGL((k_noisy<2, 8, false>), grid, dim3(256), 0, s, plan, args);
+        }
+    }
+    return check_launch("noisy MFMA read");
+}
+
 SliceLayout layout_of(const int32_t *shift, const int32_t *mask, int count) {
     SliceLayout l{};
     l.count = count;
@@ -548,8 +649,15 @@ int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t 
     SlotTests xt, wt;
     int ks = 0;
     const char *why = "";
-    *kernel_id = (has_packed_t && ideal_extent_ok(cfg, n, m, p) &&
-                  build_ideal_plan(cfg, m, p, &plan, &xt, &wt, &ks, &why)) ? 1 : 0;
+    NoisyPlan noisy;
+    if (has_packed_t && ideal_extent_ok(cfg, n, m, p) &&
+        build_ideal_plan(cfg, m, p, &plan, &xt, &wt, &ks, &why))
+        *kernel_id = 1;
+    else if (has_packed_t && noisy_extent_ok(n, m, cfg) &&
+             build_noisy_plan(cfg, m, p, &noisy, &ks, &why))
+        *kernel_id = 2;
+    else
+        *kernel_id = 0;
     return MF_OK;
 }
 
@@ -557,9 +665,20 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64
     int status = check_config(cfg);
     if (status) return status;
     if (!bytes || n < 1 || m < 1 || p < 1) return fail(MF_E_INVALID, "invalid workspace query");
-    i64 xb, wb;
-    ideal_workspace(cfg, n, m, p, &xb, &wb);
-    *bytes = xb + wb;
+    IdealPlan plan;
+    SlotTests xt, wt;
+    NoisyPlan noisy;
+    int ks = 0;
+    const char *why = "";
+    if (build_ideal_plan(cfg, m, p, &plan, &xt, &wt, &ks, &why)) {
+        i64 xb, wb;
+        ideal_workspace(cfg, n, m, p, &xb, &wb);
+        *bytes = xb + wb;
+    } else if (build_noisy_plan(cfg, m, p, &noisy, &ks, &why)) {
+        *bytes = (p * cfg->cols + 63) / 64 * 2 * noisy_block_bytes(cfg, m);
+    } else {
+        *bytes = 0;
+    }
     return MF_OK;
 }
 
@@ -635,6 +754,21 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         }
         return check_launch("ideal MFMA read");
     }
+    NoisyPlan noisy;
+    if (!g && packed_t && aligned && workspace && ideal_extent_ok(cfg, n, m, p) &&
+        noisy_extent_ok(n, m, cfg) && build_noisy_plan(cfg, m, p, &noisy, &ks, &why) &&
+        workspace_bytes >= 2 * noisy_block_bytes(cfg, m)) {
+        std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+        const int launched = launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p,
+                                          nullptr, seed, event, out, ldo, workspace,
+                                          workspace_bytes, 0, status, s);
+        if (timing.first) {
+            hipEventRecord(timing.second, s);
+            g_profile.pending.push_back(timing);
+        }
+        return launched;
+    }
     if (!g && needs_conductances(cfg))
         return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
     GeneralArgs args{};
@@ -666,6 +800,27 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         g_profile.pending.push_back(timing);
     }
     return launched;
+}
+
+int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
+                 const uint8_t *packed_t, int64_t p, const float *g, uint32_t seed, uint64_t event,
+                 float *totals, void *workspace, int64_t workspace_bytes, void *stream) {
+    const int valid = check_config(cfg);
+    if (valid) return valid;
+    if (!q || !packed_t || !totals || !workspace || n < 1 || m < 1 || p < 1)
+        return fail(MF_E_INVALID, "invalid totals arguments");
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(packed_t)) % 16)
+        return fail(MF_E_INVALID, "codes must be 16-byte aligned");
+    NoisyPlan noisy;
+    int ks = 0;
+    const char *why = "";
+    if (!ideal_extent_ok(cfg, n, m, p) || !noisy_extent_ok(n, m, cfg) ||
+        !build_noisy_plan(cfg, m, p, &noisy, &ks, &why))
+        return fail(MF_E_UNSUPPORTED, "noisy MFMA read not applicable: %s", why);
+    const i64 ncols = p * cfg->cols;
+    return launch_noisy(cfg, noisy, ks, q, nullptr, n, m, packed_t, nullptr, p, g, seed, event,
+                        totals, ncols, workspace, workspace_bytes, 1, nullptr,
+                        static_cast<hipStream_t>(stream));
 }
 
 int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,

@@ -97,6 +97,35 @@ template <typename Phys>
 __global__ void k_restore(const mf_config cfg, const u8 *packed, i64 m, i64 p, i64 begin,
                           i64 width, u32 seed, u64 event, int planes, Phys *g);
 
+// ---- noisy-device MFMA read (noisy_mfma.hip) -------------------------------
+// Per-slice constants of the fused ADC: z = k1[w] * sum_r da * (g - L),
+// S-curve z / (1 + |alpha[w] * z|), code = round(clamp(z, 0, top[w])),
+// T += fa[a] * fw[w] * code.
+struct NoisyPlan {
+    int n_in, n_w;
+    float k1[8], top[8], alpha[8], fa[8], fw[8];
+    int in_shift[8];
+    u32 in_mask4[8];   // input slice mask replicated into four bytes
+};
+
+struct NoisyArgs {
+    const u8 *q;          // [n, kp] input codes
+    const uint4 *gs;      // conductance terms of columns [c_begin, c_begin + 32*CB), fragment order
+    const float *xscale;  // [n, G]
+    const float *wscale;  // [G, ldws]
+    float *out;           // fused: [n, ldo]; totals: [n, G, ldo]
+    u32 *status;          // optional: MF_STATUS_OUTPUT for a non-finite fused output
+    i64 n, kp, G, ldo, ldws, ncols, c_begin, CB;
+    int totals;
+};
+
+template <int KS>
+__global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, const float *g_in,
+                                     i64 m, i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin,
+                                     i64 CB, uint4 *gs);
+template <int KS, int NA, bool NONLINEAR>
+__global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
+
 // ---- FP64 restore and read sum (stable.hip) --------------------------------
 __global__ void k_stable_sum(const float *totals, i64 n, i64 G, i64 wc, const float *xscale,
                              const float *wscale, i64 ldws, i64 col0, double *out, i64 ldo,

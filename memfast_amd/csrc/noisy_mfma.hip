@@ -1,0 +1,297 @@
+// Noisy-device sliced array read on gfx950 bf16 MFMA, fused with the ADC, the
+// signed shift-add, the scale restore and torch's read-order summation.
+//
+// Model (memfast/reference.py:63-117): per read group, input slice a and
+// weight slice w,
+//   I = sum_r (V * da/Ma) * (g[r,c] - L),   z = I * Ma*Mw / unit,
+//   z = z / (1 + |alpha/max_w * z|) (S-curve),  code = round(clamp(z, 0, max_w)),
+//   T = sum_a sum_w fa*fw*code.
+// Here z = (V*Mw/unit) * sum_r da * (g - L): the input digits da are small
+// integers (exact in bf16) and g - L (FP32) is split into three bf16 terms
+// hi + mid + lo that sum to it exactly, so three bf16 MFMAs with FP32
+// accumulation give the current to FP32 accuracy.  Results agree with the CPU
+// reference to its own FP32 rounding (codes may flip at rounding boundaries).
+//
+// k_split_conductances writes the conductances (programming, drift, stuck-at
+// and shared read noise, as memfast/reference.py:10-51, or an injected
+// tensor) as g - L terms in MFMA fragment order, so each wave loads its
+// 32-column x 32-row operand with one contiguous 1 KiB access per term.
+// k_noisy: block = 4 waves (2 column x 2 vector), wave tile 32 columns x 32
+// vectors, A operand = conductance terms, B operand = input digits built in
+// registers from the codes q.  Per read and pair: 3*KS MFMAs and the ADC
+// (about 7 VALU ops per output); bound: VALU (the ADC), MFMA as co-bound.
+#include <cfloat>
+
+#include "mf_kernels.h"
+
+namespace mf {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4fn __attribute__((ext_vector_type(4)));
+
+// FP32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ u32 bf16_bits(float x) {
+    const u32 b = __float_as_uint(x);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_value(u32 bits) { return __uint_as_float(bits << 16); }
+
+template <int KS>
+__global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg, const u8 *packed_t,
+                                                            const float *g_in, i64 m, i64 p,
+                                                            i64 ncols, u32 seed, u64 event,
+                                                            i64 c_begin, i64 CB, uint4 *gs) {
+    constexpr int P = 16 * KS;
+    const int R = cfg.rows, C = cfg.cols, W = cfg.n_w;
+    const i64 kp = m * R, G = kp / P;
+    const i64 total = i64(W) * CB * G * KS * 64;
+    const u64 read_seed = event_seed(seed, event);
+    for (i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += i64(gridDim.x) * blockDim.x) {
+        i64 rest = t;
+        const int lane = int(rest & 63); rest >>= 6;
+        const int ks = int(rest % KS); rest /= KS;
+        const i64 g = rest % G; rest /= G;
+        const i64 cb = rest % CB;
+        const int w = int(rest / CB);
+        const int lr = lane & 31, h = lane >> 5;
+        const i64 c = c_begin + cb * 32 + lr;
+        const i64 k0 = g * P + ks * 16 + h * 8;
+        u32 terms[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        if (c < ncols) {
+            const uint2 bytes = *reinterpret_cast<const uint2 *>(packed_t + c * kp + k0);
+            const i64 i = k0 / R, r0 = k0 - i * R;
+            const i64 tt = c / C, cc = c - tt * C;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const u8 code = u8(((j < 4 ? bytes.x : bytes.y) >> (8 * (j & 3))) & 0xFFu);
+                const u64 cell = u64((((i * p + tt) * W + w) * R + r0 + j) * C + cc);
+                const float level = g_in ? g_in[cell]
+                                         : cell_conductance<float>(cfg, code, w, cell, seed, read_seed);
+                const float delta = level - cfg.f_low;
+                const u32 hi = bf16_bits(delta);
+                const float r1 = delta - bf16_value(hi);
+                const u32 mid = bf16_bits(r1);
+                const u32 lo = bf16_bits(r1 - bf16_value(mid));
+                const int shift = 16 * (j & 1);
+                terms[0][j >> 1] |= hi << shift;
+                terms[1][j >> 1] |= mid << shift;
+                terms[2][j >> 1] |= lo << shift;
+            }
+        }
+        uint4 *dst = gs + (((w * CB + cb) * G + g) * 3 * KS + ks) * 64 + lane;
+#pragma unroll
+        for (int term = 0; term < 3; ++term)
+            dst[term * KS * 64] = make_uint4(terms[term][0], terms[term][1], terms[term][2],
+                                             terms[term][3]);
+    }
+}
+
+template __global__ void k_split_conductances<2>(const mf_config, const u8 *, const float *, i64,
+                                                 i64, i64, u32, u64, i64, i64, uint4 *);
+template __global__ void k_split_conductances<4>(const mf_config, const u8 *, const float *, i64,
+                                                 i64, i64, u32, u64, i64, i64, uint4 *);
+
+// Buffer resource over [base, base + bytes): loads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t noisy_buffer(const void *base, i64 bytes) {
+    const int records = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : int(bytes < 0 ? 0 : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), short(0), records,
+                                             0x00020000);
+}
+
+// Eight input digits (bytes of `word`, slice (shift, mask)) as eight bf16.
+__device__ __forceinline__ v8bf digits_bf16(uint2 word, int shift, u32 mask4) {
+    const u32 lo = (word.x >> shift) & mask4, hi = (word.y >> shift) & mask4;
+    // (byte of a u32) -> float compiles to v_cvt_f32_ubyte{0..3}.
+    const float f[8] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
+                        float(lo >> 24), float(hi & 0xFFu), float((hi >> 8) & 0xFFu),
+                        float((hi >> 16) & 0xFFu), float(hi >> 24)};
+    // Small integers are exact in bf16: keep the upper half of each FP32.
+    uint4 packed;
+    packed.x = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+    packed.y = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u);
+    packed.z = __builtin_amdgcn_perm(__float_as_uint(f[5]), __float_as_uint(f[4]), 0x07060302u);
+    packed.w = __builtin_amdgcn_perm(__float_as_uint(f[7]), __float_as_uint(f[6]), 0x07060302u);
+    return __builtin_bit_cast(v8bf, packed);
+}
+
+template <int KS, int NA, bool NONLINEAR>
+__global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const NoisyArgs args) {
+    constexpr int P = 16 * KS;
+    constexpr int BC = 64, BV = 64;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wc = wave & 1, wv = wave >> 1;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const i64 c0 = i64(blockIdx.x) * BC;              // chunk-relative first column
+    const i64 v0 = i64(blockIdx.y) * BV;
+    const int G = int(args.G);
+    const int A = plan.n_in, W = plan.n_w;
+    const i64 kp = args.kp;
+    const i64 cbw = (c0 + wc * 32) / 32;
+    const i64 vrows = (args.n - v0) < BV ? (args.n - v0) : BV;
+    const __amdgpu_buffer_rsrc_t qbuf = noisy_buffer(args.q + v0 * kp, vrows * kp);
+    const int q_off = (wv * 32 + lrow) * int(kp) + lhalf * 8;
+    const uint4 *frag_base = args.gs + cbw * i64(G) * 3 * KS * 64 + lane;
+    const i64 w_stride = args.CB * i64(G) * 3 * KS * 64;
+
+    // This lane's output coordinates (MFMA 32x32 layout: reg r -> column
+    // 8*(r/4) + 4*lhalf + r%4 of the wave tile, vector lrow).
+    const i64 n_out = v0 + wv * 32 + lrow;
+    const i64 col_tile = args.c_begin + c0 + wc * 32;   // absolute first column of the wave
+
+    float acc0[16], acc1[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { acc0[r] = 0.0f; acc1[r] = 0.0f; }
+
+    uint2 qw[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const u32 x = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16, 0, 0);
+        const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16 + 4, 0, 0);
+        qw[ks] = make_uint2(x, y);
+    }
+
+    for (int g = 0; g < G; ++g) {
+        // Input digits of this read for every slice (B operands).
+        v8bf B[NA][KS];
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            if (a >= A) break;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                B[a][ks] = digits_bf16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
+        }
+        if (g + 1 < G) {
+            const int next = (g + 1) * P;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const u32 x = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + next + ks * 16, 0, 0);
+                const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + next + ks * 16 + 4, 0, 0);
+                qw[ks] = make_uint2(x, y);
+            }
+        }
+
+        float T[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[r] = 0.0f;
+        const uint4 *frag_g = frag_base + i64(g) * 3 * KS * 64;
+        for (int w = 0; w < W; ++w) {
+            const uint4 *frag = frag_g + w * w_stride;
+            v8bf F[3][KS];
+#pragma unroll
+            for (int term = 0; term < 3; ++term)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    F[term][ks] = __builtin_bit_cast(v8bf, frag[(term * KS + ks) * 64]);
+            const float k1 = plan.k1[w], top = plan.top[w], alpha = plan.alpha[w];
+            const float fw = plan.fw[w];
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+                if (a >= A) break;
+                v16f I = {};
+#pragma unroll
+                for (int term = 0; term < 3; ++term)
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks)
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B[a][ks], I, 0, 0, 0);
+                const float f = plan.fa[a] * fw;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float z = I[r] * k1;
+                    if (NONLINEAR) z = z * __builtin_amdgcn_rcpf(fmaf(fabsf(z), alpha, 1.0f));
+                    z = __builtin_amdgcn_fmed3f(z, 0.0f, top);
+                    T[r] = fmaf(rintf(z), f, T[r]);
+                }
+            }
+        }
+
+        if (args.totals) {
+            if (n_out < args.n) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+                    if (c < args.ncols) args.out[(n_out * G + g) * args.ldo + c] = T[r];
+                }
+            }
+            continue;
+        }
+
+        // Scale restore (float(T) * xs) * ws and torch's cascade over reads.
+        const float xs = n_out < args.n ? args.xscale[n_out * G + g] : 0.0f;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            const i64 c = col_tile + qd * 8 + lhalf * 4;
+            v4fn ws = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (c + 3 < args.ncols) {
+                ws = *reinterpret_cast<const v4fn *>(args.wscale + i64(g) * args.ldws + c);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c + e < args.ncols) ws[e] = args.wscale[i64(g) * args.ldws + c + e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = T[qd * 4 + e] * xs;
+                v = v * ws[e];
+                acc0[qd * 4 + e] = acc0[qd * 4 + e] + v;
+            }
+        }
+        const int count = g + 1;
+        if ((count & 15) == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc1[r] = acc1[r] + acc0[r];
+                acc0[r] = 0.0f;
+            }
+            if ((count & 255) == 0) {
+                // Level 2 of the cascade lives in `out` (more than 255 reads).
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+                    if (n_out < args.n && c < args.ncols) {
+                        float *dst = args.out + n_out * args.ldo + c;
+                        *dst = count == 256 ? acc1[r] : *dst + acc1[r];
+                    }
+                    acc1[r] = 0.0f;
+                }
+            }
+        }
+    }
+    if (args.totals || n_out >= args.n) return;
+
+    bool finite = true;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+        const i64 c = col_tile + qd * 8 + lhalf * 4;
+        float *dst = args.out + n_out * args.ldo + c;
+        v4fn v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float s = acc0[qd * 4 + e] + acc1[qd * 4 + e];
+            if (G >= 256 && c + e < args.ncols) s = s + dst[e];
+            v[e] = s;
+            finite = finite && (c + e >= args.ncols || fabsf(s) <= FLT_MAX);
+        }
+        if (c + 3 < args.ncols) {
+            *reinterpret_cast<v4fn *>(dst) = v;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (c + e < args.ncols) dst[e] = v[e];
+        }
+    }
+    if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
+}
+
+template __global__ void k_noisy<2, 5, false>(const NoisyPlan, const NoisyArgs);
+template __global__ void k_noisy<2, 5, true>(const NoisyPlan, const NoisyArgs);
+template __global__ void k_noisy<2, 8, false>(const NoisyPlan, const NoisyArgs);
+template __global__ void k_noisy<2, 8, true>(const NoisyPlan, const NoisyArgs);
+template __global__ void k_noisy<4, 5, false>(const NoisyPlan, const NoisyArgs);
+template __global__ void k_noisy<4, 5, true>(const NoisyPlan, const NoisyArgs);
+
+}  // namespace mf

@@ -137,6 +137,8 @@ SIGNATURES = {
                     _P, _P, _P], ct.c_int),
     "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
                _I64, _P, _I64, _I32, _P, _P], ct.c_int),
+    "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
+                      _P], ct.c_int),
     "mf_stable_sum": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P], ct.c_int),
     "mf_profile_kernels": ([_I32], ct.c_int),
     "mf_profile_collect": ([ct.POINTER(_I64), ct.POINTER(ct.c_double)], ct.c_int),
@@ -481,7 +483,8 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     n, m, r = q.shape
     p, c = packed.shape[1], config.array_size[1]
     g = conductance
-    if g is None and needs_conductances(config):
+    kernel = mm_kernel(config, n, m, p) if g is None and packed_t is not None else 0
+    if g is None and kernel == 0 and needs_conductances(config):
         g = restore(packed, config, seed, event, 0, p)
     if g is not None:
         g = _checked_conductance(g, config, m, p, r, c)
@@ -489,7 +492,7 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     if out is None:
         out = torch.empty((n, p * c), dtype=torch.float32, device=q.device)
     workspace = None
-    if packed_t is not None:
+    if packed_t is not None and kernel:
         size = ct.c_int64()
         check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
               "workspace size")
@@ -546,8 +549,44 @@ def collect_kernel_times():
     return launches.value, ms.value
 
 
+def mm_totals(q, packed_t, config, seed, event, *, conductance=None):
+    """Slice totals T [N, m*Gr, p, C] (FP32) from the noisy-device MFMA kernel.
+
+    Same values as ``partial(q, packed, config, None, seed, event, 0, p)``
+    (memfast/cuda.py:322-373) up to ADC rounding-boundary flips; for parity
+    tests of the kernel ``mm`` uses with noisy devices.  ``conductance``
+    injects FP32 conductances [m, p, W, R, C] (one plane).
+    """
+    supported(config)
+    require_device(q)
+    n, m, r = q.shape
+    c = config.array_size[1]
+    p = packed_t.shape[0] // c
+    g = None
+    if conductance is not None:
+        g = conductance.to(device=q.device, dtype=torch.float32).contiguous()
+        if tuple(g.shape) != (m, p, len(config.weight_layout), r, c):
+            raise ValueError("injected conductances must be [m, p, W, R, C]")
+    size = ct.c_int64()
+    check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
+          "workspace size")
+    workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
+    groups = m * config.reads_per_array
+    totals = torch.empty((n, groups, p, c), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        check(
+            library().mf_mm_totals(
+                ct.byref(descriptor(config)), _ptr(q.contiguous()), n, m,
+                _ptr(packed_t.contiguous()), p, _ptr(g), seed, event, _ptr(totals),
+                _ptr(workspace), workspace.numel(), _stream(q.device),
+            ),
+            "mm totals",
+        )
+    return totals
+
+
 def mm_kernel(config, n, m, p, has_packed_t=True):
-    """0: general kernel, 1: ideal-device MFMA kernel (what ``mm`` will launch)."""
+    """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA (what ``mm`` launches)."""
     out = ct.c_int32()
     check(library().mf_mm_kernel(ct.byref(descriptor(config)), n, m, p, int(has_packed_t),
                                  ct.byref(out)), "kernel selection")

@@ -577,7 +577,7 @@ class AnalogMatrix(nn.Module):
             output = self._execute_stable(q, xscale, packed, event)
         else:
             codes_t = self._column_codes() if hip.mm_kernel(
-                config, q.shape[0], q.shape[1], self.p) == 1 else None
+                config, q.shape[0], q.shape[1], self.p) else None
             status = hip.status_word(q.device)
             output = hip.mm(q, xscale, packed, codes_t, self.weight_scale.reshape(-1, self.p * c),
                             config, self.seed, event,

@@ -363,11 +363,14 @@ def restore_scales(value, input_scale, weight_scale):
 
 
 def execute(q, xscale, packed, wscale, cfg, seed, event, out_features, *, bias=None,
-            arrays=2, stable=False, conductance=None):
+            arrays=2, stable=False, conductance=None, totals=None):
     """Fused epilogue of AnalogMatrix._execute (simulator.py:561-616).
 
     ``conductance`` (optional) is the full [m,p,W,R,C] injected tensor.
-    Zero-point correction (map_quantized) is not covered by the hot path.
+    ``totals`` (optional) supplies the slice totals [N, m*Gr, p, C] of every
+    tile instead of computing them with ``partial`` (to check a kernel's
+    epilogue on its own totals).  Zero-point correction (map_quantized) is not
+    covered by the hot path.
     """
     p = packed.shape[1]
     c = cfg.array_size[1]
@@ -377,7 +380,10 @@ def execute(q, xscale, packed, wscale, cfg, seed, event, out_features, *, bias=N
     for begin in range(0, p, width):
         end = min(begin + width, p)
         injected = None if conductance is None else conductance[:, begin:end]
-        value = partial(q, packed, cfg, seed, event, begin, end, conductance=injected)
+        if totals is not None:
+            value = totals[:, :, begin:end].to(torch.float64 if is_wide(cfg) else torch.float32)
+        else:
+            value = partial(q, packed, cfg, seed, event, begin, end, conductance=injected)
         if wide:
             value = restore_scales(value, xscale[:, :, None, None], wscale[None, :, begin:end, :])
         else:
@@ -389,7 +395,7 @@ def execute(q, xscale, packed, wscale, cfg, seed, event, out_features, *, bias=N
         output = output + bias
     if not is_wide(cfg) and not stable and not torch.isfinite(output).all():
         return execute(q, xscale, packed, wscale, cfg, seed, event, out_features, bias=bias,
-                       arrays=arrays, stable=True, conductance=conductance)
+                       arrays=arrays, stable=True, conductance=conductance, totals=totals)
     return output
 
 

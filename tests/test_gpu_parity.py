@@ -146,8 +146,11 @@ def test_ideal_mm_bit_exact(hip_device, name, cfg, n, k, o):
 def test_mfma_kernel_selected_for_baseline(hip_device):
     cfg = ideal(**CONFIG2)
     assert hip.mm_kernel(cfg, 4096, 32, 32) == 1
-    noisy = Config(**CONFIG2)
-    assert hip.mm_kernel(noisy, 4096, 32, 32) == 0
+    noisy = Config(**CONFIG2)   # default write variation
+    assert hip.mm_kernel(noisy, 4096, 32, 32) == 2
+    slice_pair = Config(**CONFIG2, nonidealities=Nonidealities(read_variation=0.01,
+                                                              read_mode="slice_pair"))
+    assert hip.mm_kernel(slice_pair, 4096, 32, 32) == 0
 
 
 @pytest.mark.parametrize("name,cfg,n,k,o", IDEAL_CASES[:4], ids=[c[0] for c in IDEAL_CASES[:4]])
@@ -420,3 +423,110 @@ def test_stable_sum_matches_cpu_restore(hip_device, groups, width, c):
     ws_rows = torch.cat([torch.ones(groups, 8), ws], dim=1)
     hip.stable_sum(totals.to(hip_device), xs.to(hip_device), ws_rows.to(hip_device), cfg, 8, out)
     assert bits_equal(out[:, 8:], expected)
+
+
+# ---------------------------------------------------------------------------
+# Noisy devices on the bf16 MFMA kernel (reads of 32 or 64 rows)
+# ---------------------------------------------------------------------------
+MFMA_NOISY = {
+    "write": (dict(), dict(write_variation=0.02)),
+    "shared_scurve": (dict(), dict(write_variation=0.02, read_variation=0.01,
+                                   adc_nonlinearity=0.1)),
+    "saf_drift": (dict(), dict(write_variation=0.02, stuck_at_low=0.05, stuck_at_high=0.03,
+                               drift_coefficient=0.05, drift_time=100.0)),
+    "binary8": (dict(input_slice=None, weight_slice=(1, 1, 2, 2, 2), adc_bits=(4, 5, 5, 6, 6)),
+                dict(write_variation=0.03, adc_nonlinearity=0.05)),
+    "rows64": (dict(array_size=(128, 32), rows_per_read=64, weight_quant_gran=(64, 1),
+                    input_quant_gran=(1, 64)), dict(write_variation=0.02, read_variation=0.01)),
+}
+NOISY_BASE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                  weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,
+                  weight_quant_gran=(32, 1), input_quant_gran=(1, 32), adc_bits=(6, 7, 7, 8, 8))
+
+
+def noisy_case(mode):
+    extra, effects = MFMA_NOISY[mode]
+    return Config(**(NOISY_BASE | extra), nonidealities=Nonidealities(**effects))
+
+
+def packed_columns(packed):
+    m, p, r, c = packed.shape
+    return packed.permute(1, 3, 0, 2).reshape(p * c, m * r).contiguous()
+
+
+@pytest.mark.parametrize("mode", list(MFMA_NOISY))
+def test_noisy_mfma_totals_with_injected_conductances(hip_device, mode):
+    """Same slice totals as the oracle given the same conductances, except ADC flips."""
+    say("noisy mfma totals", mode)
+    cfg = noisy_case(mode)
+    gen = torch.Generator().manual_seed(31)
+    a = torch.randn(40, 200, generator=gen)
+    b = torch.randn(200, 100, generator=gen)
+    q, _ = oracle.input_tiles(a, cfg)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    n, m, r = q.shape
+    p = packed.shape[1]
+    assert hip.mm_kernel(cfg, n, m, p) == 2
+    seed, event = 4242, 3
+    raw, _, _ = oracle.restored(packed, cfg, seed, event, 0, p)
+    expected = oracle.partial(q, packed, cfg, seed, event, 0, p, conductance=raw)
+    got = hip.mm_totals(q.to(hip_device), packed_columns(packed).to(hip_device), cfg, seed, event,
+                        conductance=raw.to(hip_device)).cpu()
+    diff = got.double() - expected.double()
+    codes = diff.numel() * len(cfg.input_layout) * len(cfg.weight_layout)
+    flips = int((diff != 0).sum())
+    largest = max(abs(fa * fw) for _, _, fa in cfg.input_layout for _, _, fw in cfg.weight_layout)
+    say("  totals differing", flips, "of", diff.numel(), "max", diff.abs().max().item())
+    assert flips <= max(1, 1e-4 * codes)
+    assert diff.abs().max().item() <= 2 * largest
+
+
+@pytest.mark.parametrize("mode", list(MFMA_NOISY))
+def test_noisy_mfma_sampled_conductances(hip_device, mode):
+    """Conductances sampled on the GPU (counter RNG, OCML) against the oracle's samples."""
+    cfg = noisy_case(mode)
+    gen = torch.Generator().manual_seed(32)
+    a = torch.randn(40, 200, generator=gen)
+    b = torch.randn(200, 100, generator=gen)
+    q, _ = oracle.input_tiles(a, cfg)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    p = packed.shape[1]
+    seed, event = 99, 7
+    expected = oracle.partial(q, packed, cfg, seed, event, 0, p)
+    got = hip.mm_totals(q.to(hip_device), packed_columns(packed).to(hip_device), cfg, seed,
+                        event).cpu()
+    diff = got.double() - expected.double()
+    codes = diff.numel() * len(cfg.input_layout) * len(cfg.weight_layout)
+    flips = int((diff != 0).sum())
+    say("  totals differing", flips, "of", diff.numel())
+    assert flips <= max(1, 1e-4 * codes)
+
+
+@pytest.mark.parametrize("mode", list(MFMA_NOISY))
+def test_noisy_mfma_epilogue_and_mm(hip_device, mode):
+    """Fused output = the reference epilogue of the kernel's own totals, bit for bit; and
+    Simulator.mm within the flip budget of the oracle."""
+    from memfast_amd import Simulator
+
+    cfg = noisy_case(mode)
+    gen = torch.Generator().manual_seed(33)
+    a = torch.randn(40, 200, generator=gen)
+    b = torch.randn(200, 100, generator=gen)
+    q, xs = oracle.input_tiles(a, cfg)
+    packed, ws = oracle.weight_tiles(b.T, cfg)
+    n, m, r = q.shape
+    p, c = packed.shape[1], cfg.array_size[1]
+    seed, event = 1234, 0
+    codes_t = packed_columns(packed).to(hip_device)
+    totals = hip.mm_totals(q.to(hip_device), codes_t, cfg, seed, event).cpu()
+    fused = hip.mm(q.to(hip_device), xs.to(hip_device), packed.to(hip_device), codes_t,
+                   ws.reshape(-1, p * c).to(hip_device), cfg, seed, event).cpu()
+    restored = oracle.execute(q, xs, packed, ws, cfg, seed, event, p * c, totals=totals)
+    assert bits_equal(fused, restored)
+    sim = Simulator(cfg, device=hip_device)
+    got = sim.mm(a.to(hip_device), b.to(hip_device)).cpu()
+    ref = oracle.mm(a, b, cfg)
+    rel = (got - ref).abs() / ref.abs().clamp_min(1e-6)
+    bad = (rel > 1e-5).float().mean().item()
+    say("  elements beyond 1e-5:", bad)
+    assert bad <= 0.02
