@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 1
+#define MF_ABI_VERSION 2
 #define MF_MAX_SLICES 32
 
 enum {
@@ -81,6 +81,11 @@ typedef struct mf_config {
     /* FP64 constants (precise currents) */
     double d_high, d_low, d_voltage, d_span, d_inv_unit, d_drift;
     double d_alpha_over_max[MF_MAX_SLICES];
+    /* Wide configurations (memfast/config.py:213-215 `wide`): precision above 8
+     * bits or block floating point.  Codes are 32-bit (uint32_t), scales and
+     * outputs FP64; the *_wide entry points take them. */
+    int32_t wide;
+    int32_t bw_e;                 /* BFP exponent bits, 0 for INT quantization */
 } mf_config;
 
 /* Identity of a device for the tuning-cache key (replaces memfast/cuda.py:376-389). */
@@ -182,6 +187,41 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
 int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,
                   const float *xscale, const float *wscale, int64_t ldws, int64_t col0, double *out,
                   int64_t ldo, void *stream);
+
+/* ---- wide configurations ------------------------------------------------
+ * Precision above 8 bits or BFP (cfg->wide): codes are uint32_t (the
+ * reference's int64 codes masked to the precision), scales and outputs FP64,
+ * as memfast/quantization.py:9-137 and memfast/simulator.py:561-585 compute
+ * them there.  The u8 entry points above reject wide descriptors and these
+ * reject narrow ones. */
+/* Dynamic grouped INT/BFP quantization of activations in FP64 (`work`: uint64
+ * grid scratch); BFP exponents follow floor(log2(max)) of a correctly rounded
+ * log2. */
+int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k,
+                            int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                            uint32_t *q, double *xscale, uint32_t *status, void *stream);
+/* Fixed-scale input tiles (scale [k]). */
+int mf_input_tiles_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k, int64_t ld,
+                        const double *scale, uint32_t *q, double *xscale, void *stream);
+/* Weight programming: packed [m, p, R, C] as int64 (the reference's checkpoint
+ * dtype) and the same codes as uint32_t for the read kernels. */
+int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, int64_t o,
+                             int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                             int64_t *packed, uint32_t *packed32, double *wscale, uint32_t *status,
+                             void *stream);
+/* mf_restore, mf_partial and mf_mm for wide codes (totals and outputs FP64;
+ * the fused read restores with restore_scales in FP64 and sums in torch's
+ * FP64 order). */
+int mf_restore_wide(const mf_config *cfg, const uint32_t *packed, int64_t m, int64_t p,
+                    int64_t begin, int64_t end, uint32_t seed, uint64_t event, void *g,
+                    void *stream);
+int mf_partial_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t m,
+                    const uint32_t *packed, int64_t p, int64_t begin, int64_t end, const void *g,
+                    uint32_t seed, uint64_t event, double *totals, int32_t *codes, void *stream);
+int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, int64_t n, int64_t m,
+               const uint32_t *packed, const double *wscale, int64_t p, const void *g,
+               uint32_t seed, uint64_t event, double *out, int64_t ldo, uint32_t *status,
+               void *stream);
 
 /* Benchmark timing of mf_mm's main read kernel (no reference counterpart; the
  * reference times whole candidate calls with CUDA events, memfast/simulator.py:306-316):

@@ -79,10 +79,26 @@ int check_config(const mf_config *cfg) {
         return fail(MF_E_INVALID, "invalid array geometry");
     if (cfg->n_in < 1 || cfg->n_in > MF_MAX_SLICES || cfg->n_w < 1 || cfg->n_w > MF_MAX_SLICES)
         return fail(MF_E_INVALID, "invalid slice counts");
-    if (cfg->activation_bits > 8 || cfg->weight_bits > 8)
-        return fail(MF_E_UNSUPPORTED,
-                    "precisions above 8 bits (64-bit codes, FP64 restore) are not implemented "
-                    "on the HIP backend yet");
+    if (cfg->activation_bits < 2 || cfg->activation_bits > 32 || cfg->weight_bits < 2 ||
+        cfg->weight_bits > 32)
+        return fail(MF_E_INVALID, "precisions must be 2..32 bits");
+    const bool wide = cfg->activation_bits > 8 || cfg->weight_bits > 8 || cfg->bw_e != 0;
+    if (bool(cfg->wide) != wide) return fail(MF_E_INVALID, "descriptor wide flag is inconsistent");
+    return MF_OK;
+}
+
+// Narrow (u8 codes, FP32 scales) and wide (u32 codes, FP64 scales) entry points.
+int check_narrow(const mf_config *cfg) {
+    const int status = check_config(cfg);
+    if (status) return status;
+    if (cfg->wide) return fail(MF_E_INVALID, "wide configuration: use the *_wide entry point");
+    return MF_OK;
+}
+
+int check_wide(const mf_config *cfg) {
+    const int status = check_config(cfg);
+    if (status) return status;
+    if (!cfg->wide) return fail(MF_E_INVALID, "narrow configuration: use the u8 entry point");
     return MF_OK;
 }
 
@@ -143,6 +159,7 @@ SliceForm slice_form(int shift, int mask, bool sign_slice, int bits) {
 // general kernel must be used.
 bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotTests *xtests,
                       SlotTests *wtests, int *ks, const char **why) {
+    if (cfg->wide) { *why = "wide codes"; return false; }
     if (cfg->has_write || cfg->has_read || cfg->has_vnoise || cfg->has_nonlinear || cfg->has_saf ||
         cfg->has_drift) {
         *why = "device effects enabled";
@@ -267,6 +284,7 @@ void ideal_workspace(const mf_config *cfg, i64 n, i64 m, i64 p, i64 *xbytes, i64
 // tile the array, plain cascade columns, FP32-exact totals.
 bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *ks,
                       const char **why) {
+    if (cfg->wide) { *why = "wide codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
     if (cfg->has_vnoise) { *why = "voltage variation"; return false; }
     if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
@@ -378,17 +396,28 @@ int launch_general(const mf_config *cfg, const GeneralArgs &args, int out_kind, 
     if (vec_blocks > 2147483647) return fail(MF_E_RESOURCE, "too many input vectors");
     const dim3 grid{unsigned(vec_blocks), unsigned(col_blocks), 1u};
     const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
-    if (sizeof(Phys) == 4) {
-        if (output_noise)
-            hipLaunchKernelGGL((k_general<float, 2, true>), grid, dim3(256), 0, s, *cfg, args, out_kind);
-        else
-            hipLaunchKernelGGL((k_general<float, 8, false>), grid, dim3(256), 0, s, *cfg, args, out_kind);
-    } else {
-        if (output_noise)
-            hipLaunchKernelGGL((k_general<double, 2, true>), grid, dim3(256), 0, s, *cfg, args, out_kind);
-        else
-            hipLaunchKernelGGL((k_general<double, 4, false>), grid, dim3(256), 0, s, *cfg, args, out_kind);
+#define MF_GENERAL_LAUNCH(WIDE)                                                                  \
+    if (sizeof(Phys) == 4) {                                                                     \
+        if (output_noise)                                                                        \
+            hipLaunchKernelGGL((k_general<float, 2, true, WIDE>), grid, dim3(256), 0, s, *cfg,     \
+                               args, out_kind);                                                  \
+        else                                                                                     \
+            hipLaunchKernelGGL((k_general<float, 8, false, WIDE>), grid, dim3(256), 0, s, *cfg,    \
+                               args, out_kind);                                                  \
+    } else {                                                                                     \
+        if (output_noise)                                                                        \
+            hipLaunchKernelGGL((k_general<double, 2, true, WIDE>), grid, dim3(256), 0, s, *cfg,    \
+                               args, out_kind);                                                  \
+        else                                                                                     \
+            hipLaunchKernelGGL((k_general<double, 4, false, WIDE>), grid, dim3(256), 0, s, *cfg,   \
+                               args, out_kind);                                                  \
     }
+    if (cfg->wide) {
+        MF_GENERAL_LAUNCH(true)
+    } else {
+        MF_GENERAL_LAUNCH(false)
+    }
+#undef MF_GENERAL_LAUNCH
     return check_launch("general read");
 }
 
@@ -422,7 +451,7 @@ int mf_device_identity(int device, mf_identity *out) {
 
 int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
                    const float *scale, uint8_t *q, float *xscale, void *stream) {
-    int status = check_config(cfg);
+    int status = check_narrow(cfg);
     if (status) return status;
     if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k)
         return fail(MF_E_INVALID, "invalid input-tile arguments");
@@ -445,7 +474,7 @@ static i64 lcm4(i64 gr) { return gr % 4 == 0 ? gr : (gr % 2 == 0 ? 2 * gr : 4 * 
 int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
                        int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *q,
                        float *xscale, uint32_t *status, void *stream) {
-    int status_code = check_config(cfg);
+    int status_code = check_narrow(cfg);
     if (status_code) return status_code;
     if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k || gr < 1 || gc < 1)
         return fail(MF_E_INVALID, "invalid input quantization arguments");
@@ -509,7 +538,7 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
 int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
                         int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *packed,
                         uint8_t *packed_t, float *wscale, uint32_t *status, void *stream) {
-    int status_code = check_config(cfg);
+    int status_code = check_narrow(cfg);
     if (status_code) return status_code;
     if (!b || !scale || !packed || !wscale || k < 1 || o < 1 || ld < o || gr < 1 || gc < 1)
         return fail(MF_E_INVALID, "invalid weight quantization arguments");
@@ -572,7 +601,7 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
 
 int mf_transpose_packed(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p,
                         uint8_t *packed_t, void *stream) {
-    int status = check_config(cfg);
+    int status = check_narrow(cfg);
     if (status) return status;
     if (!packed || !packed_t || m < 1 || p < 1) return fail(MF_E_INVALID, "invalid transpose arguments");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -583,7 +612,7 @@ int mf_transpose_packed(const mf_config *cfg, const uint8_t *packed, int64_t m, 
 
 int mf_restore(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p, int64_t begin,
                int64_t end, uint32_t seed, uint64_t event, void *g, void *stream) {
-    int status = check_config(cfg);
+    int status = check_narrow(cfg);
     if (status) return status;
     if (!packed || !g || m < 1 || p < 1 || begin < 0 || end <= begin || end > p)
         return fail(MF_E_INVALID, "invalid restore arguments");
@@ -591,10 +620,10 @@ int mf_restore(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p
     const i64 total = i64(planes) * m * (end - begin) * cfg->n_w * cfg->rows * cfg->cols;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (cfg->precise)
-        hipLaunchKernelGGL(k_restore<double>, dim3(grid_for(total)), dim3(256), 0, s, *cfg, packed, m,
+        hipLaunchKernelGGL((k_restore<double, u8>), dim3(grid_for(total)), dim3(256), 0, s, *cfg, packed, m,
                            p, begin, end - begin, seed, event, planes, static_cast<double *>(g));
     else
-        hipLaunchKernelGGL(k_restore<float>, dim3(grid_for(total)), dim3(256), 0, s, *cfg, packed, m,
+        hipLaunchKernelGGL((k_restore<float, u8>), dim3(grid_for(total)), dim3(256), 0, s, *cfg, packed, m,
                            p, begin, end - begin, seed, event, planes, static_cast<float *>(g));
     return check_launch("restore");
 }
@@ -602,7 +631,7 @@ int mf_restore(const mf_config *cfg, const uint8_t *packed, int64_t m, int64_t p
 int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m, const uint8_t *packed,
                int64_t p, int64_t begin, int64_t end, const void *g, uint32_t seed,
                uint64_t event, float *totals, int32_t *codes, void *stream) {
-    int status = check_config(cfg);
+    int status = check_narrow(cfg);
     if (status) return status;
     if (!q || !packed || !totals || n < 1 || m < 1 || p < 1 || begin < 0 || end <= begin || end > p)
         return fail(MF_E_INVALID, "invalid partial arguments");
@@ -686,7 +715,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
           const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo, void *workspace,
           int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream) {
-    const int valid = check_config(cfg);
+    const int valid = check_narrow(cfg);
     if (valid) return valid;
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
         ldo < p * cfg->cols)
@@ -805,7 +834,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
 int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
                  const uint8_t *packed_t, int64_t p, const float *g, uint32_t seed, uint64_t event,
                  float *totals, void *workspace, int64_t workspace_bytes, void *stream) {
-    const int valid = check_config(cfg);
+    const int valid = check_narrow(cfg);
     if (valid) return valid;
     if (!q || !packed_t || !totals || !workspace || n < 1 || m < 1 || p < 1)
         return fail(MF_E_INVALID, "invalid totals arguments");
@@ -826,7 +855,7 @@ int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
 int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,
                   const float *xscale, const float *wscale, int64_t ldws, int64_t col0, double *out,
                   int64_t ldo, void *stream) {
-    const int valid = check_config(cfg);
+    const int valid = check_narrow(cfg);
     if (valid) return valid;
     const i64 wc = width * cfg->cols;
     if (!totals || !xscale || !wscale || !out || n < 1 || G < 1 || width < 1 || col0 < 0 ||
@@ -836,6 +865,186 @@ int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t 
     hipLaunchKernelGGL(k_stable_sum, dim3(grid_for(n * wc)), dim3(256), 0, s, totals, n, G, wc,
                        xscale, wscale, ldws, col0, out, ldo, level_power(G), level_power(G / 4));
     return check_launch("stable sum");
+}
+
+// ---- wide configurations (u32 codes, FP64 scales and outputs) -------------
+int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k,
+                            int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                            uint32_t *q, double *xscale, uint32_t *status, void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!x || !work || !scale || !q || !xscale || n < 1 || k < 1 || ld < k || gr < 1 || gc < 1)
+        return fail(MF_E_INVALID, "invalid input quantization arguments");
+    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (k + R - 1) / R, kp = m * R;
+    gr = gr < n ? gr : n;
+    gc = gc < k ? gc : k;
+    const i64 nrg = (n + gr - 1) / gr, ncg = (k + gc - 1) / gc;
+    const int bits = cfg->activation_bits;
+    const double upper = double((i64(1) << (bits - 1)) - 1);
+    const double lower = cfg->bw_e ? -double(i64(1) << (bits - 1)) : -upper;
+    const u64 mask = bits == 64 ? ~u64(0) : (u64(1) << bits) - 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(2 * nrg * ncg)), dim3(256), 0, s,
+                       reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
+    hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(n * k)), dim3(256), 0, s, x, n, k, ld, gr, gc,
+                       ncg, work, status, u32(MF_STATUS_INPUT));
+    hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
+                       nrg * ncg, bits, cfg->bw_e, upper, scale);
+    hipLaunchKernelGGL(k_input_codes_f64, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
+                       scale, gr, gc, ncg, 0, lower, upper, mask, q);
+    hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
+                       m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
+    return check_launch("wide input quantization");
+}
+
+int mf_input_tiles_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k, int64_t ld,
+                        const double *scale, uint32_t *q, double *xscale, void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k)
+        return fail(MF_E_INVALID, "invalid input-tile arguments");
+    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (k + R - 1) / R, kp = m * R;
+    const int bits = cfg->activation_bits;
+    const double upper = double((i64(1) << (bits - 1)) - 1);
+    const double lower = cfg->bw_e ? -double(i64(1) << (bits - 1)) : -upper;
+    const u64 mask = (u64(1) << bits) - 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_input_codes_f64, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
+                       scale, i64(1), i64(1), k, 1, lower, upper, mask, q);
+    hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
+                       m * Gr, R, P, Gr, scale, i64(1), i64(1), k, 1, xscale);
+    return check_launch("wide input tiles");
+}
+
+int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, int64_t o,
+                             int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                             int64_t *packed, uint32_t *packed32, double *wscale, uint32_t *status,
+                             void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!b || !work || !scale || !packed || !packed32 || !wscale || k < 1 || o < 1 || ld < o ||
+        gr < 1 || gc < 1)
+        return fail(MF_E_INVALID, "invalid weight quantization arguments");
+    const int R = cfg->rows, C = cfg->cols, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (k + R - 1) / R, p = (o + C - 1) / C, kp = m * R, op = p * C;
+    gr = gr < k ? gr : k;
+    gc = gc < o ? gc : o;
+    const i64 nrg = (k + gr - 1) / gr, ncg = (o + gc - 1) / gc;
+    const int bits = cfg->weight_bits;
+    const bool is_signed = cfg->weight_signed != 0;
+    const double upper = double((i64(1) << (bits - (is_signed ? 1 : 0))) - 1);
+    const double lower = cfg->bw_e ? -double(i64(1) << (bits - 1)) : (is_signed ? -upper : 0.0);
+    const u64 mask = (u64(1) << bits) - 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(2 * nrg * ncg)), dim3(256), 0, s,
+                       reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
+    hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(k * o)), dim3(256), 0, s, b, k, o, ld, gr, gc,
+                       ncg, work, status, u32(MF_STATUS_WEIGHT));
+    hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
+                       nrg * ncg, bits, cfg->bw_e, upper, scale);
+    hipLaunchKernelGGL(k_weight_codes_f64, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o, ld, R,
+                       C, m, p, scale, gr, gc, ncg, lower, upper, mask, packed, packed32);
+    hipLaunchKernelGGL(k_weight_scales_f64, dim3(grid_for(m * Gr * op)), dim3(256), 0, s, k, o,
+                       m * Gr, op, R, P, Gr, scale, gr, gc, ncg, wscale);
+    return check_launch("wide weight quantization");
+}
+
+int mf_restore_wide(const mf_config *cfg, const uint32_t *packed, int64_t m, int64_t p,
+                    int64_t begin, int64_t end, uint32_t seed, uint64_t event, void *g,
+                    void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!packed || !g || m < 1 || p < 1 || begin < 0 || end <= begin || end > p)
+        return fail(MF_E_INVALID, "invalid restore arguments");
+    const int planes = restore_planes(cfg);
+    const i64 total = i64(planes) * m * (end - begin) * cfg->n_w * cfg->rows * cfg->cols;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (cfg->precise)
+        hipLaunchKernelGGL((k_restore<double, u32>), dim3(grid_for(total)), dim3(256), 0, s, *cfg,
+                           packed, m, p, begin, end - begin, seed, event, planes,
+                           static_cast<double *>(g));
+    else
+        hipLaunchKernelGGL((k_restore<float, u32>), dim3(grid_for(total)), dim3(256), 0, s, *cfg,
+                           packed, m, p, begin, end - begin, seed, event, planes,
+                           static_cast<float *>(g));
+    return check_launch("wide restore");
+}
+
+int mf_partial_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t m,
+                    const uint32_t *packed, int64_t p, int64_t begin, int64_t end, const void *g,
+                    uint32_t seed, uint64_t event, double *totals, int32_t *codes, void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!q || !packed || !totals || n < 1 || m < 1 || p < 1 || begin < 0 || end <= begin || end > p)
+        return fail(MF_E_INVALID, "invalid partial arguments");
+    if (!g && needs_conductances(cfg))
+        return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
+    GeneralArgs args{};
+    args.q = q;
+    args.packed = packed;
+    args.g = g;
+    args.out = totals;
+    args.codes = codes;
+    args.n = n;
+    args.m = m;
+    args.p = p;
+    args.begin = begin;
+    args.width = end - begin;
+    args.seed = seed;
+    args.event = event;
+    args.planes = g ? restore_planes(cfg) : 1;
+    const i64 G = m * cfg->reads;
+    args.lp_cascade = level_power(G);
+    args.lp_interleaved = level_power(G / 4);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return cfg->precise ? launch_general<double>(cfg, args, OUT_TOTALS, s)
+                        : launch_general<float>(cfg, args, OUT_TOTALS, s);
+}
+
+int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, int64_t n, int64_t m,
+               const uint32_t *packed, const double *wscale, int64_t p, const void *g,
+               uint32_t seed, uint64_t event, double *out, int64_t ldo, uint32_t *status,
+               void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
+        ldo < p * cfg->cols)
+        return fail(MF_E_INVALID, "invalid mm arguments");
+    if (!g && needs_conductances(cfg))
+        return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
+    GeneralArgs args{};
+    args.q = q;
+    args.packed = packed;
+    args.g = g;
+    args.xscale = xscale;
+    args.wscale = wscale;
+    args.out = out;
+    args.status = status;
+    args.n = n;
+    args.m = m;
+    args.p = p;
+    args.begin = 0;
+    args.width = p;
+    args.ldo = ldo;
+    args.ldws = p * cfg->cols;
+    args.seed = seed;
+    args.event = event;
+    args.planes = g ? restore_planes(cfg) : 1;
+    const i64 G = m * cfg->reads;
+    args.lp_cascade = level_power(G);
+    args.lp_interleaved = level_power(G / 4);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+    if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+    const int launched = cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
+                                      : launch_general<float>(cfg, args, OUT_FUSED, s);
+    if (timing.first) {
+        hipEventRecord(timing.second, s);
+        g_profile.pending.push_back(timing);
+    }
+    return launched;
 }
 
 int mf_profile_kernels(int32_t enable) {
@@ -871,9 +1080,9 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     if (kernel_id == 1)
         e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_ideal<2, 1>));
     else if (cfg->precise)
-        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<double, 4, false>));
+        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<double, 4, false, false>));
     else
-        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<float, 8, false>));
+        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<float, 8, false, false>));
     if (e != hipSuccess) return fail(MF_E_HIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
     memset(out, 0, sizeof(*out));
     out->threads = 256;
@@ -882,7 +1091,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     out->local_bytes = int32_t(attr.localSizeBytes);
     int blocks = 0;
     const void *fn = kernel_id == 1 ? reinterpret_cast<const void *>(&k_ideal<2, 1>)
-                                    : reinterpret_cast<const void *>(&k_general<float, 8, false>);
+                                    : reinterpret_cast<const void *>(&k_general<float, 8, false, false>);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) == hipSuccess)
         out->max_blocks_per_cu = blocks;
     if (out->max_blocks_per_cu < 1 && blocks == 0) return fail(MF_E_RESOURCE, "zero resident blocks");

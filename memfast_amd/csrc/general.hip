@@ -10,9 +10,14 @@
 // (float(T) * xs[n,g]) * ws[g,c] over g in torch's CPU `sum` order.
 //
 // Block: 8 vectors x 32 columns, one thread per output.  Per 32-row chunk the
-// block stages voltages (all input slices) and conductances (a group of
-// weight slices) in LDS.  Bound: VALU FMAs, K*A*W per output.
+// block stages voltages (up to 8 input slices at a time) and conductances (a
+// group of weight slices) in LDS.  Bound: VALU FMAs, K*A*W per output.
+//
+// WIDE (precisions above 8 bits or BFP, memfast/config.py `wide`): 32-bit
+// codes, FP64 scales, and the epilogue of memfast/simulator.py:578-585:
+// restore_scales (FP64 frexp/ldexp) summed over reads in torch's FP64 order.
 #include <cfloat>
+#include <type_traits>
 
 #include "mf_kernels.h"
 
@@ -34,7 +39,7 @@ __device__ __forceinline__ Phys adc_count(const mf_config &cfg, Phys current, in
 template <>
 __device__ __forceinline__ float adc_count<float>(const mf_config &cfg, float current, int a,
                                                   int w) {
-    float z = current * float(cfg.in_mask[a] * cfg.w_mask[w]);
+    float z = current * float(i64(cfg.in_mask[a]) * cfg.w_mask[w]);
     z = z * cfg.f_inv_unit;
     if (cfg.has_nonlinear) z = z / (1.0f + fabsf(cfg.f_alpha_over_max[w] * z));
     const float top = float(cfg.adc_max[w]);
@@ -58,21 +63,30 @@ __device__ __forceinline__ double adc_count<double>(const mf_config &cfg, double
 // Column class for torch's sum over reads: the reference sums chunks of two
 // tiles ([N, G, width*C] tensors); columns inside whole 4-row vector groups of
 // a chunk use the cascade, the rest the interleaved cascade.
+// FP64 sums interleave the columns beyond 16 * floor(width*C / 16).
+template <bool WIDE>
 __device__ __forceinline__ bool interleaved_column(i64 col, int C, i64 p) {
     const i64 t = col / C;
     const i64 first = (t / 2) * 2;
     const i64 chunk_width = (p - first) < 2 ? (p - first) : 2;
     const i64 wc = chunk_width * C;
     const i64 pos = col - first * C;
-    const i64 span = wc >= 8 ? 32 : 4;
+    const i64 span = WIDE ? 16 : (wc >= 8 ? 32 : 4);
     return pos >= (wc / span) * span;
 }
 
-template <typename Phys, int WG, bool OUTPUT_NOISE>
+template <typename Phys, int WG, bool OUTPUT_NOISE, bool WIDE>
 __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const GeneralArgs args,
                                                  int out_kind) {
+    typedef typename std::conditional<WIDE, u32, u8>::type Code;
+    typedef typename std::conditional<WIDE, double, float>::type Out;
     __shared__ Phys volt[GMAX_A][GV][GROWS];
     __shared__ Phys cond[WG][GROWS][GC + 1];
+    const Code *q_codes = static_cast<const Code *>(args.q);
+    const Code *packed = static_cast<const Code *>(args.packed);
+    const Out *xscale = static_cast<const Out *>(args.xscale);
+    const Out *wscale = static_cast<const Out *>(args.wscale);
+    Out *out = static_cast<Out *>(args.out);
 
     const int R = cfg.rows, C = cfg.cols, P = cfg.read_rows, Gr = cfg.reads;
     const int A = cfg.n_in, W = cfg.n_w;
@@ -91,12 +105,12 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
     const Phys low = low_of<Phys>(cfg);
     const Phys volt_level = sizeof(Phys) == 8 ? Phys(cfg.d_voltage) : Phys(cfg.f_voltage);
 
-    Cascade<float> cascade;
-    Interleaved<float> interleaved;
+    Cascade<Out> cascade;
+    Interleaved<Out> interleaved;
     cascade.reset();
     interleaved.reset();
-    const bool use_interleaved =
-        live && out_kind == OUT_FUSED && interleaved_column(args.begin * C + col, C, args.p);
+    const bool use_interleaved = live && out_kind == OUT_FUSED &&
+                                 interleaved_column<WIDE>(args.begin * C + col, C, args.p);
 
     for (i64 g = 0; g < G; ++g) {
         const i64 i = g / Gr;
@@ -104,6 +118,8 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
         const int row0 = j * P;
         const int len = (R - row0) < P ? (R - row0) : P;
         i64 total = 0;
+        // Input slices in chunks of GMAX_A (more than 8 only with wide codes).
+        for (int a0 = 0; a0 < A; a0 += GMAX_A)
         for (int w0 = 0; w0 < W; w0 += WG) {
             Phys cur[GMAX_A][WG];
             Phys mean[OUTPUT_NOISE ? GMAX_A : 1][WG];
@@ -118,9 +134,11 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
             for (int ch = 0; ch < len; ch += GROWS) {
                 const int clen = (len - ch) < GROWS ? (len - ch) : GROWS;
                 __syncthreads();
-                // Stage voltages V_a[n, r] for all input slices.
-                for (int e = threadIdx.x; e < A * GV * GROWS; e += blockDim.x) {
-                    const int a = e / (GV * GROWS);
+                // Stage voltages V_a[n, r] for input slices a0 .. a0 + GMAX_A - 1.
+                const int a_count = (A - a0) < GMAX_A ? (A - a0) : GMAX_A;
+                for (int e = threadIdx.x; e < a_count * GV * GROWS; e += blockDim.x) {
+                    const int al = e / (GV * GROWS);
+                    const int a = a0 + al;
                     const int v = (e / GROWS) % GV;
                     const int rr = e % GROWS;
                     const i64 nn = vec0 + v;
@@ -128,7 +146,8 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
                     if (nn < args.n && rr < clen) {
                         const int r = row0 + ch + rr;
                         const int mask = cfg.in_mask[a];
-                        const int digit = (int(args.q[nn * kp + i * R + r]) >> cfg.in_shift[a]) & mask;
+                        const int digit =
+                            int((u32(q_codes[nn * kp + i * R + r]) >> cfg.in_shift[a]) & u32(mask));
                         value = Phys(digit) / Phys(mask) * volt_level;
                         if (cfg.has_vnoise) {
                             const u64 address = u64(((nn * m + i) * A + a) * R + r);
@@ -136,10 +155,12 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
                             value = value * Phys(1.0f + cfg.f_vnoise * z);
                         }
                     }
-                    volt[a][v][rr] = value;
+                    volt[al][v][rr] = value;
                 }
-                for (int plane = 0; plane < args.planes; ++plane) {
-                    if (plane) __syncthreads();
+                const int plane_lo = args.planes > 1 ? a0 : 0;
+                const int plane_hi = args.planes > 1 ? a0 + a_count : 1;
+                for (int plane = plane_lo; plane < plane_hi; ++plane) {
+                    if (plane != plane_lo) __syncthreads();
                     // Stage conductances G_w[r, c] for this group of weight slices.
                     for (int e = threadIdx.x; e < WG * GROWS * GC; e += blockDim.x) {
                         const int wl = e / (GROWS * GC);
@@ -159,17 +180,18 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
                                 value = load_g<Phys>(args.g, idx);
                             } else {
                                 const i64 t = args.begin + t_rel;
-                                const u8 code = args.packed[((i * args.p + t) * R + r) * C + c];
+                                const u32 code = packed[((i * args.p + t) * R + r) * C + c];
                                 const int mask = cfg.w_mask[w];
-                                const int digit = (int(code) >> cfg.w_shift[w]) & mask;
+                                const int digit = int((code >> cfg.w_shift[w]) & u32(mask));
                                 value = nominal_level<Phys>(cfg, digit, mask) * drift_of<Phys>(cfg);
                             }
                         }
                         cond[wl][rr][ccol] = value;
                     }
                     __syncthreads();
-                    const int a_lo = args.planes > 1 ? plane : 0;
-                    const int a_hi = args.planes > 1 ? plane + 1 : A;
+                    // slice_pair planes: plane p holds input slice p's conductances.
+                    const int a_lo = args.planes > 1 ? plane - a0 : 0;
+                    const int a_hi = args.planes > 1 ? plane - a0 + 1 : a_count;
                     for (int rr = 0; rr < clen; ++rr) {
 #pragma unroll
                         for (int wl = 0; wl < WG; ++wl) {
@@ -192,20 +214,21 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
             // ADC and signed shift-add for this group of weight slices.
             if (live) {
 #pragma unroll
-                for (int a = 0; a < GMAX_A; ++a) {
+                for (int al = 0; al < GMAX_A; ++al) {
+                    const int a = a0 + al;
                     if (a >= A) continue;
 #pragma unroll
                     for (int wl = 0; wl < WG; ++wl) {
                         const int w = w0 + wl;
                         if (w >= W) continue;
-                        Phys current = cur[a][wl];
+                        Phys current = cur[al][wl];
                         if (OUTPUT_NOISE) {
                             const i64 t = args.begin + tt;
                             const u64 address = u64(
                                 ((((vec * m * Gr + g) * args.p + t) * A + a) * W + w) * C + cc);
                             const float z = normal(address, read_seed, 60u, cfg.f_two_pi);
-                            const Phys mu = mean[a][wl] * Phys(cfg.f_out_mean);
-                            const Phys sd = sqrt(var[a][wl] * Phys(cfg.f_out_var));
+                            const Phys mu = mean[al][wl] * Phys(cfg.f_out_mean);
+                            const Phys sd = sqrt(var[al][wl] * Phys(cfg.f_out_var));
                             current = current + (mu + sd * Phys(z));
                         }
                         const Phys code = adc_count<Phys>(cfg, current, a, w);
@@ -220,28 +243,40 @@ __global__ __launch_bounds__(256) void k_general(const mf_config cfg, const Gene
         }
         if (!live) continue;
         if (out_kind == OUT_TOTALS) {
-            args.out[((vec * G + g) * args.width + tt) * C + cc] = float(total);
+            out[((vec * G + g) * args.width + tt) * C + cc] = Out(total);
         } else {
             const i64 o = args.begin * C + col;
-            float value = float(total) * args.xscale[vec * G + g];
-            value = value * args.wscale[g * args.ldws + o];
+            Out value;
+            if (WIDE) {
+                value = Out(restore_f64(double(total), double(xscale[vec * G + g]),
+                                        double(wscale[g * args.ldws + o])));
+            } else {
+                value = Out(total) * xscale[vec * G + g];
+                value = value * wscale[g * args.ldws + o];
+            }
             if (use_interleaved) interleaved.push(value, int(G), args.lp_interleaved);
             else cascade.push(value, args.lp_cascade);
         }
     }
     if (live && out_kind == OUT_FUSED) {
         const i64 o = args.begin * C + col;
-        const float value = use_interleaved ? interleaved.finish(int(G)) : cascade.finish();
-        args.out[vec * args.ldo + o] = value;
-        if (!(fabsf(value) <= FLT_MAX) && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
+        const Out value = use_interleaved ? interleaved.finish(int(G)) : cascade.finish();
+        out[vec * args.ldo + o] = value;
+        if (!(fabs(double(value)) <= (WIDE ? DBL_MAX : double(FLT_MAX))) && args.status)
+            atomicOr(args.status, u32(MF_STATUS_OUTPUT));
     }
 }
 
-#define MF_GENERAL_INST(PHYS, WG, OUT)                                                       \
-    template __global__ void k_general<PHYS, WG, OUT>(const mf_config, const GeneralArgs, int);
-MF_GENERAL_INST(float, 8, false)
-MF_GENERAL_INST(float, 2, true)
-MF_GENERAL_INST(double, 4, false)
-MF_GENERAL_INST(double, 2, true)
+#define MF_GENERAL_INST(PHYS, WG, OUT, WIDE)                                                  \
+    template __global__ void k_general<PHYS, WG, OUT, WIDE>(const mf_config, const GeneralArgs, \
+                                                            int);
+MF_GENERAL_INST(float, 8, false, false)
+MF_GENERAL_INST(float, 2, true, false)
+MF_GENERAL_INST(double, 4, false, false)
+MF_GENERAL_INST(double, 2, true, false)
+MF_GENERAL_INST(float, 8, false, true)
+MF_GENERAL_INST(float, 2, true, true)
+MF_GENERAL_INST(double, 4, false, true)
+MF_GENERAL_INST(double, 2, true, true)
 
 }  // namespace mf

@@ -46,6 +46,33 @@ __host__ __device__ __forceinline__ u64 event_seed(u32 seed, u64 event) {
 }
 
 // ---------------------------------------------------------------------------
+// Overflow-safe FP64 scale restore of memfast/simulator.py:57-66
+// (restore_scales): frexp mantissas multiplied as (vm*xm)*wm, the exponent sum
+// applied with torch.ldexp, which multiplies by 2^e held in a double.
+// ---------------------------------------------------------------------------
+// x * 2^e with 2^e formed as a double (0 below 2^-1074, inf above 2^1023).
+__device__ __forceinline__ double times_pow2(double x, int e) {
+    double scale;
+    if (e > 1023) scale = __longlong_as_double(0x7FF0000000000000LL);
+    else if (e >= -1022) scale = __longlong_as_double(i64(e + 1023) << 52);
+    else if (e >= -1074) scale = __longlong_as_double(1LL << (e + 1074));
+    else scale = 0.0;
+    return x * scale;
+}
+
+__device__ __forceinline__ double restore_f64(double value, double xs, double ws) {
+    int ve, xe, we;
+    const double vm = frexp(value, &ve);
+    const double xm = frexp(xs, &xe);
+    const double wm = frexp(ws, &we);
+    const double mantissa = (vm * xm) * wm;
+    if (mantissa == 0.0) return 0.0;
+    const int exponent = ve + xe + we;
+    const int first = exponent < -1022 ? -1022 : (exponent > 1023 ? 1023 : exponent);
+    return times_pow2(times_pow2(mantissa, first), exponent - first);
+}
+
+// ---------------------------------------------------------------------------
 // torch CPU reduction order of `sum` over the read dimension
 // (aten/src/ATen/native/cpu/SumKernel.cpp as shipped in torch 2.x):
 // a 4-level cascade whose level step is 2^lp; each full block of 2^lp values is

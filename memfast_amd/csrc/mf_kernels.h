@@ -9,13 +9,15 @@ namespace mf {
 // ---- general read (general.hip) -------------------------------------------
 enum { OUT_FUSED = 0, OUT_TOTALS = 1 };
 
+// Code and scale types follow the configuration: u8 codes with FP32 scales
+// and output, or (wide) u32 codes with FP64 scales and output.
 struct GeneralArgs {
-    const u8 *q;          // [n, m*R] input codes
-    const u8 *packed;     // [m, p, R, C] (used when g == nullptr)
+    const void *q;        // [n, m*R] input codes
+    const void *packed;   // [m, p, R, C] (used when g == nullptr)
     const void *g;        // [planes][m][width][W][R][C] or nullptr
-    const float *xscale;  // [n, G]
-    const float *wscale;  // [G, ldws]
-    float *out;           // fused: [n, ldo]; totals: [n, G, width, C]
+    const void *xscale;   // [n, G]
+    const void *wscale;   // [G, ldws]
+    void *out;            // fused: [n, ldo]; totals: [n, G, width, C]
     int32_t *codes;       // optional [n, G, A, W, width*C]
     u32 *status;          // optional: MF_STATUS_OUTPUT for a non-finite fused output
     i64 n, m, p, begin, width, ldo, ldws;
@@ -25,7 +27,7 @@ struct GeneralArgs {
     int lp_cascade, lp_interleaved;   // level powers of torch's cascade
 };
 
-template <typename Phys, int WG, bool OUTPUT_NOISE>
+template <typename Phys, int WG, bool OUTPUT_NOISE, bool WIDE>
 __global__ void k_general(const mf_config cfg, const GeneralArgs args, int out_kind);
 
 // ---- ideal MFMA read (ideal_mfma.hip) -------------------------------------
@@ -93,8 +95,8 @@ __global__ void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int P,
                              uint64_t *out);
 
 // ---- conductances (restore.hip) -------------------------------------------
-template <typename Phys>
-__global__ void k_restore(const mf_config cfg, const u8 *packed, i64 m, i64 p, i64 begin,
+template <typename Phys, typename Code>
+__global__ void k_restore(const mf_config cfg, const Code *packed, i64 m, i64 p, i64 begin,
                           i64 width, u32 seed, u64 event, int planes, Phys *g);
 
 // ---- noisy-device MFMA read (noisy_mfma.hip) -------------------------------
@@ -166,5 +168,21 @@ __global__ void k_weight_codes(const float *b, i64 k, i64 o, i64 ld, int R, int 
 __global__ void k_weight_scales(i64 k, i64 o, i64 groups, i64 op, int R, int P, int Gr,
                                 const float *scale, i64 gr, i64 gc, i64 ncg, float *wscale);
 __global__ void k_transpose_packed(const u8 *packed, int R, int C, i64 m, i64 p, u8 *packed_t);
+__global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
+                                i64 ncg, u64 *work, u32 *status, u32 flag);
+__global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
+                                  double *scale);
+__global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
+                                  const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
+                                  double lower, double upper, u64 mask, u32 *q);
+__global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+                                   i64 p, const double *scale, i64 gr, i64 gc, i64 ncg,
+                                   double lower, double upper, u64 mask, i64 *packed,
+                                   u32 *packed32);
+__global__ void k_input_scales_f64(i64 n, i64 k, i64 groups, int R, int P, int Gr,
+                                   const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
+                                   double *xscale);
+__global__ void k_weight_scales_f64(i64 k, i64 o, i64 groups, i64 op, int R, int P, int Gr,
+                                    const double *scale, i64 gr, i64 gc, i64 ncg, double *wscale);
 
 }  // namespace mf

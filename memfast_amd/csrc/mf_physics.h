@@ -47,10 +47,10 @@ __device__ __forceinline__ double high_of<double>(const mf_config &cfg) { return
 
 // Programmed + (shared) read conductance of one cell.
 template <typename Phys>
-__device__ __forceinline__ Phys cell_conductance(const mf_config &cfg, u8 code, int w, u64 cell,
+__device__ __forceinline__ Phys cell_conductance(const mf_config &cfg, u32 code, int w, u64 cell,
                                                  u32 seed, u64 read_seed) {
     const int mask = cfg.w_mask[w];
-    const int digit = (int(code) >> cfg.w_shift[w]) & mask;
+    const int digit = int((code >> cfg.w_shift[w]) & u32(mask));
     Phys raw = nominal_level<Phys>(cfg, digit, mask);
     if (cfg.has_write) raw = raw * Phys(expf(cfg.f_write * normal(cell, seed, 10u, cfg.f_two_pi)));
     raw = raw * drift_of<Phys>(cfg);

@@ -434,3 +434,140 @@ __global__ void k_transpose_packed(const u8 *packed, int R, int C, i64 m, i64 p,
 }
 
 }  // namespace mf
+
+// ---------------------------------------------------------------------------
+// Wide configurations (precision above 8 bits or BFP): FP64 arithmetic and
+// 32-bit codes, as memfast/quantization.py:9-44 computes in FP64 there.
+// ---------------------------------------------------------------------------
+namespace mf {
+
+// Group max |x| of FP64 values via atomicMax on the bit pattern.
+__global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
+                                i64 ncg, u64 *work, u32 *status, u32 flag) {
+    const i64 total = rows * cols;
+    bool finite = true;
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += i64(gridDim.x) * blockDim.x) {
+        const i64 r = i / cols, c = i - r * cols;
+        const double v = fabs(x[r * ld + c]);
+        finite = finite && v <= DBL_MAX;
+        const u64 bits = u64(__double_as_longlong(v));
+        if (bits) atomicMax(reinterpret_cast<unsigned long long *>(&work[(r / gr) * ncg + c / gc]),
+                            static_cast<unsigned long long>(bits));
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
+// floor() of the correctly rounded log2(x) for normal x > 0: ilogb(x), or one
+// more when log2(x) lies within half a unit in the last place below the next
+// integer (so that it rounds up to it).
+__device__ __forceinline__ int floor_log2_rounded(double x) {
+    const int e = ilogb(x);
+    const double top = ldexp(1.0, e + 1);
+    const double distance = ((top - x) / top) * 1.4426950408889634;   // ~ (e+1) - log2(x)
+    const double target = double(e + 1);
+    const double gap = target - nextafter(target, -INFINITY);
+    return distance < 0.5 * gap ? e + 1 : e;
+}
+
+// INT: scale = (max > 0 ? max : 1) / upper, at least the smallest FP64
+// subnormal.  BFP (bw_e > 0): e = clamp(floor(log2(max(max, DBL_MIN))),
+// 1 - L, L) with L = 2^(bw_e-1) - 1, scale = 2^(e + 2 - bits).
+__global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
+                                  double *scale) {
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < groups;
+         i += i64(gridDim.x) * blockDim.x) {
+        const double peak = __longlong_as_double(static_cast<long long>(work[i]));
+        double s;
+        if (bw_e) {
+            const int limit = (1 << (bw_e - 1)) - 1;
+            int e = floor_log2_rounded(peak > DBL_MIN ? peak : DBL_MIN);
+            e = e < 1 - limit ? 1 - limit : (e > limit ? limit : e);
+            s = ldexp(1.0, e + 2 - bits);
+        } else {
+            s = (peak > 0.0 ? peak : 1.0) / upper;
+            const double tiny = __longlong_as_double(1LL);
+            s = s < tiny ? tiny : s;
+        }
+        scale[i] = s;
+    }
+}
+
+__device__ __forceinline__ u32 quantize_code_f64(double x, double s, double lower, double upper,
+                                                 u64 mask) {
+    double c = rint(x / s);
+    c = c < lower ? lower : c;
+    c = c > upper ? upper : c;
+    return u32(u64(i64(c)) & mask);
+}
+
+// q [n, kp] u32 codes; `scale` is the group grid, or a [k] row when fixed.
+__global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
+                                  const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
+                                  double lower, double upper, u64 mask, u32 *q) {
+    const i64 total = n * kp;
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += i64(gridDim.x) * blockDim.x) {
+        const i64 row = i / kp, col = i - row * kp;
+        u32 code = 0;
+        if (col < k) {
+            const double s = fixed ? scale[col] : scale[(row / gr) * ncg + col / gc];
+            code = quantize_code_f64(x[row * ld + col], s, lower, upper, mask);
+        }
+        q[i] = code;
+    }
+}
+
+// packed [m, p, R, C] as int64 (the checkpoint layout) and u32 (kernel copy).
+__global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+                                   i64 p, const double *scale, i64 gr, i64 gc, i64 ncg,
+                                   double lower, double upper, u64 mask, i64 *packed,
+                                   u32 *packed32) {
+    const i64 kp = m * R, op = p * C;
+    const i64 total = kp * op;
+    for (i64 idx = i64(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+         idx += i64(gridDim.x) * blockDim.x) {
+        // idx enumerates the packed layout, so both outputs are written in order.
+        const i64 c = idx % C;
+        const i64 r = (idx / C) % R;
+        const i64 t = (idx / (i64(C) * R)) % p;
+        const i64 i = idx / (i64(C) * R * p);
+        const i64 row = i * R + r, col = t * C + c;
+        u32 code = 0;
+        if (row < k && col < o)
+            code = quantize_code_f64(b[row * ld + col], scale[(row / gr) * ncg + col / gc], lower,
+                                     upper, mask);
+        packed[idx] = i64(code);
+        packed32[idx] = code;
+    }
+}
+
+// Per-read scales gathered at each read's first row, replicate-padded
+// (memfast/quantization.py:76-79, :104-111, :133-136), for FP64 scales.
+__global__ void k_input_scales_f64(i64 n, i64 k, i64 groups, int R, int P, int Gr,
+                                   const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
+                                   double *xscale) {
+    const i64 total = n * groups;
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += i64(gridDim.x) * blockDim.x) {
+        const i64 row = i / groups, g = i % groups;
+        i64 col = (g / Gr) * R + (g % Gr) * P;
+        col = col < k ? col : k - 1;
+        xscale[i] = fixed ? scale[col] : scale[(row / gr) * ncg + col / gc];
+    }
+}
+
+__global__ void k_weight_scales_f64(i64 k, i64 o, i64 groups, i64 op, int R, int P, int Gr,
+                                    const double *scale, i64 gr, i64 gc, i64 ncg, double *wscale) {
+    const i64 total = groups * op;
+    for (i64 idx = i64(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+         idx += i64(gridDim.x) * blockDim.x) {
+        const i64 g = idx / op, col = idx % op;
+        i64 row = (g / Gr) * R + (g % Gr) * P;
+        row = row < k ? row : k - 1;
+        const i64 cc = col < o ? col : o - 1;
+        wscale[idx] = scale[(row / gr) * ncg + cc / gc];
+    }
+}
+
+}  // namespace mf

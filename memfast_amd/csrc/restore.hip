@@ -11,8 +11,8 @@
 
 namespace mf {
 
-template <typename Phys>
-__global__ __launch_bounds__(256) void k_restore(const mf_config cfg, const u8 *packed, i64 m,
+template <typename Phys, typename Code>
+__global__ __launch_bounds__(256) void k_restore(const mf_config cfg, const Code *packed, i64 m,
                                                  i64 p, i64 begin, i64 width, u32 seed,
                                                  u64 event, int planes, Phys *g) {
     const int R = cfg.rows, C = cfg.cols, W = cfg.n_w;
@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void k_restore(const mf_config cfg, const u8 *
         const int plane = int(rest / m);
         const i64 t = begin + tt;
         const u64 cell = u64((((i * p + t) * W + w) * R + r) * C + c);
-        const u8 code = packed[((i * p + t) * R + r) * C + c];
+        const u32 code = packed[((i * p + t) * R + r) * C + c];
         Phys raw = cell_conductance<Phys>(cfg, code, w, cell, seed, read_seed);
         if (planes > 1) {
             // slice_pair: an independent read field per activation slice.
@@ -41,9 +41,13 @@ __global__ __launch_bounds__(256) void k_restore(const mf_config cfg, const u8 *
     }
 }
 
-template __global__ void k_restore<float>(const mf_config, const u8 *, i64, i64, i64, i64, u32,
-                                          u64, int, float *);
-template __global__ void k_restore<double>(const mf_config, const u8 *, i64, i64, i64, i64, u32,
-                                           u64, int, double *);
+template __global__ void k_restore<float, u8>(const mf_config, const u8 *, i64, i64, i64, i64,
+                                              u32, u64, int, float *);
+template __global__ void k_restore<double, u8>(const mf_config, const u8 *, i64, i64, i64, i64,
+                                               u32, u64, int, double *);
+template __global__ void k_restore<float, u32>(const mf_config, const u32 *, i64, i64, i64, i64,
+                                               u32, u64, int, float *);
+template __global__ void k_restore<double, u32>(const mf_config, const u32 *, i64, i64, i64, i64,
+                                                u32, u64, int, double *);
 
 }  // namespace mf

@@ -12,28 +12,6 @@
 
 namespace mf {
 
-// x * 2^e with 2^e formed as a double (0 below 2^-1074, inf above 2^1023).
-__device__ __forceinline__ double times_pow2(double x, int e) {
-    double scale;
-    if (e > 1023) scale = __longlong_as_double(0x7FF0000000000000LL);
-    else if (e >= -1022) scale = __longlong_as_double(i64(e + 1023) << 52);
-    else if (e >= -1074) scale = __longlong_as_double(1LL << (e + 1074));
-    else scale = 0.0;
-    return x * scale;
-}
-
-__device__ __forceinline__ double restore_f64(double value, double xs, double ws) {
-    int ve, xe, we;
-    const double vm = frexp(value, &ve);
-    const double xm = frexp(xs, &xe);
-    const double wm = frexp(ws, &we);
-    const double mantissa = (vm * xm) * wm;
-    if (mantissa == 0.0) return 0.0;
-    const int exponent = ve + xe + we;
-    const int first = exponent < -1022 ? -1022 : (exponent > 1023 ? 1023 : exponent);
-    return times_pow2(times_pow2(mantissa, first), exponent - first);
-}
-
 // One thread per (vector, column of the chunk): totals [n, G, width*C] (FP32,
 // integer valued), xscale [n, G], wscale [G, ldws] at columns col0 + col;
 // writes out[vec * ldo + col0 + col].

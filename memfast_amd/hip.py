@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -91,6 +91,8 @@ class MFConfig(ct.Structure):
         ("d_high", ct.c_double), ("d_low", ct.c_double), ("d_voltage", ct.c_double),
         ("d_span", ct.c_double), ("d_inv_unit", ct.c_double), ("d_drift", ct.c_double),
         ("d_alpha_over_max", ct.c_double * MAX_SLICES),
+        ("wide", ct.c_int32),
+        ("bw_e", ct.c_int32),
     ]
 
 
@@ -140,6 +142,17 @@ SIGNATURES = {
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
                       _P], ct.c_int),
     "mf_stable_sum": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P], ct.c_int),
+    "mf_quantize_inputs_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
+                                 _P], ct.c_int),
+    "mf_input_tiles_wide": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _P, _P], ct.c_int),
+    "mf_quantize_weights_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
+                                  _P, _P], ct.c_int),
+    "mf_restore_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, ct.c_uint32, ct.c_uint64, _P, _P],
+                        ct.c_int),
+    "mf_partial_wide": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
+                         _P, _P, _P], ct.c_int),
+    "mf_mm_wide": ([_CFG, _P, _P, _I64, _I64, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
+                    _I64, _P, _P], ct.c_int),
     "mf_profile_kernels": ([_I32], ct.c_int),
     "mf_profile_collect": ([ct.POINTER(_I64), ct.POINTER(ct.c_double)], ct.c_int),
     "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, ct.POINTER(_I64)], ct.c_int),
@@ -252,6 +265,8 @@ def descriptor(config):
     d.d_high, d.d_low, d.d_voltage, d.d_span = high, low, volt, high - low
     d.d_inv_unit = 1 / unit
     d.d_drift = drift
+    d.wide = int(config.wide)
+    d.bw_e = 0 if config.bw_e is None else config.bw_e
     return d
 
 
@@ -273,11 +288,15 @@ def restore_planes(config):
 
 def supported(config):
     """Raise NotImplementedError for configurations the HIP backend lacks."""
-    if config.wide:
-        raise NotImplementedError(
-            "precisions above 8 bits and BFP (64-bit codes, FP64 restore) are not "
-            "implemented on the HIP backend yet"
-        )
+    if len(config.input_layout) > MAX_SLICES or len(config.weight_layout) > MAX_SLICES:
+        raise NotImplementedError("more than 32 slices")
+
+
+def _u32(codes):
+    """Wide codes (values below 2^32) as the uint32 bit patterns the kernels read."""
+    if codes.dtype == torch.int32:
+        return codes.contiguous()
+    return codes.to(torch.int64).bitwise_and(0xFFFFFFFF).to(torch.int32).contiguous()
 
 
 # ---------------------------------------------------------------------------
@@ -306,6 +325,8 @@ def input_tiles(value, config, fixed_scale=None, *, status=None):
     """
     supported(config)
     require_device(value)
+    if config.wide:
+        return _input_tiles_wide(value, config, fixed_scale, status)
     n, k = value.shape
     if status is None and not torch.isfinite(value).all():
         raise ValueError("quantized values must be finite")
@@ -344,6 +365,46 @@ def input_tiles(value, config, fixed_scale=None, *, status=None):
     return q, xscale
 
 
+def _input_tiles_wide(value, config, fixed_scale, status):
+    """Wide input tiles: q [N, m, R] uint32 codes (int32 storage), FP64 scales [N, m*Gr]."""
+    n, k = value.shape
+    x = value.to(torch.float64).contiguous()
+    if status is None and not torch.isfinite(x).all():
+        raise ValueError("quantized values must be finite in torch.float64")
+    r = config.array_size[0]
+    m = math.ceil(k / r)
+    q = torch.empty((n, m, r), dtype=torch.int32, device=value.device)
+    xscale = torch.empty((n, m * config.reads_per_array), dtype=torch.float64, device=value.device)
+    descr = ct.byref(descriptor(config))
+    with torch.cuda.device(value.device):
+        if fixed_scale is None:
+            gr, gc = _group_dims(x.shape, config.input_quant_gran)
+            grid = (math.ceil(n / gr), math.ceil(k / gc))
+            scale = torch.empty(grid, dtype=torch.float64, device=value.device)
+            work = torch.empty(grid, dtype=torch.int64, device=value.device)
+            check(
+                library().mf_quantize_inputs_wide(
+                    descr, _ptr(x), n, k, k, gr, gc, _ptr(work), _ptr(scale), _ptr(q),
+                    _ptr(xscale), _ptr(status), _stream(value.device),
+                ),
+                "wide input quantization",
+            )
+            return q, xscale
+        if status is not None:
+            bad = torch.isfinite(x).all().logical_not().to(torch.int32) * STATUS_INPUT
+            status.bitwise_or_(bad)
+        scale = fixed_scale.to(device=value.device, dtype=torch.float64).reshape(-1).contiguous()
+        if scale.numel() != k:
+            raise ValueError("fixed input scale must have one entry per input feature")
+        check(
+            library().mf_input_tiles_wide(
+                descr, _ptr(x), n, k, k, _ptr(scale), _ptr(q), _ptr(xscale), _stream(value.device),
+            ),
+            "wide input tiles",
+        )
+    return q, xscale
+
+
 def weight_tiles(weight, config, *, transposed=True, status=None):
     """PyTorch [O,K] weights -> packed [m,p,R,C], packed_t [p*C, m*R], scales [m*Gr,p,C].
 
@@ -354,6 +415,8 @@ def weight_tiles(weight, config, *, transposed=True, status=None):
     """
     supported(config)
     require_device(weight)
+    if config.wide:
+        return _weight_tiles_wide(weight, config, status)
     o, k = weight.shape
     b = weight.detach().T.to(torch.float32).contiguous()  # [K, O]
     if status is None and not torch.isfinite(b).all():
@@ -382,6 +445,48 @@ def weight_tiles(weight, config, *, transposed=True, status=None):
             "weight quantization",
         )
     return packed, packed_t, wscale
+
+
+def _weight_tiles_wide(weight, config, status):
+    """Wide programming: packed int64 [m,p,R,C], its uint32 kernel copy, FP64 scales."""
+    o, k = weight.shape
+    b = weight.detach().T.to(torch.float64).contiguous()  # [K, O]
+    if status is None and not torch.isfinite(b).all():
+        raise ValueError("quantized values must be finite in torch.float64")
+    if not config.weight_signed and (b < 0).any():
+        raise ValueError(
+            "unsigned floating weights must be nonnegative INT values; "
+            "use map_quantized with zero_points for affine weights"
+        )
+    r, c = config.array_size
+    m, p = math.ceil(k / r), math.ceil(o / c)
+    device = b.device
+    gr, gc = _group_dims(b.shape, config.weight_quant_gran)
+    grid = (math.ceil(k / gr), math.ceil(o / gc))
+    scale = torch.empty(grid, dtype=torch.float64, device=device)
+    work = torch.empty(grid, dtype=torch.int64, device=device)
+    packed = torch.empty((m, p, r, c), dtype=torch.int64, device=device)
+    packed32 = torch.empty((m, p, r, c), dtype=torch.int32, device=device)
+    wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float64, device=device)
+    with torch.cuda.device(device):
+        check(
+            library().mf_quantize_weights_wide(
+                ct.byref(descriptor(config)), _ptr(b), k, o, o, gr, gc, _ptr(work), _ptr(scale),
+                _ptr(packed), _ptr(packed32), _ptr(wscale), _ptr(status), _stream(device),
+            ),
+            "wide weight quantization",
+        )
+    if max(config.activation_bits, config.weight_bits) <= 8:
+        packed = packed.to(torch.uint8)   # BFP at 8 bits keeps the reference's u8 buffer
+    return packed, packed32, wscale
+
+
+def kernel_codes(packed, config):
+    """The read kernels' copy of programmed codes: column-major u8 codes (MFMA
+    kernels, narrow) or uint32 codes in the packed layout (wide)."""
+    if config.wide:
+        return _u32(packed)
+    return transpose_packed(packed, config)
 
 
 def transpose_packed(packed, config):
@@ -413,13 +518,13 @@ def restore(packed, config, seed, event, begin, end):
     dtype = torch.float64 if config.precise_currents else torch.float32
     g = torch.empty((planes, m, end - begin, len(config.weight_layout), r, c), dtype=dtype,
                     device=packed.device)
-    src = packed.to(torch.uint8).contiguous()
+    wide = config.wide
+    src = _u32(packed) if wide else packed.to(torch.uint8).contiguous()
+    entry = library().mf_restore_wide if wide else library().mf_restore
     with torch.cuda.device(packed.device):
         check(
-            library().mf_restore(
-                ct.byref(descriptor(config)), _ptr(src), m, p, begin, end, seed, event, _ptr(g),
-                _stream(packed.device),
-            ),
+            entry(ct.byref(descriptor(config)), _ptr(src), m, p, begin, end, seed, event, _ptr(g),
+                  _stream(packed.device)),
             "restore",
         )
     return g
@@ -438,7 +543,9 @@ def _checked_conductance(g, config, m, width, r, c):
 
 def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance=None,
             codes=False):
-    """Integer slice totals T [N, m*Gr, end-begin, C] (FP32), as memfast/cuda.py:322-373.
+    """Integer slice totals T [N, m*Gr, end-begin, C], as memfast/cuda.py:322-373.
+
+    FP32, or FP64 for wide configurations (as the reference returns them).
 
     ``conductance`` injects a [planes, m, end-begin, W, R, C] tensor in place of
     the sampled one; ``codes=True`` also returns per-pair ADC counts
@@ -456,20 +563,22 @@ def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance
     if g is not None:
         g = _checked_conductance(g, config, m, width, r, c)
     groups = m * config.reads_per_array
-    totals = torch.empty((n, groups, width, c), dtype=torch.float32, device=q.device)
+    wide = config.wide
+    totals = torch.empty((n, groups, width, c), dtype=torch.float64 if wide else torch.float32,
+                         device=q.device)
     counts = None
     if codes:
         counts = torch.empty(
             (n, groups, len(config.input_layout), len(config.weight_layout), width * c),
             dtype=torch.int32, device=q.device,
         )
+    codes_q = _u32(q) if wide else q.contiguous()
+    codes_w = _u32(packed) if wide else packed.to(torch.uint8).contiguous()
+    entry = library().mf_partial_wide if wide else library().mf_partial
     with torch.cuda.device(q.device):
         check(
-            library().mf_partial(
-                ct.byref(descriptor(config)), _ptr(q.contiguous()), n, m,
-                _ptr(packed.to(torch.uint8).contiguous()), p, begin, end, _ptr(g), seed, event,
-                _ptr(totals), _ptr(counts), _stream(q.device),
-            ),
+            entry(ct.byref(descriptor(config)), _ptr(codes_q), n, m, _ptr(codes_w), p, begin,
+                  end, _ptr(g), seed, event, _ptr(totals), _ptr(counts), _stream(q.device)),
             "partial",
         )
     return (totals, counts) if codes else totals
@@ -477,11 +586,18 @@ def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance
 
 def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=None, out=None,
        variant=0, status=None):
-    """Fused read + scale restore: [N, p*C] FP32, summed over reads in torch's order."""
+    """Fused read + scale restore: [N, p*C] FP32, summed over reads in torch's order.
+
+    Wide configurations: ``packed_t`` is the uint32 kernel copy of the codes
+    (``kernel_codes``), scales and the output are FP64 (restore_scales).
+    """
     supported(config)
     require_device(q)
     n, m, r = q.shape
     p, c = packed.shape[1], config.array_size[1]
+    if config.wide:
+        return _mm_wide(q, xscale, packed, packed_t, wscale, config, seed, event,
+                        conductance=conductance, out=out, status=status)
     g = conductance
     kernel = mm_kernel(config, n, m, p) if g is None and packed_t is not None else 0
     if g is None and kernel == 0 and needs_conductances(config):
@@ -505,6 +621,30 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
                 _ptr(g), seed, event, _ptr(out), out.stride(0), _ptr(workspace),
                 0 if workspace is None else workspace.numel(), variant, _ptr(status),
                 _stream(q.device),
+            ),
+            "mm",
+        )
+    return out
+
+
+def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductance, out, status):
+    n, m, r = q.shape
+    p, c = packed.shape[1], config.array_size[1]
+    codes = _u32(packed) if codes is None else _u32(codes)
+    g = conductance
+    if g is None and needs_conductances(config):
+        g = restore(codes, config, seed, event, 0, p)
+    if g is not None:
+        g = _checked_conductance(g, config, m, p, r, c)
+    if out is None:
+        out = torch.empty((n, p * c), dtype=torch.float64, device=q.device)
+    with torch.cuda.device(q.device):
+        check(
+            library().mf_mm_wide(
+                ct.byref(descriptor(config)), _ptr(_u32(q)),
+                _ptr(xscale.to(torch.float64).contiguous()), n, m, _ptr(codes),
+                _ptr(wscale.to(torch.float64).contiguous()), p, _ptr(g), seed, event, _ptr(out),
+                out.stride(0), _ptr(status), _stream(q.device),
             ),
             "mm",
         )
@@ -586,7 +726,9 @@ def mm_totals(q, packed_t, config, seed, event, *, conductance=None):
 
 
 def mm_kernel(config, n, m, p, has_packed_t=True):
-    """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA (what ``mm`` launches)."""
+    """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA (what ``mm`` launches).
+
+    The kernels other than the general one read ``kernel_codes`` of the program."""
     out = ct.c_int32()
     check(library().mf_mm_kernel(ct.byref(descriptor(config)), n, m, p, int(has_packed_t),
                                  ct.byref(out)), "kernel selection")

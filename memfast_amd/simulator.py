@@ -430,10 +430,10 @@ class AnalogMatrix(nn.Module):
         return (packed.data_ptr(), packed._version, packed.device, tuple(packed.shape))
 
     def _column_codes(self):
-        """Column-major codes [p*C, m*R] for the MFMA kernel, refreshed on change."""
+        """The kernels' copy of the codes (hip.kernel_codes), refreshed on change."""
         key = self._codes_key()
         if self._kernel_codes is None or self._kernel_codes[0] != key:
-            self._kernel_codes = (key, hip.transpose_packed(self.packed, self.config))
+            self._kernel_codes = (key, hip.kernel_codes(self.packed, self.config))
         return self._kernel_codes[1]
 
     def _accepts(self, tiles):
@@ -571,12 +571,15 @@ class AnalogMatrix(nn.Module):
         """(output, finite) where ``finite`` is True when the output is known finite."""
         config = self.config
         c = config.array_size[1]
-        packed = self.packed if self.packed.dtype == torch.uint8 else self.packed.to(torch.uint8)
+        if config.wide:
+            packed = self.packed
+        else:
+            packed = self.packed if self.packed.dtype == torch.uint8 else self.packed.to(torch.uint8)
         status = None
         if stable:
             output = self._execute_stable(q, xscale, packed, event)
         else:
-            codes_t = self._column_codes() if hip.mm_kernel(
+            codes_t = self._column_codes() if config.wide or hip.mm_kernel(
                 config, q.shape[0], q.shape[1], self.p) else None
             status = hip.status_word(q.device)
             output = hip.mm(q, xscale, packed, codes_t, self.weight_scale.reshape(-1, self.p * c),
@@ -585,7 +588,7 @@ class AnalogMatrix(nn.Module):
         output = output[:, : self.out_features].contiguous()
         if self.zero_correction is not None:
             bits = config.activation_bits
-            signed = q.to(torch.int64).reshape(q.shape[0], -1)
+            signed = q.to(torch.int64).reshape(q.shape[0], -1).bitwise_and((1 << bits) - 1)
             signed = (signed ^ (1 << (bits - 1))) - (1 << (bits - 1))
             rows, step = config.array_size[0], config.read_rows
             padded = torch.nn.functional.pad(
@@ -593,7 +596,7 @@ class AnalogMatrix(nn.Module):
             )
             sums = padded.reshape(q.shape[0], -1, step).sum(-1)
             dtype = output.dtype
-            if stable:
+            if config.wide or stable:
                 for begin in range(0, self.out_features, c):
                     end = min(begin + c, self.out_features)
                     output[:, begin:end] += restore_scales(
@@ -605,6 +608,12 @@ class AnalogMatrix(nn.Module):
             output = output + self.bias
         if stable:
             return output, False
+        if config.wide:
+            # FP64 restore already; the reference's retry (simulator.py:614-615) would
+            # repeat the same FP64 computation.
+            return output, bool(torch.isfinite(output).all()) if (
+                self.zero_correction is not None or self.bias is not None
+            ) else not int(status.item()) & hip.STATUS_OUTPUT
         if self.zero_correction is None and self.bias is None:
             # The kernel flags non-finite outputs; one status read replaces the scan.
             finite = not int(status.item()) & hip.STATUS_OUTPUT

@@ -41,7 +41,29 @@ def cases():
                                  drift_coefficient=0.05, drift_time=100.0), 4, 64, 33),
         ("binary_int4", dict(activation_bits=8, weight_bits=4, array_size=(64, 64),
                              adc_bits=6), dict(write_variation=0.02), 3, 150, 20),
+        # Wide configurations (FP64 scales and restore, 64-bit codes, BFP).
+        ("bfp16_int4", dict(activation_bits=16, weight_bits=4,
+                            input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2), weight_slice=(1, 1, 2),
+                            bw_e=8, array_size=(64, 64), adc_bits=(6, 6, 7)),
+         dict(write_variation=0.02, read_variation=0.01, drift_coefficient=0.05,
+              drift_time=100.0), 3, 150, 20),
+        ("int12_ideal", dict(activation_bits=12, weight_bits=10, array_size=(32, 16),
+                             rows_per_read=16, adc_bits=8), dict(write_variation=0.0), 3, 70, 24),
+        ("bfp8_binary", dict(activation_bits=8, weight_bits=8, bw_e=4, array_size=(32, 16),
+                             rows_per_read=16, adc_bits=6),
+         dict(write_variation=0.02, adc_nonlinearity=0.05), 4, 64, 33),
     ]
+
+
+def bfp_edge_values():
+    """FP64 rows whose 4-wide group maxima sit at, just below and just above powers of two."""
+    rows = []
+    for k in (-30, -2, -1, 0, 1, 3, 7, 20, 100):
+        top = 2.0 ** k
+        for peak in (top * (1 - 2.0**-53), top, top * (1 + 2.0**-52), top * 1.5,
+                     top * (1 - 2.0**-40)):
+            rows.append([peak, -peak / 3, peak / 7, 0.0])
+    return torch.tensor(rows, dtype=torch.float64).reshape(-1, 4)
 
 
 def main():
@@ -108,6 +130,15 @@ def main():
         vectors[prefix + "seed"] = np.array(matrix.seed, dtype=np.uint64)
         names.append(name)
     vectors["case_names"] = np.array(names)
+    # BFP exponents floor(log2(max)) at power-of-two edges (quantization.py:35-40).
+    from memfast.quantization import grouped_quantize
+
+    edges = bfp_edge_values()
+    vectors["bfp_edges_in"] = edges.numpy()
+    for bits, bw_e in ((16, 8), (12, 5), (8, 11)):
+        code, scale = grouped_quantize(edges, bits, (1, 4), bw_e)
+        vectors[f"bfp_edges_code_{bits}_{bw_e}"] = code.numpy()
+        vectors[f"bfp_edges_scale_{bits}_{bw_e}"] = scale.numpy()
     vectors["reference_version"] = np.array(memfast.__version__)
     np.savez_compressed(OUT, **vectors)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")

@@ -530,3 +530,100 @@ def test_noisy_mfma_epilogue_and_mm(hip_device, mode):
     bad = (rel > 1e-5).float().mean().item()
     say("  elements beyond 1e-5:", bad)
     assert bad <= 0.02
+
+
+# ---------------------------------------------------------------------------
+# Wide configurations (precision above 8 bits, BFP): FP64 scales and restore
+# ---------------------------------------------------------------------------
+WIDE = {
+    "bfp16_int4": (dict(activation_bits=16, weight_bits=4,
+                        input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2), weight_slice=(1, 1, 2), bw_e=8,
+                        array_size=(64, 64), adc_bits=(6, 6, 7)),
+                   dict(write_variation=0.02, read_variation=0.01, drift_coefficient=0.05,
+                        drift_time=100.0)),
+    "int12_ideal": (dict(activation_bits=12, weight_bits=10, array_size=(32, 16),
+                         rows_per_read=16, adc_bits=8), dict(write_variation=0.0)),
+    "bfp8_binary": (dict(activation_bits=8, weight_bits=8, bw_e=4, array_size=(32, 16),
+                         rows_per_read=16, adc_bits=6),
+                    dict(write_variation=0.02, adc_nonlinearity=0.05)),
+}
+
+
+def wide_case(name):
+    kwargs, effects = WIDE[name]
+    return Config(**kwargs, nonidealities=Nonidealities(**effects))
+
+
+@pytest.mark.parametrize("name", list(WIDE))
+def test_wide_tiles_match_reference_vectors(hip_device, reference_vectors, name):
+    v = reference_vectors
+    cfg = wide_case(name)
+    a = torch.from_numpy(v[f"case_{name}_a"]).to(hip_device)
+    b = torch.from_numpy(v[f"case_{name}_b"]).to(hip_device)
+    q, xs = hip.input_tiles(a, cfg)
+    packed, codes, ws = hip.weight_tiles(b.T, cfg)
+    torch.cuda.synchronize()
+    expected_q = torch.from_numpy(v[f"case_{name}_q"]).to(torch.int64)
+    assert bits_equal(q.cpu().to(torch.int64) & 0xFFFFFFFF, expected_q)
+    assert bits_equal(xs, torch.from_numpy(v[f"case_{name}_xscale"]))
+    expected_packed = torch.from_numpy(v[f"case_{name}_packed"])
+    assert packed.dtype == expected_packed.dtype
+    assert bits_equal(packed, expected_packed)
+    assert bits_equal(codes.cpu().to(torch.int64) & 0xFFFFFFFF, expected_packed.to(torch.int64))
+    assert bits_equal(ws, torch.from_numpy(v[f"case_{name}_wscale"]))
+
+
+@pytest.mark.parametrize("name", list(WIDE))
+def test_wide_totals_with_injected_conductances(hip_device, reference_vectors, name):
+    v = reference_vectors
+    cfg = wide_case(name)
+    q = torch.from_numpy(v[f"case_{name}_q"]).to(hip_device)
+    packed = torch.from_numpy(v[f"case_{name}_packed"]).to(hip_device)
+    seed = int(v[f"case_{name}_seed"])
+    p = packed.shape[1]
+    raw = torch.from_numpy(v[f"case_{name}_restored"]).to(hip_device)
+    totals = hip.partial(q, packed, cfg, None, seed, 0, 0, p, conductance=raw).cpu()
+    expected = torch.from_numpy(v[f"case_{name}_totals"])
+    assert totals.dtype == torch.float64
+    diff = totals - expected
+    codes = diff.numel() * len(cfg.input_layout) * len(cfg.weight_layout)
+    say("  wide totals differing", int((diff != 0).sum()), "of", diff.numel())
+    if cfg.nonidealities.ideal:
+        assert bits_equal(totals, expected)
+    else:
+        assert int((diff != 0).sum()) <= max(1, 1e-4 * codes)
+
+
+@pytest.mark.parametrize("name", list(WIDE))
+def test_wide_mm_matches_reference_vectors(hip_device, reference_vectors, name):
+    from memfast_amd import Simulator
+
+    v = reference_vectors
+    cfg = wide_case(name)
+    a = torch.from_numpy(v[f"case_{name}_a"]).to(hip_device)
+    b = torch.from_numpy(v[f"case_{name}_b"]).to(hip_device)
+    sim = Simulator(cfg, device=hip_device)
+    for event in (0, 1):
+        got = sim.mm(a, b).cpu()
+        ref = torch.from_numpy(v[f"case_{name}_out{event}"])
+        if cfg.nonidealities.ideal:
+            assert bits_equal(got, ref)
+        else:
+            rel = (got - ref).abs() / ref.abs().clamp_min(1e-6)
+            bad = (rel > 1e-5).float().mean().item()
+            say("  wide", name, "event", event, "elements beyond 1e-5:", bad)
+            assert bad <= 0.02
+
+
+def test_bfp_exponent_edges_on_gpu(hip_device, reference_vectors):
+    """BFP scales and codes at power-of-two group maxima (quantization.py:35-40)."""
+    v = reference_vectors
+    edges = torch.from_numpy(v["bfp_edges_in"])
+    for bits, bw_e in ((16, 8), (12, 5), (8, 11)):
+        cfg = Config(activation_bits=bits, weight_bits=4, bw_e=bw_e, array_size=(4, 4),
+                     input_quant_gran=(1, 4), adc_bits=4)
+        q, xs = hip.input_tiles(edges.to(hip_device), cfg)
+        codes = torch.from_numpy(v[f"bfp_edges_code_{bits}_{bw_e}"]) & ((1 << bits) - 1)
+        scales = torch.from_numpy(v[f"bfp_edges_scale_{bits}_{bw_e}"])
+        assert bits_equal(q.reshape(edges.shape).cpu().to(torch.int64) & 0xFFFFFFFF, codes)
+        assert bits_equal(xs[:, 0].cpu(), scales[:, 0])

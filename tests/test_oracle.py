@@ -51,11 +51,38 @@ def _cfg(case, **extra):
         "saf_drift": dict(write_variation=0.02, stuck_at_low=0.05, stuck_at_high=0.03,
                           drift_coefficient=0.05, drift_time=100.0),
         "binary_int4": dict(write_variation=0.02),
+        "bfp16_int4": dict(write_variation=0.02, read_variation=0.01, drift_coefficient=0.05,
+                           drift_time=100.0),
+        "int12_ideal": dict(write_variation=0.0),
+        "bfp8_binary": dict(write_variation=0.02, adc_nonlinearity=0.05),
     }[case]
-    if case == "binary_int4":
+    if case in WIDE_CASES:
+        base = dict(WIDE_CASES[case])
+    elif case == "binary_int4":
         base = dict(activation_bits=8, weight_bits=4, array_size=(64, 64), adc_bits=6)
     base.update(extra)
     return Config(**base, nonidealities=Nonidealities(**noise))
+
+
+# Wide configurations of the fixture (precision above 8 bits or BFP).
+WIDE_CASES = {
+    "bfp16_int4": dict(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                       weight_slice=(1, 1, 2), bw_e=8, array_size=(64, 64), adc_bits=(6, 6, 7)),
+    "int12_ideal": dict(activation_bits=12, weight_bits=10, array_size=(32, 16), rows_per_read=16,
+                        adc_bits=8),
+    "bfp8_binary": dict(activation_bits=8, weight_bits=8, bw_e=4, array_size=(32, 16),
+                        rows_per_read=16, adc_bits=6),
+}
+
+
+def test_bfp_exponents_at_power_of_two_edges(reference_vectors):
+    """BFP scales/codes around 2^k (floor(log2(max)), quantization.py:35-40)."""
+    v = reference_vectors
+    edges = torch.from_numpy(v["bfp_edges_in"])
+    for bits, bw_e in ((16, 8), (12, 5), (8, 11)):
+        code, scale = oracle.grouped_quantize(edges, bits, (1, 4), bw_e)
+        np.testing.assert_array_equal(code.numpy(), v[f"bfp_edges_code_{bits}_{bw_e}"])
+        np.testing.assert_array_equal(scale.numpy(), v[f"bfp_edges_scale_{bits}_{bw_e}"])
 
 
 # ---------------------------------------------------------------------------
