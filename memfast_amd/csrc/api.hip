@@ -251,6 +251,9 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
             if (cfg->w_factor[w] < 0) plan->cw_negative |= 1u << cw_of[w];
         }
     }
+    for (int a = 0; a < cfg->n_in; ++a)
+        for (int w = 0; w < cfg->n_w; ++w)
+            if (!is_free[a][w]) plan->ca_wnat[ca_of[a]] |= plan->cw_wnat[cw_of[w]];
     memset(xtests, 0, sizeof(*xtests));
     memset(wtests, 0, sizeof(*wtests));
     for (int a = 0; a < cfg->n_in; ++a)

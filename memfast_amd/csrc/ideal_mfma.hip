@@ -275,34 +275,30 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
 
         // Slots (ca * 8 + cw) proven clamp-free on either side merge into one
         // MFMA per input slice; the others get their own MFMA and a clamp.
-        const uint64_t proven = xbits[g] | wbits[g];
-        const uint64_t fail = plan.exists & ~proven;
-        const uint64_t safe = plan.exists & proven;
+        // Every clamp candidate enters one linear MFMA per input slice (its row
+        // mask).  Pairs not proven clamp-free by the digit sums are recomputed
+        // alone, Y = fa*fw*S, and only a tile where some |Y| exceeds the limit
+        // lim = fa*fw*max_w pays the per-output correction min(Y, lim) - Y
+        // (max() for negative pairs).
+        const uint64_t fail = plan.exists & ~(xbits[g] | wbits[g]);
         for (int ca = 0; ca < plan.n_ca; ++ca) {
-            const u32 safe_w = u32(safe >> (ca * 8)) & 0xFFu;
-            u32 fail_w = u32(fail >> (ca * 8)) & 0xFFu;
-            if (!(safe_w | fail_w)) continue;
             v4i Xn[TN][KS];
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) Xn[tn][ks] = and4(Xr[tn][ks], plan.ca_xnat[ca]);
-            if (safe_w) {
-                u32 merged = 0;
-                for (u32 bits = safe_w; bits; bits &= bits - 1)
-                    merged |= plan.cw_wnat[__builtin_ctz(bits)];
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const v4i wm = and4(Wr[ks], merged);
+            for (int ks = 0; ks < KS; ++ks) {
+                const v4i wm = and4(Wr[ks], plan.ca_wnat[ca]);
 #pragma unroll
-                    for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, Xn[tn][ks], T[tn]);
-                }
+                for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, Xn[tn][ks], T[tn]);
             }
-            // A clamped pair's product Y = fa*fw*S has the sign of its limit
-            // lim = fa*fw*max: min() clamps positive pairs, max() negative ones.
+            const u32 fail_w = u32(fail >> (ca * 8)) & 0xFFu;
+            if (!fail_w) continue;
             const int fa = plan.ca_factor[ca];
             const u32 neg_w = fail_w & (fa < 0 ? ~plan.cw_negative : plan.cw_negative);
-            auto clamped = [&](u32 bits, auto negative) {
+            auto corrected = [&](u32 bits, auto negative) {
+                constexpr bool NEG = decltype(negative)::value;
                 for (; bits; bits &= bits - 1) {
                     const int cw = __builtin_ctz(bits);
                     v4i Wn[KS];
@@ -314,16 +310,25 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
                         v16i y = mfma(Wn[0], Xn[tn][0], v16i{});
 #pragma unroll
                         for (int ks = 1; ks < KS; ++ks) y = mfma(Wn[ks], Xn[tn][ks], y);
+                        // Extreme of the tile (three-input max/min tree).
+                        int e0 = NEG ? min(min(y[0], y[1]), y[2]) : max(max(y[0], y[1]), y[2]);
+                        int e1 = NEG ? min(min(y[3], y[4]), y[5]) : max(max(y[3], y[4]), y[5]);
+                        int e2 = NEG ? min(min(y[6], y[7]), y[8]) : max(max(y[6], y[7]), y[8]);
+                        int e3 = NEG ? min(min(y[9], y[10]), y[11]) : max(max(y[9], y[10]), y[11]);
+                        int e4 = NEG ? min(min(y[12], y[13]), y[14]) : max(max(y[12], y[13]), y[14]);
+                        int e = NEG ? min(min(e0, e1), e2) : max(max(e0, e1), e2);
+                        e = NEG ? min(min(e, e3), e4) : max(max(e, e3), e4);
+                        e = NEG ? min(e, y[15]) : max(e, y[15]);
+                        const bool over = NEG ? e < lim : e > lim;
+                        if (__builtin_amdgcn_ballot_w64(over) == 0) continue;
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            if constexpr (decltype(negative)::value) T[tn][r] += max(y[r], lim);
-                            else T[tn][r] += min(y[r], lim);
-                        }
+                        for (int r = 0; r < 16; ++r)
+                            T[tn][r] += NEG ? max(lim - y[r], 0) : min(lim - y[r], 0);
                     }
                 }
             };
-            clamped(fail_w & ~neg_w, std::false_type{});
-            clamped(neg_w, std::true_type{});
+            corrected(fail_w & ~neg_w, std::false_type{});
+            corrected(neg_w, std::true_type{});
         }
 
         // Scale restore (float(T) * xs) * ws and cascade accumulation.

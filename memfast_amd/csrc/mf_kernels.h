@@ -50,6 +50,7 @@ struct IdealPlan {
     u32 lin_w[IDEAL_MAX_LIN], lin_x[IDEAL_MAX_LIN];   // weight / input side masks
     int n_ca, n_cw;
     u32 ca_xnat[IDEAL_MAX_CA];
+    u32 ca_wnat[IDEAL_MAX_CA];                        // OR of cw_wnat over the row's slots
     int ca_factor[IDEAL_MAX_CA];                      // fa
     u32 cw_wnat[IDEAL_MAX_CW];
     int cw_limit[IDEAL_MAX_CW];                       // fw * max_w
