@@ -196,16 +196,11 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
     if (fa_sum * fw_sum >= 2147483647.0) { *why = "slice totals exceed int32"; return false; }
 
     memset(plan, 0, sizeof(*plan));
+    // A pair is clamp-free when even P rows of full digits stay within max_w.
     bool is_free[MF_MAX_SLICES][MF_MAX_SLICES];
-    unsigned free_sets[MF_MAX_SLICES];
-    for (int w = 0; w < cfg->n_w; ++w) {
-        free_sets[w] = 0;
-        for (int a = 0; a < cfg->n_in; ++a) {
-            const i64 smax = i64(P) * cfg->in_mask[a] * cfg->w_mask[w];
-            is_free[a][w] = smax <= cfg->adc_max[w];
-            if (is_free[a][w]) free_sets[w] |= 1u << a;
-        }
-    }
+    for (int w = 0; w < cfg->n_w; ++w)
+        for (int a = 0; a < cfg->n_in; ++a)
+            is_free[a][w] = i64(P) * cfg->in_mask[a] * cfg->w_mask[w] <= cfg->adc_max[w];
     SliceForm xf[MF_MAX_SLICES], wf[MF_MAX_SLICES];
     for (int a = 0; a < cfg->n_in; ++a)
         xf[a] = slice_form(cfg->in_shift[a], cfg->in_mask[a], a == cfg->n_in - 1,
@@ -213,23 +208,6 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
     for (int w = 0; w < cfg->n_w; ++w)
         wf[w] = slice_form(cfg->w_shift[w], cfg->w_mask[w], w == cfg->n_w - 1,
                            cfg->weight_bits);
-    // Static linear terms: weight slices grouped by their clamp-free input sets.
-    bool grouped[MF_MAX_SLICES] = {false};
-    for (int w = 0; w < cfg->n_w; ++w) {
-        if (grouped[w] || free_sets[w] == 0) continue;
-        u32 xmask = 0, wmask = 0;
-        for (int a = 0; a < cfg->n_in; ++a)
-            if (free_sets[w] >> a & 1) xmask |= xf[a].nat;
-        for (int v = w; v < cfg->n_w; ++v)
-            if (!grouped[v] && free_sets[v] == free_sets[w]) {
-                grouped[v] = true;
-                wmask |= wf[v].nat;
-            }
-        if (plan->n_lin >= IDEAL_MAX_LIN) { *why = "too many linear terms"; return false; }
-        plan->lin_w[plan->n_lin] = wmask;
-        plan->lin_x[plan->n_lin] = xmask;
-        ++plan->n_lin;
-    }
     // Clamp-candidate grid: slot ca * 8 + cw.
     int ca_of[MF_MAX_SLICES], cw_of[MF_MAX_SLICES];
     for (int a = 0; a < cfg->n_in; ++a) {
@@ -251,9 +229,6 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
             if (cfg->w_factor[w] < 0) plan->cw_negative |= 1u << cw_of[w];
         }
     }
-    for (int a = 0; a < cfg->n_in; ++a)
-        for (int w = 0; w < cfg->n_w; ++w)
-            if (!is_free[a][w]) plan->ca_wnat[ca_of[a]] |= plan->cw_wnat[cw_of[w]];
     memset(xtests, 0, sizeof(*xtests));
     memset(wtests, 0, sizeof(*wtests));
     for (int a = 0; a < cfg->n_in; ++a)

@@ -5,16 +5,15 @@
 // form code = min(S_aw, max_w), S_aw = sum_r da[n,r] * dw[r,c] (memfast/
 // reference.py:63-117 with ideal conductances; exact because FP32 current
 // errors stay far below half a count, checked on the host).  Per read:
-//   * static linear terms: pairs that can never exceed max_w.  Their signed sum
-//     is an int8 x int8 MFMA of masked two's complement codes (a masked byte's
-//     int8 value is exactly sum factor*digit over the slices in the mask);
-//   * for the remaining pairs, a per-read, per-wave test on precomputed digit
-//     sums proves most of them clamp-free (S <= Mw*max_n sum_r da, or
-//     S <= Ma*max_c sum_r dw); those merge into one natural-form MFMA per input
-//     slice, again with no VALU work;
-//   * pairs still at risk get their own natural-form MFMA; its product
-//     Y = fa*fw*S has the sign of fa*fw, so one v_min_i32 (positive pairs) or
-//     v_max_i32 (negative pairs) against fa*fw*max_w and one add per output.
+//   * T = sum_aw fa*fw*min(S_aw, max_w) starts as the linear part
+//     sum_aw fa*fw*S_aw, which is the plain int8 x int8 MFMA of the codes;
+//   * pairs that can exceed max_w are tested on precomputed digit sums per
+//     wave block (S <= Mw*max_n sum_r da, or S <= Ma*max_c sum_r dw); most
+//     are proven clamp-free and need nothing more;
+//   * each remaining pair gets its own MFMA on natural operand forms (masked
+//     bytes whose int8 value is factor*digit), Y = fa*fw*S, a wave-wide
+//     max (min) test against fa*fw*max_w, and -- only if some output exceeds
+//     it -- the correction min(Y, lim) - Y per output.
 // T is restored as (float(T) * xs[n,g]) * ws[g,c] and summed over reads in
 // torch's CPU cascade order (level step 16; level 2 kept in `out`).
 //
@@ -251,50 +250,29 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
                     &sX[cur][(wv * TN * 32 + tn * 32 + lrow) * STRIDE + ks * 32 + lhalf * 16]);
         }
 
-        // Static linear terms (the first one starts the accumulator from zero).
+        // Linear part: sum over all pairs of fa*fw*S = the plain int8 product of
+        // the (sign-extended) codes, one MFMA per 32 rows.
         v16i T[TN];
-        {
-            const u32 mw = plan.lin_w[0], mx = plan.lin_x[0];
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-                T[tn] = mfma(and4(Wr[0], mw), and4(Xr[tn][0], mx), v16i{});
+        for (int tn = 0; tn < TN; ++tn) {
+            T[tn] = mfma(Wr[0], Xr[tn][0], v16i{});
 #pragma unroll
-                for (int ks = 1; ks < KS; ++ks)
-                    T[tn] = mfma(and4(Wr[ks], mw), and4(Xr[tn][ks], mx), T[tn]);
-            }
-        }
-        for (int t = 1; t < plan.n_lin; ++t) {
-            const u32 mw = plan.lin_w[t], mx = plan.lin_x[t];
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const v4i wm = and4(Wr[ks], mw);
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, and4(Xr[tn][ks], mx), T[tn]);
-            }
+            for (int ks = 1; ks < KS; ++ks) T[tn] = mfma(Wr[ks], Xr[tn][ks], T[tn]);
         }
 
-        // Slots (ca * 8 + cw) proven clamp-free on either side merge into one
-        // MFMA per input slice; the others get their own MFMA and a clamp.
-        // Every clamp candidate enters one linear MFMA per input slice (its row
-        // mask).  Pairs not proven clamp-free by the digit sums are recomputed
-        // alone, Y = fa*fw*S, and only a tile where some |Y| exceeds the limit
-        // lim = fa*fw*max_w pays the per-output correction min(Y, lim) - Y
-        // (max() for negative pairs).
+        // Clamp candidates (pairs that can exceed max_w) not proven clamp-free
+        // by the digit sums are recomputed alone, Y = fa*fw*S; only a tile where
+        // some |Y| exceeds the limit lim = fa*fw*max_w pays the per-output
+        // correction min(Y, lim) - Y (max() for negative pairs).
         const uint64_t fail = plan.exists & ~(xbits[g] | wbits[g]);
-        for (int ca = 0; ca < plan.n_ca; ++ca) {
+        for (int ca = 0; fail && ca < plan.n_ca; ++ca) {
+            const u32 fail_w = u32(fail >> (ca * 8)) & 0xFFu;
+            if (!fail_w) continue;
             v4i Xn[TN][KS];
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) Xn[tn][ks] = and4(Xr[tn][ks], plan.ca_xnat[ca]);
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const v4i wm = and4(Wr[ks], plan.ca_wnat[ca]);
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) T[tn] = mfma(wm, Xn[tn][ks], T[tn]);
-            }
-            const u32 fail_w = u32(fail >> (ca * 8)) & 0xFFu;
-            if (!fail_w) continue;
             const int fa = plan.ca_factor[ca];
             const u32 neg_w = fail_w & (fa < 0 ? ~plan.cw_negative : plan.cw_negative);
             auto corrected = [&](u32 bits, auto negative) {

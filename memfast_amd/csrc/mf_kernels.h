@@ -31,26 +31,22 @@ template <typename Phys, int WG, bool OUTPUT_NOISE, bool WIDE>
 __global__ void k_general(const mf_config cfg, const GeneralArgs args, int out_kind);
 
 // ---- ideal MFMA read (ideal_mfma.hip) -------------------------------------
-constexpr int IDEAL_MAX_LIN = 16;   // static linear terms
 constexpr int IDEAL_MAX_CA = 8;     // input slices with at least one clamped pair
 constexpr int IDEAL_MAX_CW = 8;     // weight slices with at least one clamped pair
 
-// Slice pairs that can exceed their ADC limit form a (clamp-a x clamp-w) grid of
-// slots s = ca * 8 + cw.  Per read and wave a slot is *proven clamp-free* (and
-// merged into a linear MFMA, exactly) when a digit-sum bound shows S <= max:
-// max_n sum_r da <= floor(max_w / Mw) (input side) or max_c sum_r dw <=
-// floor(max_w / Ma) (weight side).  The pre-pass k_digit_bits evaluates these
-// tests and stores one 64-bit slot mask per (block, read).
-// Operands are "natural" forms: masked two's complement bytes whose int8 value
-// is the sum of factor*digit over the slices in the mask.  A clamped pair's
-// product Y = fa*fw*S is clamped to fa*fw*max_w (min for positive pairs,
-// max for negative ones).
+// The linear part of every slice pair, sum_aw fa*fw*S_aw, is the plain int8
+// product of the codes.  Pairs that can exceed their ADC limit form a
+// (clamp-a x clamp-w) grid of slots s = ca * 8 + cw.  Per read and wave a slot
+// is *proven clamp-free* when a digit-sum bound shows S <= max: max_n sum_r da
+// <= floor(max_w / Mw) (input side) or max_c sum_r dw <= floor(max_w / Ma)
+// (weight side).  The pre-pass k_digit_bits evaluates these tests and stores
+// one 64-bit slot mask per (block, read).  Other candidates are recomputed on
+// "natural" operand forms (masked two's complement bytes whose int8 value is
+// factor*digit), Y = fa*fw*S, and corrected to min(Y, fa*fw*max_w) (max for
+// negative pairs) where needed.
 struct IdealPlan {
-    int n_lin;
-    u32 lin_w[IDEAL_MAX_LIN], lin_x[IDEAL_MAX_LIN];   // weight / input side masks
     int n_ca, n_cw;
     u32 ca_xnat[IDEAL_MAX_CA];
-    u32 ca_wnat[IDEAL_MAX_CA];                        // OR of cw_wnat over the row's slots
     int ca_factor[IDEAL_MAX_CA];                      // fa
     u32 cw_wnat[IDEAL_MAX_CW];
     int cw_limit[IDEAL_MAX_CW];                       // fw * max_w
