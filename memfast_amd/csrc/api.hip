@@ -533,7 +533,19 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
     const i64 unit = lcm4(gr);
     const i64 span = unit >= 128 ? unit : unit * (128 / unit);
     const bool reg_group = gr == 8 || gr == 16 || gr == 32 || gr == 64;
-    if (gc == 1 && reg_group && (kp + gr - 1) / gr <= 65535) {
+    const bool tiled = (gr == 16 || gr == 32) && cfg->cols % 64 == 0 && R % (4 * gr) == 0 &&
+                       kp % 16 == 0;
+    if (gc == 1 && tiled && kp / (4 * gr) <= 65535) {
+        const dim3 grid{unsigned(op / 64), unsigned(kp / (4 * gr)), 1u};
+        if (gr == 16)
+            hipLaunchKernelGGL(k_col_groups_tile<16>, grid, dim3(256), 0, s, b, k, o, ld, R, C, m, p,
+                               lower, upper, mask, packed, packed_t, scale, status,
+                               u32(MF_STATUS_WEIGHT));
+        else
+            hipLaunchKernelGGL(k_col_groups_tile<32>, grid, dim3(256), 0, s, b, k, o, ld, R, C, m, p,
+                               lower, upper, mask, packed, packed_t, scale, status,
+                               u32(MF_STATUS_WEIGHT));
+    } else if (gc == 1 && reg_group && (kp + gr - 1) / gr <= 65535) {
         const dim3 grid{unsigned((op + 255) / 256), unsigned((kp + gr - 1) / gr), 1u};
         const bool word = kp % 4 == 0;
 #define MF_COL_REG_LAUNCH(GR)                                                                    \
@@ -719,10 +731,12 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         const SliceLayout xl = layout_of(cfg->in_shift, cfg->in_mask, cfg->n_in);
         const SliceLayout wl = layout_of(cfg->w_shift, cfg->w_mask, cfg->n_w);
         const unsigned gblocks = unsigned((G + 63) / 64);
-        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((n + 63) / 64)), dim3(256), 0, s,
-                           q, n, kp, G, cfg->read_rows, xl, 64, xtests, xbits);
-        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((ncols + 31) / 32)), dim3(256), 0,
-                           s, packed_t, ncols, kp, G, cfg->read_rows, wl, 32, wtests, wbits);
+        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((n + 63) / 64)),
+                           dim3(64 * DIGIT_WAVES), 0, s, q, n, kp, G, cfg->read_rows, xl, 64,
+                           xtests, xbits);
+        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((ncols + 31) / 32)),
+                           dim3(64 * DIGIT_WAVES), 0, s, packed_t, ncols, kp, G, cfg->read_rows, wl,
+                           32, wtests, wbits);
         IdealArgs args{};
         args.q = q;
         args.wt = packed_t;

@@ -57,26 +57,26 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 // Per-read digit sums, maximized over blocks of `block` (32 or 64) rows, then
 // tested against the slot thresholds: out[rb][g] = mask of proven slots.
 // Workgroup = 64 reads (one per lane, so a wave loads 64 consecutive P-byte
-// runs of a row) x 4 waves that split the block's rows; LDS combines the
-// four partial maxima.  Digit sums use SWAR: (word >> shift) & mask per byte,
-// then v_sad_u8 adds the four bytes.  Requires P in {32, 64} and reads that
-// start at g * P (R a multiple of P).
-__global__ __launch_bounds__(256) void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int P,
-                                                    const SliceLayout layout, int block,
-                                                    const SlotTests tests, uint64_t *out) {
-    __shared__ int partial[3][8][64];
-    const int lane = threadIdx.x & 63, quarter = threadIdx.x >> 6;
+// runs of a row) x 16 waves that split the block's rows; LDS combines the
+// partial maxima.  Digit sums use SWAR: (word >> shift) & mask per byte, then
+// v_sad_u8 adds the four bytes.  Requires P in {32, 64} and reads that start
+// at g * P (R a multiple of P).
+__global__ __launch_bounds__(64 * DIGIT_WAVES) void k_digit_bits(
+    const u8 *codes, i64 rows, i64 kp, i64 G, int P, const SliceLayout layout, int block,
+    const SlotTests tests, uint64_t *out) {
+    __shared__ int partial[DIGIT_WAVES][8][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const i64 g = i64(blockIdx.x) * 64 + lane;
     const i64 rb = blockIdx.y;
     const int S = layout.count;
-    const int per = block / 4;
+    const int per = block / DIGIT_WAVES;
     int best[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     u32 masks[8];
 #pragma unroll
     for (int sl = 0; sl < 8; ++sl) masks[sl] = sl < S ? u32(layout.mask[sl]) * 0x01010101u : 0u;
     if (g < G) {
         for (int i = 0; i < per; ++i) {
-            const i64 row = rb * block + quarter * per + i;
+            const i64 row = rb * block + wave * per + i;
             if (row >= rows) break;
             const uint4 *src = reinterpret_cast<const uint4 *>(codes + row * kp + g * P);
             uint4 chunk[4];
@@ -104,15 +104,13 @@ __global__ __launch_bounds__(256) void k_digit_bits(const u8 *codes, i64 rows, i
             }
         }
     }
-    if (quarter > 0) {
 #pragma unroll
-        for (int sl = 0; sl < 8; ++sl) partial[quarter - 1][sl][lane] = best[sl];
-    }
+    for (int sl = 0; sl < 8; ++sl) partial[wave][sl][lane] = best[sl];
     __syncthreads();
-    if (quarter > 0 || g >= G || rb * block >= rows) return;
+    if (wave > 0 || g >= G || rb * block >= rows) return;
 #pragma unroll
     for (int sl = 0; sl < 8; ++sl)
-        best[sl] = max(max(best[sl], partial[0][sl][lane]), max(partial[1][sl][lane], partial[2][sl][lane]));
+        for (int w = 1; w < DIGIT_WAVES; ++w) best[sl] = max(best[sl], partial[w][sl][lane]);
     uint64_t bits = 0;
     for (int slot = 0; slot < 64; ++slot) {
         if (!((tests.exists >> slot) & 1)) continue;

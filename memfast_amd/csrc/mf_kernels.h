@@ -87,6 +87,7 @@ struct SliceLayout {
 
 // Per-read digit sums of every slice, maximized over blocks of `block` rows,
 // turned into the slot mask of `tests`: out[rb][g].
+constexpr int DIGIT_WAVES = 16;   // waves per k_digit_bits workgroup
 __global__ void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int P,
                              const SliceLayout layout, int block, const SlotTests tests,
                              uint64_t *out);
@@ -149,6 +150,10 @@ template <int GR, bool WORD>
 __global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
                                  i64 p, float lower, float upper, u32 mask, u8 *packed,
                                  u8 *packed_t, float *scale, u32 *status, u32 flag);
+template <int GR>
+__global__ void k_col_groups_tile(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+                                  i64 p, float lower, float upper, u32 mask, u8 *packed,
+                                  u8 *packed_t, float *scale, u32 *status, u32 flag);
 template <bool WORD>
 __global__ void k_col_groups(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 span, int R,
                              int C, i64 m, i64 p, float lower, float upper, u32 mask,

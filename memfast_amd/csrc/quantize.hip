@@ -281,6 +281,76 @@ __global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, in
     }
     if (!finite && status) atomicOr(status, flag);
 }
+// Column groups through an LDS tile: workgroup = 64 physical columns (lanes)
+// x 4 row groups of GR rows (waves), i.e. a [4*GR x 64] code tile.  Each lane
+// holds its group's GR values in registers (coalesced 256-byte row loads),
+// writes its codes into the tile, and the workgroup then stores the tile as
+// 64-byte row segments of packed [m, p, R, C] and 4*GR-byte column runs of
+// packed_t [p*C, m*R], 16 bytes per store.  Requires C % 64 == 0, R % (4*GR)
+// == 0 (row segments stay inside one array tile) and kp % 16 == 0.
+template <int GR>
+__global__ __launch_bounds__(256) void k_col_groups_tile(
+    const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m, i64 p, float lower, float upper,
+    u32 mask, u8 *packed, u8 *packed_t, float *scale, u32 *status, u32 flag) {
+    constexpr int ROWS = 4 * GR;
+    __shared__ __align__(16) u8 tile_rc[ROWS][64 + 16];   // row-major codes
+    __shared__ __align__(16) u8 tile_cr[64][ROWS + 16];   // column-major codes
+    const i64 kp = m * R;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const i64 c0 = i64(blockIdx.x) * 64, r_block = i64(blockIdx.y) * ROWS;
+    const i64 col = c0 + lane;
+    const i64 r0 = r_block + wave * GR;
+    const bool live = col < o;
+    float v[GR];
+#pragma unroll
+    for (int i = 0; i < GR; ++i) {
+        const i64 row = r0 + i;
+        v[i] = (live && row < k) ? b[row * ld + col] : 0.0f;
+    }
+    float peak = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < GR; ++i) {
+        const float a = fabsf(v[i]);
+        finite = finite && a <= FLT_MAX;
+        peak = fmaxf(peak, a);
+    }
+    const float sc = group_scale(peak, upper);
+    if (live && r0 < k) scale[(r0 / GR) * o + col] = sc;
+#pragma unroll
+    for (int i = 0; i < GR; ++i) {
+        const u8 code = (live && r0 + i < k) ? quantize_code(v[i], sc, lower, upper, mask) : u8(0);
+        tile_rc[wave * GR + i][lane] = code;
+        tile_cr[lane][wave * GR + i] = code;
+    }
+    __syncthreads();
+    // packed: ROWS rows x 64 bytes = 4 x 16-byte chunks per row.
+    const i64 t = c0 / C, cc0 = c0 - t * C;
+    for (int e = threadIdx.x; e < ROWS * 4; e += 256) {
+        const int rr = e >> 2, chunk = e & 3;
+        const i64 row = r_block + rr;
+        if (row >= kp) continue;
+        const i64 i = row / R, r = row - i * R;
+        *reinterpret_cast<uint4 *>(packed + ((i * p + t) * R + r) * C + cc0 + chunk * 16) =
+            *reinterpret_cast<const uint4 *>(&tile_rc[rr][chunk * 16]);
+    }
+    // packed_t: 64 columns x ROWS bytes = ROWS/16 chunks per column.
+    if (packed_t) {
+        for (int e = threadIdx.x; e < 64 * (ROWS / 16); e += 256) {
+            const int cl = e / (ROWS / 16), chunk = e % (ROWS / 16);
+            const i64 row = r_block + chunk * 16;
+            if (row >= kp) continue;
+            *reinterpret_cast<uint4 *>(packed_t + (c0 + cl) * kp + row) =
+                *reinterpret_cast<const uint4 *>(&tile_cr[cl][chunk * 16]);
+        }
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+template __global__ void k_col_groups_tile<16>(const float *, i64, i64, i64, int, int, i64, i64,
+                                               float, float, u32, u8 *, u8 *, float *, u32 *, u32);
+template __global__ void k_col_groups_tile<32>(const float *, i64, i64, i64, int, int, i64, i64,
+                                               float, float, u32, u8 *, u8 *, float *, u32 *, u32);
+
 #define MF_COL_REG_INST(GR, WORD)                                                               \
     template __global__ void k_col_groups_reg<GR, WORD>(const float *, i64, i64, i64, int, int, \
                                                         i64, i64, float, float, u32, u8 *, u8 *,  \

@@ -83,6 +83,9 @@ IDEAL_CASES = [
     ("whole_rows", ideal(adc_bits=8), 3, 1500, 20),
     # one wave per 1024-float row group,
     ("row_wave", ideal(adc_bits=8), 3, 1024, 20),
+    # LDS-tiled weight groups with a ragged last group and padded columns,
+    ("tile_ragged", ideal(array_size=(64, 64), rows_per_read=16, weight_quant_gran=(16, 1),
+                          input_quant_gran=(1, 16), adc_bits=8), 5, 150, 100),
     # register column groups with byte stores (kp = 54 is not a multiple of 4).
     ("col_bytes", ideal(array_size=(18, 32), rows_per_read=2, weight_quant_gran=(8, 1),
                         adc_bits=6), 4, 45, 36),
