@@ -130,6 +130,36 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, i6
                                              0x00020000);
 }
 
+// T += min(Y, lim) - Y for a positive pair (max() for a negative one, lim < 0),
+// skipped when no output of the 32x32 tile crosses lim (the usual case).
+__device__ __forceinline__ void correct_tile(v16i &T, const v16i &y, int lim) {
+    if (lim >= 0) {
+        int e = max(max(y[0], y[1]), y[2]);
+        e = max(max(e, y[3]), y[4]);
+        e = max(max(e, y[5]), y[6]);
+        e = max(max(e, y[7]), y[8]);
+        e = max(max(e, y[9]), y[10]);
+        e = max(max(e, y[11]), y[12]);
+        e = max(max(e, y[13]), y[14]);
+        e = max(e, y[15]);
+        if (__builtin_amdgcn_ballot_w64(e > lim) == 0) return;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[r] += min(lim - y[r], 0);
+    } else {
+        int e = min(min(y[0], y[1]), y[2]);
+        e = min(min(e, y[3]), y[4]);
+        e = min(min(e, y[5]), y[6]);
+        e = min(min(e, y[7]), y[8]);
+        e = min(min(e, y[9]), y[10]);
+        e = min(min(e, y[11]), y[12]);
+        e = min(min(e, y[13]), y[14]);
+        e = min(e, y[15]);
+        if (__builtin_amdgcn_ballot_w64(e < lim) == 0) return;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[r] += max(lim - y[r], 0);
+    }
+}
+
 template <int TN, int KS>
 __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const IdealArgs args) {
     constexpr int BC = 64;                 // output columns per block
@@ -233,6 +263,12 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
 
     const uint64_t *xbits = args.xbits + vblock * G;
     const uint64_t *wbits = args.wbits + cblock * G;
+    // Per-slot constants, lane s holding slot s = ca * 8 + cw (read with readlane).
+    const int slot_ca = lane >> 3, slot_cw = lane & 7;
+    const bool slot_live = slot_ca < plan.n_ca && slot_cw < plan.n_cw;
+    const u32 slot_x = slot_live ? plan.ca_xnat[slot_ca] : 0u;
+    const u32 slot_w = slot_live ? plan.cw_wnat[slot_cw] : 0u;
+    const int slot_lim = slot_live ? plan.ca_factor[slot_ca] * plan.cw_limit[slot_cw] : 0;
     for (int g = 0; g < G; ++g) {
         const int cur = g & 1;
         if (g + 1 < G) fetch(g + 1);
@@ -262,49 +298,20 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
         // by the digit sums are recomputed alone, Y = fa*fw*S; only a tile where
         // some |Y| exceeds the limit lim = fa*fw*max_w pays the per-output
         // correction min(Y, lim) - Y (max() for negative pairs).
-        const uint64_t fail = plan.exists & ~(xbits[g] | wbits[g]);
-        for (int ca = 0; fail && ca < plan.n_ca; ++ca) {
-            const u32 fail_w = u32(fail >> (ca * 8)) & 0xFFu;
-            if (!fail_w) continue;
-            v4i Xn[TN][KS];
+        uint64_t fail = plan.exists & ~(xbits[g] | wbits[g]);
+        while (fail) {
+            const int slot = __builtin_ctzll(fail);
+            fail &= fail - 1;
+            const u32 xm = u32(__builtin_amdgcn_readlane(int(slot_x), slot));
+            const u32 wm = u32(__builtin_amdgcn_readlane(int(slot_w), slot));
+            const int lim = __builtin_amdgcn_readlane(slot_lim, slot);
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn)
+            for (int tn = 0; tn < TN; ++tn) {
+                v16i y = mfma(and4(Wr[0], wm), and4(Xr[tn][0], xm), v16i{});
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) Xn[tn][ks] = and4(Xr[tn][ks], plan.ca_xnat[ca]);
-            const int fa = plan.ca_factor[ca];
-            const u32 neg_w = fail_w & (fa < 0 ? ~plan.cw_negative : plan.cw_negative);
-            auto corrected = [&](u32 bits, auto negative) {
-                constexpr bool NEG = decltype(negative)::value;
-                for (; bits; bits &= bits - 1) {
-                    const int cw = __builtin_ctz(bits);
-                    v4i Wn[KS];
-#pragma unroll
-                    for (int ks = 0; ks < KS; ++ks) Wn[ks] = and4(Wr[ks], plan.cw_wnat[cw]);
-                    const int lim = fa * plan.cw_limit[cw];
-#pragma unroll
-                    for (int tn = 0; tn < TN; ++tn) {
-                        v16i y = mfma(Wn[0], Xn[tn][0], v16i{});
-#pragma unroll
-                        for (int ks = 1; ks < KS; ++ks) y = mfma(Wn[ks], Xn[tn][ks], y);
-                        // Extreme of the tile (three-input max/min tree).
-                        int e0 = NEG ? min(min(y[0], y[1]), y[2]) : max(max(y[0], y[1]), y[2]);
-                        int e1 = NEG ? min(min(y[3], y[4]), y[5]) : max(max(y[3], y[4]), y[5]);
-                        int e2 = NEG ? min(min(y[6], y[7]), y[8]) : max(max(y[6], y[7]), y[8]);
-                        int e3 = NEG ? min(min(y[9], y[10]), y[11]) : max(max(y[9], y[10]), y[11]);
-                        int e4 = NEG ? min(min(y[12], y[13]), y[14]) : max(max(y[12], y[13]), y[14]);
-                        int e = NEG ? min(min(e0, e1), e2) : max(max(e0, e1), e2);
-                        e = NEG ? min(min(e, e3), e4) : max(max(e, e3), e4);
-                        e = NEG ? min(e, y[15]) : max(e, y[15]);
-                        const bool over = NEG ? e < lim : e > lim;
-                        if (__builtin_amdgcn_ballot_w64(over) == 0) continue;
-#pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            T[tn][r] += NEG ? max(lim - y[r], 0) : min(lim - y[r], 0);
-                    }
-                }
-            };
-            corrected(fail_w & ~neg_w, std::false_type{});
-            corrected(neg_w, std::true_type{});
+                for (int ks = 1; ks < KS; ++ks) y = mfma(and4(Wr[ks], wm), and4(Xr[tn][ks], xm), y);
+                correct_tile(T[tn], y, lim);
+            }
         }
 
         // Scale restore (float(T) * xs) * ws and cascade accumulation.
