@@ -13,6 +13,7 @@ The most significant slice of a signed code carries factor ``-(1 << shift)``.
 import math
 import struct
 from dataclasses import dataclass, fields
+from functools import cached_property
 
 _FP32_MAX = 3.4028234663852886e38
 _FP32_MIN_SUBNORMAL = 1.401298464324817e-45
@@ -226,12 +227,13 @@ class Config:
             raise TypeError("nonidealities must be Nonidealities")
 
     # -- derived geometry (memfast/config.py:167-224) -------------------------
+    # Layouts and flags are computed once per (immutable) Config.
     @property
     def current_unit(self):
         """Current of one ideal digit product: (H - L) * V_read."""
         return (self.high_conductance - self.low_conductance) * self.read_voltage
 
-    @property
+    @cached_property
     def adc_maxima(self):
         """Largest ADC count per weight slice, LSB-first (adc_bits is MSB-first)."""
         count = len(self.weight_layout)
@@ -259,11 +261,11 @@ class Config:
     def _layout(widths, bits, signed=True):
         return layout(widths, bits, signed)
 
-    @property
+    @cached_property
     def input_layout(self):
         return layout(self.input_slice, self.activation_bits, True)
 
-    @property
+    @cached_property
     def weight_layout(self):
         return layout(self.weight_slice, self.weight_bits, self.weight_signed)
 
@@ -276,7 +278,7 @@ class Config:
         )
         return inputs * weights
 
-    @property
+    @cached_property
     def wide(self):
         """FP64 scale restoration and 64-bit codes (precision > 8 or BFP)."""
         return max(self.activation_bits, self.weight_bits) > 8 or self.bw_e is not None
@@ -285,7 +287,7 @@ class Config:
     def wide_codes(self):
         return max(self.activation_bits, self.weight_bits) > 8
 
-    @property
+    @cached_property
     def precise_currents(self):
         """FP64 currents where FP32 rounding could move ideal ADC counts."""
         widest = max(entry[1] for entry in (*self.input_layout, *self.weight_layout))

@@ -186,28 +186,73 @@ class Simulator:
         self._matrix_cache[identity] = (weakref.ref(matrix, release), metadata, programmed)
         return programmed
 
+    def _program_plan(self, matrix, tiles):
+        """(name, event) of the program ``_matrix_for(matrix, tiles)`` would return, no side effects."""
+        record = self._matrix_cache.get(id(matrix))
+        same_tensor = record is not None and record[0]() is matrix
+        previous = record[2] if same_tensor else None
+        metadata = (
+            tuple(matrix.shape), tuple(matrix.stride()), matrix.storage_offset(),
+            matrix.data_ptr(), matrix.dtype, matrix.device,
+        )
+        if previous is None:
+            return f"matrix.{self._next_id}", 0, None
+        reusable = (
+            record[1] == metadata
+            and previous.config == self.config
+            and previous.packed.device == self.device
+            and previous._accepts(tiles)
+        )
+        return previous.name, previous._event, (previous if reusable else None)
+
     def _product(self, x, matrix):
         """``x @ matrix`` for the functional API with one status read before any state change.
 
-        The RHS and the input are quantized first, with finiteness recorded in a
-        device status word instead of host checks; a non-finite operand raises
-        the errors of memfast/functional.py:49-53 (A before B) while this
-        simulator is still unchanged.  Then the RHS is programmed
-        (``_matrix_for``) and read as ``AnalogMatrix.forward`` would.
+        The RHS and the input are quantized and, where possible, read at once,
+        with finiteness recorded in a device status word instead of host checks.
+        A single read of the status word then raises the errors of
+        memfast/functional.py:49-53 (A before B) while this simulator is still
+        unchanged; only afterwards is the RHS program committed
+        (``_matrix_for``) and its read event advanced, as AnalogMatrix.forward
+        would.  The read uses the name and event that commit will assign.
         """
+        config = self.config
         status = hip.status_word(self.device)
-        tiles = hip.weight_tiles(matrix.T, self.config, status=status)
+        tiles = hip.weight_tiles(matrix.T, config, status=status)
         flat = x.reshape(-1, x.shape[-1])
-        q, xscale = hip.input_tiles(flat, self.config, status=status)
+        q, xscale = hip.input_tiles(flat, config, status=status)
+        name, event, reused = self._program_plan(matrix, tiles)
+        speculative = (
+            self.mode == "default"
+            and event < 2**63
+            and (reused is None or reused.input_scale is None)
+        )
+        output = None
+        if speculative:
+            out_features = matrix.shape[1]
+            p = math.ceil(out_features / config.array_size[1])
+            tag = int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little")
+            packed, codes, wscale = tiles
+            output = hip.mm(q, xscale, packed, codes if hip.mm_kernel(
+                config, q.shape[0], q.shape[1], p) or config.wide else None,
+                wscale.reshape(-1, p * config.array_size[1]), config, config.seed ^ tag, event,
+                variant=TILE_VARIANTS[KERNEL_TILES[0]], status=status)
         flags = int(status.item())
         if flags & hip.STATUS_INPUT:
             raise ValueError("A must be finite")
         if flags & hip.STATUS_WEIGHT:
             raise ValueError("B must be finite")
         program = self._matrix_for(matrix, tiles=tiles)
-        if program.input_scale is not None:
-            q, xscale = hip.input_tiles(flat, self.config, program.input_scale)
-        return program._run(x, q, xscale)
+        if not speculative:
+            if program.input_scale is not None:
+                q, xscale = hip.input_tiles(flat, config, program.input_scale)
+            return program._run(x, q, xscale)
+        output = output[:, : program.out_features].contiguous()
+        finite = not flags & hip.STATUS_OUTPUT
+        if not finite and not config.wide:
+            output, finite = program._execute_checked(q, xscale, default_schedule(config), event,
+                                                      stable=True)
+        return program._finish(x, output, finite)
 
     def map_quantized(self, codes, scales, *, zero_points=None, bias=None, name=None):
         """Import integer [O,K] weights as ``scales * (codes - zero_points)``."""
@@ -670,8 +715,12 @@ class AnalogMatrix(nn.Module):
                     self._prepared[key] = self.simulator._select(self, x, q, xscale, event)
             schedule = self._prepared[key]
         output, finite = self._execute_checked(q, xscale, schedule, event)
+        return self._finish(x, output, finite)
+
+    def _finish(self, x, output, finite):
+        """Cast to the input dtype, check finiteness, advance the read event."""
         same_dtype = output.dtype == x.dtype
-        output = output.reshape(*shape[:-1], self.out_features).to(x.dtype)
+        output = output.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
         if not (finite and same_dtype) and not torch.isfinite(output).all():
             raise FloatingPointError("nonfinite analog output")
         self._event += 1
