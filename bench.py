@@ -70,6 +70,137 @@ def time_steps(fn, steps, warmup):
     return elapsed / steps * 1e3, total_ms / max(1, launches)
 
 
+def timed(fn, repeats=1):
+    """Seconds per call of fn (after one untimed call), synchronized."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(repeats):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - start) / repeats
+
+
+def resnet18():
+    """ResNet-18 (BasicBlock [2, 2, 2, 2], 1000 classes), Kaiming-normal conv init."""
+    from torch import nn
+
+    class Block(nn.Module):
+        def __init__(self, cin, cout, stride):
+            super().__init__()
+            self.conv1 = nn.Conv2d(cin, cout, 3, stride, 1, bias=False)
+            self.bn1 = nn.BatchNorm2d(cout)
+            self.conv2 = nn.Conv2d(cout, cout, 3, 1, 1, bias=False)
+            self.bn2 = nn.BatchNorm2d(cout)
+            self.down = None
+            if stride != 1 or cin != cout:
+                self.down = nn.Sequential(nn.Conv2d(cin, cout, 1, stride, bias=False),
+                                          nn.BatchNorm2d(cout))
+
+        def forward(self, x):
+            out = self.bn1(self.conv1(x)).relu()
+            out = self.bn2(self.conv2(out))
+            return (out + (x if self.down is None else self.down(x))).relu()
+
+    layers = [nn.Conv2d(3, 64, 7, 2, 3, bias=False), nn.BatchNorm2d(64), nn.ReLU(),
+              nn.MaxPool2d(3, 2, 1)]
+    cin = 64
+    for cout, stride in ((64, 1), (128, 2), (256, 2), (512, 2)):
+        layers += [Block(cin, cout, stride), Block(cout, cout, 1)]
+        cin = cout
+    layers += [nn.AdaptiveAvgPool2d(1), nn.Flatten(), nn.Linear(512, 1000)]
+    model = nn.Sequential(*layers)
+    for module in model.modules():
+        if isinstance(module, nn.Conv2d):
+            nn.init.kaiming_normal_(module.weight, mode="fan_out", nonlinearity="relu")
+    return model.eval()
+
+
+def secondary(device):
+    """The other BASELINE configurations, one timed run each (latency or throughput)."""
+    import torch
+    from torch import nn
+
+    import memfast_amd as memfast
+
+    out = {}
+    int8 = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                weight_slice=(1, 1, 2, 2, 2))
+    # Config 1: README first simulation (4x128 @ 128x32, write variation).
+    cfg = memfast.Config(**int8, array_size=(128, 128), rows_per_read=32,
+                         weight_quant_gran=(32, 1), input_quant_gran=(1, 32), adc_bits=7,
+                         nonidealities=memfast.Nonidealities(write_variation=0.02))
+    torch.manual_seed(135)
+    a, b = torch.randn(4, 128, device=device), torch.randn(128, 32, device=device)
+    sim = memfast.Simulator(cfg, device=device)
+    seconds = timed(lambda: sim.mm(a, b), 50)
+    out["config1_readme_mm"] = dict(us_per_call=round(seconds * 1e6, 1), macs=4 * 128 * 32)
+    # Config 3: converted 1-layer GRU (40 -> 512), batch 32, 200 steps.
+    cfg = memfast.Config(**int8, array_size=(128, 128), rows_per_read=32, adc_bits=7,
+                         nonidealities=memfast.Nonidealities(write_variation=0.02))
+    torch.manual_seed(135)
+    gru = nn.GRU(40, 512, 1).to(device)
+    analog = memfast.convert_model(gru, memfast.Simulator(cfg, device=device))
+    x = torch.randn(200, 32, 40, device=device)
+    seconds = timed(lambda: analog(x))
+    macs = 200 * 32 * (40 + 512) * 3 * 512
+    out["config3_gru"] = dict(ms_per_sequence=round(seconds * 1e3, 2),
+                              us_per_step=round(seconds / 200 * 1e6, 1),
+                              gmac_per_s=round(macs / seconds / 1e9, 2))
+    # Config 4: ResNet-18, batch 64 at 224^2, every Conv2d/Linear converted, fixed input
+    # scales from a 4-batch synthetic calibration, write variation + 0.1% stuck-at faults.
+    cfg = memfast.Config(**int8, array_size=(256, 256), rows_per_read=64,
+                         weight_quant_gran=(None, 1), adc_bits=8,
+                         nonidealities=memfast.Nonidealities(write_variation=0.02,
+                                                             stuck_at_low=0.0005,
+                                                             stuck_at_high=0.0005))
+    torch.manual_seed(135)
+    model = resnet18().to(device)
+    maxima = {}
+    hooks = [module.register_forward_pre_hook(
+        lambda module, inputs, name=name: maxima.__setitem__(
+            name, max(maxima.get(name, 0.0), float(inputs[0].detach().abs().amax()))))
+        for name, module in model.named_modules() if isinstance(module, (nn.Conv2d, nn.Linear))]
+    with torch.no_grad():
+        for _ in range(4):
+            model(torch.randn(16, 3, 224, 224, device=device))
+    for hook in hooks:
+        hook.remove()
+    analog = memfast.convert_model(model, memfast.Simulator(cfg, device=device))
+    upper = (1 << (cfg.activation_bits - 1)) - 1
+    for name, module in analog.named_modules():
+        if name in maxima:
+            scale = max(maxima[name] if maxima[name] > 0 else 1.0, 1.1754943508222875e-38) / upper
+            matrices = module.matrices if hasattr(module, "matrices") else [module]
+            for matrix in matrices:
+                matrix.set_input_scale(scale)
+    images = torch.randn(64, 3, 224, 224, device=device)
+    with torch.no_grad():
+        seconds = timed(lambda: analog(images))
+    out["config4_resnet18"] = dict(ms_per_batch=round(seconds * 1e3, 1), batch=64,
+                                   images_per_s=round(64 / seconds, 1),
+                                   gmac_per_s=round(116.0e9 / seconds / 1e9, 1))
+    # Config 5 (sample): one q_proj 4096x4096 on 2048 tokens, BFP bw_e=8 16-bit inputs
+    # (1,1,2,2,2,2,2,2,2) x INT4 weights (1,1,2), drift + read noise; default schedule.
+    cfg = memfast.Config(activation_bits=16, weight_bits=4,
+                         input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2), weight_slice=(1, 1, 2),
+                         bw_e=8, adc_bits=(6, 6, 7),
+                         nonidealities=memfast.Nonidealities(read_variation=0.01,
+                                                             drift_coefficient=0.05,
+                                                             drift_time=100.0))
+    torch.manual_seed(135)
+    tokens = torch.randn(2048, 4096, device=device)
+    tokens[:, torch.randperm(4096, device=device)[:41]] *= 20   # 1% outlier channels
+    weight = torch.randn(4096, 4096, device=device) * 0.02
+    sim = memfast.Simulator(cfg, device=device)
+    seconds = timed(lambda: sim.mm(tokens, weight))
+    out["config5_llm_q_proj"] = dict(ms_per_call=round(seconds * 1e3, 1), tokens=2048,
+                                     gmac_per_s=round(2048 * 4096 * 4096 / seconds / 1e9, 2))
+    return out
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -77,6 +208,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--noisy-steps", type=int, default=2)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-secondary", action="store_true",
+                        help="skip the timing of BASELINE configurations 1, 3, 4 and 5")
     parser.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                         help="first run one device-to-device copy of MIB MiB (a known-size "
                              "kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -123,6 +256,8 @@ def main():
                      value=round(macs / (noisy_ms * 1e-3) / 1e9, 3), unit="GMAC/s",
                      config="write_variation=0.02, read_variation=0.01 shared, "
                             "adc_nonlinearity=0.1")
+
+    others = None if args.no_secondary else secondary(device)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -172,6 +307,7 @@ def main():
                            "(HIP events on its stream); traffic = HBM bytes per launch"),
         noisy=noisy,
         cpu_baseline=cpu,
+        secondary=others,
         kernels=kernels,
     )
     print(json.dumps(line), flush=True)
