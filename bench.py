@@ -37,7 +37,7 @@ HBM_PEAK_GBS = 8000.0
 # 225.1 MiB read + 64.0 MiB written.  Summary and commands:
 # profiles/k_ideal_config2_pmc.md.  Only valid for the kernel sources it was
 # measured on (hash prefix below); otherwise the bench reports null.
-MEASURED_TRAFFIC = dict(kernels="ce3a6329d20ce4c8", bytes=303186787)
+MEASURED_TRAFFIC = dict(kernels="7f1036e682691187", bytes=303676060)
 
 
 def cpu_model():
