@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 2
+#define MF_ABI_VERSION 3
 #define MF_MAX_SLICES 32
 
 enum {
@@ -211,7 +211,10 @@ int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, i
                              void *stream);
 /* mf_restore, mf_partial and mf_mm for wide codes (totals and outputs FP64;
  * the fused read restores with restore_scales in FP64 and sums in torch's
- * FP64 order). */
+ * FP64 order).  mf_mm_wide uses the noisy-device bf16 MFMA read when the
+ * configuration allows it (mf_mm_kernel reports 3) and `workspace` holds at
+ * least the 64-column minimum of mf_mm_workspace (smaller than its full
+ * figure: column chunks); otherwise the general read. */
 int mf_restore_wide(const mf_config *cfg, const uint32_t *packed, int64_t m, int64_t p,
                     int64_t begin, int64_t end, uint32_t seed, uint64_t event, void *g,
                     void *stream);
@@ -220,8 +223,17 @@ int mf_partial_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t 
                     uint32_t seed, uint64_t event, double *totals, int32_t *codes, void *stream);
 int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, int64_t n, int64_t m,
                const uint32_t *packed, const double *wscale, int64_t p, const void *g,
-               uint32_t seed, uint64_t event, double *out, int64_t ldo, uint32_t *status,
-               void *stream);
+               uint32_t seed, uint64_t event, double *out, int64_t ldo, void *workspace,
+               int64_t workspace_bytes, uint32_t *status, void *stream);
+/* Integer slice totals T [n, m*Gr, p*C] (FP64) of the wide noisy-device MFMA
+ * read (mf_mm_kernel 3), for parity tests: the values mf_partial_wide returns
+ * for tiles [0, p).  g NULL samples conductances from packed (seed, event), or
+ * g is an injected FP32 [m][p][W][R][C] tensor.  MF_E_UNSUPPORTED when
+ * mf_mm_wide would not use that kernel. */
+int mf_mm_totals_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t m,
+                      const uint32_t *packed, int64_t p, const float *g, uint32_t seed,
+                      uint64_t event, double *totals, void *workspace, int64_t workspace_bytes,
+                      void *stream);
 
 /* Benchmark timing of mf_mm's main read kernel (no reference counterpart; the
  * reference times whole candidate calls with CUDA events, memfast/simulator.py:306-316):
@@ -246,8 +258,9 @@ int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
                  const uint8_t *packed_t, int64_t p, const float *g, uint32_t seed, uint64_t event,
                  float *totals, void *workspace, int64_t workspace_bytes, void *stream);
 
-/* Kernel selected by mf_mm for this shape: 0 = general, 1 = MFMA ideal,
- * 2 = MFMA noisy (bf16 split conductances). */
+/* Kernel selected by mf_mm (mf_mm_wide) for this shape: 0 = general, 1 = MFMA
+ * ideal, 2 = MFMA noisy (bf16 split conductances), 3 = MFMA noisy for wide
+ * codes. */
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
                  int32_t *kernel_id);
 

@@ -358,6 +358,163 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
     return check_launch("noisy MFMA read");
 }
 
+// Whether every output column of a wide read uses the plain cascade of torch's
+// FP64 sum (columns beyond 16 * floor(width*C / 16) of a two-tile chunk are
+// interleaved).
+bool all_cascade_columns_wide(int C, i64 p) {
+    for (i64 first = 0; first < p; first += 2) {
+        const i64 wc = ((p - first) < 2 ? (p - first) : 2) * C;
+        if (wc % 16) return false;
+    }
+    return true;
+}
+
+// Wide noisy-device MFMA eligibility and plan (noisy_wide.hip): the narrow
+// kernel's device model, input codes of at most 16 bits with digits up to 255,
+// fewer than 256 reads, exact int32 totals.
+bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *plan, int *ks,
+                           bool *small, const char **why) {
+    if (!cfg->wide) { *why = "narrow codes"; return false; }
+    if (cfg->precise) { *why = "FP64 currents"; return false; }
+    if (cfg->has_vnoise) { *why = "voltage variation"; return false; }
+    if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
+    if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
+        *why = "rows_per_read must be 32 or 64 and divide the array rows";
+        return false;
+    }
+    if (cfg->activation_bits > 16) { *why = "input codes wider than 16 bits"; return false; }
+    if (cfg->n_in > WIDE_MFMA_MAX_A || cfg->n_w > WIDE_MFMA_MAX_W) { *why = "too many slices"; return false; }
+    const i64 G = m * cfg->reads;
+    if (G >= 256) { *why = "256 or more reads per output"; return false; }
+    if (!all_cascade_columns_wide(cfg->cols, p)) { *why = "interleaved summation columns"; return false; }
+    bool all_small = true;
+    double fa_sum = 0.0, fw_sum = 0.0;
+    for (int a = 0; a < cfg->n_in; ++a) {
+        if (cfg->in_mask[a] > 255) { *why = "input digits above 255"; return false; }
+        all_small = all_small && cfg->in_mask[a] <= 3;
+        fa_sum += std::fabs(double(cfg->in_factor[a]));
+    }
+    for (int w = 0; w < cfg->n_w; ++w) fw_sum += std::fabs(double(cfg->w_factor[w])) * cfg->adc_max[w];
+    if (fa_sum * fw_sum >= 2147483647.0) { *why = "slice totals exceed int32"; return false; }
+    for (int a = 0; a < cfg->n_in; ++a)
+        for (int w = 0; w < cfg->n_w; ++w)
+            if (std::fabs(double(cfg->in_factor[a]) * double(cfg->w_factor[w])) >= 8388608.0) {
+                *why = "slice factor products beyond 24 bits";
+                return false;
+            }
+    memset(plan, 0, sizeof(*plan));
+    plan->n_in = cfg->n_in;
+    plan->n_w = cfg->n_w;
+    i64 factor_sum = 0;
+    for (int w = 0; w < cfg->n_w; ++w) {
+        plan->k1[w] = float(cfg->d_voltage * double(cfg->w_mask[w]) * cfg->d_inv_unit);
+        plan->top[w] = float(cfg->adc_max[w]);
+        plan->alpha[w] = cfg->has_nonlinear ? cfg->f_alpha_over_max[w] : 0.0f;
+        plan->fw[w] = int(cfg->w_factor[w]);
+    }
+    for (int a = 0; a < cfg->n_in; ++a) {
+        plan->fa[a] = int(cfg->in_factor[a]);
+        plan->in_shift[a] = cfg->in_shift[a];
+        plan->in_mask2[a] = u32(cfg->in_mask[a]) * 0x00010001u;
+        for (int w = 0; w < cfg->n_w; ++w) factor_sum += cfg->in_factor[a] * cfg->w_factor[w];
+    }
+    plan->bias = u32(0) - u32(u64(factor_sum) * 0x400000u);
+    *ks = cfg->read_rows / 16;
+    *small = all_small;
+    return true;
+}
+
+// Workspace of the wide MFMA read: 16-bit input codes, then the conductance
+// terms of up to every 32-column block (3 bf16 terms per cell and slice).
+i64 wide_codes_bytes(i64 n, i64 m, const mf_config *cfg) { return align256(n * m * cfg->rows * 2); }
+i64 wide_block_bytes(const mf_config *cfg, i64 m) { return i64(cfg->n_w) * 32 * m * cfg->rows * 3 * 2; }
+
+bool wide_extent_ok(i64 n, i64 m, const mf_config *cfg) {
+    const i64 kp = m * cfg->rows;
+    return 64 * kp <= 0x7FFFFFFF && (n + 127) / 128 <= 65535;
+}
+
+template <int KS, bool NL, bool SMALL>
+int launch_noisy_wide_kernel(dim3 grid, size_t lds, hipStream_t s, const NoisyWidePlan &plan,
+                             const NoisyWideArgs &args) {
+    // Dynamic LDS above 64 KiB is opted into once per device.
+    static u64 configured = 0;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return fail(MF_E_HIP, "hipGetDevice failed");
+    const u64 bit = u64(1) << (device & 63);
+    if (!(configured & bit)) {
+        const hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&k_noisy_wide<KS, NL, SMALL>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess)
+            return fail(MF_E_HIP, "wide MFMA read: LDS attribute: %s", hipGetErrorString(e));
+        configured |= bit;
+    }
+    hipLaunchKernelGGL((k_noisy_wide<KS, NL, SMALL>), grid, dim3(256), lds, s, plan, args);
+    return MF_OK;
+}
+
+// Repack codes to 16 bits, split conductances and run k_noisy_wide over column
+// chunks that fit the workspace.  g: optional injected conductances.
+int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, bool small,
+                      const u32 *q, const double *xscale, i64 n, i64 m, const u32 *packed,
+                      const double *wscale, i64 p, const float *g, u32 seed, u64 event,
+                      double *out, i64 ldo, void *workspace, i64 bytes, int totals, u32 *status,
+                      hipStream_t s) {
+    const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
+    const i64 codes_bytes = wide_codes_bytes(n, m, cfg);
+    const i64 per_block = wide_block_bytes(cfg, m);
+    const i64 max_cb = (bytes - codes_bytes) / per_block;
+    if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
+    const size_t lds = size_t(2) * cfg->n_w * 3 * ks * 1024;
+    if (lds > 160 * 1024) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
+    uint16_t *q16 = static_cast<uint16_t *>(workspace);
+    uint4 *gs = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + codes_bytes);
+    hipLaunchKernelGGL(k_codes16, dim3(grid_for(n * kp)), dim3(256), 0, s, q, n * kp, q16);
+    for (i64 c_begin = 0; c_begin < ncols; c_begin += max_cb * 32) {
+        const i64 cols = (ncols - c_begin) < max_cb * 32 ? (ncols - c_begin) : max_cb * 32;
+        const i64 CB = (cols + 31) / 32;
+        const i64 threads = CB * G * cfg->n_w * ks * 64;
+        if (ks == 2)
+            hipLaunchKernelGGL(k_split_wide<2>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
+                               packed, g, m, p, ncols, seed, event, c_begin, CB, gs);
+        else
+            hipLaunchKernelGGL(k_split_wide<4>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
+                               packed, g, m, p, ncols, seed, event, c_begin, CB, gs);
+        NoisyWideArgs args{};
+        args.q16 = q16;
+        args.gs = gs;
+        args.xscale = xscale;
+        args.wscale = wscale;
+        args.out = out;
+        args.status = status;
+        args.n = n;
+        args.kp = kp;
+        args.G = G;
+        args.ldo = ldo;
+        args.ldws = ncols;
+        args.ncols = ncols;
+        args.c_begin = c_begin;
+        args.totals = totals;
+        const dim3 grid{unsigned(CB), unsigned((n + 127) / 128), 1u};
+        const bool nl = cfg->has_nonlinear != 0;
+        int launched;
+#define MF_WIDE_LAUNCH(KS)                                                                       \
+    if (nl) launched = small ? launch_noisy_wide_kernel<KS, true, true>(grid, lds, s, plan, args) \
+                             : launch_noisy_wide_kernel<KS, true, false>(grid, lds, s, plan, args); \
+    else launched = small ? launch_noisy_wide_kernel<KS, false, true>(grid, lds, s, plan, args)  \
+                          : launch_noisy_wide_kernel<KS, false, false>(grid, lds, s, plan, args);
+        if (ks == 4) {
+            MF_WIDE_LAUNCH(4)
+        } else {
+            MF_WIDE_LAUNCH(2)
+        }
+#undef MF_WIDE_LAUNCH
+        if (launched) return launched;
+    }
+    return check_launch("wide noisy MFMA read");
+}
+
 SliceLayout layout_of(const int32_t *shift, const int32_t *mask, int count) {
     SliceLayout l{};
     l.count = count;
@@ -659,6 +816,14 @@ static bool ideal_extent_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
            (n + 63) / 64 <= 65535 && (ncols + 31) / 32 <= 65535;
 }
 
+static bool wide_plan_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
+    NoisyWidePlan plan;
+    int ks = 0;
+    bool small = false;
+    const char *why = "";
+    return wide_extent_ok(n, m, cfg) && build_noisy_wide_plan(cfg, m, p, &plan, &ks, &small, &why);
+}
+
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
                  int32_t *kernel_id) {
     int status = check_config(cfg);
@@ -675,6 +840,8 @@ int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t 
     else if (has_packed_t && noisy_extent_ok(n, m, cfg) &&
              build_noisy_plan(cfg, m, p, &noisy, &ks, &why))
         *kernel_id = 2;
+    else if (wide_plan_ok(cfg, n, m, p))
+        *kernel_id = 3;
     else
         *kernel_id = 0;
     return MF_OK;
@@ -695,6 +862,8 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64
         *bytes = xb + wb;
     } else if (build_noisy_plan(cfg, m, p, &noisy, &ks, &why)) {
         *bytes = (p * cfg->cols + 63) / 64 * 2 * noisy_block_bytes(cfg, m);
+    } else if (wide_plan_ok(cfg, n, m, p)) {
+        *bytes = wide_codes_bytes(n, m, cfg) + (p * cfg->cols + 31) / 32 * wide_block_bytes(cfg, m);
     } else {
         *bytes = 0;
     }
@@ -997,13 +1166,32 @@ int mf_partial_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t 
 
 int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, int64_t n, int64_t m,
                const uint32_t *packed, const double *wscale, int64_t p, const void *g,
-               uint32_t seed, uint64_t event, double *out, int64_t ldo, uint32_t *status,
-               void *stream) {
+               uint32_t seed, uint64_t event, double *out, int64_t ldo, void *workspace,
+               int64_t workspace_bytes, uint32_t *status, void *stream) {
     const int valid = check_wide(cfg);
     if (valid) return valid;
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
         ldo < p * cfg->cols)
         return fail(MF_E_INVALID, "invalid mm arguments");
+    NoisyWidePlan wplan;
+    int ks = 0;
+    bool small = false;
+    const char *why = "";
+    if (!g && workspace && (reinterpret_cast<uintptr_t>(workspace) % 256) == 0 &&
+        wide_extent_ok(n, m, cfg) && build_noisy_wide_plan(cfg, m, p, &wplan, &ks, &small, &why) &&
+        workspace_bytes >= wide_codes_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m)) {
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+        const int launched = launch_noisy_wide(cfg, wplan, ks, small, q, xscale, n, m, packed,
+                                               wscale, p, nullptr, seed, event, out, ldo,
+                                               workspace, workspace_bytes, 0, status, s);
+        if (timing.first) {
+            hipEventRecord(timing.second, s);
+            g_profile.pending.push_back(timing);
+        }
+        return launched;
+    }
     if (!g && needs_conductances(cfg))
         return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
     GeneralArgs args{};
@@ -1037,6 +1225,30 @@ int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, in
         g_profile.pending.push_back(timing);
     }
     return launched;
+}
+
+int mf_mm_totals_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t m,
+                      const uint32_t *packed, int64_t p, const float *g, uint32_t seed,
+                      uint64_t event, double *totals, void *workspace, int64_t workspace_bytes,
+                      void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!q || !packed || !totals || !workspace || n < 1 || m < 1 || p < 1)
+        return fail(MF_E_INVALID, "invalid totals arguments");
+    if (reinterpret_cast<uintptr_t>(workspace) % 256)
+        return fail(MF_E_INVALID, "workspace must be 256-byte aligned");
+    NoisyWidePlan plan;
+    int ks = 0;
+    bool small = false;
+    const char *why = "";
+    if (!wide_extent_ok(n, m, cfg) || !build_noisy_wide_plan(cfg, m, p, &plan, &ks, &small, &why))
+        return fail(MF_E_UNSUPPORTED, "wide MFMA read not applicable: %s", why);
+    if (workspace_bytes < wide_codes_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m))
+        return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
+    const i64 ncols = p * cfg->cols;
+    return launch_noisy_wide(cfg, plan, ks, small, q, nullptr, n, m, packed, nullptr, p, g, seed,
+                             event, totals, ncols, workspace, workspace_bytes, 1, nullptr,
+                             static_cast<hipStream_t>(stream));
 }
 
 int mf_profile_kernels(int32_t enable) {

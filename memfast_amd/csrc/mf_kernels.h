@@ -126,6 +126,40 @@ __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, co
 template <int KS, int NA, bool NONLINEAR>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
 
+// ---- noisy-device MFMA read, wide configurations (noisy_wide.hip) ----------
+// Same ADC model as NoisyPlan; integer totals accumulate modulo 2^32 as
+// fa*fw*(0x400000 + code) and `bias` = -0x400000 * sum(fa*fw) restores them.
+constexpr int WIDE_MFMA_MAX_A = 16;
+constexpr int WIDE_MFMA_MAX_W = 8;
+struct NoisyWidePlan {
+    int n_in, n_w;
+    float k1[WIDE_MFMA_MAX_W], top[WIDE_MFMA_MAX_W], alpha[WIDE_MFMA_MAX_W];
+    int fw[WIDE_MFMA_MAX_W];
+    int fa[WIDE_MFMA_MAX_A];
+    int in_shift[WIDE_MFMA_MAX_A];
+    u32 in_mask2[WIDE_MFMA_MAX_A];   // input slice mask in both 16-bit halves
+    u32 bias;
+};
+
+struct NoisyWideArgs {
+    const uint16_t *q16;   // [n, kp] input codes, 16 bits
+    const uint4 *gs;       // conductance terms [CB][G][W][3][KS][64 lanes] of the column chunk
+    const double *xscale;  // [n, G]
+    const double *wscale;  // [G, ldws]
+    double *out;           // fused: [n, ldo]; totals: [n, G, ldo]
+    u32 *status;           // optional: MF_STATUS_OUTPUT for a non-finite fused output
+    i64 n, kp, G, ldo, ldws, ncols, c_begin;
+    int totals;
+};
+
+__global__ void k_codes16(const u32 *q, i64 count, uint16_t *q16);
+template <int KS>
+__global__ void k_split_wide(const mf_config cfg, const u32 *packed, const float *g_in, i64 m,
+                             i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin, i64 CB,
+                             uint4 *gs);
+template <int KS, bool NONLINEAR, bool SMALL>
+__global__ void k_noisy_wide(const NoisyWidePlan plan, const NoisyWideArgs args);
+
 // ---- FP64 restore and read sum (stable.hip) --------------------------------
 __global__ void k_stable_sum(const float *totals, i64 n, i64 G, i64 wc, const float *xscale,
                              const float *wscale, i64 ldws, i64 col0, double *out, i64 ldo,

@@ -1,0 +1,333 @@
+// Noisy-device sliced array read for wide configurations (precision above 8
+// bits or BFP inputs, memfast/config.py `wide`) on gfx950 bf16 MFMA, fused with
+// the ADC, the signed shift-add, the FP64 scale restore and torch's FP64
+// read-order summation.  Only `out` (FP64) is written.
+//
+// Model (memfast/reference.py:63-117, memfast/simulator.py:57-66, 578-585):
+// per read group g, input slice a and weight slice w,
+//   I = sum_r (V * da/Ma) * (g[r,c] - L),   z = I * Ma*Mw / unit,
+//   z = z / (1 + |alpha/max_w * z|) (S-curve),  code = round(clamp(z, 0, max_w)),
+//   T = sum_a sum_w fa*fw*code                 (exact integer)
+//   out[n,c] = sum_g restore_scales(T, xs[n,g], ws[g,c])   (FP64, torch order)
+// As in the narrow kernel, z = (V*Mw/unit) * sum_r da * (g - L): input digits
+// are exact in bf16 and g - L is split into three bf16 terms that sum to it
+// exactly, so three bf16 MFMAs with FP32 accumulation give the FP32 current.
+//
+// Integer totals: the rounded, clamped count is formed in the exponent-fixed
+// domain y = fma(I, k1, 1.5*2^23) (one rounding, half-even), med3-clamped to
+// [1.5*2^23, 1.5*2^23 + max_w]; the low 24 bits of y are 0x400000 + code, and
+// v_mad_i32_i24 accumulates fa*fw*(0x400000 + code) modulo 2^32.  The constant
+// 0x400000 * sum(fa*fw) is removed at the end; the host checks that every true
+// total fits in int32, so the modular sum is exact.
+//
+// Layout: k_split_wide writes the conductance terms of each 32-column block
+// and read as one contiguous run [w][term][ks] of 1 KiB fragments (MFMA lane
+// order).  Block = 4 waves on the same 32 columns and 128 vectors (32 per
+// wave); per read the block copies the run into LDS with global_load_lds
+// (double-buffered, one barrier per read) and every wave reads it from there.
+// Input codes are repacked to 16 bits (k_codes16) so a lane's 8 rows of a
+// 16-row step are one 16-byte load.  Bound: VALU (digit expansion + ADC per
+// slice pair) with bf16 MFMA as co-bound.
+#include <cfloat>
+
+#include "mf_kernels.h"
+
+namespace mf {
+
+typedef __bf16 v8bf_w __attribute__((ext_vector_type(8)));
+typedef float v16f_w __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+namespace {
+
+__device__ __forceinline__ u32 bf16_round_bits(float x) {
+    const u32 b = __float_as_uint(x);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_bits_value(u32 bits) { return __uint_as_float(bits << 16); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_buffer(const void *base, i64 bytes) {
+    const int records = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : int(bytes < 0 ? 0 : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), short(0), records,
+                                             0x00020000);
+}
+
+// Digits of slice (shift, mask <= 3) of eight 16-bit codes (rows 0..7, two per
+// word, low half first) as eight bf16.  x = d0 | d1 << 16 selects, per output
+// byte, the low or high byte of bf16(d) from two 4-entry byte tables with one
+// v_perm: selector bytes (d0, 4 + d0, d1, 4 + d1) = x * 0x101 + 0x04000400.
+__device__ __forceinline__ v8bf_w digits_small(uint4 c, int shift, u32 mask2) {
+    constexpr u32 LO = 0x40008000u;   // low bytes of bf16(0), bf16(1), bf16(2), bf16(3)
+    constexpr u32 HI = 0x40403F00u;   // high bytes
+    uint4 r;
+    r.x = __builtin_amdgcn_perm(HI, LO, ((c.x >> shift) & mask2) * 0x101u + 0x04000400u);
+    r.y = __builtin_amdgcn_perm(HI, LO, ((c.y >> shift) & mask2) * 0x101u + 0x04000400u);
+    r.z = __builtin_amdgcn_perm(HI, LO, ((c.z >> shift) & mask2) * 0x101u + 0x04000400u);
+    r.w = __builtin_amdgcn_perm(HI, LO, ((c.w >> shift) & mask2) * 0x101u + 0x04000400u);
+    return __builtin_bit_cast(v8bf_w, r);
+}
+
+// Same for digits up to 255 (exact in bf16): convert each half and keep the
+// upper 16 bits of the FP32 values.
+__device__ __forceinline__ v8bf_w digits_any(uint4 c, int shift, u32 mask2) {
+    const u32 w[4] = {(c.x >> shift) & mask2, (c.y >> shift) & mask2, (c.z >> shift) & mask2,
+                      (c.w >> shift) & mask2};
+    u32 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o[i] = __builtin_amdgcn_perm(__float_as_uint(float(w[i] >> 16)),
+                                     __float_as_uint(float(w[i] & 0xFFFFu)), 0x07060302u);
+    return __builtin_bit_cast(v8bf_w, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// restore_scales of one total: (T * xs) * ws when no intermediate leaves the
+// normal FP64 range (then it equals the frexp/ldexp form exactly), else the
+// frexp/ldexp form itself.
+__device__ __forceinline__ double restore_fast(int total, double xs, double ws) {
+    if (total == 0) return 0.0;
+    const double v1 = double(total) * xs;
+    const double v2 = v1 * ws;
+    const double a1 = fabs(v1), a2 = fabs(v2);
+    if (a1 >= DBL_MIN && a2 >= DBL_MIN && a2 <= DBL_MAX) return v2;
+    return restore_f64(double(total), xs, ws);
+}
+
+}  // namespace
+
+__global__ void k_codes16(const u32 *q, i64 count, uint16_t *q16) {
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += i64(gridDim.x) * blockDim.x)
+        q16[i] = uint16_t(q[i]);
+}
+
+template <int KS>
+__global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u32 *packed,
+                                                    const float *g_in, i64 m, i64 p, i64 ncols,
+                                                    u32 seed, u64 event, i64 c_begin, i64 CB,
+                                                    uint4 *gs) {
+    constexpr int P = 16 * KS;
+    const int R = cfg.rows, C = cfg.cols, W = cfg.n_w;
+    const i64 G = m * R / P;
+    const i64 total = CB * G * W * KS * 64;
+    const u64 read_seed = event_seed(seed, event);
+    for (i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += i64(gridDim.x) * blockDim.x) {
+        i64 rest = t;
+        const int lane = int(rest & 63); rest >>= 6;
+        const int ks = int(rest % KS); rest /= KS;
+        const int w = int(rest % W); rest /= W;
+        const i64 g = rest % G;
+        const i64 cb = rest / G;
+        const int lr = lane & 31, h = lane >> 5;
+        const i64 c = c_begin + cb * 32 + lr;
+        const i64 k0 = g * P + ks * 16 + h * 8;
+        u32 terms[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        if (c < ncols) {
+            const i64 i = k0 / R, r0 = k0 - i * R;
+            const i64 tt = c / C, cc = c - tt * C;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const i64 r = r0 + j;
+                const u64 cell = u64((((i * p + tt) * W + w) * R + r) * C + cc);
+                float level;
+                if (g_in) {
+                    level = g_in[cell];
+                } else {
+                    const u32 code = packed[((i * p + tt) * R + r) * C + cc];
+                    level = cell_conductance<float>(cfg, code, w, cell, seed, read_seed);
+                }
+                const float delta = level - cfg.f_low;
+                const u32 hi = bf16_round_bits(delta);
+                const float r1 = delta - bf16_bits_value(hi);
+                const u32 mid = bf16_round_bits(r1);
+                const u32 lo = bf16_round_bits(r1 - bf16_bits_value(mid));
+                const int shift = 16 * (j & 1);
+                terms[0][j >> 1] |= hi << shift;
+                terms[1][j >> 1] |= mid << shift;
+                terms[2][j >> 1] |= lo << shift;
+            }
+        }
+        uint4 *dst = gs + ((((cb * G + g) * W + w) * 3) * KS + ks) * 64 + lane;
+#pragma unroll
+        for (int term = 0; term < 3; ++term)
+            dst[term * KS * 64] = make_uint4(terms[term][0], terms[term][1], terms[term][2],
+                                             terms[term][3]);
+    }
+}
+
+template __global__ void k_split_wide<2>(const mf_config, const u32 *, const float *, i64, i64,
+                                         i64, u32, u64, i64, i64, uint4 *);
+template __global__ void k_split_wide<4>(const mf_config, const u32 *, const float *, i64, i64,
+                                         i64, u32, u64, i64, i64, uint4 *);
+
+template <int KS, bool NONLINEAR, bool SMALL>
+__global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
+                                                       const NoisyWideArgs args) {
+    extern __shared__ __align__(16) uint4 sF[];   // [2][W * 3 * KS][64]
+    constexpr int P = 16 * KS;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int A = plan.n_in, W = plan.n_w;
+    const int G = int(args.G);
+    const int FR = W * 3 * KS;                    // fragments per read
+    const i64 cb = blockIdx.x;                    // chunk-relative 32-column block
+    const i64 v0 = i64(blockIdx.y) * 128 + wave * 32;
+    const i64 kp = args.kp;
+
+    // Conductance terms of this column block: [g][w][term][ks][lane].
+    const uint4 *frag = args.gs + cb * i64(G) * FR * 64 + lane;
+    auto fetch = [&](int g, int buf) {
+        const uint4 *src = frag + i64(g) * FR * 64;
+        for (int f = wave; f < FR; f += 4)
+            __builtin_amdgcn_global_load_lds(src + f * 64, (lds_void *)(sF + (buf * FR + f) * 64),
+                                             16, 0, 0);
+    };
+
+    // 16-bit input codes of this wave's 32 vectors (rows past n read as zero).
+    const i64 vrows = (args.n - v0) < 32 ? (args.n - v0) : 32;
+    const __amdgpu_buffer_rsrc_t qbuf =
+        wide_buffer(args.q16 + (vrows > 0 ? v0 : 0) * kp, (vrows > 0 ? vrows : 0) * kp * 2);
+    const int q_off = (lrow * int(kp) + lhalf * 8) * 2;
+    uint4 qc[KS], qn[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        qc[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               qbuf, q_off + ks * 32, 0, 0));
+
+    const i64 n_out = v0 + lrow;
+    const bool live_n = n_out < args.n;
+    const i64 col_tile = args.c_begin + cb * 32;   // absolute first column of the block
+    double acc0[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc0[r] = 0.0;
+
+    fetch(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    const float MAGIC = 12582912.0f;   // 1.5 * 2^23
+    for (int g = 0; g < G; ++g) {
+        const int cur = g & 1;
+        if (g + 1 < G) {
+            fetch(g + 1, cur ^ 1);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                qn[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       qbuf, q_off + (g + 1) * P * 2 + ks * 32, 0, 0));
+        }
+        u32 T[16];   // modulo 2^32, offset by 0x400000 * sum(fa*fw) (plan.bias undoes it)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[r] = 0u;
+        const uint4 *fl = sF + i64(cur) * FR * 64 + lane;
+        for (int w = 0; w < W; ++w) {
+            v8bf_w F[3][KS];
+#pragma unroll
+            for (int term = 0; term < 3; ++term)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    F[term][ks] = __builtin_bit_cast(v8bf_w, fl[((w * 3 + term) * KS + ks) * 64]);
+            const float k1 = plan.k1[w], top = MAGIC + plan.top[w], alpha = plan.alpha[w];
+            const int fw = plan.fw[w];   // |fa*fw| < 2^23: a signed 24-bit operand
+            for (int a = 0; a < A; ++a) {
+                const int shift = plan.in_shift[a];
+                const u32 mask2 = plan.in_mask2[a];
+                v16f_w I = {};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const v8bf_w B = SMALL ? digits_small(qc[ks], shift, mask2)
+                                           : digits_any(qc[ks], shift, mask2);
+#pragma unroll
+                    for (int term = 0; term < 3; ++term)
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B, I, 0, 0, 0);
+                }
+                const u32 f = u32(plan.fa[a] * fw);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float y;
+                    if (NONLINEAR) {
+                        float z = I[r] * k1;
+                        z = z * __builtin_amdgcn_rcpf(fmaf(fabsf(z), alpha, 1.0f));
+                        y = z + MAGIC;
+                    } else {
+                        y = fmaf(I[r], k1, MAGIC);
+                    }
+                    y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
+                    // low 24 bits of y: 0x400000 + code (v_mad_i32_i24)
+                    const int low = int(__float_as_uint(y) << 8) >> 8;
+                    T[r] += u32(low) * u32(int(f << 8) >> 8);
+                }
+            }
+        }
+
+        // FP64 restore and torch's cascade over reads (level step 16; level 1
+        // is kept in `out`, reads < 256).
+        if (args.totals) {
+            if (live_n) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+                    if (c < args.ncols)
+                        args.out[(n_out * G + g) * args.ldo + c] = double(int(T[r] + plan.bias));
+                }
+            }
+        } else {
+            const double xs = live_n ? args.xscale[n_out * G + g] : 0.0;
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const i64 c = col_tile + qd * 8 + lhalf * 4;
+                double ws[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    ws[e] = (c + e < args.ncols) ? args.wscale[i64(g) * args.ldws + c + e] : 0.0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc0[qd * 4 + e] = acc0[qd * 4 + e] + restore_fast(int(T[qd * 4 + e] + plan.bias),
+                                                                       xs, ws[e]);
+            }
+            if (((g + 1) & 15) == 0) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+                    if (live_n && c < args.ncols) {
+                        double *dst = args.out + n_out * args.ldo + c;
+                        *dst = g + 1 == 16 ? acc0[r] : *dst + acc0[r];
+                    }
+                    acc0[r] = 0.0;
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qc[ks] = qn[ks];
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+    if (args.totals || !live_n) return;
+
+    bool finite = true;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+        if (c >= args.ncols) continue;
+        double *dst = args.out + n_out * args.ldo + c;
+        const double s = acc0[r] + (G >= 16 ? *dst : 0.0);
+        *dst = s;
+        finite = finite && fabs(s) <= DBL_MAX;
+    }
+    if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
+}
+
+#define MF_NOISY_WIDE_INST(KS, NL, SMALL) \
+    template __global__ void k_noisy_wide<KS, NL, SMALL>(const NoisyWidePlan, const NoisyWideArgs);
+MF_NOISY_WIDE_INST(2, false, true)
+MF_NOISY_WIDE_INST(2, true, true)
+MF_NOISY_WIDE_INST(2, false, false)
+MF_NOISY_WIDE_INST(2, true, false)
+MF_NOISY_WIDE_INST(4, false, true)
+MF_NOISY_WIDE_INST(4, true, true)
+MF_NOISY_WIDE_INST(4, false, false)
+MF_NOISY_WIDE_INST(4, true, false)
+
+}  // namespace mf

@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -152,7 +152,9 @@ SIGNATURES = {
     "mf_partial_wide": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
                          _P, _P, _P], ct.c_int),
     "mf_mm_wide": ([_CFG, _P, _P, _I64, _I64, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
-                    _I64, _P, _P], ct.c_int),
+                    _I64, _P, _I64, _P, _P], ct.c_int),
+    "mf_mm_totals_wide": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
+                           _P, _I64, _P], ct.c_int),
     "mf_profile_kernels": ([_I32], ct.c_int),
     "mf_profile_collect": ([ct.POINTER(_I64), ct.POINTER(ct.c_double)], ct.c_int),
     "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, ct.POINTER(_I64)], ct.c_int),
@@ -613,11 +615,15 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
         check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
               "workspace size")
         workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
+    # Converted operands stay referenced until the launch is queued (a freed
+    # temporary could be handed to the next conversion by the caching allocator).
+    q, xscale = q.contiguous(), xscale.contiguous()
+    packed, wscale = packed.contiguous(), wscale.contiguous()
     with torch.cuda.device(q.device):
         check(
             library().mf_mm(
-                ct.byref(descriptor(config)), _ptr(q.contiguous()), _ptr(xscale.contiguous()), n,
-                m, _ptr(packed.contiguous()), _ptr(packed_t), _ptr(wscale.contiguous()), p,
+                ct.byref(descriptor(config)), _ptr(q), _ptr(xscale), n,
+                m, _ptr(packed), _ptr(packed_t), _ptr(wscale), p,
                 _ptr(g), seed, event, _ptr(out), out.stride(0), _ptr(workspace),
                 0 if workspace is None else workspace.numel(), variant, _ptr(status),
                 _stream(q.device),
@@ -632,23 +638,39 @@ def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductan
     p, c = packed.shape[1], config.array_size[1]
     codes = _u32(packed) if codes is None else _u32(codes)
     g = conductance
-    if g is None and needs_conductances(config):
+    workspace = None
+    if g is None and mm_kernel(config, n, m, p) == 3:
+        # The wide MFMA read samples conductances itself.
+        workspace = _workspace(config, n, m, p, q.device)
+    elif g is None and needs_conductances(config):
         g = restore(codes, config, seed, event, 0, p)
     if g is not None:
         g = _checked_conductance(g, config, m, p, r, c)
     if out is None:
         out = torch.empty((n, p * c), dtype=torch.float64, device=q.device)
+    q = _u32(q)
+    xscale = xscale.to(torch.float64).contiguous()
+    wscale = wscale.to(torch.float64).contiguous()
     with torch.cuda.device(q.device):
         check(
             library().mf_mm_wide(
-                ct.byref(descriptor(config)), _ptr(_u32(q)),
-                _ptr(xscale.to(torch.float64).contiguous()), n, m, _ptr(codes),
-                _ptr(wscale.to(torch.float64).contiguous()), p, _ptr(g), seed, event, _ptr(out),
-                out.stride(0), _ptr(status), _stream(q.device),
+                ct.byref(descriptor(config)), _ptr(q),
+                _ptr(xscale), n, m, _ptr(codes),
+                _ptr(wscale), p, _ptr(g), seed, event, _ptr(out),
+                out.stride(0), _ptr(workspace), 0 if workspace is None else workspace.numel(),
+                _ptr(status), _stream(q.device),
             ),
             "mm",
         )
     return out
+
+
+def _workspace(config, n, m, p, device):
+    """Device scratch for the MFMA reads (mf_mm_workspace bytes, 256-byte aligned)."""
+    size = ct.c_int64()
+    check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
+          "workspace size")
+    return torch.empty(max(1, size.value), dtype=torch.uint8, device=device)
 
 
 def stable_sum(totals, xscale, wscale, config, col0, out):
@@ -713,11 +735,12 @@ def mm_totals(q, packed_t, config, seed, event, *, conductance=None):
     workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
     groups = m * config.reads_per_array
     totals = torch.empty((n, groups, p, c), dtype=torch.float32, device=q.device)
+    q, packed_t = q.contiguous(), packed_t.contiguous()
     with torch.cuda.device(q.device):
         check(
             library().mf_mm_totals(
-                ct.byref(descriptor(config)), _ptr(q.contiguous()), n, m,
-                _ptr(packed_t.contiguous()), p, _ptr(g), seed, event, _ptr(totals),
+                ct.byref(descriptor(config)), _ptr(q), n, m,
+                _ptr(packed_t), p, _ptr(g), seed, event, _ptr(totals),
                 _ptr(workspace), workspace.numel(), _stream(q.device),
             ),
             "mm totals",
@@ -725,8 +748,41 @@ def mm_totals(q, packed_t, config, seed, event, *, conductance=None):
     return totals
 
 
+def mm_totals_wide(q, packed, config, seed, event, *, conductance=None):
+    """Slice totals T [N, m*Gr, p, C] (FP64) from the wide noisy-device MFMA kernel.
+
+    Same values as ``partial(q, packed, config, None, seed, event, 0, p)`` for a
+    wide configuration, up to ADC rounding-boundary flips; for parity tests.
+    ``packed`` is the [m, p, R, C] program (int64 or uint32 codes);
+    ``conductance`` injects FP32 conductances [m, p, W, R, C].
+    """
+    supported(config)
+    require_device(q)
+    n, m, r = q.shape
+    p, c = packed.shape[1], config.array_size[1]
+    g = None
+    if conductance is not None:
+        g = conductance.to(device=q.device, dtype=torch.float32).contiguous()
+        if tuple(g.shape) != (m, p, len(config.weight_layout), r, c):
+            raise ValueError("injected conductances must be [m, p, W, R, C]")
+    workspace = _workspace(config, n, m, p, q.device)
+    groups = m * config.reads_per_array
+    totals = torch.empty((n, groups, p, c), dtype=torch.float64, device=q.device)
+    q, packed = _u32(q), _u32(packed)
+    with torch.cuda.device(q.device):
+        check(
+            library().mf_mm_totals_wide(
+                ct.byref(descriptor(config)), _ptr(q), n, m, _ptr(packed), p, _ptr(g),
+                seed, event, _ptr(totals), _ptr(workspace), workspace.numel(), _stream(q.device),
+            ),
+            "mm totals",
+        )
+    return totals
+
+
 def mm_kernel(config, n, m, p, has_packed_t=True):
-    """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA (what ``mm`` launches).
+    """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA, 3: noisy-device MFMA for
+    wide codes (what ``mm`` launches).
 
     The kernels other than the general one read ``kernel_codes`` of the program."""
     out = ct.c_int32()

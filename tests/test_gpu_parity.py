@@ -630,3 +630,147 @@ def test_bfp_exponent_edges_on_gpu(hip_device, reference_vectors):
         scales = torch.from_numpy(v[f"bfp_edges_scale_{bits}_{bw_e}"])
         assert bits_equal(q.reshape(edges.shape).cpu().to(torch.int64) & 0xFFFFFFFF, codes)
         assert bits_equal(xs[:, 0].cpu(), scales[:, 0])
+
+
+# ---------------------------------------------------------------------------
+# Wide configurations on the noisy-device bf16 MFMA kernel (mm_kernel 3)
+# ---------------------------------------------------------------------------
+WIDE_MFMA = {
+    # BASELINE config 5's slicing: BFP16 x INT4, 64-row reads, 2-bit digits.
+    "bfp16_int4": (WIDE["bfp16_int4"][0], WIDE["bfp16_int4"][1], 70, 300, 150),
+    # 4-bit input digits (byte conversion path), 32-row reads, S-curve ADC.
+    "int12_s4": (dict(activation_bits=12, weight_bits=8, input_slice=(1, 3, 4, 4),
+                      weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,
+                      adc_bits=8), dict(write_variation=0.02, adc_nonlinearity=0.05), 45, 200, 70),
+    # BFP8 inputs, stuck-at faults and shared read noise, a ragged vector block.
+    "bfp8_p64": (dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                      weight_slice=(1, 1, 2, 2, 2), bw_e=4, array_size=(128, 64),
+                      rows_per_read=64, adc_bits=(6, 7, 7, 8, 8)),
+                 dict(write_variation=0.03, read_variation=0.02, stuck_at_low=0.01,
+                      stuck_at_high=0.01), 130, 400, 100),
+}
+
+
+def wide_mfma_case(name, seed):
+    kwargs, effects, n, k, o = WIDE_MFMA[name]
+    cfg = Config(**kwargs, nonidealities=Nonidealities(**effects))
+    gen = torch.Generator().manual_seed(seed)
+    a = torch.randn(n, k, generator=gen)
+    a[:, ::17] *= 20     # outlier channels
+    b = torch.randn(k, o, generator=gen) * 0.02
+    return cfg, a, b
+
+
+def flip_budget(cfg, diff):
+    codes = diff.numel() * len(cfg.input_layout) * len(cfg.weight_layout)
+    return max(1, 1e-4 * codes)
+
+
+@pytest.mark.parametrize("name", list(WIDE_MFMA))
+def test_wide_mfma_totals_with_injected_conductances(hip_device, name):
+    """Same integer slice totals as the oracle given the same conductances, except ADC flips."""
+    say("wide mfma totals", name)
+    cfg, a, b = wide_mfma_case(name, 41)
+    q, _ = oracle.input_tiles(a, cfg)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    n, m, r = q.shape
+    p = packed.shape[1]
+    assert hip.mm_kernel(cfg, n, m, p) == 3
+    seed, event = 777, 5
+    raw, _, _ = oracle.restored(packed, cfg, seed, event, 0, p)
+    expected = oracle.partial(q, packed, cfg, seed, event, 0, p, conductance=raw)
+    got = hip.mm_totals_wide(q.to(hip_device), packed.to(hip_device), cfg, seed, event,
+                             conductance=raw.to(hip_device)).cpu()
+    assert got.dtype == torch.float64 and got.shape == expected.shape
+    diff = got - expected.double()
+    flips = int((diff != 0).sum())
+    largest = max(abs(fa * fw) for _, _, fa in cfg.input_layout for _, _, fw in cfg.weight_layout)
+    say("  totals differing", flips, "of", diff.numel(), "max", diff.abs().max().item())
+    assert flips <= flip_budget(cfg, diff)
+    assert diff.abs().max().item() <= 2 * largest
+
+
+def test_wide_mfma_reference_vectors(hip_device, reference_vectors):
+    """The reference's own totals for the BFP16 x INT4 case, given its conductances."""
+    v = reference_vectors
+    cfg = wide_case("bfp16_int4")
+    q = torch.from_numpy(v["case_bfp16_int4_q"]).to(hip_device)
+    packed = torch.from_numpy(v["case_bfp16_int4_packed"]).to(hip_device)
+    seed = int(v["case_bfp16_int4_seed"])
+    n, m, _ = q.shape
+    assert hip.mm_kernel(cfg, n, m, packed.shape[1]) == 3
+    raw = torch.from_numpy(v["case_bfp16_int4_restored"]).to(hip_device)
+    got = hip.mm_totals_wide(q, packed, cfg, seed, 0, conductance=raw).cpu()
+    expected = torch.from_numpy(v["case_bfp16_int4_totals"])
+    diff = got - expected
+    say("  reference totals differing", int((diff != 0).sum()), "of", diff.numel())
+    assert int((diff != 0).sum()) <= flip_budget(cfg, diff)
+
+
+@pytest.mark.parametrize("name", list(WIDE_MFMA))
+def test_wide_mfma_sampled_conductances(hip_device, name):
+    """Conductances sampled on the GPU (counter RNG, OCML) against the oracle's samples."""
+    cfg, a, b = wide_mfma_case(name, 42)
+    q, _ = oracle.input_tiles(a, cfg)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    p = packed.shape[1]
+    seed, event = 31337, 2
+    expected = oracle.partial(q, packed, cfg, seed, event, 0, p)
+    got = hip.mm_totals_wide(q.to(hip_device), packed.to(hip_device), cfg, seed, event).cpu()
+    diff = got - expected.double()
+    flips = int((diff != 0).sum())
+    say("  sampled totals differing", flips, "of", diff.numel())
+    assert flips <= flip_budget(cfg, diff)
+
+
+@pytest.mark.parametrize("name", list(WIDE_MFMA))
+def test_wide_mfma_epilogue_and_mm(hip_device, name):
+    """Fused FP64 output = restore_scales + torch's FP64 read sum of the kernel's own totals,
+    bit for bit; Simulator.mm within the flip budget of the oracle for two read events."""
+    from memfast_amd import Simulator
+
+    cfg, a, b = wide_mfma_case(name, 43)
+    q, xs = oracle.input_tiles(a, cfg)
+    packed, ws = oracle.weight_tiles(b.T, cfg)
+    n, m, r = q.shape
+    p, c = packed.shape[1], cfg.array_size[1]
+    seed, event = 2024, 1
+    totals = hip.mm_totals_wide(q.to(hip_device), packed.to(hip_device), cfg, seed, event).cpu()
+    fused = hip.mm(q.to(hip_device), xs.to(hip_device), packed.to(hip_device), None,
+                   ws.reshape(-1, p * c).to(hip_device), cfg, seed, event).cpu()
+    assert fused.dtype == torch.float64
+    restored = oracle.execute(q, xs, packed, ws, cfg, seed, event, p * c, totals=totals)
+    assert bits_equal(fused, restored)
+    sim = Simulator(cfg, device=hip_device)
+    ad, bd = a.to(hip_device), b.to(hip_device)
+    for ev in (0, 1):
+        got = sim.mm(ad, bd).cpu()
+        ref = oracle.mm(a, b, cfg, event=ev)
+        rel = (got - ref).abs() / ref.abs().clamp_min(1e-6)
+        bad = (rel > 1e-5).float().mean().item()
+        say("  wide mm", name, "event", ev, "elements beyond 1e-5:", bad)
+        assert bad <= 0.02
+
+
+def test_wide_mfma_column_chunks(hip_device):
+    """A workspace of one 64-column chunk gives the same totals as the full workspace."""
+    cfg, a, b = wide_mfma_case("bfp8_p64", 44)
+    q, _ = oracle.input_tiles(a, cfg)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    qd, pd = q.to(hip_device), packed.to(hip_device)
+    full = hip.mm_totals_wide(qd, pd, cfg, 5, 0)
+    n, m, r = q.shape
+    p = packed.shape[1]
+    import ctypes as ct
+
+    lib = hip.library()
+    per_block = len(cfg.weight_layout) * 32 * m * r * 3 * 2
+    codes = (n * m * r * 2 + 255) // 256 * 256
+    workspace = torch.empty(codes + 2 * per_block, dtype=torch.uint8, device=hip_device)
+    chunked = torch.empty_like(full)
+    q32, p32 = hip._u32(qd), hip._u32(pd)
+    hip.check(lib.mf_mm_totals_wide(ct.byref(hip.descriptor(cfg)), hip._ptr(q32), n, m,
+                                    hip._ptr(p32), p, None, 5, 0, hip._ptr(chunked),
+                                    hip._ptr(workspace), workspace.numel(),
+                                    hip._stream(qd.device)), "chunked totals")
+    assert bits_equal(chunked, full)
