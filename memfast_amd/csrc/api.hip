@@ -1028,6 +1028,23 @@ int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t 
     return check_launch("stable sum");
 }
 
+// Group maxima |x| of an FP64 matrix into work[row group][col group] (cleared).
+static void launch_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
+                                 i64 ncg, u64 *work, u32 *status, u32 flag, hipStream_t s) {
+    const i64 chunks = (rows + COL_CHUNK_ROWS - 1) / COL_CHUNK_ROWS;
+    const i64 row_chunks = (cols + ROW_CHUNK_COLS - 1) / ROW_CHUNK_COLS;
+    if (gc == 1 && (cols + 63) / 64 <= 2147483647 && chunks <= 65535) {
+        hipLaunchKernelGGL(k_col_group_max_f64, dim3(unsigned((cols + 63) / 64), unsigned(chunks)),
+                           dim3(256), 0, s, x, rows, cols, ld, gr, work, status, flag);
+    } else if (gr == 1 && gc >= 64 && (rows + 3) / 4 <= 65535 && row_chunks <= 2147483647) {
+        hipLaunchKernelGGL(k_row_group_max_f64, dim3(unsigned(row_chunks), unsigned((rows + 3) / 4)),
+                           dim3(256), 0, s, x, rows, cols, ld, gc, ncg, work, status, flag);
+    } else {
+        hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(rows * cols)), dim3(256), 0, s, x, rows,
+                           cols, ld, gr, gc, ncg, work, status, flag);
+    }
+}
+
 // ---- wide configurations (u32 codes, FP64 scales and outputs) -------------
 int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k,
                             int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
@@ -1048,8 +1065,7 @@ int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, in
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(2 * nrg * ncg)), dim3(256), 0, s,
                        reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
-    hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(n * k)), dim3(256), 0, s, x, n, k, ld, gr, gc,
-                       ncg, work, status, u32(MF_STATUS_INPUT));
+    launch_group_max_f64(x, n, k, ld, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT), s);
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
                        nrg * ncg, bits, cfg->bw_e, upper, scale);
     hipLaunchKernelGGL(k_input_codes_f64, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
@@ -1101,8 +1117,7 @@ int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, i
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(2 * nrg * ncg)), dim3(256), 0, s,
                        reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
-    hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(k * o)), dim3(256), 0, s, b, k, o, ld, gr, gc,
-                       ncg, work, status, u32(MF_STATUS_WEIGHT));
+    launch_group_max_f64(b, k, o, ld, gr, gc, ncg, work, status, u32(MF_STATUS_WEIGHT), s);
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
                        nrg * ncg, bits, cfg->bw_e, upper, scale);
     hipLaunchKernelGGL(k_weight_codes_f64, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o, ld, R,

@@ -53,18 +53,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_buffer(const void *base, 
                                              0x00020000);
 }
 
+// x * 0x101 + bias in one v_mad_u32_u24 (x < 2^24); the compiler otherwise
+// emits a shift-add and an add.  `bias` is kept in a VGPR (one SGPR operand).
+__device__ __forceinline__ u32 mad_u24(u32 x, u32 mul, u32 bias) {
+    u32 r;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mul), "v"(bias));
+    return r;
+}
+
 // Digits of slice (shift, mask <= 3) of eight 16-bit codes (rows 0..7, two per
 // word, low half first) as eight bf16.  x = d0 | d1 << 16 selects, per output
 // byte, the low or high byte of bf16(d) from two 4-entry byte tables with one
 // v_perm: selector bytes (d0, 4 + d0, d1, 4 + d1) = x * 0x101 + 0x04000400.
-__device__ __forceinline__ v8bf_w digits_small(uint4 c, int shift, u32 mask2) {
+__device__ __forceinline__ v8bf_w digits_small(uint4 c, int shift, u32 mask2, u32 sel_bias) {
     constexpr u32 LO = 0x40008000u;   // low bytes of bf16(0), bf16(1), bf16(2), bf16(3)
     constexpr u32 HI = 0x40403F00u;   // high bytes
     uint4 r;
-    r.x = __builtin_amdgcn_perm(HI, LO, ((c.x >> shift) & mask2) * 0x101u + 0x04000400u);
-    r.y = __builtin_amdgcn_perm(HI, LO, ((c.y >> shift) & mask2) * 0x101u + 0x04000400u);
-    r.z = __builtin_amdgcn_perm(HI, LO, ((c.z >> shift) & mask2) * 0x101u + 0x04000400u);
-    r.w = __builtin_amdgcn_perm(HI, LO, ((c.w >> shift) & mask2) * 0x101u + 0x04000400u);
+    r.x = __builtin_amdgcn_perm(HI, LO, mad_u24((c.x >> shift) & mask2, 0x101u, sel_bias));
+    r.y = __builtin_amdgcn_perm(HI, LO, mad_u24((c.y >> shift) & mask2, 0x101u, sel_bias));
+    r.z = __builtin_amdgcn_perm(HI, LO, mad_u24((c.z >> shift) & mask2, 0x101u, sel_bias));
+    r.w = __builtin_amdgcn_perm(HI, LO, mad_u24((c.w >> shift) & mask2, 0x101u, sel_bias));
     return __builtin_bit_cast(v8bf_w, r);
 }
 
@@ -79,6 +87,11 @@ __device__ __forceinline__ v8bf_w digits_any(uint4 c, int shift, u32 mask2) {
         o[i] = __builtin_amdgcn_perm(__float_as_uint(float(w[i] >> 16)),
                                      __float_as_uint(float(w[i] & 0xFFFFu)), 0x07060302u);
     return __builtin_bit_cast(v8bf_w, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// Float value held by lane `i` (readlane moves 32-bit integers).
+__device__ __forceinline__ float lane_float(float v, int i) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
 }
 
 // restore_scales of one total: (T * xs) * ws when no intermediate leaves the
@@ -208,6 +221,15 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
+    // Per-slice constants in a lane table (lane a: slice a), read with readlane.
+    const int slice_shift = lane < A ? plan.in_shift[lane] : 0;
+    const u32 slice_mask2 = lane < A ? plan.in_mask2[lane] : 0u;
+    const int slice_factor = lane < A ? plan.fa[lane] : 0;
+    const float w_k1 = lane < W ? plan.k1[lane] : 0.0f;
+    const float w_top = lane < W ? plan.top[lane] : 0.0f;
+    const float w_alpha = lane < W ? plan.alpha[lane] : 0.0f;
+    const int w_factor = lane < W ? plan.fw[lane] : 0;
+    const u32 sel_bias = 0x04000400u;
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     for (int g = 0; g < G; ++g) {
         const int cur = g & 1;
@@ -222,43 +244,81 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
 #pragma unroll
         for (int r = 0; r < 16; ++r) T[r] = 0u;
         const uint4 *fl = sF + i64(cur) * FR * 64 + lane;
-        for (int w = 0; w < W; ++w) {
-            v8bf_w F[3][KS];
+        // ADC of one slice pair's current: per output fma into the exponent-fixed
+        // domain, med3 clamp, 24-bit multiply-accumulate of fa*fw*(0x400000 + code).
+        auto convert = [&](const v16f_w &I, int w, int a) {
+            const float k1 = lane_float(w_k1, w);
+            const float top = MAGIC + lane_float(w_top, w);
+            const int f = __builtin_amdgcn_readlane(slice_factor, a) *
+                          __builtin_amdgcn_readlane(w_factor, w);   // |fa*fw| < 2^23
+            const u32 f24 = u32(int(u32(f) << 8) >> 8);
+            float alpha = 0.0f;
+            if (NONLINEAR) alpha = lane_float(w_alpha, w);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float y;
+                if (NONLINEAR) {
+                    float z = I[r] * k1;
+                    z = z * __builtin_amdgcn_rcpf(fmaf(fabsf(z), alpha, 1.0f));
+                    y = z + MAGIC;
+                } else {
+                    y = fmaf(I[r], k1, MAGIC);
+                }
+                y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
+                const int low = int(__float_as_uint(y) << 8) >> 8;   // 0x400000 + code
+                T[r] += u32(low) * f24;
+            }
+        };
+        auto digits = [&](v8bf_w (&B)[KS], int a) {
+            const int shift = __builtin_amdgcn_readlane(slice_shift, a);
+            const u32 mask2 = u32(__builtin_amdgcn_readlane(int(slice_mask2), a));
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                B[ks] = SMALL ? digits_small(qc[ks], shift, mask2, sel_bias)
+                              : digits_any(qc[ks], shift, mask2);
+        };
+        auto terms = [&](v8bf_w (&F)[3][KS], int w) {
 #pragma unroll
             for (int term = 0; term < 3; ++term)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
                     F[term][ks] = __builtin_bit_cast(v8bf_w, fl[((w * 3 + term) * KS + ks) * 64]);
-            const float k1 = plan.k1[w], top = MAGIC + plan.top[w], alpha = plan.alpha[w];
-            const int fw = plan.fw[w];   // |fa*fw| < 2^23: a signed 24-bit operand
-            for (int a = 0; a < A; ++a) {
-                const int shift = plan.in_shift[a];
-                const u32 mask2 = plan.in_mask2[a];
-                v16f_w I = {};
+        };
+        // Input slices in pairs: the digits of a slice are built once per read;
+        // per weight slice the two currents are two interleaved MFMA chains.
+        int a = 0;
+        for (; a + 1 < A; a += 2) {
+            v8bf_w B0[KS], B1[KS];
+            digits(B0, a);
+            digits(B1, a + 1);
+            for (int w = 0; w < W; ++w) {
+                v8bf_w F[3][KS];
+                terms(F, w);
+                v16f_w I0 = {}, I1 = {};
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const v8bf_w B = SMALL ? digits_small(qc[ks], shift, mask2)
-                                           : digits_any(qc[ks], shift, mask2);
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int term = 0; term < 3; ++term) {
+                        I0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B0[ks], I0, 0, 0, 0);
+                        I1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B1[ks], I1, 0, 0, 0);
+                    }
+                convert(I0, w, a);
+                convert(I1, w, a + 1);
+            }
+        }
+        if (a < A) {
+            v8bf_w B0[KS];
+            digits(B0, a);
+            for (int w = 0; w < W; ++w) {
+                v8bf_w F[3][KS];
+                terms(F, w);
+                v16f_w I0 = {};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
                     for (int term = 0; term < 3; ++term)
-                        I = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B, I, 0, 0, 0);
-                }
-                const u32 f = u32(plan.fa[a] * fw);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float y;
-                    if (NONLINEAR) {
-                        float z = I[r] * k1;
-                        z = z * __builtin_amdgcn_rcpf(fmaf(fabsf(z), alpha, 1.0f));
-                        y = z + MAGIC;
-                    } else {
-                        y = fmaf(I[r], k1, MAGIC);
-                    }
-                    y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
-                    // low 24 bits of y: 0x400000 + code (v_mad_i32_i24)
-                    const int low = int(__float_as_uint(y) << 8) >> 8;
-                    T[r] += u32(low) * u32(int(f << 8) >> 8);
-                }
+                        I0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B0[ks], I0, 0, 0, 0);
+                convert(I0, w, a);
             }
         }
 

@@ -528,6 +528,85 @@ __global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64
     if (!finite && status) atomicOr(status, flag);
 }
 
+// Column groups (gc == 1, any gr) of an FP64 matrix: block = 64 columns x 4
+// row lanes over a chunk of COL_CHUNK rows (coalesced across the columns).
+// Each thread keeps a running maximum while its rows stay in one group and
+// flushes it to LDS; the four row lanes are folded there and one atomicMax per
+// (column, group) and chunk remains.  |x| bit patterns order like the values.
+constexpr int COL_CHUNK = COL_CHUNK_ROWS;
+__global__ __launch_bounds__(256) void k_col_group_max_f64(const double *x, i64 rows, i64 cols,
+                                                           i64 ld, i64 gr, u64 *work, u32 *status,
+                                                           u32 flag) {
+    __shared__ u64 part[4][64];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const i64 c = i64(blockIdx.x) * 64 + tx;
+    const i64 r0 = i64(blockIdx.y) * COL_CHUNK;
+    const i64 r1 = (r0 + COL_CHUNK) < rows ? (r0 + COL_CHUNK) : rows;
+    bool finite = true;
+    // Groups that intersect this chunk, handled one at a time (uniform loop).
+    for (i64 g = r0 / gr; g * gr < r1; ++g) {
+        const i64 lo = (g * gr) > r0 ? (g * gr) : r0;
+        const i64 hi = ((g + 1) * gr) < r1 ? ((g + 1) * gr) : r1;
+        u64 best = 0;
+        if (c < cols) {
+            for (i64 r = lo + ty; r < hi; r += 4) {
+                const double v = fabs(x[r * ld + c]);
+                finite = finite && v <= DBL_MAX;
+                const u64 bits = u64(__double_as_longlong(v));
+                best = bits > best ? bits : best;
+            }
+        }
+        part[ty][tx] = best;
+        __syncthreads();
+        if (ty == 0 && c < cols) {
+            u64 m = part[0][tx];
+            m = part[1][tx] > m ? part[1][tx] : m;
+            m = part[2][tx] > m ? part[2][tx] : m;
+            m = part[3][tx] > m ? part[3][tx] : m;
+            if (m) atomicMax(reinterpret_cast<unsigned long long *>(&work[g * cols + c]),
+                             static_cast<unsigned long long>(m));
+        }
+        __syncthreads();
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
+// Row groups (gr == 1, gc >= 64) of an FP64 matrix: one wave per row and chunk
+// of ROW_CHUNK columns (coalesced); per group in the chunk a lane maximum, a
+// wave maximum by shuffles, and one atomicMax per (row, group, chunk).
+constexpr int ROW_CHUNK = ROW_CHUNK_COLS;
+__global__ __launch_bounds__(256) void k_row_group_max_f64(const double *x, i64 rows, i64 cols,
+                                                           i64 ld, i64 gc, i64 ncg, u64 *work,
+                                                           u32 *status, u32 flag) {
+    const int lane = threadIdx.x & 63;
+    const i64 row = i64(blockIdx.y) * 4 + (threadIdx.x >> 6);
+    const i64 c0 = i64(blockIdx.x) * ROW_CHUNK;
+    if (row >= rows) return;
+    const i64 c1 = (c0 + ROW_CHUNK) < cols ? (c0 + ROW_CHUNK) : cols;
+    const double *src = x + row * ld;
+    bool finite = true;
+    for (i64 g = c0 / gc; g * gc < c1; ++g) {
+        const i64 lo = (g * gc) > c0 ? (g * gc) : c0;
+        const i64 hi = ((g + 1) * gc) < c1 ? ((g + 1) * gc) : c1;
+        u64 best = 0;
+        for (i64 c = lo + lane; c < hi; c += 64) {
+            const double v = fabs(src[c]);
+            finite = finite && v <= DBL_MAX;
+            const u64 bits = u64(__double_as_longlong(v));
+            best = bits > best ? bits : best;
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            const u64 other = u64(__shfl_xor(static_cast<unsigned long long>(best), d, 64));
+            best = other > best ? other : best;
+        }
+        if (lane == 0 && best)
+            atomicMax(reinterpret_cast<unsigned long long *>(&work[row * ncg + g]),
+                      static_cast<unsigned long long>(best));
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
 // floor() of the correctly rounded log2(x) for normal x > 0: ilogb(x), or one
 // more when log2(x) lies within half a unit in the last place below the next
 // integer (so that it rounds up to it).

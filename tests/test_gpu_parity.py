@@ -774,3 +774,30 @@ def test_wide_mfma_column_chunks(hip_device):
                                     hip._ptr(workspace), workspace.numel(),
                                     hip._stream(qd.device)), "chunked totals")
     assert bits_equal(chunked, full)
+
+
+# Groups align with the 64-row reads; 192, 320 and 1088 straddle the kernels'
+# 256-row and 1024-column chunks; (64, 3) and (2, 64) take the 2-D group path.
+WIDE_GROUPS = [((None, 1), (1, None)), ((64, 1), (1, 64)), ((192, 1), (1, 192)),
+               ((320, 1), (1, 1088)), ((64, 3), (2, 64))]
+
+
+@pytest.mark.parametrize("wgran,igran", WIDE_GROUPS, ids=[f"{w}-{i}" for w, i in WIDE_GROUPS])
+def test_wide_group_quantizers_bit_exact(hip_device, wgran, igran):
+    """FP64 group maxima (column, row and 2-D groups, chunk-straddling groups) -> codes and
+    scales identical to the oracle's."""
+    cfg = Config(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                 weight_slice=(1, 1, 2), bw_e=8, array_size=(64, 64), adc_bits=(6, 6, 7),
+                 weight_quant_gran=wgran, input_quant_gran=igran)
+    gen = torch.Generator().manual_seed(45)
+    a = torch.randn(9, 1500, generator=gen)
+    a[:, 700] = 50.0
+    b = torch.randn(1500, 70, generator=gen) * 0.02
+    b[513, :] = -3.0
+    q, xs = hip.input_tiles(a.to(hip_device), cfg)
+    packed, _, ws = hip.weight_tiles(b.T.to(hip_device), cfg)
+    q_ref, xs_ref = oracle.input_tiles(a, cfg)
+    packed_ref, ws_ref = oracle.weight_tiles(b.T, cfg)
+    assert bits_equal(q.cpu().to(torch.int64) & 0xFFFF, q_ref & 0xFFFF)
+    assert bits_equal(xs, xs_ref)
+    assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
