@@ -383,7 +383,11 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
         return false;
     }
     if (cfg->activation_bits > 16) { *why = "input codes wider than 16 bits"; return false; }
-    if (cfg->n_in > WIDE_MFMA_MAX_A || cfg->n_w > WIDE_MFMA_MAX_W) { *why = "too many slices"; return false; }
+    if (cfg->n_in > WIDE_MFMA_MAX_A || cfg->n_w > WIDE_MFMA_MAX_W ||
+        cfg->n_w * 3 * (cfg->read_rows / 16) > WIDE_FRAGS_LARGE) {
+        *why = "too many slices";
+        return false;
+    }
     const i64 G = m * cfg->reads;
     if (G >= 256) { *why = "256 or more reads per output"; return false; }
     if (!all_cascade_columns_wide(cfg->cols, p)) { *why = "interleaved summation columns"; return false; }
@@ -434,26 +438,6 @@ bool wide_extent_ok(i64 n, i64 m, const mf_config *cfg) {
     return 64 * kp <= 0x7FFFFFFF && (n + 127) / 128 <= 65535;
 }
 
-template <int KS, bool NL, bool SMALL>
-int launch_noisy_wide_kernel(dim3 grid, size_t lds, hipStream_t s, const NoisyWidePlan &plan,
-                             const NoisyWideArgs &args) {
-    // Dynamic LDS above 64 KiB is opted into once per device.
-    static u64 configured = 0;
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) return fail(MF_E_HIP, "hipGetDevice failed");
-    const u64 bit = u64(1) << (device & 63);
-    if (!(configured & bit)) {
-        const hipError_t e = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_noisy_wide<KS, NL, SMALL>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess)
-            return fail(MF_E_HIP, "wide MFMA read: LDS attribute: %s", hipGetErrorString(e));
-        configured |= bit;
-    }
-    hipLaunchKernelGGL((k_noisy_wide<KS, NL, SMALL>), grid, dim3(256), lds, s, plan, args);
-    return MF_OK;
-}
-
 // Repack codes to 16 bits, split conductances and run k_noisy_wide over column
 // chunks that fit the workspace.  g: optional injected conductances.
 int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, bool small,
@@ -466,8 +450,9 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
     const i64 per_block = wide_block_bytes(cfg, m);
     const i64 max_cb = (bytes - codes_bytes) / per_block;
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
-    const size_t lds = size_t(2) * cfg->n_w * 3 * ks * 1024;
-    if (lds > 160 * 1024) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
+    const int frags = cfg->n_w * 3 * ks;
+    if (frags > WIDE_FRAGS_LARGE) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
+    const bool large = frags > WIDE_FRAGS_SMALL;
     uint16_t *q16 = static_cast<uint16_t *>(workspace);
     uint4 *gs = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + codes_bytes);
     hipLaunchKernelGGL(k_codes16, dim3(grid_for(n * kp)), dim3(256), 0, s, q, n * kp, q16);
@@ -498,19 +483,24 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
         args.totals = totals;
         const dim3 grid{unsigned(CB), unsigned((n + 127) / 128), 1u};
         const bool nl = cfg->has_nonlinear != 0;
-        int launched;
-#define MF_WIDE_LAUNCH(KS)                                                                       \
-    if (nl) launched = small ? launch_noisy_wide_kernel<KS, true, true>(grid, lds, s, plan, args) \
-                             : launch_noisy_wide_kernel<KS, true, false>(grid, lds, s, plan, args); \
-    else launched = small ? launch_noisy_wide_kernel<KS, false, true>(grid, lds, s, plan, args)  \
-                          : launch_noisy_wide_kernel<KS, false, false>(grid, lds, s, plan, args);
+#define MF_WIDE_LAUNCH(KS, FR)                                                                   \
+    if (nl) {                                                                                    \
+        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, true, true, FR>), grid, dim3(256), 0, s,  \
+                                      plan, args);                                               \
+        else hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR>), grid, dim3(256), 0, s, plan, \
+                                args);                                                           \
+    } else {                                                                                     \
+        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, false, true, FR>), grid, dim3(256), 0, s, \
+                                      plan, args);                                               \
+        else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR>), grid, dim3(256), 0, s,      \
+                                plan, args);                                                     \
+    }
         if (ks == 4) {
-            MF_WIDE_LAUNCH(4)
+            if (large) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_LARGE) } else { MF_WIDE_LAUNCH(4, WIDE_FRAGS_SMALL) }
         } else {
-            MF_WIDE_LAUNCH(2)
+            if (large) { MF_WIDE_LAUNCH(2, WIDE_FRAGS_LARGE) } else { MF_WIDE_LAUNCH(2, WIDE_FRAGS_SMALL) }
         }
 #undef MF_WIDE_LAUNCH
-        if (launched) return launched;
     }
     return check_launch("wide noisy MFMA read");
 }

@@ -24,7 +24,8 @@
 // and read as one contiguous run [w][term][ks] of 1 KiB fragments (MFMA lane
 // order).  Block = 4 waves on the same 32 columns and 128 vectors (32 per
 // wave); per read the block copies the run into LDS with global_load_lds
-// (double-buffered, one barrier per read) and every wave reads it from there.
+// (double-buffered in two LDS objects, one barrier per read) and every wave
+// reads it from there.  FRMAX bounds the fragments per read (W * 3 * KS).
 // Input codes are repacked to 16 bits (k_codes16) so a lane's 8 rows of a
 // 16-row step are one 16-byte load.  Bound: VALU (digit expansion + ADC per
 // slice pair) with bf16 MFMA as co-bound.
@@ -87,6 +88,32 @@ __device__ __forceinline__ v8bf_w digits_any(uint4 c, int shift, u32 mask2) {
         o[i] = __builtin_amdgcn_perm(__float_as_uint(float(w[i] >> 16)),
                                      __float_as_uint(float(w[i] & 0xFFFFu)), 0x07060302u);
     return __builtin_bit_cast(v8bf_w, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// One 1 KiB LDS DMA: lane l's 16 bytes at src go to lds_base + 16 * l.  Issued
+// as inline assembly so that the compiler's wait-count analysis does not track
+// it (it would otherwise wait for it at the next loop header); the kernel waits
+// for it explicitly (s_waitcnt vmcnt(0) and a barrier) before reading the data.
+__device__ __forceinline__ void lds_dma_16(const void *src, u32 lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+// After an explicit s_waitcnt vmcnt(0): re-define the loaded registers so the
+// compiler's wait-count analysis no longer sees a load pending on them (it
+// would otherwise flush vmcnt at the next loop header, where the next read's
+// LDS DMA is in flight).
+template <int N>
+__device__ __forceinline__ void settle(uint4 (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i].x), "+v"(v[i].y), "+v"(v[i].z), "+v"(v[i].w));
+}
+
+template <typename T>
+__device__ __forceinline__ void settle_one(T &v) {
+    asm volatile("" : "+v"(v));
 }
 
 // Float value held by lane `i` (readlane moves 32-bit integers).
@@ -174,10 +201,13 @@ template __global__ void k_split_wide<2>(const mf_config, const u32 *, const flo
 template __global__ void k_split_wide<4>(const mf_config, const u32 *, const float *, i64, i64,
                                          i64, u32, u64, i64, i64, uint4 *);
 
-template <int KS, bool NONLINEAR, bool SMALL>
+template <int KS, bool NONLINEAR, bool SMALL, int FRMAX>
 __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
                                                        const NoisyWideArgs args) {
-    extern __shared__ __align__(16) uint4 sF[];   // [2][W * 3 * KS][64]
+    // Two LDS objects (read g in one, read g+1 arriving in the other) so that the
+    // compiler can tell the in-flight LDS DMA from the LDS reads of the current
+    // read and does not wait for the DMA before them.
+    __shared__ __align__(16) uint4 sF0[FRMAX * 64], sF1[FRMAX * 64];
     constexpr int P = 16 * KS;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -192,19 +222,27 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
 
     // Conductance terms of this column block: [g][w][term][ks][lane].
     const uint4 *frag = args.gs + cb * i64(G) * FR * 64 + lane;
-    auto fetch = [&](int g, int buf) {
+    auto fetch = [&](int g, uint4 *dst) {
         const uint4 *src = frag + i64(g) * FR * 64;
+        const u32 base = u32(reinterpret_cast<uintptr_t>((lds_void *)dst));
         for (int f = wave; f < FR; f += 4)
-            __builtin_amdgcn_global_load_lds(src + f * 64, (lds_void *)(sF + (buf * FR + f) * 64),
-                                             16, 0, 0);
+            lds_dma_16(src + f * 64, __builtin_amdgcn_readfirstlane(base + u32(f) * 1024u));
     };
 
+    // Per-slice constants in a lane table (lane a: slice a), read with readlane.
+    int slice_shift = lane < A ? plan.in_shift[lane] : 0;
+    u32 slice_mask2 = lane < A ? plan.in_mask2[lane] : 0u;
+    int slice_factor = lane < A ? plan.fa[lane] : 0;
+    float w_k1 = lane < W ? plan.k1[lane] : 0.0f;
+    float w_top = lane < W ? plan.top[lane] : 0.0f;
+    float w_alpha = lane < W ? plan.alpha[lane] : 0.0f;
+    int w_factor = lane < W ? plan.fw[lane] : 0;
     // 16-bit input codes of this wave's 32 vectors (rows past n read as zero).
     const i64 vrows = (args.n - v0) < 32 ? (args.n - v0) : 32;
     const __amdgpu_buffer_rsrc_t qbuf =
         wide_buffer(args.q16 + (vrows > 0 ? v0 : 0) * kp, (vrows > 0 ? vrows : 0) * kp * 2);
     const int q_off = (lrow * int(kp) + lhalf * 8) * 2;
-    uint4 qc[KS], qn[KS];
+    uint4 qc[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
         qc[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -217,33 +255,26 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc0[r] = 0.0;
 
-    fetch(0, 0);
+    fetch(0, sF0);
     __builtin_amdgcn_s_waitcnt(0);
+    settle(qc);
+    settle_one(slice_shift);
+    settle_one(slice_mask2);
+    settle_one(slice_factor);
+    settle_one(w_k1);
+    settle_one(w_top);
+    settle_one(w_alpha);
+    settle_one(w_factor);
     __syncthreads();
 
-    // Per-slice constants in a lane table (lane a: slice a), read with readlane.
-    const int slice_shift = lane < A ? plan.in_shift[lane] : 0;
-    const u32 slice_mask2 = lane < A ? plan.in_mask2[lane] : 0u;
-    const int slice_factor = lane < A ? plan.fa[lane] : 0;
-    const float w_k1 = lane < W ? plan.k1[lane] : 0.0f;
-    const float w_top = lane < W ? plan.top[lane] : 0.0f;
-    const float w_alpha = lane < W ? plan.alpha[lane] : 0.0f;
-    const int w_factor = lane < W ? plan.fw[lane] : 0;
     const u32 sel_bias = 0x04000400u;
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
-    for (int g = 0; g < G; ++g) {
-        const int cur = g & 1;
-        if (g + 1 < G) {
-            fetch(g + 1, cur ^ 1);
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                qn[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       qbuf, q_off + (g + 1) * P * 2 + ks * 32, 0, 0));
-        }
+    auto step = [&](int g, const uint4 *sCur, uint4 *sNext) {
+        if (g + 1 < G) fetch(g + 1, sNext);
         u32 T[16];   // modulo 2^32, offset by 0x400000 * sum(fa*fw) (plan.bias undoes it)
 #pragma unroll
         for (int r = 0; r < 16; ++r) T[r] = 0u;
-        const uint4 *fl = sF + i64(cur) * FR * 64 + lane;
+        const uint4 *fl = sCur + lane;
         // ADC of one slice pair's current: per output fma into the exponent-fixed
         // domain, med3 clamp, 24-bit multiply-accumulate of fa*fw*(0x400000 + code).
         auto convert = [&](const v16f_w &I, int w, int a) {
@@ -359,10 +390,21 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
                 }
             }
         }
+        // The next read's codes arrive with its conductance terms, before the
+        // barrier, so no load is outstanding inside the next step's compute.
+        if (g + 1 < G) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qc[ks] = qn[ks];
+            for (int ks = 0; ks < KS; ++ks)
+                qc[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       qbuf, q_off + (g + 1) * P * 2 + ks * 32, 0, 0));
+        }
         __builtin_amdgcn_s_waitcnt(0);
+        settle(qc);
         __syncthreads();
+    };
+    for (int g = 0; g < G; g += 2) {
+        step(g, sF0, sF1);
+        if (g + 1 < G) step(g + 1, sF1, sF0);
     }
     if (args.totals || !live_n) return;
 
@@ -379,15 +421,17 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
-#define MF_NOISY_WIDE_INST(KS, NL, SMALL) \
-    template __global__ void k_noisy_wide<KS, NL, SMALL>(const NoisyWidePlan, const NoisyWideArgs);
-MF_NOISY_WIDE_INST(2, false, true)
-MF_NOISY_WIDE_INST(2, true, true)
-MF_NOISY_WIDE_INST(2, false, false)
-MF_NOISY_WIDE_INST(2, true, false)
-MF_NOISY_WIDE_INST(4, false, true)
-MF_NOISY_WIDE_INST(4, true, true)
-MF_NOISY_WIDE_INST(4, false, false)
-MF_NOISY_WIDE_INST(4, true, false)
+#define MF_NOISY_WIDE_INST(KS, NL, SMALL, FRMAX)                                            \
+    template __global__ void k_noisy_wide<KS, NL, SMALL, FRMAX>(const NoisyWidePlan,          \
+                                                                const NoisyWideArgs);
+#define MF_NOISY_WIDE_INST4(KS, FRMAX)              \
+    MF_NOISY_WIDE_INST(KS, false, true, FRMAX)      \
+    MF_NOISY_WIDE_INST(KS, true, true, FRMAX)       \
+    MF_NOISY_WIDE_INST(KS, false, false, FRMAX)     \
+    MF_NOISY_WIDE_INST(KS, true, false, FRMAX)
+MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_SMALL)
+MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_LARGE)
+MF_NOISY_WIDE_INST4(4, WIDE_FRAGS_SMALL)
+MF_NOISY_WIDE_INST4(4, WIDE_FRAGS_LARGE)
 
 }  // namespace mf
