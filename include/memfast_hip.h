@@ -164,6 +164,13 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
                const uint8_t *packed, int64_t p, int64_t begin, int64_t end, const void *g,
                uint32_t seed, uint64_t event, float *totals, int32_t *codes, void *stream);
 
+/* mf_mm `variant` flag (no reference counterpart): the workspace still holds the
+ * conductance terms that a previous mf_mm call of the same program (codes,
+ * seed, descriptor, workspace) sampled for every column, so the noisy-device
+ * MFMA read skips sampling them again.  Honoured only when the terms do not
+ * depend on the read event (no read variation); otherwise ignored. */
+#define MF_MM_REUSE_TERMS 0x100
+
 /* Fused read + scale restore (memfast/simulator.py:561-586 without the bias):
  * out [n, ldo] FP32 receives columns [0, p*C) of
  *   sum over reads g in torch's CPU order of (float(T[n,g,o]) * xscale[n,g]) * wscale[g,o].
@@ -178,6 +185,13 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
           const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo,
           void *workspace, int64_t workspace_bytes, int32_t variant, uint32_t *status,
           void *stream);
+
+/* Bias of an FP32 read (memfast/simulator.py:612-613, `out + bias`): out[v, c]
+ * += bias[c] for c < o, one FP32 add each; a non-finite sum sets
+ * MF_STATUS_OUTPUT in status (may be NULL), which replaces the host-side
+ * finiteness scan that decides the FP64 retry (:614-615). */
+int mf_bias_add(float *out, int64_t n, int64_t o, int64_t ldo, const float *bias,
+                uint32_t *status, void *stream);
 
 /* Overflow-safe FP64 restore and read sum of one chunk of `width` tiles
  * (memfast/simulator.py:57-66 restore_scales and :578-585, the wide/retry path

@@ -305,27 +305,68 @@ bool noisy_extent_ok(i64 n, i64 m, const mf_config *cfg) {
     return 64 * kp <= 0x7FFFFFFF && (n + 63) / 64 <= 65535;
 }
 
+// Blocks of the noisy read (64 columns x 64 vectors each) below which the
+// reads are split across blocks (grid z): each block writes integer slice
+// totals for its reads and k_restore_sum_f32 restores and sums them.
+constexpr i64 NOISY_SPLIT_BELOW = 512;
+
+i64 noisy_terms_bytes(const mf_config *cfg, i64 m, i64 p) {
+    return (p * cfg->cols + 63) / 64 * 2 * noisy_block_bytes(cfg, m);
+}
+
+// Read chunks of a split read (1: not split).
+i64 noisy_split(const mf_config *cfg, i64 n, i64 m, i64 p) {
+    const i64 G = m * cfg->reads;
+    const i64 blocks = (p * cfg->cols + 63) / 64 * ((n + 63) / 64);
+    if (G < 2 || blocks >= NOISY_SPLIT_BELOW) return 1;
+    i64 z = (NOISY_SPLIT_BELOW + blocks - 1) / blocks;
+    if (z > G) z = G;
+    const i64 step = (G + z - 1) / z;
+    return (G + step - 1) / step;
+}
+
+i64 noisy_scratch_bytes(const mf_config *cfg, i64 n, i64 m, i64 p) {
+    if (noisy_split(cfg, n, m, p) < 2) return 0;
+    return align256(n * m * cfg->reads * p * cfg->cols * 4);
+}
+
+// Conductance terms depend on the read event only through shared read noise.
+bool terms_event_independent(const mf_config *cfg) { return !cfg->has_read; }
+
 // Split conductances and run k_noisy over column chunks that fit `bytes` of
 // workspace (at least 64 columns).  g: optional injected conductances.
+// reuse: the workspace already holds this program's event-independent terms
+// for every column (a previous call with the same codes, seed and config).
 int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *q,
                  const float *xscale, i64 n, i64 m, const u8 *packed_t, const float *wscale, i64 p,
                  const float *g, u32 seed, u64 event, float *out, i64 ldo, void *workspace,
-                 i64 bytes, int totals, u32 *status, hipStream_t s) {
+                 i64 bytes, int totals, u32 *status, hipStream_t s, bool reuse = false) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     const i64 per_block = noisy_block_bytes(cfg, m);
-    const i64 max_cb = (bytes / per_block) / 2 * 2;
+    // Split read (fused output only, when the whole program's terms fit).
+    const i64 split = totals ? 1 : noisy_split(cfg, n, m, p);
+    const i64 full = noisy_terms_bytes(cfg, m, p);
+    const i64 scratch = noisy_scratch_bytes(cfg, n, m, p);
+    const bool use_split = split > 1 && bytes >= full + scratch;
+    const i64 max_cb = use_split ? full / per_block : (bytes / per_block) / 2 * 2;
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
+    reuse = reuse && g == nullptr && terms_event_independent(cfg) && max_cb * 32 >= ncols;
     uint4 *gs = static_cast<uint4 *>(workspace);
+    float *partial = use_split ? reinterpret_cast<float *>(static_cast<char *>(workspace) + full)
+                               : nullptr;
     for (i64 c_begin = 0; c_begin < ncols; c_begin += max_cb * 32) {
         const i64 cols = (ncols - c_begin) < max_cb * 32 ? (ncols - c_begin) : max_cb * 32;
         const i64 CB = (cols + 63) / 64 * 2;
         const i64 threads = i64(cfg->n_w) * CB * G * ks * 64;
-        if (ks == 2)
+        if (reuse) {
+            // terms already in place
+        } else if (ks == 2) {
             hipLaunchKernelGGL(k_split_conductances<2>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
                                packed_t, g, m, p, ncols, seed, event, c_begin, CB, gs);
-        else
+        } else {
             hipLaunchKernelGGL(k_split_conductances<4>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
                                packed_t, g, m, p, ncols, seed, event, c_begin, CB, gs);
+        }
         NoisyArgs args{};
         args.q = q;
         args.gs = gs;
@@ -342,7 +383,18 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         args.c_begin = c_begin;
         args.CB = CB;
         args.totals = totals;
-        const dim3 grid{unsigned(CB / 2), unsigned((n + 63) / 64), 1u};
+        args.g_begin = 0;
+        args.g_end = G;
+        args.g_step = G;
+        unsigned gz = 1;
+        if (use_split) {
+            args.totals = 1;
+            args.out = partial;
+            args.ldo = ncols;
+            args.g_step = (G + split - 1) / split;
+            gz = unsigned((G + args.g_step - 1) / args.g_step);
+        }
+        const dim3 grid{unsigned(CB / 2), unsigned((n + 63) / 64), gz};
         const bool nl = cfg->has_nonlinear != 0;
         if (ks == 4) {
             if (nl) hipLaunchKernelGGL((k_noisy<4, 5, true>), grid, dim3(256), 0, s, plan, args);
@@ -355,6 +407,9 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
             else hipLaunchKernelGGL((k_noisy<2, 8, false>), grid, dim3(256), 0, s, plan, args);
         }
     }
+    if (use_split)
+        hipLaunchKernelGGL(k_restore_sum_f32, dim3(grid_for(n * ncols)), dim3(256), 0, s, partial, n,
+                           G, ncols, ncols, xscale, wscale, ncols, out, ldo, level_power(G), status);
     return check_launch("noisy MFMA read");
 }
 
@@ -851,7 +906,7 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64
         ideal_workspace(cfg, n, m, p, &xb, &wb);
         *bytes = xb + wb;
     } else if (build_noisy_plan(cfg, m, p, &noisy, &ks, &why)) {
-        *bytes = (p * cfg->cols + 63) / 64 * 2 * noisy_block_bytes(cfg, m);
+        *bytes = noisy_terms_bytes(cfg, m, p) + noisy_scratch_bytes(cfg, n, m, p);
     } else if (wide_plan_ok(cfg, n, m, p)) {
         *bytes = wide_codes_bytes(n, m, cfg) + (p * cfg->cols + 31) / 32 * wide_block_bytes(cfg, m);
     } else {
@@ -918,6 +973,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         args.w_bits = cfg->weight_bits;
         // Tile variants: 0 default (32 vectors per wave), 1 = 64 vectors per wave,
         // 2 = 32 vectors per wave.
+        variant &= ~MF_MM_REUSE_TERMS;
         if (variant < 0 || variant > 2) return fail(MF_E_INVALID, "unknown kernel variant %d", variant);
         const int tn = (ks == 1 && variant == 1) ? 2 : 1;
         const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (ncols + 63) / 64;
@@ -942,7 +998,8 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
         const int launched = launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p,
                                           nullptr, seed, event, out, ldo, workspace,
-                                          workspace_bytes, 0, status, s);
+                                          workspace_bytes, 0, status, s,
+                                          (variant & MF_MM_REUSE_TERMS) != 0);
         if (timing.first) {
             hipEventRecord(timing.second, s);
             g_profile.pending.push_back(timing);
@@ -1001,6 +1058,15 @@ int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
     return launch_noisy(cfg, noisy, ks, q, nullptr, n, m, packed_t, nullptr, p, g, seed, event,
                         totals, ncols, workspace, workspace_bytes, 1, nullptr,
                         static_cast<hipStream_t>(stream));
+}
+
+int mf_bias_add(float *out, int64_t n, int64_t o, int64_t ldo, const float *bias,
+                uint32_t *status, void *stream) {
+    if (!out || !bias || n < 1 || o < 1 || ldo < o) return fail(MF_E_INVALID, "invalid bias arguments");
+    hipLaunchKernelGGL(k_bias_add, dim3(grid_for(n * o)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), out, n, o, ldo, bias, status,
+                       u32(MF_STATUS_OUTPUT));
+    return check_launch("bias add");
 }
 
 int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,

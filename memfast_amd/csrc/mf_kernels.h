@@ -116,6 +116,8 @@ struct NoisyArgs {
     float *out;           // fused: [n, ldo]; totals: [n, G, ldo]
     u32 *status;          // optional: MF_STATUS_OUTPUT for a non-finite fused output
     i64 n, kp, G, ldo, ldws, ncols, c_begin, CB;
+    i64 g_begin, g_end;   // reads of this launch (blockIdx.z adds g_step)
+    i64 g_step;
     int totals;
 };
 
@@ -125,6 +127,11 @@ __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, co
                                      i64 CB, uint4 *gs);
 template <int KS, int NA, bool NONLINEAR>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
+// (float(T) * xs) * ws summed over reads in torch's cascade order, from slice
+// totals [n, G, ldt]: the epilogue of a read split across blocks.
+__global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 ldt, i64 ncols,
+                                  const float *xscale, const float *wscale, i64 ldws, float *out,
+                                  i64 ldo, int lp, u32 *status);
 
 // ---- noisy-device MFMA read, wide configurations (noisy_wide.hip) ----------
 // Same ADC model as NoisyPlan; integer totals accumulate modulo 2^32 as
@@ -171,6 +178,8 @@ __global__ void k_stable_sum(const float *totals, i64 n, i64 G, i64 wc, const fl
 
 // ---- quantization (quantize.hip) ------------------------------------------
 __global__ void k_fill_u32(u32 *p, i64 count, u32 value);
+__global__ void k_bias_add(float *out, i64 n, i64 o, i64 ldo, const float *bias, u32 *status,
+                           u32 flag);
 __global__ void k_group_max(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,
                             u32 *work, u32 *status, u32 flag);
 template <bool VEC>

@@ -147,15 +147,18 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
 #pragma unroll
     for (int r = 0; r < 16; ++r) { acc0[r] = 0.0f; acc1[r] = 0.0f; }
 
+    // Reads of this block: [g0, g1) (a read split across blocks writes totals).
+    const int g0 = int(args.g_begin + i64(blockIdx.z) * args.g_step);
+    const int g1 = int((g0 + args.g_step) < args.g_end ? (g0 + args.g_step) : args.g_end);
     uint2 qw[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-        const u32 x = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16, 0, 0);
-        const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16 + 4, 0, 0);
+        const u32 x = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + g0 * P + ks * 16, 0, 0);
+        const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + g0 * P + ks * 16 + 4, 0, 0);
         qw[ks] = make_uint2(x, y);
     }
 
-    for (int g = 0; g < G; ++g) {
+    for (int g = g0; g < g1; ++g) {
         // Input digits of this read for every slice (B operands).
         v8bf B[NA][KS];
 #pragma unroll
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
             for (int ks = 0; ks < KS; ++ks)
                 B[a][ks] = digits_bf16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
         }
-        if (g + 1 < G) {
+        if (g + 1 < g1) {
             const int next = (g + 1) * P;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -285,6 +288,27 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
         }
     }
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
+}
+
+__global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 ldt, i64 ncols,
+                                  const float *xscale, const float *wscale, i64 ldws, float *out,
+                                  i64 ldo, int lp, u32 *status) {
+    bool finite = true;
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < n * ncols;
+         i += i64(gridDim.x) * blockDim.x) {
+        const i64 v = i / ncols, c = i - v * ncols;
+        Cascade<float> cascade;
+        cascade.reset();
+        for (i64 g = 0; g < G; ++g) {
+            float x = totals[(v * G + g) * ldt + c] * xscale[v * G + g];
+            x = x * wscale[g * ldws + c];
+            cascade.push(x, lp);
+        }
+        const float s = cascade.finish();
+        out[v * ldo + c] = s;
+        finite = finite && fabsf(s) <= FLT_MAX;
+    }
+    if (!finite && status) atomicOr(status, u32(MF_STATUS_OUTPUT));
 }
 
 template __global__ void k_noisy<2, 5, false>(const NoisyPlan, const NoisyArgs);

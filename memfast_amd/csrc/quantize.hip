@@ -12,6 +12,21 @@
 
 namespace mf {
 
+// out[v, c] += bias[c] (one FP32 add, as torch's broadcast add), flagging a
+// non-finite sum in the status word.
+__global__ void k_bias_add(float *out, i64 n, i64 o, i64 ldo, const float *bias, u32 *status,
+                           u32 flag) {
+    bool finite = true;
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < n * o;
+         i += i64(gridDim.x) * blockDim.x) {
+        const i64 v = i / o, c = i - v * o;
+        const float s = out[v * ldo + c] + bias[c];
+        out[v * ldo + c] = s;
+        finite = finite && fabsf(s) <= FLT_MAX;
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
 __global__ void k_fill_u32(u32 *p, i64 count, u32 value) {
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
          i += i64(gridDim.x) * blockDim.x)

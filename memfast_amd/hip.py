@@ -141,6 +141,7 @@ SIGNATURES = {
                _I64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
                       _P], ct.c_int),
+    "mf_bias_add": ([_P, _I64, _I64, _I64, _P, _P, _P], ct.c_int),
     "mf_stable_sum": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P], ct.c_int),
     "mf_quantize_inputs_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                  _P], ct.c_int),
@@ -319,6 +320,14 @@ def status_word(device):
     return torch.zeros(1, dtype=torch.int32, device=device)
 
 
+def input_error(config, fixed_scale=None):
+    """The reference's message for non-finite activations (memfast/quantization.py:12-13 for
+    grouped scales, :124-125 for fixed scales)."""
+    if fixed_scale is not None:
+        return "quantized values must be finite"
+    return f"quantized values must be finite in {torch.float64 if config.wide else torch.float32}"
+
+
 def input_tiles(value, config, fixed_scale=None, *, status=None):
     """Codes q [N, m, R] (uint8) and per-read scales [N, m*Gr] (quantization.py:115-137).
 
@@ -331,7 +340,7 @@ def input_tiles(value, config, fixed_scale=None, *, status=None):
         return _input_tiles_wide(value, config, fixed_scale, status)
     n, k = value.shape
     if status is None and not torch.isfinite(value).all():
-        raise ValueError("quantized values must be finite")
+        raise ValueError(input_error(config, fixed_scale))
     x = value.to(torch.float32).contiguous()
     r = config.array_size[0]
     m = math.ceil(k / r)
@@ -372,7 +381,7 @@ def _input_tiles_wide(value, config, fixed_scale, status):
     n, k = value.shape
     x = value.to(torch.float64).contiguous()
     if status is None and not torch.isfinite(x).all():
-        raise ValueError("quantized values must be finite in torch.float64")
+        raise ValueError(input_error(config, fixed_scale))
     r = config.array_size[0]
     m = math.ceil(k / r)
     q = torch.empty((n, m, r), dtype=torch.int32, device=value.device)
@@ -586,12 +595,24 @@ def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance
     return (totals, counts) if codes else totals
 
 
+REUSE_TERMS = 0x100   # MF_MM_REUSE_TERMS
+
+
+def terms_event_independent(config):
+    """Whether the noisy read's sampled conductances are the same on every read event."""
+    return not config.nonidealities.read_variation
+
+
 def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=None, out=None,
-       variant=0, status=None):
+       variant=0, status=None, workspace=None, reuse_terms=False):
     """Fused read + scale restore: [N, p*C] FP32, summed over reads in torch's order.
 
     Wide configurations: ``packed_t`` is the uint32 kernel copy of the codes
     (``kernel_codes``), scales and the output are FP64 (restore_scales).
+    ``workspace`` (optional, at least ``mm_workspace_bytes``) is the MFMA
+    kernels' scratch; with ``reuse_terms`` it still holds the conductance terms
+    a previous call of this program sampled (honoured when they do not depend
+    on the read event).
     """
     supported(config)
     require_device(q)
@@ -609,12 +630,17 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
         packed_t = None
     if out is None:
         out = torch.empty((n, p * c), dtype=torch.float32, device=q.device)
-    workspace = None
     if packed_t is not None and kernel:
-        size = ct.c_int64()
-        check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
-              "workspace size")
-        workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
+        size = mm_workspace_bytes(config, n, m, p)
+        if workspace is None:
+            workspace = torch.empty(max(1, size), dtype=torch.uint8, device=q.device)
+            reuse_terms = False
+        elif workspace.numel() < size or workspace.device != q.device:
+            raise ValueError(f"mm workspace needs {size} bytes on {q.device}")
+        if reuse_terms and kernel == 2:
+            variant |= REUSE_TERMS
+    else:
+        workspace = None
     # Converted operands stay referenced until the launch is queued (a freed
     # temporary could be handed to the next conversion by the caching allocator).
     q, xscale = q.contiguous(), xscale.contiguous()
@@ -665,12 +691,31 @@ def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductan
     return out
 
 
-def _workspace(config, n, m, p, device):
-    """Device scratch for the MFMA reads (mf_mm_workspace bytes, 256-byte aligned)."""
+def mm_workspace_bytes(config, n, m, p):
+    """Bytes of MFMA-kernel scratch ``mm`` uses for this shape (0 for the general kernel)."""
     size = ct.c_int64()
     check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
           "workspace size")
-    return torch.empty(max(1, size.value), dtype=torch.uint8, device=device)
+    return size.value
+
+
+def _workspace(config, n, m, p, device):
+    """Device scratch for the MFMA reads (mf_mm_workspace bytes, 256-byte aligned)."""
+    return torch.empty(max(1, mm_workspace_bytes(config, n, m, p)), dtype=torch.uint8,
+                       device=device)
+
+
+def bias_add(out, bias, status=None):
+    """out += bias in place (FP32 [N, O], row stride out.stride(0)); a non-finite sum sets
+    STATUS_OUTPUT in ``status``."""
+    require_device(out)
+    if out.dtype != torch.float32 or out.stride(1) != 1 or bias.shape != (out.shape[1],):
+        raise ValueError("bias_add takes an FP32 row-major output and a matching bias")
+    bias = bias.to(device=out.device, dtype=torch.float32).contiguous()
+    with torch.cuda.device(out.device):
+        check(library().mf_bias_add(_ptr(out), out.shape[0], out.shape[1], out.stride(0),
+                                    _ptr(bias), _ptr(status), _stream(out.device)), "bias add")
+    return out
 
 
 def stable_sum(totals, xscale, wscale, config, col0, out):

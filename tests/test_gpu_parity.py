@@ -801,3 +801,89 @@ def test_wide_group_quantizers_bit_exact(hip_device, wgran, igran):
     assert bits_equal(q.cpu().to(torch.int64) & 0xFFFF, q_ref & 0xFFFF)
     assert bits_equal(xs, xs_ref)
     assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
+
+
+def test_noisy_mfma_unsplit_epilogue(hip_device):
+    """A grid of 512 blocks or more keeps the fused single-kernel read (no read split):
+    its output is the reference epilogue of the kernel's own totals, bit for bit."""
+    cfg = noisy_case("write")
+    gen = torch.Generator().manual_seed(34)
+    a = torch.randn(1024, 128, generator=gen)
+    b = torch.randn(128, 2048, generator=gen)
+    q, xs = oracle.input_tiles(a, cfg)
+    packed, ws = oracle.weight_tiles(b.T, cfg)
+    n, m, r = q.shape
+    p, c = packed.shape[1], cfg.array_size[1]
+    assert (p * c + 63) // 64 * ((n + 63) // 64) >= 512
+    codes_t = packed_columns(packed).to(hip_device)
+    totals = hip.mm_totals(q.to(hip_device), codes_t, cfg, 77, 2).cpu()
+    fused = hip.mm(q.to(hip_device), xs.to(hip_device), packed.to(hip_device), codes_t,
+                   ws.reshape(-1, p * c).to(hip_device), cfg, 77, 2).cpu()
+    restored = oracle.execute(q, xs, packed, ws, cfg, 77, 2, p * c, totals=totals)
+    assert bits_equal(fused, restored)
+
+
+def test_noisy_terms_reused_across_reads(hip_device):
+    """Write noise is event-independent: a programmed matrix samples its conductances
+    once; later reads reuse them and give the same output as a fresh program, and
+    reprogramming samples new ones."""
+    from memfast_amd import AnalogMatrix, Simulator
+
+    cfg = noisy_case("write")
+    gen = torch.Generator().manual_seed(35)
+    w = torch.randn(100, 200, generator=gen)
+    x = torch.randn(40, 200, generator=gen).to(hip_device)
+    sim = Simulator(cfg, device=hip_device)
+    matrix = AnalogMatrix(w.to(hip_device), sim, name="layer")
+    assert hip.mm_kernel(cfg, 40, 4, matrix.p) == 2
+    first = matrix(x)
+    assert matrix._terms_source is not None
+    second = matrix(x)
+    fresh = AnalogMatrix(w.to(hip_device), Simulator(cfg, device=hip_device), name="layer")(x)
+    assert bits_equal(first, second) and bits_equal(second, fresh)
+    expected = oracle.mm(x.cpu(), w.T, cfg, name="layer")
+    rel = (second.cpu() - expected).abs() / expected.abs().clamp_min(1e-6)
+    assert (rel > 1e-5).float().mean().item() <= 0.02
+    w2 = torch.randn(100, 200, generator=gen)
+    matrix.update_weight(w2.T.to(hip_device))
+    after = matrix(x)
+    fresh2 = AnalogMatrix(w2.to(hip_device), Simulator(cfg, device=hip_device), name="layer")(x)
+    assert bits_equal(after, fresh2)
+
+
+def test_layer_input_and_bias_checks_in_one_status_read(hip_device):
+    """AnalogLinear defers the finiteness check of its input to the read's status word:
+    the reference's messages (memfast/quantization.py:12-13 grouped, :124-125 fixed scale),
+    raised before the read event advances; a bias that overflows FP32 takes the FP64
+    retry and then raises like the reference (simulator.py:612-615, :643-644)."""
+    from torch import nn
+
+    from memfast_amd import Simulator
+    from memfast_amd.nn import AnalogLinear
+
+    cfg = ideal(**CONFIG2 | dict(array_size=(64, 32), adc_bits=8, input_quant_gran=(1, 32)))
+    torch.manual_seed(9)
+    source = nn.Linear(70, 40)
+    layer = AnalogLinear(source, Simulator(cfg, device=hip_device)).to(hip_device)
+    x = torch.randn(5, 70, device=hip_device)
+    good = layer(x)
+    assert layer._event == 1
+    bad = x.clone()
+    bad[2, 3] = float("nan")
+    with pytest.raises(ValueError, match="finite in torch.float32"):
+        layer(bad)
+    assert layer._event == 1
+    layer.set_input_scale(0.05)
+    with pytest.raises(ValueError, match=r"^quantized values must be finite$"):
+        layer(bad)
+    assert layer._event == 1
+    layer.set_input_scale(None)
+    again = layer(x)
+    assert layer._event == 2 and bits_equal(again, good)
+    # Output + bias beyond FP32 (FLT_MAX + ~1e32): the FP64 retry holds it, the cast back
+    # to FP32 does not.
+    layer.bias.fill_(torch.finfo(torch.float32).max)
+    big = torch.full((2, 70), 1e32, device=hip_device)
+    with pytest.raises(FloatingPointError):
+        layer(big)
+    assert layer._event == 2
