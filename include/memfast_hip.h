@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 3
+#define MF_ABI_VERSION 4
 #define MF_MAX_SLICES 32
 
 enum {
@@ -179,12 +179,18 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
  * mf_mm_workspace() bytes (256-byte aligned) the MFMA kernel is used;
  * `variant` picks its tiling (0 default, 1: 64 vectors per wave, 2: 32 vectors
  * per wave; the tuned mode's schedule grid).  Results do not depend on it.
+ * out_cols (1..p*C) and k_rows (1..m*R) are the matrix's logical output columns
+ * and input rows: the MFMA kernels compute only columns [0, out_cols) (the
+ * reference slices the rest away before any check, :586) and skip the reads
+ * that lie wholly in the zero padding past row k_rows, whose counts are 0
+ * (leaving out those +0 terms does not change torch's sum).  Pass p*C and m*R
+ * for every column and read.
  * status (may be NULL) receives MF_STATUS_OUTPUT when an output is non-finite. */
 int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
-          const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo,
-          void *workspace, int64_t workspace_bytes, int32_t variant, uint32_t *status,
-          void *stream);
+          int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed, uint64_t event,
+          float *out, int64_t ldo, void *workspace, int64_t workspace_bytes, int32_t variant,
+          uint32_t *status, void *stream);
 
 /* Bias of an FP32 read (memfast/simulator.py:612-613, `out + bias`): out[v, c]
  * += bias[c] for c < o, one FP32 add each; a non-finite sum sets

@@ -337,11 +337,16 @@ bool terms_event_independent(const mf_config *cfg) { return !cfg->has_read; }
 // workspace (at least 64 columns).  g: optional injected conductances.
 // reuse: the workspace already holds this program's event-independent terms
 // for every column (a previous call with the same codes, seed and config).
+// ocols, g_run: output columns computed and reads executed (the logical matrix;
+// columns past ocols are left unwritten, reads past g_run hold only padding).
 int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *q,
                  const float *xscale, i64 n, i64 m, const u8 *packed_t, const float *wscale, i64 p,
                  const float *g, u32 seed, u64 event, float *out, i64 ldo, void *workspace,
-                 i64 bytes, int totals, u32 *status, hipStream_t s, bool reuse = false) {
+                 i64 bytes, int totals, u32 *status, hipStream_t s, bool reuse = false,
+                 i64 ocols = -1, i64 g_run = -1) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
+    if (ocols < 0) ocols = ncols;
+    if (g_run < 0) g_run = G;
     const i64 per_block = noisy_block_bytes(cfg, m);
     // Split read (fused output only, when the whole program's terms fit).
     const i64 split = totals ? 1 : noisy_split(cfg, n, m, p);
@@ -350,12 +355,12 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
     const bool use_split = split > 1 && bytes >= full + scratch;
     const i64 max_cb = use_split ? full / per_block : (bytes / per_block) / 2 * 2;
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
-    reuse = reuse && g == nullptr && terms_event_independent(cfg) && max_cb * 32 >= ncols;
+    reuse = reuse && g == nullptr && terms_event_independent(cfg) && max_cb * 32 >= ocols;
     uint4 *gs = static_cast<uint4 *>(workspace);
     float *partial = use_split ? reinterpret_cast<float *>(static_cast<char *>(workspace) + full)
                                : nullptr;
-    for (i64 c_begin = 0; c_begin < ncols; c_begin += max_cb * 32) {
-        const i64 cols = (ncols - c_begin) < max_cb * 32 ? (ncols - c_begin) : max_cb * 32;
+    for (i64 c_begin = 0; c_begin < ocols; c_begin += max_cb * 32) {
+        const i64 cols = (ocols - c_begin) < max_cb * 32 ? (ocols - c_begin) : max_cb * 32;
         const i64 CB = (cols + 63) / 64 * 2;
         const i64 threads = i64(cfg->n_w) * CB * G * ks * 64;
         if (reuse) {
@@ -379,20 +384,20 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         args.G = G;
         args.ldo = ldo;
         args.ldws = ncols;
-        args.ncols = ncols;
+        args.ncols = ocols;
         args.c_begin = c_begin;
         args.CB = CB;
         args.totals = totals;
         args.g_begin = 0;
-        args.g_end = G;
-        args.g_step = G;
+        args.g_end = g_run;
+        args.g_step = g_run;
         unsigned gz = 1;
         if (use_split) {
             args.totals = 1;
             args.out = partial;
             args.ldo = ncols;
-            args.g_step = (G + split - 1) / split;
-            gz = unsigned((G + args.g_step - 1) / args.g_step);
+            args.g_step = (g_run + split - 1) / split;
+            gz = unsigned((g_run + args.g_step - 1) / args.g_step);
         }
         const dim3 grid{unsigned(CB / 2), unsigned((n + 63) / 64), gz};
         const bool nl = cfg->has_nonlinear != 0;
@@ -408,8 +413,9 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         }
     }
     if (use_split)
-        hipLaunchKernelGGL(k_restore_sum_f32, dim3(grid_for(n * ncols)), dim3(256), 0, s, partial, n,
-                           G, ncols, ncols, xscale, wscale, ncols, out, ldo, level_power(G), status);
+        hipLaunchKernelGGL(k_restore_sum_f32, dim3(grid_for(n * ocols)), dim3(256), 0, s, partial, n,
+                           G, g_run, ncols, ocols, xscale, wscale, ncols, out, ldo, level_power(G),
+                           status);
     return check_launch("noisy MFMA read");
 }
 
@@ -915,15 +921,28 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64
     return MF_OK;
 }
 
+// Reads that hold at least one of the first k_rows rows (reads tile the
+// arrays: R a multiple of P, as the MFMA kernels require).
+static i64 reads_with_rows(const mf_config *cfg, i64 m, i64 k_rows) {
+    const i64 G = m * cfg->reads;
+    if (cfg->rows % cfg->read_rows) return G;
+    const i64 used = (k_rows + cfg->read_rows - 1) / cfg->read_rows;
+    return used < G ? used : G;
+}
+
 int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
           const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
-          const void *g, uint32_t seed, uint64_t event, float *out, int64_t ldo, void *workspace,
-          int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream) {
+          int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed, uint64_t event,
+          float *out, int64_t ldo, void *workspace, int64_t workspace_bytes, int32_t variant,
+          uint32_t *status, void *stream) {
     const int valid = check_narrow(cfg);
     if (valid) return valid;
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
         ldo < p * cfg->cols)
         return fail(MF_E_INVALID, "invalid mm arguments");
+    if (out_cols < 1 || out_cols > p * cfg->cols || k_rows < 1 || k_rows > m * cfg->rows)
+        return fail(MF_E_INVALID, "out_cols must be in [1, p*C] and k_rows in [1, m*R]");
+    const i64 g_run = reads_with_rows(cfg, m, k_rows);
     if (cfg->n_in > 8 || cfg->n_w > 8) return fail(MF_E_UNSUPPORTED, "more than 8 slices");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const i64 G = m * cfg->reads;
@@ -963,9 +982,10 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         args.n = n;
         args.kp = kp;
         args.G = G;
+        args.G_run = g_run;
         args.ldo = ldo;
         args.ldws = ncols;
-        args.ncols = ncols;
+        args.ncols = out_cols;
         args.Gr = cfg->reads;
         args.R = cfg->rows;
         args.P = cfg->read_rows;
@@ -976,7 +996,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         variant &= ~MF_MM_REUSE_TERMS;
         if (variant < 0 || variant > 2) return fail(MF_E_INVALID, "unknown kernel variant %d", variant);
         const int tn = (ks == 1 && variant == 1) ? 2 : 1;
-        const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (ncols + 63) / 64;
+        const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (out_cols + 63) / 64;
         if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
         const dim3 grid{unsigned(gx), unsigned(gy), 1u};
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
@@ -999,7 +1019,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         const int launched = launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p,
                                           nullptr, seed, event, out, ldo, workspace,
                                           workspace_bytes, 0, status, s,
-                                          (variant & MF_MM_REUSE_TERMS) != 0);
+                                          (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run);
         if (timing.first) {
             hipEventRecord(timing.second, s);
             g_profile.pending.push_back(timing);

@@ -269,9 +269,10 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
     const u32 slot_x = slot_live ? plan.ca_xnat[slot_ca] : 0u;
     const u32 slot_w = slot_live ? plan.cw_wnat[slot_cw] : 0u;
     const int slot_lim = slot_live ? plan.ca_factor[slot_ca] * plan.cw_limit[slot_cw] : 0;
-    for (int g = 0; g < G; ++g) {
+    const int G_run = int(args.G_run);   // reads past G_run hold only zero padding
+    for (int g = 0; g < G_run; ++g) {
         const int cur = g & 1;
-        if (g + 1 < G) fetch(g + 1);
+        if (g + 1 < G_run) fetch(g + 1);
 
         v4i Wr[KS], Xr[TN][KS];
 #pragma unroll
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
             }
         }
 
-        if (g + 1 < G) stash(cur ^ 1);
+        if (g + 1 < G_run) stash(cur ^ 1);
         __syncthreads();
     }
 
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float s = acc0[tn][qd * 4 + e] + acc1[tn][qd * 4 + e];
-                if (G >= 256 && c + e < args.ncols) s = s + dst[e];
+                if (G_run >= 256 && c + e < args.ncols) s = s + dst[e];
                 v[e] = s;
                 finite = finite && (c + e >= args.ncols || fabsf(s) <= FLT_MAX);
             }

@@ -72,6 +72,7 @@ struct IdealArgs {
     float *out;             // [n, ldo]
     u32 *status;            // optional: MF_STATUS_OUTPUT for a non-finite output
     i64 n, kp, G, ldo, ldws, ncols;
+    i64 G_run;              // reads executed: [0, G_run) (the rest is zero padding)
     int Gr, R, P;
     int a_bits, w_bits;     // code widths (< 8: sign-extend bytes on load)
 };
@@ -129,9 +130,9 @@ template <int KS, int NA, bool NONLINEAR>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
 // (float(T) * xs) * ws summed over reads in torch's cascade order, from slice
 // totals [n, G, ldt]: the epilogue of a read split across blocks.
-__global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 ldt, i64 ncols,
-                                  const float *xscale, const float *wscale, i64 ldws, float *out,
-                                  i64 ldo, int lp, u32 *status);
+__global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, i64 ldt,
+                                  i64 ncols, const float *xscale, const float *wscale, i64 ldws,
+                                  float *out, i64 ldo, int lp, u32 *status);
 
 // ---- noisy-device MFMA read, wide configurations (noisy_wide.hip) ----------
 // Same ADC model as NoisyPlan; integer totals accumulate modulo 2^32 as

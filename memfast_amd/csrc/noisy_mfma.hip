@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float s = acc0[qd * 4 + e] + acc1[qd * 4 + e];
-            if (G >= 256 && c + e < args.ncols) s = s + dst[e];
+            if (g1 >= 256 && c + e < args.ncols) s = s + dst[e];
             v[e] = s;
             finite = finite && (c + e >= args.ncols || fabsf(s) <= FLT_MAX);
         }
@@ -290,16 +290,16 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
-__global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 ldt, i64 ncols,
-                                  const float *xscale, const float *wscale, i64 ldws, float *out,
-                                  i64 ldo, int lp, u32 *status) {
+__global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, i64 ldt,
+                                  i64 ncols, const float *xscale, const float *wscale, i64 ldws,
+                                  float *out, i64 ldo, int lp, u32 *status) {
     bool finite = true;
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < n * ncols;
          i += i64(gridDim.x) * blockDim.x) {
         const i64 v = i / ncols, c = i - v * ncols;
         Cascade<float> cascade;
         cascade.reset();
-        for (i64 g = 0; g < G; ++g) {
+        for (i64 g = 0; g < g_run; ++g) {
             float x = totals[(v * G + g) * ldt + c] * xscale[v * G + g];
             x = x * wscale[g * ldws + c];
             cascade.push(x, lp);

@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -137,8 +137,8 @@ SIGNATURES = {
                    ct.c_int),
     "mf_partial": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
                     _P, _P, _P], ct.c_int),
-    "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
-               _I64, _P, _I64, _I32, _P, _P], ct.c_int),
+    "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
+               ct.c_uint64, _P, _I64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
                       _P], ct.c_int),
     "mf_bias_add": ([_P, _I64, _I64, _I64, _P, _P, _P], ct.c_int),
@@ -604,7 +604,7 @@ def terms_event_independent(config):
 
 
 def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=None, out=None,
-       variant=0, status=None, workspace=None, reuse_terms=False):
+       variant=0, status=None, workspace=None, reuse_terms=False, out_cols=None, k_rows=None):
     """Fused read + scale restore: [N, p*C] FP32, summed over reads in torch's order.
 
     Wide configurations: ``packed_t`` is the uint32 kernel copy of the codes
@@ -612,7 +612,9 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     ``workspace`` (optional, at least ``mm_workspace_bytes``) is the MFMA
     kernels' scratch; with ``reuse_terms`` it still holds the conductance terms
     a previous call of this program sampled (honoured when they do not depend
-    on the read event).
+    on the read event).  ``out_cols``/``k_rows`` (default: all) are the logical
+    output columns and input rows; the MFMA kernels leave columns past
+    ``out_cols`` unwritten and skip reads wholly past row ``k_rows``.
     """
     supported(config)
     require_device(q)
@@ -621,6 +623,10 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     if config.wide:
         return _mm_wide(q, xscale, packed, packed_t, wscale, config, seed, event,
                         conductance=conductance, out=out, status=status)
+    if out_cols is not None and not 1 <= out_cols <= p * c:
+        raise ValueError("out_cols must be in [1, p*C]")
+    if k_rows is not None and not 1 <= k_rows <= m * r:
+        raise ValueError("k_rows must be in [1, m*R]")
     g = conductance
     kernel = mm_kernel(config, n, m, p) if g is None and packed_t is not None else 0
     if g is None and kernel == 0 and needs_conductances(config):
@@ -650,6 +656,7 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
             library().mf_mm(
                 ct.byref(descriptor(config)), _ptr(q), _ptr(xscale), n,
                 m, _ptr(packed), _ptr(packed_t), _ptr(wscale), p,
+                p * c if out_cols is None else out_cols, m * r if k_rows is None else k_rows,
                 _ptr(g), seed, event, _ptr(out), out.stride(0), _ptr(workspace),
                 0 if workspace is None else workspace.numel(), variant, _ptr(status),
                 _stream(q.device),

@@ -236,7 +236,8 @@ class Simulator:
             output = hip.mm(q, xscale, packed, codes if hip.mm_kernel(
                 config, q.shape[0], q.shape[1], p) or config.wide else None,
                 wscale.reshape(-1, p * config.array_size[1]), config, config.seed ^ tag, event,
-                variant=TILE_VARIANTS[KERNEL_TILES[0]], status=status)
+                variant=TILE_VARIANTS[KERNEL_TILES[0]], status=status,
+                out_cols=out_features, k_rows=matrix.shape[0])
         flags = int(status.item())
         if flags & hip.STATUS_INPUT:
             raise ValueError("A must be finite")
@@ -639,7 +640,8 @@ class AnalogMatrix(nn.Module):
             output = hip.mm(q, xscale, packed, codes_t, self.weight_scale.reshape(-1, self.p * c),
                             config, self.seed, event,
                             variant=TILE_VARIANTS.get(schedule.get("tile"), 0), status=status,
-                            workspace=workspace, reuse_terms=reuse)
+                            workspace=workspace, reuse_terms=reuse,
+                            out_cols=self.out_features, k_rows=self.in_features)
             if source is not None:
                 self._terms_source = source
         output = output[:, : self.out_features].contiguous()

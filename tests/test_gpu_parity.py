@@ -887,3 +887,31 @@ def test_layer_input_and_bias_checks_in_one_status_read(hip_device):
     with pytest.raises(FloatingPointError):
         layer(big)
     assert layer._event == 2
+
+
+EXTENT_CASES = [
+    ("ideal", ideal(**CONFIG2 | dict(array_size=(64, 32))), 9, 200, 70),
+    ("ideal_258_reads", ideal(**CONFIG2 | dict(array_size=(64, 32))), 3, 8200, 40),
+    ("write_split", noisy_case("write"), 9, 200, 70),
+    ("shared_unsplit", noisy_case("rows64"), 1030, 300, 2040),
+]
+
+
+@pytest.mark.parametrize("name,cfg,n,k,o", EXTENT_CASES, ids=[c[0] for c in EXTENT_CASES])
+def test_logical_extent_matches_full_read(hip_device, name, cfg, n, k, o):
+    """Computing only the logical output columns and skipping reads wholly in the zero
+    padding past row K gives the same outputs, bit for bit, as the full read."""
+    gen = torch.Generator().manual_seed(46)
+    a = torch.randn(n, k, generator=gen).to(hip_device)
+    b = torch.randn(k, o, generator=gen).to(hip_device)
+    q, xs = hip.input_tiles(a, cfg)
+    packed, packed_t, ws = hip.weight_tiles(b.T, cfg)
+    nq, m, r = q.shape
+    p, c = packed.shape[1], cfg.array_size[1]
+    kernel = hip.mm_kernel(cfg, nq, m, p)
+    assert kernel in (1, 2)
+    assert m * cfg.reads_per_array > -(-k // cfg.read_rows)     # some reads are all padding
+    full = hip.mm(q, xs, packed, packed_t, ws.reshape(-1, p * c), cfg, 11, 4)
+    part = hip.mm(q, xs, packed, packed_t, ws.reshape(-1, p * c), cfg, 11, 4, out_cols=o,
+                  k_rows=k)
+    assert bits_equal(part[:, :o], full[:, :o])
