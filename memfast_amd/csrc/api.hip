@@ -288,11 +288,14 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
         plan->alpha[w] = cfg->has_nonlinear ? cfg->f_alpha_over_max[w] : 0.0f;
         plan->fw[w] = float(cfg->w_factor[w]);
     }
+    i64 factor_sum = 0;
     for (int a = 0; a < cfg->n_in; ++a) {
         plan->fa[a] = float(cfg->in_factor[a]);
         plan->in_shift[a] = cfg->in_shift[a];
         plan->in_mask4[a] = u32(cfg->in_mask[a]) * 0x01010101u;
+        for (int w = 0; w < cfg->n_w; ++w) factor_sum += cfg->in_factor[a] * cfg->w_factor[w];
     }
+    plan->bias = u32(0) - u32(u64(factor_sum) * 0x400000u);
     *ks = cfg->read_rows / 16;
     return true;
 }
@@ -302,7 +305,7 @@ i64 noisy_block_bytes(const mf_config *cfg, i64 m) { return i64(cfg->n_w) * 32 *
 
 bool noisy_extent_ok(i64 n, i64 m, const mf_config *cfg) {
     const i64 kp = m * cfg->rows;
-    return 64 * kp <= 0x7FFFFFFF && (n + 63) / 64 <= 65535;
+    return 64 * kp <= 0x7FFFFFFF && (n + 63) / 64 <= 0x7FFFFFFF;
 }
 
 // Blocks of the noisy read (64 columns x 64 vectors each) below which the
@@ -367,10 +370,10 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
             // terms already in place
         } else if (ks == 2) {
             hipLaunchKernelGGL(k_split_conductances<2>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
-                               packed_t, g, m, p, ncols, seed, event, c_begin, CB, gs);
+                               packed_t, g, m, p, ncols, seed, event, c_begin, CB, plan, gs);
         } else {
             hipLaunchKernelGGL(k_split_conductances<4>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
-                               packed_t, g, m, p, ncols, seed, event, c_begin, CB, gs);
+                               packed_t, g, m, p, ncols, seed, event, c_begin, CB, plan, gs);
         }
         NoisyArgs args{};
         args.q = q;
@@ -399,7 +402,7 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
             args.g_step = (g_run + split - 1) / split;
             gz = unsigned((g_run + args.g_step - 1) / args.g_step);
         }
-        const dim3 grid{unsigned(CB / 2), unsigned((n + 63) / 64), gz};
+        const dim3 grid{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
         const bool nl = cfg->has_nonlinear != 0;
         if (ks == 4) {
             if (nl) hipLaunchKernelGGL((k_noisy<4, 5, true>), grid, dim3(256), 0, s, plan, args);

@@ -107,6 +107,7 @@ struct NoisyPlan {
     float k1[8], top[8], alpha[8], fa[8], fw[8];
     int in_shift[8];
     u32 in_mask4[8];   // input slice mask replicated into four bytes
+    u32 bias;          // -0x400000 * sum(fa*fw) modulo 2^32
 };
 
 struct NoisyArgs {
@@ -122,10 +123,11 @@ struct NoisyArgs {
     int totals;
 };
 
+// Terms are k1[w] * (g - L), so the read's MFMA output is in ADC counts.
 template <int KS>
 __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, const float *g_in,
                                      i64 m, i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin,
-                                     i64 CB, uint4 *gs);
+                                     i64 CB, const NoisyPlan plan, uint4 *gs);
 template <int KS, int NA, bool NONLINEAR>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
 // (float(T) * xs) * ws summed over reads in torch's cascade order, from slice

@@ -6,11 +6,14 @@
 //   I = sum_r (V * da/Ma) * (g[r,c] - L),   z = I * Ma*Mw / unit,
 //   z = z / (1 + |alpha/max_w * z|) (S-curve),  code = round(clamp(z, 0, max_w)),
 //   T = sum_a sum_w fa*fw*code.
-// Here z = (V*Mw/unit) * sum_r da * (g - L): the input digits da are small
-// integers (exact in bf16) and g - L (FP32) is split into three bf16 terms
-// hi + mid + lo that sum to it exactly, so three bf16 MFMAs with FP32
-// accumulation give the current to FP32 accuracy.  Results agree with the CPU
+// Here z = sum_r da * k1 * (g - L) with k1 = V*Mw/unit: the input digits da are
+// small integers (exact in bf16) and k1 * (g - L) (FP32) is split into three
+// bf16 terms hi + mid + lo that sum to it exactly, so three bf16 MFMAs with
+// FP32 accumulation give z to FP32 accuracy.  Results agree with the CPU
 // reference to its own FP32 rounding (codes may flip at rounding boundaries).
+// ADC: y = z + 1.5*2^23 (fma with the S-curve factor) rounds half-even, med3
+// clamps, and v_mad_i32_i24 accumulates fa*fw*(0x400000 + code) modulo 2^32;
+// plan.bias removes the offset (|T| < 2^24, so float(T) is exact).
 //
 // k_split_conductances writes the conductances (programming, drift, stuck-at
 // and shared read noise, as memfast/reference.py:10-51, or an injected
@@ -42,7 +45,8 @@ template <int KS>
 __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg, const u8 *packed_t,
                                                             const float *g_in, i64 m, i64 p,
                                                             i64 ncols, u32 seed, u64 event,
-                                                            i64 c_begin, i64 CB, uint4 *gs) {
+                                                            i64 c_begin, i64 CB,
+                                                            const NoisyPlan plan, uint4 *gs) {
     constexpr int P = 16 * KS;
     const int R = cfg.rows, C = cfg.cols, W = cfg.n_w;
     const i64 kp = m * R, G = kp / P;
@@ -70,7 +74,7 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
                 const u64 cell = u64((((i * p + tt) * W + w) * R + r0 + j) * C + cc);
                 const float level = g_in ? g_in[cell]
                                          : cell_conductance<float>(cfg, code, w, cell, seed, read_seed);
-                const float delta = level - cfg.f_low;
+                const float delta = (level - cfg.f_low) * plan.k1[w];   // ADC counts per digit
                 const u32 hi = bf16_bits(delta);
                 const float r1 = delta - bf16_value(hi);
                 const u32 mid = bf16_bits(r1);
@@ -90,9 +94,11 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
 }
 
 template __global__ void k_split_conductances<2>(const mf_config, const u8 *, const float *, i64,
-                                                 i64, i64, u32, u64, i64, i64, uint4 *);
+                                                 i64, i64, u32, u64, i64, i64, const NoisyPlan,
+                                                 uint4 *);
 template __global__ void k_split_conductances<4>(const mf_config, const u8 *, const float *, i64,
-                                                 i64, i64, u32, u64, i64, i64, uint4 *);
+                                                 i64, i64, u32, u64, i64, i64, const NoisyPlan,
+                                                 uint4 *);
 
 // Buffer resource over [base, base + bytes): loads past the end return zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t noisy_buffer(const void *base, i64 bytes) {
@@ -119,6 +125,7 @@ __device__ __forceinline__ v8bf digits_bf16(uint2 word, int shift, u32 mask4) {
 
 template <int KS, int NA, bool NONLINEAR>
 __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const NoisyArgs args) {
+    const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     constexpr int P = 16 * KS;
     constexpr int BC = 64, BV = 64;
     const int tid = threadIdx.x;
@@ -126,8 +133,10 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wc = wave & 1, wv = wave >> 1;
     const int lrow = lane & 31, lhalf = lane >> 5;
-    const i64 c0 = i64(blockIdx.x) * BC;              // chunk-relative first column
-    const i64 v0 = i64(blockIdx.y) * BV;
+    // Vector blocks are the fast grid axis, so the blocks that share a column
+    // block's conductance terms run together (on one XCD's L2).
+    const i64 c0 = i64(blockIdx.y) * BC;              // chunk-relative first column
+    const i64 v0 = i64(blockIdx.x) * BV;
     const int G = int(args.G);
     const int A = plan.n_in, W = plan.n_w;
     const i64 kp = args.kp;
@@ -178,20 +187,40 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
             }
         }
 
-        float T[16];
+        // Integer totals modulo 2^32, offset by 0x400000 * sum(fa*fw) (plan.bias).
+        u32 Ti[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) T[r] = 0.0f;
+        for (int r = 0; r < 16; ++r) Ti[r] = 0u;
         const uint4 *frag_g = frag_base + i64(g) * 3 * KS * 64;
-        for (int w = 0; w < W; ++w) {
+        auto load_terms = [&](v8bf (&F)[3][KS], int w) {
             const uint4 *frag = frag_g + w * w_stride;
-            v8bf F[3][KS];
 #pragma unroll
             for (int term = 0; term < 3; ++term)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
                     F[term][ks] = __builtin_bit_cast(v8bf, frag[(term * KS + ks) * 64]);
-            const float k1 = plan.k1[w], top = plan.top[w], alpha = plan.alpha[w];
+        };
+        auto slice_reads = [&](const v8bf (&F)[3][KS], int w) {
+            const float top = MAGIC + plan.top[w], alpha = plan.alpha[w];
             const float fw = plan.fw[w];
+            auto convert = [&](const v16f &I, int a) {
+                const int f = int(plan.fa[a] * fw);   // |fa*fw| <= 2^14
+                const u32 f24 = u32(int(u32(f) << 8) >> 8);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    // The terms carry k1, so I is already z = I * Ma*Mw / unit.  Rounding
+                    // to an integer happens in the add (fma) to 1.5 * 2^23, then med3
+                    // clamps in that domain; its low 24 bits are 0x400000 + code.
+                    float y;
+                    if (NONLINEAR)
+                        y = fmaf(I[r], __builtin_amdgcn_rcpf(fmaf(fabsf(I[r]), alpha, 1.0f)), MAGIC);
+                    else
+                        y = I[r] + MAGIC;
+                    y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
+                    const int low = int(__float_as_uint(y) << 8) >> 8;
+                    Ti[r] += u32(low) * f24;
+                }
+            };
 #pragma unroll
             for (int a = 0; a < NA; ++a) {
                 if (a >= A) break;
@@ -201,16 +230,17 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks)
                         I = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B[a][ks], I, 0, 0, 0);
-                const float f = plan.fa[a] * fw;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float z = I[r] * k1;
-                    if (NONLINEAR) z = z * __builtin_amdgcn_rcpf(fmaf(fabsf(z), alpha, 1.0f));
-                    z = __builtin_amdgcn_fmed3f(z, 0.0f, top);
-                    T[r] = fmaf(rintf(z), f, T[r]);
-                }
+                convert(I, a);
             }
+        };
+        for (int w = 0; w < W; ++w) {
+            v8bf F[3][KS];
+            load_terms(F, w);
+            slice_reads(F, w);
         }
+        float T[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) T[r] = float(int(Ti[r] + plan.bias));
 
         if (args.totals) {
             if (n_out < args.n) {
