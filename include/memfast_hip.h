@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 4
+#define MF_ABI_VERSION 5
 #define MF_MAX_SLICES 32
 
 enum {
@@ -198,6 +198,30 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
  * finiteness scan that decides the FP64 retry (:614-615). */
 int mf_bias_add(float *out, int64_t n, int64_t o, int64_t ldo, const float *bias,
                 uint32_t *status, void *stream);
+
+/* Geometry of one convolution group for mf_conv_input_tiles: NCHW input
+ * [n, channels, height, width], this group's channels [c0, c0 + group_channels),
+ * output [out_height, out_width] and the kernel's size, stride, zero padding
+ * and dilation (as nn.Conv2d holds them). */
+typedef struct mf_conv_geometry {
+    int64_t n, channels, height, width;
+    int64_t c0, group_channels;
+    int64_t out_height, out_width;
+    int32_t kh, kw, sh, sw, ph, pw, dh, dw;
+} mf_conv_geometry;
+
+/* Implicit im2col: the input tiles that mf_input_tiles (fixed_scale != NULL,
+ * [K] per-column scales) or mf_quantize_inputs (fixed_scale == NULL, groups of
+ * gr rows and gc columns; `work` uint32 [ceil(rows/gr), ceil(K/gc)] scratch and
+ * `scale` FP32 of that shape) produce from the patch matrix that F.unfold
+ * builds for one convolution group (memfast/nn/convolution.py:49-54: row
+ * b*L + oh*out_width + ow, column (c*kh + i)*kw + j, K = group_channels*kh*kw),
+ * read straight from the FP32 NCHW input.  q [rows, m, R], xscale
+ * [rows, m*Gr]; a non-finite gathered value sets MF_STATUS_INPUT in status
+ * (may be NULL). */
+int mf_conv_input_tiles(const mf_config *cfg, const float *x, const mf_conv_geometry *geom,
+                        const float *fixed_scale, int64_t gr, int64_t gc, uint32_t *work,
+                        float *scale, uint8_t *q, float *xscale, uint32_t *status, void *stream);
 
 /* Overflow-safe FP64 restore and read sum of one chunk of `width` tiles
  * (memfast/simulator.py:57-66 restore_scales and :578-585, the wide/retry path

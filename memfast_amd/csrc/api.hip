@@ -658,6 +658,60 @@ int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, i
     return check_launch("input tiles");
 }
 
+int mf_conv_input_tiles(const mf_config *cfg, const float *x, const mf_conv_geometry *geom,
+                        const float *fixed_scale, int64_t gr, int64_t gc, uint32_t *work,
+                        float *scale, uint8_t *q, float *xscale, uint32_t *status, void *stream) {
+    int st = check_narrow(cfg);
+    if (st) return st;
+    if (!x || !geom || !q || !xscale) return fail(MF_E_INVALID, "invalid conv input-tile arguments");
+    const mf_conv_geometry g = *geom;
+    if (g.n < 1 || g.channels < 1 || g.height < 1 || g.width < 1 || g.c0 < 0 ||
+        g.group_channels < 1 || g.c0 + g.group_channels > g.channels || g.kh < 1 || g.kw < 1 ||
+        g.sh < 1 || g.sw < 1 || g.ph < 0 || g.pw < 0 || g.dh < 1 || g.dw < 1)
+        return fail(MF_E_INVALID, "invalid convolution geometry");
+    if (g.height > 0x3FFFFFFF || g.width > 0x3FFFFFFF || g.ph > 0x3FFFFFFF || g.pw > 0x3FFFFFFF ||
+        i64(g.dh) * (g.kh - 1) > 0x3FFFFFFF || i64(g.dw) * (g.kw - 1) > 0x3FFFFFFF)
+        return fail(MF_E_UNSUPPORTED, "convolution extent too large");
+    const i64 ho = (g.height + 2 * i64(g.ph) - i64(g.dh) * (g.kh - 1) - 1) / g.sh + 1;
+    const i64 wo = (g.width + 2 * i64(g.pw) - i64(g.dw) * (g.kw - 1) - 1) / g.sw + 1;
+    if (g.height + 2 * i64(g.ph) <= i64(g.dh) * (g.kh - 1) ||
+        g.width + 2 * i64(g.pw) <= i64(g.dw) * (g.kw - 1) || g.out_height != ho ||
+        g.out_width != wo)
+        return fail(MF_E_INVALID, "convolution output size does not match the geometry");
+    const i64 rows = g.n * ho * wo;
+    const i64 K = g.group_channels * g.kh * g.kw;
+    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (K + R - 1) / R, kp = m * R;
+    const int bits = cfg->activation_bits;
+    const float upper = float((1 << (bits - 1)) - 1);
+    const u32 mask = (1u << bits) - 1u;
+    if ((rows + 255) / 256 > 2147483647) return fail(MF_E_RESOURCE, "too many patches");
+    const dim3 grid(unsigned((rows + 255) / 256));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (fixed_scale) {
+        hipLaunchKernelGGL(k_conv_codes, grid, dim3(256), 0, s, x, g, K, kp, fixed_scale, i64(1),
+                           i64(0), i64(1), -upper, upper, mask, q, status, u32(MF_STATUS_INPUT));
+        hipLaunchKernelGGL(k_input_scales, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s, rows, K,
+                           m * Gr, R, P, Gr, fixed_scale, i64(1), i64(1), K, 1, xscale);
+        return check_launch("conv input tiles");
+    }
+    if (!work || !scale || gr < 1 || gc < 1)
+        return fail(MF_E_INVALID, "dynamic conv input tiles need work, scale and group sizes");
+    gr = gr < rows ? gr : rows;
+    gc = gc < K ? gc : K;
+    const i64 nrg = (rows + gr - 1) / gr, ncg = (K + gc - 1) / gc;
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
+    hipLaunchKernelGGL(k_conv_group_max, grid, dim3(256), 0, s, x, g, K, gr, gc, ncg, work, status,
+                       u32(MF_STATUS_INPUT));
+    hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg,
+                       upper, scale);
+    hipLaunchKernelGGL(k_conv_codes, grid, dim3(256), 0, s, x, g, K, kp, scale, gr, gc, ncg, -upper,
+                       upper, mask, q, status, u32(MF_STATUS_INPUT));
+    hipLaunchKernelGGL(k_input_scales, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s, rows, K,
+                       m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
+    return check_launch("conv input tiles");
+}
+
 static i64 lcm4(i64 gr) { return gr % 4 == 0 ? gr : (gr % 2 == 0 ? 2 * gr : 4 * gr); }
 
 int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,

@@ -212,6 +212,11 @@ __global__ void k_group_scale(const u32 *work, i64 groups, float upper, float *s
 __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
                               i64 gr, i64 gc, i64 ncg, int fixed, float lower, float upper,
                               u32 mask, u8 *q);
+__global__ void k_conv_codes(const float *x, const mf_conv_geometry g, i64 K, i64 kp,
+                             const float *scale, i64 gr, i64 gc, i64 ncg, float lower, float upper,
+                             u32 mask, u8 *q, u32 *status, u32 flag);
+__global__ void k_conv_group_max(const float *x, const mf_conv_geometry g, i64 K, i64 gr, i64 gc,
+                                 i64 ncg, u32 *work, u32 *status, u32 flag);
 __global__ void k_input_scales(i64 n, i64 k, i64 groups, int R, int P, int Gr, const float *scale,
                                i64 gr, i64 gc, i64 ncg, int fixed, float *xscale);
 __global__ void k_weight_codes(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m, i64 p,

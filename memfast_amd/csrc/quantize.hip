@@ -459,6 +459,134 @@ __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, cons
     }
 }
 
+// ---- implicit im2col: input tiles of a convolution's patch matrix ----------
+// Patch row r = b * L + oh * wo + ow (L = ho * wo), column k = (c * kh + i) * kw + j
+// (F.unfold's order) holds x[b, c0 + c, oh*sh - ph + i*dh, ow*sw - pw + j*dw], or 0
+// outside the image.  A wave owns 64 rows; lane t keeps row t's batch offset and
+// top-left input coordinate, and per 64-wide chunk of k each lane decomposes its
+// own k once and walks the rows (uniform loop), so stores are coalesced.
+struct ConvRows {
+    i64 base;   // offset of (b, c0, 0, 0) in x
+    int ih0, iw0;
+};
+
+__device__ __forceinline__ ConvRows conv_row(const mf_conv_geometry &g, i64 row) {
+    const i64 L = g.out_height * g.out_width;
+    const i64 b = row / L, l = row - b * L;
+    const i64 oh = l / g.out_width, ow = l - oh * g.out_width;
+    ConvRows r;
+    r.base = (b * g.channels + g.c0) * g.height * g.width;
+    r.ih0 = int(oh * g.sh - g.ph);
+    r.iw0 = int(ow * g.sw - g.pw);
+    return r;
+}
+
+struct ConvCol {
+    i64 offset;   // c * H * W
+    int di, dj;   // i * dh, j * dw
+};
+
+__device__ __forceinline__ ConvCol conv_col(const mf_conv_geometry &g, i64 k) {
+    const int kk = g.kh * g.kw;
+    const i64 c = k / kk;
+    const int rem = int(k - c * kk);
+    const int i = rem / g.kw, j = rem - (rem / g.kw) * g.kw;
+    ConvCol col;
+    col.offset = c * g.height * g.width;
+    col.di = i * g.dh;
+    col.dj = j * g.dw;
+    return col;
+}
+
+__device__ __forceinline__ float conv_value(const float *x, const mf_conv_geometry &g,
+                                            i64 base, int ih0, int iw0, const ConvCol &col) {
+    const int ih = ih0 + col.di, iw = iw0 + col.dj;
+    if (ih < 0 || ih >= g.height || iw < 0 || iw >= g.width) return 0.0f;
+    return x[base + col.offset + i64(ih) * g.width + iw];
+}
+
+// Codes q [rows, kp] (zero past K) with a fixed per-column scale (gc == 0) or
+// per-(group of gr rows, group of gc columns) scales [rows/gr, ncg].
+__global__ __launch_bounds__(256) void k_conv_codes(const float *x, const mf_conv_geometry g,
+                                                    i64 K, i64 kp, const float *scale, i64 gr,
+                                                    i64 gc, i64 ncg, float lower, float upper,
+                                                    u32 mask, u8 *q, u32 *status, u32 flag) {
+    const int lane = threadIdx.x & 63;
+    const i64 rows = g.n * g.out_height * g.out_width;
+    const i64 r0 = (i64(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64;
+    if (r0 >= rows) return;
+    const int count = int((rows - r0) < 64 ? (rows - r0) : 64);
+    const ConvRows mine = conv_row(g, r0 + (lane < count ? lane : 0));
+    bool finite = true;
+    for (i64 kc = 0; kc < kp; kc += 64) {
+        const i64 k = kc + lane;
+        const bool live = k < K;
+        const ConvCol col = conv_col(g, live ? k : 0);
+        const float fixed = (live && gc == 0) ? scale[k] : 1.0f;
+        for (int t = 0; t < count; ++t) {
+            const i64 base = (i64(__builtin_amdgcn_readlane(int(mine.base >> 32), t)) << 32) |
+                             u32(__builtin_amdgcn_readlane(int(mine.base), t));
+            const int ih0 = __builtin_amdgcn_readlane(mine.ih0, t);
+            const int iw0 = __builtin_amdgcn_readlane(mine.iw0, t);
+            const i64 row = r0 + t;
+            u8 code = 0;
+            if (live) {
+                const float v = conv_value(x, g, base, ih0, iw0, col);
+                finite = finite && fabsf(v) <= FLT_MAX;
+                const float sc = gc == 0 ? fixed : scale[(row / gr) * ncg + k / gc];
+                code = quantize_code(v, sc, lower, upper, mask);
+            }
+            if (k < kp) q[row * kp + k] = code;
+        }
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
+// Group maxima |x| of the patch matrix for groups of gr rows and gc columns:
+// work [rows/gr, ncg] (cleared), as float bits.
+__global__ __launch_bounds__(256) void k_conv_group_max(const float *x, const mf_conv_geometry g,
+                                                        i64 K, i64 gr, i64 gc, i64 ncg, u32 *work,
+                                                        u32 *status, u32 flag) {
+    const int lane = threadIdx.x & 63;
+    const i64 rows = g.n * g.out_height * g.out_width;
+    const i64 r0 = (i64(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64;
+    if (r0 >= rows) return;
+    const int count = int((rows - r0) < 64 ? (rows - r0) : 64);
+    const ConvRows mine = conv_row(g, r0 + (lane < count ? lane : 0));
+    bool finite = true;
+    for (i64 kc = 0; kc < K; kc += 64) {
+        const i64 k = kc + lane;
+        const bool live = k < K;
+        const ConvCol col = conv_col(g, live ? k : 0);
+        const i64 last = (kc + 63) < (K - 1) ? (kc + 63) : (K - 1);
+        const bool one_group = kc / gc == last / gc;
+        for (int t = 0; t < count; ++t) {
+            const i64 base = (i64(__builtin_amdgcn_readlane(int(mine.base >> 32), t)) << 32) |
+                             u32(__builtin_amdgcn_readlane(int(mine.base), t));
+            const int ih0 = __builtin_amdgcn_readlane(mine.ih0, t);
+            const int iw0 = __builtin_amdgcn_readlane(mine.iw0, t);
+            const i64 row = r0 + t;
+            float v = 0.0f;
+            if (live) {
+                v = fabsf(conv_value(x, g, base, ih0, iw0, col));
+                finite = finite && v <= FLT_MAX;
+            }
+            u32 bits = __float_as_uint(v);
+            if (one_group) {
+#pragma unroll
+                for (int d = 32; d >= 1; d >>= 1) {
+                    const u32 other = u32(__shfl_xor(int(bits), d, 64));
+                    bits = other > bits ? other : bits;
+                }
+                if (lane == 0 && bits) atomicMax(&work[(row / gr) * ncg + kc / gc], bits);
+            } else if (live && bits) {
+                atomicMax(&work[(row / gr) * ncg + k / gc], bits);
+            }
+        }
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
 // xscale [n, m*Gr]: scale of the read's first physical row, replicate-padded.
 __global__ void k_input_scales(i64 n, i64 k, i64 groups, int R, int P, int Gr,
                                const float *scale, i64 gr, i64 gc, i64 ncg, int fixed,

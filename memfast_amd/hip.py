@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -117,6 +117,12 @@ class MFResources(ct.Structure):
     ]
 
 
+class MFConvGeometry(ct.Structure):
+    _fields_ = [(name, ct.c_int64) for name in (
+        "n", "channels", "height", "width", "c0", "group_channels", "out_height", "out_width",
+    )] + [(name, ct.c_int32) for name in ("kh", "kw", "sh", "sw", "ph", "pw", "dh", "dw")]
+
+
 _P = ct.c_void_p
 _I64 = ct.c_int64
 _I32 = ct.c_int32
@@ -128,6 +134,8 @@ SIGNATURES = {
     "mf_source_hash": ([], ct.c_char_p),
     "mf_device_identity": ([ct.c_int, ct.POINTER(MFIdentity)], ct.c_int),
     "mf_input_tiles": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _P, _P], ct.c_int),
+    "mf_conv_input_tiles": ([_CFG, _P, ct.POINTER(MFConvGeometry), _P, _I64, _I64, _P, _P, _P,
+                             _P, _P, _P], ct.c_int),
     "mf_quantize_inputs": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P],
                            ct.c_int),
     "mf_quantize_weights": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P,
@@ -373,6 +381,56 @@ def input_tiles(value, config, fixed_scale=None, *, status=None):
             ),
             "input tiles",
         )
+    return q, xscale
+
+
+def conv_input_tiles(x, config, geometry, fixed_scale=None, *, status=None):
+    """Input tiles of one convolution group's patch matrix, gathered from NCHW ``x``.
+
+    Equals ``input_tiles(F.unfold(x, ...)[:, group block].transpose(1, 2).reshape(-1, K))``
+    (memfast/nn/convolution.py:49-54) without building the patch matrix.  ``geometry``
+    holds (c0, group_channels, kernel_size, stride, padding, dilation, out_size).
+    Narrow configurations only; a non-finite gathered value raises here without
+    ``status``, else sets STATUS_INPUT."""
+    supported(config)
+    require_device(x)
+    if config.wide:
+        raise BackendError("implicit im2col covers narrow configurations only")
+    c0, cg, kernel, stride, padding, dilation, out_size = geometry
+    value = x.to(torch.float32).contiguous()
+    n = value.shape[0]
+    rows = n * out_size[0] * out_size[1]
+    k = cg * kernel[0] * kernel[1]
+    r = config.array_size[0]
+    m = math.ceil(k / r)
+    q = torch.empty((rows, m, r), dtype=torch.uint8, device=x.device)
+    xscale = torch.empty((rows, m * config.reads_per_array), dtype=torch.float32, device=x.device)
+    geom = MFConvGeometry(n, value.shape[1], value.shape[2], value.shape[3], c0, cg,
+                          out_size[0], out_size[1], kernel[0], kernel[1], stride[0], stride[1],
+                          padding[0], padding[1], dilation[0], dilation[1])
+    own_status = status if status is not None else status_word(x.device)
+    scale = work = fixed = None
+    gr = gc = 0
+    if fixed_scale is None:
+        gr, gc = _group_dims((rows, k), config.input_quant_gran)
+        grid = (math.ceil(rows / gr), math.ceil(k / gc))
+        scale = torch.empty(grid, dtype=torch.float32, device=x.device)
+        work = torch.empty(grid, dtype=torch.int32, device=x.device)
+    else:
+        fixed = fixed_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
+        if fixed.numel() != k:
+            raise ValueError("fixed input scale must have one entry per input feature")
+    with torch.cuda.device(x.device):
+        check(
+            library().mf_conv_input_tiles(
+                ct.byref(descriptor(config)), _ptr(value), ct.byref(geom), _ptr(fixed), gr, gc,
+                _ptr(work), _ptr(scale), _ptr(q), _ptr(xscale), _ptr(own_status),
+                _stream(x.device),
+            ),
+            "conv input tiles",
+        )
+    if status is None and int(own_status.item()) & STATUS_INPUT:
+        raise ValueError(input_error(config, fixed_scale))
     return q, xscale
 
 

@@ -144,3 +144,120 @@ def test_convert_model(hip_device):
     expected = oracle_matrix(hidden, linear.weight, linear.bias, cfg, "3")
     check(got, expected, "ideal")
     assert math.isfinite(got.abs().max().item())
+
+
+# Implicit im2col: (N, C, H, W, groups, kernel, stride, padding, dilation).
+CONV_GEOMETRIES = [
+    (2, 4, 9, 9, 1, (3, 3), (2, 2), (1, 1), (1, 1)),
+    (3, 6, 11, 7, 2, (3, 2), (1, 2), (2, 0), (1, 1)),
+    (1, 8, 13, 13, 4, (3, 3), (1, 1), (2, 2), (2, 2)),
+    (2, 3, 20, 17, 1, (1, 1), (2, 2), (0, 0), (1, 1)),
+    (2, 16, 10, 10, 1, (5, 5), (1, 1), (2, 2), (1, 1)),
+    (1, 3, 96, 96, 1, (7, 7), (2, 2), (3, 3), (1, 1)),
+    (1, 5, 4, 6, 1, (4, 6), (3, 1), (0, 0), (1, 1)),
+]
+# (array_size, rows_per_read, input quantization): 48-row arrays pad K to a non-multiple of 64.
+CONV_QUANT = [((64, 32), 32, g) for g in ("fixed", (1, None), (1, 32), (4, 64), (None, None),
+                                           (3, None))]
+CONV_QUANT += [((48, 32), 16, g) for g in ("fixed", (1, None), (1, 16), (4, 16))]
+
+
+def _conv_case(geometry):
+    n, c, h, w, groups, kernel, stride, padding, dilation = geometry
+    out = [(e + 2 * p - d * (k - 1) - 1) // s + 1
+           for e, p, d, k, s in zip((h, w), padding, dilation, kernel, stride)]
+    return n, c, groups, kernel, stride, padding, dilation, out
+
+
+@pytest.mark.parametrize("geometry", CONV_GEOMETRIES)
+@pytest.mark.parametrize("quant", CONV_QUANT, ids=lambda q: f"{q[0][0]}-{q[2]}")
+def test_conv_input_tiles_match_unfold(hip_device, geometry, quant):
+    """mf_conv_input_tiles == input quantization of F.unfold's patch matrix, bit for bit,
+    for every convolution group; small cases also against the oracle's quantizer."""
+    from memfast_amd import hip
+    n, c, groups, kernel, stride, padding, dilation, out = _conv_case(geometry)
+    array, rows_per_read, gran = quant
+    extra = dict(array_size=array, rows_per_read=rows_per_read)
+    if gran != "fixed":
+        extra["input_quant_gran"] = gran
+    cfg = config("ideal", **extra)
+    torch.manual_seed(31)
+    x = torch.randn(n, c, *geometry[2:4]) * 3
+    x[:, :, ::3, 1::2] *= 20.0     # scale outliers so groups differ
+    patches = F.unfold(x, kernel, dilation, padding, stride)
+    per_group = c // groups
+    size = per_group * kernel[0] * kernel[1]
+    xd = x.to(hip_device)
+    for g in range(groups):
+        flat = patches[:, g * size:(g + 1) * size].transpose(1, 2).reshape(-1, size)
+        fixed = None
+        if gran == "fixed":
+            fixed = (torch.rand(1, size) * 0.1 + 0.01)
+        geom = (g * per_group, per_group, kernel, stride, padding, dilation, out)
+        status = hip.status_word(hip_device)
+        q, xscale = hip.conv_input_tiles(
+            xd, cfg, geom, None if fixed is None else fixed.to(hip_device), status=status)
+        ref_q, ref_scale = hip.input_tiles(
+            flat.to(hip_device), cfg, None if fixed is None else fixed.to(hip_device))
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        assert torch.equal(q.cpu(), ref_q.cpu()), (geometry, gran, g)
+        assert torch.equal(xscale.cpu().view(torch.int32), ref_scale.cpu().view(torch.int32))
+        if flat.shape[0] * size <= 200_000:
+            oq, oscale = oracle.input_tiles(flat, cfg, fixed)
+            assert torch.equal(q.cpu(), oq)
+            assert torch.equal(xscale.cpu().view(torch.int32), oscale.view(torch.int32))
+
+
+@pytest.mark.parametrize("gran", ["fixed", (1, 32)])
+def test_conv_input_tiles_flag_only_gathered_nonfinite(hip_device, gran):
+    """A non-finite pixel that some patch reads sets STATUS_INPUT; one that stride skips
+    (absent from F.unfold's patches as well) does not."""
+    from memfast_amd import hip
+    extra = {} if gran == "fixed" else dict(input_quant_gran=gran)
+    cfg = config("ideal", **extra)
+    x = torch.randn(1, 2, 8, 8)
+    geom = (0, 2, (1, 1), (2, 2), (0, 0), (1, 1), (4, 4))
+    fixed = torch.full((1, 2), 0.05, device=hip_device) if gran == "fixed" else None
+    skipped = x.clone()
+    skipped[0, 1, 3, 5] = float("nan")        # odd row: never on the stride-2 grid
+    assert torch.isfinite(F.unfold(skipped, 1, 1, 0, 2)).all()
+    read = x.clone()
+    read[0, 0, 4, 2] = float("inf")
+    for value, flagged in ((skipped, False), (read, True)):
+        status = hip.status_word(hip_device)
+        hip.conv_input_tiles(value.to(hip_device), cfg, geom, fixed, status=status)
+        torch.cuda.synchronize()
+        assert bool(int(status.item()) & hip.STATUS_INPUT) == flagged
+        if flagged:
+            with pytest.raises(ValueError, match="finite"):
+                hip.conv_input_tiles(value.to(hip_device), cfg, geom, fixed)
+
+
+@pytest.mark.parametrize("kind", list(EFFECTS))
+@pytest.mark.parametrize("geometry", CONV_GEOMETRIES[:5])
+def test_conv_implicit_path_matches_unfold_path(hip_device, kind, geometry):
+    """AnalogConv2d's implicit-im2col forward equals reading F.unfold's patches through the
+    same programmed matrices (same read events), bit for bit; fixed scales too."""
+    n, c, groups, kernel, stride, padding, dilation, out = _conv_case(geometry)
+    cfg = config(kind)
+    torch.manual_seed(32)
+    source = nn.Conv2d(c, 2 * groups, kernel, stride=stride, padding=padding, dilation=dilation,
+                       groups=groups).to(hip_device)
+    sim = Simulator(cfg, device=hip_device)
+    layer = AnalogConv2d(source, sim, name="conv")
+    x = torch.randn(n, c, *geometry[2:4], device=hip_device)
+    for fixed in (None, 0.04):
+        for matrix in layer.matrices:
+            matrix.set_input_scale(fixed)
+            matrix.reset_read()
+        got = layer(x)
+        for matrix in layer.matrices:
+            matrix.reset_read()
+        patches = F.unfold(x, kernel, dilation, padding, stride)
+        size = c // groups * kernel[0] * kernel[1]
+        parts = [matrix(patches[:, g * size:(g + 1) * size].transpose(1, 2))
+                 for g, matrix in enumerate(layer.matrices)]
+        expected = torch.cat(parts, dim=-1).transpose(1, 2).reshape(n, 2 * groups, *out)
+        assert torch.equal(got.view(torch.int32), expected.view(torch.int32)), (geometry, fixed)
+        assert all(matrix._event == 1 for matrix in layer.matrices)

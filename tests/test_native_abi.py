@@ -49,22 +49,27 @@ def test_abi_version_and_hash():
 
 
 def test_struct_layout_matches_c(tmp_path):
-    """Offsets of mf_config / sizes of mf_identity and mf_resources agree with gcc's."""
+    """Offsets of mf_config and mf_conv_geometry, sizes of mf_identity and mf_resources
+    agree with gcc's."""
     fields = [name for name, _ in hip.MFConfig._fields_]
+    geometry = [name for name, _ in hip.MFConvGeometry._fields_]
     probe = tmp_path / "layout.c"
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(){"]
     lines += [f'printf("%zu\\n", offsetof(mf_config, {name}));' for name in fields]
-    lines += ['printf("%zu\\n%zu\\n%zu\\n", sizeof(mf_config), sizeof(mf_identity), '
-              'sizeof(mf_resources)); return 0;}']
+    lines += [f'printf("%zu\\n", offsetof(mf_conv_geometry, {name}));' for name in geometry]
+    lines += ['printf("%zu\\n%zu\\n%zu\\n%zu\\n", sizeof(mf_config), sizeof(mf_identity), '
+              'sizeof(mf_resources), sizeof(mf_conv_geometry)); return 0;}']
     probe.write_text("\n".join(lines))
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-o", str(exe), str(probe)], check=True)
     values = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
                                              check=True).stdout.split()]
     offsets = [getattr(hip.MFConfig, name).offset for name in fields]
-    assert values[:len(fields)] == offsets
-    assert values[len(fields):] == [ctypes.sizeof(hip.MFConfig), ctypes.sizeof(hip.MFIdentity),
-                                    ctypes.sizeof(hip.MFResources)]
+    offsets += [getattr(hip.MFConvGeometry, name).offset for name in geometry]
+    assert values[:len(offsets)] == offsets
+    assert values[len(offsets):] == [ctypes.sizeof(hip.MFConfig), ctypes.sizeof(hip.MFIdentity),
+                                     ctypes.sizeof(hip.MFResources),
+                                     ctypes.sizeof(hip.MFConvGeometry)]
 
 
 def test_error_reporting_without_device():
