@@ -685,12 +685,15 @@ int mf_conv_input_tiles(const mf_config *cfg, const float *x, const mf_conv_geom
     const int bits = cfg->activation_bits;
     const float upper = float((1 << (bits - 1)) - 1);
     const u32 mask = (1u << bits) - 1u;
-    if ((rows + 255) / 256 > 2147483647) return fail(MF_E_RESOURCE, "too many patches");
-    const dim3 grid(unsigned((rows + 255) / 256));
+    if (rows > 0x7FFFFFFF || K > 0x7FFFFFFF || (kp + CONV_CHUNK_COLS - 1) / CONV_CHUNK_COLS > 65535)
+        return fail(MF_E_UNSUPPORTED, "too many patches or patch columns");
+    const dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((kp + CONV_CHUNK_COLS - 1) / CONV_CHUNK_COLS));
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const int vec = kp % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0;
     if (fixed_scale) {
         hipLaunchKernelGGL(k_conv_codes, grid, dim3(256), 0, s, x, g, K, kp, fixed_scale, i64(1),
-                           i64(0), i64(1), -upper, upper, mask, q, status, u32(MF_STATUS_INPUT));
+                           i64(0), i64(1), -upper, upper, mask, q, vec, status,
+                           u32(MF_STATUS_INPUT));
         hipLaunchKernelGGL(k_input_scales, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s, rows, K,
                            m * Gr, R, P, Gr, fixed_scale, i64(1), i64(1), K, 1, xscale);
         return check_launch("conv input tiles");
@@ -701,12 +704,12 @@ int mf_conv_input_tiles(const mf_config *cfg, const float *x, const mf_conv_geom
     gc = gc < K ? gc : K;
     const i64 nrg = (rows + gr - 1) / gr, ncg = (K + gc - 1) / gc;
     hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
-    hipLaunchKernelGGL(k_conv_group_max, grid, dim3(256), 0, s, x, g, K, gr, gc, ncg, work, status,
-                       u32(MF_STATUS_INPUT));
+    hipLaunchKernelGGL(k_conv_group_max, dim3(unsigned((rows + 255) / 256)), dim3(256), 0, s, x, g,
+                       K, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT));
     hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg,
                        upper, scale);
     hipLaunchKernelGGL(k_conv_codes, grid, dim3(256), 0, s, x, g, K, kp, scale, gr, gc, ncg, -upper,
-                       upper, mask, q, status, u32(MF_STATUS_INPUT));
+                       upper, mask, q, vec, status, u32(MF_STATUS_INPUT));
     hipLaunchKernelGGL(k_input_scales, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s, rows, K,
                        m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
     return check_launch("conv input tiles");

@@ -212,9 +212,10 @@ __global__ void k_group_scale(const u32 *work, i64 groups, float upper, float *s
 __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
                               i64 gr, i64 gc, i64 ncg, int fixed, float lower, float upper,
                               u32 mask, u8 *q);
+constexpr int CONV_CHUNK_COLS = 128;   // patch columns per k_conv_codes block
 __global__ void k_conv_codes(const float *x, const mf_conv_geometry g, i64 K, i64 kp,
                              const float *scale, i64 gr, i64 gc, i64 ncg, float lower, float upper,
-                             u32 mask, u8 *q, u32 *status, u32 flag);
+                             u32 mask, u8 *q, int vec, u32 *status, u32 flag);
 __global__ void k_conv_group_max(const float *x, const mf_conv_geometry g, i64 K, i64 gr, i64 gc,
                                  i64 ncg, u32 *work, u32 *status, u32 flag);
 __global__ void k_input_scales(i64 n, i64 k, i64 groups, int R, int P, int Gr, const float *scale,

@@ -462,88 +462,147 @@ __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, cons
 // ---- implicit im2col: input tiles of a convolution's patch matrix ----------
 // Patch row r = b * L + oh * wo + ow (L = ho * wo), column k = (c * kh + i) * kw + j
 // (F.unfold's order) holds x[b, c0 + c, oh*sh - ph + i*dh, ow*sw - pw + j*dw], or 0
-// outside the image.  A wave owns 64 rows; lane t keeps row t's batch offset and
-// top-left input coordinate, and per 64-wide chunk of k each lane decomposes its
-// own k once and walks the rows (uniform loop), so stores are coalesced.
-struct ConvRows {
-    i64 base;   // offset of (b, c0, 0, 0) in x
+// outside the image.  Lanes own consecutive patch rows, so for one k a wave reads
+// neighbouring pixels of one image row (coalesced); k is uniform across the wave and
+// its (c, i, j) decomposition advances incrementally in scalar registers.
+struct ConvLane {
+    i64 pixel;    // offset of x[b, c0, ih0, iw0] (may point outside the image)
     int ih0, iw0;
 };
 
-__device__ __forceinline__ ConvRows conv_row(const mf_conv_geometry &g, i64 row) {
-    const i64 L = g.out_height * g.out_width;
-    const i64 b = row / L, l = row - b * L;
-    const i64 oh = l / g.out_width, ow = l - oh * g.out_width;
-    ConvRows r;
-    r.base = (b * g.channels + g.c0) * g.height * g.width;
-    r.ih0 = int(oh * g.sh - g.ph);
-    r.iw0 = int(ow * g.sw - g.pw);
-    return r;
+__device__ __forceinline__ ConvLane conv_lane(const mf_conv_geometry &g, u32 row) {
+    const u32 wo = u32(g.out_width), L = u32(g.out_height) * wo;
+    const u32 b = row / L, l = row - b * L;
+    const u32 oh = l / wo, ow = l - oh * wo;
+    ConvLane lane;
+    lane.ih0 = int(oh) * g.sh - g.ph;
+    lane.iw0 = int(ow) * g.sw - g.pw;
+    lane.pixel = (i64(b) * g.channels + g.c0) * g.height * g.width + i64(lane.ih0) * g.width +
+                 lane.iw0;
+    return lane;
 }
 
-struct ConvCol {
-    i64 offset;   // c * H * W
-    int di, dj;   // i * dh, j * dw
+// Position (c, i, j) of column k in the patch and its offset from the patch origin.
+struct ConvTap {
+    int c, i, j;
+    i64 delta;   // c*H*W + i*dh*W + j*dw
+    int di, dj;  // i*dh, j*dw
+
+    __device__ __forceinline__ void start(const mf_conv_geometry &g, int k) {
+        const int kk = g.kh * g.kw;
+        c = k / kk;
+        const int rem = k - c * kk;
+        i = rem / g.kw;
+        j = rem - i * g.kw;
+        di = i * g.dh;
+        dj = j * g.dw;
+        delta = i64(c) * g.height * g.width + i64(di) * g.width + dj;
+    }
+    __device__ __forceinline__ void next(const mf_conv_geometry &g) {
+        if (++j < g.kw) {
+            dj += g.dw;
+            delta += g.dw;
+            return;
+        }
+        j = 0;
+        delta -= i64(dj);
+        dj = 0;
+        if (++i < g.kh) {
+            di += g.dh;
+            delta += i64(g.dh) * g.width;
+            return;
+        }
+        i = 0;
+        delta += i64(g.height - di) * g.width;
+        di = 0;
+        ++c;
+    }
 };
 
-__device__ __forceinline__ ConvCol conv_col(const mf_conv_geometry &g, i64 k) {
-    const int kk = g.kh * g.kw;
-    const i64 c = k / kk;
-    const int rem = int(k - c * kk);
-    const int i = rem / g.kw, j = rem - (rem / g.kw) * g.kw;
-    ConvCol col;
-    col.offset = c * g.height * g.width;
-    col.di = i * g.dh;
-    col.dj = j * g.dw;
-    return col;
+__device__ __forceinline__ float conv_load(const float *x, const mf_conv_geometry &g,
+                                           const ConvLane &lane, bool live, const ConvTap &t) {
+    const u32 ih = u32(lane.ih0 + t.di), iw = u32(lane.iw0 + t.dj);
+    return live && ih < u32(g.height) && iw < u32(g.width) ? x[lane.pixel + t.delta] : 0.0f;
 }
 
-__device__ __forceinline__ float conv_value(const float *x, const mf_conv_geometry &g,
-                                            i64 base, int ih0, int iw0, const ConvCol &col) {
-    const int ih = ih0 + col.di, iw = iw0 + col.dj;
-    if (ih < 0 || ih >= g.height || iw < 0 || iw >= g.width) return 0.0f;
-    return x[base + col.offset + i64(ih) * g.width + iw];
-}
+// Codes q [rows, kp] (zero past K) for a tile of 64 rows x CONV_CHUNK columns per
+// block, with a fixed per-column scale (gc == 0) or per-(gr rows, gc columns) group
+// scales [ceil(rows/gr), ncg].  Each wave quantizes CONV_CHUNK/4 columns of the 64
+// rows into LDS; the block then writes whole row segments.
+constexpr int CONV_CHUNK = CONV_CHUNK_COLS;
+constexpr int CONV_PITCH = CONV_CHUNK / 4 + 1;   // dwords per LDS row (odd: no conflicts)
 
-// Codes q [rows, kp] (zero past K) with a fixed per-column scale (gc == 0) or
-// per-(group of gr rows, group of gc columns) scales [rows/gr, ncg].
 __global__ __launch_bounds__(256) void k_conv_codes(const float *x, const mf_conv_geometry g,
                                                     i64 K, i64 kp, const float *scale, i64 gr,
                                                     i64 gc, i64 ncg, float lower, float upper,
-                                                    u32 mask, u8 *q, u32 *status, u32 flag) {
+                                                    u32 mask, u8 *q, int vec, u32 *status,
+                                                    u32 flag) {
+    __shared__ u32 tile[64 * CONV_PITCH];
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const i64 rows = g.n * g.out_height * g.out_width;
-    const i64 r0 = (i64(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64;
-    if (r0 >= rows) return;
-    const int count = int((rows - r0) < 64 ? (rows - r0) : 64);
-    const ConvRows mine = conv_row(g, r0 + (lane < count ? lane : 0));
+    const i64 r0 = i64(blockIdx.x) * 64;
+    const i64 kc = i64(blockIdx.y) * CONV_CHUNK;
+    const bool live = r0 + lane < rows;
+    const ConvLane me = conv_lane(g, u32(live ? r0 + lane : r0));
+    const int k0 = int(kc) + wave * (CONV_CHUNK / 4);
     bool finite = true;
-    for (i64 kc = 0; kc < kp; kc += 64) {
-        const i64 k = kc + lane;
-        const bool live = k < K;
-        const ConvCol col = conv_col(g, live ? k : 0);
-        const float fixed = (live && gc == 0) ? scale[k] : 1.0f;
-        for (int t = 0; t < count; ++t) {
-            const i64 base = (i64(__builtin_amdgcn_readlane(int(mine.base >> 32), t)) << 32) |
-                             u32(__builtin_amdgcn_readlane(int(mine.base), t));
-            const int ih0 = __builtin_amdgcn_readlane(mine.ih0, t);
-            const int iw0 = __builtin_amdgcn_readlane(mine.iw0, t);
-            const i64 row = r0 + t;
-            u8 code = 0;
-            if (live) {
-                const float v = conv_value(x, g, base, ih0, iw0, col);
-                finite = finite && fabsf(v) <= FLT_MAX;
-                const float sc = gc == 0 ? fixed : scale[(row / gr) * ncg + k / gc];
-                code = quantize_code(v, sc, lower, upper, mask);
+    if (k0 < K) {
+        ConvTap tap;
+        tap.start(g, k0);
+        const i64 rg = gc ? ((live ? r0 + lane : r0) / gr) * ncg : 0;
+        i64 cg = gc ? k0 / gc : 0, cr = gc ? k0 - cg * gc : 0;
+#pragma unroll 1
+        for (int e = 0; e < CONV_CHUNK / 16; ++e) {
+            u32 word = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int k = k0 + e * 4 + b;
+                if (k < K) {
+                    const float v = conv_load(x, g, me, live, tap);
+                    finite = finite && fabsf(v) <= FLT_MAX;
+                    const float sc = gc ? scale[rg + cg] : scale[k];
+                    word |= u32(quantize_code(v, sc, lower, upper, mask)) << (8 * b);
+                    tap.next(g);
+                    if (gc && ++cr == gc) {
+                        cr = 0;
+                        ++cg;
+                    }
+                }
             }
-            if (k < kp) q[row * kp + k] = code;
+            tile[lane * CONV_PITCH + wave * (CONV_CHUNK / 16) + e] = word;
         }
+    } else {
+#pragma unroll
+        for (int e = 0; e < CONV_CHUNK / 16; ++e) tile[lane * CONV_PITCH + wave * (CONV_CHUNK / 16) + e] = 0;
     }
     if (!finite && status) atomicOr(status, flag);
+    __syncthreads();
+    // Row `row` of the tile: 4 threads x CONV_CHUNK/4 bytes.
+    const int row = threadIdx.x >> 2, part = threadIdx.x & 3;
+    constexpr int WORDS = CONV_CHUNK / 16;
+    if (r0 + row >= rows) return;
+    const i64 col = kc + part * (CONV_CHUNK / 4);
+    if (col >= kp) return;
+    u32 w[WORDS];
+#pragma unroll
+    for (int e = 0; e < WORDS; ++e) w[e] = tile[row * CONV_PITCH + part * WORDS + e];
+    u8 *dst = q + (r0 + row) * kp + col;
+    if (vec) {   // kp and q 16-byte aligned: whole 16-byte pieces below kp
+#pragma unroll
+        for (int e = 0; e < WORDS; e += 4)
+            if (col + 4 * e < kp)
+                *reinterpret_cast<uint4 *>(dst + 4 * e) =
+                    make_uint4(w[e], w[e + 1], w[e + 2], w[e + 3]);
+    } else {
+        const int count = int(kp - col < CONV_CHUNK / 4 ? kp - col : CONV_CHUNK / 4);
+        for (int t = 0; t < count; ++t) dst[t] = u8(w[t >> 2] >> (8 * (t & 3)));
+    }
 }
 
-// Group maxima |x| of the patch matrix for groups of gr rows and gc columns:
-// work [rows/gr, ncg] (cleared), as float bits.
+// Group maxima |x| of the patch matrix for groups of gr rows and gc columns into
+// work [ceil(rows/gr), ncg] (cleared; float bits).  A wave owns 64 rows and walks all
+// K columns, flushing each lane's running maximum at column-group boundaries.
 __global__ __launch_bounds__(256) void k_conv_group_max(const float *x, const mf_conv_geometry g,
                                                         i64 K, i64 gr, i64 gc, i64 ncg, u32 *work,
                                                         u32 *status, u32 flag) {
@@ -551,37 +610,25 @@ __global__ __launch_bounds__(256) void k_conv_group_max(const float *x, const mf
     const i64 rows = g.n * g.out_height * g.out_width;
     const i64 r0 = (i64(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64;
     if (r0 >= rows) return;
-    const int count = int((rows - r0) < 64 ? (rows - r0) : 64);
-    const ConvRows mine = conv_row(g, r0 + (lane < count ? lane : 0));
+    const bool live = r0 + lane < rows;
+    const ConvLane me = conv_lane(g, u32(live ? r0 + lane : r0));
+    u32 *target = work + ((live ? r0 + lane : r0) / gr) * ncg;
+    ConvTap tap;
+    tap.start(g, 0);
     bool finite = true;
-    for (i64 kc = 0; kc < K; kc += 64) {
-        const i64 k = kc + lane;
-        const bool live = k < K;
-        const ConvCol col = conv_col(g, live ? k : 0);
-        const i64 last = (kc + 63) < (K - 1) ? (kc + 63) : (K - 1);
-        const bool one_group = kc / gc == last / gc;
-        for (int t = 0; t < count; ++t) {
-            const i64 base = (i64(__builtin_amdgcn_readlane(int(mine.base >> 32), t)) << 32) |
-                             u32(__builtin_amdgcn_readlane(int(mine.base), t));
-            const int ih0 = __builtin_amdgcn_readlane(mine.ih0, t);
-            const int iw0 = __builtin_amdgcn_readlane(mine.iw0, t);
-            const i64 row = r0 + t;
-            float v = 0.0f;
-            if (live) {
-                v = fabsf(conv_value(x, g, base, ih0, iw0, col));
-                finite = finite && v <= FLT_MAX;
-            }
-            u32 bits = __float_as_uint(v);
-            if (one_group) {
-#pragma unroll
-                for (int d = 32; d >= 1; d >>= 1) {
-                    const u32 other = u32(__shfl_xor(int(bits), d, 64));
-                    bits = other > bits ? other : bits;
-                }
-                if (lane == 0 && bits) atomicMax(&work[(row / gr) * ncg + kc / gc], bits);
-            } else if (live && bits) {
-                atomicMax(&work[(row / gr) * ncg + k / gc], bits);
-            }
+    float peak = 0.0f;
+    i64 cr = 0;
+#pragma unroll 1
+    for (i64 k = 0; k < K; ++k) {
+        const float v = fabsf(conv_load(x, g, me, live, tap));
+        finite = finite && v <= FLT_MAX;
+        peak = v > peak || v != v ? v : peak;
+        tap.next(g);
+        if (++cr == gc || k + 1 == K) {
+            if (live && __float_as_uint(peak)) atomicMax(target, __float_as_uint(peak));
+            ++target;
+            cr = 0;
+            peak = 0.0f;
         }
     }
     if (!finite && status) atomicOr(status, flag);
