@@ -279,6 +279,8 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
     for (int a = 0; a < cfg->n_in; ++a) fa_sum += std::fabs(double(cfg->in_factor[a]));
     for (int w = 0; w < cfg->n_w; ++w) fw_sum += std::fabs(double(cfg->w_factor[w])) * cfg->adc_max[w];
     if (fa_sum * fw_sum >= 16777216.0) { *why = "slice totals exceed FP32 integers"; return false; }
+    for (int w = 0; w < cfg->n_w; ++w)
+        if (cfg->w_mask[w] > 255) { *why = "weight slice above 8 bits"; return false; }
     memset(plan, 0, sizeof(*plan));
     plan->n_in = cfg->n_in;
     plan->n_w = cfg->n_w;
@@ -296,12 +298,20 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
         for (int w = 0; w < cfg->n_w; ++w) factor_sum += cfg->in_factor[a] * cfg->w_factor[w];
     }
     plan->bias = u32(0) - u32(u64(factor_sum) * 0x400000u);
+    for (int a = 0; a < cfg->n_in; ++a)
+        for (int w = 0; w < cfg->n_w; ++w)
+            if (std::abs(double(cfg->in_factor[a]) * double(cfg->w_factor[w])) >= 8388608.0) {
+                *why = "slice factor product beyond 24 bits";
+                return false;
+            }
     *ks = cfg->read_rows / 16;
     return true;
 }
 
-// Bytes of conductance terms per 32-column block: 3 bf16 terms per cell and slice.
-i64 noisy_block_bytes(const mf_config *cfg, i64 m) { return i64(cfg->n_w) * 32 * m * cfg->rows * 3 * 2; }
+// Bytes of conductance terms per 32-column block: NOISY_TERMS fp16 terms per cell and slice.
+i64 noisy_block_bytes(const mf_config *cfg, i64 m) {
+    return i64(cfg->n_w) * 32 * m * cfg->rows * NOISY_TERMS * 2;
+}
 
 bool noisy_extent_ok(i64 n, i64 m, const mf_config *cfg) {
     const i64 kp = m * cfg->rows;
@@ -404,16 +414,17 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         }
         const dim3 grid{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
         const bool nl = cfg->has_nonlinear != 0;
-        if (ks == 4) {
-            if (nl) hipLaunchKernelGGL((k_noisy<4, 5, true>), grid, dim3(256), 0, s, plan, args);
-            else hipLaunchKernelGGL((k_noisy<4, 5, false>), grid, dim3(256), 0, s, plan, args);
-        } else if (cfg->n_in <= 5) {
-            if (nl) hipLaunchKernelGGL((k_noisy<2, 5, true>), grid, dim3(256), 0, s, plan, args);
-            else hipLaunchKernelGGL((k_noisy<2, 5, false>), grid, dim3(256), 0, s, plan, args);
-        } else {
-            if (nl) hipLaunchKernelGGL((k_noisy<2, 8, true>), grid, dim3(256), 0, s, plan, args);
-            else hipLaunchKernelGGL((k_noisy<2, 8, false>), grid, dim3(256), 0, s, plan, args);
-        }
+#define MF_NOISY_LAUNCH(KS, NA)                                                                \
+    {                                                                                          \
+        if (nl)                                                                                \
+            hipLaunchKernelGGL((k_noisy<KS, NA, true>), grid, dim3(256), 0, s, plan, args);    \
+        else                                                                                   \
+            hipLaunchKernelGGL((k_noisy<KS, NA, false>), grid, dim3(256), 0, s, plan, args);   \
+    }
+        if (ks == 4) MF_NOISY_LAUNCH(4, 5)
+        else if (cfg->n_in <= 5) MF_NOISY_LAUNCH(2, 5)
+        else MF_NOISY_LAUNCH(2, 8)
+#undef MF_NOISY_LAUNCH
     }
     if (use_split)
         hipLaunchKernelGGL(k_restore_sum_f32, dim3(grid_for(n * ocols)), dim3(256), 0, s, partial, n,

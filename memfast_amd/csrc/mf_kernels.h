@@ -99,6 +99,8 @@ __global__ void k_restore(const mf_config cfg, const Code *packed, i64 m, i64 p,
                           i64 width, u32 seed, u64 event, int planes, Phys *g);
 
 // ---- noisy-device MFMA read (noisy_mfma.hip) -------------------------------
+constexpr int NOISY_TERMS = 2;   // fp16 terms per conductance (hi, lo)
+
 // Per-slice constants of the fused ADC: z = k1[w] * sum_r da * (g - L),
 // S-curve z / (1 + |alpha[w] * z|), code = round(clamp(z, 0, top[w])),
 // T += fa[a] * fw[w] * code.

@@ -1,4 +1,4 @@
-// Noisy-device sliced array read on gfx950 bf16 MFMA, fused with the ADC, the
+// Noisy-device sliced array read on gfx950 fp16 MFMA, fused with the ADC, the
 // signed shift-add, the scale restore and torch's read-order summation.
 //
 // Model (memfast/reference.py:63-117): per read group, input slice a and
@@ -7,10 +7,13 @@
 //   z = z / (1 + |alpha/max_w * z|) (S-curve),  code = round(clamp(z, 0, max_w)),
 //   T = sum_a sum_w fa*fw*code.
 // Here z = sum_r da * k1 * (g - L) with k1 = V*Mw/unit: the input digits da are
-// small integers (exact in bf16) and k1 * (g - L) (FP32) is split into three
-// bf16 terms hi + mid + lo that sum to it exactly, so three bf16 MFMAs with
-// FP32 accumulation give z to FP32 accuracy.  Results agree with the CPU
-// reference to its own FP32 rounding (codes may flip at rounding boundaries).
+// small integers (exact in fp16) and k1 * (g - L) (FP32, at most Mw <= 255 times
+// the conductance noise) is held as two fp16 terms hi + lo, hi = fp16(x) and
+// lo = fp16(x - hi): 22 significant bits, within 2^-23 of x relative to its
+// magnitude (the FP32 value itself carries 24).  Two fp16 MFMAs with FP32
+// accumulation give z to about FP32 accuracy; codes may flip where z lies within
+// that error of a rounding boundary (a few in 10^7 codes on the bench shapes),
+// the same order as FP32 summation-order differences from the CPU reference.
 // ADC: y = z + 1.5*2^23 (fma with the S-curve factor) rounds half-even, med3
 // clamps, and v_mad_i32_i24 accumulates fa*fw*(0x400000 + code) modulo 2^32;
 // plan.bias removes the offset (|T| < 2^24, so float(T) is exact).
@@ -21,25 +24,16 @@
 // 32-column x 32-row operand with one contiguous 1 KiB access per term.
 // k_noisy: block = 4 waves (2 column x 2 vector), wave tile 32 columns x 32
 // vectors, A operand = conductance terms, B operand = input digits built in
-// registers from the codes q.  Per read and pair: 3*KS MFMAs and the ADC
-// (about 7 VALU ops per output); bound: VALU (the ADC), MFMA as co-bound.
+// registers from the codes q.  Per read and pair: 2*KS MFMAs and the ADC.
 #include <cfloat>
 
 #include "mf_kernels.h"
 
 namespace mf {
 
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4fn __attribute__((ext_vector_type(4)));
-
-// FP32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ u32 bf16_bits(float x) {
-    const u32 b = __float_as_uint(x);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-}
-
-__device__ __forceinline__ float bf16_value(u32 bits) { return __uint_as_float(bits << 16); }
 
 template <int KS>
 __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg, const u8 *packed_t,
@@ -63,7 +57,7 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
         const int lr = lane & 31, h = lane >> 5;
         const i64 c = c_begin + cb * 32 + lr;
         const i64 k0 = g * P + ks * 16 + h * 8;
-        u32 terms[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        u32 terms[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
         if (c < ncols) {
             const uint2 bytes = *reinterpret_cast<const uint2 *>(packed_t + c * kp + k0);
             const i64 i = k0 / R, r0 = k0 - i * R;
@@ -75,19 +69,16 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
                 const float level = g_in ? g_in[cell]
                                          : cell_conductance<float>(cfg, code, w, cell, seed, read_seed);
                 const float delta = (level - cfg.f_low) * plan.k1[w];   // ADC counts per digit
-                const u32 hi = bf16_bits(delta);
-                const float r1 = delta - bf16_value(hi);
-                const u32 mid = bf16_bits(r1);
-                const u32 lo = bf16_bits(r1 - bf16_value(mid));
+                const _Float16 hi = static_cast<_Float16>(delta);        // round to nearest even
+                const _Float16 lo = static_cast<_Float16>(delta - static_cast<float>(hi));
                 const int shift = 16 * (j & 1);
-                terms[0][j >> 1] |= hi << shift;
-                terms[1][j >> 1] |= mid << shift;
-                terms[2][j >> 1] |= lo << shift;
+                terms[0][j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << shift;
+                terms[1][j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << shift;
             }
         }
-        uint4 *dst = gs + (((w * CB + cb) * G + g) * 3 * KS + ks) * 64 + lane;
+        uint4 *dst = gs + (((w * CB + cb) * G + g) * NOISY_TERMS * KS + ks) * 64 + lane;
 #pragma unroll
-        for (int term = 0; term < 3; ++term)
+        for (int term = 0; term < NOISY_TERMS; ++term)
             dst[term * KS * 64] = make_uint4(terms[term][0], terms[term][1], terms[term][2],
                                              terms[term][3]);
     }
@@ -107,20 +98,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t noisy_buffer(const void *base,
                                              0x00020000);
 }
 
-// Eight input digits (bytes of `word`, slice (shift, mask)) as eight bf16.
-__device__ __forceinline__ v8bf digits_bf16(uint2 word, int shift, u32 mask4) {
+// Eight input digits (bytes of `word`, slice (shift, mask)) as eight fp16.
+__device__ __forceinline__ v8h digits_f16(uint2 word, int shift, u32 mask4) {
     const u32 lo = (word.x >> shift) & mask4, hi = (word.y >> shift) & mask4;
-    // (byte of a u32) -> float compiles to v_cvt_f32_ubyte{0..3}.
+    // (byte of a u32) -> float compiles to v_cvt_f32_ubyte{0..3}; small integers
+    // pack into fp16 exactly (round toward zero is exact here).
     const float f[8] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
                         float(lo >> 24), float(hi & 0xFFu), float((hi >> 8) & 0xFFu),
                         float((hi >> 16) & 0xFFu), float(hi >> 24)};
-    // Small integers are exact in bf16: keep the upper half of each FP32.
-    uint4 packed;
-    packed.x = __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
-    packed.y = __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u);
-    packed.z = __builtin_amdgcn_perm(__float_as_uint(f[5]), __float_as_uint(f[4]), 0x07060302u);
-    packed.w = __builtin_amdgcn_perm(__float_as_uint(f[7]), __float_as_uint(f[6]), 0x07060302u);
-    return __builtin_bit_cast(v8bf, packed);
+    typedef __fp16 v2h __attribute__((ext_vector_type(2)));
+    const v2h a = __builtin_amdgcn_cvt_pkrtz(f[0], f[1]), b = __builtin_amdgcn_cvt_pkrtz(f[2], f[3]);
+    const v2h c = __builtin_amdgcn_cvt_pkrtz(f[4], f[5]), d = __builtin_amdgcn_cvt_pkrtz(f[6], f[7]);
+    uint4 packed = make_uint4(__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b),
+                              __builtin_bit_cast(u32, c), __builtin_bit_cast(u32, d));
+    return __builtin_bit_cast(v8h, packed);
 }
 
 template <int KS, int NA, bool NONLINEAR>
@@ -144,8 +135,8 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     const i64 vrows = (args.n - v0) < BV ? (args.n - v0) : BV;
     const __amdgpu_buffer_rsrc_t qbuf = noisy_buffer(args.q + v0 * kp, vrows * kp);
     const int q_off = (wv * 32 + lrow) * int(kp) + lhalf * 8;
-    const uint4 *frag_base = args.gs + cbw * i64(G) * 3 * KS * 64 + lane;
-    const i64 w_stride = args.CB * i64(G) * 3 * KS * 64;
+    const uint4 *frag_base = args.gs + cbw * i64(G) * NOISY_TERMS * KS * 64 + lane;
+    const i64 w_stride = args.CB * i64(G) * NOISY_TERMS * KS * 64;
 
     // This lane's output coordinates (MFMA 32x32 layout: reg r -> column
     // 8*(r/4) + 4*lhalf + r%4 of the wave tile, vector lrow).
@@ -169,13 +160,13 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
 
     for (int g = g0; g < g1; ++g) {
         // Input digits of this read for every slice (B operands).
-        v8bf B[NA][KS];
+        v8h B[NA][KS];
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
             if (a >= A) break;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                B[a][ks] = digits_bf16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
+                B[a][ks] = digits_f16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
         }
         if (g + 1 < g1) {
             const int next = (g + 1) * P;
@@ -191,20 +182,20 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
         u32 Ti[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) Ti[r] = 0u;
-        const uint4 *frag_g = frag_base + i64(g) * 3 * KS * 64;
-        auto load_terms = [&](v8bf (&F)[3][KS], int w) {
+        const uint4 *frag_g = frag_base + i64(g) * NOISY_TERMS * KS * 64;
+        auto load_terms = [&](v8h (&F)[NOISY_TERMS][KS], int w) {
             const uint4 *frag = frag_g + w * w_stride;
 #pragma unroll
-            for (int term = 0; term < 3; ++term)
+            for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
-                    F[term][ks] = __builtin_bit_cast(v8bf, frag[(term * KS + ks) * 64]);
+                    F[term][ks] = __builtin_bit_cast(v8h, frag[(term * KS + ks) * 64]);
         };
-        auto slice_reads = [&](const v8bf (&F)[3][KS], int w) {
+        auto slice_reads = [&](const v8h (&F)[NOISY_TERMS][KS], int w) {
             const float top = MAGIC + plan.top[w], alpha = plan.alpha[w];
             const float fw = plan.fw[w];
             auto convert = [&](const v16f &I, int a) {
-                const int f = int(plan.fa[a] * fw);   // |fa*fw| <= 2^14
+                const int f = int(plan.fa[a] * fw);   // |fa*fw| < 2^23 (plan)
                 const u32 f24 = u32(int(u32(f) << 8) >> 8);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -226,15 +217,15 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
                 if (a >= A) break;
                 v16f I = {};
 #pragma unroll
-                for (int term = 0; term < 3; ++term)
+                for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks)
-                        I = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B[a][ks], I, 0, 0, 0);
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], B[a][ks], I, 0, 0, 0);
                 convert(I, a);
             }
         };
         for (int w = 0; w < W; ++w) {
-            v8bf F[3][KS];
+            v8h F[NOISY_TERMS][KS];
             load_terms(F, w);
             slice_reads(F, w);
         }
@@ -341,11 +332,12 @@ __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, 
     if (!finite && status) atomicOr(status, u32(MF_STATUS_OUTPUT));
 }
 
-template __global__ void k_noisy<2, 5, false>(const NoisyPlan, const NoisyArgs);
-template __global__ void k_noisy<2, 5, true>(const NoisyPlan, const NoisyArgs);
-template __global__ void k_noisy<2, 8, false>(const NoisyPlan, const NoisyArgs);
-template __global__ void k_noisy<2, 8, true>(const NoisyPlan, const NoisyArgs);
-template __global__ void k_noisy<4, 5, false>(const NoisyPlan, const NoisyArgs);
-template __global__ void k_noisy<4, 5, true>(const NoisyPlan, const NoisyArgs);
+#define MF_NOISY_INST(KS, NA)                                                               \
+    template __global__ void k_noisy<KS, NA, true>(const NoisyPlan, const NoisyArgs);       \
+    template __global__ void k_noisy<KS, NA, false>(const NoisyPlan, const NoisyArgs);
+MF_NOISY_INST(2, 5)
+MF_NOISY_INST(2, 8)
+MF_NOISY_INST(4, 5)
+#undef MF_NOISY_INST
 
 }  // namespace mf
