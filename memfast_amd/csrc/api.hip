@@ -458,8 +458,10 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
         return false;
     }
     if (cfg->activation_bits > 16) { *why = "input codes wider than 16 bits"; return false; }
+    for (int w = 0; w < cfg->n_w; ++w)
+        if (cfg->w_mask[w] > 255) { *why = "weight slice above 8 bits"; return false; }
     if (cfg->n_in > WIDE_MFMA_MAX_A || cfg->n_w > WIDE_MFMA_MAX_W ||
-        cfg->n_w * 3 * (cfg->read_rows / 16) > WIDE_FRAGS_LARGE) {
+        cfg->n_w * NOISY_TERMS * (cfg->read_rows / 16) > WIDE_FRAGS_LARGE) {
         *why = "too many slices";
         return false;
     }
@@ -504,9 +506,11 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
 }
 
 // Workspace of the wide MFMA read: 16-bit input codes, then the conductance
-// terms of up to every 32-column block (3 bf16 terms per cell and slice).
+// terms of up to every 32-column block (NOISY_TERMS fp16 terms per cell and slice).
 i64 wide_codes_bytes(i64 n, i64 m, const mf_config *cfg) { return align256(n * m * cfg->rows * 2); }
-i64 wide_block_bytes(const mf_config *cfg, i64 m) { return i64(cfg->n_w) * 32 * m * cfg->rows * 3 * 2; }
+i64 wide_block_bytes(const mf_config *cfg, i64 m) {
+    return i64(cfg->n_w) * 32 * m * cfg->rows * NOISY_TERMS * 2;
+}
 
 bool wide_extent_ok(i64 n, i64 m, const mf_config *cfg) {
     const i64 kp = m * cfg->rows;
@@ -525,7 +529,7 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
     const i64 per_block = wide_block_bytes(cfg, m);
     const i64 max_cb = (bytes - codes_bytes) / per_block;
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
-    const int frags = cfg->n_w * 3 * ks;
+    const int frags = cfg->n_w * NOISY_TERMS * ks;
     if (frags > WIDE_FRAGS_LARGE) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
     const bool large = frags > WIDE_FRAGS_SMALL;
     uint16_t *q16 = static_cast<uint16_t *>(workspace);
@@ -537,10 +541,10 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
         const i64 threads = CB * G * cfg->n_w * ks * 64;
         if (ks == 2)
             hipLaunchKernelGGL(k_split_wide<2>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
-                               packed, g, m, p, ncols, seed, event, c_begin, CB, gs);
+                               packed, g, m, p, ncols, seed, event, c_begin, CB, plan, gs);
         else
             hipLaunchKernelGGL(k_split_wide<4>, dim3(grid_for(threads)), dim3(256), 0, s, *cfg,
-                               packed, g, m, p, ncols, seed, event, c_begin, CB, gs);
+                               packed, g, m, p, ncols, seed, event, c_begin, CB, plan, gs);
         NoisyWideArgs args{};
         args.q16 = q16;
         args.gs = gs;

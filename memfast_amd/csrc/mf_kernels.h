@@ -168,7 +168,7 @@ __global__ void k_codes16(const u32 *q, i64 count, uint16_t *q16);
 template <int KS>
 __global__ void k_split_wide(const mf_config cfg, const u32 *packed, const float *g_in, i64 m,
                              i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin, i64 CB,
-                             uint4 *gs);
+                             const NoisyWidePlan plan, uint4 *gs);
 // LDS capacity of the wide read: fragments (1 KiB) per read and buffer.  36:
 // two buffers in 72 KiB (two blocks per CU); 72: 144 KiB (one block per CU).
 constexpr int WIDE_FRAGS_SMALL = 36;

@@ -1,5 +1,5 @@
 // Noisy-device sliced array read for wide configurations (precision above 8
-// bits or BFP inputs, memfast/config.py `wide`) on gfx950 bf16 MFMA, fused with
+// bits or BFP inputs, memfast/config.py `wide`) on gfx950 fp16 MFMA, fused with
 // the ADC, the signed shift-add, the FP64 scale restore and torch's FP64
 // read-order summation.  Only `out` (FP64) is written.
 //
@@ -9,12 +9,14 @@
 //   z = z / (1 + |alpha/max_w * z|) (S-curve),  code = round(clamp(z, 0, max_w)),
 //   T = sum_a sum_w fa*fw*code                 (exact integer)
 //   out[n,c] = sum_g restore_scales(T, xs[n,g], ws[g,c])   (FP64, torch order)
-// As in the narrow kernel, z = (V*Mw/unit) * sum_r da * (g - L): input digits
-// are exact in bf16 and g - L is split into three bf16 terms that sum to it
-// exactly, so three bf16 MFMAs with FP32 accumulation give the FP32 current.
+// As in the narrow kernel, z = sum_r da * k1 * (g - L) with k1 = V*Mw/unit:
+// input digits are exact in fp16 and k1 * (g - L) (at most Mw <= 255 times the
+// conductance noise) is held as two fp16 terms hi = fp16(x), lo = fp16(x - hi),
+// within 2^-23 of x relative to its magnitude, so two fp16 MFMAs with FP32
+// accumulation give z to about FP32 accuracy.
 //
 // Integer totals: the rounded, clamped count is formed in the exponent-fixed
-// domain y = fma(I, k1, 1.5*2^23) (one rounding, half-even), med3-clamped to
+// domain y = z + 1.5*2^23 (one rounding, half-even), med3-clamped to
 // [1.5*2^23, 1.5*2^23 + max_w]; the low 24 bits of y are 0x400000 + code, and
 // v_mad_i32_i24 accumulates fa*fw*(0x400000 + code) modulo 2^32.  The constant
 // 0x400000 * sum(fa*fw) is removed at the end; the host checks that every true
@@ -25,28 +27,21 @@
 // order).  Block = 4 waves on the same 32 columns and 128 vectors (32 per
 // wave); per read the block copies the run into LDS with global_load_lds
 // (double-buffered in two LDS objects, one barrier per read) and every wave
-// reads it from there.  FRMAX bounds the fragments per read (W * 3 * KS).
+// reads it from there.  FRMAX bounds the fragments per read (W * 2 * KS).
 // Input codes are repacked to 16 bits (k_codes16) so a lane's 8 rows of a
 // 16-row step are one 16-byte load.  Bound: VALU (digit expansion + ADC per
-// slice pair) with bf16 MFMA as co-bound.
+// slice pair) with fp16 MFMA as co-bound.
 #include <cfloat>
 
 #include "mf_kernels.h"
 
 namespace mf {
 
-typedef __bf16 v8bf_w __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h_w __attribute__((ext_vector_type(8)));
 typedef float v16f_w __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 namespace {
-
-__device__ __forceinline__ u32 bf16_round_bits(float x) {
-    const u32 b = __float_as_uint(x);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-}
-
-__device__ __forceinline__ float bf16_bits_value(u32 bits) { return __uint_as_float(bits << 16); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_buffer(const void *base, i64 bytes) {
     const int records = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : int(bytes < 0 ? 0 : bytes);
@@ -63,31 +58,32 @@ __device__ __forceinline__ u32 mad_u24(u32 x, u32 mul, u32 bias) {
 }
 
 // Digits of slice (shift, mask <= 3) of eight 16-bit codes (rows 0..7, two per
-// word, low half first) as eight bf16.  x = d0 | d1 << 16 selects, per output
-// byte, the low or high byte of bf16(d) from two 4-entry byte tables with one
+// word, low half first) as eight fp16.  x = d0 | d1 << 16 selects, per output
+// byte, the low or high byte of fp16(d) from two 4-entry byte tables with one
 // v_perm: selector bytes (d0, 4 + d0, d1, 4 + d1) = x * 0x101 + 0x04000400.
-__device__ __forceinline__ v8bf_w digits_small(uint4 c, int shift, u32 mask2, u32 sel_bias) {
-    constexpr u32 LO = 0x40008000u;   // low bytes of bf16(0), bf16(1), bf16(2), bf16(3)
-    constexpr u32 HI = 0x40403F00u;   // high bytes
+__device__ __forceinline__ v8h_w digits_small(uint4 c, int shift, u32 mask2, u32 sel_bias) {
+    constexpr u32 LO = 0x00000000u;   // low bytes of fp16(0), fp16(1), fp16(2), fp16(3)
+    constexpr u32 HI = 0x42403C00u;   // high bytes
     uint4 r;
     r.x = __builtin_amdgcn_perm(HI, LO, mad_u24((c.x >> shift) & mask2, 0x101u, sel_bias));
     r.y = __builtin_amdgcn_perm(HI, LO, mad_u24((c.y >> shift) & mask2, 0x101u, sel_bias));
     r.z = __builtin_amdgcn_perm(HI, LO, mad_u24((c.z >> shift) & mask2, 0x101u, sel_bias));
     r.w = __builtin_amdgcn_perm(HI, LO, mad_u24((c.w >> shift) & mask2, 0x101u, sel_bias));
-    return __builtin_bit_cast(v8bf_w, r);
+    return __builtin_bit_cast(v8h_w, r);
 }
 
-// Same for digits up to 255 (exact in bf16): convert each half and keep the
-// upper 16 bits of the FP32 values.
-__device__ __forceinline__ v8bf_w digits_any(uint4 c, int shift, u32 mask2) {
+// Same for digits up to 255 (exact in fp16): convert each half to FP32 and pack
+// the pair (round toward zero, exact for these integers).
+__device__ __forceinline__ v8h_w digits_any(uint4 c, int shift, u32 mask2) {
+    typedef __fp16 v2h_w __attribute__((ext_vector_type(2)));
     const u32 w[4] = {(c.x >> shift) & mask2, (c.y >> shift) & mask2, (c.z >> shift) & mask2,
                       (c.w >> shift) & mask2};
     u32 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        o[i] = __builtin_amdgcn_perm(__float_as_uint(float(w[i] >> 16)),
-                                     __float_as_uint(float(w[i] & 0xFFFFu)), 0x07060302u);
-    return __builtin_bit_cast(v8bf_w, make_uint4(o[0], o[1], o[2], o[3]));
+        o[i] = __builtin_bit_cast(u32, __builtin_amdgcn_cvt_pkrtz(float(w[i] & 0xFFFFu),
+                                                                  float(w[i] >> 16)));
+    return __builtin_bit_cast(v8h_w, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
 // One 1 KiB LDS DMA: lane l's 16 bytes at src go to lds_base + 16 * l.  Issued
@@ -145,7 +141,7 @@ template <int KS>
 __global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u32 *packed,
                                                     const float *g_in, i64 m, i64 p, i64 ncols,
                                                     u32 seed, u64 event, i64 c_begin, i64 CB,
-                                                    uint4 *gs) {
+                                                    const NoisyWidePlan plan, uint4 *gs) {
     constexpr int P = 16 * KS;
     const int R = cfg.rows, C = cfg.cols, W = cfg.n_w;
     const i64 G = m * R / P;
@@ -162,7 +158,7 @@ __global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u
         const int lr = lane & 31, h = lane >> 5;
         const i64 c = c_begin + cb * 32 + lr;
         const i64 k0 = g * P + ks * 16 + h * 8;
-        u32 terms[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        u32 terms[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
         if (c < ncols) {
             const i64 i = k0 / R, r0 = k0 - i * R;
             const i64 tt = c / C, cc = c - tt * C;
@@ -177,29 +173,26 @@ __global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u
                     const u32 code = packed[((i * p + tt) * R + r) * C + cc];
                     level = cell_conductance<float>(cfg, code, w, cell, seed, read_seed);
                 }
-                const float delta = level - cfg.f_low;
-                const u32 hi = bf16_round_bits(delta);
-                const float r1 = delta - bf16_bits_value(hi);
-                const u32 mid = bf16_round_bits(r1);
-                const u32 lo = bf16_round_bits(r1 - bf16_bits_value(mid));
+                const float delta = (level - cfg.f_low) * plan.k1[w];   // ADC counts per digit
+                const _Float16 hi = static_cast<_Float16>(delta);        // round to nearest even
+                const _Float16 lo = static_cast<_Float16>(delta - static_cast<float>(hi));
                 const int shift = 16 * (j & 1);
-                terms[0][j >> 1] |= hi << shift;
-                terms[1][j >> 1] |= mid << shift;
-                terms[2][j >> 1] |= lo << shift;
+                terms[0][j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << shift;
+                terms[1][j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << shift;
             }
         }
-        uint4 *dst = gs + ((((cb * G + g) * W + w) * 3) * KS + ks) * 64 + lane;
+        uint4 *dst = gs + ((((cb * G + g) * W + w) * NOISY_TERMS) * KS + ks) * 64 + lane;
 #pragma unroll
-        for (int term = 0; term < 3; ++term)
+        for (int term = 0; term < NOISY_TERMS; ++term)
             dst[term * KS * 64] = make_uint4(terms[term][0], terms[term][1], terms[term][2],
                                              terms[term][3]);
     }
 }
 
 template __global__ void k_split_wide<2>(const mf_config, const u32 *, const float *, i64, i64,
-                                         i64, u32, u64, i64, i64, uint4 *);
+                                         i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 template __global__ void k_split_wide<4>(const mf_config, const u32 *, const float *, i64, i64,
-                                         i64, u32, u64, i64, i64, uint4 *);
+                                         i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 
 template <int KS, bool NONLINEAR, bool SMALL, int FRMAX>
 __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
@@ -215,7 +208,7 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
     const int lrow = lane & 31, lhalf = lane >> 5;
     const int A = plan.n_in, W = plan.n_w;
     const int G = int(args.G);
-    const int FR = W * 3 * KS;                    // fragments per read
+    const int FR = W * NOISY_TERMS * KS;          // fragments per read
     const i64 cb = blockIdx.x;                    // chunk-relative 32-column block
     const i64 v0 = i64(blockIdx.y) * 128 + wave * 32;
     const i64 kp = args.kp;
@@ -233,7 +226,6 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
     int slice_shift = lane < A ? plan.in_shift[lane] : 0;
     u32 slice_mask2 = lane < A ? plan.in_mask2[lane] : 0u;
     int slice_factor = lane < A ? plan.fa[lane] : 0;
-    float w_k1 = lane < W ? plan.k1[lane] : 0.0f;
     float w_top = lane < W ? plan.top[lane] : 0.0f;
     float w_alpha = lane < W ? plan.alpha[lane] : 0.0f;
     int w_factor = lane < W ? plan.fw[lane] : 0;
@@ -261,7 +253,6 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
     settle_one(slice_shift);
     settle_one(slice_mask2);
     settle_one(slice_factor);
-    settle_one(w_k1);
     settle_one(w_top);
     settle_one(w_alpha);
     settle_one(w_factor);
@@ -275,10 +266,10 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
 #pragma unroll
         for (int r = 0; r < 16; ++r) T[r] = 0u;
         const uint4 *fl = sCur + lane;
-        // ADC of one slice pair's current: per output fma into the exponent-fixed
-        // domain, med3 clamp, 24-bit multiply-accumulate of fa*fw*(0x400000 + code).
+        // ADC of one slice pair's count argument (the terms carry k1): per output
+        // add into the exponent-fixed domain, med3 clamp, 24-bit multiply-accumulate
+        // of fa*fw*(0x400000 + code).
         auto convert = [&](const v16f_w &I, int w, int a) {
-            const float k1 = lane_float(w_k1, w);
             const float top = MAGIC + lane_float(w_top, w);
             const int f = __builtin_amdgcn_readlane(slice_factor, a) *
                           __builtin_amdgcn_readlane(w_factor, w);   // |fa*fw| < 2^23
@@ -289,18 +280,17 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
             for (int r = 0; r < 16; ++r) {
                 float y;
                 if (NONLINEAR) {
-                    float z = I[r] * k1;
-                    z = z * __builtin_amdgcn_rcpf(fmaf(fabsf(z), alpha, 1.0f));
+                    const float z = I[r] * __builtin_amdgcn_rcpf(fmaf(fabsf(I[r]), alpha, 1.0f));
                     y = z + MAGIC;
                 } else {
-                    y = fmaf(I[r], k1, MAGIC);
+                    y = I[r] + MAGIC;
                 }
                 y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
                 const int low = int(__float_as_uint(y) << 8) >> 8;   // 0x400000 + code
                 T[r] += u32(low) * f24;
             }
         };
-        auto digits = [&](v8bf_w (&B)[KS], int a) {
+        auto digits = [&](v8h_w (&B)[KS], int a) {
             const int shift = __builtin_amdgcn_readlane(slice_shift, a);
             const u32 mask2 = u32(__builtin_amdgcn_readlane(int(slice_mask2), a));
 #pragma unroll
@@ -308,47 +298,48 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
                 B[ks] = SMALL ? digits_small(qc[ks], shift, mask2, sel_bias)
                               : digits_any(qc[ks], shift, mask2);
         };
-        auto terms = [&](v8bf_w (&F)[3][KS], int w) {
+        auto terms = [&](v8h_w (&F)[NOISY_TERMS][KS], int w) {
 #pragma unroll
-            for (int term = 0; term < 3; ++term)
+            for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
-                    F[term][ks] = __builtin_bit_cast(v8bf_w, fl[((w * 3 + term) * KS + ks) * 64]);
+                    F[term][ks] = __builtin_bit_cast(
+                        v8h_w, fl[((w * NOISY_TERMS + term) * KS + ks) * 64]);
         };
         // Input slices in pairs: the digits of a slice are built once per read;
         // per weight slice the two currents are two interleaved MFMA chains.
         int a = 0;
         for (; a + 1 < A; a += 2) {
-            v8bf_w B0[KS], B1[KS];
+            v8h_w B0[KS], B1[KS];
             digits(B0, a);
             digits(B1, a + 1);
             for (int w = 0; w < W; ++w) {
-                v8bf_w F[3][KS];
+                v8h_w F[NOISY_TERMS][KS];
                 terms(F, w);
                 v16f_w I0 = {}, I1 = {};
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                    for (int term = 0; term < 3; ++term) {
-                        I0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B0[ks], I0, 0, 0, 0);
-                        I1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B1[ks], I1, 0, 0, 0);
+                    for (int term = 0; term < NOISY_TERMS; ++term) {
+                        I0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], B0[ks], I0, 0, 0, 0);
+                        I1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], B1[ks], I1, 0, 0, 0);
                     }
                 convert(I0, w, a);
                 convert(I1, w, a + 1);
             }
         }
         if (a < A) {
-            v8bf_w B0[KS];
+            v8h_w B0[KS];
             digits(B0, a);
             for (int w = 0; w < W; ++w) {
-                v8bf_w F[3][KS];
+                v8h_w F[NOISY_TERMS][KS];
                 terms(F, w);
                 v16f_w I0 = {};
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                    for (int term = 0; term < 3; ++term)
-                        I0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F[term][ks], B0[ks], I0, 0, 0, 0);
+                    for (int term = 0; term < NOISY_TERMS; ++term)
+                        I0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], B0[ks], I0, 0, 0, 0);
                 convert(I0, w, a);
             }
         }
