@@ -6,14 +6,37 @@ nonlinearities stay digital.  Sequences support stacked layers, both
 directions, inter-layer dropout, explicit initial state and unbatched input;
 PackedSequence is not supported.  Every timestep reads both projections, so
 a T-step sequence issues 2*T analog products per layer and direction.
+
+When a read's result cannot depend on its read event (no read or voltage
+variation) and input quantization groups do not span rows, the T input
+projections of a sequence equal one product over all T*B rows: that product
+is issued once and the input matrix's event counter still advances by T.
 """
 
 import torch
 from torch import nn
 from torch.nn import functional as F
 
+from .. import hip
 from .linear import AnalogLinear
 from .training import TrainableAnalogLinear, _SurrogateGradient, _validate_gradient_mode
+
+
+def _batchable_inputs(projection, steps, batch):
+    """Whether the T per-step reads of ``projection`` (``batch`` rows each) equal one
+    read over all rows: same kernel, no event-dependent noise, per-row input scales."""
+    if type(projection) is not AnalogLinear or steps < 2:
+        return False
+    config = projection.config
+    effects = config.nonidealities
+    per_row = projection.input_scale is not None or config.input_quant_gran[0] == 1
+    if not (projection.simulator.mode == "default" and per_row
+            and not effects.read_variation and not effects.voltage_variation
+            and projection._event + steps < 2**63):
+        return False
+    m = -(-projection.in_features // config.array_size[0])
+    return (hip.mm_kernel(config, steps * batch, m, projection.p)
+            == hip.mm_kernel(config, batch, m, projection.p))
 
 
 def _projection(weight, bias, simulator, name, training, gradient_mode):
@@ -67,6 +90,11 @@ class AnalogRNNCell(nn.Module):
             return _SurrogateGradient.apply(analog, activation(value.float()))
         return analog
 
+    def _step(self, inputs, hx):
+        """One inference step given this step's input projection."""
+        activation = torch.tanh if self.nonlinearity == "tanh" else F.relu
+        return activation(inputs + self.hidden(hx))
+
 
 class AnalogGRUCell(nn.Module):
     """``nn.GRUCell`` gates (reset, update, new) over analog projections."""
@@ -103,6 +131,10 @@ class AnalogGRUCell(nn.Module):
             surrogate = self._gates(inputs.float(), hidden.float(), hx.float())
             return _SurrogateGradient.apply(analog, surrogate)
         return analog
+
+    def _step(self, inputs, hx):
+        """One inference step given this step's input projection."""
+        return self._gates(inputs, self.hidden(hx), hx)
 
 
 class _AnalogRecurrent(nn.Module):
@@ -173,9 +205,23 @@ class _AnalogRecurrent(nn.Module):
                 if direction:
                     steps = reversed(steps)
                 values = []
-                for step in steps:
-                    hidden = self.cells[index](sequence[step], hidden)
-                    values.append(hidden)
+                cell = self.cells[index]
+                projected = self._projected_inputs(cell, sequence)
+                if projected is None:
+                    for step in steps:
+                        hidden = cell(sequence[step], hidden)
+                        values.append(hidden)
+                else:
+                    matrix, start = cell.input, cell.input._event
+                    for count, step in enumerate(steps):
+                        try:
+                            hidden = cell._step(projected[step], hidden)
+                        except Exception:
+                            # The reference would have read the input projection
+                            # count + 1 times when this step's hidden read failed.
+                            matrix._event = start + count + 1
+                            raise
+                        values.append(hidden)
                 if direction:
                     values.reverse()
                 outputs.append(torch.stack(values))
@@ -193,6 +239,28 @@ class _AnalogRecurrent(nn.Module):
             return sequence.squeeze(1), hidden.squeeze(1)
         output = sequence.transpose(0, 1) if self.batch_first else sequence
         return output, hidden
+
+
+    def _projected_inputs(self, cell, sequence):
+        """All steps' input projections from one read, or None to read per step."""
+        steps = sequence.shape[0]
+        batch = sequence[0].numel() // sequence.shape[-1]
+        if ((self._hardware_aware_training and torch.is_grad_enabled()) or batch == 0
+                or not _batchable_inputs(cell.input, steps, batch)):
+            return None
+        matrix = cell.input
+        start = matrix._event
+        try:
+            with torch.no_grad():
+                projected = matrix._forward(sequence, retry=False)
+        except (ValueError, FloatingPointError):
+            projected = None
+        if projected is None:
+            # Per-step reads then raise (or retry in FP64) where the reference does.
+            matrix._event = start
+            return None
+        matrix._event = start + steps
+        return projected
 
 
 class AnalogRNN(_AnalogRecurrent):

@@ -616,11 +616,13 @@ class AnalogMatrix(nn.Module):
         return self._execute_checked(q, xscale, schedule, event, stable)[0]
 
     def _execute_checked(self, q, xscale, schedule, event, stable=False, status=None,
-                         input_error=None):
+                         input_error=None, retry=True):
         """(output, finite) where ``finite`` is True when the output is known finite.
 
         ``status`` may carry STATUS_INPUT from a deferred input quantization; the
-        one status read raises ``input_error`` for it before anything else."""
+        one status read raises ``input_error`` for it before anything else.  With
+        ``retry`` False, a non-finite FP32 result returns (None, False) instead of
+        the FP64 retry (which changes every row's rounding)."""
         config = self.config
         c = config.array_size[1]
         if config.wide:
@@ -687,6 +689,8 @@ class AnalogMatrix(nn.Module):
         else:
             finite = bool(torch.isfinite(output).all())
         if not finite:
+            if not retry:
+                return None, False
             return self._execute_checked(q, xscale, schedule, event, stable=True)
         return output, True
 
@@ -726,6 +730,12 @@ class AnalogMatrix(nn.Module):
 
     @torch.no_grad()
     def forward(self, x):
+        return self._forward(x)
+
+    def _forward(self, x, retry=True):
+        """forward(); with ``retry`` False it returns None (event unchanged) where the
+        FP32 read is not finite, so that a caller batching independent rows can fall
+        back to separate calls."""
         if x.ndim < 1 or x.shape[-1] != self.in_features or not x.is_floating_point():
             raise ValueError("input must be floating with matching in_features")
         if x.device != self.packed.device or x.device != self.simulator.device:
@@ -744,9 +754,9 @@ class AnalogMatrix(nn.Module):
         status = hip.status_word(x.device) if self.simulator.mode == "default" else None
         q, xscale = hip.input_tiles(x.reshape(-1, self.in_features), self.config, self.input_scale,
                                     status=status)
-        return self._run(x, q, xscale, status=status)
+        return self._run(x, q, xscale, status=status, retry=retry)
 
-    def _run(self, x, q, xscale, status=None):
+    def _run(self, x, q, xscale, status=None, retry=True):
         """Read quantized inputs, cast, check and advance the event (simulator.py:632-646)."""
         if self._event >= 2**63:
             raise OverflowError("read-event counter exhausted")
@@ -761,7 +771,9 @@ class AnalogMatrix(nn.Module):
             schedule = self._prepared[key]
         output, finite = self._execute_checked(
             q, xscale, schedule, event, status=status,
-            input_error=hip.input_error(self.config, self.input_scale))
+            input_error=hip.input_error(self.config, self.input_scale), retry=retry)
+        if output is None:
+            return None
         return self._finish(x, output, finite)
 
     def _finish(self, x, output, finite):

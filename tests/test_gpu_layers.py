@@ -261,3 +261,55 @@ def test_conv_implicit_path_matches_unfold_path(hip_device, kind, geometry):
         expected = torch.cat(parts, dim=-1).transpose(1, 2).reshape(n, 2 * groups, *out)
         assert torch.equal(got.view(torch.int32), expected.view(torch.int32)), (geometry, fixed)
         assert all(matrix._event == 1 for matrix in layer.matrices)
+
+
+@pytest.mark.parametrize("effects", [dict(write_variation=0.02),
+                                     dict(write_variation=0.02, read_variation=0.01)])
+@pytest.mark.parametrize("bidirectional", [False, True])
+def test_gru_sequence_matches_per_step_cells(hip_device, effects, bidirectional):
+    """AnalogGRU over a sequence (input projections read in one product when the read
+    cannot depend on its event) equals stepping each cell, bit for bit, with the same
+    read-event counts."""
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))), nonidealities=Nonidealities(**effects))
+    torch.manual_seed(7)
+    source = nn.GRU(40, 64, num_layers=2, bidirectional=bidirectional).to(hip_device)
+    x = torch.randn(9, 3, 40, device=hip_device)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    stepped = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    output, hidden = layer(x)
+    directions = 2 if bidirectional else 1
+    sequence, finals = x, []
+    for lay in range(2):
+        outs = []
+        for d in range(directions):
+            cell = stepped.cells[lay * directions + d]
+            h = torch.zeros(3, 64, device=hip_device)
+            values = []
+            for t in (reversed(range(9)) if d else range(9)):
+                h = cell(sequence[t], h)
+                values.append(h)
+            if d:
+                values.reverse()
+            outs.append(torch.stack(values))
+            finals.append(h)
+        sequence = torch.cat(outs, dim=-1) if directions == 2 else outs[0]
+    assert torch.equal(output.view(torch.int32), sequence.view(torch.int32))
+    assert torch.equal(hidden.view(torch.int32), torch.stack(finals).view(torch.int32))
+    for a, b in zip(layer.cells, stepped.cells):
+        assert a.input._event == b.input._event == 9
+        assert a.hidden._event == b.hidden._event == 9
+
+
+def test_gru_nonfinite_input_raises_at_its_step(hip_device):
+    """A non-finite input at step t raises as in per-step reading: both projections have
+    then completed t reads."""
+    cfg = config("write", input_quant_gran=(1, None))
+    torch.manual_seed(8)
+    source = nn.GRU(40, 64).to(hip_device)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    x = torch.randn(6, 2, 40, device=hip_device)
+    x[4, 1, 3] = float("nan")
+    with pytest.raises(ValueError, match="finite"):
+        layer(x)
+    cell = layer.cells[0]
+    assert cell.input._event == 4 and cell.hidden._event == 4
