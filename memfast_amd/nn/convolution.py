@@ -64,7 +64,7 @@ class AnalogConv2d(nn.Module):
                 matrix(patches[:, g * size:(g + 1) * size].transpose(1, 2))
                 for g, matrix in enumerate(self.matrices)
             ]
-        merged = torch.cat(outputs, dim=-1).transpose(1, 2)
+        merged = (outputs[0] if len(outputs) == 1 else torch.cat(outputs, dim=-1)).transpose(1, 2)
         return merged.reshape(x.shape[0], self.out_channels, *spatial)
 
     def _implicit(self, x, padding, spatial):

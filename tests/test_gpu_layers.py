@@ -236,14 +236,18 @@ def test_conv_input_tiles_flag_only_gathered_nonfinite(hip_device, gran):
 
 @pytest.mark.parametrize("kind", list(EFFECTS))
 @pytest.mark.parametrize("geometry", CONV_GEOMETRIES[:5])
-def test_conv_implicit_path_matches_unfold_path(hip_device, kind, geometry):
+@pytest.mark.parametrize("mode", ["zeros", "reflect", "circular"])
+def test_conv_implicit_path_matches_unfold_path(hip_device, kind, geometry, mode):
     """AnalogConv2d's implicit-im2col forward equals reading F.unfold's patches through the
-    same programmed matrices (same read events), bit for bit; fixed scales too."""
+    same programmed matrices (same read events), bit for bit; fixed scales and padding
+    modes too."""
     n, c, groups, kernel, stride, padding, dilation, out = _conv_case(geometry)
+    if mode != "zeros" and max(padding) == 0:
+        pytest.skip("padding modes only differ with padding")
     cfg = config(kind)
     torch.manual_seed(32)
     source = nn.Conv2d(c, 2 * groups, kernel, stride=stride, padding=padding, dilation=dilation,
-                       groups=groups).to(hip_device)
+                       groups=groups, padding_mode=mode).to(hip_device)
     sim = Simulator(cfg, device=hip_device)
     layer = AnalogConv2d(source, sim, name="conv")
     x = torch.randn(n, c, *geometry[2:4], device=hip_device)
@@ -254,7 +258,11 @@ def test_conv_implicit_path_matches_unfold_path(hip_device, kind, geometry):
         got = layer(x)
         for matrix in layer.matrices:
             matrix.reset_read()
-        patches = F.unfold(x, kernel, dilation, padding, stride)
+        source_x, unfold_padding = x, padding
+        if mode != "zeros":
+            ph, pw = padding
+            source_x, unfold_padding = F.pad(x, (pw, pw, ph, ph), mode=mode), (0, 0)
+        patches = F.unfold(source_x, kernel, dilation, unfold_padding, stride)
         size = c // groups * kernel[0] * kernel[1]
         parts = [matrix(patches[:, g * size:(g + 1) * size].transpose(1, 2))
                  for g, matrix in enumerate(layer.matrices)]
