@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 5
+#define MF_ABI_VERSION 6
 #define MF_MAX_SLICES 32
 
 enum {
@@ -222,6 +222,16 @@ typedef struct mf_conv_geometry {
 int mf_conv_input_tiles(const mf_config *cfg, const float *x, const mf_conv_geometry *geom,
                         const float *fixed_scale, int64_t gr, int64_t gc, uint32_t *work,
                         float *scale, uint8_t *q, float *xscale, uint32_t *status, void *stream);
+
+/* GRU gates over the two projections of one step (memfast/nn/recurrent.py
+ * `AnalogGRUCell`, PyTorch's gate equations): with inputs and hidden [n, 3H]
+ * (chunks r, z, n) and hx [n, H],
+ *   out = (1 - z) * tanh(in + r * hn) + z * hx,  r|z = sigmoid(i + h),
+ * every operation rounded to FP32 as PyTorch's separate elementwise ops are.
+ * Leading dimensions in elements. */
+int mf_gru_gates(const float *inputs, int64_t ldi, const float *hidden, int64_t ldh,
+                 const float *hx, int64_t ldx, float *out, int64_t ldo, int64_t n, int64_t width,
+                 void *stream);
 
 /* Overflow-safe FP64 restore and read sum of one chunk of `width` tiles
  * (memfast/simulator.py:57-66 restore_scales and :578-585, the wide/retry path

@@ -1164,6 +1164,18 @@ int mf_bias_add(float *out, int64_t n, int64_t o, int64_t ldo, const float *bias
     return check_launch("bias add");
 }
 
+int mf_gru_gates(const float *inputs, int64_t ldi, const float *hidden, int64_t ldh,
+                 const float *hx, int64_t ldx, float *out, int64_t ldo, int64_t n, int64_t width,
+                 void *stream) {
+    if (!inputs || !hidden || !hx || !out || n < 1 || width < 1 || ldi < 3 * width ||
+        ldh < 3 * width || ldx < width || ldo < width)
+        return fail(MF_E_INVALID, "invalid GRU gate arguments");
+    hipLaunchKernelGGL(k_gru_gates, dim3(grid_for(n * width)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), inputs, ldi, hidden, ldh, hx, ldx, out, ldo,
+                       n, width);
+    return check_launch("GRU gates");
+}
+
 int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,
                   const float *xscale, const float *wscale, int64_t ldws, int64_t col0, double *out,
                   int64_t ldo, void *stream) {

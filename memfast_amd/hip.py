@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -150,6 +150,7 @@ SIGNATURES = {
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
                       _P], ct.c_int),
     "mf_bias_add": ([_P, _I64, _I64, _I64, _P, _P, _P], ct.c_int),
+    "mf_gru_gates": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P], ct.c_int),
     "mf_stable_sum": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P], ct.c_int),
     "mf_quantize_inputs_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                  _P], ct.c_int),
@@ -780,6 +781,23 @@ def bias_add(out, bias, status=None):
     with torch.cuda.device(out.device):
         check(library().mf_bias_add(_ptr(out), out.shape[0], out.shape[1], out.stride(0),
                                     _ptr(bias), _ptr(status), _stream(out.device)), "bias add")
+    return out
+
+
+def gru_gates(inputs, hidden, hx):
+    """PyTorch's GRU gate equations over one step's projections (FP32 [N, 3H] each,
+    hx [N, H]) in one kernel; the same FP32 roundings as the separate elementwise ops."""
+    require_device(inputs)
+    n, width = hx.shape
+    for t, cols in ((inputs, 3 * width), (hidden, 3 * width), (hx, width)):
+        if (t.dtype != torch.float32 or t.ndim != 2 or t.shape != (n, cols) or t.stride(1) != 1
+                or t.device != inputs.device):
+            raise ValueError("gru_gates takes FP32 row-major [N, 3H], [N, 3H] and [N, H]")
+    out = torch.empty((n, width), dtype=torch.float32, device=inputs.device)
+    with torch.cuda.device(inputs.device):
+        check(library().mf_gru_gates(_ptr(inputs), inputs.stride(0), _ptr(hidden), hidden.stride(0),
+                                     _ptr(hx), hx.stride(0), _ptr(out), width, n, width,
+                                     _stream(inputs.device)), "GRU gates")
     return out
 
 

@@ -116,11 +116,12 @@ class AnalogGRUCell(nn.Module):
 
     @staticmethod
     def _gates(inputs, hidden, hx):
-        ir, iz, inn = inputs.chunk(3, dim=-1)
-        hr, hz, hn = hidden.chunk(3, dim=-1)
-        reset = torch.sigmoid(ir + hr)
-        update = torch.sigmoid(iz + hz)
-        candidate = torch.tanh(inn + reset * hn)
+        # reset and update gates in one elementwise pass over both chunks (the same
+        # per-element operations as sigmoid(ir + hr) and sigmoid(iz + hz)).
+        width = inputs.shape[-1] // 3
+        gates = torch.sigmoid(inputs[..., :2 * width] + hidden[..., :2 * width])
+        reset, update = gates[..., :width], gates[..., width:]
+        candidate = torch.tanh(inputs[..., 2 * width:] + reset * hidden[..., 2 * width:])
         return (1 - update) * candidate + update * hx
 
     def forward(self, x, hx=None):
@@ -133,8 +134,13 @@ class AnalogGRUCell(nn.Module):
         return analog
 
     def _step(self, inputs, hx):
-        """One inference step given this step's input projection."""
-        return self._gates(inputs, self.hidden(hx), hx)
+        """One inference step given this step's input projection.  FP32 gates run as one
+        kernel with the same roundings as the elementwise ops of ``_gates``."""
+        hidden = self.hidden(hx)
+        if (inputs.ndim == 2 and inputs.dtype == hidden.dtype == hx.dtype == torch.float32
+                and inputs.stride(1) == hidden.stride(1) == hx.stride(1) == 1):
+            return hip.gru_gates(inputs, hidden, hx)
+        return self._gates(inputs, hidden, hx)
 
 
 class _AnalogRecurrent(nn.Module):

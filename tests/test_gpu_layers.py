@@ -321,3 +321,22 @@ def test_gru_nonfinite_input_raises_at_its_step(hip_device):
         layer(x)
     cell = layer.cells[0]
     assert cell.input._event == 4 and cell.hidden._event == 4
+
+
+def test_gru_gates_kernel_matches_torch_ops(hip_device):
+    """mf_gru_gates equals PyTorch's separate elementwise gate ops on the GPU, bit for bit."""
+    from memfast_amd import hip
+    torch.manual_seed(9)
+    n, width = 67, 131
+    inputs = torch.randn(n, 3 * width, device=hip_device) * 4
+    hidden = torch.randn(n, 3 * width, device=hip_device) * 4
+    hx = torch.randn(n, width, device=hip_device)
+    inputs[0, :8] = torch.tensor([0.0, -0.0, 88.0, -88.0, 1e-30, -104.0, 30.0, -30.0])
+    got = hip.gru_gates(inputs, hidden, hx)
+    ir, iz, inn = inputs.chunk(3, dim=-1)
+    hr, hz, hn = hidden.chunk(3, dim=-1)
+    reset = torch.sigmoid(ir + hr)
+    update = torch.sigmoid(iz + hz)
+    expected = (1 - update) * torch.tanh(inn + reset * hn) + update * hx
+    assert torch.equal(got.view(torch.int32), expected.view(torch.int32)), (
+        (got != expected).sum().item(), (got - expected).abs().max().item())
