@@ -215,8 +215,35 @@ def _ptr(tensor):
     return ct.c_void_p(tensor.data_ptr()) if tensor is not None else None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device):
+    """The current HIP stream of ``device`` as a pointer."""
+    if _raw_stream is not None and isinstance(device, torch.device):
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return ct.c_void_p(_raw_stream(index))
     return ct.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class _Unchanged:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
+_UNCHANGED = _Unchanged()
+
+
+def _on(device):
+    """torch.cuda.device(device), skipped when it is already the current device."""
+    if not isinstance(device, torch.device):
+        return torch.cuda.device(device)
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _UNCHANGED
+    return torch.cuda.device(device)
 
 
 def require_device(tensor):
@@ -356,7 +383,7 @@ def input_tiles(value, config, fixed_scale=None, *, status=None):
     q = torch.empty((n, m, r), dtype=torch.uint8, device=value.device)
     xscale = torch.empty((n, m * config.reads_per_array), dtype=torch.float32, device=value.device)
     descr = ct.byref(descriptor(config))
-    with torch.cuda.device(value.device):
+    with _on(value.device):
         if fixed_scale is None:
             gr, gc = _group_dims(x.shape, config.input_quant_gran)
             grid = (math.ceil(n / gr), math.ceil(k / gc))
@@ -421,7 +448,7 @@ def conv_input_tiles(x, config, geometry, fixed_scale=None, *, status=None):
         fixed = fixed_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
         if fixed.numel() != k:
             raise ValueError("fixed input scale must have one entry per input feature")
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         check(
             library().mf_conv_input_tiles(
                 ct.byref(descriptor(config)), _ptr(value), ct.byref(geom), _ptr(fixed), gr, gc,
@@ -446,7 +473,7 @@ def _input_tiles_wide(value, config, fixed_scale, status):
     q = torch.empty((n, m, r), dtype=torch.int32, device=value.device)
     xscale = torch.empty((n, m * config.reads_per_array), dtype=torch.float64, device=value.device)
     descr = ct.byref(descriptor(config))
-    with torch.cuda.device(value.device):
+    with _on(value.device):
         if fixed_scale is None:
             gr, gc = _group_dims(x.shape, config.input_quant_gran)
             grid = (math.ceil(n / gr), math.ceil(k / gc))
@@ -506,7 +533,7 @@ def weight_tiles(weight, config, *, transposed=True, status=None):
     packed = torch.empty((m, p, r, c), dtype=torch.uint8, device=device)
     packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=device) if transposed else None
     wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float32, device=device)
-    with torch.cuda.device(device):
+    with _on(device):
         check(
             library().mf_quantize_weights(
                 ct.byref(descriptor(config)), _ptr(b), k, o, o, gr, gc, _ptr(work), _ptr(scale),
@@ -538,7 +565,7 @@ def _weight_tiles_wide(weight, config, status):
     packed = torch.empty((m, p, r, c), dtype=torch.int64, device=device)
     packed32 = torch.empty((m, p, r, c), dtype=torch.int32, device=device)
     wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float64, device=device)
-    with torch.cuda.device(device):
+    with _on(device):
         check(
             library().mf_quantize_weights_wide(
                 ct.byref(descriptor(config)), _ptr(b), k, o, o, gr, gc, _ptr(work), _ptr(scale),
@@ -565,7 +592,7 @@ def transpose_packed(packed, config):
     m, p, r, c = packed.shape
     packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=packed.device)
     src = packed.to(torch.uint8).contiguous()
-    with torch.cuda.device(packed.device):
+    with _on(packed.device):
         check(
             library().mf_transpose_packed(
                 ct.byref(descriptor(config)), _ptr(src), m, p, _ptr(packed_t),
@@ -591,7 +618,7 @@ def restore(packed, config, seed, event, begin, end):
     wide = config.wide
     src = _u32(packed) if wide else packed.to(torch.uint8).contiguous()
     entry = library().mf_restore_wide if wide else library().mf_restore
-    with torch.cuda.device(packed.device):
+    with _on(packed.device):
         check(
             entry(ct.byref(descriptor(config)), _ptr(src), m, p, begin, end, seed, event, _ptr(g),
                   _stream(packed.device)),
@@ -645,7 +672,7 @@ def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance
     codes_q = _u32(q) if wide else q.contiguous()
     codes_w = _u32(packed) if wide else packed.to(torch.uint8).contiguous()
     entry = library().mf_partial_wide if wide else library().mf_partial
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         check(
             entry(ct.byref(descriptor(config)), _ptr(codes_q), n, m, _ptr(codes_w), p, begin,
                   end, _ptr(g), seed, event, _ptr(totals), _ptr(counts), _stream(q.device)),
@@ -710,7 +737,7 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     # temporary could be handed to the next conversion by the caching allocator).
     q, xscale = q.contiguous(), xscale.contiguous()
     packed, wscale = packed.contiguous(), wscale.contiguous()
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         check(
             library().mf_mm(
                 ct.byref(descriptor(config)), _ptr(q), _ptr(xscale), n,
@@ -743,7 +770,7 @@ def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductan
     q = _u32(q)
     xscale = xscale.to(torch.float64).contiguous()
     wscale = wscale.to(torch.float64).contiguous()
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         check(
             library().mf_mm_wide(
                 ct.byref(descriptor(config)), _ptr(q),
@@ -757,6 +784,7 @@ def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductan
     return out
 
 
+@lru_cache(maxsize=4096)
 def mm_workspace_bytes(config, n, m, p):
     """Bytes of MFMA-kernel scratch ``mm`` uses for this shape (0 for the general kernel)."""
     size = ct.c_int64()
@@ -778,7 +806,7 @@ def bias_add(out, bias, status=None):
     if out.dtype != torch.float32 or out.stride(1) != 1 or bias.shape != (out.shape[1],):
         raise ValueError("bias_add takes an FP32 row-major output and a matching bias")
     bias = bias.to(device=out.device, dtype=torch.float32).contiguous()
-    with torch.cuda.device(out.device):
+    with _on(out.device):
         check(library().mf_bias_add(_ptr(out), out.shape[0], out.shape[1], out.stride(0),
                                     _ptr(bias), _ptr(status), _stream(out.device)), "bias add")
     return out
@@ -794,7 +822,7 @@ def gru_gates(inputs, hidden, hx):
                 or t.device != inputs.device):
             raise ValueError("gru_gates takes FP32 row-major [N, 3H], [N, 3H] and [N, H]")
     out = torch.empty((n, width), dtype=torch.float32, device=inputs.device)
-    with torch.cuda.device(inputs.device):
+    with _on(inputs.device):
         check(library().mf_gru_gates(_ptr(inputs), inputs.stride(0), _ptr(hidden), hidden.stride(0),
                                      _ptr(hx), hx.stride(0), _ptr(out), width, n, width,
                                      _stream(inputs.device)), "GRU gates")
@@ -815,7 +843,7 @@ def stable_sum(totals, xscale, wscale, config, col0, out):
     totals = totals.to(torch.float32).contiguous()
     xscale = xscale.to(torch.float32).contiguous()
     wscale = wscale.to(torch.float32).contiguous()
-    with torch.cuda.device(totals.device):
+    with _on(totals.device):
         check(
             library().mf_stable_sum(
                 ct.byref(descriptor(config)), _ptr(totals), n, groups, width, _ptr(xscale),
@@ -864,7 +892,7 @@ def mm_totals(q, packed_t, config, seed, event, *, conductance=None):
     groups = m * config.reads_per_array
     totals = torch.empty((n, groups, p, c), dtype=torch.float32, device=q.device)
     q, packed_t = q.contiguous(), packed_t.contiguous()
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         check(
             library().mf_mm_totals(
                 ct.byref(descriptor(config)), _ptr(q), n, m,
@@ -897,7 +925,7 @@ def mm_totals_wide(q, packed, config, seed, event, *, conductance=None):
     groups = m * config.reads_per_array
     totals = torch.empty((n, groups, p, c), dtype=torch.float64, device=q.device)
     q, packed = _u32(q), _u32(packed)
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         check(
             library().mf_mm_totals_wide(
                 ct.byref(descriptor(config)), _ptr(q), n, m, _ptr(packed), p, _ptr(g),
@@ -908,6 +936,7 @@ def mm_totals_wide(q, packed, config, seed, event, *, conductance=None):
     return totals
 
 
+@lru_cache(maxsize=4096)
 def mm_kernel(config, n, m, p, has_packed_t=True):
     """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA, 3: noisy-device MFMA for
     wide codes (what ``mm`` launches).
@@ -927,7 +956,7 @@ def rng(address, seed, stream, kind="uniform"):
     addr = address.to(torch.int64).contiguous()
     out = torch.empty(addr.shape, dtype=torch.float32, device=addr.device)
     fn = library().mf_rng_uniform if kind == "uniform" else library().mf_rng_normal
-    with torch.cuda.device(addr.device):
+    with _on(addr.device):
         check(fn(_ptr(addr), addr.numel(), int(seed) & (2**64 - 1), stream, _ptr(out),
                  _stream(addr.device)), f"rng {kind}")
     return out
@@ -955,7 +984,7 @@ class Program:
 
 @lru_cache(maxsize=256)
 def program(config, vectors, columns, device):
-    with torch.cuda.device(device):
+    with _on(device):
         torch.empty(0, device=device)
         return Program(config, vectors, columns)
 
