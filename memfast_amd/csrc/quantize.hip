@@ -547,34 +547,45 @@ __global__ __launch_bounds__(256) void k_conv_codes(const float *x, const mf_con
     const ConvLane me = conv_lane(g, u32(live ? r0 + lane : r0));
     const int k0 = int(kc) + wave * (CONV_CHUNK / 4);
     bool finite = true;
+    constexpr int CPW = CONV_CHUNK / 4;   // columns per wave
     if (k0 < K) {
+        // Gather every value (and scale) first, so the loads are all in flight
+        // before the first one is needed.
+        float v[CPW], sc[CPW];
         ConvTap tap;
         tap.start(g, k0);
         const i64 rg = gc ? ((live ? r0 + lane : r0) / gr) * ncg : 0;
         i64 cg = gc ? k0 / gc : 0, cr = gc ? k0 - cg * gc : 0;
-#pragma unroll 1
-        for (int e = 0; e < CONV_CHUNK / 16; ++e) {
+#pragma unroll
+        for (int t = 0; t < CPW; ++t) {
+            v[t] = 0.0f;
+            sc[t] = 1.0f;
+            if (k0 + t < K) {
+                v[t] = conv_load(x, g, me, live, tap);
+                sc[t] = gc ? scale[rg + cg] : scale[k0 + t];
+                tap.next(g);
+                if (gc && ++cr == gc) {
+                    cr = 0;
+                    ++cg;
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < CPW / 4; ++e) {
             u32 word = 0;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const int k = k0 + e * 4 + b;
-                if (k < K) {
-                    const float v = conv_load(x, g, me, live, tap);
-                    finite = finite && fabsf(v) <= FLT_MAX;
-                    const float sc = gc ? scale[rg + cg] : scale[k];
-                    word |= u32(quantize_code(v, sc, lower, upper, mask)) << (8 * b);
-                    tap.next(g);
-                    if (gc && ++cr == gc) {
-                        cr = 0;
-                        ++cg;
-                    }
+                const int t = e * 4 + b;
+                if (k0 + t < K) {
+                    finite = finite && fabsf(v[t]) <= FLT_MAX;
+                    word |= u32(quantize_code(v[t], sc[t], lower, upper, mask)) << (8 * b);
                 }
             }
-            tile[lane * CONV_PITCH + wave * (CONV_CHUNK / 16) + e] = word;
+            tile[lane * CONV_PITCH + wave * (CPW / 4) + e] = word;
         }
     } else {
 #pragma unroll
-        for (int e = 0; e < CONV_CHUNK / 16; ++e) tile[lane * CONV_PITCH + wave * (CONV_CHUNK / 16) + e] = 0;
+        for (int e = 0; e < CPW / 4; ++e) tile[lane * CONV_PITCH + wave * (CPW / 4) + e] = 0;
     }
     if (!finite && status) atomicOr(status, flag);
     __syncthreads();
