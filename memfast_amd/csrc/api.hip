@@ -3,6 +3,7 @@
 // Host side of the gfx950 engine: argument validation, kernel selection, the
 // ideal-device MFMA plan, launches on the caller's stream and error strings.
 // Nothing here allocates device memory; the caller owns every buffer.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -256,6 +257,25 @@ void ideal_workspace(const mf_config *cfg, i64 n, i64 m, i64 p, i64 *xbytes, i64
     *wbytes = align256((p * cfg->cols + 31) / 32 * G * 8);
 }
 
+// Whether every conductance term k1[w] * (g - L) fits fp16 with margin.  The
+// sampled normals are sqrt(-2 ln u) cos(2 pi v) with u >= 2^-25, so |z| < 5.9;
+// programming and shared read noise multiply g by at most exp(5.9 sigma) each,
+// drift by the drift factor, and stuck-at faults set L or H.
+bool fp16_terms_fit(const mf_config *cfg) {
+    const double zmax = 5.9;
+    double high = cfg->f_high;
+    if (cfg->has_write) high *= std::exp(zmax * double(cfg->f_write));
+    if (cfg->has_read) high *= std::exp(zmax * double(cfg->f_read));
+    if (cfg->has_drift && cfg->f_drift > 1.0f) high *= double(cfg->f_drift);
+    const double low = cfg->f_low;
+    const double span = std::max(high - low, low);   // |g - L| for g in [0, high]
+    for (int w = 0; w < cfg->n_w; ++w) {
+        const double k1 = double(float(cfg->d_voltage * double(cfg->w_mask[w]) * cfg->d_inv_unit));
+        if (!(k1 * span < 16384.0)) return false;
+    }
+    return true;
+}
+
 // Noisy-device MFMA eligibility and plan (noisy_mfma.hip): FP32 currents,
 // conductances that do not depend on the input slice (no slice_pair read
 // noise), no voltage or output-mode read noise, reads of 32 or 64 rows that
@@ -279,8 +299,7 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
     for (int a = 0; a < cfg->n_in; ++a) fa_sum += std::fabs(double(cfg->in_factor[a]));
     for (int w = 0; w < cfg->n_w; ++w) fw_sum += std::fabs(double(cfg->w_factor[w])) * cfg->adc_max[w];
     if (fa_sum * fw_sum >= 16777216.0) { *why = "slice totals exceed FP32 integers"; return false; }
-    for (int w = 0; w < cfg->n_w; ++w)
-        if (cfg->w_mask[w] > 255) { *why = "weight slice above 8 bits"; return false; }
+    if (!fp16_terms_fit(cfg)) { *why = "conductance terms beyond the fp16 range"; return false; }
     memset(plan, 0, sizeof(*plan));
     plan->n_in = cfg->n_in;
     plan->n_w = cfg->n_w;
@@ -458,8 +477,7 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
         return false;
     }
     if (cfg->activation_bits > 16) { *why = "input codes wider than 16 bits"; return false; }
-    for (int w = 0; w < cfg->n_w; ++w)
-        if (cfg->w_mask[w] > 255) { *why = "weight slice above 8 bits"; return false; }
+    if (!fp16_terms_fit(cfg)) { *why = "conductance terms beyond the fp16 range"; return false; }
     if (cfg->n_in > WIDE_MFMA_MAX_A || cfg->n_w > WIDE_MFMA_MAX_W ||
         cfg->n_w * NOISY_TERMS * (cfg->read_rows / 16) > WIDE_FRAGS_LARGE) {
         *why = "too many slices";

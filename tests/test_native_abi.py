@@ -103,3 +103,23 @@ def test_descriptor_fp32_constants():
     assert d.f_out_mean == f32(math.expm1(0.5 * 0.03**2))
     assert list(d.adc_max)[:len(cfg.adc_maxima)] == list(cfg.adc_maxima)
     assert d.f_alpha_over_max[0] == f32(0.1 / cfg.adc_maxima[0])
+
+
+def test_noisy_mfma_kernels_require_fp16_range():
+    """The noisy MFMA reads hold k1*(g - L) in fp16; configurations whose sampled
+    conductances could leave that range (huge noise, 8-bit weight slices with extreme
+    variation) are routed to the general kernel by the host plan."""
+    from memfast_amd import Config, Nonidealities
+    base = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                weight_slice=(1, 1, 2, 2, 2), array_size=(128, 128), rows_per_read=32)
+    ok = Config(**base, nonidealities=Nonidealities(write_variation=0.02))
+    assert hip.mm_kernel(ok, 64, 4, 4) == 2
+    wild = Config(**base, nonidealities=Nonidealities(write_variation=3.0))
+    assert hip.mm_kernel(wild, 64, 4, 4) == 0
+    wide = Config(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                  weight_slice=(1, 1, 2), bw_e=8, nonidealities=Nonidealities(read_variation=0.01))
+    assert hip.mm_kernel(wide, 64, 4, 4) == 3
+    wide_wild = Config(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                       weight_slice=(1, 1, 2), bw_e=8,
+                       nonidealities=Nonidealities(read_variation=2.5))
+    assert hip.mm_kernel(wide_wild, 64, 4, 4) == 0
