@@ -9,8 +9,8 @@
 // Here z = sum_r da * k1 * (g - L) with k1 = V*Mw/unit: the input digits da are
 // small integers (exact in fp16) and k1 * (g - L) (FP32, at most Mw <= 255 times
 // the conductance noise) is held as two fp16 terms hi + lo, hi = fp16(x) and
-// lo = fp16(x - hi): 22 significant bits, within 2^-23 of x relative to its
-// magnitude (the FP32 value itself carries 24).  Two fp16 MFMAs with FP32
+// lo = fp16(x - hi): 22 significant bits, within 2^-23 |x| of x (or 2^-25
+// absolute where lo is an fp16 subnormal; the FP32 value itself carries 24 bits).  Two fp16 MFMAs with FP32
 // accumulation give z to about FP32 accuracy; codes may flip where z lies within
 // that error of a rounding boundary (a few in 10^7 codes on the bench shapes),
 // the same order as FP32 summation-order differences from the CPU reference.
