@@ -549,7 +549,7 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
     const int frags = cfg->n_w * NOISY_TERMS * ks;
     if (frags > WIDE_FRAGS_LARGE) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
-    const bool large = frags > WIDE_FRAGS_SMALL;
+    const int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
     uint16_t *q16 = static_cast<uint16_t *>(workspace);
     uint4 *gs = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + codes_bytes);
     hipLaunchKernelGGL(k_codes16, dim3(grid_for(n * kp)), dim3(256), 0, s, q, n * kp, q16);
@@ -593,9 +593,13 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
                                 plan, args);                                                     \
     }
         if (ks == 4) {
-            if (large) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_LARGE) } else { MF_WIDE_LAUNCH(4, WIDE_FRAGS_SMALL) }
+            if (tier == 2) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_LARGE) }
+            else if (tier == 1) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_SMALL) }
+            else { MF_WIDE_LAUNCH(4, WIDE_FRAGS_TINY) }
         } else {
-            if (large) { MF_WIDE_LAUNCH(2, WIDE_FRAGS_LARGE) } else { MF_WIDE_LAUNCH(2, WIDE_FRAGS_SMALL) }
+            if (tier == 2) { MF_WIDE_LAUNCH(2, WIDE_FRAGS_LARGE) }
+            else if (tier == 1) { MF_WIDE_LAUNCH(2, WIDE_FRAGS_SMALL) }
+            else { MF_WIDE_LAUNCH(2, WIDE_FRAGS_TINY) }
         }
 #undef MF_WIDE_LAUNCH
     }

@@ -169,10 +169,17 @@ template <int KS>
 __global__ void k_split_wide(const mf_config cfg, const u32 *packed, const float *g_in, i64 m,
                              i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin, i64 CB,
                              const NoisyWidePlan plan, uint4 *gs);
-// LDS capacity of the wide read: fragments (1 KiB) per read and buffer.  36:
-// two buffers in 72 KiB (two blocks per CU); 72: 144 KiB (one block per CU).
+// LDS capacity of the wide read: fragments (1 KiB) per read and buffer.  24:
+// two buffers in 48 KiB (three blocks per CU); 36: 72 KiB (two blocks per CU);
+// 72: 144 KiB (one block per CU).
+constexpr int WIDE_FRAGS_TINY = 24;
 constexpr int WIDE_FRAGS_SMALL = 36;
 constexpr int WIDE_FRAGS_LARGE = 72;
+// Blocks per CU the wide read is compiled for: three (at most 168 VGPRs) where
+// the LDS allows it and the linear converter leaves the registers to spare.
+constexpr int wide_blocks_per_cu(int frmax, bool nonlinear) {
+    return frmax <= WIDE_FRAGS_TINY && !nonlinear ? 3 : 2;
+}
 template <int KS, bool NONLINEAR, bool SMALL, int FRMAX>
 __global__ void k_noisy_wide(const NoisyWidePlan plan, const NoisyWideArgs args);
 

@@ -27,7 +27,8 @@
 // order).  Block = 4 waves on the same 32 columns and 128 vectors (32 per
 // wave); per read the block copies the run into LDS with global_load_lds
 // (double-buffered in two LDS objects, one barrier per read) and every wave
-// reads it from there.  FRMAX bounds the fragments per read (W * 2 * KS).
+// reads it from there.  FRMAX bounds the fragments per read (W * 2 * KS); the
+// smallest capacity is compiled for three blocks per CU.
 // Input codes are repacked to 16 bits (k_codes16) so a lane's 8 rows of a
 // 16-row step are one 16-byte load.  Bound: VALU (digit expansion + ADC per
 // slice pair) with fp16 MFMA as co-bound.
@@ -195,7 +196,8 @@ template __global__ void k_split_wide<4>(const mf_config, const u32 *, const flo
                                          i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 
 template <int KS, bool NONLINEAR, bool SMALL, int FRMAX>
-__global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
+__global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_noisy_wide(
+    const NoisyWidePlan plan,
                                                        const NoisyWideArgs args) {
     // Two LDS objects (read g in one, read g+1 arriving in the other) so that the
     // compiler can tell the in-flight LDS DMA from the LDS reads of the current
@@ -420,8 +422,10 @@ __global__ __launch_bounds__(256, 2) void k_noisy_wide(const NoisyWidePlan plan,
     MF_NOISY_WIDE_INST(KS, true, true, FRMAX)       \
     MF_NOISY_WIDE_INST(KS, false, false, FRMAX)     \
     MF_NOISY_WIDE_INST(KS, true, false, FRMAX)
+MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_TINY)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_SMALL)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_LARGE)
+MF_NOISY_WIDE_INST4(4, WIDE_FRAGS_TINY)
 MF_NOISY_WIDE_INST4(4, WIDE_FRAGS_SMALL)
 MF_NOISY_WIDE_INST4(4, WIDE_FRAGS_LARGE)
 

@@ -648,6 +648,12 @@ WIDE_MFMA = {
                       rows_per_read=64, adc_bits=(6, 7, 7, 8, 8)),
                  dict(write_variation=0.03, read_variation=0.02, stuck_at_low=0.01,
                       stuck_at_high=0.01), 130, 400, 100),
+    # Four 2-bit weight slices at 64-row reads (32 KiB of terms per read: the middle
+    # LDS capacity), 4-bit input digits.
+    "int10_w4": (dict(activation_bits=10, weight_bits=7, input_slice=(1, 1, 4, 4),
+                      weight_slice=(1, 2, 2, 2), array_size=(128, 64), rows_per_read=64,
+                      adc_bits=8), dict(write_variation=0.02, drift_coefficient=0.05,
+                                        drift_time=100.0), 90, 300, 130),
 }
 
 
