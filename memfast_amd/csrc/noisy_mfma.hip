@@ -158,6 +158,21 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
         qw[ks] = make_uint2(x, y);
     }
 
+    // Conductance terms of (read g, weight slice w), double-buffered in registers:
+    // the next slice's terms are in flight while the current slice's MFMAs run.
+    auto load_terms = [&](v8h (&F)[NOISY_TERMS][KS], int g, int w) {
+        const uint4 *frag = frag_base + i64(g) * NOISY_TERMS * KS * 64 + w * w_stride;
+#pragma unroll
+        for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                F[term][ks] = __builtin_bit_cast(v8h, frag[(term * KS + ks) * 64]);
+    };
+    // (With KS == 2 a second buffer would cost the third wave per SIMD: 32-row reads
+    // load each slice's terms where they are used.)
+    v8h Fa[NOISY_TERMS][KS], Fb[NOISY_TERMS][KS];
+    if (KS != 2 && g0 < g1) load_terms(Fa, g0, 0);
+
     for (int g = g0; g < g1; ++g) {
         // Input digits of this read for every slice (B operands).
         v8h B[NA][KS];
@@ -182,15 +197,6 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
         u32 Ti[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) Ti[r] = 0u;
-        const uint4 *frag_g = frag_base + i64(g) * NOISY_TERMS * KS * 64;
-        auto load_terms = [&](v8h (&F)[NOISY_TERMS][KS], int w) {
-            const uint4 *frag = frag_g + w * w_stride;
-#pragma unroll
-            for (int term = 0; term < NOISY_TERMS; ++term)
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    F[term][ks] = __builtin_bit_cast(v8h, frag[(term * KS + ks) * 64]);
-        };
         auto slice_reads = [&](const v8h (&F)[NOISY_TERMS][KS], int w) {
             const float top = MAGIC + plan.top[w], alpha = plan.alpha[w];
             const float fw = plan.fw[w];
@@ -224,10 +230,29 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
                 convert(I, a);
             }
         };
-        for (int w = 0; w < W; ++w) {
-            v8h F[NOISY_TERMS][KS];
-            load_terms(F, w);
-            slice_reads(F, w);
+        if (KS == 2) {
+            for (int w = 0; w < W; ++w) {
+                load_terms(Fa, g, w);
+                slice_reads(Fa, w);
+            }
+        } else {
+            // Fa holds (g, 0) on entry; on exit it holds (g + 1, 0) when that read exists.
+            int w = 0;
+            for (; w + 1 < W; w += 2) {
+                load_terms(Fb, g, w + 1);
+                slice_reads(Fa, w);
+                if (w + 2 < W) load_terms(Fa, g, w + 2);
+                else if (g + 1 < g1) load_terms(Fa, g + 1, 0);
+                slice_reads(Fb, w + 1);
+            }
+            if (w < W) {
+                if (g + 1 < g1) load_terms(Fb, g + 1, 0);
+                slice_reads(Fa, w);
+#pragma unroll
+                for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) Fa[term][ks] = Fb[term][ks];
+            }
         }
         float T[16];
 #pragma unroll
