@@ -340,3 +340,81 @@ def test_gru_gates_kernel_matches_torch_ops(hip_device):
     expected = (1 - update) * torch.tanh(inn + reset * hn) + update * hx
     assert torch.equal(got.view(torch.int32), expected.view(torch.int32)), (
         (got != expected).sum().item(), (got - expected).abs().max().item())
+
+
+def _step_cells(model, x, directions, layers, hidden_size):
+    """Reference traversal: each cell called per step (per-step reads), as the reference."""
+    sequence, finals = x, []
+    batch = x.shape[1]
+    for lay in range(layers):
+        outs = []
+        for d in range(directions):
+            cell = model.cells[lay * directions + d]
+            h = torch.zeros(batch, hidden_size, device=x.device, dtype=x.dtype)
+            values = []
+            for t in (reversed(range(x.shape[0])) if d else range(x.shape[0])):
+                h = cell(sequence[t], h)
+                values.append(h)
+            if d:
+                values.reverse()
+            outs.append(torch.stack(values))
+            finals.append(h)
+        sequence = torch.cat(outs, dim=-1) if directions == 2 else outs[0]
+    return sequence, torch.stack(finals)
+
+
+@pytest.mark.parametrize("nonlinearity", ["tanh", "relu"])
+@pytest.mark.parametrize("bidirectional", [False, True])
+def test_rnn_sequence_matches_per_step_cells(hip_device, nonlinearity, bidirectional):
+    """AnalogRNN over a sequence equals stepping its cells, bit for bit, with the same
+    read-event counts (write noise: input projections read in one product)."""
+    from memfast_amd.nn import AnalogRNN
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(10)
+    source = nn.RNN(24, 48, num_layers=2, nonlinearity=nonlinearity,
+                    bidirectional=bidirectional).to(hip_device)
+    x = torch.randn(7, 5, 24, device=hip_device)
+    layer = AnalogRNN(source, Simulator(cfg, device=hip_device), name="rnn")
+    stepped = AnalogRNN(source, Simulator(cfg, device=hip_device), name="rnn")
+    output, hidden = layer(x)
+    directions = 2 if bidirectional else 1
+    expected, finals = _step_cells(stepped, x, directions, 2, 48)
+    assert torch.equal(output.view(torch.int32), expected.view(torch.int32))
+    assert torch.equal(hidden.view(torch.int32), finals.view(torch.int32))
+    for a, b in zip(layer.cells, stepped.cells):
+        assert a.input._event == b.input._event == 7
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gru_half_precision_sequence_matches_per_step_cells(hip_device, dtype):
+    """Half-precision sequences take PyTorch's gate ops; the sequence equals stepping the
+    cells bit for bit."""
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(11)
+    source = nn.GRU(40, 64).to(hip_device).to(dtype)
+    x = torch.randn(6, 3, 40, device=hip_device, dtype=dtype)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    stepped = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    output, hidden = layer(x)
+    expected, finals = _step_cells(stepped, x, 1, 1, 64)
+    assert output.dtype == dtype
+    assert torch.equal(output.view(torch.int16), expected.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_conv_half_precision_implicit_matches_unfold(hip_device, dtype):
+    """Half-precision inputs: the implicit-im2col forward equals reading F.unfold's
+    patches of the same tensor, bit for bit, and keeps the input dtype."""
+    cfg = config("write")
+    torch.manual_seed(12)
+    source = nn.Conv2d(6, 8, 3, stride=1, padding=1).to(hip_device)
+    layer = AnalogConv2d(source, Simulator(cfg, device=hip_device), name="conv")
+    x = torch.randn(2, 6, 10, 10, device=hip_device).to(dtype)
+    got = layer(x)
+    layer.matrices[0].reset_read()
+    patches = F.unfold(x, 3, 1, 1, 1)
+    expected = layer.matrices[0](patches.transpose(1, 2)).transpose(1, 2).reshape(2, 8, 10, 10)
+    assert got.dtype == dtype
+    assert torch.equal(got.view(torch.int16), expected.view(torch.int16))
