@@ -118,16 +118,31 @@ def resnet18():
     return model.eval()
 
 
-def secondary(device):
-    """The other BASELINE configurations, one timed run each (latency or throughput)."""
-    import torch
-    from torch import nn
-
-    import memfast_amd as memfast
+def secondary(device, only=None):
+    """The other BASELINE configurations, one timed run each (latency or throughput);
+    ``only`` (a set of result names) restricts the run to those configurations."""
+    def want(name):
+        return only is None or name in only
 
     out = {}
     int8 = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
                 weight_slice=(1, 1, 2, 2, 2))
+    if want("config1_readme_mm"):
+        _config1(out, int8, device)
+    if want("config3_gru"):
+        _config3(out, int8, device)
+    if want("config4_resnet18"):
+        _config4(out, int8, device)
+    if want("config5_llm_q_proj"):
+        _config5(out, device)
+    return out
+
+
+def _config1(out, int8, device):
+    import torch
+
+    import memfast_amd as memfast
+
     # Config 1: README first simulation (4x128 @ 128x32, write variation).
     cfg = memfast.Config(**int8, array_size=(128, 128), rows_per_read=32,
                          weight_quant_gran=(32, 1), input_quant_gran=(1, 32), adc_bits=7,
@@ -137,6 +152,14 @@ def secondary(device):
     sim = memfast.Simulator(cfg, device=device)
     seconds = timed(lambda: sim.mm(a, b), 50)
     out["config1_readme_mm"] = dict(us_per_call=round(seconds * 1e6, 1), macs=4 * 128 * 32)
+
+
+def _config3(out, int8, device):
+    import torch
+    from torch import nn
+
+    import memfast_amd as memfast
+
     # Config 3: converted 1-layer GRU (40 -> 512), batch 32, 200 steps.
     cfg = memfast.Config(**int8, array_size=(128, 128), rows_per_read=32, adc_bits=7,
                          nonidealities=memfast.Nonidealities(write_variation=0.02))
@@ -149,6 +172,14 @@ def secondary(device):
     out["config3_gru"] = dict(ms_per_sequence=round(seconds * 1e3, 2),
                               us_per_step=round(seconds / 200 * 1e6, 1),
                               gmac_per_s=round(macs / seconds / 1e9, 2))
+
+
+def _config4(out, int8, device):
+    import torch
+    from torch import nn
+
+    import memfast_amd as memfast
+
     # Config 4: ResNet-18, batch 64 at 224^2, every Conv2d/Linear converted, fixed input
     # scales from a 4-batch synthetic calibration, write variation + 0.1% stuck-at faults.
     cfg = memfast.Config(**int8, array_size=(256, 256), rows_per_read=64,
@@ -182,6 +213,13 @@ def secondary(device):
     out["config4_resnet18"] = dict(ms_per_batch=round(seconds * 1e3, 1), batch=64,
                                    images_per_s=round(64 / seconds, 1),
                                    gmac_per_s=round(116.0e9 / seconds / 1e9, 1))
+
+
+def _config5(out, device):
+    import torch
+
+    import memfast_amd as memfast
+
     # Config 5 (sample): one q_proj 4096x4096 on 2048 tokens, BFP bw_e=8 16-bit inputs
     # (1,1,2,2,2,2,2,2,2) x INT4 weights (1,1,2), drift + read noise; default schedule.
     cfg = memfast.Config(activation_bits=16, weight_bits=4,
@@ -198,7 +236,6 @@ def secondary(device):
     seconds = timed(lambda: sim.mm(tokens, weight))
     out["config5_llm_q_proj"] = dict(ms_per_call=round(seconds * 1e3, 1), tokens=2048,
                                      gmac_per_s=round(2048 * 4096 * 4096 / seconds / 1e9, 2))
-    return out
 
 
 def main():
@@ -210,6 +247,9 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true",
                         help="skip the timing of BASELINE configurations 1, 3, 4 and 5")
+    parser.add_argument("--secondary-only", default=None, metavar="NAMES",
+                        help="time only these secondary configurations (comma-separated result "
+                             "names, e.g. config4_resnet18) and print them; for profiling")
     parser.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                         help="first run one device-to-device copy of MIB MiB (a known-size "
                              "kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -226,6 +266,10 @@ def main():
     from memfast_amd import hip
 
     device = torch.device("cuda", 0)
+    if args.secondary_only:
+        names = set(args.secondary_only.split(","))
+        print(json.dumps(dict(secondary=secondary(device, only=names))), flush=True)
+        return
     torch.manual_seed(135)
     a_cpu = torch.randn(SIZE, SIZE)
     b_cpu = torch.randn(SIZE, SIZE)

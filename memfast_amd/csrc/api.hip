@@ -647,6 +647,26 @@ int launch_general(const mf_config *cfg, const GeneralArgs &args, int out_kind, 
     return check_launch("general read");
 }
 
+// Group maxima |x| into work[row group][col group] (cleared): column groups and
+// wide row groups by chunked reductions with few atomics, others elementwise.
+static void launch_group_max_f32(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
+                                 i64 ncg, u32 *work, u32 *status, u32 flag, hipStream_t s) {
+    const i64 chunks = (rows + COL_CHUNK_ROWS - 1) / COL_CHUNK_ROWS;
+    const i64 row_chunks = (cols + ROW_CHUNK_COLS - 1) / ROW_CHUNK_COLS;
+    if (gr == 1 && gc >= 64 && (rows + 3) / 4 <= 65535 && row_chunks <= 2147483647) {
+        hipLaunchKernelGGL((k_row_group_max<float, u32>),
+                           dim3(unsigned(row_chunks), unsigned((rows + 3) / 4)), dim3(256), 0, s, x,
+                           rows, cols, ld, gc, ncg, work, status, flag);
+    } else if ((gr > 1 || gc == 1) && (cols + 63) / 64 <= 2147483647 && chunks <= 65535) {
+        hipLaunchKernelGGL((k_col_group_max<float, u32>),
+                           dim3(unsigned((cols + 63) / 64), unsigned(chunks)), dim3(256), 0, s, x,
+                           rows, cols, ld, gr, gc, ncg, work, status, flag);
+    } else {
+        hipLaunchKernelGGL(k_group_max, dim3(grid_for(rows * ((cols + 7) / 8))), dim3(256), 0, s, x,
+                           rows, cols, ld, gr, gc, ncg, work, status, flag);
+    }
+}
+
 }  // namespace mf
 
 using namespace mf;
@@ -806,8 +826,7 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
     } else {
         if (!work) return fail(MF_E_INVALID, "grouped input quantization needs a work buffer");
         hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
-        hipLaunchKernelGGL(k_group_max, dim3(grid_for(n * ((k + 7) / 8))), dim3(256), 0, s, x, n, k,
-                           ld, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT));
+        launch_group_max_f32(x, n, k, ld, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT), s);
         hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
                            nrg * ncg, upper, scale);
         hipLaunchKernelGGL(k_input_codes, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
@@ -882,8 +901,7 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
     } else {
         if (!work) return fail(MF_E_INVALID, "grouped weight quantization needs a work buffer");
         hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
-        hipLaunchKernelGGL(k_group_max, dim3(grid_for(k * ((o + 7) / 8))), dim3(256), 0, s, b, k, o,
-                           ld, gr, gc, ncg, work, status, u32(MF_STATUS_WEIGHT));
+        launch_group_max_f32(b, k, o, ld, gr, gc, ncg, work, status, u32(MF_STATUS_WEIGHT), s);
         hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
                            nrg * ncg, upper, scale);
         hipLaunchKernelGGL(k_weight_codes, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o, ld, R,
@@ -1218,12 +1236,15 @@ static void launch_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i6
                                  i64 ncg, u64 *work, u32 *status, u32 flag, hipStream_t s) {
     const i64 chunks = (rows + COL_CHUNK_ROWS - 1) / COL_CHUNK_ROWS;
     const i64 row_chunks = (cols + ROW_CHUNK_COLS - 1) / ROW_CHUNK_COLS;
-    if (gc == 1 && (cols + 63) / 64 <= 2147483647 && chunks <= 65535) {
-        hipLaunchKernelGGL(k_col_group_max_f64, dim3(unsigned((cols + 63) / 64), unsigned(chunks)),
-                           dim3(256), 0, s, x, rows, cols, ld, gr, work, status, flag);
-    } else if (gr == 1 && gc >= 64 && (rows + 3) / 4 <= 65535 && row_chunks <= 2147483647) {
-        hipLaunchKernelGGL(k_row_group_max_f64, dim3(unsigned(row_chunks), unsigned((rows + 3) / 4)),
-                           dim3(256), 0, s, x, rows, cols, ld, gc, ncg, work, status, flag);
+    unsigned long long *w = reinterpret_cast<unsigned long long *>(work);
+    if (gr == 1 && gc >= 64 && (rows + 3) / 4 <= 65535 && row_chunks <= 2147483647) {
+        hipLaunchKernelGGL((k_row_group_max<double, unsigned long long>),
+                           dim3(unsigned(row_chunks), unsigned((rows + 3) / 4)), dim3(256), 0, s, x,
+                           rows, cols, ld, gc, ncg, w, status, flag);
+    } else if ((gr > 1 || gc == 1) && (cols + 63) / 64 <= 2147483647 && chunks <= 65535) {
+        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long>),
+                           dim3(unsigned((cols + 63) / 64), unsigned(chunks)), dim3(256), 0, s, x,
+                           rows, cols, ld, gr, gc, ncg, w, status, flag);
     } else {
         hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(rows * cols)), dim3(256), 0, s, x, rows,
                            cols, ld, gr, gc, ncg, work, status, flag);

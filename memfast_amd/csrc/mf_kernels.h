@@ -239,12 +239,16 @@ __global__ void k_weight_scales(i64 k, i64 o, i64 groups, i64 op, int R, int P, 
 __global__ void k_transpose_packed(const u8 *packed, int R, int C, i64 m, i64 p, u8 *packed_t);
 __global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
                                 i64 ncg, u64 *work, u32 *status, u32 flag);
-__global__ void k_col_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr,
-                                    u64 *work, u32 *status, u32 flag);
-constexpr int COL_CHUNK_ROWS = 256;   // rows per k_col_group_max_f64 block
-__global__ void k_row_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gc, i64 ncg,
-                                    u64 *work, u32 *status, u32 flag);
-constexpr int ROW_CHUNK_COLS = 1024;  // columns per k_row_group_max_f64 wave
+// Group maxima of |x| as bit patterns (U = u32 for float, unsigned long long for
+// double): reduced along rows first (any gr, gc), or along a row (gr == 1).
+template <typename T, typename U>
+__global__ void k_col_group_max(const T *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,
+                                U *work, u32 *status, u32 flag);
+constexpr int COL_CHUNK_ROWS = 256;   // rows per k_col_group_max block
+template <typename T, typename U>
+__global__ void k_row_group_max(const T *x, i64 rows, i64 cols, i64 ld, i64 gc, i64 ncg, U *work,
+                                u32 *status, u32 flag);
+constexpr int ROW_CHUNK_COLS = 1024;  // columns per k_row_group_max wave
 __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
                                   double *scale);
 __global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,

@@ -729,84 +729,123 @@ __global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64
     if (!finite && status) atomicOr(status, flag);
 }
 
-// Column groups (gc == 1, any gr) of an FP64 matrix: block = 64 columns x 4
-// row lanes over a chunk of COL_CHUNK rows (coalesced across the columns).
-// Each thread keeps a running maximum while its rows stay in one group and
-// flushes it to LDS; the four row lanes are folded there and one atomicMax per
-// (column, group) and chunk remains.  |x| bit patterns order like the values.
+// |x| as its bit pattern (which orders like the value for |x| >= 0) and the
+// largest finite magnitude, for FP32 (u32 bits) and FP64 (u64 bits).
+template <typename T> struct AbsBits;
+template <> struct AbsBits<float> {
+    typedef u32 U;
+    static __device__ __forceinline__ U of(float v) { return __float_as_uint(v); }
+    static constexpr float LARGEST = FLT_MAX;
+};
+template <> struct AbsBits<double> {
+    typedef unsigned long long U;
+    static __device__ __forceinline__ U of(double v) { return U(__double_as_longlong(v)); }
+    static constexpr double LARGEST = DBL_MAX;
+};
+
+// Groups of gr rows x gc columns, reduced along the rows first: block = 64
+// columns x 4 row lanes over a chunk of COL_CHUNK rows (coalesced across the
+// columns).  Each thread keeps a running maximum while its rows stay in one row
+// group; LDS folds the four row lanes; then the 64 column maxima go to their
+// column groups: a wave maximum and one atomicMax when the block's columns lie
+// in one group, else one atomicMax per column.  work [ceil(rows/gr), ncg].
 constexpr int COL_CHUNK = COL_CHUNK_ROWS;
-__global__ __launch_bounds__(256) void k_col_group_max_f64(const double *x, i64 rows, i64 cols,
-                                                           i64 ld, i64 gr, u64 *work, u32 *status,
-                                                           u32 flag) {
-    __shared__ u64 part[4][64];
+template <typename T, typename U>
+__global__ __launch_bounds__(256) void k_col_group_max(const T *x, i64 rows, i64 cols, i64 ld,
+                                                       i64 gr, i64 gc, i64 ncg, U *work,
+                                                       u32 *status, u32 flag) {
+    __shared__ U part[4][64];
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    const i64 c = i64(blockIdx.x) * 64 + tx;
+    const i64 c0 = i64(blockIdx.x) * 64;
+    const i64 c = c0 + tx;
     const i64 r0 = i64(blockIdx.y) * COL_CHUNK;
     const i64 r1 = (r0 + COL_CHUNK) < rows ? (r0 + COL_CHUNK) : rows;
+    const i64 c_last = (c0 + 63) < (cols - 1) ? (c0 + 63) : (cols - 1);
+    const bool one_group = c0 / gc == c_last / gc;
     bool finite = true;
-    // Groups that intersect this chunk, handled one at a time (uniform loop).
+    // Row groups that intersect this chunk, handled one at a time (uniform loop).
     for (i64 g = r0 / gr; g * gr < r1; ++g) {
         const i64 lo = (g * gr) > r0 ? (g * gr) : r0;
         const i64 hi = ((g + 1) * gr) < r1 ? ((g + 1) * gr) : r1;
-        u64 best = 0;
+        U best = 0;
         if (c < cols) {
             for (i64 r = lo + ty; r < hi; r += 4) {
-                const double v = fabs(x[r * ld + c]);
-                finite = finite && v <= DBL_MAX;
-                const u64 bits = u64(__double_as_longlong(v));
+                const T v = fabs(x[r * ld + c]);
+                finite = finite && v <= AbsBits<T>::LARGEST;
+                const U bits = U(AbsBits<T>::of(v));
                 best = bits > best ? bits : best;
             }
         }
         part[ty][tx] = best;
         __syncthreads();
-        if (ty == 0 && c < cols) {
-            u64 m = part[0][tx];
+        if (ty == 0) {
+            U m = part[0][tx];
             m = part[1][tx] > m ? part[1][tx] : m;
             m = part[2][tx] > m ? part[2][tx] : m;
             m = part[3][tx] > m ? part[3][tx] : m;
-            if (m) atomicMax(reinterpret_cast<unsigned long long *>(&work[g * cols + c]),
-                             static_cast<unsigned long long>(m));
+            if (one_group) {
+#pragma unroll
+                for (int d = 32; d >= 1; d >>= 1) {
+                    const U other = U(__shfl_xor(m, d, 64));
+                    m = other > m ? other : m;
+                }
+                if (tx == 0 && m) atomicMax(&work[g * ncg + c0 / gc], m);
+            } else if (c < cols && m) {
+                atomicMax(&work[g * ncg + c / gc], m);
+            }
         }
         __syncthreads();
     }
     if (!finite && status) atomicOr(status, flag);
 }
 
-// Row groups (gr == 1, gc >= 64) of an FP64 matrix: one wave per row and chunk
-// of ROW_CHUNK columns (coalesced); per group in the chunk a lane maximum, a
-// wave maximum by shuffles, and one atomicMax per (row, group, chunk).
+// Row groups (gr == 1, gc >= 64): one wave per row and chunk of ROW_CHUNK
+// columns (coalesced); per group in the chunk a lane maximum, a wave maximum by
+// shuffles, and one atomicMax per (row, group, chunk).  work [rows, ncg].
 constexpr int ROW_CHUNK = ROW_CHUNK_COLS;
-__global__ __launch_bounds__(256) void k_row_group_max_f64(const double *x, i64 rows, i64 cols,
-                                                           i64 ld, i64 gc, i64 ncg, u64 *work,
-                                                           u32 *status, u32 flag) {
+template <typename T, typename U>
+__global__ __launch_bounds__(256) void k_row_group_max(const T *x, i64 rows, i64 cols, i64 ld,
+                                                       i64 gc, i64 ncg, U *work, u32 *status,
+                                                       u32 flag) {
     const int lane = threadIdx.x & 63;
     const i64 row = i64(blockIdx.y) * 4 + (threadIdx.x >> 6);
     const i64 c0 = i64(blockIdx.x) * ROW_CHUNK;
     if (row >= rows) return;
     const i64 c1 = (c0 + ROW_CHUNK) < cols ? (c0 + ROW_CHUNK) : cols;
-    const double *src = x + row * ld;
+    const T *src = x + row * ld;
     bool finite = true;
     for (i64 g = c0 / gc; g * gc < c1; ++g) {
         const i64 lo = (g * gc) > c0 ? (g * gc) : c0;
         const i64 hi = ((g + 1) * gc) < c1 ? ((g + 1) * gc) : c1;
-        u64 best = 0;
+        U best = 0;
         for (i64 c = lo + lane; c < hi; c += 64) {
-            const double v = fabs(src[c]);
-            finite = finite && v <= DBL_MAX;
-            const u64 bits = u64(__double_as_longlong(v));
+            const T v = fabs(src[c]);
+            finite = finite && v <= AbsBits<T>::LARGEST;
+            const U bits = U(AbsBits<T>::of(v));
             best = bits > best ? bits : best;
         }
 #pragma unroll
         for (int d = 32; d >= 1; d >>= 1) {
-            const u64 other = u64(__shfl_xor(static_cast<unsigned long long>(best), d, 64));
+            const U other = U(__shfl_xor(best, d, 64));
             best = other > best ? other : best;
         }
-        if (lane == 0 && best)
-            atomicMax(reinterpret_cast<unsigned long long *>(&work[row * ncg + g]),
-                      static_cast<unsigned long long>(best));
+        if (lane == 0 && best) atomicMax(&work[row * ncg + g], best);
     }
     if (!finite && status) atomicOr(status, flag);
 }
+
+template __global__ void k_col_group_max<float, u32>(const float *, i64, i64, i64, i64, i64, i64,
+                                                     u32 *, u32 *, u32);
+template __global__ void k_col_group_max<double, unsigned long long>(const double *, i64, i64, i64,
+                                                                     i64, i64, i64,
+                                                                     unsigned long long *, u32 *,
+                                                                     u32);
+template __global__ void k_row_group_max<float, u32>(const float *, i64, i64, i64, i64, i64, u32 *,
+                                                     u32 *, u32);
+template __global__ void k_row_group_max<double, unsigned long long>(const double *, i64, i64, i64,
+                                                                     i64, i64,
+                                                                     unsigned long long *, u32 *,
+                                                                     u32);
 
 // floor() of the correctly rounded log2(x) for normal x > 0: ilogb(x), or one
 // more when log2(x) lies within half a unit in the last place below the next

@@ -809,6 +809,32 @@ def test_wide_group_quantizers_bit_exact(hip_device, wgran, igran):
     assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
 
 
+# Narrow (FP32) group quantizers: whole-column and whole-matrix groups, groups that straddle
+# the kernels' 256-row chunks, and 2-D groups (the row-first reduction path).
+NARROW_GROUPS = [((None, 1), (1, None)), ((192, 1), (None, 64)), ((320, 3), (None, None)),
+                 ((64, 70), (2, 64)), ((None, 7), (5, 128)), ((128, 2), (300, 1088))]
+
+
+@pytest.mark.parametrize("wgran,igran", NARROW_GROUPS, ids=[f"{w}-{i}" for w, i in NARROW_GROUPS])
+def test_narrow_group_quantizers_bit_exact(hip_device, wgran, igran):
+    """FP32 group maxima of every group shape -> codes and scales identical to the oracle's."""
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                 weight_slice=(1, 1, 2, 2, 2), array_size=(64, 64), adc_bits=8,
+                 weight_quant_gran=wgran, input_quant_gran=igran)
+    gen = torch.Generator().manual_seed(46)
+    a = torch.randn(600, 1500, generator=gen)
+    a[:, 700] = 50.0
+    a[333, 10] = -80.0
+    b = torch.randn(1500, 70, generator=gen) * 0.02
+    b[513, :] = -3.0
+    q, xs = hip.input_tiles(a.to(hip_device), cfg)
+    packed, _, ws = hip.weight_tiles(b.T.to(hip_device), cfg)
+    q_ref, xs_ref = oracle.input_tiles(a, cfg)
+    packed_ref, ws_ref = oracle.weight_tiles(b.T, cfg)
+    assert bits_equal(q, q_ref) and bits_equal(xs, xs_ref)
+    assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
+
+
 def test_noisy_mfma_unsplit_epilogue(hip_device):
     """A grid of 512 blocks or more keeps the fused single-kernel read (no read split):
     its output is the reference epilogue of the kernel's own totals, bit for bit."""
