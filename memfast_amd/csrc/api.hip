@@ -862,12 +862,12 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
     if (gc == 1 && tiled && kp / (4 * gr) <= 65535) {
         const dim3 grid{unsigned(op / 64), unsigned(kp / (4 * gr)), 1u};
         if (gr == 16)
-            hipLaunchKernelGGL(k_col_groups_tile<16>, grid, dim3(256), 0, s, b, k, o, ld, R, C, m, p,
-                               lower, upper, mask, packed, packed_t, scale, status,
+            hipLaunchKernelGGL((k_col_groups_tile<16, false>), grid, dim3(256), 0, s, b, k, o, ld, R,
+                               C, m, p, lower, upper, mask, packed, packed_t, scale, gr, status,
                                u32(MF_STATUS_WEIGHT));
         else
-            hipLaunchKernelGGL(k_col_groups_tile<32>, grid, dim3(256), 0, s, b, k, o, ld, R, C, m, p,
-                               lower, upper, mask, packed, packed_t, scale, status,
+            hipLaunchKernelGGL((k_col_groups_tile<32, false>), grid, dim3(256), 0, s, b, k, o, ld, R,
+                               C, m, p, lower, upper, mask, packed, packed_t, scale, gr, status,
                                u32(MF_STATUS_WEIGHT));
     } else if (gc == 1 && reg_group && (kp + gr - 1) / gr <= 65535) {
         const dim3 grid{unsigned((op + 255) / 256), unsigned((kp + gr - 1) / gr), 1u};
@@ -898,6 +898,30 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
             hipLaunchKernelGGL(k_col_groups<false>, grid, dim3(256), 0, s, b, k, o, ld, gr, span, R,
                                C, m, p, lower, upper, mask, packed, packed_t, scale, status,
                                u32(MF_STATUS_WEIGHT));
+    } else if (gc == 1 && (kp + 255) / 256 <= 65535) {
+        // Tall column groups: maxima reduced along the rows, then codes in 256-row chunks.
+        if (!work) return fail(MF_E_INVALID, "grouped weight quantization needs a work buffer");
+        hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);
+        launch_group_max_f32(b, k, o, ld, gr, gc, ncg, work, status, u32(MF_STATUS_WEIGHT), s);
+        hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
+                           nrg * ncg, upper, scale);
+        if (cfg->cols % 64 == 0 && R % 128 == 0 && kp % 16 == 0 && kp / 128 <= 65535) {
+            // The LDS tile of 32-row groups, each row taking its group's scale.
+            const dim3 grid{unsigned(op / 64), unsigned(kp / 128), 1u};
+            hipLaunchKernelGGL((k_col_groups_tile<32, true>), grid, dim3(256), 0, s, b, k, o, ld, R,
+                               C, m, p, lower, upper, mask, packed, packed_t, scale, gr, status,
+                               u32(MF_STATUS_WEIGHT));
+        } else {
+            const dim3 grid{unsigned((op + 255) / 256), unsigned((kp + 255) / 256), 1u};
+            if (kp % 4 == 0)
+                hipLaunchKernelGGL(k_col_codes<true>, grid, dim3(256), 0, s, b, k, o, ld, gr,
+                                   i64(256), R, C, m, p, scale, lower, upper, mask, packed,
+                                   packed_t);
+            else
+                hipLaunchKernelGGL(k_col_codes<false>, grid, dim3(256), 0, s, b, k, o, ld, gr,
+                                   i64(256), R, C, m, p, scale, lower, upper, mask, packed,
+                                   packed_t);
+        }
     } else {
         if (!work) return fail(MF_E_INVALID, "grouped weight quantization needs a work buffer");
         hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work, nrg * ncg, 0u);

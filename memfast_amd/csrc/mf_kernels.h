@@ -211,10 +211,10 @@ template <int GR, bool WORD>
 __global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
                                  i64 p, float lower, float upper, u32 mask, u8 *packed,
                                  u8 *packed_t, float *scale, u32 *status, u32 flag);
-template <int GR>
-__global__ void k_col_groups_tile(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
-                                  i64 p, float lower, float upper, u32 mask, u8 *packed,
-                                  u8 *packed_t, float *scale, u32 *status, u32 flag);
+template <int GR, bool GIVEN>
+__global__ void k_col_groups_tile(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m, i64 p,
+                                  float lower, float upper, u32 mask, u8 *packed, u8 *packed_t,
+                                  float *scale, i64 gr, u32 *status, u32 flag);
 template <bool WORD>
 __global__ void k_col_groups(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 span, int R,
                              int C, i64 m, i64 p, float lower, float upper, u32 mask,
@@ -236,6 +236,10 @@ __global__ void k_weight_codes(const float *b, i64 k, i64 o, i64 ld, int R, int 
                                float upper, u32 mask, u8 *packed, u8 *packed_t);
 __global__ void k_weight_scales(i64 k, i64 o, i64 groups, i64 op, int R, int P, int Gr,
                                 const float *scale, i64 gr, i64 gc, i64 ncg, float *wscale);
+template <bool WORD>
+__global__ void k_col_codes(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 span, int R, int C,
+                            i64 m, i64 p, const float *scale, float lower, float upper, u32 mask,
+                            u8 *packed, u8 *packed_t);
 __global__ void k_transpose_packed(const u8 *packed, int R, int C, i64 m, i64 p, u8 *packed_t);
 __global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
                                 i64 ncg, u64 *work, u32 *status, u32 flag);

@@ -303,10 +303,12 @@ __global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, in
 // 64-byte row segments of packed [m, p, R, C] and 4*GR-byte column runs of
 // packed_t [p*C, m*R], 16 bytes per store.  Requires C % 64 == 0, R % (4*GR)
 // == 0 (row segments stay inside one array tile) and kp % 16 == 0.
-template <int GR>
+// GIVEN: the group scales [ceil(k/gr), o] are already in `scale` (any gr, from
+// a separate group-maximum pass); each row takes its group's scale.
+template <int GR, bool GIVEN>
 __global__ __launch_bounds__(256) void k_col_groups_tile(
     const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m, i64 p, float lower, float upper,
-    u32 mask, u8 *packed, u8 *packed_t, float *scale, u32 *status, u32 flag) {
+    u32 mask, u8 *packed, u8 *packed_t, float *scale, i64 gr, u32 *status, u32 flag) {
     constexpr int ROWS = 4 * GR;
     __shared__ __align__(16) u8 tile_rc[ROWS][64 + 16];   // row-major codes
     __shared__ __align__(16) u8 tile_cr[64][ROWS + 16];   // column-major codes
@@ -322,21 +324,38 @@ __global__ __launch_bounds__(256) void k_col_groups_tile(
         const i64 row = r0 + i;
         v[i] = (live && row < k) ? b[row * ld + col] : 0.0f;
     }
-    float peak = 0.0f;
     bool finite = true;
+    if (GIVEN) {
+        i64 g = r0 / gr, boundary = (g + 1) * gr;
+        float sc = (live && r0 < k) ? scale[g * o + col] : 1.0f;
 #pragma unroll
-    for (int i = 0; i < GR; ++i) {
-        const float a = fabsf(v[i]);
-        finite = finite && a <= FLT_MAX;
-        peak = fmaxf(peak, a);
-    }
-    const float sc = group_scale(peak, upper);
-    if (live && r0 < k) scale[(r0 / GR) * o + col] = sc;
+        for (int i = 0; i < GR; ++i) {
+            const i64 row = r0 + i;
+            if (live && row < k && row >= boundary) {
+                g = row / gr;
+                boundary = (g + 1) * gr;
+                sc = scale[g * o + col];
+            }
+            const u8 code = (live && row < k) ? quantize_code(v[i], sc, lower, upper, mask) : u8(0);
+            tile_rc[wave * GR + i][lane] = code;
+            tile_cr[lane][wave * GR + i] = code;
+        }
+    } else {
+        float peak = 0.0f;
 #pragma unroll
-    for (int i = 0; i < GR; ++i) {
-        const u8 code = (live && r0 + i < k) ? quantize_code(v[i], sc, lower, upper, mask) : u8(0);
-        tile_rc[wave * GR + i][lane] = code;
-        tile_cr[lane][wave * GR + i] = code;
+        for (int i = 0; i < GR; ++i) {
+            const float a = fabsf(v[i]);
+            finite = finite && a <= FLT_MAX;
+            peak = fmaxf(peak, a);
+        }
+        const float sc = group_scale(peak, upper);
+        if (live && r0 < k) scale[(r0 / GR) * o + col] = sc;
+#pragma unroll
+        for (int i = 0; i < GR; ++i) {
+            const u8 code = (live && r0 + i < k) ? quantize_code(v[i], sc, lower, upper, mask) : u8(0);
+            tile_rc[wave * GR + i][lane] = code;
+            tile_cr[lane][wave * GR + i] = code;
+        }
     }
     __syncthreads();
     // packed: ROWS rows x 64 bytes = 4 x 16-byte chunks per row.
@@ -361,10 +380,14 @@ __global__ __launch_bounds__(256) void k_col_groups_tile(
     }
     if (!finite && status) atomicOr(status, flag);
 }
-template __global__ void k_col_groups_tile<16>(const float *, i64, i64, i64, int, int, i64, i64,
-                                               float, float, u32, u8 *, u8 *, float *, u32 *, u32);
-template __global__ void k_col_groups_tile<32>(const float *, i64, i64, i64, int, int, i64, i64,
-                                               float, float, u32, u8 *, u8 *, float *, u32 *, u32);
+#define MF_COL_TILE_INST(GR, GIVEN)                                                             \
+    template __global__ void k_col_groups_tile<GR, GIVEN>(const float *, i64, i64, i64, int, int, \
+                                                          i64, i64, float, float, u32, u8 *, u8 *,  \
+                                                          float *, i64, u32 *, u32);
+MF_COL_TILE_INST(16, false)
+MF_COL_TILE_INST(32, false)
+MF_COL_TILE_INST(32, true)
+#undef MF_COL_TILE_INST
 
 #define MF_COL_REG_INST(GR, WORD)                                                               \
     template __global__ void k_col_groups_reg<GR, WORD>(const float *, i64, i64, i64, int, int, \
@@ -441,6 +464,65 @@ template __global__ void k_col_groups<true>(const float *, i64, i64, i64, i64, i
 template __global__ void k_col_groups<false>(const float *, i64, i64, i64, i64, i64, int, int, i64,
                                              i64, float, float, u32, u8 *, u8 *, float *, u32 *,
                                              u32);
+
+// Codes of column-local groups (gc == 1) from precomputed group scales
+// [ceil(k/gr), o] (any gr): the layout of k_col_groups with rows in chunks of
+// `span` (a multiple of 4) independent of the group size.
+template <bool WORD>
+__global__ void k_col_codes(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 span, int R, int C,
+                            i64 m, i64 p, const float *scale, float lower, float upper, u32 mask,
+                            u8 *packed, u8 *packed_t) {
+    const i64 kp = m * R, op = p * C;
+    const i64 col = i64(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (col >= op) return;
+    const i64 r0 = i64(blockIdx.y) * span;
+    const i64 r1 = (r0 + span) < kp ? (r0 + span) : kp;
+    if (r0 >= r1) return;
+    const i64 t = col / C, c = col - t * C;
+    i64 tile = r0 / R, r = r0 - tile * R;   // packed coordinates of the current row
+    u8 *column_t = packed_t ? packed_t + col * kp : nullptr;
+    u32 word = 0;
+    auto put = [&](i64 row, u8 code) {
+        packed[((tile * p + t) * R + r) * C + c] = code;
+        if (++r == R) { r = 0; ++tile; }
+        if (column_t) {
+            if (WORD) {
+                word |= u32(code) << (8 * (row & 3));
+                if ((row & 3) == 3) {
+                    *reinterpret_cast<u32 *>(column_t + row - 3) = word;
+                    word = 0;
+                }
+            } else {
+                column_t[row] = code;
+            }
+        }
+    };
+    const bool live_col = col < o;
+    const i64 live = live_col ? (r1 < k ? r1 : k) : r0;   // rows with data: [r0, live)
+    i64 g = r0 / gr, boundary = (g + 1) * gr;
+    float s = live_col && r0 < live ? scale[g * o + col] : 1.0f;
+    // Four rows per step: independent loads in flight.
+    for (i64 row = r0; row < r1; row += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = row + u < live ? b[(row + u) * ld + col] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const i64 rr = row + u;
+            if (rr >= r1) break;
+            if (rr < live && rr >= boundary) {
+                g = rr / gr;
+                boundary = (g + 1) * gr;
+                s = scale[g * o + col];
+            }
+            put(rr, rr < live ? quantize_code(v[u], s, lower, upper, mask) : u8(0));
+        }
+    }
+}
+template __global__ void k_col_codes<true>(const float *, i64, i64, i64, i64, i64, int, int, i64,
+                                           i64, const float *, float, float, u32, u8 *, u8 *);
+template __global__ void k_col_codes<false>(const float *, i64, i64, i64, i64, i64, int, int, i64,
+                                            i64, const float *, float, float, u32, u8 *, u8 *);
 
 // q [n, kp] with kp = m*R; columns >= k are zero padding.
 __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
@@ -769,7 +851,20 @@ __global__ __launch_bounds__(256) void k_col_group_max(const T *x, i64 rows, i64
         const i64 hi = ((g + 1) * gr) < r1 ? ((g + 1) * gr) : r1;
         U best = 0;
         if (c < cols) {
-            for (i64 r = lo + ty; r < hi; r += 4) {
+            i64 r = lo + ty;
+            // Four rows per step: independent loads in flight.
+            for (; r + 12 < hi; r += 16) {
+                T v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = fabs(x[(r + 4 * u) * ld + c]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    finite = finite && v[u] <= AbsBits<T>::LARGEST;
+                    const U bits = U(AbsBits<T>::of(v[u]));
+                    best = bits > best ? bits : best;
+                }
+            }
+            for (; r < hi; r += 4) {
                 const T v = fabs(x[r * ld + c]);
                 finite = finite && v <= AbsBits<T>::LARGEST;
                 const U bits = U(AbsBits<T>::of(v));

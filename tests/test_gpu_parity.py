@@ -835,6 +835,24 @@ def test_narrow_group_quantizers_bit_exact(hip_device, wgran, igran):
     assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
 
 
+@pytest.mark.parametrize("wgran", [(None, 1), (384, 1), (1024, 1)])
+def test_tall_weight_groups_on_array_tiles_bit_exact(hip_device, wgran):
+    """Tall column groups on 128x128 arrays (group maxima first, then the LDS code tile
+    with each row's group scale) -> packed codes and scales identical to the oracle's."""
+    say("tall weight groups", wgran)
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                 weight_slice=(1, 1, 2, 2, 2), array_size=(128, 128), rows_per_read=32,
+                 adc_bits=8, weight_quant_gran=wgran, input_quant_gran=(1, 32))
+    gen = torch.Generator().manual_seed(47)
+    b = torch.randn(1500, 200, generator=gen) * 0.02
+    b[700, 3] = 5.0
+    b[1499, :] = -1.0
+    packed, codes_t, ws = hip.weight_tiles(b.T.to(hip_device), cfg)
+    packed_ref, ws_ref = oracle.weight_tiles(b.T, cfg)
+    assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
+    assert bits_equal(codes_t, packed_columns(packed_ref))
+
+
 def test_noisy_mfma_unsplit_epilogue(hip_device):
     """A grid of 512 blocks or more keeps the fused single-kernel read (no read split):
     its output is the reference epilogue of the kernel's own totals, bit for bit."""
