@@ -649,18 +649,48 @@ int launch_general(const mf_config *cfg, const GeneralArgs &args, int out_kind, 
 
 // Group maxima |x| into work[row group][col group] (cleared): column groups and
 // wide row groups by chunked reductions with few atomics, others elementwise.
+static void launch_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
+                               i64 gr, i64 gc, i64 ncg, int fixed, float lower, float upper,
+                               u32 mask, u8 *q, hipStream_t s) {
+    const bool vec = k % 4 == 0 && kp % 4 == 0 && ld % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(q) % 4 == 0;
+    if (vec) {
+        const i64 quads = n * (kp / 4);
+        const unsigned grid = grid_for(quads);
+        const i64 limit = i64(1) << 31;
+        if (quads + i64(grid) * 256 < limit && kp < limit && gr < limit && gc < limit)
+            hipLaunchKernelGGL(k_input_codes4<u32>, dim3(grid), dim3(256), 0, s, x, n, k, ld, kp,
+                               scale, gr, gc, ncg, fixed, lower, upper, mask, q);
+        else
+            hipLaunchKernelGGL(k_input_codes4<i64>, dim3(grid), dim3(256), 0, s, x, n, k, ld, kp,
+                               scale, gr, gc, ncg, fixed, lower, upper, mask, q);
+    } else {
+        hipLaunchKernelGGL(k_input_codes, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
+                           scale, gr, gc, ncg, fixed, lower, upper, mask, q);
+    }
+}
+
 static void launch_group_max_f32(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
                                  i64 ncg, u32 *work, u32 *status, u32 flag, hipStream_t s) {
     const i64 chunks = (rows + COL_CHUNK_ROWS - 1) / COL_CHUNK_ROWS;
     const i64 row_chunks = (cols + ROW_CHUNK_COLS - 1) / ROW_CHUNK_COLS;
+    const bool vec_ok = cols % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (gr == 1 && gc >= 64 && (rows + 3) / 4 <= 65535 && row_chunks <= 2147483647) {
         hipLaunchKernelGGL((k_row_group_max<float, u32>),
                            dim3(unsigned(row_chunks), unsigned((rows + 3) / 4)), dim3(256), 0, s, x,
                            rows, cols, ld, gc, ncg, work, status, flag);
+    } else if ((gr > 1 || gc == 1) && vec_ok && (cols + 63) / 64 <= 2147483647 &&
+               (rows + COL_CHUNK_ROWS_VEC - 1) / COL_CHUNK_ROWS_VEC <= 65535) {
+        hipLaunchKernelGGL((k_col_group_max<float, u32, 4>),
+                           dim3(unsigned((cols + 255) / 256),
+                                unsigned((rows + COL_CHUNK_ROWS_VEC - 1) / COL_CHUNK_ROWS_VEC)),
+                           dim3(256), 0, s, x, rows, cols, ld, gr, gc, ncg, i64(COL_CHUNK_ROWS_VEC),
+                           work, status, flag);
     } else if ((gr > 1 || gc == 1) && (cols + 63) / 64 <= 2147483647 && chunks <= 65535) {
-        hipLaunchKernelGGL((k_col_group_max<float, u32>),
+        hipLaunchKernelGGL((k_col_group_max<float, u32, 1>),
                            dim3(unsigned((cols + 63) / 64), unsigned(chunks)), dim3(256), 0, s, x,
-                           rows, cols, ld, gr, gc, ncg, work, status, flag);
+                           rows, cols, ld, gr, gc, ncg, i64(COL_CHUNK_ROWS), work, status, flag);
     } else {
         hipLaunchKernelGGL(k_group_max, dim3(grid_for(rows * ((cols + 7) / 8))), dim3(256), 0, s, x,
                            rows, cols, ld, gr, gc, ncg, work, status, flag);
@@ -708,8 +738,7 @@ int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, i
     const float upper = float((1 << (bits - 1)) - 1);
     const u32 mask = (1u << bits) - 1u;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(k_input_codes, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
-                       scale, i64(1), i64(1), k, 1, -upper, upper, mask, q);
+    launch_input_codes(x, n, k, ld, kp, scale, 1, 1, k, 1, -upper, upper, mask, q, s);
     hipLaunchKernelGGL(k_input_scales, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k, m * Gr,
                        R, P, Gr, scale, i64(1), i64(1), k, 1, xscale);
     return check_launch("input tiles");
@@ -829,8 +858,7 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
         launch_group_max_f32(x, n, k, ld, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT), s);
         hipLaunchKernelGGL(k_group_scale, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
                            nrg * ncg, upper, scale);
-        hipLaunchKernelGGL(k_input_codes, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
-                           scale, gr, gc, ncg, 0, -upper, upper, mask, q);
+        launch_input_codes(x, n, k, ld, kp, scale, gr, gc, ncg, 0, -upper, upper, mask, q, s);
     }
     hipLaunchKernelGGL(k_input_scales, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k, m * Gr, R,
                        P, Gr, scale, gr, gc, ncg, 0, xscale);
@@ -1261,14 +1289,22 @@ static void launch_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i6
     const i64 chunks = (rows + COL_CHUNK_ROWS - 1) / COL_CHUNK_ROWS;
     const i64 row_chunks = (cols + ROW_CHUNK_COLS - 1) / ROW_CHUNK_COLS;
     unsigned long long *w = reinterpret_cast<unsigned long long *>(work);
+    const bool vec_ok = cols % 2 == 0 && ld % 2 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (gr == 1 && gc >= 64 && (rows + 3) / 4 <= 65535 && row_chunks <= 2147483647) {
         hipLaunchKernelGGL((k_row_group_max<double, unsigned long long>),
                            dim3(unsigned(row_chunks), unsigned((rows + 3) / 4)), dim3(256), 0, s, x,
                            rows, cols, ld, gc, ncg, w, status, flag);
+    } else if ((gr > 1 || gc == 1) && vec_ok && (cols + 63) / 64 <= 2147483647 &&
+               (rows + COL_CHUNK_ROWS_VEC - 1) / COL_CHUNK_ROWS_VEC <= 65535) {
+        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long, 2>),
+                           dim3(unsigned((cols + 127) / 128),
+                                unsigned((rows + COL_CHUNK_ROWS_VEC - 1) / COL_CHUNK_ROWS_VEC)),
+                           dim3(256), 0, s, x, rows, cols, ld, gr, gc, ncg, i64(COL_CHUNK_ROWS_VEC),
+                           w, status, flag);
     } else if ((gr > 1 || gc == 1) && (cols + 63) / 64 <= 2147483647 && chunks <= 65535) {
-        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long>),
+        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long, 1>),
                            dim3(unsigned((cols + 63) / 64), unsigned(chunks)), dim3(256), 0, s, x,
-                           rows, cols, ld, gr, gc, ncg, w, status, flag);
+                           rows, cols, ld, gr, gc, ncg, i64(COL_CHUNK_ROWS), w, status, flag);
     } else {
         hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(rows * cols)), dim3(256), 0, s, x, rows,
                            cols, ld, gr, gc, ncg, work, status, flag);

@@ -223,6 +223,10 @@ __global__ void k_group_scale(const u32 *work, i64 groups, float upper, float *s
 __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
                               i64 gr, i64 gc, i64 ncg, int fixed, float lower, float upper,
                               u32 mask, u8 *q);
+template <typename I>
+__global__ void k_input_codes4(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
+                               i64 gr, i64 gc, i64 ncg, int fixed, float lower, float upper,
+                               u32 mask, u8 *q);
 constexpr int CONV_CHUNK_COLS = 128;   // patch columns per k_conv_codes block
 __global__ void k_conv_codes(const float *x, const mf_conv_geometry g, i64 K, i64 kp,
                              const float *scale, i64 gr, i64 gc, i64 ncg, float lower, float upper,
@@ -244,11 +248,13 @@ __global__ void k_transpose_packed(const u8 *packed, int R, int C, i64 m, i64 p,
 __global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
                                 i64 ncg, u64 *work, u32 *status, u32 flag);
 // Group maxima of |x| as bit patterns (U = u32 for float, unsigned long long for
-// double): reduced along rows first (any gr, gc), or along a row (gr == 1).
-template <typename T, typename U>
+// double): reduced along rows first (any gr, gc; V adjacent columns per lane),
+// or along a row (gr == 1).
+template <typename T, typename U, int V>
 __global__ void k_col_group_max(const T *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,
-                                U *work, u32 *status, u32 flag);
-constexpr int COL_CHUNK_ROWS = 256;   // rows per k_col_group_max block
+                                i64 chunk, U *work, u32 *status, u32 flag);
+constexpr int COL_CHUNK_ROWS = 256;   // rows per k_col_group_max block, one column per lane
+constexpr int COL_CHUNK_ROWS_VEC = 64;  // rows per block, 16 bytes of columns per lane
 template <typename T, typename U>
 __global__ void k_row_group_max(const T *x, i64 rows, i64 cols, i64 ld, i64 gc, i64 ncg, U *work,
                                 u32 *status, u32 flag);

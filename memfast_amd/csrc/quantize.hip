@@ -541,6 +541,53 @@ __global__ void k_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, cons
     }
 }
 
+// Four consecutive columns per thread: one 16-byte load and one 4-byte store.
+// Needs k % 4 == 0, kp % 4 == 0, ld % 4 == 0, a 16-byte aligned x and a 4-byte
+// aligned q.  I is the index type: u32 when n*kp/4 plus one grid stride, kp, gr
+// and gc all stay below 2^31, else i64.  The column group advances incrementally
+// over the four columns instead of a division per column.
+template <typename I>
+__global__ __launch_bounds__(256) void k_input_codes4(const float *x, i64 n, i64 k, i64 ld, i64 kp,
+                                                      const float *scale, i64 gr, i64 gc, i64 ncg,
+                                                      int fixed, float lower, float upper, u32 mask,
+                                                      u8 *q) {
+    const I kq = I(kp / 4), total = I(n) * kq;
+    const I group_rows = I(gr), group_cols = I(gc);
+    for (I e = I(blockIdx.x) * I(blockDim.x) + I(threadIdx.x); e < total;
+         e += I(gridDim.x) * I(blockDim.x)) {
+        const I row = e / kq, col = (e - row * kq) * 4;
+        u32 word = 0;
+        if (i64(col) < k) {
+            const float4 v = *reinterpret_cast<const float4 *>(x + i64(row) * ld + i64(col));
+            float sc[4];
+            if (fixed) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sc[j] = scale[i64(col) + j];
+            } else {
+                const float *srow = scale + i64(row / group_rows) * ncg;
+                I g = col / group_cols, rem = col - g * group_cols;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sc[j] = srow[g];
+                    if (++rem == group_cols) {
+                        ++g;
+                        rem = 0;
+                    }
+                }
+            }
+            word = u32(quantize_code(v.x, sc[0], lower, upper, mask)) |
+                   u32(quantize_code(v.y, sc[1], lower, upper, mask)) << 8 |
+                   u32(quantize_code(v.z, sc[2], lower, upper, mask)) << 16 |
+                   u32(quantize_code(v.w, sc[3], lower, upper, mask)) << 24;
+        }
+        *reinterpret_cast<u32 *>(q + i64(row) * kp + i64(col)) = word;
+    }
+}
+template __global__ void k_input_codes4<u32>(const float *, i64, i64, i64, i64, const float *, i64,
+                                             i64, i64, int, float, float, u32, u8 *);
+template __global__ void k_input_codes4<i64>(const float *, i64, i64, i64, i64, const float *, i64,
+                                             i64, i64, int, float, float, u32, u8 *);
+
 // ---- implicit im2col: input tiles of a convolution's patch matrix ----------
 // Patch row r = b * L + oh * wo + ow (L = ho * wo), column k = (c * kh + i) * kw + j
 // (F.unfold's order) holds x[b, c0 + c, oh*sh - ph + i*dh, ow*sw - pw + j*dw], or 0
@@ -826,68 +873,112 @@ template <> struct AbsBits<double> {
 };
 
 // Groups of gr rows x gc columns, reduced along the rows first: block = 64
-// columns x 4 row lanes over a chunk of COL_CHUNK rows (coalesced across the
-// columns).  Each thread keeps a running maximum while its rows stay in one row
-// group; LDS folds the four row lanes; then the 64 column maxima go to their
-// column groups: a wave maximum and one atomicMax when the block's columns lie
-// in one group, else one atomicMax per column.  work [ceil(rows/gr), ncg].
-constexpr int COL_CHUNK = COL_CHUNK_ROWS;
-template <typename T, typename U>
+// column lanes x 4 row lanes over a chunk of `chunk` rows; each column lane
+// covers V adjacent columns (V > 1: one 16-byte load per row, needs cols % V
+// == 0, ld % V == 0 and a 16-byte aligned x), so a wave reads 64*V*sizeof(T)
+// contiguous bytes per row.  Each thread keeps running maxima while its rows
+// stay in one row group; LDS folds the four row lanes; then the block's 64*V
+// column maxima go to their column groups: a block maximum and one atomicMax
+// when all its columns lie in one group, else a shuffle maximum over aligned
+// segments of `seg` columns (the largest power of two dividing gc, at most 64:
+// such a segment never crosses a group boundary) and one atomicMax per
+// segment.  work [ceil(rows/gr), ncg].
+template <typename T> struct __align__(16) Vec16 { T e[16 / sizeof(T)]; };
+template <typename T, typename U, int V>
 __global__ __launch_bounds__(256) void k_col_group_max(const T *x, i64 rows, i64 cols, i64 ld,
-                                                       i64 gr, i64 gc, i64 ncg, U *work,
-                                                       u32 *status, u32 flag) {
-    __shared__ U part[4][64];
+                                                       i64 gr, i64 gc, i64 ncg, i64 chunk,
+                                                       U *work, u32 *status, u32 flag) {
+    constexpr int BC = 64 * V;   // columns per block
+    __shared__ U part[4][BC];
+    __shared__ U wave_max[4];
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    const i64 c0 = i64(blockIdx.x) * 64;
-    const i64 c = c0 + tx;
-    const i64 r0 = i64(blockIdx.y) * COL_CHUNK;
-    const i64 r1 = (r0 + COL_CHUNK) < rows ? (r0 + COL_CHUNK) : rows;
-    const i64 c_last = (c0 + 63) < (cols - 1) ? (c0 + 63) : (cols - 1);
+    const i64 c0 = i64(blockIdx.x) * BC;
+    const i64 c = c0 + i64(tx) * V;
+    const i64 r0 = i64(blockIdx.y) * chunk;
+    const i64 r1 = (r0 + chunk) < rows ? (r0 + chunk) : rows;
+    const i64 c_last = (c0 + BC - 1) < (cols - 1) ? (c0 + BC - 1) : (cols - 1);
     const bool one_group = c0 / gc == c_last / gc;
+    const i64 low_bit = gc & -gc;
+    const int seg = low_bit < 64 ? int(low_bit) : 64;
     bool finite = true;
     // Row groups that intersect this chunk, handled one at a time (uniform loop).
     for (i64 g = r0 / gr; g * gr < r1; ++g) {
         const i64 lo = (g * gr) > r0 ? (g * gr) : r0;
         const i64 hi = ((g + 1) * gr) < r1 ? ((g + 1) * gr) : r1;
-        U best = 0;
+        U best[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) best[j] = 0;
         if (c < cols) {
             i64 r = lo + ty;
             // Four rows per step: independent loads in flight.
             for (; r + 12 < hi; r += 16) {
-                T v[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) v[u] = fabs(x[(r + 4 * u) * ld + c]);
+                Vec16<T> v[4];
+                T w[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    finite = finite && v[u] <= AbsBits<T>::LARGEST;
-                    const U bits = U(AbsBits<T>::of(v[u]));
-                    best = bits > best ? bits : best;
+                    if (V > 1) v[u] = *reinterpret_cast<const Vec16<T> *>(x + (r + 4 * u) * ld + c);
+                    else w[u] = x[(r + 4 * u) * ld + c];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                    for (int j = 0; j < V; ++j) {
+                        const T a = fabs(V > 1 ? v[u].e[j] : w[u]);
+                        finite = finite && a <= AbsBits<T>::LARGEST;
+                        const U bits = U(AbsBits<T>::of(a));
+                        best[j] = bits > best[j] ? bits : best[j];
+                    }
                 }
             }
             for (; r < hi; r += 4) {
-                const T v = fabs(x[r * ld + c]);
-                finite = finite && v <= AbsBits<T>::LARGEST;
-                const U bits = U(AbsBits<T>::of(v));
-                best = bits > best ? bits : best;
+                Vec16<T> v;
+                T w = 0;
+                if (V > 1) v = *reinterpret_cast<const Vec16<T> *>(x + r * ld + c);
+                else w = x[r * ld + c];
+#pragma unroll
+                for (int j = 0; j < V; ++j) {
+                    const T a = fabs(V > 1 ? v.e[j] : w);
+                    finite = finite && a <= AbsBits<T>::LARGEST;
+                    const U bits = U(AbsBits<T>::of(a));
+                    best[j] = bits > best[j] ? bits : best[j];
+                }
             }
         }
-        part[ty][tx] = best;
-        __syncthreads();
-        if (ty == 0) {
-            U m = part[0][tx];
-            m = part[1][tx] > m ? part[1][tx] : m;
-            m = part[2][tx] > m ? part[2][tx] : m;
-            m = part[3][tx] > m ? part[3][tx] : m;
-            if (one_group) {
 #pragma unroll
-                for (int d = 32; d >= 1; d >>= 1) {
-                    const U other = U(__shfl_xor(m, d, 64));
-                    m = other > m ? other : m;
-                }
-                if (tx == 0 && m) atomicMax(&work[g * ncg + c0 / gc], m);
-            } else if (c < cols && m) {
-                atomicMax(&work[g * ncg + c / gc], m);
+        for (int j = 0; j < V; ++j) part[ty][tx * V + j] = best[j];
+        __syncthreads();
+        // Thread t folds column c0 + t of the block (threads >= BC hold 0).
+        const int t = threadIdx.x;
+        U m = 0;
+        if (t < BC) {
+            m = part[0][t];
+            m = part[1][t] > m ? part[1][t] : m;
+            m = part[2][t] > m ? part[2][t] : m;
+            m = part[3][t] > m ? part[3][t] : m;
+        }
+        if (one_group) {
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) {
+                const U other = U(__shfl_xor(m, d, 64));
+                m = other > m ? other : m;
             }
+            if (tx == 0) wave_max[ty] = m;
+            __syncthreads();
+            if (t == 0) {
+                U b = wave_max[0];
+                b = wave_max[1] > b ? wave_max[1] : b;
+                b = wave_max[2] > b ? wave_max[2] : b;
+                b = wave_max[3] > b ? wave_max[3] : b;
+                if (b) atomicMax(&work[g * ncg + c0 / gc], b);
+            }
+        } else {
+            for (int d = seg >> 1; d >= 1; d >>= 1) {
+                const U other = U(__shfl_xor(m, d, 64));
+                m = other > m ? other : m;
+            }
+            const i64 col = c0 + t;
+            if (t < BC && (t & (seg - 1)) == 0 && col < cols && m)
+                atomicMax(&work[g * ncg + col / gc], m);
         }
         __syncthreads();
     }
@@ -929,12 +1020,14 @@ __global__ __launch_bounds__(256) void k_row_group_max(const T *x, i64 rows, i64
     if (!finite && status) atomicOr(status, flag);
 }
 
-template __global__ void k_col_group_max<float, u32>(const float *, i64, i64, i64, i64, i64, i64,
-                                                     u32 *, u32 *, u32);
-template __global__ void k_col_group_max<double, unsigned long long>(const double *, i64, i64, i64,
-                                                                     i64, i64, i64,
-                                                                     unsigned long long *, u32 *,
-                                                                     u32);
+template __global__ void k_col_group_max<float, u32, 1>(const float *, i64, i64, i64, i64, i64,
+                                                        i64, i64, u32 *, u32 *, u32);
+template __global__ void k_col_group_max<float, u32, 4>(const float *, i64, i64, i64, i64, i64,
+                                                        i64, i64, u32 *, u32 *, u32);
+template __global__ void k_col_group_max<double, unsigned long long, 1>(
+    const double *, i64, i64, i64, i64, i64, i64, i64, unsigned long long *, u32 *, u32);
+template __global__ void k_col_group_max<double, unsigned long long, 2>(
+    const double *, i64, i64, i64, i64, i64, i64, i64, unsigned long long *, u32 *, u32);
 template __global__ void k_row_group_max<float, u32>(const float *, i64, i64, i64, i64, i64, u32 *,
                                                      u32 *, u32);
 template __global__ void k_row_group_max<double, unsigned long long>(const double *, i64, i64, i64,
