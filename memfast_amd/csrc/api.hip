@@ -1031,7 +1031,7 @@ static bool ideal_extent_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     const i64 limit = 0x7FFFFFFF;
     return 128 * kp <= limit && G * ncols * 4 <= limit && 128 * G * 4 <= limit &&
-           (n + 63) / 64 <= 65535 && (ncols + 31) / 32 <= 65535;
+           (n + 63) / 64 + (ncols + 31) / 32 <= 65535;
 }
 
 static bool wide_plan_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
@@ -1131,12 +1131,12 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         const SliceLayout xl = layout_of(cfg->in_shift, cfg->in_mask, cfg->n_in);
         const SliceLayout wl = layout_of(cfg->w_shift, cfg->w_mask, cfg->n_w);
         const unsigned gblocks = unsigned((G + 63) / 64);
-        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((n + 63) / 64)),
-                           dim3(64 * DIGIT_WAVES), 0, s, q, n, kp, G, cfg->read_rows, xl, 64,
-                           xtests, xbits);
-        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned((ncols + 31) / 32)),
-                           dim3(64 * DIGIT_WAVES), 0, s, packed_t, ncols, kp, G, cfg->read_rows, wl,
-                           32, wtests, wbits);
+        const DigitJob xjob{q, n, 64, xl, xtests, xbits};
+        const DigitJob wjob{packed_t, ncols, 32, wl, wtests, wbits};
+        const i64 xblocks = (n + 63) / 64;
+        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned(xblocks + (ncols + 31) / 32)),
+                           dim3(64 * DIGIT_WAVES), 0, s, xjob, wjob, xblocks, kp, G,
+                           cfg->read_rows);
         IdealArgs args{};
         args.q = q;
         args.wt = packed_t;

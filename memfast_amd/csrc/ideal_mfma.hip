@@ -62,12 +62,19 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 // v_sad_u8 adds the four bytes.  Requires P in {32, 64} and reads that start
 // at g * P (R a multiple of P).
 __global__ __launch_bounds__(64 * DIGIT_WAVES) void k_digit_bits(
-    const u8 *codes, i64 rows, i64 kp, i64 G, int P, const SliceLayout layout, int block,
-    const SlotTests tests, uint64_t *out) {
+    const DigitJob a, const DigitJob b, i64 first_blocks, i64 kp, i64 G, int P) {
     __shared__ int partial[DIGIT_WAVES][8][64];
+    const bool second = i64(blockIdx.y) >= first_blocks;
+    const DigitJob &job = second ? b : a;
+    const u8 *codes = job.codes;
+    const i64 rows = job.rows;
+    const int block = job.block;
+    const SliceLayout &layout = job.layout;
+    const SlotTests &tests = job.tests;
+    uint64_t *out = job.out;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const i64 g = i64(blockIdx.x) * 64 + lane;
-    const i64 rb = blockIdx.y;
+    const i64 rb = second ? i64(blockIdx.y) - first_blocks : i64(blockIdx.y);
     const int S = layout.count;
     const int per = block / DIGIT_WAVES;
     int best[8] = {0, 0, 0, 0, 0, 0, 0, 0};

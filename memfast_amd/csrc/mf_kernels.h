@@ -87,11 +87,20 @@ struct SliceLayout {
 };
 
 // Per-read digit sums of every slice, maximized over blocks of `block` rows,
-// turned into the slot mask of `tests`: out[rb][g].
+// turned into the slot mask of `tests`: out[rb][g].  One launch serves both
+// sides: grid rows [0, first_blocks) take job `a` (the inputs), the rest job `b`
+// (the weight columns).
 constexpr int DIGIT_WAVES = 16;   // waves per k_digit_bits workgroup
-__global__ void k_digit_bits(const u8 *codes, i64 rows, i64 kp, i64 G, int P,
-                             const SliceLayout layout, int block, const SlotTests tests,
-                             uint64_t *out);
+struct DigitJob {
+    const u8 *codes;   // [rows, kp]
+    i64 rows;
+    int block;         // rows per maximum (32 or 64)
+    SliceLayout layout;
+    SlotTests tests;
+    uint64_t *out;     // [ceil(rows / block), G]
+};
+__global__ void k_digit_bits(const DigitJob a, const DigitJob b, i64 first_blocks, i64 kp, i64 G,
+                             int P);
 
 // ---- conductances (restore.hip) -------------------------------------------
 template <typename Phys, typename Code>

@@ -11,6 +11,7 @@ backward pass (when gradients are requested) uses the FP32 quantized-operand
 surrogate of memfast/nn/training.py.
 """
 
+import contextlib
 import itertools
 import weakref
 from pathlib import Path
@@ -145,10 +146,13 @@ def _matmul(a, b, *, simulator, config, mode, cache_dir, out):
         right = b.unsqueeze(-1) if right_vector else b
         if left.shape[-1] != right.shape[-2]:
             raise ValueError("A and B have incompatible reduction dimensions")
-        try:
-            batch = torch.broadcast_shapes(left.shape[:-2], right.shape[:-2])
-        except RuntimeError:
-            raise ValueError("A and B batch dimensions cannot broadcast") from None
+        if left.ndim == 2 and right.ndim == 2:
+            batch = torch.Size()
+        else:
+            try:
+                batch = torch.broadcast_shapes(left.shape[:-2], right.shape[:-2])
+            except RuntimeError:
+                raise ValueError("A and B batch dimensions cannot broadcast") from None
         rows, reduction, columns = left.shape[-2], left.shape[-1], right.shape[-1]
         shape = batch + (() if left_vector else (rows,)) + (() if right_vector else (columns,))
         _out(a, b, out, shape)
@@ -163,13 +167,20 @@ def _matmul(a, b, *, simulator, config, mode, cache_dir, out):
     )
     if not fused:
         _finite(a, b)
-    with torch.autocast(device_type=a.device.type, enabled=False):
+    # Autocast is switched off around the product; when it is already off the
+    # context would change nothing and is skipped.
+    autocast_off = (
+        torch.autocast(device_type=a.device.type, enabled=False)
+        if torch.is_autocast_enabled(a.device.type) else contextlib.nullcontext()
+    )
+    with autocast_off:
         if empty:
             result = a.new_zeros(shape)
             if torch.is_grad_enabled() and (a.requires_grad or b.requires_grad):
                 result = _SurrogateGradient.apply(result, torch.matmul(a.float(), b.float()))
         else:
-            left = left.expand(batch + (rows, reduction))
+            if batch:
+                left = left.expand(batch + (rows, reduction))
             rhs_batch = right.shape[:-2]
             if shared_rhs:
                 rhs = right if right.ndim == 2 else right.reshape(reduction, columns)

@@ -351,6 +351,24 @@ def _group_dims(shape, granularity):
 STATUS_INPUT, STATUS_WEIGHT, STATUS_OUTPUT = 1, 2, 4
 
 
+class _Scratch(ct.c_void_p):
+    """A device address inside a scratch tensor, which it keeps alive until the
+    launch that uses it has been queued (the caching allocator then orders any
+    reuse of the memory after the launch on the same stream)."""
+
+    __slots__ = ("owner",)
+
+
+def _group_scratch(groups, device):
+    """Group-maximum words and group scales (4 bytes each, ``groups`` of both)
+    in one allocation; the scales start at a 256-byte boundary."""
+    offset = -(-groups // 64) * 64
+    block = torch.empty(offset + groups, dtype=torch.int32, device=device)
+    work, scale = _Scratch(block.data_ptr()), _Scratch(block.data_ptr() + 4 * offset)
+    work.owner = scale.owner = block
+    return work, scale
+
+
 def status_word(device):
     """Zeroed device status word (int32) that kernels OR their MF_STATUS_* bits into."""
     return torch.zeros(1, dtype=torch.int32, device=device)
@@ -386,12 +404,10 @@ def input_tiles(value, config, fixed_scale=None, *, status=None):
     with _on(value.device):
         if fixed_scale is None:
             gr, gc = _group_dims(x.shape, config.input_quant_gran)
-            grid = (math.ceil(n / gr), math.ceil(k / gc))
-            scale = torch.empty(grid, dtype=torch.float32, device=value.device)
-            work = torch.empty(grid, dtype=torch.int32, device=value.device)
+            work, scale = _group_scratch(math.ceil(n / gr) * math.ceil(k / gc), value.device)
             check(
                 library().mf_quantize_inputs(
-                    descr, _ptr(x), n, k, k, gr, gc, _ptr(work), _ptr(scale), _ptr(q),
+                    descr, _ptr(x), n, k, k, gr, gc, work, scale, _ptr(q),
                     _ptr(xscale), _ptr(status), _stream(value.device),
                 ),
                 "input quantization",
@@ -527,16 +543,14 @@ def weight_tiles(weight, config, *, transposed=True, status=None):
     m, p = math.ceil(k / r), math.ceil(o / c)
     device = b.device
     gr, gc = _group_dims(b.shape, config.weight_quant_gran)
-    grid = (math.ceil(k / gr), math.ceil(o / gc))
-    scale = torch.empty(grid, dtype=torch.float32, device=device)
-    work = torch.empty(grid, dtype=torch.int32, device=device)
+    work, scale = _group_scratch(math.ceil(k / gr) * math.ceil(o / gc), device)
     packed = torch.empty((m, p, r, c), dtype=torch.uint8, device=device)
     packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=device) if transposed else None
     wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float32, device=device)
     with _on(device):
         check(
             library().mf_quantize_weights(
-                ct.byref(descriptor(config)), _ptr(b), k, o, o, gr, gc, _ptr(work), _ptr(scale),
+                ct.byref(descriptor(config)), _ptr(b), k, o, o, gr, gc, work, scale,
                 _ptr(packed), _ptr(packed_t), _ptr(wscale), _ptr(status), _stream(device),
             ),
             "weight quantization",

@@ -17,6 +17,7 @@ import math
 import time
 import weakref
 from dataclasses import asdict
+from functools import lru_cache
 from pathlib import Path
 
 import torch
@@ -231,7 +232,7 @@ class Simulator:
         if speculative:
             out_features = matrix.shape[1]
             p = math.ceil(out_features / config.array_size[1])
-            tag = int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little")
+            tag = _name_tag(name)
             packed, codes, wscale = tiles
             output = hip.mm(q, xscale, packed, codes if hip.mm_kernel(
                 config, q.shape[0], q.shape[1], p) or config.wide else None,
@@ -243,7 +244,13 @@ class Simulator:
             raise ValueError("A must be finite")
         if flags & hip.STATUS_WEIGHT:
             raise ValueError("B must be finite")
-        program = self._matrix_for(matrix, tiles=tiles)
+        if reused is not None:
+            # The program _matrix_for would keep (same tensor, metadata, config,
+            # device and tile shapes, as _program_plan checked): install in place.
+            reused._install(tiles)
+            program = reused
+        else:
+            program = self._matrix_for(matrix, tiles=tiles)
         if not speculative:
             if program.input_scale is not None:
                 q, xscale = hip.input_tiles(flat, config, program.input_scale)
@@ -463,7 +470,7 @@ class AnalogMatrix(nn.Module):
         if self.bias is not None and not torch.isfinite(self.bias).all():
             raise ValueError("bias exceeds the reconstruction dtype")
         self._event = 0
-        tag = int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little")
+        tag = _name_tag(name)
         self.seed = self.config.seed ^ tag
         self._prepared = {}
         self._kernel_codes = None
@@ -473,8 +480,9 @@ class AnalogMatrix(nn.Module):
             self._kernel_codes = (self._codes_key(), packed_t)
 
     # -- kernel-side copy of the codes -------------------------------------
-    def _codes_key(self):
-        packed = self.packed
+    def _codes_key(self, packed=None):
+        if packed is None:
+            packed = self.packed
         return (packed.data_ptr(), packed._version, packed.device, tuple(packed.shape))
 
     def _column_codes(self):
@@ -486,18 +494,28 @@ class AnalogMatrix(nn.Module):
 
     def _accepts(self, tiles):
         packed, _, scale = tiles
+        buffers = self._buffers   # registered buffers, read without Module.__getattr__
+        current, current_scale = buffers["packed"], buffers["weight_scale"]
         return (
-            self.packed.dtype == packed.dtype and self.packed.shape == packed.shape
-            and self.weight_scale.dtype == scale.dtype and self.weight_scale.shape == scale.shape
-            and self.zero_correction is None and self.bias is None
+            current.dtype == packed.dtype and current.shape == packed.shape
+            and current_scale.dtype == scale.dtype and current_scale.shape == scale.shape
+            and buffers["zero_correction"] is None and buffers["bias"] is None
         )
 
     def _install(self, tiles):
-        """Take freshly quantized codes and scales of the same matrix (see _matrix_for)."""
+        """Take freshly quantized codes and scales of the same matrix (see _matrix_for).
+
+        ``packed`` and ``weight_scale`` are registered buffers (of the same
+        dtype and shape, as ``_accepts`` checked), replaced in place in the
+        buffer table; this is what attribute assignment does for a buffer.
+        """
         packed, packed_t, scale = tiles
-        self.packed = packed
-        self.weight_scale = scale
-        self._kernel_codes = (self._codes_key(), packed_t) if packed_t is not None else None
+        buffers = self._buffers
+        buffers["packed"] = packed
+        buffers["weight_scale"] = scale
+        self.__dict__["_kernel_codes"] = (
+            (self._codes_key(packed), packed_t) if packed_t is not None else None
+        )
 
     def set_input_scale(self, scale):
         """Fix symmetric activation scales for subsequent calls; None restores dynamic scales."""
@@ -784,6 +802,12 @@ class AnalogMatrix(nn.Module):
             raise FloatingPointError("nonfinite analog output")
         self._event += 1
         return output
+
+
+@lru_cache(maxsize=4096)
+def _name_tag(name):
+    """32-bit seed tag of a matrix name (first four bytes of its SHA-256, little-endian)."""
+    return int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little")
 
 
 def _comparable(config_dict):
