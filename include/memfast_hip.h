@@ -127,7 +127,10 @@ int mf_input_tiles(const mf_config *cfg, const float *x, int64_t n, int64_t k, i
  * followed by input_tiles :115-137): group-scale grid scale [ceil(n/gr), ceil(k/gc)],
  * codes q [n, m*R] and per-read scales xscale [n, m*Gr] in one call.  Row-local
  * groups (gr == 1) run one fused pass; other shapes need `work` (uint32, grid
- * sized).  status (may be NULL) receives MF_STATUS_INPUT for a non-finite x. */
+ * sized).  status (may be NULL) receives MF_STATUS_INPUT for a non-finite x.
+ * `scale` may equal `xscale` when every group is one read (gr == 1, gc ==
+ * read_rows, k == m*R): the grid is then the per-read table and no gather runs;
+ * any other aliasing is MF_E_INVALID. */
 int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ld,
                        int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *q,
                        float *xscale, uint32_t *status, void *stream);
@@ -136,7 +139,9 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
  * matrix (memfast/quantization.py:9-44 followed by weight_tiles :82-112):
  * scale grid, packed [m, p, R, C], packed_t [p*C, m*R] (may be NULL) and
  * wscale [m*Gr, p*C].  Column-local groups (gc == 1, gr <= 256) run one fused
- * pass; other shapes need `work`.  status receives MF_STATUS_WEIGHT. */
+ * pass; other shapes need `work`.  status receives MF_STATUS_WEIGHT.  `scale`
+ * may equal `wscale` when every group is one read of one column (gc == 1, gr
+ * == read_rows, k == m*R, o == p*C); any other aliasing is MF_E_INVALID. */
 int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t o, int64_t ld,
                         int64_t gr, int64_t gc, uint32_t *work, float *scale, uint8_t *packed,
                         uint8_t *packed_t, float *wscale, uint32_t *status, void *stream);

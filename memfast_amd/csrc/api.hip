@@ -815,6 +815,12 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
     gr = gr < n ? gr : n;
     gc = gc < k ? gc : k;
     const i64 nrg = (n + gr - 1) / gr, ncg = (k + gc - 1) / gc;
+    // scale == xscale: groups of exactly one read and no padded reads make the
+    // group grid the per-read scale table itself, and the gather is skipped.
+    const bool direct = scale == xscale;
+    if (direct && !(gr == 1 && gc == P && kp == k))
+        return fail(MF_E_INVALID, "scale may alias xscale only for groups of one read "
+                                  "(gr == 1, gc == read rows, k == m*R)");
     const int bits = cfg->activation_bits;
     const float upper = float((1 << (bits - 1)) - 1);
     const u32 mask = (1u << bits) - 1u;
@@ -860,8 +866,9 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
                            nrg * ncg, upper, scale);
         launch_input_codes(x, n, k, ld, kp, scale, gr, gc, ncg, 0, -upper, upper, mask, q, s);
     }
-    hipLaunchKernelGGL(k_input_scales, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k, m * Gr, R,
-                       P, Gr, scale, gr, gc, ncg, 0, xscale);
+    if (!direct)
+        hipLaunchKernelGGL(k_input_scales, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
+                           m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
     return check_launch("input quantization");
 }
 
@@ -877,6 +884,12 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
     gr = gr < k ? gr : k;
     gc = gc < o ? gc : o;
     const i64 nrg = (k + gr - 1) / gr, ncg = (o + gc - 1) / gc;
+    // scale == wscale: column groups of exactly one read, no padded reads or
+    // columns: the group grid is the per-read scale table, no gather runs.
+    const bool direct = scale == wscale;
+    if (direct && !(gc == 1 && gr == P && kp == k && op == o))
+        return fail(MF_E_INVALID, "scale may alias wscale only for groups of one read "
+                                  "(gc == 1, gr == read rows, k == m*R, o == p*C)");
     const int bits = cfg->weight_bits;
     const float upper = float((1 << (bits - (cfg->weight_signed ? 1 : 0))) - 1);
     const float lower = cfg->weight_signed ? -upper : 0.0f;
@@ -959,8 +972,9 @@ int mf_quantize_weights(const mf_config *cfg, const float *b, int64_t k, int64_t
         hipLaunchKernelGGL(k_weight_codes, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o, ld, R,
                            C, m, p, scale, gr, gc, ncg, lower, upper, mask, packed, packed_t);
     }
-    hipLaunchKernelGGL(k_weight_scales, dim3(grid_for(m * Gr * op)), dim3(256), 0, s, k, o, m * Gr,
-                       op, R, P, Gr, scale, gr, gc, ncg, wscale);
+    if (!direct)
+        hipLaunchKernelGGL(k_weight_scales, dim3(grid_for(m * Gr * op)), dim3(256), 0, s, k, o,
+                           m * Gr, op, R, P, Gr, scale, gr, gc, ncg, wscale);
     return check_launch("weight quantization");
 }
 

@@ -359,6 +359,14 @@ class _Scratch(ct.c_void_p):
     __slots__ = ("owner",)
 
 
+def _work_words(groups, device):
+    """Group-maximum words alone (the scales go straight to the per-read table)."""
+    block = torch.empty(groups, dtype=torch.int32, device=device)
+    work = _Scratch(block.data_ptr())
+    work.owner = block
+    return work
+
+
 def _group_scratch(groups, device):
     """Group-maximum words and group scales (4 bytes each, ``groups`` of both)
     in one allocation; the scales start at a 256-byte boundary."""
@@ -404,7 +412,12 @@ def input_tiles(value, config, fixed_scale=None, *, status=None):
     with _on(value.device):
         if fixed_scale is None:
             gr, gc = _group_dims(x.shape, config.input_quant_gran)
-            work, scale = _group_scratch(math.ceil(n / gr) * math.ceil(k / gc), value.device)
+            groups = math.ceil(n / gr) * math.ceil(k / gc)
+            if gr == 1 and gc == config.read_rows and k == m * r:
+                # Groups of one read: the group grid is xscale itself.
+                work, scale = _work_words(groups, value.device), _ptr(xscale)
+            else:
+                work, scale = _group_scratch(groups, value.device)
             check(
                 library().mf_quantize_inputs(
                     descr, _ptr(x), n, k, k, gr, gc, work, scale, _ptr(q),
@@ -543,10 +556,15 @@ def weight_tiles(weight, config, *, transposed=True, status=None):
     m, p = math.ceil(k / r), math.ceil(o / c)
     device = b.device
     gr, gc = _group_dims(b.shape, config.weight_quant_gran)
-    work, scale = _group_scratch(math.ceil(k / gr) * math.ceil(o / gc), device)
+    groups = math.ceil(k / gr) * math.ceil(o / gc)
     packed = torch.empty((m, p, r, c), dtype=torch.uint8, device=device)
     packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=device) if transposed else None
     wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float32, device=device)
+    if gc == 1 and gr == config.read_rows and k == m * r and o == p * c:
+        # Groups of one read of one column: the group grid is wscale itself.
+        work, scale = _work_words(groups, device), _ptr(wscale)
+    else:
+        work, scale = _group_scratch(groups, device)
     with _on(device):
         check(
             library().mf_quantize_weights(

@@ -6,6 +6,7 @@ except rounding-boundary flips (<= 1e-4 of codes) and output relative error
 <= 1e-5 elsewhere (the BASELINE tolerance).
 """
 
+import ctypes as ct
 import math
 
 import numpy as np
@@ -851,6 +852,51 @@ def test_tall_weight_groups_on_array_tiles_bit_exact(hip_device, wgran):
     packed_ref, ws_ref = oracle.weight_tiles(b.T, cfg)
     assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
     assert bits_equal(codes_t, packed_columns(packed_ref))
+
+
+def test_groups_of_one_read_share_the_scale_tables(hip_device):
+    """Input groups (1, P) and weight groups (P, 1) with no padded reads or columns: the group
+    grids are written straight into xscale and wscale (no gather) -> identical to the oracle."""
+    say("groups of one read")
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                 weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,
+                 adc_bits=8, weight_quant_gran=(32, 1), input_quant_gran=(1, 32))
+    gen = torch.Generator().manual_seed(48)
+    a = torch.randn(40, 256, generator=gen)
+    a[7, 100] = 30.0
+    b = torch.randn(256, 96, generator=gen)
+    b[33, 5] = -9.0
+    q, xs = hip.input_tiles(a.to(hip_device), cfg)
+    packed, codes_t, ws = hip.weight_tiles(b.T.to(hip_device), cfg)
+    q_ref, xs_ref = oracle.input_tiles(a, cfg)
+    packed_ref, ws_ref = oracle.weight_tiles(b.T, cfg)
+    assert bits_equal(q, q_ref) and bits_equal(xs, xs_ref)
+    assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
+    assert bits_equal(codes_t, packed_columns(packed_ref))
+
+
+def test_scale_aliasing_outside_groups_of_one_read_is_rejected(hip_device):
+    """The C-ABI accepts scale == xscale / wscale only where the grid is the per-read table."""
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                 weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,
+                 adc_bits=8, weight_quant_gran=(32, 1), input_quant_gran=(1, 32))
+    descr = ct.byref(hip.descriptor(cfg))
+    lib = hip.library()
+    x = torch.zeros(4, 200, device=hip_device)   # k = 200: padded reads
+    q = torch.empty(4, 256, dtype=torch.uint8, device=hip_device)
+    xs = torch.empty(4, 8, device=hip_device)
+    work = torch.empty(64, dtype=torch.int32, device=hip_device)
+    rc = lib.mf_quantize_inputs(descr, hip._ptr(x), 4, 200, 200, 1, 32, hip._ptr(work),
+                                hip._ptr(xs), hip._ptr(q), hip._ptr(xs), None,
+                                hip._stream(hip_device))
+    assert rc == hip.E_INVALID and b"alias" in lib.mf_last_error()
+    w = torch.zeros(256, 90, device=hip_device)  # o = 90: padded columns
+    packed = torch.empty(4, 3, 64, 32, dtype=torch.uint8, device=hip_device)
+    ws = torch.empty(8, 96, device=hip_device)
+    rc = lib.mf_quantize_weights(descr, hip._ptr(w), 256, 90, 90, 32, 1, hip._ptr(work),
+                                 hip._ptr(ws), hip._ptr(packed), None, hip._ptr(ws), None,
+                                 hip._stream(hip_device))
+    assert rc == hip.E_INVALID and b"alias" in lib.mf_last_error()
 
 
 def test_noisy_mfma_unsplit_epilogue(hip_device):
