@@ -212,13 +212,16 @@ class _AnalogRecurrent(nn.Module):
                     steps = reversed(steps)
                 values = []
                 cell = self.cells[index]
+                # Read count of the input projection before this traversal (the
+                # batched projection below advances it by the number of steps).
+                start = cell.input._event
                 projected = self._projected_inputs(cell, sequence)
                 if projected is None:
                     for step in steps:
                         hidden = cell(sequence[step], hidden)
                         values.append(hidden)
                 else:
-                    matrix, start = cell.input, cell.input._event
+                    matrix = cell.input
                     for count, step in enumerate(steps):
                         try:
                             hidden = cell._step(projected[step], hidden)

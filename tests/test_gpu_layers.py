@@ -323,6 +323,26 @@ def test_gru_nonfinite_input_raises_at_its_step(hip_device):
     assert cell.input._event == 4 and cell.hidden._event == 4
 
 
+def test_gru_hidden_read_failure_leaves_per_step_read_counts(hip_device):
+    """A hidden read that fails at step 1 (its FP32 and FP64 results overflow FP32) raises
+    as in per-step reading, after two input reads and one hidden read.  Every hidden weight
+    is 3e38 and the input biases hold the update gate shut and the candidate at +1, so after
+    step 0 every hidden unit is about 1 and each hidden sum is about 64 * 3e38."""
+    cfg = config("write", input_quant_gran=(1, None))
+    torch.manual_seed(9)
+    source = nn.GRU(40, 64).to(hip_device)
+    with torch.no_grad():
+        source.weight_hh_l0.fill_(3e38)
+        source.bias_ih_l0[64:128] = -30.0
+        source.bias_ih_l0[128:] = 30.0
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    x = torch.randn(6, 2, 40, device=hip_device)
+    with pytest.raises(FloatingPointError):
+        layer(x)
+    cell = layer.cells[0]
+    assert cell.input._event == 2 and cell.hidden._event == 1
+
+
 def test_gru_gates_kernel_matches_torch_ops(hip_device):
     """mf_gru_gates equals PyTorch's separate elementwise gate ops on the GPU, bit for bit."""
     from memfast_amd import hip
