@@ -90,10 +90,12 @@ class AnalogRNNCell(nn.Module):
             return _SurrogateGradient.apply(analog, activation(value.float()))
         return analog
 
-    def _step(self, inputs, hx):
-        """One inference step given this step's input projection."""
+    def _step(self, inputs, hx, status=None):
+        """One inference step given this step's input projection (``status``: the
+        deferred status word of ``_AnalogRecurrent._deferred_steps``)."""
         activation = torch.tanh if self.nonlinearity == "tanh" else F.relu
-        return activation(inputs + self.hidden(hx))
+        hidden = self.hidden(hx) if status is None else self.hidden._forward_deferred(hx, status)
+        return activation(inputs + hidden)
 
 
 class AnalogGRUCell(nn.Module):
@@ -133,10 +135,11 @@ class AnalogGRUCell(nn.Module):
             return _SurrogateGradient.apply(analog, surrogate)
         return analog
 
-    def _step(self, inputs, hx):
+    def _step(self, inputs, hx, status=None):
         """One inference step given this step's input projection.  FP32 gates run as one
-        kernel with the same roundings as the elementwise ops of ``_gates``."""
-        hidden = self.hidden(hx)
+        kernel with the same roundings as the elementwise ops of ``_gates``.  ``status``:
+        the deferred status word of ``_AnalogRecurrent._deferred_steps``."""
+        hidden = self.hidden(hx) if status is None else self.hidden._forward_deferred(hx, status)
         if (inputs.ndim == 2 and inputs.dtype == hidden.dtype == hx.dtype == torch.float32
                 and inputs.stride(1) == hidden.stride(1) == hx.stride(1) == 1):
             return hip.gru_gates(inputs, hidden, hx)
@@ -210,6 +213,7 @@ class _AnalogRecurrent(nn.Module):
                 steps = range(sequence.shape[0])
                 if direction:
                     steps = reversed(steps)
+                steps = list(steps)
                 values = []
                 cell = self.cells[index]
                 # Read count of the input projection before this traversal (the
@@ -220,6 +224,8 @@ class _AnalogRecurrent(nn.Module):
                     for step in steps:
                         hidden = cell(sequence[step], hidden)
                         values.append(hidden)
+                elif (deferred := self._deferred_steps(cell, projected, steps, hidden)):
+                    values, hidden = deferred
                 else:
                     matrix = cell.input
                     for count, step in enumerate(steps):
@@ -249,6 +255,36 @@ class _AnalogRecurrent(nn.Module):
         output = sequence.transpose(0, 1) if self.batch_first else sequence
         return output, hidden
 
+
+    @staticmethod
+    def _deferred_steps(cell, projected, steps, hidden):
+        """The step loop with one status read for the whole traversal, or None.
+
+        Each hidden read ORs its status bits into one word (``_forward_deferred``),
+        so the reads queue without a host wait per step.  A clear word at the end
+        means every step read what a per-step read returns and nothing raised.
+        Otherwise the hidden projection's read count is restored and None makes
+        the caller redo the loop with a status read per step, which raises or
+        retries at the step where per-step reading does."""
+        matrix = cell.hidden
+        if not matrix._deferrable(hidden, len(steps)):
+            return None
+        start = matrix._event
+        status = hip.status_word(hidden.device)
+        values = []
+        try:
+            with torch.no_grad():   # as forward() of the hidden projection
+                for step in steps:
+                    hidden = cell._step(projected[step], hidden, status)
+                    values.append(hidden)
+            clear = int(status.item()) == 0
+        except Exception:
+            matrix._event = start
+            raise
+        if not clear:
+            matrix._event = start
+            return None
+        return values, hidden
 
     def _projected_inputs(self, cell, sequence):
         """All steps' input projections from one read, or None to read per step."""

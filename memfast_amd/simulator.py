@@ -634,13 +634,15 @@ class AnalogMatrix(nn.Module):
         return self._execute_checked(q, xscale, schedule, event, stable)[0]
 
     def _execute_checked(self, q, xscale, schedule, event, stable=False, status=None,
-                         input_error=None, retry=True):
+                         input_error=None, retry=True, defer=False):
         """(output, finite) where ``finite`` is True when the output is known finite.
 
         ``status`` may carry STATUS_INPUT from a deferred input quantization; the
         one status read raises ``input_error`` for it before anything else.  With
         ``retry`` False, a non-finite FP32 result returns (None, False) instead of
-        the FP64 retry (which changes every row's rounding)."""
+        the FP64 retry (which changes every row's rounding).  With ``defer`` the
+        status word is not read: the FP32 output returns as it is and the caller
+        reads ``status`` later (``_forward_deferred``)."""
         config = self.config
         c = config.array_size[1]
         if config.wide:
@@ -692,6 +694,8 @@ class AnalogMatrix(nn.Module):
             return output, False
         if fused_bias:
             hip.bias_add(output, self.bias, status)
+        if defer:
+            return output, True
         # One status read: deferred input check, then non-finite outputs.
         flags = int(status.item())
         if flags & hip.STATUS_INPUT:
@@ -773,6 +777,32 @@ class AnalogMatrix(nn.Module):
         q, xscale = hip.input_tiles(x.reshape(-1, self.in_features), self.config, self.input_scale,
                                     status=status)
         return self._run(x, q, xscale, status=status, retry=retry)
+
+    def _deferrable(self, x, reads):
+        """Whether ``reads`` reads of inputs like ``x`` can go through ``_forward_deferred``:
+        default mode, narrow FP32 reads with the bias added by the checking kernel."""
+        return (
+            self.simulator.mode == "default" and not self.config.wide
+            and self._buffers["zero_correction"] is None
+            and x.dtype == torch.float32 and x.ndim == 2 and x.shape[0] > 0
+            and x.shape[1] == self.in_features and x.device == self.simulator.device
+            and self.weight_scale.dtype == torch.float32 and self._event + reads < 2**63
+        )
+
+    def _forward_deferred(self, x, status):
+        """forward() for a ``_deferrable`` input that ORs its status bits into ``status``
+        and returns without reading it, so that reads can queue back to back.
+
+        When ``status`` is still clear after the last such read, every output
+        equals what forward() returns and no forward() would have raised.  When
+        any bit is set, the caller restores the read count and reads again
+        through forward(), which raises or retries exactly where it would have.
+        """
+        q, xscale = hip.input_tiles(x, self.config, self.input_scale, status=status)
+        output, _ = self._execute_checked(q, xscale, default_schedule(self.config), self._event,
+                                          status=status, defer=True)
+        self.__dict__["_event"] = self._event + 1
+        return output
 
     def _run(self, x, q, xscale, status=None, retry=True):
         """Read quantized inputs, cast, check and advance the event (simulator.py:632-646)."""
