@@ -33,11 +33,11 @@ HBM_PEAK_GBS = 8000.0
 
 # HBM bytes per launch of the read kernel on this workload, from two rocprofv3
 # --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the
-# same counters read for a 256 MiB device copy (FETCH x1.99968, WRITE x1.0):
-# 225.5 MiB read + 64.0 MiB written.  Summary and commands:
+# same counters read for a 256 MiB device copy (FETCH x1.99964, WRITE x1.0):
+# 226.9 MiB read + 64.0 MiB written.  Summary and commands:
 # profiles/k_ideal_config2_pmc.md.  Only valid for the kernel sources it was
 # measured on (hash prefix below); otherwise the bench reports null.
-MEASURED_TRAFFIC = dict(kernels="cb7710e236a74e26", bytes=303618385)
+MEASURED_TRAFFIC = dict(kernels="11680d3e295b2cfe", bytes=305103299)
 
 
 def cpu_model():
