@@ -347,6 +347,27 @@ def test_config2_full_size_rows(hip_device):
     assert bits_equal(out[rows.to(hip_device)], expected)
 
 
+def test_config2_full_size_permutation_equivariance(hip_device):
+    """BASELINE config 2 at full size, every row and column: with per-row input groups (1, 32)
+    and per-column weight groups (32, 1) an output element depends only on its row of A and
+    its column of B, so permuting A's rows and B's columns permutes the output, bit for bit."""
+    from memfast_amd import Simulator
+
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(136)
+    a = torch.randn(4096, 4096, generator=gen)
+    b = torch.randn(4096, 4096, generator=gen)
+    rows = torch.randperm(4096, generator=gen)
+    cols = torch.randperm(4096, generator=gen)
+    say("config2 4096^3 permutation equivariance")
+    out = Simulator(cfg, device=hip_device).mm(a.to(hip_device), b.to(hip_device))
+    permuted = Simulator(cfg, device=hip_device).mm(a[rows].to(hip_device),
+                                                    b[:, cols].contiguous().to(hip_device))
+    expected = out.cpu()[rows][:, cols]
+    assert bits_equal(permuted, expected)
+    assert not torch.equal(permuted.cpu(), out.cpu())   # the permutation moved values
+
+
 def test_functional_nonfinite_operands_leave_simulator_unchanged(hip_device):
     """The fused product checks finiteness on the device (functional.py:49-53 order)."""
     from memfast_amd import Simulator, mm
