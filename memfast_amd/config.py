@@ -151,6 +151,22 @@ class Config:
     bw_e: object = None
     weight_signed: bool = True
 
+    def __hash__(self):
+        """The hash of the field values (what the generated ``__hash__`` computes), kept after
+        the first call: the instance is frozen and the lookup caches keyed by it hash it on
+        every read."""
+        cached = self.__dict__.get("_hash")
+        if cached is None:
+            cached = hash(tuple(getattr(self, field.name) for field in fields(self)))
+            object.__setattr__(self, "_hash", cached)
+        return cached
+
+    def __getstate__(self):
+        # String hashes differ between processes: a pickled copy computes its own.
+        state = dict(self.__dict__)
+        state.pop("_hash", None)
+        return state
+
     def __post_init__(self):
         _check_int(self.activation_bits, "activation_bits", 2, 32)
         _check_int(self.weight_bits, "weight_bits", 2, 32)
