@@ -216,12 +216,21 @@ def _ptr(tensor):
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def _current_device():
+    """torch.cuda.current_device(), without its lazy-initialisation check once the HIP
+    runtime is up (every caller here already holds device tensors)."""
+    if _get_device is not None and torch.cuda.is_initialized():
+        return _get_device()
+    return torch.cuda.current_device()
 
 
 def _stream(device):
     """The current HIP stream of ``device`` as a pointer."""
     if _raw_stream is not None and isinstance(device, torch.device):
-        index = device.index if device.index is not None else torch.cuda.current_device()
+        index = device.index if device.index is not None else _current_device()
         return ct.c_void_p(_raw_stream(index))
     return ct.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
@@ -241,7 +250,7 @@ def _on(device):
     """torch.cuda.device(device), skipped when it is already the current device."""
     if not isinstance(device, torch.device):
         return torch.cuda.device(device)
-    if device.index is None or device.index == torch.cuda.current_device():
+    if device.index is None or device.index == _current_device():
         return _UNCHANGED
     return torch.cuda.device(device)
 
