@@ -29,15 +29,16 @@ BASE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
             weight_slice=(1, 1, 2, 2, 2), array_size=(128, 128), rows_per_read=32,
             weight_quant_gran=(32, 1), input_quant_gran=(1, 32), adc_bits=(6, 7, 7, 8, 8))
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, tera-ops/s
+FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, TFLOP/s (the noisy read's precision)
 HBM_PEAK_GBS = 8000.0
 
 # HBM bytes per launch of the read kernel on this workload, from two rocprofv3
 # --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the
-# same counters read for a 256 MiB device copy (FETCH x1.99964, WRITE x1.0):
-# 226.9 MiB read + 64.0 MiB written.  Summary and commands:
+# same counters read for a 256 MiB device copy (FETCH x1.99974, WRITE x1.0):
+# 227.3 MiB read + 64.0 MiB written.  Summary and commands:
 # profiles/k_ideal_config2_pmc.md.  Only valid for the kernel sources it was
 # measured on (hash prefix below); otherwise the bench reports null.
-MEASURED_TRAFFIC = dict(kernels="11680d3e295b2cfe", bytes=305103299)
+MEASURED_TRAFFIC = dict(kernels="9d7f452db651d630", bytes=305445809)
 
 
 def cpu_model():
@@ -296,10 +297,19 @@ def main():
             write_variation=0.02, read_variation=0.01, adc_nonlinearity=0.1))
         noisy_sim = memfast.Simulator(noisy_cfg, device=device)
         noisy_ms, noisy_kernel_ms = time_steps(lambda: noisy_sim.mm(a, b), args.noisy_steps, 1)
-        noisy = dict(ms_per_step=round(noisy_ms, 3), kernel_ms=round(noisy_kernel_ms, 3),
-                     value=round(macs / (noisy_ms * 1e-3) / 1e9, 3), unit="GMAC/s",
-                     config="write_variation=0.02, read_variation=0.01 shared, "
-                            "adc_nonlinearity=0.1")
+        noisy_achieved = 2 * slice_macs / (noisy_kernel_ms * 1e-3) / 1e12
+        noisy = dict(
+            ms_per_step=round(noisy_ms, 3), kernel_ms=round(noisy_kernel_ms, 3),
+            value=round(macs / (noisy_ms * 1e-3) / 1e9, 3), unit="GMAC/s",
+            config="write_variation=0.02, read_variation=0.01 shared, adc_nonlinearity=0.1",
+            roofline=dict(bound="mfma", achieved=round(noisy_achieved, 2), peak=FP16_PEAK_TFLOPS,
+                          unit="TFLOP/s", frac=round(noisy_achieved / FP16_PEAK_TFLOPS, 4),
+                          traffic=None,
+                          note="2 flops per slice-MAC (25 pairs) / k_noisy time (HIP events "
+                               "on its stream, the conductance split excluded); the hardware "
+                               "issues two fp16 MFMAs (hi and lo conductance terms) per "
+                               "slice-MAC, twice this count"),
+        )
 
     others = None if args.no_secondary else secondary(device)
 

@@ -433,6 +433,9 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         }
         const dim3 grid{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
         const bool nl = cfg->has_nonlinear != 0;
+        // Benchmark timing brackets the read kernel alone (not the conductance split).
+        std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
 #define MF_NOISY_LAUNCH(KS, NA)                                                                \
     {                                                                                          \
         if (nl)                                                                                \
@@ -444,6 +447,10 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         else if (cfg->n_in <= 5) MF_NOISY_LAUNCH(2, 5)
         else MF_NOISY_LAUNCH(2, 8)
 #undef MF_NOISY_LAUNCH
+        if (timing.first) {
+            hipEventRecord(timing.second, s);
+            g_profile.pending.push_back(timing);
+        }
     }
     if (use_split)
         hipLaunchKernelGGL(k_restore_sum_f32, dim3(grid_for(n * ocols)), dim3(256), 0, s, partial, n,
@@ -1195,17 +1202,9 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
     if (!g && packed_t && aligned && workspace && ideal_extent_ok(cfg, n, m, p) &&
         noisy_extent_ok(n, m, cfg) && build_noisy_plan(cfg, m, p, &noisy, &ks, &why) &&
         workspace_bytes >= 2 * noisy_block_bytes(cfg, m)) {
-        std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
-        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-        const int launched = launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p,
-                                          nullptr, seed, event, out, ldo, workspace,
-                                          workspace_bytes, 0, status, s,
-                                          (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run);
-        if (timing.first) {
-            hipEventRecord(timing.second, s);
-            g_profile.pending.push_back(timing);
-        }
-        return launched;
+        return launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p, nullptr, seed,
+                            event, out, ldo, workspace, workspace_bytes, 0, status, s,
+                            (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run);
     }
     if (!g && needs_conductances(cfg))
         return fail(MF_E_INVALID, "device noise needs restored conductances (g)");

@@ -23,7 +23,7 @@ from pathlib import Path
 import torch
 from torch import nn
 
-from . import hip
+from . import hip, host_order
 from .config import Config
 from .quantization import check_read_scales, expanded_parameter, pack_weight, read_starts
 
@@ -108,6 +108,7 @@ class Simulator:
         if torch.device(requested).type not in ("cpu", "cuda"):
             raise ValueError("device must be cpu or cuda")
         self.device = _hip_device(requested)
+        host_order.warn_if_different()
         self.cache_dir = Path(cache_dir) if cache_dir is not None else hip.cache_root() / "tuning"
         self.workspace_bytes = int(workspace_mb * 1024**2)
         self.records = []

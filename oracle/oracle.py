@@ -363,21 +363,27 @@ def restore_scales(value, input_scale, weight_scale):
 
 
 def execute(q, xscale, packed, wscale, cfg, seed, event, out_features, *, bias=None,
-            arrays=2, stable=False, conductance=None, totals=None):
+            arrays=2, stable=False, conductance=None, totals=None, tiles=None):
     """Fused epilogue of AnalogMatrix._execute (simulator.py:561-616).
 
     ``conductance`` (optional) is the full [m,p,W,R,C] injected tensor.
     ``totals`` (optional) supplies the slice totals [N, m*Gr, p, C] of every
     tile instead of computing them with ``partial`` (to check a kernel's
-    epilogue on its own totals).  Zero-point correction (map_quantized) is not
-    covered by the hot path.
+    epilogue on its own totals).  ``tiles`` = (begin, end), with ``begin`` a
+    multiple of ``arrays``, runs only the chunks of those tiles (same per-chunk
+    arithmetic, since each output column depends only on its own chunk) and
+    returns their [N, (end-begin)*C] columns, before bias and the FP64 retry.
+    Zero-point correction (map_quantized) is not covered by the hot path.
     """
     p = packed.shape[1]
     c = cfg.array_size[1]
     wide = is_wide(cfg) or stable
     output = torch.empty((q.shape[0], p * c), dtype=torch.float64 if wide else torch.float32)
     width = min(arrays, p)
-    for begin in range(0, p, width):
+    first, last = (0, p) if tiles is None else tiles
+    if first % width or not 0 <= first < last <= p:
+        raise ValueError("tiles must start on a chunk boundary and lie within [0, p]")
+    for begin in range(first, last, width):
         end = min(begin + width, p)
         injected = None if conductance is None else conductance[:, begin:end]
         if totals is not None:
@@ -390,6 +396,8 @@ def execute(q, xscale, packed, wscale, cfg, seed, event, out_features, *, bias=N
             value = value * xscale[:, :, None, None]
             value = value * wscale[None, :, begin:end, :]
         output[:, begin * c:end * c] = value.sum(1).flatten(1)
+    if tiles is not None:
+        return output[:, first * c:min(last, end) * c].contiguous()
     output = output[:, :out_features].contiguous()
     if bias is not None:
         output = output + bias

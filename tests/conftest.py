@@ -8,8 +8,9 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 GOLDEN = ROOT / "tests" / "golden"
-if str(ROOT) not in sys.path:
-    sys.path.insert(0, str(ROOT))
+for path in (ROOT, ROOT / "tests"):   # the package, oracle/ and the test helper modules
+    if str(path) not in sys.path:
+        sys.path.insert(0, str(path))
 
 
 def pytest_configure(config):

@@ -304,3 +304,93 @@ def test_dft_known_answer():
     # The notebook's own assertion; its recorded 9.537e-07 came from the CUDA path,
     # whose summation order differs from the CPU reference's.
     torch.testing.assert_close(actual, expected, rtol=1e-5, atol=2e-5)
+
+
+# ---------------------------------------------------------------------------
+# Flip accounting (oracle/flips.py) and chunked execution, pinned by planted mistakes
+# ---------------------------------------------------------------------------
+def _flip_case():
+    from oracle import flips  # noqa: F401
+
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                 weight_slice=(1, 1, 2, 2, 2), array_size=(32, 16), rows_per_read=16,
+                 adc_bits=(6, 7, 7, 8, 8), nonidealities=Nonidealities(write_variation=0.02))
+    gen = torch.Generator().manual_seed(61)
+    a = torch.randn(6, 70, generator=gen)
+    b = torch.randn(70, 40, generator=gen)
+    q, xs = oracle.input_tiles(a, cfg)
+    packed, ws = oracle.weight_tiles(b.T, cfg)
+    totals = oracle.partial(q, packed, cfg, 5, 0, 0, packed.shape[1])
+    out = oracle.execute(q, xs, packed, ws, cfg, 5, 0, 40, totals=totals)
+    return cfg, q, xs, packed, ws, totals, out
+
+
+def test_flip_accounting_accepts_one_planted_flip():
+    """One code of pair (a=1, w=2) moved by one count: one flip, one flagged output, the
+    output moved by exactly its effect, every other output unchanged."""
+    from oracle import flips
+
+    cfg, q, xs, packed, ws, totals, out = _flip_case()
+    fa, fw = cfg.input_layout[1][2], cfg.weight_layout[2][2]
+    moved = totals.clone()
+    moved[2, 3, 1, 5] += fa * fw
+    got = oracle.execute(q, xs, packed, ws, cfg, 5, 0, 40, totals=moved)
+    report = flips.check_noisy(cfg, got, out, moved, totals, xscale=xs, wscale=ws)
+    assert report["differing"] == 1 and report["flips"] == 1
+    assert report["flagged_outputs"] == 1 and report["clean_inexact"] == 0
+    assert got[2, 16 + 5] != out[2, 16 + 5]
+
+
+def test_flip_accounting_counts_multiple_flips_in_one_total():
+    from oracle import flips
+
+    cfg, *_, totals, _ = _flip_case()
+    factors = flips.pair_factors(cfg)
+    moved = totals.clone()
+    moved[0, 0, 0, 0] += factors[0] - factors[7] + factors[24]
+    _, count, unexplained, _ = flips.count_flips(cfg, moved, totals)
+    assert unexplained == 0 and count >= 2
+
+
+def test_flip_accounting_rejects_planted_mistakes():
+    """Planted in the oracle's own output: a difference no three single-count flips
+    explain, an unflipped output off by 1e-4, a flipped output that moved too far, and
+    more flips than the 1e-4 budget all fail."""
+    from oracle import flips
+
+    cfg, q, xs, packed, ws, totals, out = _flip_case()
+    bad = totals.clone()
+    bad[1, 1, 0, 1] += 7777
+    with pytest.raises(AssertionError, match="beyond three code flips"):
+        flips.check_noisy(cfg, out, out, bad, totals)
+    wrong = out.clone()
+    wrong[4, 7] *= 1 + 1e-4
+    with pytest.raises(AssertionError, match="1e-5 relative"):
+        flips.check_noisy(cfg, wrong, out, totals, totals)
+    moved = totals.clone()
+    moved[3, 2, 0, 9] += 1
+    far = oracle.execute(q, xs, packed, ws, cfg, 5, 0, 40, totals=moved)
+    far[3, 9] += 10 * abs(float(far[3, 9] - out[3, 9])) + 1e-3
+    with pytest.raises(AssertionError, match="more than their flips explain"):
+        flips.check_noisy(cfg, far, out, moved, totals, xscale=xs, wscale=ws)
+    many = totals.clone()
+    many[:, :, :, :] += 1
+    with pytest.raises(AssertionError, match="budget"):
+        flips.check_noisy(cfg, out, out, many, totals)
+
+
+def test_execute_tiles_equals_full_columns():
+    """oracle.execute(tiles=...) returns exactly the full product's columns of those tiles."""
+    cfg = Config(activation_bits=8, weight_bits=8, array_size=(32, 16), rows_per_read=16,
+                 adc_bits=8, nonidealities=Nonidealities(write_variation=0.02))
+    gen = torch.Generator().manual_seed(62)
+    a = torch.randn(5, 70, generator=gen)
+    b = torch.randn(70, 90, generator=gen)
+    q, xs = oracle.input_tiles(a, cfg)
+    packed, ws = oracle.weight_tiles(b.T, cfg)
+    full = oracle.execute(q, xs, packed, ws, cfg, 9, 2, 96)
+    for tiles in ((0, 2), (2, 4), (4, 6), (2, 3)):
+        part = oracle.execute(q, xs, packed, ws, cfg, 9, 2, 96, tiles=tiles)
+        assert torch.equal(part, full[:, tiles[0] * 16:tiles[1] * 16])
+    with pytest.raises(ValueError):
+        oracle.execute(q, xs, packed, ws, cfg, 9, 2, 96, tiles=(1, 3))

@@ -108,3 +108,37 @@ def test_large_read_counts():
         x = (torch.randn(1, groups, 64, generator=gen) * 1e3).float()
         np.testing.assert_array_equal(kernel_sum(x[0].numpy()).view(np.int32),
                                       x.sum(1)[0].numpy().view(np.int32))
+
+
+def test_host_capability_and_order_probe():
+    """Record this host's torch CPU capability and check the product's probe: torch's sum
+    here follows the cascade the kernels reproduce (memfast_amd/host_order.py)."""
+    from memfast_amd import host_order
+
+    capability = torch.backends.cpu.get_cpu_capability()
+    print("torch CPU capability:", capability)
+    assert host_order.sum_order_matches(), (
+        f"torch CPU sum order on this host ({capability}) differs from the kernels' cascade")
+    assert capability in host_order.VERIFIED_CAPABILITIES
+    # The product's restatement agrees with this file's incremental one, column by column.
+    values = host_order.probe_values()[0]
+    np.testing.assert_array_equal(host_order.cascade_sum(values).numpy().view(np.int32),
+                                  cascade_sum(values.numpy()).view(np.int32))
+
+
+def test_order_probe_rejects_planted_orders():
+    """A plain sequential sum and a cascade with another block size both differ from
+    torch's sum on the probe values, so a host with either layout would be flagged."""
+    from memfast_amd import host_order
+
+    values = host_order.probe_values()[0]
+    expected = values[None].sum(1)[0]
+    sequential = torch.zeros(values.shape[1])
+    for row in values:
+        sequential = sequential + row
+    assert not torch.equal(sequential, expected)
+    blocks = [values[i:i + 8].sum(0) for i in range(0, values.shape[0], 8)]
+    eights = torch.zeros(values.shape[1])
+    for block in blocks:
+        eights = eights + block
+    assert not torch.equal(eights, expected)
