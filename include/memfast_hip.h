@@ -197,6 +197,28 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
           float *out, int64_t ldo, void *workspace, int64_t workspace_bytes, int32_t variant,
           uint32_t *status, void *stream);
 
+/* No counterpart in the reference.  mf_mm for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same read, arguments and results, with the scratch that mf_mm
+ * takes as `workspace` drawn from a static device array of MF_STATIC_SCRATCH_BYTES
+ * that the library holds on each GPU it runs on until the process ends.  The call
+ * allocates nothing (no hipMalloc/hipFree; benchmark timing is off for it); its
+ * first call on a device looks the array's address up on that device.
+ *  - Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ *    (other streams or host threads) race.  Serialize them.
+ *  - Noisy reads sample their conductance terms on every call (MF_MM_REUSE_TERMS
+ *    is ignored) and run in column chunks that fit the array.
+ *  - A read whose least scratch exceeds the array (the ideal-device read's digit
+ *    masks, ceil(n/64)*G*8 + ceil(p*C/32)*G*8 bytes rounded up to 256; or one
+ *    64-column chunk of noisy conductance terms, 256*W*m*R bytes) fails with
+ *    MF_E_RESOURCE before launching anything. */
+#define MF_STATIC_SCRATCH_BYTES (64ll << 20)
+int mf_mm_static(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n,
+                 int64_t m, const uint8_t *packed, const uint8_t *packed_t, const float *wscale,
+                 int64_t p, int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed,
+                 uint64_t event, float *out, int64_t ldo, int32_t variant, uint32_t *status,
+                 void *stream);
+
 /* Bias of an FP32 read (memfast/simulator.py:612-613, `out + bias`): out[v, c]
  * += bias[c] for c < o, one FP32 add each; a non-finite sum sets
  * MF_STATUS_OUTPUT in status (may be NULL), which replaces the host-side

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -1236,6 +1237,93 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         hipEventRecord(timing.second, s);
         g_profile.pending.push_back(timing);
     }
+    return launched;
+}
+
+}  // extern "C"
+
+// Scratch of mf_mm_static: device memory the library holds on each GPU it runs
+// on (the code object's zero-initialised data, mapped when the module loads on
+// that device) until the process ends.  Host code never passes this name to a
+// kernel: on the host it is only a stand-in for the per-device address that
+// hipGetSymbolAddress returns, which static_scratch() records once per device.
+static __device__ __align__(256) unsigned char scratch[MF_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first call).
+int static_scratch(void **out) {
+    int device = -1;
+    const hipError_t got = hipGetDevice(&device);
+    if (got != hipSuccess) return fail(MF_E_HIP, "hipGetDevice: %s", hipGetErrorString(got));
+    if (device < 0 || device >= kMaxDevices)
+        return fail(MF_E_UNSUPPORTED, "device %d beyond the %d the static scratch serves", device,
+                    kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_lock);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(MF_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                        hipGetErrorString(e));
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return MF_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int mf_mm_static(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n,
+                 int64_t m, const uint8_t *packed, const uint8_t *packed_t, const float *wscale,
+                 int64_t p, int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed,
+                 uint64_t event, float *out, int64_t ldo, int32_t variant, uint32_t *status,
+                 void *stream) {
+    const int valid = check_narrow(cfg);
+    if (valid) return valid;
+    if (n < 1 || m < 1 || p < 1) return fail(MF_E_INVALID, "invalid mm arguments");
+    // The least scratch each read kernel can run in: the ideal kernel's digit masks,
+    // or one 64-column chunk of noisy conductance terms (mf_mm runs wider noisy
+    // reads chunk by chunk within the scratch it is given).
+    i64 need = 0;
+    const char *what = "";
+    IdealPlan plan;
+    SlotTests xt, wt;
+    NoisyPlan noisy;
+    int ks = 0;
+    const char *why = "";
+    if (!g && packed_t && build_ideal_plan(cfg, m, p, &plan, &xt, &wt, &ks, &why)) {
+        i64 xb = 0, wb = 0;
+        ideal_workspace(cfg, n, m, p, &xb, &wb);
+        need = xb + wb;
+        what = "digit masks of the ideal-device read";
+    } else if (!g && packed_t && build_noisy_plan(cfg, m, p, &noisy, &ks, &why)) {
+        need = 2 * noisy_block_bytes(cfg, m);
+        what = "one 64-column chunk of noisy conductance terms";
+    }
+    if (need > MF_STATIC_SCRATCH_BYTES)
+        return fail(MF_E_RESOURCE,
+                    "mf_mm_static needs %lld bytes of scratch for the %s; its static scratch "
+                    "holds %lld (MF_STATIC_SCRATCH_BYTES)",
+                    static_cast<long long>(need), what,
+                    static_cast<long long>(MF_STATIC_SCRATCH_BYTES));
+    void *ptr = nullptr;
+    const int found = static_scratch(&ptr);
+    if (found) return found;
+    // The scratch is shared by every call on this GPU, so it never holds this
+    // program's conductance terms from an earlier call: sample them again.
+    // Benchmark timing (hipEventCreate) stays off for the call.
+    variant &= ~MF_MM_REUSE_TERMS;
+    const bool profiling = g_profile.enabled;
+    g_profile.enabled = false;
+    const int launched = mf_mm(cfg, q, xscale, n, m, packed, packed_t, wscale, p, out_cols,
+                               k_rows, g, seed, event, out, ldo, ptr, MF_STATIC_SCRATCH_BYTES,
+                               variant, status, stream);
+    g_profile.enabled = profiling;
     return launched;
 }
 

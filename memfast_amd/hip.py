@@ -147,6 +147,8 @@ SIGNATURES = {
                     _P, _P, _P], ct.c_int),
     "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
                ct.c_uint64, _P, _I64, _P, _I64, _I32, _P, _P], ct.c_int),
+    "mf_mm_static": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
+                      ct.c_uint64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
                       _P], ct.c_int),
     "mf_bias_add": ([_P, _I64, _I64, _I64, _P, _P, _P], ct.c_int),
