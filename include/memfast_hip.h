@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 6
+#define MF_ABI_VERSION 7
 #define MF_MAX_SLICES 32
 
 enum {
@@ -176,14 +176,30 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
  * depend on the read event (no read variation); otherwise ignored. */
 #define MF_MM_REUSE_TERMS 0x100
 
+/* Schedule fields of the `variant` word of mf_mm, mf_mm_static and mf_mm_wide (the
+ * tuned mode's grid; memfast/simulator.py:27-45 holds the reference's).  Results
+ * never depend on them; a field the selected kernel does not have is ignored.
+ *   bits 0-7   ideal-device read tiling: 0 default (32 vectors per wave),
+ *              1: 64 vectors per wave (32-row reads), 2: 32 vectors per wave.
+ *   bits 12-15 noisy-device read: read chunks per output block.  0 automatic
+ *              (grids under 512 blocks are split), 1 never, s >= 2 that many
+ *              chunks (each writes integer totals to the workspace; one pass
+ *              restores and sums them); MF_E_RESOURCE when the workspace cannot
+ *              hold the chunks' totals (mf_mm_workspace prices them).
+ *   bits 16-19 wide noisy-device read: LDS capacity per read, 0 automatic (the
+ *              smallest holding a read's conductance terms), 1..3: 24, 36 or 72
+ *              fragments; MF_E_RESOURCE when it cannot hold them. */
+#define MF_MM_SPLIT_SHIFT 12
+#define MF_MM_TIER_SHIFT 16
+
 /* Fused read + scale restore (memfast/simulator.py:561-586 without the bias):
  * out [n, ldo] FP32 receives columns [0, p*C) of
  *   sum over reads g in torch's CPU order of (float(T[n,g,o]) * xscale[n,g]) * wscale[g,o].
  * g as for mf_partial over all tiles (begin=0, end=p); NULL means ideal devices.
  * For ideal devices with packed_t != NULL and a workspace of at least
  * mf_mm_workspace() bytes (256-byte aligned) the MFMA kernel is used;
- * `variant` picks its tiling (0 default, 1: 64 vectors per wave, 2: 32 vectors
- * per wave; the tuned mode's schedule grid).  Results do not depend on it.
+ * `variant` holds the schedule fields above (the tuned mode's grid) and
+ * MF_MM_REUSE_TERMS.  Results do not depend on the schedule fields.
  * out_cols (1..p*C) and k_rows (1..m*R) are the matrix's logical output columns
  * and input rows: the MFMA kernels compute only columns [0, out_cols) (the
  * reference slices the rest away before any check, :586) and skip the reads
@@ -305,7 +321,7 @@ int mf_partial_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t 
 int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, int64_t n, int64_t m,
                const uint32_t *packed, const double *wscale, int64_t p, const void *g,
                uint32_t seed, uint64_t event, double *out, int64_t ldo, void *workspace,
-               int64_t workspace_bytes, uint32_t *status, void *stream);
+               int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream);
 /* Integer slice totals T [n, m*Gr, p*C] (FP64) of the wide noisy-device MFMA
  * read (mf_mm_kernel 3), for parity tests: the values mf_partial_wide returns
  * for tiles [0, p).  g NULL samples conductances from packed (seed, event), or
@@ -324,11 +340,14 @@ int mf_mm_totals_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_
 int mf_profile_kernels(int32_t enable);
 int mf_profile_collect(int64_t *launches, double *milliseconds);
 
-/* Workspace bytes mf_mm needs for its MFMA kernels: per-read digit-sum maxima
- * (ideal devices) or the conductance terms of every column (noisy devices; a
- * smaller workspace of at least 64 columns' worth makes mf_mm work in column
- * chunks).  0 when the general kernel is used. */
-int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64_t *bytes);
+/* Workspace bytes mf_mm (mf_mm_wide) needs for its MFMA kernels under the
+ * schedule fields of `variant`: per-read digit-sum maxima (ideal devices), or
+ * the conductance terms of every column plus a split read's integer totals
+ * (noisy devices; a smaller workspace of at least 64 columns' worth makes mf_mm
+ * work in column chunks, unsplit), or 16-bit input codes and terms (wide
+ * codes).  0 when the general kernel is used. */
+int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t variant,
+                    int64_t *bytes);
 
 /* Integer slice totals T [n, m*Gr, p*C] (FP32) of the noisy-device MFMA read,
  * the values memfast/cuda.py:322-373 partial returns for tiles [0, p), for
@@ -345,7 +364,9 @@ int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
                  int32_t *kernel_id);
 
-/* Resource figures of the kernel mf_mm would launch. */
+/* Resource figures (registers, scratch spill, LDS, resident blocks per CU) of the
+ * read kernel mf_mm (mf_mm_wide) launches as `kernel_id` (mf_mm_kernel): 0 general,
+ * 1 ideal MFMA, 2 noisy MFMA, 3 wide noisy MFMA (its largest LDS tier). */
 int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *out);
 
 /* ---- counter-based RNG (memfast/random.py:8-33), for parity tests -------- */

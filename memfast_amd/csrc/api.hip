@@ -347,20 +347,38 @@ i64 noisy_terms_bytes(const mf_config *cfg, i64 m, i64 p) {
     return (p * cfg->cols + 63) / 64 * 2 * noisy_block_bytes(cfg, m);
 }
 
-// Read chunks of a split read (1: not split).
-i64 noisy_split(const mf_config *cfg, i64 n, i64 m, i64 p) {
+// Read chunks of a split read (1: not split).  `requested` (the variant's
+// split field) overrides the automatic choice: 1 never splits, s >= 2 splits
+// into s chunks (at most one per read).
+i64 noisy_split(const mf_config *cfg, i64 n, i64 m, i64 p, int requested = 0) {
     const i64 G = m * cfg->reads;
-    const i64 blocks = (p * cfg->cols + 63) / 64 * ((n + 63) / 64);
-    if (G < 2 || blocks >= NOISY_SPLIT_BELOW) return 1;
-    i64 z = (NOISY_SPLIT_BELOW + blocks - 1) / blocks;
+    i64 z;
+    if (requested > 0) {
+        z = requested;
+    } else {
+        const i64 blocks = (p * cfg->cols + 63) / 64 * ((n + 63) / 64);
+        if (G < 2 || blocks >= NOISY_SPLIT_BELOW) return 1;
+        z = (NOISY_SPLIT_BELOW + blocks - 1) / blocks;
+    }
     if (z > G) z = G;
+    if (z < 2) return 1;
     const i64 step = (G + z - 1) / z;
     return (G + step - 1) / step;
 }
 
-i64 noisy_scratch_bytes(const mf_config *cfg, i64 n, i64 m, i64 p) {
-    if (noisy_split(cfg, n, m, p) < 2) return 0;
+i64 noisy_scratch_bytes(const mf_config *cfg, i64 n, i64 m, i64 p, int requested = 0) {
+    if (noisy_split(cfg, n, m, p, requested) < 2) return 0;
     return align256(n * m * cfg->reads * p * cfg->cols * 4);
+}
+
+// Fields of the `variant` word (include/memfast_hip.h).
+int variant_tile(int32_t v) { return v & 0xFF; }
+int variant_split(int32_t v) { return (v >> MF_MM_SPLIT_SHIFT) & 0xF; }
+int variant_tier(int32_t v) { return (v >> MF_MM_TIER_SHIFT) & 0xF; }
+bool variant_valid(int32_t v) {
+    const int32_t known = 0xFF | MF_MM_REUSE_TERMS | (0xF << MF_MM_SPLIT_SHIFT) |
+                          (0xF << MF_MM_TIER_SHIFT);
+    return (v & ~known) == 0 && variant_tile(v) <= 2 && variant_tier(v) <= 3;
 }
 
 // Conductance terms depend on the read event only through shared read noise.
@@ -376,16 +394,21 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
                  const float *xscale, i64 n, i64 m, const u8 *packed_t, const float *wscale, i64 p,
                  const float *g, u32 seed, u64 event, float *out, i64 ldo, void *workspace,
                  i64 bytes, int totals, u32 *status, hipStream_t s, bool reuse = false,
-                 i64 ocols = -1, i64 g_run = -1) {
+                 i64 ocols = -1, i64 g_run = -1, int split_request = 0) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     if (ocols < 0) ocols = ncols;
     if (g_run < 0) g_run = G;
     const i64 per_block = noisy_block_bytes(cfg, m);
     // Split read (fused output only, when the whole program's terms fit).
-    const i64 split = totals ? 1 : noisy_split(cfg, n, m, p);
+    const i64 split = totals ? 1 : noisy_split(cfg, n, m, p, split_request);
     const i64 full = noisy_terms_bytes(cfg, m, p);
-    const i64 scratch = noisy_scratch_bytes(cfg, n, m, p);
+    const i64 scratch = noisy_scratch_bytes(cfg, n, m, p, split_request);
     const bool use_split = split > 1 && bytes >= full + scratch;
+    if (split > 1 && split_request > 1 && !use_split)
+        return fail(MF_E_RESOURCE,
+                    "workspace of %lld bytes below the %lld a %lld-way read split needs",
+                    static_cast<long long>(bytes), static_cast<long long>(full + scratch),
+                    static_cast<long long>(split));
     const i64 max_cb = use_split ? full / per_block : (bytes / per_block) / 2 * 2;
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
     reuse = reuse && g == nullptr && terms_event_independent(cfg) && max_cb * 32 >= ocols;
@@ -549,7 +572,7 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
                       const u32 *q, const double *xscale, i64 n, i64 m, const u32 *packed,
                       const double *wscale, i64 p, const float *g, u32 seed, u64 event,
                       double *out, i64 ldo, void *workspace, i64 bytes, int totals, u32 *status,
-                      hipStream_t s) {
+                      hipStream_t s, int tier_request = 0) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     const i64 codes_bytes = wide_codes_bytes(n, m, cfg);
     const i64 per_block = wide_block_bytes(cfg, m);
@@ -557,7 +580,15 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
     const int frags = cfg->n_w * NOISY_TERMS * ks;
     if (frags > WIDE_FRAGS_LARGE) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
-    const int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
+    int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
+    if (tier_request > 0) {
+        // A tuned schedule's LDS capacity: 24, 36 or 72 fragments per read.
+        const int capacity[3] = {WIDE_FRAGS_TINY, WIDE_FRAGS_SMALL, WIDE_FRAGS_LARGE};
+        if (frags > capacity[tier_request - 1])
+            return fail(MF_E_RESOURCE, "LDS tier of %d fragments below a read's %d",
+                        capacity[tier_request - 1], frags);
+        tier = tier_request - 1;
+    }
     uint16_t *q16 = static_cast<uint16_t *>(workspace);
     uint4 *gs = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + codes_bytes);
     hipLaunchKernelGGL(k_codes16, dim3(grid_for(n * kp)), dim3(256), 0, s, q, n * kp, q16);
@@ -1087,10 +1118,12 @@ int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t 
     return MF_OK;
 }
 
-int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64_t *bytes) {
+int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t variant,
+                    int64_t *bytes) {
     int status = check_config(cfg);
     if (status) return status;
     if (!bytes || n < 1 || m < 1 || p < 1) return fail(MF_E_INVALID, "invalid workspace query");
+    if (!variant_valid(variant)) return fail(MF_E_INVALID, "unknown kernel variant 0x%x", variant);
     IdealPlan plan;
     SlotTests xt, wt;
     NoisyPlan noisy;
@@ -1101,7 +1134,8 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int64
         ideal_workspace(cfg, n, m, p, &xb, &wb);
         *bytes = xb + wb;
     } else if (build_noisy_plan(cfg, m, p, &noisy, &ks, &why)) {
-        *bytes = noisy_terms_bytes(cfg, m, p) + noisy_scratch_bytes(cfg, n, m, p);
+        *bytes = noisy_terms_bytes(cfg, m, p) +
+                 noisy_scratch_bytes(cfg, n, m, p, variant_split(variant));
     } else if (wide_plan_ok(cfg, n, m, p)) {
         *bytes = wide_codes_bytes(n, m, cfg) + (p * cfg->cols + 31) / 32 * wide_block_bytes(cfg, m);
     } else {
@@ -1133,6 +1167,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         return fail(MF_E_INVALID, "out_cols must be in [1, p*C] and k_rows in [1, m*R]");
     const i64 g_run = reads_with_rows(cfg, m, k_rows);
     if (cfg->n_in > 8 || cfg->n_w > 8) return fail(MF_E_UNSUPPORTED, "more than 8 slices");
+    if (!variant_valid(variant)) return fail(MF_E_INVALID, "unknown kernel variant 0x%x", variant);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const i64 G = m * cfg->reads;
     IdealPlan plan;
@@ -1182,9 +1217,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         args.w_bits = cfg->weight_bits;
         // Tile variants: 0 default (32 vectors per wave), 1 = 64 vectors per wave,
         // 2 = 32 vectors per wave.
-        variant &= ~MF_MM_REUSE_TERMS;
-        if (variant < 0 || variant > 2) return fail(MF_E_INVALID, "unknown kernel variant %d", variant);
-        const int tn = (ks == 1 && variant == 1) ? 2 : 1;
+        const int tn = (ks == 1 && variant_tile(variant) == 1) ? 2 : 1;
         const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (out_cols + 63) / 64;
         if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
         const dim3 grid{unsigned(gx), unsigned(gy), 1u};
@@ -1205,7 +1238,8 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         workspace_bytes >= 2 * noisy_block_bytes(cfg, m)) {
         return launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p, nullptr, seed,
                             event, out, ldo, workspace, workspace_bytes, 0, status, s,
-                            (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run);
+                            (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run,
+                            variant_split(variant));
     }
     if (!g && needs_conductances(cfg))
         return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
@@ -1549,9 +1583,10 @@ int mf_partial_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t 
 int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, int64_t n, int64_t m,
                const uint32_t *packed, const double *wscale, int64_t p, const void *g,
                uint32_t seed, uint64_t event, double *out, int64_t ldo, void *workspace,
-               int64_t workspace_bytes, uint32_t *status, void *stream) {
+               int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream) {
     const int valid = check_wide(cfg);
     if (valid) return valid;
+    if (!variant_valid(variant)) return fail(MF_E_INVALID, "unknown kernel variant 0x%x", variant);
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
         ldo < p * cfg->cols)
         return fail(MF_E_INVALID, "invalid mm arguments");
@@ -1567,7 +1602,8 @@ int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, in
         if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
         const int launched = launch_noisy_wide(cfg, wplan, ks, small, q, xscale, n, m, packed,
                                                wscale, p, nullptr, seed, event, out, ldo,
-                                               workspace, workspace_bytes, 0, status, s);
+                                               workspace, workspace_bytes, 0, status, s,
+                                               variant_tier(variant));
         if (timing.first) {
             hipEventRecord(timing.second, s);
             g_profile.pending.push_back(timing);
@@ -1661,14 +1697,32 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     int status = check_config(cfg);
     if (status) return status;
     if (!out) return fail(MF_E_INVALID, "resources output is NULL");
+    // The instance of the read kernel mf_mm (mf_mm_wide) launches for this descriptor.
+    const bool nl = cfg->has_nonlinear != 0;
+    const bool ks4 = cfg->read_rows == 64;
+    const void *fn = nullptr;
+    if (kernel_id == 1) {
+        fn = reinterpret_cast<const void *>(&k_ideal<1, 1>);
+    } else if (kernel_id == 2) {
+        if (ks4) fn = nl ? reinterpret_cast<const void *>(&k_noisy<4, 5, true>)
+                         : reinterpret_cast<const void *>(&k_noisy<4, 5, false>);
+        else if (cfg->n_in <= 5) fn = nl ? reinterpret_cast<const void *>(&k_noisy<2, 5, true>)
+                                         : reinterpret_cast<const void *>(&k_noisy<2, 5, false>);
+        else fn = nl ? reinterpret_cast<const void *>(&k_noisy<2, 8, true>)
+                     : reinterpret_cast<const void *>(&k_noisy<2, 8, false>);
+    } else if (kernel_id == 3) {
+        fn = ks4 ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<4, true, false, WIDE_FRAGS_LARGE>)
+                       : reinterpret_cast<const void *>(&k_noisy_wide<4, false, false, WIDE_FRAGS_LARGE>))
+                 : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<2, true, false, WIDE_FRAGS_LARGE>)
+                       : reinterpret_cast<const void *>(&k_noisy_wide<2, false, false, WIDE_FRAGS_LARGE>));
+    } else if (kernel_id == 0) {
+        fn = cfg->precise ? reinterpret_cast<const void *>(&k_general<double, 4, false, false>)
+                          : reinterpret_cast<const void *>(&k_general<float, 8, false, false>);
+    } else {
+        return fail(MF_E_INVALID, "unknown read kernel %d", kernel_id);
+    }
     hipFuncAttributes attr;
-    hipError_t e;
-    if (kernel_id == 1)
-        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_ideal<2, 1>));
-    else if (cfg->precise)
-        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<double, 4, false, false>));
-    else
-        e = hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(&k_general<float, 8, false, false>));
+    const hipError_t e = hipFuncGetAttributes(&attr, fn);
     if (e != hipSuccess) return fail(MF_E_HIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
     memset(out, 0, sizeof(*out));
     out->threads = 256;
@@ -1676,11 +1730,9 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     out->registers = attr.numRegs;
     out->local_bytes = int32_t(attr.localSizeBytes);
     int blocks = 0;
-    const void *fn = kernel_id == 1 ? reinterpret_cast<const void *>(&k_ideal<2, 1>)
-                                    : reinterpret_cast<const void *>(&k_general<float, 8, false, false>);
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) == hipSuccess)
         out->max_blocks_per_cu = blocks;
-    if (out->max_blocks_per_cu < 1 && blocks == 0) return fail(MF_E_RESOURCE, "zero resident blocks");
+    if (blocks == 0) return fail(MF_E_RESOURCE, "zero resident blocks");
     return MF_OK;
 }
 

@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -164,12 +164,12 @@ SIGNATURES = {
     "mf_partial_wide": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
                          _P, _P, _P], ct.c_int),
     "mf_mm_wide": ([_CFG, _P, _P, _I64, _I64, _P, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
-                    _I64, _P, _I64, _P, _P], ct.c_int),
+                    _I64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals_wide": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
                            _P, _I64, _P], ct.c_int),
     "mf_profile_kernels": ([_I32], ct.c_int),
     "mf_profile_collect": ([ct.POINTER(_I64), ct.POINTER(ct.c_double)], ct.c_int),
-    "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, ct.POINTER(_I64)], ct.c_int),
+    "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I64)], ct.c_int),
     "mf_mm_kernel": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I32)], ct.c_int),
     "mf_resources_query": ([_CFG, _I32, ct.POINTER(MFResources)], ct.c_int),
     "mf_rng_uniform": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
@@ -725,6 +725,16 @@ def partial(q, packed, config, schedule, seed, event, begin, end, *, conductance
 
 
 REUSE_TERMS = 0x100   # MF_MM_REUSE_TERMS
+SPLIT_SHIFT, TIER_SHIFT = 12, 16   # MF_MM_SPLIT_SHIFT, MF_MM_TIER_SHIFT
+
+
+def variant_word(tile=0, split=0, tier=0):
+    """The schedule fields of mf_mm's ``variant`` (include/memfast_hip.h): the ideal read's
+    tiling (0-2), the noisy read's read split (0 automatic, 1 never, s chunks) and the wide
+    read's LDS tier (0 automatic, 1-3)."""
+    if not (0 <= tile <= 2 and 0 <= split <= 15 and 0 <= tier <= 3):
+        raise ValueError("schedule fields out of range")
+    return tile | split << SPLIT_SHIFT | tier << TIER_SHIFT
 
 
 def terms_event_independent(config):
@@ -751,7 +761,8 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     p, c = packed.shape[1], config.array_size[1]
     if config.wide:
         return _mm_wide(q, xscale, packed, packed_t, wscale, config, seed, event,
-                        conductance=conductance, out=out, status=status)
+                        conductance=conductance, out=out, status=status,
+                        variant=variant & ~REUSE_TERMS)
     if out_cols is not None and not 1 <= out_cols <= p * c:
         raise ValueError("out_cols must be in [1, p*C]")
     if k_rows is not None and not 1 <= k_rows <= m * r:
@@ -766,7 +777,7 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     if out is None:
         out = torch.empty((n, p * c), dtype=torch.float32, device=q.device)
     if packed_t is not None and kernel:
-        size = mm_workspace_bytes(config, n, m, p)
+        size = mm_workspace_bytes(config, n, m, p, variant & ~REUSE_TERMS)
         if workspace is None:
             workspace = torch.empty(max(1, size), dtype=torch.uint8, device=q.device)
             reuse_terms = False
@@ -795,7 +806,8 @@ def mm(q, xscale, packed, packed_t, wscale, config, seed, event, *, conductance=
     return out
 
 
-def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductance, out, status):
+def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductance, out, status,
+             variant=0):
     n, m, r = q.shape
     p, c = packed.shape[1], config.array_size[1]
     codes = _u32(packed) if codes is None else _u32(codes)
@@ -803,7 +815,7 @@ def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductan
     workspace = None
     if g is None and mm_kernel(config, n, m, p) == 3:
         # The wide MFMA read samples conductances itself.
-        workspace = _workspace(config, n, m, p, q.device)
+        workspace = _workspace(config, n, m, p, q.device, variant)
     elif g is None and needs_conductances(config):
         g = restore(codes, config, seed, event, 0, p)
     if g is not None:
@@ -820,7 +832,7 @@ def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductan
                 _ptr(xscale), n, m, _ptr(codes),
                 _ptr(wscale), p, _ptr(g), seed, event, _ptr(out),
                 out.stride(0), _ptr(workspace), 0 if workspace is None else workspace.numel(),
-                _ptr(status), _stream(q.device),
+                variant, _ptr(status), _stream(q.device),
             ),
             "mm",
         )
@@ -828,17 +840,18 @@ def _mm_wide(q, xscale, packed, codes, wscale, config, seed, event, *, conductan
 
 
 @lru_cache(maxsize=4096)
-def mm_workspace_bytes(config, n, m, p):
-    """Bytes of MFMA-kernel scratch ``mm`` uses for this shape (0 for the general kernel)."""
+def mm_workspace_bytes(config, n, m, p, variant=0):
+    """Bytes of MFMA-kernel scratch ``mm`` uses for this shape and schedule (``variant``'s
+    fields; 0 for the general kernel)."""
     size = ct.c_int64()
-    check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
-          "workspace size")
+    check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, variant,
+                                    ct.byref(size)), "workspace size")
     return size.value
 
 
-def _workspace(config, n, m, p, device):
+def _workspace(config, n, m, p, device, variant=0):
     """Device scratch for the MFMA reads (mf_mm_workspace bytes, 256-byte aligned)."""
-    return torch.empty(max(1, mm_workspace_bytes(config, n, m, p)), dtype=torch.uint8,
+    return torch.empty(max(1, mm_workspace_bytes(config, n, m, p, variant)), dtype=torch.uint8,
                        device=device)
 
 
@@ -928,10 +941,7 @@ def mm_totals(q, packed_t, config, seed, event, *, conductance=None):
         g = conductance.to(device=q.device, dtype=torch.float32).contiguous()
         if tuple(g.shape) != (m, p, len(config.weight_layout), r, c):
             raise ValueError("injected conductances must be [m, p, W, R, C]")
-    size = ct.c_int64()
-    check(library().mf_mm_workspace(ct.byref(descriptor(config)), n, m, p, ct.byref(size)),
-          "workspace size")
-    workspace = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
+    workspace = _workspace(config, n, m, p, q.device)
     groups = m * config.reads_per_array
     totals = torch.empty((n, groups, p, c), dtype=torch.float32, device=q.device)
     q, packed_t = q.contiguous(), packed_t.contiguous()
@@ -1016,9 +1026,12 @@ class Program:
         self.vectors = vectors
         self.columns = columns
 
-    def resources(self, config, vectors, columns, workers):
+    def resources(self, config, vectors, columns, workers, kernel=None):
+        """Resources of the read kernel ``kernel`` (mf_mm_kernel's id; by default the ideal
+        MFMA read for ideal devices, else the general one)."""
         info = MFResources()
-        kernel = 1 if config.nonidealities.ideal else 0
+        if kernel is None:
+            kernel = 1 if config.nonidealities.ideal else 0
         check(library().mf_resources_query(ct.byref(descriptor(config)), kernel, ct.byref(info)),
               "resources")
         return dict(threads=info.threads, shared=info.shared_bytes, local_bytes=info.local_bytes,

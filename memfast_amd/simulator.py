@@ -23,29 +23,10 @@ from pathlib import Path
 import torch
 from torch import nn
 
-from . import hip, host_order
+from . import hip, host_order, tuning
 from .config import Config
 from .quantization import check_read_scales, expanded_parameter, pack_weight, read_starts
-
-# Block tiles (vectors x columns) of the ideal-device MFMA read kernel that the
-# tuned mode traverses, and the mf_mm variant of each.  This re-keys the
-# reference's grid of arrays x vectors x columns x workers (simulator.py:31-45);
-# the general (noisy) kernel has one tiling, so its configs see one candidate.
-TILE_VARIANTS = {"64x64": 2, "128x64": 1}
-KERNEL_TILES = tuple(TILE_VARIANTS)
-
-
-def default_schedule(config):
-    """Default execution schedule (keys kept from memfast/simulator.py:27-28)."""
-    return dict(arrays=2, vectors=2, columns=4, workers=min(2, len(config.weight_layout)),
-                tile=KERNEL_TILES[0])
-
-
-def schedule_grid(config, n, partitions):
-    """Finite tuning domain of the HIP kernels (one entry per kernel tile variant)."""
-    for tile in KERNEL_TILES:
-        yield dict(arrays=2, vectors=2, columns=4, workers=min(2, len(config.weight_layout)),
-                   tile=tile)
+from .tuning import default_schedule, schedule_grid
 
 
 def source_hash():
@@ -238,7 +219,7 @@ class Simulator:
             output = hip.mm(q, xscale, packed, codes if hip.mm_kernel(
                 config, q.shape[0], q.shape[1], p) or config.wide else None,
                 wscale.reshape(-1, p * config.array_size[1]), config, config.seed ^ tag, event,
-                variant=TILE_VARIANTS[KERNEL_TILES[0]], status=status,
+                variant=tuning.DEFAULT_VARIANT, status=status,
                 out_cols=out_features, k_rows=matrix.shape[0])
         flags = int(status.item())
         if flags & hip.STATUS_INPUT:
@@ -275,120 +256,31 @@ class Simulator:
         return dict(mode=self.mode, device=str(self.device), config=asdict(self.config),
                     selections=self.records)
 
-    # -- tuned mode ----------------------------------------------------------
-    def _key(self, matrix, x):
+    # -- tuned mode (memfast_amd/tuning.py) -------------------------------------
+    def _key(self, matrix, x, grid):
+        """(digest, payload) of a selection (memfast/simulator.py:195-214, grid re-keyed)."""
         if self._fingerprint is None:
             self._fingerprint = source_hash()
-        payload = dict(
-            config=asdict(self.config),
-            hardware=hip.identity(self.device),
-            shape=list(x.shape),
-            output=matrix.out_features,
-            dtype=str(x.dtype),
-            sources=self._fingerprint,
-            workspace_bytes=self.workspace_bytes,
-            grid=dict(tile=list(KERNEL_TILES)),
-        )
-        payload = json.loads(json.dumps(payload))
-        digest = hashlib.sha256(json.dumps(payload, sort_keys=True).encode()).hexdigest()
-        return digest, payload
+        return tuning.selection_key(self, matrix, x, grid, self._fingerprint)
 
     def _admit(self, matrix, q, schedule):
-        """Resource admission of a schedule (workspace of the restored conductances)."""
+        """Resources of a schedule; ResourceError when its scratch exceeds the workspace
+        budget or its kernel would spill registers."""
         c = self.config
-        n, m, r = q.shape
-        planes = hip.restore_planes(c) if hip.needs_conductances(c) else 0
-        size = (8 if c.precise_currents else 4) * planes * m * matrix.p * len(
-            c.weight_layout) * r * c.array_size[1]
-        if size > self.workspace_bytes:
+        n, arrays, _ = q.shape
+        if tuning.workspace_need(c, n, arrays, matrix.p, schedule) > self.workspace_bytes:
             raise hip.ResourceError("workspace budget")
+        kernel = tuning.read_kernel(c, n, arrays, matrix.p)
         with torch.cuda.device(self.device):
-            resource = hip.program(c, 2, 4, self.device.index).resources(c, 2, 4, 2)
+            resource = hip.program(c, schedule["vectors"], schedule["columns"],
+                                   self.device.index).resources(
+                c, schedule["vectors"], schedule["columns"], schedule["workers"], kernel=kernel)
         if resource["local_bytes"]:
             raise hip.ResourceError("register spill policy")
         return resource
 
     def _select(self, matrix, x, q, xscale, event):
-        started = time.perf_counter()
-        key, payload = self._key(matrix, x)
-        population = list(schedule_grid(self.config, q.shape[0], matrix.p))
-        reference_output = None
-        for baseline in [default_schedule(self.config), *population]:
-            try:
-                self._admit(matrix, q, baseline)
-                reference_output = matrix._execute(q, xscale, baseline, event)
-                break
-            except (hip.ResourceError, torch.cuda.OutOfMemoryError):
-                torch.cuda.empty_cache()
-        if reference_output is None:
-            raise RuntimeError("no feasible reference schedule in the declared grid")
-        if not torch.isfinite(reference_output).all():
-            raise FloatingPointError("nonfinite default output during tuning")
-        path = self.cache_dir / f"{key}.json"
-        record = dict(key=key, layer=matrix.name, shape=list(x.shape), cache_hit=False,
-                      candidates=[], selected=None, complete=False)
-        self.records.append(record)
-        cached = self._selections.get(key)
-        if cached is None and path.is_file():
-            try:
-                content = json.loads(path.read_text(encoding="utf-8"))
-                if (
-                    content["fingerprint"] == payload
-                    and content["complete"]
-                    and content["selected"] in population
-                ):
-                    cached = content["selected"]
-            except (KeyError, ValueError, TypeError):
-                cached = None
-        if cached is not None:
-            try:
-                self._admit(matrix, q, cached)
-                output = matrix._execute(q, xscale, cached, event)
-                if not torch.equal(reference_output.view(torch.int32), output.view(torch.int32)):
-                    raise RuntimeError("cached schedule changes output")
-                record.update(cache_hit=True, selected=cached, complete=True,
-                              preparation_seconds=time.perf_counter() - started)
-                self._selections[key] = cached
-                return cached
-            except (hip.ResourceError, torch.cuda.OutOfMemoryError):
-                torch.cuda.empty_cache()
-                cached = None
-        for schedule in population:
-            candidate = dict(schedule=schedule, status="rejected", timed_samples=0)
-            record["candidates"].append(candidate)
-            try:
-                candidate["resources"] = self._admit(matrix, q, schedule)
-                output = matrix._execute(q, xscale, schedule, event)
-                if not torch.equal(reference_output.view(torch.int32), output.view(torch.int32)):
-                    raise RuntimeError("schedule changes output")
-                del output
-                start = torch.cuda.Event(enable_timing=True)
-                end = torch.cuda.Event(enable_timing=True)
-                start.record()
-                output = matrix._execute(q, xscale, schedule, event)
-                end.record()
-                end.synchronize()
-                candidate.update(status="accepted", seconds=start.elapsed_time(end) / 1000,
-                                 timed_samples=1)
-                del output
-            except hip.ResourceError as error:
-                candidate["reason"] = str(error)
-            except torch.cuda.OutOfMemoryError:
-                candidate["reason"] = "HIP out of memory"
-                torch.cuda.empty_cache()
-        accepted = [item for item in record["candidates"] if item["status"] == "accepted"]
-        if not accepted:
-            raise RuntimeError("no feasible schedule in the declared grid")
-        selected = min(accepted, key=lambda item: item["seconds"])["schedule"]
-        record.update(selected=selected, complete=True, domain_count=len(population),
-                      preparation_seconds=time.perf_counter() - started)
-        hip.atomic_write(
-            path,
-            json.dumps(dict(fingerprint=payload, complete=True, selected=selected,
-                            candidates=record["candidates"]), sort_keys=True).encode(),
-        )
-        self._selections[key] = selected
-        return selected
+        return tuning.ScheduleSearch(self, matrix, x, q, xscale, event).run()
 
 
 class AnalogMatrix(nn.Module):
@@ -658,11 +550,11 @@ class AnalogMatrix(nn.Module):
             if status is None:
                 status = hip.status_word(q.device)
             workspace, reuse, source = None, False, None
+            variant = tuning.schedule_variant(schedule)
             if kernel == 2 and hip.terms_event_independent(config):
-                workspace, reuse, source = self._terms_workspace(q, codes_t)
+                workspace, reuse, source = self._terms_workspace(q, codes_t, variant)
             output = hip.mm(q, xscale, packed, codes_t, self.weight_scale.reshape(-1, self.p * c),
-                            config, self.seed, event,
-                            variant=TILE_VARIANTS.get(schedule.get("tile"), 0), status=status,
+                            config, self.seed, event, variant=variant, status=status,
                             workspace=workspace, reuse_terms=reuse,
                             out_cols=self.out_features, k_rows=self.in_features)
             if source is not None:
@@ -717,14 +609,14 @@ class AnalogMatrix(nn.Module):
             return self._execute_checked(q, xscale, schedule, event, stable=True)
         return output, True
 
-    def _terms_workspace(self, q, codes_t):
+    def _terms_workspace(self, q, codes_t, variant=tuning.DEFAULT_VARIANT):
         """Workspace of the noisy MFMA read kept across calls, and whether it still holds
         this program's conductance terms (same kernel codes object and version, seed).
 
         Write variation, drift and stuck-at faults do not depend on the read event
         (memfast/reference.py:36-46), so those samples are identical on every read
         of a programmed matrix and need not be drawn again."""
-        need = hip.mm_workspace_bytes(self.config, q.shape[0], q.shape[1], self.p)
+        need = hip.mm_workspace_bytes(self.config, q.shape[0], q.shape[1], self.p, variant)
         workspace = self._workspace
         if workspace is None or workspace.numel() < need or workspace.device != q.device:
             workspace = torch.empty(max(1, need), dtype=torch.uint8, device=q.device)
