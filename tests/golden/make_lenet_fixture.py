@@ -2,12 +2,18 @@
 
 Reads /root/reference/examples/checkpoints/lenet5_mnist.pt (float weights) and
 lenet5_mnist_static_int4.pt (packed signed INT4 codes, scales, fixed input
-scales, per-matrix names and seeds) with ``torch.load(weights_only=True)``;
-the static checkpoint was produced by the reference from the float one
-(examples/checkpoints/README.md:28-41), so the pair pins weight quantization,
-two's complement masking, [m,p,R,C] packing, padding and seed derivation.
+scales, biases, per-matrix names, seeds and read events) with
+``torch.load(weights_only=True)``; the static checkpoint was produced by the
+reference from the float one (examples/checkpoints/README.md:28-41), so the
+pair pins weight quantization, two's complement masking, [m,p,R,C] packing,
+padding and seed derivation.  The static checkpoint's whole state dict is kept
+too (tensors, plus each matrix's ``_extra_state`` as JSON, and the saved
+simulator Config), so that tests can load it into a converted LeNet-5 with
+``load_state_dict`` as examples/04_lenet5_mnist_static_quant.py:165-185 does.
 Run in the build container: python tests/golden/make_lenet_fixture.py
 """
+
+import json
 
 from pathlib import Path
 
@@ -44,7 +50,14 @@ def main():
         out[f"l{index}_seed"] = np.array(extra["seed"], dtype=np.uint64)
         out[f"l{index}_maximum"] = np.array(
             static["calibration"]["layers"][prefix]["maximum"], dtype=np.float64)
+        out[f"l{index}_prefix"] = np.array(prefix)
+        out[f"l{index}_bias"] = state[prefix + ".bias"].numpy()
+        out[f"l{index}_extra_state"] = np.array(json.dumps(extra))
     out["count"] = np.array(len(LAYERS))
+    out["state_keys"] = np.array(sorted(state))
+    out["config"] = np.array(json.dumps(static["config"]))
+    out["conversion"] = np.array(json.dumps(static["conversion"]))
+    out["format"] = np.array(static["format"])
     np.savez_compressed(OUT, **out)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
 
