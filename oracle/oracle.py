@@ -24,6 +24,9 @@ Pinning status (what checks each function beyond this restatement):
   * partial / restored with noise: vectors written by
     tests/golden/make_reference_vectors.py (transcendentals are torch CPU).
   * execute epilogue order: torch's own CPU ``sum`` (called directly here).
+  * imported_tiles / zero_point_correction (map_quantized): with ideal devices
+    and an ADC that never clamps, the product equals the dequantized affine
+    weights' product (tests/test_oracle.py closed form).
 """
 
 import hashlib
@@ -362,8 +365,47 @@ def restore_scales(value, input_scale, weight_scale):
     return torch.where(mantissa == 0, 0.0, result)
 
 
+def imported_tiles(codes, scales, cfg, zero_points=None):
+    """``map_quantized`` programming of integer [O,K] weights (simulator.py:173-185, :399-425):
+    packed codes, per-read scales and, with zero points, the per-read correction rows
+    ``-(zero_point * scale)`` at each read's first row [m*Gr, O]."""
+    o, k = codes.shape
+    dtype = torch.float64 if is_wide(cfg) else torch.float32
+    code = codes.to(torch.int64).T.contiguous()
+    scale_full = scales.to(dtype).expand(o, k).T.contiguous()
+    packed, wscale = pack_weight(code, scale_full, cfg)
+    if zero_points is None:
+        return packed, wscale, None
+    zeros = zero_points.to(dtype).expand(o, k).T.contiguous()
+    starts = read_starts(math.ceil(k / cfg.array_size[0]), cfg).clamp_max(k - 1)
+    return packed, wscale, -(zeros[starts] * scale_full[starts])
+
+
+def zero_point_correction(output, q, xscale, correction, cfg, stable=False):
+    """Add the digital zero-point term of simulator.py:587-611 to ``output`` [N, O]: each
+    read's signed input code sum times its input scale times the correction row, in FP32
+    as one matrix product, or per chunk of C columns with restore_scales in FP64."""
+    bits = cfg.activation_bits
+    signed = q.to(torch.int64).reshape(q.shape[0], -1) & ((1 << bits) - 1)
+    signed = (signed ^ (1 << (bits - 1))) - (1 << (bits - 1))
+    rows, step = cfg.array_size[0], read_rows(cfg)
+    padded = F.pad(signed.reshape(q.shape[0], -1, rows), (0, reads_per_array(cfg) * step - rows))
+    sums = padded.reshape(q.shape[0], -1, step).sum(-1)
+    if is_wide(cfg) or stable:
+        output = output.clone()
+        c = cfg.array_size[1]
+        for begin in range(0, output.shape[1], c):
+            end = min(begin + c, output.shape[1])
+            output[:, begin:end] += restore_scales(sums[:, :, None], xscale[:, :, None],
+                                                   correction[None, :, begin:end]).sum(1)
+        return output
+    dtype = output.dtype
+    return output + (sums.to(dtype) * xscale.to(dtype)) @ correction.to(dtype)
+
+
 def execute(q, xscale, packed, wscale, cfg, seed, event, out_features, *, bias=None,
-            arrays=2, stable=False, conductance=None, totals=None, tiles=None):
+            arrays=2, stable=False, conductance=None, totals=None, tiles=None,
+            zero_correction=None):
     """Fused epilogue of AnalogMatrix._execute (simulator.py:561-616).
 
     ``conductance`` (optional) is the full [m,p,W,R,C] injected tensor.
@@ -399,11 +441,14 @@ def execute(q, xscale, packed, wscale, cfg, seed, event, out_features, *, bias=N
     if tiles is not None:
         return output[:, first * c:min(last, end) * c].contiguous()
     output = output[:, :out_features].contiguous()
+    if zero_correction is not None:
+        output = zero_point_correction(output, q, xscale, zero_correction, cfg, stable)
     if bias is not None:
         output = output + bias
     if not is_wide(cfg) and not stable and not torch.isfinite(output).all():
         return execute(q, xscale, packed, wscale, cfg, seed, event, out_features, bias=bias,
-                       arrays=arrays, stable=True, conductance=conductance, totals=totals)
+                       arrays=arrays, stable=True, conductance=conductance, totals=totals,
+                       zero_correction=zero_correction)
     return output
 
 

@@ -394,3 +394,33 @@ def test_execute_tiles_equals_full_columns():
         assert torch.equal(part, full[:, tiles[0] * 16:tiles[1] * 16])
     with pytest.raises(ValueError):
         oracle.execute(q, xs, packed, ws, cfg, 9, 2, 96, tiles=(1, 3))
+
+
+@pytest.mark.parametrize("wide", [False, True])
+def test_zero_point_correction_closed_form(wide):
+    """map_quantized with zero points (simulator.py:173-185, :587-611): with ideal devices
+    and an ADC that never clamps (max 2^12-1 > 32 rows x 3 x 3 per pair), the read equals
+    x_dequantized @ (scale * (code - zero_point)).T up to rounding; a dropped or
+    sign-flipped correction misses by the zero points' whole contribution."""
+    cfg = Config(activation_bits=12 if wide else 8, weight_bits=4, weight_signed=False,
+                 input_slice=(1, 1, 2, 2, 2, 2, 2) if wide else (1, 1, 2, 2, 2),
+                 weight_slice=(2, 2), array_size=(64, 32), rows_per_read=32, adc_bits=12,
+                 input_quant_gran=(1, 32), nonidealities=Nonidealities(write_variation=0.0))
+    gen = torch.Generator().manual_seed(63)
+    o, k = 40, 150
+    codes = torch.randint(0, 16, (o, k), generator=gen)
+    scales = torch.rand(o, 1, generator=gen) * 0.1 + 0.01
+    zero_points = torch.randint(3, 12, (o, 1), generator=gen).float()
+    x = torch.randn(6, k, generator=gen, dtype=torch.float64 if wide else torch.float32)
+    packed, wscale, correction = oracle.imported_tiles(codes, scales, cfg, zero_points)
+    q, xs = oracle.input_tiles(x, cfg)
+    got = oracle.execute(q, xs, packed, wscale, cfg, 1, 0, o, zero_correction=correction)
+    bits = cfg.activation_bits
+    signed = (q.long().reshape(6, -1)[:, :k] & ((1 << bits) - 1))
+    signed = (signed ^ (1 << (bits - 1))) - (1 << (bits - 1))
+    per_row_scale = xs.repeat_interleave(32, dim=1)[:, :k]
+    dequantized = signed.double() * per_row_scale.double()
+    expected = dequantized @ (scales.double() * (codes.double() - zero_points.double())).T
+    torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-5)
+    without = oracle.execute(q, xs, packed, wscale, cfg, 1, 0, o)
+    assert (without.double() - expected).abs().max() > 1e-2
