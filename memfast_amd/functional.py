@@ -1,61 +1,90 @@
-"""Natural-order analog matrix products with the FP32 quantized-operand STE.
+"""``mm`` and ``matmul`` in natural ``A @ B`` order, read on the GPU.
 
-Drop-in for memfast/functional.py: ``mm(A, B)`` and ``matmul(A, B)`` take
-operands in ordinary ``A @ B`` order and follow torch.mm / torch.matmul
-shapes (vector promotion, broadcast batches).  A supplied simulator caches
-RHS programming; without one each call builds a fresh simulator, so the
-matrix is always ``matrix.0`` at read event 0.  A shared RHS quantizes its
-input vectors together in flattened row order; each distinct batched RHS is
-programmed separately.  Forward values come from the analog kernels; the
-backward pass (when gradients are requested) uses the FP32 quantized-operand
-surrogate of memfast/nn/training.py.
+Behaviour of the reference's memfast/functional.py:
+* shapes follow torch.mm / torch.matmul: vector promotion and broadcast batches;
+* operands are real floating dense tensors of one dtype on one device, checked with
+  the reference's messages and in its order (types first, then finiteness, then
+  shapes, ``out`` and the simulator);
+* a supplied simulator keeps the RHS programs between calls; without one each call
+  builds a fresh simulator, so its matrix is ``matrix.0`` at read event 0;
+* a RHS shared by every batch entry quantizes all input vectors together, in flattened
+  row order; each distinct RHS of a batched operand is programmed on its own and reads
+  the stacked inputs of the batch entries that use it;
+* backward, when gradients are wanted, goes through the FP32 quantized-operand
+  surrogate of the hardware-aware layers (memfast_amd/nn/training.py), with the RHS's
+  program as its weights.
+
+A shared RHS of a simulator instance is read by ``Simulator._product``: both operands
+are quantized and read in one pass with the finiteness checks on the device.  Other
+routes check finiteness on the host before any state changes.
 """
 
 import contextlib
-import itertools
-import weakref
+import math
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 
 from .config import Config
-from .nn.training import _quantized_linear, _SurrogateGradient
+from .nn.training import _SurrogateGradient, _linear_surrogate
 from .simulator import Simulator
 
 _FLOATING = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
+# Dtypes whose FP32 quantization keeps finiteness, so that the device-side check of the
+# single-pass product raises exactly where a host check would.
+_SINGLE_PASS_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
-def _operands(a, b, *, finite=True):
-    """Type, device and (unless deferred) finiteness checks of functional.py:32-53."""
-    for name, value in (("A", a), ("B", b)):
-        if not isinstance(value, torch.Tensor):
-            raise TypeError(f"{name} must be a torch.Tensor")
-        if value.layout != torch.strided or value.dtype not in _FLOATING:
-            raise TypeError(f"{name} must be a real floating dense tensor")
-        if value.ndim == 0:
-            raise ValueError(f"{name} must have at least one dimension")
+def _check_operands(a, b):
+    """Type, layout, dtype and device checks (memfast/functional.py:32-48)."""
+    for label, operand in (("A", a), ("B", b)):
+        if not isinstance(operand, torch.Tensor):
+            raise TypeError(f"{label} must be a torch.Tensor")
+        if operand.layout != torch.strided or operand.dtype not in _FLOATING:
+            raise TypeError(f"{label} must be a real floating dense tensor")
+        if operand.ndim == 0:
+            raise ValueError(f"{label} must have at least one dimension")
     if a.dtype != b.dtype:
         raise ValueError("A and B must have the same dtype")
     if a.device != b.device:
         raise ValueError("A and B must use the same device")
     if a.device.type not in ("cpu", "cuda"):
         raise ValueError("matrix simulation requires CPU or CUDA operands")
-    if finite:
-        _finite(a, b)
 
 
-def _finite(a, b):
-    for name, value in (("A", a), ("B", b)):
-        if not torch.isfinite(value).all():
-            raise ValueError(f"{name} must be finite")
+def _check_finite(a, b):
+    for label, operand in (("A", a), ("B", b)):
+        if not bool(torch.isfinite(operand).all()):
+            raise ValueError(f"{label} must be finite")
 
 
-# Operand dtypes whose FP32 quantization preserves finiteness, so the fused
-# product's device-side check raises exactly where the host check would.
-_FUSED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+class _Layout(NamedTuple):
+    left: torch.Tensor      # A with a leading row axis when A is a vector
+    right: torch.Tensor     # B with a trailing column axis when B is a vector
+    batch: torch.Size       # broadcast batch dimensions
+    rows: int
+    reduction: int
+    columns: int
+    shape: torch.Size       # the result's shape
 
 
-def _engine(a, simulator, config, mode, cache_dir):
+def _layout(a, b):
+    left = a.unsqueeze(0) if a.ndim == 1 else a
+    right = b.unsqueeze(-1) if b.ndim == 1 else b
+    if left.shape[-1] != right.shape[-2]:
+        raise ValueError("A and B have incompatible reduction dimensions")
+    try:
+        batch = torch.broadcast_shapes(left.shape[:-2], right.shape[:-2])
+    except RuntimeError:
+        raise ValueError("A and B batch dimensions cannot broadcast") from None
+    rows, reduction, columns = left.shape[-2], left.shape[-1], right.shape[-1]
+    shape = batch + ((rows,) if a.ndim > 1 else ()) + ((columns,) if b.ndim > 1 else ())
+    return _Layout(left, right, batch, rows, reduction, columns, torch.Size(shape))
+
+
+def _resolve_simulator(a, simulator, config, mode, cache_dir):
+    """The caller's simulator, checked against the other options, or a fresh one."""
     if mode not in ("default", "tuned"):
         raise ValueError("mode must be default or tuned")
     if config is not None and not isinstance(config, Config):
@@ -64,18 +93,21 @@ def _engine(a, simulator, config, mode, cache_dir):
         return Simulator(config, mode=mode, device=a.device, cache_dir=cache_dir)
     if not isinstance(simulator, Simulator):
         raise TypeError("simulator must be Simulator")
-    if simulator.device != a.device:
-        raise ValueError("operands and simulator must use the same device")
-    if config is not None and config != simulator.config:
-        raise ValueError("config differs from the supplied simulator")
-    if mode != "default" and mode != simulator.mode:
-        raise ValueError("mode differs from the supplied simulator")
-    if cache_dir is not None and Path(cache_dir) != simulator.cache_dir:
-        raise ValueError("cache_dir differs from the supplied simulator")
+    conflicts = (
+        (simulator.device != a.device, "operands and simulator must use the same device"),
+        (config is not None and config != simulator.config,
+         "config differs from the supplied simulator"),
+        (mode != "default" and mode != simulator.mode, "mode differs from the supplied simulator"),
+        (cache_dir is not None and Path(cache_dir) != simulator.cache_dir,
+         "cache_dir differs from the supplied simulator"),
+    )
+    for conflict, message in conflicts:
+        if conflict:
+            raise ValueError(message)
     return simulator
 
 
-def _out(a, b, out, shape):
+def _check_out(a, b, out, shape):
     if out is None:
         return
     if not isinstance(out, torch.Tensor) or out.layout != torch.strided:
@@ -86,129 +118,80 @@ def _out(a, b, out, shape):
         raise RuntimeError("out= does not support automatic differentiation")
 
 
-def _map_rhs(simulator, b):
-    mapper = getattr(simulator, "_matrix_for", None)
-    if mapper is not None:
-        return mapper(b)
-    return simulator.map(b.detach().transpose(0, 1))
+def _wants_grad(*operands):
+    return torch.is_grad_enabled() and any(t.requires_grad for t in operands)
 
 
-def _rhs_view(simulator, owner, rhs, index):
-    """Stable detached RHS views keyed by the caller's tensor (without keeping it alive)."""
-    cache = getattr(simulator, "_functional_rhs_views", None)
-    if cache is None:
-        cache = simulator._functional_rhs_views = {}
-    identity = id(owner)
-    geometry = (
-        tuple(owner.shape), tuple(owner.stride()), owner.storage_offset(), owner.data_ptr(),
-        owner.dtype, owner.device, owner.is_neg(),
-    )
-    record = cache.get(identity)
-    if record is None or record[0]() is not owner or record[1] != geometry:
-        engine = weakref.ref(simulator)
-
-        def release(reference):
-            instance = engine()
-            if instance is not None:
-                entries = instance._functional_rhs_views
-                previous = entries.get(identity)
-                if previous is not None and previous[0] is reference:
-                    entries.pop(identity, None)
-
-        record = (weakref.ref(owner, release), geometry, {})
-        cache[identity] = record
-    if index not in record[2]:
-        record[2][index] = rhs.detach()
-    return record[2][index]
-
-
-def _product(a, b, simulator, cached_rhs=None, fused=False):
-    rhs = b if cached_rhs is None else cached_rhs
-    if fused:
-        analog = simulator._product(a.detach(), rhs)
+def _read(simulator, inputs, rhs, owner, index, single_pass):
+    """Analog ``inputs @ rhs`` through the RHS program kept for (owner, index), with the
+    surrogate gradient attached when one is wanted."""
+    if single_pass:
+        analog, program = simulator._product(inputs.detach(), rhs, owner=owner, index=index)
     else:
-        matrix = _map_rhs(simulator, rhs)
-        analog = matrix(a.detach())
-    if not torch.is_grad_enabled() or not (a.requires_grad or b.requires_grad):
+        program = simulator._matrix_for(rhs, owner=owner, index=index)
+        analog = program(inputs.detach())
+    if not _wants_grad(inputs, rhs):
         return analog
-    surrogate = _quantized_linear(a, b.transpose(0, 1), None, simulator.config)
-    return _SurrogateGradient.apply(analog, surrogate)
+    return _SurrogateGradient.apply(analog, _linear_surrogate(inputs, rhs.T, None, program))
+
+
+def _batched_rhs(simulator, layout, owner):
+    """Products for a RHS with its own batch entries: the batch entries are grouped by
+    the RHS entry they broadcast from, in row-major order; each RHS entry is programmed
+    once and reads its group's stacked inputs; the results go back to batch order."""
+    left, right, batch = layout.left, layout.right, layout.batch
+    rhs_batch = right.shape[:-2]
+    padded = (1,) * (len(batch) - len(rhs_batch)) + tuple(rhs_batch)
+    owners = torch.arange(math.prod(rhs_batch)).reshape(padded).expand(batch).reshape(-1)
+    order = torch.argsort(owners, stable=True)
+    counts = torch.bincount(owners, minlength=math.prod(rhs_batch)).tolist()
+    inputs = left.expand(batch + left.shape[-2:]).reshape(-1, layout.rows, layout.reduction)
+    matrices = right.reshape(-1, layout.reduction, layout.columns)
+    device_order = order.to(inputs.device)
+    pieces = [
+        _read(simulator, inputs.index_select(0, members), matrices[entry], owner, entry, False)
+        for entry, members in enumerate(device_order.split(counts))
+    ]
+    grouped = torch.cat(pieces)
+    restore = torch.empty_like(order)
+    restore[order] = torch.arange(order.numel())
+    return grouped.index_select(0, restore.to(grouped.device))
 
 
 def _matmul(a, b, *, simulator, config, mode, cache_dir, out):
-    # Finiteness is checked on the device inside the fused product when it
-    # applies; every other route (and every error raised before the product)
-    # checks it on the host first, keeping the reference's error order.
-    _operands(a, b, finite=False)
+    _check_operands(a, b)
+    # Finiteness is checked before anything else can fail, as in the reference; the
+    # single-pass product defers it to the device, so errors raised before the product
+    # check it on the host first to keep that order.
     try:
-        left_vector, right_vector = a.ndim == 1, b.ndim == 1
-        left = a.unsqueeze(0) if left_vector else a
-        right = b.unsqueeze(-1) if right_vector else b
-        if left.shape[-1] != right.shape[-2]:
-            raise ValueError("A and B have incompatible reduction dimensions")
-        if left.ndim == 2 and right.ndim == 2:
-            batch = torch.Size()
-        else:
-            try:
-                batch = torch.broadcast_shapes(left.shape[:-2], right.shape[:-2])
-            except RuntimeError:
-                raise ValueError("A and B batch dimensions cannot broadcast") from None
-        rows, reduction, columns = left.shape[-2], left.shape[-1], right.shape[-1]
-        shape = batch + (() if left_vector else (rows,)) + (() if right_vector else (columns,))
-        _out(a, b, out, shape)
-        engine = _engine(a, simulator, config, mode, cache_dir)
+        layout = _layout(a, b)
+        _check_out(a, b, out, layout.shape)
+        engine = _resolve_simulator(a, simulator, config, mode, cache_dir)
     except Exception:
-        _finite(a, b)
+        _check_finite(a, b)
         raise
-    shared_rhs = all(size == 1 for size in right.shape[:-2])
-    empty = a.numel() == 0 or b.numel() == 0 or 0 in shape
-    fused = (
-        isinstance(engine, Simulator) and a.dtype in _FUSED_DTYPES and shared_rhs and not empty
-    )
-    if not fused:
-        _finite(a, b)
-    # Autocast is switched off around the product; when it is already off the
-    # context would change nothing and is skipped.
-    autocast_off = (
-        torch.autocast(device_type=a.device.type, enabled=False)
-        if torch.is_autocast_enabled(a.device.type) else contextlib.nullcontext()
-    )
+    shared = all(size == 1 for size in layout.right.shape[:-2])
+    empty = a.numel() == 0 or b.numel() == 0 or 0 in layout.shape
+    single_pass = shared and not empty and a.dtype in _SINGLE_PASS_DTYPES
+    if not single_pass:
+        _check_finite(a, b)
+    autocast_off = (torch.autocast(device_type=a.device.type, enabled=False)
+                    if torch.is_autocast_enabled(a.device.type) else contextlib.nullcontext())
     with autocast_off:
         if empty:
-            result = a.new_zeros(shape)
-            if torch.is_grad_enabled() and (a.requires_grad or b.requires_grad):
+            result = a.new_zeros(layout.shape)
+            if _wants_grad(a, b):
                 result = _SurrogateGradient.apply(result, torch.matmul(a.float(), b.float()))
+        elif shared:
+            rhs = layout.right.reshape(layout.reduction, layout.columns)
+            inputs = layout.left.expand(layout.batch + layout.left.shape[-2:])
+            result = _read(engine, inputs, rhs, b, (), single_pass).reshape(layout.shape)
         else:
-            if batch:
-                left = left.expand(batch + (rows, reduction))
-            rhs_batch = right.shape[:-2]
-            if shared_rhs:
-                rhs = right if right.ndim == 2 else right.reshape(reduction, columns)
-                cached = None if b.ndim == 2 else _rhs_view(engine, b, rhs, ())
-                result = _product(left, rhs, engine, cached, fused)
-            else:
-                groups = {}
-                padding = len(batch) - len(rhs_batch)
-                for index in itertools.product(*(range(size) for size in batch)):
-                    key = tuple(
-                        0 if size == 1 else index[padding + axis]
-                        for axis, size in enumerate(rhs_batch)
-                    )
-                    groups.setdefault(key, []).append(index)
-                outputs = {}
-                for key, indices in groups.items():
-                    inputs = torch.stack([left[index] for index in indices])
-                    rhs = right[key]
-                    values = _product(inputs, rhs, engine, _rhs_view(engine, b, rhs, key))
-                    outputs.update((index, values[row]) for row, index in enumerate(indices))
-                result = torch.stack(
-                    [outputs[index] for index in itertools.product(*(range(s) for s in batch))]
-                ).reshape(batch + (rows, columns))
-            result = result.reshape(shape)
-    if out is not None:
-        out.copy_(result)
-        return out
-    return result
+            result = _batched_rhs(engine, layout, b).reshape(layout.shape)
+    if out is None:
+        return result
+    out.copy_(result)
+    return out
 
 
 def mm(input, mat2, *, simulator=None, config=None, mode="default", cache_dir=None, out=None):

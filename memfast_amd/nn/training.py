@@ -1,28 +1,46 @@
-"""Hardware-aware training: analog forward values, FP32 surrogate gradients.
+"""Hardware-aware training: analog forward values, surrogate gradients.
 
-Restates memfast/nn/training.py.  Master weights and biases are ordinary
-Parameters; every forward reprograms the persistent analog buffers from them
-(so parameter and buffer identities stay stable for optimizers), runs the
-analog kernels, and attaches a surrogate whose gradient is used in backward:
+Behaviour of memfast/nn/training.py.  A trainable layer keeps ordinary master
+Parameters.  Every forward writes the current parameters into the layer's programmed
+matrices in place (identities of parameters and buffers never change, so optimizers
+and distributed wrappers see stable objects), reads the matrices on the GPU, and, when
+gradients are wanted, ties the analog values to a surrogate whose gradient backward
+uses:
 
-* ``gradient_mode="quantized"`` (default): dx uses dequantized grouped
-  weights, dw uses dequantized grouped inputs, quantizers pass gradients
-  through unchanged;
-* ``gradient_mode="digital"``: derivatives of the unquantized digital layer.
+* ``gradient_mode="quantized"`` (default): the surrogate multiplies dequantized
+  operands, and the quantizers pass gradients through unchanged.  dx therefore uses the
+  dequantized grouped weights and dw the dequantized grouped inputs.  The weights'
+  values are the program just written (its codes times their read scales).  The inputs'
+  values come from the GPU quantizer's codes and read scales under dynamic grouped
+  scales, whatever fixed scale the forward read used;
+* ``gradient_mode="digital"``: the unquantized layer's derivatives.
 
-Neither mode differentiates device effects.  Surrogate arithmetic is FP32.
+Neither mode differentiates device effects (noise, faults, the ADC).  The surrogate
+computes in FP32 with autocast off, and gradients reach leaf Parameters in their own
+dtype.  Convolutions form their surrogate on unfolded patches, one programmed matrix
+per group, so input gradients fold back over overlapping patches.
 """
 
 import torch
 from torch import nn
 from torch.nn import functional as F
 
-from ..quantization import grouped_quantize
+from .. import hip
+from ..quantization import dequantize_inputs, dequantize_program
 from .convolution import AnalogConv2d
+
+GRADIENT_MODES = ("quantized", "digital")
+
+
+def _validate_gradient_mode(mode):
+    if not isinstance(mode, str) or mode not in GRADIENT_MODES:
+        raise ValueError("gradient_mode must be quantized or digital")
+    return mode
 
 
 class _SurrogateGradient(torch.autograd.Function):
-    """Forward returns the analog value; backward routes the gradient to the surrogate."""
+    """Forward passes the analog value through; backward hands the incoming gradient to
+    the surrogate (in the surrogate's dtype) and none to the analog value."""
 
     @staticmethod
     def forward(ctx, analog, surrogate):
@@ -34,60 +52,72 @@ class _SurrogateGradient(torch.autograd.Function):
         return None, grad_output.to(ctx.surrogate_dtype)
 
 
+def _through(value, replacement):
+    """``replacement``'s values with the identity derivative with respect to ``value``."""
+    return value + (replacement - value).detach()
+
+
 @torch.no_grad()
-def _program(matrix, weight, bias):
-    """Reprogram ``matrix`` in place, keeping its name, read counter and selections."""
-    fresh = matrix.simulator.map(weight, bias=bias, name=matrix.name)
-    matrix.packed.copy_(fresh.packed)
-    matrix.weight_scale.copy_(fresh.weight_scale)
-    if matrix.bias is not None:
-        matrix.bias.copy_(fresh.bias)
-    matrix._kernel_codes = fresh._kernel_codes if fresh._kernel_codes is None else (
-        matrix._codes_key(), fresh._kernel_codes[1]
-    )
+def _dequantized_inputs(flat, config):
+    """FP32 grouped-quantized values of ``flat`` [N, K] (dynamic scales), from the GPU
+    quantizer's codes and read scales."""
+    if flat.numel() == 0:
+        return flat.float()
+    q, xscale = hip.input_tiles(flat.detach(), config)
+    return dequantize_inputs(q, xscale, config, flat.shape[1])
 
 
-def _parameter(value, device):
+@torch.no_grad()
+def _dequantized_weights(matrix):
+    """FP32 physical [K, O] weights of ``matrix``'s current program."""
+    return dequantize_program(matrix.packed, matrix.weight_scale, matrix.config,
+                              matrix.in_features, matrix.out_features)
+
+
+def _linear_surrogate(x, weight, bias, matrix):
+    """Quantized-operand surrogate of ``x @ weight.T + bias`` read through ``matrix``
+    (programmed from ``weight``); leading dimensions of ``x`` are flattened first."""
+    flat = x.reshape(-1, matrix.in_features).float()
+    inputs = _through(flat, _dequantized_inputs(flat, matrix.config))
+    weights = _through(weight.float().T, _dequantized_weights(matrix))
+    value = inputs @ weights
+    if bias is not None:
+        value = value + bias.float()
+    return value.reshape(*x.shape[:-1], matrix.out_features)
+
+
+def _master(value, device):
+    """A trainable copy of a source layer's Parameter on ``device`` (None stays None)."""
     if value is None:
         return None
     return nn.Parameter(value.detach().to(device).clone(), requires_grad=value.requires_grad)
 
 
-def _validate_gradient_mode(mode):
-    if not isinstance(mode, str) or mode not in ("quantized", "digital"):
-        raise ValueError("gradient_mode must be quantized or digital")
-    return mode
+class _HardwareAware(nn.Module):
+    """Shared forward of the trainable layers: program, read, attach the surrogate.
+
+    Subclasses provide ``_programs`` (each programmed matrix with its block of the
+    master parameters), ``_read`` (the analog forward of detached inputs) and the two
+    surrogates."""
+
+    def _program(self):
+        """Write the master parameters into the programmed matrices."""
+        for matrix, weight, bias in self._programs():
+            matrix._reprogram(weight, bias)
+
+    def forward(self, x):
+        with torch.autocast(device_type=x.device.type, enabled=False):
+            self._program()
+            analog = self._read(x.detach())
+            if not torch.is_grad_enabled():
+                return analog
+            surrogate = (self._quantized_surrogate(x) if self.gradient_mode == "quantized"
+                         else self._digital_surrogate(x))
+        return _SurrogateGradient.apply(analog, surrogate)
 
 
-def _quantized_operand(value, bits, granularity, config, reference=None, *, signed=True):
-    """Straight-through dequantized operand in FP32."""
-    operand = value.float()
-    if value.numel() == 0:
-        return operand
-    with torch.no_grad():
-        source = value if reference is None else reference
-        code, scale = grouped_quantize(source.detach(), bits, granularity, config.bw_e,
-                                       signed=signed)
-        dequantized = (code * scale).float()
-    return operand + (dequantized - operand).detach()
-
-
-def _quantized_linear(x, weight, bias, config, input_reference=None):
-    """FP32 surrogate of the analog linear map: quantized inputs @ quantized weights."""
-    flat = x.reshape(-1, weight.shape[1])
-    reference = None if input_reference is None else input_reference.reshape(-1, weight.shape[1])
-    inputs = _quantized_operand(flat, config.activation_bits, config.input_quant_gran, config,
-                                reference=reference)
-    weights = _quantized_operand(weight.T, config.weight_bits, config.weight_quant_gran, config,
-                                 signed=config.weight_signed)
-    output = inputs @ weights
-    if bias is not None:
-        output = output + bias.to(output.dtype)
-    return output.reshape(*x.shape[:-1], weight.shape[0])
-
-
-class TrainableAnalogLinear(nn.Module):
-    """Linear layer with an analog forward and a selectable STE backward."""
+class TrainableAnalogLinear(_HardwareAware):
+    """``nn.Linear`` with an analog forward and surrogate gradients."""
 
     def __init__(self, source, simulator, *, name="linear", gradient_mode="quantized"):
         super().__init__()
@@ -95,81 +125,85 @@ class TrainableAnalogLinear(nn.Module):
             raise TypeError("source must be torch.nn.Linear")
         self.gradient_mode = _validate_gradient_mode(gradient_mode)
         self.in_features, self.out_features = source.in_features, source.out_features
-        self.weight = _parameter(source.weight, simulator.device)
-        self.register_parameter("bias", _parameter(source.bias, simulator.device))
+        self.weight = _master(source.weight, simulator.device)
+        self.register_parameter("bias", _master(source.bias, simulator.device))
         self.matrix = simulator.map(self.weight, bias=self.bias, name=name)
         self.train(source.training)
 
-    def forward(self, x):
-        with torch.autocast(device_type=x.device.type, enabled=False):
-            _program(self.matrix, self.weight, self.bias)
-            analog = self.matrix(x.detach())
-            if not torch.is_grad_enabled():
-                return analog
-            if self.gradient_mode == "quantized":
-                surrogate = _quantized_linear(x, self.weight, self.bias, self.matrix.config)
-            else:
-                bias = None if self.bias is None else self.bias.float()
-                surrogate = F.linear(x.float(), self.weight.float(), bias)
-        return _SurrogateGradient.apply(analog, surrogate)
+    def _programs(self, weight=None):
+        yield self.matrix, self.weight if weight is None else weight, self.bias
+
+    def _read(self, x):
+        return self.matrix(x)
+
+    def _quantized_surrogate(self, x):
+        return _linear_surrogate(x, self.weight, self.bias, self.matrix)
+
+    def _digital_surrogate(self, x):
+        return F.linear(x.float(), self.weight.float(),
+                        None if self.bias is None else self.bias.float())
 
 
-class TrainableAnalogConv2d(nn.Module):
-    """Grouped Conv2d with an analog forward and a selectable STE backward."""
+_CONV_ATTRIBUTES = ("in_channels", "out_channels", "kernel_size", "stride", "padding",
+                    "dilation", "groups", "padding_mode")
+
+
+class TrainableAnalogConv2d(_HardwareAware):
+    """Grouped ``nn.Conv2d`` with an analog forward and surrogate gradients."""
 
     def __init__(self, source, simulator, *, name="conv", gradient_mode="quantized"):
         super().__init__()
         if not isinstance(source, nn.Conv2d):
             raise TypeError("source must be torch.nn.Conv2d")
         self.gradient_mode = _validate_gradient_mode(gradient_mode)
-        self.weight = _parameter(source.weight, simulator.device)
-        self.register_parameter("bias", _parameter(source.bias, simulator.device))
+        self.weight = _master(source.weight, simulator.device)
+        self.register_parameter("bias", _master(source.bias, simulator.device))
         self.analog = AnalogConv2d(source, simulator, name=name)
-        for attr in ("in_channels", "out_channels", "kernel_size", "stride", "padding",
-                     "dilation", "groups", "padding_mode"):
-            setattr(self, attr, getattr(source, attr))
+        for attribute in _CONV_ATTRIBUTES:
+            setattr(self, attribute, getattr(source, attribute))
         self.train(source.training)
 
-    def forward(self, x):
-        with torch.autocast(device_type=x.device.type, enabled=False):
-            return self._forward(x)
-
-    def _forward(self, x):
-        per_group = self.out_channels // self.groups
+    def _programs(self, weight=None):
+        """(matrix, [O/g, Cin/g*kh*kw] block of ``weight`` (the master weight by default),
+        bias block or None) of every convolution group."""
+        weight = self.weight if weight is None else weight
+        width = self.out_channels // self.groups
         for group, matrix in enumerate(self.analog.matrices):
-            block = slice(group * per_group, (group + 1) * per_group)
-            bias = None if self.bias is None else self.bias[block]
-            _program(matrix, self.weight[block].flatten(1), bias)
-        analog = self.analog(x.detach())
-        if not torch.is_grad_enabled():
-            return analog
-        original = x.detach()
+            rows = slice(group * width, (group + 1) * width)
+            yield matrix, weight[rows].flatten(1), None if self.bias is None else self.bias[rows]
+
+    def _read(self, x):
+        return self.analog(x)
+
+    def _padded(self, x):
+        """FP32 input and the padding left for unfold/conv2d (non-zero padding modes pad
+        explicitly, as the analog forward does)."""
         x = x.float()
-        padding = self.padding
-        if self.padding_mode != "zeros":
-            ph, pw = padding
-            x = F.pad(x, (pw, pw, ph, ph), mode=self.padding_mode)
-            original = F.pad(original, (pw, pw, ph, ph), mode=self.padding_mode)
-            padding = (0, 0)
-        if self.gradient_mode == "quantized":
-            patches = F.unfold(x, self.kernel_size, self.dilation, padding, self.stride)
-            reference = (
-                patches.detach() if original.dtype == torch.float32
-                else F.unfold(original, self.kernel_size, self.dilation, padding, self.stride)
-            )
-            size = self.weight[0].numel()
-            pieces = []
-            for group, matrix in enumerate(self.analog.matrices):
-                block = slice(group * per_group, (group + 1) * per_group)
-                bias = None if self.bias is None else self.bias[block]
-                cols = slice(group * size, (group + 1) * size)
-                pieces.append(_quantized_linear(
-                    patches[:, cols].transpose(1, 2), self.weight[block].flatten(1), bias,
-                    matrix.config, input_reference=reference[:, cols].transpose(1, 2),
-                ))
-            surrogate = torch.cat(pieces, dim=-1).transpose(1, 2).reshape(analog.shape)
-        else:
-            bias = None if self.bias is None else self.bias.float()
-            surrogate = F.conv2d(x, self.weight.float(), bias, self.stride, padding,
-                                 self.dilation, self.groups)
-        return _SurrogateGradient.apply(analog, surrogate)
+        if self.padding_mode == "zeros":
+            return x, self.padding
+        ph, pw = self.padding
+        return F.pad(x, (pw, pw, ph, ph), mode=self.padding_mode), (0, 0)
+
+    def _quantized_surrogate(self, x):
+        source, padding = self._padded(x)
+        patches = F.unfold(source, self.kernel_size, self.dilation, padding, self.stride)
+        size = self.weight[0].numel()
+        pieces = [
+            _linear_surrogate(patches[:, g * size:(g + 1) * size].transpose(1, 2), weight, bias,
+                              matrix)
+            for g, (matrix, weight, bias) in enumerate(self._programs())
+        ]
+        merged = torch.cat(pieces, dim=-1).transpose(1, 2)
+        spatial = [(extent + 2 * pad - dil * (k - 1) - 1) // step + 1
+                   for extent, pad, dil, k, step in zip(x.shape[-2:], self.padding, self.dilation,
+                                                        self.kernel_size, self.stride)]
+        return merged.reshape(x.shape[0], self.out_channels, *spatial)
+
+    def _digital_surrogate(self, x):
+        source, padding = self._padded(x)
+        return F.conv2d(source, self.weight.float(),
+                        None if self.bias is None else self.bias.float(), self.stride, padding,
+                        self.dilation, self.groups)
+
+
+__all__ = ["TrainableAnalogLinear", "TrainableAnalogConv2d", "GRADIENT_MODES"]

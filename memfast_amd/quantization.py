@@ -1,111 +1,98 @@
-"""Quantization and packing with independent rectangular scale groups.
+"""Read geometry, imported-parameter handling, packing, and the inverse of the quantizers.
 
-Same public functions as the reference's memfast/quantization.py.  The hot
-path (``weight_tiles``/``input_tiles``: quantize, slice-pack, gather per-read
-scales) runs in the gfx950 kernels of libmemfast_hip.so with IEEE FP32
-division and round-half-even, bit-identical to the reference CPU path.
+Quantization itself runs only in the gfx950 kernels of libmemfast_hip.so:
+``input_tiles`` and ``weight_tiles`` below (memfast/quantization.py:82-137) quantize
+rectangular scale groups with IEEE division and round-half-even, bit for bit as the
+reference's CPU routine does, and write the codes straight into array tiles.  There
+is no host quantizer in this package.
 
-``grouped_quantize`` remains a device-agnostic torch routine: the product
-uses it only for the FP32 surrogate gradient of hardware-aware training
-(memfast/nn/training.py:72-93), never for the analog forward.
+What remains here is tensor bookkeeping around those kernels:
+* the read geometry: which read every physical row belongs to and where each read
+  starts (memfast/quantization.py:76-79);
+* imported scales and zero points for ``Simulator.map_quantized``: broadcasting and
+  validation (memfast/quantization.py:47-73) and packing of imported integer codes
+  (memfast/quantization.py:94-112);
+* dequantization, codes times their read's scale, which the hardware-aware training
+  surrogate uses instead of quantizing its operands a second time.
 """
 
 import math
 
 import torch
-from torch.nn import functional as F
 
 from . import hip
 
 
-def grouped_quantize(value, bits, granularity, bw_e=None, *, signed=True):
-    """INT/BFP codes and expanded scales of rectangular groups (quantization.py:9-44)."""
-    dtype = torch.float64 if bits > 8 or bw_e is not None else torch.float32
-    value = value.to(dtype)
-    if not torch.isfinite(value).all():
-        raise ValueError(f"quantized values must be finite in {dtype}")
-    if not signed and ((value < 0).any() or bw_e is not None):
-        raise ValueError(
-            "unsigned floating weights must be nonnegative INT values; "
-            "use map_quantized with zero_points for affine weights"
-        )
-    rows, cols = value.shape
-    gr = rows if granularity[0] is None else min(granularity[0], rows)
-    gc = cols if granularity[1] is None else min(granularity[1], cols)
-    nr, nc = math.ceil(rows / gr), math.ceil(cols / gc)
-    blocks = F.pad(value, (0, nc * gc - cols, 0, nr * gr - rows)).reshape(nr, gr, nc, gc)
-    peak = blocks.abs().amax((1, 3), keepdim=True)
-    upper = (1 << (bits - int(signed))) - 1
-    if bw_e is None:
-        scale = torch.where(peak > 0, peak, torch.ones_like(peak)) / upper
-        tiny = torch.finfo(dtype).smallest_normal * torch.finfo(dtype).eps
-        scale = scale.clamp_min(tiny)
-        lower = -upper if signed else 0
-    else:
-        limit = (1 << (bw_e - 1)) - 1
-        exponent = peak.clamp_min(torch.finfo(dtype).tiny).log2().floor().clamp(1 - limit, limit)
-        scale = torch.pow(2.0, exponent + 2 - bits)
-        lower = -(1 << (bits - 1))
-    code = (blocks / scale).round().clamp_(lower, upper)
-    code = code.reshape(nr * gr, nc * gc)[:rows, :cols].to(torch.int64)
-    full = scale.expand(nr, gr, nc, gc).reshape(nr * gr, nc * gc)[:rows, :cols]
-    return code, full
-
-
-def expanded_parameter(value, shape, device, dtype, name, *, positive=False):
-    """Broadcast a scalar/tensor parameter to ``shape`` with finiteness checks."""
-    if torch.is_tensor(value):
-        original = torch.as_tensor(value, device=device)
-    else:
-        original = torch.as_tensor(value, device=device, dtype=torch.float64)
-    if original.is_complex() or not torch.isfinite(original).all():
-        raise ValueError(f"{name} must be real and finite")
-    if positive and (original < 0).any():
-        raise ValueError(f"{name} must be finite and nonnegative")
-    converted = original.to(dtype)
-    try:
-        converted = torch.broadcast_to(converted, shape)
-    except RuntimeError:
-        raise ValueError(f"{name} must broadcast to {tuple(shape)}") from None
-    if not torch.isfinite(converted).all() or (positive and (converted < 0).any()):
-        raise ValueError(f"{name} must be finite" + (" and nonnegative" if positive else ""))
-    return converted
-
-
-def check_read_scales(value, config, name):
-    """Reject scales or zero points that change inside one ADC read."""
-    rows = config.array_size[0]
-    index = torch.arange(value.shape[0], device=value.device)
-    start = (index // rows) * rows + ((index % rows) // config.read_rows) * config.read_rows
-    if not torch.equal(value, value[start]):
-        raise ValueError(f"{name} changes inside an ADC read; reduce rows_per_read")
+# ---------------------------------------------------------------------------
+# Read geometry
+# ---------------------------------------------------------------------------
+def row_reads(rows, config, device):
+    """Index of the ADC read (array i, read j -> i*Gr + j) holding each of ``rows`` rows."""
+    row = torch.arange(rows, device=device)
+    array_rows = config.array_size[0]
+    return row // array_rows * config.reads_per_array + row % array_rows // config.read_rows
 
 
 def read_starts(partitions, config, device):
-    """First physical row of each ADC read (quantization.py:76-79)."""
-    base = torch.arange(partitions, device=device)[:, None] * config.array_size[0]
-    offsets = torch.arange(config.reads_per_array, device=device)[None] * config.read_rows
-    return (base + offsets).flatten()
+    """First physical row of each ADC read of ``partitions`` arrays (quantization.py:76-79)."""
+    read = torch.arange(partitions * config.reads_per_array, device=device)
+    per_array = config.reads_per_array
+    return read // per_array * config.array_size[0] + read % per_array * config.read_rows
+
+
+def check_read_scales(value, config, name):
+    """Reject a [rows, cols] scale or zero-point table that changes inside one ADC read."""
+    reads = row_reads(value.shape[0], config, value.device)
+    starts = read_starts(math.ceil(value.shape[0] / config.array_size[0]), config, value.device)
+    if not torch.equal(value, value[starts[reads]]):
+        raise ValueError(f"{name} changes inside an ADC read; reduce rows_per_read")
+
+
+# ---------------------------------------------------------------------------
+# Imported parameters (Simulator.map_quantized)
+# ---------------------------------------------------------------------------
+def expanded_parameter(value, shape, device, dtype, name, *, positive=False):
+    """Broadcast a scalar or tensor parameter to ``shape`` in ``dtype``; the reference's
+    checks (memfast/quantization.py:47-64): real and finite as given, nonnegative when
+    ``positive``, broadcastable, and still finite after the cast."""
+    suffix = " and nonnegative" if positive else ""
+    given = torch.as_tensor(value, device=device,
+                            dtype=None if torch.is_tensor(value) else torch.float64)
+    if given.is_complex() or not bool(torch.isfinite(given).all()):
+        raise ValueError(f"{name} must be real and finite")
+    if positive and bool((given < 0).any()):
+        raise ValueError(f"{name} must be finite and nonnegative")
+    try:
+        cast = torch.broadcast_to(given.to(dtype), shape)
+    except RuntimeError:
+        raise ValueError(f"{name} must broadcast to {tuple(shape)}") from None
+    if not bool(torch.isfinite(cast).all()) or (positive and bool((cast < 0).any())):
+        raise ValueError(f"{name} must be finite{suffix}")
+    return cast
 
 
 def pack_weight(code, scale, config):
-    """Pack logical [K,O] integer codes (no scale estimation); quantization.py:94-112.
-
-    Integer masking and reshaping only, so it is exact on any device.
-    """
+    """Tiles of imported integer codes: packed [m, p, R, C] (two's complement masked to
+    weight_bits) and per-read scales [m*Gr, p, C], taken at each read's first row; padded
+    rows and columns repeat the last logical row's and column's scale
+    (memfast/quantization.py:94-112).  No scale is estimated."""
     k, o = code.shape
-    r, c = config.array_size
-    m, p = math.ceil(k / r), math.ceil(o / c)
-    scale = scale.to(torch.float64 if config.wide else torch.float32)
-    padded = F.pad(code, (0, p * c - o, 0, m * r - k))
+    rows, cols = config.array_size
+    m, p = math.ceil(k / rows), math.ceil(o / cols)
+    grid = code.new_zeros((m * rows, p * cols))
+    grid[:k, :o] = code & ((1 << config.weight_bits) - 1)
     store = torch.int64 if config.wide_codes else torch.uint8
-    packed = (padded & ((1 << config.weight_bits) - 1)).to(store)
-    packed = packed.reshape(m, r, p, c).permute(0, 2, 1, 3).contiguous()
-    grown = F.pad(scale[None, None], (0, p * c - o, 0, m * r - k), mode="replicate")[0, 0]
-    scales = grown[read_starts(m, config, code.device)]
-    return packed, scales.reshape(m * config.reads_per_array, p, c).contiguous()
+    packed = grid.view(m, rows, p, cols).transpose(1, 2).contiguous().to(store)
+    table = scale.to(torch.float64 if config.wide else torch.float32)
+    first_rows = read_starts(m, config, code.device).clamp_max(k - 1)
+    columns = torch.arange(p * cols, device=code.device).clamp_max(o - 1)
+    scales = table[first_rows][:, columns]
+    return packed, scales.reshape(m * config.reads_per_array, p, cols).contiguous()
 
 
+# ---------------------------------------------------------------------------
+# The gfx950 quantizers and their inverse
+# ---------------------------------------------------------------------------
 def weight_tiles(weight, config):
     """PyTorch-layout [O,K] weights -> (packed [m,p,R,C], scales [m*Gr,p,C]) on the GPU."""
     packed, _, scales = hip.weight_tiles(weight, config, transposed=False)
@@ -117,7 +104,38 @@ def input_tiles(value, config, fixed_scale=None):
     return hip.input_tiles(value, config, fixed_scale)
 
 
+def _signed(codes, bits):
+    """Two's complement ``bits``-bit codes (any integer storage) as int32 values."""
+    value = codes.to(torch.int64) & ((1 << bits) - 1)
+    return (value ^ (1 << (bits - 1))) - (1 << (bits - 1))
+
+
+def dequantize_inputs(q, xscale, config, k):
+    """Codes q [N, m, R] and per-read scales [N, m*Gr] -> FP32 values [N, k].
+
+    Equals code * scale of the reference's grouped quantizer for every row (scale
+    groups never cross a read, so a row's read scale is its group scale), formed in the
+    scale's precision and rounded to FP32 as memfast/nn/training.py:62-72 does."""
+    codes = _signed(q.reshape(q.shape[0], -1)[:, :k], config.activation_bits)
+    scales = xscale[:, row_reads(k, config, q.device)]
+    return (codes.to(scales.dtype) * scales).float()
+
+
+def dequantize_program(packed, weight_scale, config, k, o):
+    """A program's packed codes [m, p, R, C] and read scales [m*Gr, p, C] -> FP32 [k, o]
+    physical weights (codes are signed unless ``config.weight_signed`` is False)."""
+    m, p, rows, cols = packed.shape
+    grid = packed.transpose(1, 2).reshape(m * rows, p * cols)[:k, :o]
+    if config.weight_signed:
+        codes = _signed(grid, config.weight_bits)
+    else:
+        codes = grid.to(torch.int64) & ((1 << config.weight_bits) - 1)
+    table = weight_scale.reshape(m * config.reads_per_array, p * cols)[:, :o]
+    scales = table[row_reads(k, config, packed.device)]
+    return (codes.to(scales.dtype) * scales).float()
+
+
 __all__ = [
-    "grouped_quantize", "expanded_parameter", "check_read_scales", "read_starts",
-    "pack_weight", "weight_tiles", "input_tiles",
+    "row_reads", "read_starts", "check_read_scales", "expanded_parameter", "pack_weight",
+    "weight_tiles", "input_tiles", "dequantize_inputs", "dequantize_program",
 ]

@@ -1,32 +1,40 @@
-"""Mapping, execution, schedule selection and the persistent selection cache.
+"""Programming, reading, read events and the functional API's program cache.
 
-Drop-in for the reference's memfast/simulator.py.  ``Simulator`` and
-``AnalogMatrix`` keep their constructor arguments, buffers, checkpoint state,
-read-event bookkeeping and error behaviour; execution goes to the gfx950
-kernels of libmemfast_hip.so (memfast_amd/hip.py) instead of the reference's
-CPU runner or NVRTC kernels.  There is no CPU execution path.
+Drop-in for the reference's memfast/simulator.py.  ``Simulator`` and ``AnalogMatrix``
+keep their constructor arguments, buffers, checkpoint state, read-event bookkeeping and
+error behaviour.  Reading goes to the gfx950 kernels of libmemfast_hip.so
+(memfast_amd/hip.py); there is no CPU execution path.
 
-Execution (``AnalogMatrix._execute``, simulator.py:561-616 in the reference):
-one fused launch reads every array tile, converts every slice pair, restores
-the scales and sums the reads in torch's CPU order, writing only [N, p*C].
+A read (``AnalogMatrix._execute``, memfast/simulator.py:561-616 in the reference) is
+one fused launch: every array tile is read, every slice pair converted, the scales
+restored and the reads summed in torch's CPU order, and only [N, p*C] is written.
+Errors the reference finds with host-side scans (non-finite inputs, a non-finite FP32
+result that needs the FP64 retry) are flagged in a device status word that is read
+once per call, before the read event advances.
+
+Tuned mode lives in memfast_amd/tuning.py, checkpoint validation in
+memfast_amd/checkpoint.py.
 """
 
 import hashlib
-import json
 import math
-import time
 import weakref
 from dataclasses import asdict
 from functools import lru_cache
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 from torch import nn
 
-from . import hip, host_order, tuning
+from . import checkpoint, hip, host_order, tuning
 from .config import Config
-from .quantization import check_read_scales, expanded_parameter, pack_weight, read_starts
+from .quantization import (_signed, check_read_scales, expanded_parameter, pack_weight,
+                           read_starts, row_reads)
 from .tuning import default_schedule, schedule_grid
+
+_CODE_DTYPES = (torch.uint8, torch.int8, torch.int16, torch.int32, torch.int64)
+_EVENT_LIMIT = 1 << 63
 
 
 def source_hash():
@@ -41,15 +49,16 @@ def source_hash():
 
 
 def restore_scales(value, input_scale, weight_scale):
-    """Overflow-safe FP64 value * xs * ws via frexp/ldexp (memfast/simulator.py:57-66)."""
-    vm, ve = torch.frexp(value.double())
-    xm, xe = torch.frexp(input_scale.double())
-    wm, we = torch.frexp(weight_scale.double())
-    mantissa = vm * xm * wm
-    exponent = ve + xe + we
-    first = exponent.clamp(-1022, 1023)
-    result = torch.ldexp(torch.ldexp(mantissa, first), exponent - first)
-    return torch.where(mantissa == 0, torch.zeros_like(result), result)
+    """value * input_scale * weight_scale in FP64 without intermediate overflow
+    (memfast/simulator.py:57-66): mantissas multiply, exponents add, and the product is
+    rebuilt with two ldexp steps so that an exponent beyond the FP64 range saturates only
+    when the result itself does."""
+    parts = [torch.frexp(t.double()) for t in (value, input_scale, weight_scale)]
+    mantissa = parts[0][0] * parts[1][0] * parts[2][0]
+    exponent = parts[0][1] + parts[1][1] + parts[2][1]
+    head = exponent.clamp(-1022, 1023)
+    rebuilt = torch.ldexp(torch.ldexp(mantissa, head), exponent - head)
+    return torch.where(mantissa == 0, torch.zeros_like(rebuilt), rebuilt)
 
 
 def _hip_device(device):
@@ -65,29 +74,96 @@ def _hip_device(device):
     return torch.device("cuda", index)
 
 
-class Simulator:
-    """Fixed default execution or a traversal of the declared kernel grid.
+@lru_cache(maxsize=4096)
+def _name_tag(name):
+    """32-bit seed tag of a matrix name (first four bytes of its SHA-256, little-endian;
+    memfast/simulator.py:428-429)."""
+    return int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little")
 
-    Interface of memfast/simulator.py:69-347.  ``tuned`` selects per input
-    shape, saves the winner under ``cache_dir`` and revalidates cached winners
-    against default execution without timing candidates again.
+
+# ---------------------------------------------------------------------------
+# Functional RHS programs
+# ---------------------------------------------------------------------------
+class _CacheEntry(NamedTuple):
+    owner: weakref.ref     # the caller's RHS tensor, held weakly
+    geometry: tuple        # its shape, strides, offset, storage and dtype when programmed
+    program: "AnalogMatrix"
+
+
+def _geometry(tensor):
+    return (tuple(tensor.shape), tuple(tensor.stride()), tensor.storage_offset(),
+            tensor.data_ptr(), tensor.dtype, tensor.device, tensor.is_neg())
+
+
+class _ProgramCache(dict):
+    """Programs of the functional API's right-hand matrices, keyed by the caller's tensor
+    (held weakly) and the RHS entry of a batched operand.
+
+    memfast/simulator.py:133-171 with memfast/functional.py:94-126: each call reprograms
+    the RHS (in-place edits need not advance a tensor's version).  A program of the same
+    tensor with the same geometry, configuration and device is kept when its codes and
+    scales are unchanged; a changed program of a rank-two RHS takes over the old one's
+    name and read-event counter.  A RHS read through a view of the caller's tensor (a
+    vector, or a batched operand) whose tensor changed geometry is a new RHS.  Entries
+    drop out when their tensor is freed."""
+
+    def __init__(self, simulator):
+        super().__init__()
+        self._simulator = weakref.ref(simulator)
+
+    def program(self, owner, index=()):
+        """The program kept for ``owner`` (entry ``index``), or None."""
+        entry = self.get((id(owner), index))
+        return None if entry is None or entry.owner() is not owner else entry.program
+
+    def previous(self, rhs, owner, index):
+        """(program last made for this RHS or None, whether it may be kept)."""
+        previous = self.program(owner, index)
+        if previous is None:
+            return None, False
+        same_layout = self[(id(owner), index)].geometry == _geometry(owner)
+        if not same_layout and owner is not rhs:
+            return None, False
+        simulator = self._simulator()
+        keepable = (same_layout and previous.config == simulator.config
+                    and previous.packed.device == simulator.device)
+        return previous, keepable
+
+    def remember(self, owner, index, program):
+        key = (id(owner), index)
+        cache_ref = weakref.ref(self)
+
+        def forget(reference):
+            cache = cache_ref()
+            if cache is not None and key in cache and cache[key].owner is reference:
+                del cache[key]
+
+        self[key] = _CacheEntry(weakref.ref(owner, forget), _geometry(owner), program)
+
+
+class Simulator:
+    """Configuration, device, and the choice of fixed defaults or a tuned schedule.
+
+    Interface of memfast/simulator.py:69-347.  ``tuned`` selects a schedule per input
+    shape, saves the winner under ``cache_dir`` and revalidates cached winners against
+    the default schedule (memfast_amd/tuning.py).
     """
 
     def __init__(self, config=None, *, mode="default", device=None, cache_dir=None,
                  workspace_mb=1024):
-        self.config = Config() if config is None else config
-        if not isinstance(self.config, Config):
+        config = Config() if config is None else config
+        if not isinstance(config, Config):
             raise TypeError("config must be Config")
         if mode not in ("default", "tuned"):
             raise ValueError("mode must be default or tuned")
-        if isinstance(workspace_mb, bool) or not isinstance(workspace_mb, (int, float)):
+        budget_ok = (isinstance(workspace_mb, (int, float)) and not isinstance(workspace_mb, bool)
+                     and math.isfinite(workspace_mb) and workspace_mb > 0)
+        if not budget_ok:
             raise ValueError("workspace_mb must be positive and finite")
-        if not math.isfinite(workspace_mb) or workspace_mb <= 0:
-            raise ValueError("workspace_mb must be positive and finite")
-        self.mode = mode
-        requested = device if device is not None else "cuda"
+        requested = "cuda" if device is None else device
         if torch.device(requested).type not in ("cpu", "cuda"):
             raise ValueError("device must be cpu or cuda")
+        self.config, self.mode = config, mode
         self.device = _hip_device(requested)
         host_order.warn_if_different()
         self.cache_dir = Path(cache_dir) if cache_dir is not None else hip.cache_root() / "tuning"
@@ -96,15 +172,28 @@ class Simulator:
         self._selections = {}
         self._fingerprint = None
         self._next_id = 0
-        self._matrix_cache = {}
+        self._matrix_cache = _ProgramCache(self)
+
+    def _next_name(self):
+        name = f"matrix.{self._next_id}"
+        self._next_id += 1
+        return name
+
+    def _relocated(self, device):
+        """A simulator with this one's configuration, mode, cache and budget on ``device``."""
+        return Simulator(self.config, mode=self.mode, device=device, cache_dir=self.cache_dir,
+                         workspace_mb=self.workspace_bytes / 1024**2)
 
     # -- programming ---------------------------------------------------------
     def map(self, weight, *, bias=None, name=None, _tiles=None):
         """Low-level layer-weight adapter using PyTorch [O,K] weight layout."""
-        if name is None:
-            name = f"matrix.{self._next_id}"
-            self._next_id += 1
-        return AnalogMatrix(weight, self, bias=bias, name=name, _tiles=_tiles)
+        return AnalogMatrix(weight, self, bias=bias, name=name or self._next_name(),
+                            _tiles=_tiles)
+
+    def map_quantized(self, codes, scales, *, zero_points=None, bias=None, name=None):
+        """Import integer [O,K] weights as ``scales * (codes - zero_points)``."""
+        return AnalogMatrix(codes, self, bias=bias, name=name or self._next_name(),
+                            scales=scales, zero_points=zero_points)
 
     def mm(self, input, mat2, *, out=None):
         """Simulate a two-dimensional matrix product, following torch.mm."""
@@ -118,143 +207,84 @@ class Simulator:
 
         return matmul(input, other, simulator=self, out=out)
 
-    def _matrix_for(self, matrix, tiles=None):
-        """Reprogram the RHS and reuse the cached program while codes and scales agree.
+    def report(self):
+        return dict(mode=self.mode, device=str(self.device), config=asdict(self.config),
+                    selections=self.records)
 
-        Same policy as memfast/simulator.py:133-171: programming is repeated
-        every call (catching in-place edits that bypass tensor versions); the
-        old program, its name and its read-event counter survive if unchanged.
-        With ``tiles`` (codes already quantized by ``_product``) the program of
-        the same unchanged tensor takes the new codes in place: a changed
-        program would inherit the same name and event counter, so both cases
-        of the reference read identically without comparing codes on the host.
-        """
-        identity = id(matrix)
-        record = self._matrix_cache.get(identity)
-        same_tensor = record is not None and record[0]() is matrix
-        metadata = (
-            tuple(matrix.shape), tuple(matrix.stride()), matrix.storage_offset(),
-            matrix.data_ptr(), matrix.dtype, matrix.device,
-        )
-        previous = record[2] if same_tensor else None
-        reusable = (
-            same_tensor
-            and record[1] == metadata
-            and previous.config == self.config
-            and previous.packed.device == self.device
-        )
-        if tiles is not None and reusable and previous._accepts(tiles):
+    def _matrix_for(self, rhs, tiles=None, *, owner=None, index=()):
+        """The program of a functional RHS [K, O] read from ``owner`` (the caller's
+        tensor, ``rhs`` itself by default) at batch entry ``index``
+        (memfast/simulator.py:133-171).
+
+        ``tiles`` are the RHS's freshly quantized (packed, packed_t, wscale); a keepable
+        program takes them in place, which reads exactly as the reference's kept or
+        renamed program would, without comparing codes on the host."""
+        owner = rhs if owner is None else owner
+        previous, keepable = self._matrix_cache.previous(rhs, owner, index)
+        if keepable and tiles is not None and previous._accepts(tiles):
             previous._install(tiles)
             return previous
-        programmed = self.map(matrix.T, name=None if previous is None else previous.name,
-                              _tiles=tiles)
-        if (
-            tiles is None
-            and reusable
-            and torch.equal(previous.packed, programmed.packed)
-            and torch.equal(previous.weight_scale, programmed.weight_scale)
-        ):
+        fresh = self.map(rhs.T, name=None if previous is None else previous.name, _tiles=tiles)
+        if keepable and tiles is None and previous._same_program(fresh):
             return previous
         if previous is not None:
-            programmed._event = previous._event
-        owner = weakref.ref(self)
+            fresh._event = previous._event
+        self._matrix_cache.remember(owner, index, fresh)
+        return fresh
 
-        def release(reference):
-            simulator = owner()
-            if simulator is not None:
-                cached = simulator._matrix_cache.get(identity)
-                if cached is not None and cached[0] is reference:
-                    simulator._matrix_cache.pop(identity, None)
+    def _product(self, x, rhs, *, owner=None, index=()):
+        """(``x @ rhs``, the RHS program) for the functional API, with one status read
+        before any state change.
 
-        self._matrix_cache[identity] = (weakref.ref(matrix, release), metadata, programmed)
-        return programmed
-
-    def _program_plan(self, matrix, tiles):
-        """(name, event) of the program ``_matrix_for(matrix, tiles)`` would return, no side effects."""
-        record = self._matrix_cache.get(id(matrix))
-        same_tensor = record is not None and record[0]() is matrix
-        previous = record[2] if same_tensor else None
-        metadata = (
-            tuple(matrix.shape), tuple(matrix.stride()), matrix.storage_offset(),
-            matrix.data_ptr(), matrix.dtype, matrix.device,
-        )
-        if previous is None:
-            return f"matrix.{self._next_id}", 0, None
-        reusable = (
-            record[1] == metadata
-            and previous.config == self.config
-            and previous.packed.device == self.device
-            and previous._accepts(tiles)
-        )
-        return previous.name, previous._event, (previous if reusable else None)
-
-    def _product(self, x, matrix):
-        """``x @ matrix`` for the functional API with one status read before any state change.
-
-        The RHS and the input are quantized and, where possible, read at once,
-        with finiteness recorded in a device status word instead of host checks.
-        A single read of the status word then raises the errors of
-        memfast/functional.py:49-53 (A before B) while this simulator is still
-        unchanged; only afterwards is the RHS program committed
-        (``_matrix_for``) and its read event advanced, as AnalogMatrix.forward
-        would.  The read uses the name and event that commit will assign.
+        Both operands are quantized on the device and, in default mode, read at once; the
+        quantizers flag non-finite values in a status word instead of host scans.  Its one
+        read raises the errors of memfast/functional.py:49-53 (A before B) while this
+        simulator is unchanged; only then is the RHS program committed (``_matrix_for``)
+        and its read event advanced, as AnalogMatrix.forward would.  The read uses the
+        name and event that the commit assigns.
         """
         config = self.config
+        owner = rhs if owner is None else owner
         status = hip.status_word(self.device)
-        tiles = hip.weight_tiles(matrix.T, config, status=status)
+        tiles = hip.weight_tiles(rhs.T, config, status=status)
         flat = x.reshape(-1, x.shape[-1])
         q, xscale = hip.input_tiles(flat, config, status=status)
-        name, event, reused = self._program_plan(matrix, tiles)
-        speculative = (
-            self.mode == "default"
-            and event < 2**63
-            and (reused is None or reused.input_scale is None)
-        )
+        previous, keepable = self._matrix_cache.previous(rhs, owner, index)
+        kept = previous if keepable and previous._accepts(tiles) else None
+        name = f"matrix.{self._next_id}" if previous is None else previous.name
+        event = 0 if previous is None else previous._event
+        fused = (self.mode == "default" and event < _EVENT_LIMIT
+                 and (kept is None or kept.input_scale is None))
         output = None
-        if speculative:
-            out_features = matrix.shape[1]
-            p = math.ceil(out_features / config.array_size[1])
-            tag = _name_tag(name)
-            packed, codes, wscale = tiles
-            output = hip.mm(q, xscale, packed, codes if hip.mm_kernel(
-                config, q.shape[0], q.shape[1], p) or config.wide else None,
-                wscale.reshape(-1, p * config.array_size[1]), config, config.seed ^ tag, event,
-                variant=tuning.DEFAULT_VARIANT, status=status,
-                out_cols=out_features, k_rows=matrix.shape[0])
+        if fused:
+            k, o = rhs.shape
+            p = math.ceil(o / config.array_size[1])
+            packed, codes_t, wscale = tiles
+            if not (config.wide or hip.mm_kernel(config, q.shape[0], q.shape[1], p)):
+                codes_t = None
+            output = hip.mm(q, xscale, packed, codes_t, wscale.reshape(-1, p * config.array_size[1]),
+                            config, config.seed ^ _name_tag(name), event,
+                            variant=tuning.DEFAULT_VARIANT, status=status, out_cols=o, k_rows=k)
         flags = int(status.item())
         if flags & hip.STATUS_INPUT:
             raise ValueError("A must be finite")
         if flags & hip.STATUS_WEIGHT:
             raise ValueError("B must be finite")
-        if reused is not None:
-            # The program _matrix_for would keep (same tensor, metadata, config,
-            # device and tile shapes, as _program_plan checked): install in place.
-            reused._install(tiles)
-            program = reused
+        if kept is not None:
+            kept._install(tiles)
+            program = kept
         else:
-            program = self._matrix_for(matrix, tiles=tiles)
-        if not speculative:
+            program = self._matrix_for(rhs, tiles=tiles, owner=owner, index=index)
+        if not fused:
             if program.input_scale is not None:
                 q, xscale = hip.input_tiles(flat, config, program.input_scale)
-            return program._run(x, q, xscale)
-        output = output[:, : program.out_features].contiguous()
+            return program._run(x, q, xscale), program
+        output = output[:, :program.out_features].contiguous()
         finite = not flags & hip.STATUS_OUTPUT
         if not finite and not config.wide:
             output, finite = program._execute_checked(q, xscale, default_schedule(config), event,
                                                       stable=True)
-        return program._finish(x, output, finite)
-
-    def map_quantized(self, codes, scales, *, zero_points=None, bias=None, name=None):
-        """Import integer [O,K] weights as ``scales * (codes - zero_points)``."""
-        if name is None:
-            name = f"matrix.{self._next_id}"
-            self._next_id += 1
-        return AnalogMatrix(codes, self, bias=bias, name=name, scales=scales,
-                            zero_points=zero_points)
-
-    def report(self):
-        return dict(mode=self.mode, device=str(self.device), config=asdict(self.config),
-                    selections=self.records)
+        return program._finish(x, output, finite), program
 
     # -- tuned mode (memfast_amd/tuning.py) -------------------------------------
     def _key(self, matrix, x, grid):
@@ -283,8 +313,70 @@ class Simulator:
         return tuning.ScheduleSearch(self, matrix, x, q, xscale, event).run()
 
 
+# ---------------------------------------------------------------------------
+# Program sources of an AnalogMatrix
+# ---------------------------------------------------------------------------
+def _from_float(weight, zero_points, simulator, tiles):
+    """(packed, packed_t, weight_scale) of floating [O,K] weights, quantized on the GPU
+    (memfast/quantization.py:82-112), or the caller's already quantized ``tiles``."""
+    if tiles is not None:
+        return tiles
+    if not weight.is_floating_point():
+        raise ValueError("unquantized weight must be floating")
+    if zero_points is not None:
+        raise ValueError("zero_points requires imported integer codes and scales")
+    return hip.weight_tiles(weight.detach().to(simulator.device), simulator.config)
+
+
+def _from_codes(codes, scales, zero_points, simulator):
+    """(packed, weight_scale, zero_correction) of imported integer [O,K] codes with
+    ``scales`` and optional ``zero_points`` (memfast/simulator.py:173-185, :380-404)."""
+    config, device = simulator.config, simulator.device
+    if codes.dtype not in _CODE_DTYPES:
+        raise ValueError("imported weight codes must have an integer dtype")
+    if config.bw_e is not None:
+        raise ValueError("native INT weight import requires bw_e=None")
+    signed = config.weight_signed
+    low = -(1 << (config.weight_bits - 1)) if signed else 0
+    high = (1 << (config.weight_bits - int(signed))) - 1
+    values = codes.detach().to(device=device, dtype=torch.int64)
+    if bool(values.lt(low).any()) or bool(values.gt(high).any()):
+        raise ValueError("weight codes exceed configured signedness or bit width")
+    dtype = torch.float64 if config.wide else torch.float32
+    shape = tuple(codes.shape)
+    physical_scale = expanded_parameter(scales, shape, device, dtype, "scales",
+                                        positive=True).detach().T.contiguous()
+    check_read_scales(physical_scale, config, "weight scale")
+    packed, table = pack_weight(values.T.contiguous(), physical_scale, config)
+    if zero_points is None:
+        return packed, table, None
+    zeros = expanded_parameter(zero_points, shape, device, dtype,
+                               "zero_points").detach().T.contiguous()
+    check_read_scales(zeros, config, "weight zero point")
+    k = shape[1]
+    first = read_starts(math.ceil(k / config.array_size[0]), config, device).clamp_max(k - 1)
+    correction = -(zeros[first] * physical_scale[first])
+    if not bool(torch.isfinite(correction).all()):
+        raise ValueError("scaled zero points exceed the reconstruction dtype")
+    return packed, table, correction
+
+
+def _bias_buffer(bias, out_features, device, dtype):
+    """The bias buffer in the reconstruction dtype, with the reference's checks."""
+    if bias is None:
+        return None
+    valid = (bias.is_floating_point() and tuple(bias.shape) == (out_features,)
+             and bool(torch.isfinite(bias).all()))
+    if not valid:
+        raise ValueError("bias must be finite and match out_features")
+    stored = bias.detach().to(device=device, dtype=dtype).clone()
+    if not bool(torch.isfinite(stored).all()):
+        raise ValueError("bias exceeds the reconstruction dtype")
+    return stored
+
+
 class AnalogMatrix(nn.Module):
-    """Programmed matrix with optional digital zero-point compensation.
+    """A programmed matrix: codes, scales and optional digital zero-point compensation.
 
     Buffers, checkpoint state and validation follow memfast/simulator.py:350-646.
     """
@@ -294,88 +386,35 @@ class AnalogMatrix(nn.Module):
         super().__init__()
         if weight.ndim != 2 or min(weight.shape) < 1:
             raise ValueError("weight must be a nonempty [O,K] matrix")
-        if _tiles is None and not torch.isfinite(weight).all():
+        if _tiles is None and not bool(torch.isfinite(weight).all()):
             raise ValueError("weights must be finite")
         self.simulator, self.config, self.name = simulator, simulator.config, name
         hip.supported(self.config)
         self.out_features, self.in_features = weight.shape
         self.p = math.ceil(self.out_features / self.config.array_size[1])
-        dtype = torch.float64 if self.config.wide else torch.float32
-        zero_correction = None
-        packed_t = None
-        if _tiles is not None:
-            packed, packed_t, scale = _tiles
-        elif scales is None:
-            if not weight.is_floating_point():
-                raise ValueError("unquantized weight must be floating")
-            if zero_points is not None:
-                raise ValueError("zero_points requires imported integer codes and scales")
-            packed, packed_t, scale = hip.weight_tiles(
-                weight.detach().to(simulator.device), self.config
-            )
+        column_codes, correction = None, None
+        if scales is None:
+            packed, column_codes, table = _from_float(weight, zero_points, simulator, _tiles)
         else:
-            if weight.dtype not in (torch.uint8, torch.int8, torch.int16, torch.int32,
-                                    torch.int64):
-                raise ValueError("imported weight codes must have an integer dtype")
-            if self.config.bw_e is not None:
-                raise ValueError("native INT weight import requires bw_e=None")
-            signed = self.config.weight_signed
-            lower = -(1 << (self.config.weight_bits - 1)) if signed else 0
-            upper = (1 << (self.config.weight_bits - int(signed))) - 1
-            codes = weight.detach().to(device=simulator.device, dtype=torch.int64)
-            if (codes < lower).any() or (codes > upper).any():
-                raise ValueError("weight codes exceed configured signedness or bit width")
-            code = codes.T.contiguous()
-            scale_full = (
-                expanded_parameter(scales, weight.shape, simulator.device, dtype, "scales",
-                                   positive=True).detach().T.contiguous()
-            )
-            check_read_scales(scale_full, self.config, "weight scale")
-            packed, scale = pack_weight(code, scale_full, self.config)
-            if zero_points is not None:
-                zeros = (
-                    expanded_parameter(zero_points, weight.shape, simulator.device, dtype,
-                                       "zero_points").detach().T.contiguous()
-                )
-                check_read_scales(zeros, self.config, "weight zero point")
-                rows = self.config.array_size[0]
-                starts = read_starts(math.ceil(self.in_features / rows), self.config,
-                                     code.device)
-                indices = starts.clamp_max(self.in_features - 1)
-                zero_correction = -(zeros[indices] * scale_full[indices])
-                if not torch.isfinite(zero_correction).all():
-                    raise ValueError("scaled zero points exceed the reconstruction dtype")
-        self.register_buffer("packed", packed)
-        self.register_buffer("weight_scale", scale)
-        self.register_buffer("zero_correction", zero_correction)
-        self.register_buffer("input_scale", None)
-        if bias is not None and (
-            not bias.is_floating_point()
-            or bias.shape != (self.out_features,)
-            or not torch.isfinite(bias).all()
-        ):
-            raise ValueError("bias must be finite and match out_features")
-        self.register_buffer(
-            "bias",
-            None if bias is None
-            else bias.detach().to(device=simulator.device, dtype=dtype).clone(),
-        )
-        if self.bias is not None and not torch.isfinite(self.bias).all():
-            raise ValueError("bias exceeds the reconstruction dtype")
+            packed, table, correction = _from_codes(weight, scales, zero_points, simulator)
+        dtype = torch.float64 if self.config.wide else torch.float32
+        for key, tensor in (("packed", packed), ("weight_scale", table),
+                            ("zero_correction", correction), ("input_scale", None),
+                            ("bias", _bias_buffer(bias, self.out_features, simulator.device,
+                                                  dtype))):
+            self.register_buffer(key, tensor)
         self._event = 0
-        tag = _name_tag(name)
-        self.seed = self.config.seed ^ tag
-        self._prepared = {}
-        self._kernel_codes = None
-        self._workspace = None        # noisy MFMA scratch kept across reads
-        self._terms_source = None     # (kernel codes, version, seed) of the terms it holds
-        if packed_t is not None:
-            self._kernel_codes = (self._codes_key(), packed_t)
+        self.seed = self.config.seed ^ _name_tag(name)
+        self._prepared = {}          # tuned schedules by (input shape, dtype)
+        self._kernel_codes = None    # (codes key, the kernels' copy of the codes)
+        self._workspace = None       # noisy MFMA scratch kept across reads
+        self._terms_source = None    # (kernel codes, version, seed) of the terms it holds
+        if column_codes is not None:
+            self._kernel_codes = (self._codes_key(), column_codes)
 
-    # -- kernel-side copy of the codes -------------------------------------
+    # -- the kernels' copy of the codes ----------------------------------------
     def _codes_key(self, packed=None):
-        if packed is None:
-            packed = self.packed
+        packed = self.packed if packed is None else packed
         return (packed.data_ptr(), packed._version, packed.device, tuple(packed.shape))
 
     def _column_codes(self):
@@ -386,228 +425,204 @@ class AnalogMatrix(nn.Module):
         return self._kernel_codes[1]
 
     def _accepts(self, tiles):
-        packed, _, scale = tiles
-        buffers = self._buffers   # registered buffers, read without Module.__getattr__
-        current, current_scale = buffers["packed"], buffers["weight_scale"]
-        return (
-            current.dtype == packed.dtype and current.shape == packed.shape
-            and current_scale.dtype == scale.dtype and current_scale.shape == scale.shape
-            and buffers["zero_correction"] is None and buffers["bias"] is None
-        )
+        """Whether freshly quantized ``tiles`` can replace this program's in place."""
+        packed, _, table = tiles
+        own = self._buffers   # the registered buffers, without Module.__getattr__
+        return (own["zero_correction"] is None and own["bias"] is None
+                and own["packed"].dtype == packed.dtype and own["packed"].shape == packed.shape
+                and own["weight_scale"].dtype == table.dtype
+                and own["weight_scale"].shape == table.shape)
 
     def _install(self, tiles):
-        """Take freshly quantized codes and scales of the same matrix (see _matrix_for).
-
-        ``packed`` and ``weight_scale`` are registered buffers (of the same
-        dtype and shape, as ``_accepts`` checked), replaced in place in the
-        buffer table; this is what attribute assignment does for a buffer.
-        """
-        packed, packed_t, scale = tiles
-        buffers = self._buffers
-        buffers["packed"] = packed
-        buffers["weight_scale"] = scale
+        """Take freshly quantized codes and scales of the same matrix (``_accepts``):
+        the buffer table entries are replaced, as attribute assignment would."""
+        packed, column_codes, table = tiles
+        self._buffers["packed"], self._buffers["weight_scale"] = packed, table
         self.__dict__["_kernel_codes"] = (
-            (self._codes_key(packed), packed_t) if packed_t is not None else None
-        )
+            None if column_codes is None else (self._codes_key(packed), column_codes))
 
+    def _same_program(self, other):
+        return (torch.equal(self.packed, other.packed)
+                and torch.equal(self.weight_scale, other.weight_scale))
+
+    @torch.no_grad()
+    def _prepare(self, weight, bias=None):
+        """A new program of floating [O,K] weights (and bias) for ``_commit``, with the
+        checks of programming a fresh matrix (memfast/nn/training.py:40-47); nothing of
+        this matrix changes."""
+        if not bool(torch.isfinite(weight).all()):
+            raise ValueError("weights must be finite")
+        if not weight.is_floating_point():
+            raise ValueError("unquantized weight must be floating")
+        packed, column_codes, table = hip.weight_tiles(weight.detach().to(self.packed.device),
+                                                       self.config)
+        dtype = torch.float64 if self.config.wide else torch.float32
+        return packed, column_codes, table, _bias_buffer(bias, self.out_features,
+                                                         self.packed.device, dtype)
+
+    @torch.no_grad()
+    def _commit(self, prepared):
+        """Write a ``_prepare``d program into the existing buffers (the bias only where
+        this matrix has one): buffer identities, name, seed, read count and tuned
+        schedules stay."""
+        packed, column_codes, table, bias = prepared
+        self.packed.copy_(packed)
+        self.weight_scale.copy_(table)
+        if bias is not None and self.bias is not None:
+            self.bias.copy_(bias)
+        self._kernel_codes = None if column_codes is None else (self._codes_key(), column_codes)
+
+    def _reprogram(self, weight, bias=None):
+        self._commit(self._prepare(weight, bias))
+
+    # -- settings ----------------------------------------------------------------
     def set_input_scale(self, scale):
         """Fix symmetric activation scales for subsequent calls; None restores dynamic scales."""
-        if scale is None:
-            self.input_scale = None
-        else:
+        if scale is not None:
             dtype = torch.float64 if self.config.wide else torch.float32
-            expanded = expanded_parameter(scale, (1, self.in_features), self.packed.device, dtype,
-                                          "input scale").detach()
-            if (expanded <= 0).any():
+            fixed = expanded_parameter(scale, (1, self.in_features), self.packed.device, dtype,
+                                       "input scale").detach()
+            if bool((fixed <= 0).any()):
                 raise ValueError("input scale must be strictly positive")
-            check_read_scales(expanded.T, self.config, "input scale")
-            self.input_scale = expanded.clone()
+            check_read_scales(fixed.T, self.config, "input scale")
+            scale = fixed.clone()
+        self.input_scale = scale
         self._prepared.clear()
         return self
-
-    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
-        packed = state_dict.get(prefix + "packed")
-        if packed is not None:
-            if not torch.is_tensor(packed) or packed.dtype not in (
-                torch.uint8, torch.int8, torch.int16, torch.int32, torch.int64,
-            ):
-                raise ValueError("checkpoint packed weights must have an integer dtype")
-            values = packed.to(torch.int64)
-            if (values < 0).any() or (values > (1 << self.config.weight_bits) - 1).any():
-                raise ValueError("checkpoint packed weights exceed the configured bit width")
-        scales = state_dict.get(prefix + "weight_scale")
-        if scales is not None and (
-            not torch.is_tensor(scales)
-            or not scales.is_floating_point()
-            or not torch.isfinite(scales).all()
-            or (scales < 0).any()
-        ):
-            raise ValueError("checkpoint weight scales must be finite and nonnegative")
-        for name in ("input_scale", "zero_correction"):
-            key = prefix + name
-            if key in state_dict and self._buffers[name] is None:
-                self._buffers[name] = torch.empty_like(state_dict[key], device=self.packed.device)
-        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
-        if not torch.isfinite(self.weight_scale).all() or (self.weight_scale < 0).any():
-            raise ValueError("checkpoint weight scales exceed the reconstruction dtype")
-        if self.bias is not None and not torch.isfinite(self.bias).all():
-            raise ValueError("checkpoint bias exceeds the reconstruction dtype")
-        if self.input_scale is not None:
-            self.set_input_scale(self.input_scale)
-        if self.zero_correction is not None:
-            expected = (self.weight_scale.shape[0], self.out_features)
-            if tuple(self.zero_correction.shape) != expected:
-                raise ValueError("checkpoint zero-point correction has an invalid shape")
-            if not torch.isfinite(self.zero_correction).all():
-                raise ValueError("checkpoint zero-point correction must be finite")
-        self._kernel_codes = None
-
-    def _apply(self, fn, recurse=True):
-        programmed = {name: buf for name, buf in self._buffers.items() if buf is not None}
-        super()._apply(fn, recurse=recurse)
-        for name, original in programmed.items():
-            transformed = self._buffers[name]
-            if transformed.dtype != original.dtype:
-                self._buffers[name] = original.to(device=transformed.device)
-            if transformed.device != original.device:
-                self._prepared.clear()
-                self._kernel_codes = None
-        return self
-
-    def get_extra_state(self):
-        return dict(config=asdict(self.config), in_features=self.in_features,
-                    out_features=self.out_features, name=self.name, seed=self.seed,
-                    event=self._event)
-
-    def set_extra_state(self, state):
-        for key in ("in_features", "out_features"):
-            if key in state and (type(state[key]) is not int or state[key] != getattr(self, key)):
-                raise ValueError("checkpoint logical matrix dimensions differ")
-        loaded = dict(state["config"])
-        effects = dict(loaded["nonidealities"])
-        if effects.pop("output_noise", 0) != 0:
-            raise ValueError("checkpoint uses a removed noise model")
-        loaded["nonidealities"] = effects
-        for name in ("rows_per_read", "input_slice", "weight_slice", "bw_e"):
-            loaded.setdefault(name, None)
-        loaded.setdefault("weight_signed", True)
-        if loaded != _comparable(asdict(self.config)):
-            if _comparable(loaded) != _comparable(asdict(self.config)):
-                raise ValueError("checkpoint physical configuration differs")
-        if type(state["seed"]) is not int or not 0 <= state["seed"] < 2**32:
-            raise ValueError("invalid checkpoint sampling seed")
-        self.reset_read(state["event"])
-        self.name, self.seed, self._event = state["name"], state["seed"], state["event"]
-        self._prepared.clear()
 
     def reset_read(self, event=0):
-        if type(event) is not int or not 0 <= event < 2**63:
+        if type(event) is not int or not 0 <= event < _EVENT_LIMIT:
             raise ValueError("event must be a nonnegative signed 64-bit integer")
         self._event = event
 
     @torch.no_grad()
     def update_weight(self, matrix):
-        """Reprogram a right-hand [K,O] matrix without replacing this module."""
-        if not isinstance(matrix, torch.Tensor) or tuple(matrix.shape) != (
-            self.in_features, self.out_features,
-        ):
+        """Reprogram a right-hand [K,O] matrix without replacing this module; the read
+        count restarts at zero (memfast/simulator.py:541-559)."""
+        if not isinstance(matrix, torch.Tensor) or tuple(matrix.shape) != (self.in_features,
+                                                                            self.out_features):
             raise ValueError("replacement matrix must have the original [K,O] shape")
-        replacement = AnalogMatrix(matrix.T, self.simulator, bias=self.bias, name=self.name)
-        self.packed.copy_(replacement.packed)
-        self.weight_scale.copy_(replacement.weight_scale)
+        self._reprogram(matrix.T)
         self.zero_correction = None
         self._prepared.clear()
-        self._kernel_codes = None
         self.reset_read()
         return self
 
-    # -- execution -----------------------------------------------------------
+    # -- checkpoints (memfast_amd/checkpoint.py) ---------------------------------
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        checkpoint.check_incoming(self, state_dict, prefix)
+        checkpoint.shape_optional_buffers(self, state_dict, prefix)
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+        checkpoint.check_loaded(self)
+        self._kernel_codes = None
+
+    def get_extra_state(self):
+        return checkpoint.extra_state(self)
+
+    def set_extra_state(self, state):
+        name, seed, event = checkpoint.check_extra_state(self, state)
+        self.reset_read(event)
+        self.name, self.seed = name, seed
+        self._prepared.clear()
+
+    def _apply(self, fn, recurse=True):
+        """Device moves keep the programmed buffers' dtypes (memfast/simulator.py:484-493)."""
+        before = {key: buffer for key, buffer in self._buffers.items() if buffer is not None}
+        super()._apply(fn, recurse=recurse)
+        for key, original in before.items():
+            moved = self._buffers[key]
+            if moved.dtype != original.dtype:
+                self._buffers[key] = original.to(device=moved.device)
+            if moved.device != original.device:
+                self._prepared.clear()
+                self._kernel_codes = None
+        return self
+
+    # -- reading -------------------------------------------------------------------
     def _execute(self, q, xscale, schedule, event, stable=False):
         """One fused read of every tile; memfast/simulator.py:561-616."""
         return self._execute_checked(q, xscale, schedule, event, stable)[0]
+
+    def _zero_point_term(self, q, xscale, stable):
+        """The digital zero-point correction [N, O] of memfast/simulator.py:587-611: each
+        read's sum of signed input codes times its input scale, times the correction row
+        of that read.  One FP32 matrix product, or in FP64 per C columns through
+        restore_scales for wide configurations and the overflow retry."""
+        config = self.config
+        codes = _signed(q.reshape(q.shape[0], -1), config.activation_bits)
+        reads = row_reads(codes.shape[1], config, q.device)
+        sums = torch.zeros((q.shape[0], xscale.shape[1]), dtype=torch.int64, device=q.device)
+        sums.index_add_(1, reads, codes)
+        correction = self.zero_correction
+        if not (config.wide or stable):
+            return (sums.float() * xscale.float()) @ correction.float()
+        width = config.array_size[1]
+        term = torch.empty((q.shape[0], self.out_features), dtype=torch.float64,
+                           device=q.device)
+        for first in range(0, self.out_features, width):
+            block = slice(first, min(first + width, self.out_features))
+            term[:, block] = restore_scales(sums[:, :, None], xscale[:, :, None],
+                                            correction[None, :, block]).sum(1)
+        return term
 
     def _execute_checked(self, q, xscale, schedule, event, stable=False, status=None,
                          input_error=None, retry=True, defer=False):
         """(output, finite) where ``finite`` is True when the output is known finite.
 
-        ``status`` may carry STATUS_INPUT from a deferred input quantization; the
-        one status read raises ``input_error`` for it before anything else.  With
-        ``retry`` False, a non-finite FP32 result returns (None, False) instead of
-        the FP64 retry (which changes every row's rounding).  With ``defer`` the
-        status word is not read: the FP32 output returns as it is and the caller
-        reads ``status`` later (``_forward_deferred``)."""
+        ``status`` may carry STATUS_INPUT from a deferred input quantization; the one
+        status read raises ``input_error`` for it before anything else.  With ``retry``
+        False, a non-finite FP32 result returns (None, False) instead of the FP64 retry
+        (which changes every row's rounding).  With ``defer`` the status word is not
+        read: the FP32 output returns as it is and the caller reads ``status`` later
+        (``_forward_deferred``)."""
         config = self.config
-        c = config.array_size[1]
-        if config.wide:
-            packed = self.packed
-        else:
-            packed = self.packed if self.packed.dtype == torch.uint8 else self.packed.to(torch.uint8)
+        columns = self.p * config.array_size[1]
+        packed = self.packed
+        if not config.wide and packed.dtype != torch.uint8:
+            packed = packed.to(torch.uint8)
         if stable:
             output = self._execute_stable(q, xscale, packed, event)
         else:
             kernel = hip.mm_kernel(config, q.shape[0], q.shape[1], self.p)
             codes_t = self._column_codes() if config.wide or kernel else None
-            if status is None:
-                status = hip.status_word(q.device)
-            workspace, reuse, source = None, False, None
+            status = hip.status_word(q.device) if status is None else status
             variant = tuning.schedule_variant(schedule)
+            workspace, reuse, source = None, False, None
             if kernel == 2 and hip.terms_event_independent(config):
                 workspace, reuse, source = self._terms_workspace(q, codes_t, variant)
-            output = hip.mm(q, xscale, packed, codes_t, self.weight_scale.reshape(-1, self.p * c),
+            output = hip.mm(q, xscale, packed, codes_t, self.weight_scale.reshape(-1, columns),
                             config, self.seed, event, variant=variant, status=status,
                             workspace=workspace, reuse_terms=reuse,
                             out_cols=self.out_features, k_rows=self.in_features)
             if source is not None:
                 self._terms_source = source
-        output = output[:, : self.out_features].contiguous()
+        output = output[:, :self.out_features].contiguous()
         if self.zero_correction is not None:
-            bits = config.activation_bits
-            signed = q.to(torch.int64).reshape(q.shape[0], -1).bitwise_and((1 << bits) - 1)
-            signed = (signed ^ (1 << (bits - 1))) - (1 << (bits - 1))
-            rows, step = config.array_size[0], config.read_rows
-            padded = torch.nn.functional.pad(
-                signed.reshape(q.shape[0], -1, rows), (0, config.reads_per_array * step - rows)
-            )
-            sums = padded.reshape(q.shape[0], -1, step).sum(-1)
-            dtype = output.dtype
-            if config.wide or stable:
-                for begin in range(0, self.out_features, c):
-                    end = min(begin + c, self.out_features)
-                    output[:, begin:end] += restore_scales(
-                        sums[:, :, None], xscale[:, :, None], self.zero_correction[None, :, begin:end]
-                    ).sum(1)
-            else:
-                output = output + (sums.to(dtype) * xscale.to(dtype)) @ self.zero_correction.to(dtype)
-        # The bias of an FP32 read is added by a kernel that also flags non-finite sums.
-        fused_bias = (self.bias is not None and self.zero_correction is None and not config.wide
-                      and not stable)
-        if self.bias is not None and not fused_bias:
+            output = output + self._zero_point_term(q, xscale, stable).to(output.dtype)
+        # An FP32 read's bias goes through a kernel that also flags non-finite sums.
+        checked_bias = (self.bias is not None and self.zero_correction is None
+                        and not config.wide and not stable)
+        if self.bias is not None and not checked_bias:
             output = output + self.bias
         if stable:
             return output, False
-        if fused_bias:
+        if checked_bias:
             hip.bias_add(output, self.bias, status)
         if defer:
             return output, True
-        # One status read: deferred input check, then non-finite outputs.
-        flags = int(status.item())
+        flags = int(status.item())   # the one status read: deferred input check, then outputs
         if flags & hip.STATUS_INPUT:
             raise ValueError(input_error or "quantized values must be finite")
-        if config.wide:
-            # FP64 restore already; the reference's retry (simulator.py:614-615) would
-            # repeat the same FP64 computation.
-            return output, bool(torch.isfinite(output).all()) if (
-                self.zero_correction is not None or self.bias is not None
-            ) else not flags & hip.STATUS_OUTPUT
-        if self.zero_correction is None:
-            finite = not flags & hip.STATUS_OUTPUT
-        else:
-            finite = bool(torch.isfinite(output).all())
-        if not finite:
-            if not retry:
-                return None, False
-            return self._execute_checked(q, xscale, schedule, event, stable=True)
-        return output, True
+        flagged = bool(flags & hip.STATUS_OUTPUT)
+        host_scan = self.zero_correction is not None or (config.wide and self.bias is not None)
+        finite = bool(torch.isfinite(output).all()) if host_scan else not flagged
+        if finite or config.wide:
+            # A wide read is already an FP64 restore; the reference's retry
+            # (memfast/simulator.py:614-615) would repeat the same computation.
+            return output, finite
+        if not retry:
+            return None, False
+        return self._execute_checked(q, xscale, schedule, event, stable=True)
 
     def _terms_workspace(self, q, codes_t, variant=tuning.DEFAULT_VARIANT):
         """Workspace of the noisy MFMA read kept across calls, and whether it still holds
@@ -630,18 +645,27 @@ class AnalogMatrix(nn.Module):
     def _execute_stable(self, q, xscale, packed, event):
         """FP64 overflow-safe restore of the slice totals (non-finite FP32 retry).
 
-        Chunks of two tiles as memfast/simulator.py:561-585; the restore and the
-        read sum run in one kernel with torch's CPU summation order.
+        Chunks of two tiles as memfast/simulator.py:561-585; the restore and the read
+        sum run in one kernel with torch's CPU summation order.
         """
-        c = self.config.array_size[1]
-        output = torch.empty((q.shape[0], self.p * c), dtype=torch.float64, device=q.device)
-        wscale = self.weight_scale.reshape(-1, self.p * c)
-        width = min(2, self.p)
-        for begin in range(0, self.p, width):
-            end = min(begin + width, self.p)
-            value = hip.partial(q, packed, self.config, None, self.seed, event, begin, end)
-            hip.stable_sum(value, xscale, wscale, self.config, begin * c, output)
+        width = self.config.array_size[1]
+        output = torch.empty((q.shape[0], self.p * width), dtype=torch.float64, device=q.device)
+        wscale = self.weight_scale.reshape(-1, self.p * width)
+        chunk = min(2, self.p)
+        for first in range(0, self.p, chunk):
+            last = min(first + chunk, self.p)
+            totals = hip.partial(q, packed, self.config, None, self.seed, event, first, last)
+            hip.stable_sum(totals, xscale, wscale, self.config, first * width, output)
         return output
+
+    def _check_input(self, x):
+        """Argument checks of a read (memfast/simulator.py:618-631)."""
+        if x.ndim < 1 or x.shape[-1] != self.in_features or not x.is_floating_point():
+            raise ValueError("input must be floating with matching in_features")
+        if x.device != self.packed.device or x.device != self.simulator.device:
+            raise ValueError("input and simulator must use the same device")
+        if self.weight_scale.dtype != (torch.float64 if self.config.wide else torch.float32):
+            raise RuntimeError("keep simulator scale buffers at their mapped dtype")
 
     @torch.no_grad()
     def forward(self, x):
@@ -651,24 +675,17 @@ class AnalogMatrix(nn.Module):
         """forward(); with ``retry`` False it returns None (event unchanged) where the
         FP32 read is not finite, so that a caller batching independent rows can fall
         back to separate calls."""
-        if x.ndim < 1 or x.shape[-1] != self.in_features or not x.is_floating_point():
-            raise ValueError("input must be floating with matching in_features")
-        if x.device != self.packed.device or x.device != self.simulator.device:
-            raise ValueError("input and simulator must use the same device")
-        scale_dtype = torch.float64 if self.config.wide else torch.float32
-        if self.weight_scale.dtype != scale_dtype:
-            raise RuntimeError("keep simulator scale buffers at their mapped dtype")
-        shape = x.shape
+        self._check_input(x)
         if x.numel() == 0:
-            return x.new_empty((*shape[:-1], self.out_features))
-        if self._event >= 2**63:
+            return x.new_empty((*x.shape[:-1], self.out_features))
+        if self._event >= _EVENT_LIMIT:
             raise OverflowError("read-event counter exhausted")
-        # Default mode defers the finiteness check of x to the read's status word
-        # (raised before the event advances); tuned mode checks first, as its
-        # schedule search runs before the read.
+        # Default mode defers the finiteness check of x to the read's status word (raised
+        # before the event advances); tuned mode checks first, as its schedule search
+        # runs before the read.
         status = hip.status_word(x.device) if self.simulator.mode == "default" else None
-        q, xscale = hip.input_tiles(x.reshape(-1, self.in_features), self.config, self.input_scale,
-                                    status=status)
+        q, xscale = hip.input_tiles(x.reshape(-1, self.in_features), self.config,
+                                    self.input_scale, status=status)
         return self._run(x, q, xscale, status=status, retry=retry)
 
     def _deferrable(self, x, reads):
@@ -679,17 +696,17 @@ class AnalogMatrix(nn.Module):
             and self._buffers["zero_correction"] is None
             and x.dtype == torch.float32 and x.ndim == 2 and x.shape[0] > 0
             and x.shape[1] == self.in_features and x.device == self.simulator.device
-            and self.weight_scale.dtype == torch.float32 and self._event + reads < 2**63
+            and self.weight_scale.dtype == torch.float32 and self._event + reads < _EVENT_LIMIT
         )
 
     def _forward_deferred(self, x, status):
         """forward() for a ``_deferrable`` input that ORs its status bits into ``status``
         and returns without reading it, so that reads can queue back to back.
 
-        When ``status`` is still clear after the last such read, every output
-        equals what forward() returns and no forward() would have raised.  When
-        any bit is set, the caller restores the read count and reads again
-        through forward(), which raises or retries exactly where it would have.
+        When ``status`` is still clear after the last such read, every output equals
+        what forward() returns and no forward() would have raised.  When any bit is set,
+        the caller restores the read count and reads again through forward(), which
+        raises or retries exactly where it would have.
         """
         q, xscale = hip.input_tiles(x, self.config, self.input_scale, status=status)
         output, _ = self._execute_checked(q, xscale, default_schedule(self.config), self._event,
@@ -698,14 +715,13 @@ class AnalogMatrix(nn.Module):
         return output
 
     def _run(self, x, q, xscale, status=None, retry=True):
-        """Read quantized inputs, cast, check and advance the event (simulator.py:632-646)."""
-        if self._event >= 2**63:
+        """Read quantized inputs under the mode's schedule, then ``_finish``."""
+        if self._event >= _EVENT_LIMIT:
             raise OverflowError("read-event counter exhausted")
-        shape = x.shape
         event = self._event
         schedule = default_schedule(self.config)
-        key = tuple(shape), str(x.dtype)
         if self.simulator.mode == "tuned":
+            key = (tuple(x.shape), str(x.dtype))
             if key not in self._prepared:
                 with torch.cuda.device(x.device):
                     self._prepared[key] = self.simulator._select(self, x, q, xscale, event)
@@ -713,29 +729,16 @@ class AnalogMatrix(nn.Module):
         output, finite = self._execute_checked(
             q, xscale, schedule, event, status=status,
             input_error=hip.input_error(self.config, self.input_scale), retry=retry)
-        if output is None:
-            return None
-        return self._finish(x, output, finite)
+        return None if output is None else self._finish(x, output, finite)
 
     def _finish(self, x, output, finite):
-        """Cast to the input dtype, check finiteness, advance the read event."""
-        same_dtype = output.dtype == x.dtype
-        output = output.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
-        if not (finite and same_dtype) and not torch.isfinite(output).all():
+        """Cast to the input dtype, check finiteness, advance the read event
+        (memfast/simulator.py:632-646)."""
+        converted = output.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
+        if not (finite and output.dtype == x.dtype) and not bool(torch.isfinite(converted).all()):
             raise FloatingPointError("nonfinite analog output")
         self._event += 1
-        return output
-
-
-@lru_cache(maxsize=4096)
-def _name_tag(name):
-    """32-bit seed tag of a matrix name (first four bytes of its SHA-256, little-endian)."""
-    return int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little")
-
-
-def _comparable(config_dict):
-    """Normalise tuple/list differences of a serialized Config for comparison."""
-    return json.loads(json.dumps(config_dict))
+        return converted
 
 
 __all__ = ["Simulator", "AnalogMatrix", "default_schedule", "schedule_grid", "restore_scales"]

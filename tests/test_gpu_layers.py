@@ -437,3 +437,117 @@ def test_conv_half_precision_implicit_matches_unfold(hip_device, dtype):
     expected = layer.matrices[0](patches.transpose(1, 2)).transpose(1, 2).reshape(2, 8, 10, 10)
     assert got.dtype == dtype
     assert torch.equal(got.view(torch.int16), expected.view(torch.int16))
+
+
+def _assert_same_traversal(layer, stepped, x, layers, hidden_size, bidirectional=False):
+    directions = 2 if bidirectional else 1
+    output, hidden = layer(x)
+    expected, finals = _step_cells(stepped, x, directions, layers, hidden_size)
+    assert torch.equal(output.view(torch.int32), expected.view(torch.int32))
+    assert torch.equal(hidden.view(torch.int32), finals.view(torch.int32))
+    for a, b in zip(layer.cells, stepped.cells):
+        assert (a.input._event, a.hidden._event) == (b.input._event, b.hidden._event)
+
+
+def test_rnn_hidden_overflow_recovered_by_fp64_retry(hip_device):
+    """ReLU hidden states near 2e36 make every hidden read from step 1 on overflow in its
+    FP32 restore ((T * xs) * ws), while the FP64 retry gives sums near 5e25.  The deferred
+    hidden reads flag this; the traversal then reads per step with the retry, exactly as
+    stepping the cells does."""
+    from memfast_amd.nn import AnalogRNN
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(13)
+    source = nn.RNN(8, 16, nonlinearity="relu").to(hip_device)
+    with torch.no_grad():
+        source.weight_ih_l0.fill_(3e35)
+        source.weight_hh_l0.uniform_(1e-12, 2e-12)
+    x = torch.rand(5, 2, 8, device=hip_device) * 0.5 + 0.5
+    layer = AnalogRNN(source, Simulator(cfg, device=hip_device), name="rnn")
+    stepped = AnalogRNN(source, Simulator(cfg, device=hip_device), name="rnn")
+    _assert_same_traversal(layer, stepped, x, 1, 16)
+    output, _ = stepped(x)
+    assert bool(torch.isfinite(output).all()) and output.abs().max() > 1e35
+
+
+def test_gru_without_bias_sequence_matches_per_step_cells(hip_device):
+    """bias=False: both projections are programmed without bias; the sequence equals
+    stepping the cells."""
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(14)
+    source = nn.GRU(40, 64, num_layers=2, bias=False).to(hip_device)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    stepped = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    assert all(cell.input.bias is None and cell.hidden.bias is None for cell in layer.cells)
+    _assert_same_traversal(layer, stepped, torch.randn(7, 3, 40, device=hip_device), 2, 64)
+
+
+def test_gru_config3_shape_sequence_matches_per_step_cells(hip_device):
+    """BASELINE config 3's shapes (input 40, hidden 512, batch 32) over 12 steps: the
+    single input read and the deferred hidden reads equal stepping the cell."""
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                 weight_slice=(1, 1, 2, 2, 2), array_size=(128, 128), rows_per_read=32,
+                 weight_quant_gran=(32, 1), input_quant_gran=(1, 32), adc_bits=7,
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(15)
+    source = nn.GRU(40, 512).to(hip_device)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    stepped = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    _assert_same_traversal(layer, stepped, torch.randn(12, 32, 40, device=hip_device), 1, 512)
+
+
+def test_gru_hooks_see_every_step(hip_device):
+    """Hooks on a cell or its projections see one call per step: with hooks present
+    the traversal calls the cell at every step, as the reference does."""
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(16)
+    source = nn.GRU(40, 64).to(hip_device)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    plain = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    calls = {"cell": 0, "input": 0, "hidden": 0}
+
+    def counter(key):
+        def hook(module, args, output):
+            calls[key] += 1
+        return hook
+
+    cell = layer.cells[0]
+    handles = [cell.register_forward_hook(counter("cell")),
+               cell.input.register_forward_hook(counter("input")),
+               cell.hidden.register_forward_hook(counter("hidden"))]
+    x = torch.randn(6, 3, 40, device=hip_device)
+    output, _ = layer(x)
+    assert calls == {"cell": 6, "input": 6, "hidden": 6}
+    expected, _ = plain(x)
+    assert torch.equal(output.view(torch.int32), expected.view(torch.int32))
+    for handle in handles:
+        handle.remove()
+    layer(x)
+    assert calls == {"cell": 6, "input": 6, "hidden": 6}
+
+
+def test_gru_gate_failure_sets_per_step_read_counts(hip_device, monkeypatch):
+    """A failure after step 2's hidden read (forced from the host in the gate call)
+    leaves both projections at three reads, as per-step reading would."""
+    from memfast_amd.nn import recurrent
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(17)
+    source = nn.GRU(40, 64).to(hip_device)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    gates = recurrent.hip.gru_gates
+    count = {"calls": 0}
+
+    def failing(*args):
+        count["calls"] += 1
+        if count["calls"] == 3:
+            raise RuntimeError("forced gate failure")
+        return gates(*args)
+
+    monkeypatch.setattr(recurrent.hip, "gru_gates", failing)
+    with pytest.raises(RuntimeError, match="forced gate failure"):
+        layer(torch.randn(6, 3, 40, device=hip_device))
+    cell = layer.cells[0]
+    assert (cell.input._event, cell.hidden._event) == (3, 3)

@@ -416,10 +416,10 @@ def test_functional_reprogramming_follows_in_place_edits(hip_device):
     sim = Simulator(cfg, device=hip_device)
     a_dev, b_dev = a.to(hip_device), b.to(hip_device)
     outputs = [sim.mm(a_dev, b_dev)]
-    program = sim._matrix_cache[id(b_dev)][2]
+    program = sim._matrix_cache.program(b_dev)
     b_dev.mul_(-0.5)
     outputs.append(sim.mm(a_dev, b_dev))
-    assert sim._matrix_cache[id(b_dev)][2] is program and program._event == 2
+    assert sim._matrix_cache.program(b_dev) is program and program._event == 2
     assert program.name == "matrix.0" and sim._next_id == 1
     for event, (weights, got) in enumerate(zip((b, b * -0.5), outputs)):
         check_product(cfg, got, a, weights, hip_device, event=event, label=f"event {event}")
