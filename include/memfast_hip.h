@@ -276,6 +276,30 @@ int mf_gru_gates(const float *inputs, int64_t ldi, const float *hidden, int64_t 
                  const float *hx, int64_t ldx, float *out, int64_t ldo, int64_t n, int64_t width,
                  void *stream);
 
+/* One direction of a GRU layer after its input projections (memfast/nn/recurrent.py:204-210,
+ * the per-step `AnalogGRUCell.forward` of :101-116, replacing its hidden read, bias add and
+ * gate ops with one call).  For i = 0 .. steps-1, t = reverse ? steps-1-i : i, and
+ * h_{-1} = h0 ([batch, width], leading dimension ld_h0):
+ *   hidden = mf_mm(mf_quantize_inputs(h_{i-1}), hidden program) read at event event0 + i,
+ *   h_i    = gates(projected + t*proj_step, hidden + bias, h_{i-1})   (as mf_gru_gates),
+ * written to out + t*out_step (rows out_row apart).  projected holds each step's input
+ * projection [batch, 3*width] (rows proj_row apart), bias (may be NULL) the hidden bias [3*width].
+ * gr, gc, work, scale, q, xscale: the dynamic input groups and scratch of mf_quantize_inputs;
+ * packed .. p, seed, workspace, variant: the hidden program's arguments of mf_mm (out_cols
+ * 3*width, k_rows width), with `hidden` [batch, ld_hidden] its output scratch.  Reads after
+ * the first reuse the first read's conductance terms where they do not depend on the event.
+ * Non-finite values set bits of *status as the separate calls do; nothing is read back, so
+ * the caller checks *status once after the call. */
+int mf_gru_sequence(const mf_config *cfg, int64_t steps, int32_t reverse, int64_t batch,
+                    int64_t width, const float *projected, int64_t proj_step, int64_t proj_row,
+                    const float *h0, int64_t ld_h0, int64_t gr, int64_t gc, uint32_t *work,
+                    float *scale, uint8_t *q, float *xscale, const uint8_t *packed,
+                    const uint8_t *packed_t, const float *wscale, int64_t m, int64_t p,
+                    const float *bias, uint32_t seed, uint64_t event0, float *hidden,
+                    int64_t ld_hidden, void *workspace, int64_t workspace_bytes, int32_t variant,
+                    float *out, int64_t out_step, int64_t out_row, uint32_t *status,
+                    void *stream);
+
 /* Overflow-safe FP64 restore and read sum of one chunk of `width` tiles
  * (memfast/simulator.py:57-66 restore_scales and :578-585, the wide/retry path
  * taken when the FP32 restore is non-finite, :614-615): totals [n, G, width*C]

@@ -1399,8 +1399,55 @@ int mf_gru_gates(const float *inputs, int64_t ldi, const float *hidden, int64_t 
         return fail(MF_E_INVALID, "invalid GRU gate arguments");
     hipLaunchKernelGGL(k_gru_gates, dim3(grid_for(n * width)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), inputs, ldi, hidden, ldh, hx, ldx, out, ldo,
-                       n, width);
+                       n, width, nullptr, nullptr, 0u);
     return check_launch("GRU gates");
+}
+
+int mf_gru_sequence(const mf_config *cfg, int64_t steps, int32_t reverse, int64_t batch,
+                    int64_t width, const float *projected, int64_t proj_step, int64_t proj_row,
+                    const float *h0, int64_t ld_h0, int64_t gr, int64_t gc, uint32_t *work,
+                    float *scale, uint8_t *q, float *xscale, const uint8_t *packed,
+                    const uint8_t *packed_t, const float *wscale, int64_t m, int64_t p,
+                    const float *bias, uint32_t seed, uint64_t event0, float *hidden,
+                    int64_t ld_hidden, void *workspace, int64_t workspace_bytes, int32_t variant,
+                    float *out, int64_t out_step, int64_t out_row, uint32_t *status,
+                    void *stream) {
+    const int valid = check_narrow(cfg);
+    if (valid) return valid;
+    if (!projected || !h0 || !q || !xscale || !scale || !packed || !wscale || !hidden || !out ||
+        !status || steps < 1 || batch < 1 || width < 1 || m < 1 || p < 1)
+        return fail(MF_E_INVALID, "invalid GRU sequence arguments");
+    if (proj_row < 3 * width || proj_step < batch * proj_row || ld_h0 < width ||
+        out_row < width || out_step < batch * out_row || ld_hidden < p * cfg->cols ||
+        3 * width > p * cfg->cols || width > m * cfg->rows ||
+        (width + cfg->rows - 1) / cfg->rows != m)
+        return fail(MF_E_INVALID, "GRU sequence shapes do not match the hidden program");
+    if (event0 > uint64_t(INT64_MAX) - uint64_t(steps))
+        return fail(MF_E_INVALID, "read events of the sequence exceed the signed 64-bit range");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (i64 i = 0; i < steps; ++i) {
+        const i64 t = reverse ? steps - 1 - i : i;
+        const float *hx = i == 0 ? h0 : out + (reverse ? t + 1 : t - 1) * out_step;
+        const i64 ldx = i == 0 ? ld_h0 : out_row;
+        int rc = mf_quantize_inputs(cfg, hx, batch, width, ldx, gr, gc, work, scale, q, xscale,
+                                    status, stream);
+        if (rc) return rc;
+        // The first read writes the program's event-independent conductance terms
+        // into the workspace (unless the caller's variant says they are there);
+        // later reads of the same program reuse them.
+        const int32_t v = i == 0 ? variant : (variant | MF_MM_REUSE_TERMS);
+        rc = mf_mm(cfg, q, xscale, batch, m, packed, packed_t, wscale, p, 3 * width, width,
+                   nullptr, seed, event0 + uint64_t(i), hidden, ld_hidden, workspace,
+                   workspace_bytes, v, status, stream);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_gru_gates, dim3(grid_for(batch * width)), dim3(256), 0, s,
+                           projected + t * proj_step, proj_row, hidden, ld_hidden, hx, ldx,
+                           out + t * out_step, out_row, batch, width, bias, status,
+                           u32(MF_STATUS_OUTPUT));
+        rc = check_launch("GRU sequence gates");
+        if (rc) return rc;
+    }
+    return MF_OK;
 }
 
 int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t G, int64_t width,

@@ -200,7 +200,8 @@ __global__ void k_stable_sum(const float *totals, i64 n, i64 G, i64 wc, const fl
 // ---- quantization (quantize.hip) ------------------------------------------
 __global__ void k_fill_u32(u32 *p, i64 count, u32 value);
 __global__ void k_gru_gates(const float *inputs, i64 ldi, const float *hidden, i64 ldh,
-                            const float *hx, i64 ldx, float *out, i64 ldo, i64 n, i64 width);
+                            const float *hx, i64 ldx, float *out, i64 ldo, i64 n, i64 width,
+                            const float *bias, u32 *status, u32 flag);
 __global__ void k_bias_add(float *out, i64 n, i64 o, i64 ldo, const float *bias, u32 *status,
                            u32 flag);
 __global__ void k_group_max(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,

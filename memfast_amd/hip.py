@@ -153,6 +153,9 @@ SIGNATURES = {
                       _P], ct.c_int),
     "mf_bias_add": ([_P, _I64, _I64, _I64, _P, _P, _P], ct.c_int),
     "mf_gru_gates": ([_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P], ct.c_int),
+    "mf_gru_sequence": ([_CFG, _I64, _I32, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _P,
+                         _P, _P, _P, _P, _P, _P, _I64, _I64, _P, ct.c_uint32, ct.c_uint64, _P,
+                         _I64, _P, _I64, _I32, _P, _I64, _I64, _P, _P], ct.c_int),
     "mf_stable_sum": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P], ct.c_int),
     "mf_quantize_inputs_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                  _P], ct.c_int),
@@ -882,6 +885,59 @@ def gru_gates(inputs, hidden, hx):
         check(library().mf_gru_gates(_ptr(inputs), inputs.stride(0), _ptr(hidden), hidden.stride(0),
                                      _ptr(hx), hx.stride(0), _ptr(out), width, n, width,
                                      _stream(inputs.device)), "GRU gates")
+    return out
+
+
+def gru_sequence(config, projected, h0, packed, packed_t, wscale, bias, seed, event, *, reverse,
+                 status, workspace, reuse_terms=False):
+    """One GRU direction's hidden reads and gates (``mf_gru_sequence``): ``projected``
+    [T, B, 3H] FP32 input projections, ``h0`` [B, H] FP32; the hidden program's packed
+    codes, kernel codes ``packed_t``, read scales ``wscale`` [G, p*C], FP32 ``bias`` [3H]
+    or None and ``seed``; step i reads at event ``event + i``.  Returns the states
+    [T, B, H] in time order.  Non-finite values set bits of ``status``, which is not read."""
+    supported(config)
+    require_device(projected)
+    if config.wide:
+        raise BackendError("the native GRU sequence covers narrow configurations")
+    steps, batch, three = projected.shape
+    width = h0.shape[1]
+    r, c = config.array_size
+    m, p = math.ceil(width / r), packed.shape[1]
+    shapes_ok = (three == 3 * width and tuple(h0.shape) == (batch, width)
+                 and projected.dtype == h0.dtype == wscale.dtype == torch.float32
+                 and projected.is_contiguous() and h0.stride(1) == 1 and packed.shape[0] == m
+                 and (bias is None or (bias.dtype == torch.float32 and bias.is_contiguous()
+                                       and tuple(bias.shape) == (3 * width,))))
+    if not shapes_ok:
+        raise ValueError("gru_sequence takes FP32 [T, B, 3H] projections, [B, H] states and a "
+                         "matching hidden program")
+    size = mm_workspace_bytes(config, batch, m, p, 0)
+    if workspace.numel() < size or workspace.device != projected.device:
+        raise ValueError(f"gru_sequence workspace needs {size} bytes on {projected.device}")
+    device = projected.device
+    q = torch.empty((batch, m, r), dtype=torch.uint8, device=device)
+    xscale = torch.empty((batch, m * config.reads_per_array), dtype=torch.float32, device=device)
+    gr, gc = _group_dims((batch, width), config.input_quant_gran)
+    groups = math.ceil(batch / gr) * math.ceil(width / gc)
+    if gr == 1 and gc == config.read_rows and width == m * r:
+        work, scale = _work_words(groups, device), _ptr(xscale)
+    else:
+        work, scale = _group_scratch(groups, device)
+    hidden = torch.empty((batch, p * c), dtype=torch.float32, device=device)
+    out = torch.empty((steps, batch, width), dtype=torch.float32, device=device)
+    wscale = wscale.contiguous()
+    with _on(device):
+        check(
+            library().mf_gru_sequence(
+                ct.byref(descriptor(config)), steps, int(reverse), batch, width, _ptr(projected),
+                batch * three, three, _ptr(h0), h0.stride(0), gr, gc, work, scale, _ptr(q),
+                _ptr(xscale), _ptr(packed), _ptr(packed_t), _ptr(wscale), m, p, _ptr(bias), seed,
+                event, _ptr(hidden), p * c, _ptr(workspace), workspace.numel(),
+                REUSE_TERMS if reuse_terms else 0, _ptr(out), batch * width, width, _ptr(status),
+                _stream(device),
+            ),
+            "GRU sequence",
+        )
     return out
 
 

@@ -14,10 +14,12 @@ Two ways of issuing those reads give the same results with fewer host round trip
   input reads of a direction equal one read of all T*B rows; that read is made once
   and the matrix's read event still advances by T;
 * the hidden reads of a direction then queue back to back, each OR-ing its error bits
-  into one device status word that is read once at the end.  A clear word means every
-  step read what a checked read returns; otherwise the hidden read count is restored
-  and the direction runs again with a check per step, which raises or retries in FP64
-  at the step where the reference does.
+  into one device status word that is read once at the end.  A GRU whose hidden read
+  runs on an MFMA kernel issues all its steps (quantize the state, read, add the bias,
+  gates) from one native call, ``hip.gru_sequence``; other cells queue them from
+  Python.  A clear word means every step read what a checked read returns; otherwise
+  the hidden read count is restored and the direction runs again with a check per
+  step, which raises or retries in FP64 at the step where the reference does.
 
 Both apply only to inference (no hardware-aware gradients wanted) and only where no
 module hooks are registered on the cell or its projections, since they call the
@@ -279,16 +281,13 @@ class _AnalogRecurrent(nn.Module):
         if reverse:
             order.reverse()
         projected = self._projected_inputs(cell, sequence)
-        if projected is None:
-            states = []
-            for step in order:
-                hidden = cell(sequence[step], hidden)
-                states.append(hidden)
-        else:
-            states, hidden = self._steps(cell, projected, order, hidden)
-        if reverse:
-            states.reverse()
-        return torch.stack(states), hidden
+        if projected is not None:
+            return self._steps(cell, projected, order, hidden)
+        states = []
+        for step in order:
+            hidden = cell(sequence[step], hidden)
+            states.append(hidden)
+        return _in_time_order(states, order), hidden
 
     def _projected_inputs(self, cell, sequence):
         """Every step's input projection from one read, or None to read per step."""
@@ -315,14 +314,24 @@ class _AnalogRecurrent(nn.Module):
 
     @staticmethod
     def _steps(cell, projected, order, hidden):
-        """The steps of one direction from precomputed input projections: first with the
-        hidden reads' checks deferred to one status word, if the hidden projection allows
-        it, then (if that word is set) again with a check per step.
+        """([T, B, H] states in time order, final state) of one direction from precomputed
+        input projections.  A GRU whose hidden read allows it runs every step in one native
+        call (``hip.gru_sequence``) with the checks deferred to one status word; other
+        cells queue their steps from Python with the same deferral; if that word is set,
+        the steps run again with a check per step.
 
         If a step raises, the input projection's read count is set to what per-step
         reading would have left (one more than the steps completed before it); the
         hidden projection's count is what its reads left."""
         input_start = cell.input._event - len(order)
+        if _native_eligible(cell, projected, hidden, len(order)):
+            try:
+                result = _native_steps(cell, projected, order, hidden)
+            except Exception:
+                cell.input._event = input_start + 1
+                raise
+            if result is not None:
+                return result
         attempts = ((True, False) if cell.hidden._deferrable(hidden, len(order)) else (False,))
         for deferred in attempts:
             hidden_start = cell.hidden._event
@@ -338,9 +347,58 @@ class _AnalogRecurrent(nn.Module):
                 cell.input._event = input_start + done + 1
                 raise
             if status is None or int(status.item()) == 0:
-                return states, state
+                return _in_time_order(states, order), state
             cell.hidden._event = hidden_start
         raise AssertionError("the checked attempt always returns or raises")
+
+
+def _in_time_order(states, order):
+    """Stack states collected in traversal ``order`` as [T, ...] in time order."""
+    if order and order[0] > order[-1]:
+        states = states[::-1]
+    return torch.stack(states)
+
+
+def _native_eligible(cell, projected, hidden, steps):
+    """Whether a GRU direction can run in one ``hip.gru_sequence`` call: an inference
+    cell whose hidden read is deferrable FP32 with dynamic input scales on an MFMA kernel."""
+    if not isinstance(cell, AnalogGRUCell):
+        return False
+    matrix = cell.hidden
+    if (type(matrix) is not AnalogLinear or matrix.input_scale is not None
+            or projected.dtype != torch.float32 or not matrix._deferrable(hidden, steps)):
+        return False
+    arrays = -(-matrix.in_features // matrix.config.array_size[0])
+    return hip.mm_kernel(matrix.config, hidden.shape[0], arrays, matrix.p) in (1, 2)
+
+
+def _native_steps(cell, projected, order, hidden):
+    """The steps of ``_AnalogRecurrent._steps`` as one native call: ([T, B, H] states,
+    final state), or None (read count unchanged) when the status word is set."""
+    matrix = cell.hidden
+    config = matrix.config
+    batch = hidden.shape[0]
+    arrays = -(-matrix.in_features // config.array_size[0])
+    codes_t = matrix._column_codes()
+    source = None
+    if hip.mm_kernel(config, batch, arrays, matrix.p) == 2 and hip.terms_event_independent(config):
+        workspace, reuse, source = matrix._terms_workspace(batch, arrays, hidden.device, codes_t)
+    else:
+        workspace = hip._workspace(config, batch, arrays, matrix.p, hidden.device)
+        reuse = False
+    status = hip.status_word(hidden.device)
+    bias = None if matrix.bias is None else matrix.bias.contiguous()
+    columns = matrix.p * config.array_size[1]
+    states = hip.gru_sequence(config, projected.contiguous(), hidden.contiguous(), matrix.packed,
+                              codes_t, matrix.weight_scale.reshape(-1, columns), bias,
+                              matrix.seed, matrix._event, reverse=order[0] > order[-1],
+                              status=status, workspace=workspace, reuse_terms=reuse)
+    if source is not None:
+        matrix._terms_source = source
+    if int(status.item()):
+        return None
+    matrix._event += len(order)
+    return states, states[order[-1]]
 
 
 class AnalogRNN(_AnalogRecurrent):

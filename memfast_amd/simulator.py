@@ -589,7 +589,8 @@ class AnalogMatrix(nn.Module):
             variant = tuning.schedule_variant(schedule)
             workspace, reuse, source = None, False, None
             if kernel == 2 and hip.terms_event_independent(config):
-                workspace, reuse, source = self._terms_workspace(q, codes_t, variant)
+                workspace, reuse, source = self._terms_workspace(q.shape[0], q.shape[1], q.device,
+                                                                 codes_t, variant)
             output = hip.mm(q, xscale, packed, codes_t, self.weight_scale.reshape(-1, columns),
                             config, self.seed, event, variant=variant, status=status,
                             workspace=workspace, reuse_terms=reuse,
@@ -624,17 +625,17 @@ class AnalogMatrix(nn.Module):
             return None, False
         return self._execute_checked(q, xscale, schedule, event, stable=True)
 
-    def _terms_workspace(self, q, codes_t, variant=tuning.DEFAULT_VARIANT):
+    def _terms_workspace(self, rows, arrays, device, codes_t, variant=tuning.DEFAULT_VARIANT):
         """Workspace of the noisy MFMA read kept across calls, and whether it still holds
         this program's conductance terms (same kernel codes object and version, seed).
 
         Write variation, drift and stuck-at faults do not depend on the read event
         (memfast/reference.py:36-46), so those samples are identical on every read
         of a programmed matrix and need not be drawn again."""
-        need = hip.mm_workspace_bytes(self.config, q.shape[0], q.shape[1], self.p, variant)
+        need = hip.mm_workspace_bytes(self.config, rows, arrays, self.p, variant)
         workspace = self._workspace
-        if workspace is None or workspace.numel() < need or workspace.device != q.device:
-            workspace = torch.empty(max(1, need), dtype=torch.uint8, device=q.device)
+        if workspace is None or workspace.numel() < need or workspace.device != device:
+            workspace = torch.empty(max(1, need), dtype=torch.uint8, device=device)
             self._workspace, self._terms_source = workspace, None
         source = (codes_t, codes_t._version, self.seed)
         held = self._terms_source

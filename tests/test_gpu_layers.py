@@ -529,14 +529,15 @@ def test_gru_hooks_see_every_step(hip_device):
 
 
 def test_gru_gate_failure_sets_per_step_read_counts(hip_device, monkeypatch):
-    """A failure after step 2's hidden read (forced from the host in the gate call)
-    leaves both projections at three reads, as per-step reading would."""
+    """Steps queued from Python: a failure after step 2's hidden read (forced from the host
+    in the gate call) leaves both projections at three reads, as per-step reading would."""
     from memfast_amd.nn import recurrent
     cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
                  nonidealities=Nonidealities(write_variation=0.02))
     torch.manual_seed(17)
     source = nn.GRU(40, 64).to(hip_device)
     layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    monkeypatch.setattr(recurrent, "_native_eligible", lambda *args: False)
     gates = recurrent.hip.gru_gates
     count = {"calls": 0}
 
@@ -551,3 +552,50 @@ def test_gru_gate_failure_sets_per_step_read_counts(hip_device, monkeypatch):
         layer(torch.randn(6, 3, 40, device=hip_device))
     cell = layer.cells[0]
     assert (cell.input._event, cell.hidden._event) == (3, 3)
+
+
+def test_gru_native_sequence_failure_counts_one_input_read(hip_device, monkeypatch):
+    """A failing native sequence call (forced from the host) fails as step 0's hidden read
+    would: one input read, no hidden read."""
+    from memfast_amd.nn import recurrent
+    cfg = Config(**(BASE | dict(input_quant_gran=(1, None))),
+                 nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(18)
+    source = nn.GRU(40, 64).to(hip_device)
+    layer = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    x = torch.randn(6, 3, 40, device=hip_device)
+    assert recurrent._native_eligible(layer.cells[0], torch.empty(6, 3, 192, device=hip_device),
+                                      torch.zeros(3, 64, device=hip_device), 6)
+
+    def failing(*args, **kwargs):
+        raise RuntimeError("forced sequence failure")
+
+    monkeypatch.setattr(recurrent.hip, "gru_sequence", failing)
+    with pytest.raises(RuntimeError, match="forced sequence failure"):
+        layer(x)
+    cell = layer.cells[0]
+    assert (cell.input._event, cell.hidden._event) == (1, 0)
+
+
+@pytest.mark.parametrize("kind", ["ideal", "write"])
+@pytest.mark.parametrize("bidirectional", [False, True])
+def test_gru_native_and_python_steps_agree(hip_device, kind, bidirectional, monkeypatch):
+    """The native sequence call (ideal: k_ideal, write noise: k_noisy) equals the steps
+    queued from Python, bit for bit, with the same read counts."""
+    from memfast_amd.nn import recurrent
+    cfg = config(kind, input_quant_gran=(1, None))
+    torch.manual_seed(19)
+    source = nn.GRU(40, 96, num_layers=2, bidirectional=bidirectional).to(hip_device)
+    x = torch.randn(8, 5, 40, device=hip_device)
+    native = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    python = AnalogGRU(source, Simulator(cfg, device=hip_device), name="gru")
+    assert recurrent._native_eligible(native.cells[0], torch.empty(8, 5, 288, device=hip_device),
+                                      torch.zeros(5, 96, device=hip_device), 8)
+    got, got_h = native(x)
+    with monkeypatch.context() as patch:
+        patch.setattr(recurrent, "_native_eligible", lambda *args: False)
+        expected, expected_h = python(x)
+    assert torch.equal(got.view(torch.int32), expected.view(torch.int32))
+    assert torch.equal(got_h.view(torch.int32), expected_h.view(torch.int32))
+    for a, b in zip(native.cells, python.cells):
+        assert (a.input._event, a.hidden._event) == (b.input._event, b.hidden._event) == (8, 8)
