@@ -877,18 +877,21 @@ int mf_quantize_inputs(const mf_config *cfg, const float *x, int64_t n, int64_t 
     } else if (gr == 1 && vec && pow2 && quads <= 1024) {
         const dim3 grid{unsigned((n * ncg * 64 + 255) / 256)};
         const int V = int(quads / 64);
+        // The waves fill the per-read scale table themselves.
+        const ReadTable reads{direct ? nullptr : xscale, m * Gr, R, P, Gr};
         if (V == 2)
             hipLaunchKernelGGL(k_row_groups_wave<2>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
-                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT), reads);
         else if (V == 4)
             hipLaunchKernelGGL(k_row_groups_wave<4>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
-                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT), reads);
         else if (V == 8)
             hipLaunchKernelGGL(k_row_groups_wave<8>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
-                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT), reads);
         else
             hipLaunchKernelGGL(k_row_groups_wave<16>, grid, dim3(256), 0, s, x, n, k, ld, ncg, kp,
-                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT));
+                               -upper, upper, mask, q, scale, status, u32(MF_STATUS_INPUT), reads);
+        return check_launch("input quantization");
     } else if (gr == 1 && gc <= 1024) {
         if (vec)
             hipLaunchKernelGGL(k_row_groups<true>, dim3(grid_for(n * ncg)), dim3(256), 0, s, x, n, k,

@@ -213,10 +213,17 @@ __global__ void k_row_groups(const float *x, i64 n, i64 k, i64 ld, i64 gc, i64 n
 __global__ void k_row_groups_lanes(const float *x, i64 n, i64 k, i64 ld, int L, i64 ncg, i64 kp,
                                    float lower, float upper, u32 mask, u8 *q, float *scale,
                                    u32 *status, u32 flag);
+// The per-read scale table a row-group quantizer may fill as it goes: xscale
+// [n, G] (NULL: not filled) over reads of P rows, Gr per array of R rows.
+struct ReadTable {
+    float *xscale;
+    i64 G;
+    int R, P, Gr;
+};
 template <int V>
 __global__ void k_row_groups_wave(const float *x, i64 n, i64 k, i64 ld, i64 ncg, i64 kp,
                                   float lower, float upper, u32 mask, u8 *q, float *scale,
-                                  u32 *status, u32 flag);
+                                  u32 *status, u32 flag, const ReadTable reads);
 template <int GR, bool WORD>
 __global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
                                  i64 p, float lower, float upper, u32 mask, u8 *packed,

@@ -339,16 +339,36 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
 __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, i64 ldt,
                                   i64 ncols, const float *xscale, const float *wscale, i64 ldws,
                                   float *out, i64 ldo, int lp, u32 *status) {
+    // Reads arrive in batches of RESTORE_BATCH: a batch's loads are all issued before
+    // its values enter the cascade, so a thread waits on memory once per batch rather
+    // than once per read.  The arithmetic and the summation order are unchanged.
+    constexpr int RESTORE_BATCH = 8;
     bool finite = true;
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < n * ncols;
          i += i64(gridDim.x) * blockDim.x) {
         const i64 v = i / ncols, c = i - v * ncols;
+        const float *tv = totals + v * G * ldt + c;
+        const float *xv = xscale + v * G;
+        const float *wv = wscale + c;
         Cascade<float> cascade;
         cascade.reset();
-        for (i64 g = 0; g < g_run; ++g) {
-            float x = totals[(v * G + g) * ldt + c] * xscale[v * G + g];
-            x = x * wscale[g * ldws + c];
-            cascade.push(x, lp);
+        for (i64 g0 = 0; g0 < g_run; g0 += RESTORE_BATCH) {
+            float t[RESTORE_BATCH], xs[RESTORE_BATCH], ws[RESTORE_BATCH];
+#pragma unroll
+            for (int j = 0; j < RESTORE_BATCH; ++j) {
+                const i64 g = g0 + j < g_run ? g0 + j : g_run - 1;   // past the end: unused
+                t[j] = tv[g * ldt];
+                xs[j] = xv[g];
+                ws[j] = wv[g * ldws];
+            }
+#pragma unroll
+            for (int j = 0; j < RESTORE_BATCH; ++j) {
+                if (g0 + j < g_run) {
+                    float x = t[j] * xs[j];
+                    x = x * ws[j];
+                    cascade.push(x, lp);
+                }
+            }
         }
         const float s = cascade.finish();
         out[v * ldo + c] = s;

@@ -190,11 +190,14 @@ __global__ void k_row_groups_lanes(const float *x, i64 n, i64 k, i64 ld, int L, 
 }
 
 // Wave-wide row groups of gc = 256*V floats: one wave per group, V float4 per
-// lane kept in registers (one pass), peak reduced across the wave.
+// lane kept in registers (one pass), peak reduced across the wave.  With `reads`
+// (not NULL) the wave also writes the per-read scale table xscale [n, G] for the
+// reads whose first physical row (clamped to k-1, as k_input_scales takes it)
+// lies in its group, so no separate gather pass is needed.
 template <int V>
 __global__ void k_row_groups_wave(const float *x, i64 n, i64 k, i64 ld, i64 ncg, i64 kp,
                                   float lower, float upper, u32 mask, u8 *q, float *scale,
-                                  u32 *status, u32 flag) {
+                                  u32 *status, u32 flag, const ReadTable reads) {
     const i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x;
     const i64 grp = t >> 6;
     const int lane = int(t & 63);
@@ -217,6 +220,13 @@ __global__ void k_row_groups_wave(const float *x, i64 n, i64 k, i64 ld, i64 ncg,
     for (int off = 1; off < 64; off <<= 1) peak = fmaxf(peak, __shfl_xor(peak, off, 64));
     const float s = group_scale(peak, upper);
     if (lane == 0) scale[grp] = s;
+    if (reads.xscale) {
+        for (i64 rd = lane; rd < reads.G; rd += 64) {
+            i64 first = (rd / reads.Gr) * reads.R + (rd % reads.Gr) * reads.P;
+            first = first < k ? first : k - 1;
+            if (first / (256 * V) == j) reads.xscale[row * reads.G + rd] = s;
+        }
+    }
     u8 *dst = q + row * kp;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
@@ -234,13 +244,14 @@ __global__ void k_row_groups_wave(const float *x, i64 n, i64 k, i64 ld, i64 ncg,
     if (!finite && status) atomicOr(status, flag);
 }
 template __global__ void k_row_groups_wave<2>(const float *, i64, i64, i64, i64, i64, float, float,
-                                              u32, u8 *, float *, u32 *, u32);
+                                              u32, u8 *, float *, u32 *, u32, const ReadTable);
 template __global__ void k_row_groups_wave<4>(const float *, i64, i64, i64, i64, i64, float, float,
-                                              u32, u8 *, float *, u32 *, u32);
+                                              u32, u8 *, float *, u32 *, u32, const ReadTable);
 template __global__ void k_row_groups_wave<8>(const float *, i64, i64, i64, i64, i64, float, float,
-                                              u32, u8 *, float *, u32 *, u32);
+                                              u32, u8 *, float *, u32 *, u32, const ReadTable);
 template __global__ void k_row_groups_wave<16>(const float *, i64, i64, i64, i64, i64, float,
-                                               float, u32, u8 *, float *, u32 *, u32);
+                                               float, u32, u8 *, float *, u32 *, u32,
+                                               const ReadTable);
 
 // Column groups of GR rows held in registers: thread = (physical column, one
 // row group), so every lane issues its GR coalesced loads at once.  Writes the
