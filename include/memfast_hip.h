@@ -324,6 +324,18 @@ int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, in
 /* Fixed-scale input tiles (scale [k]). */
 int mf_input_tiles_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k, int64_t ld,
                         const double *scale, uint32_t *q, double *xscale, void *stream);
+
+/* Implicit im2col for wide configurations: the tiles mf_input_tiles_wide (fixed_scale
+ * != NULL, [K] FP64 per-column scales) or mf_quantize_inputs_wide (fixed_scale == NULL:
+ * groups of gr rows and gc columns, `work` uint64 and `scale` FP64 scratch of
+ * [ceil(rows/gr), ceil(K/gc)]) produce from a convolution group's patch matrix
+ * (memfast/nn/convolution.py:49-54, the same order as mf_conv_input_tiles), gathered
+ * from the FP64 NCHW input x.  q [rows, m, R] uint32 codes, xscale [rows, m*Gr] FP64; a
+ * non-finite gathered value sets MF_STATUS_INPUT in status (may be NULL). */
+int mf_conv_input_tiles_wide(const mf_config *cfg, const double *x, const mf_conv_geometry *geom,
+                             const double *fixed_scale, int64_t gr, int64_t gc, uint64_t *work,
+                             double *scale, uint32_t *q, double *xscale, uint32_t *status,
+                             void *stream);
 /* Weight programming: packed [m, p, R, C] as int64 (the reference's checkpoint
  * dtype) and the same codes as uint32_t for the read kernels. */
 int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, int64_t o,

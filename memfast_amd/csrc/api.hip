@@ -740,6 +740,24 @@ static void launch_group_max_f32(const float *x, i64 rows, i64 cols, i64 ld, i64
 
 using namespace mf;
 
+// Shape checks shared by the implicit im2col entry points.
+static int check_conv_geometry(const mf_conv_geometry &g) {
+    if (g.n < 1 || g.channels < 1 || g.height < 1 || g.width < 1 || g.c0 < 0 ||
+        g.group_channels < 1 || g.c0 + g.group_channels > g.channels || g.kh < 1 || g.kw < 1 ||
+        g.sh < 1 || g.sw < 1 || g.ph < 0 || g.pw < 0 || g.dh < 1 || g.dw < 1)
+        return fail(MF_E_INVALID, "invalid convolution geometry");
+    if (g.height > 0x3FFFFFFF || g.width > 0x3FFFFFFF || g.ph > 0x3FFFFFFF || g.pw > 0x3FFFFFFF ||
+        i64(g.dh) * (g.kh - 1) > 0x3FFFFFFF || i64(g.dw) * (g.kw - 1) > 0x3FFFFFFF)
+        return fail(MF_E_UNSUPPORTED, "convolution extent too large");
+    const i64 ho = (g.height + 2 * i64(g.ph) - i64(g.dh) * (g.kh - 1) - 1) / g.sh + 1;
+    const i64 wo = (g.width + 2 * i64(g.pw) - i64(g.dw) * (g.kw - 1) - 1) / g.sw + 1;
+    if (g.height + 2 * i64(g.ph) <= i64(g.dh) * (g.kh - 1) ||
+        g.width + 2 * i64(g.pw) <= i64(g.dw) * (g.kw - 1) || g.out_height != ho ||
+        g.out_width != wo)
+        return fail(MF_E_INVALID, "convolution output size does not match the geometry");
+    return MF_OK;
+}
+
 extern "C" {
 
 int32_t mf_abi_version(void) { return MF_ABI_VERSION; }
@@ -790,20 +808,9 @@ int mf_conv_input_tiles(const mf_config *cfg, const float *x, const mf_conv_geom
     if (st) return st;
     if (!x || !geom || !q || !xscale) return fail(MF_E_INVALID, "invalid conv input-tile arguments");
     const mf_conv_geometry g = *geom;
-    if (g.n < 1 || g.channels < 1 || g.height < 1 || g.width < 1 || g.c0 < 0 ||
-        g.group_channels < 1 || g.c0 + g.group_channels > g.channels || g.kh < 1 || g.kw < 1 ||
-        g.sh < 1 || g.sw < 1 || g.ph < 0 || g.pw < 0 || g.dh < 1 || g.dw < 1)
-        return fail(MF_E_INVALID, "invalid convolution geometry");
-    if (g.height > 0x3FFFFFFF || g.width > 0x3FFFFFFF || g.ph > 0x3FFFFFFF || g.pw > 0x3FFFFFFF ||
-        i64(g.dh) * (g.kh - 1) > 0x3FFFFFFF || i64(g.dw) * (g.kw - 1) > 0x3FFFFFFF)
-        return fail(MF_E_UNSUPPORTED, "convolution extent too large");
-    const i64 ho = (g.height + 2 * i64(g.ph) - i64(g.dh) * (g.kh - 1) - 1) / g.sh + 1;
-    const i64 wo = (g.width + 2 * i64(g.pw) - i64(g.dw) * (g.kw - 1) - 1) / g.sw + 1;
-    if (g.height + 2 * i64(g.ph) <= i64(g.dh) * (g.kh - 1) ||
-        g.width + 2 * i64(g.pw) <= i64(g.dw) * (g.kw - 1) || g.out_height != ho ||
-        g.out_width != wo)
-        return fail(MF_E_INVALID, "convolution output size does not match the geometry");
-    const i64 rows = g.n * ho * wo;
+    st = check_conv_geometry(g);
+    if (st) return st;
+    const i64 rows = g.n * g.out_height * g.out_width;
     const i64 K = g.group_channels * g.kh * g.kw;
     const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
     const i64 m = (K + R - 1) / R, kp = m * R;
@@ -838,6 +845,51 @@ int mf_conv_input_tiles(const mf_config *cfg, const float *x, const mf_conv_geom
     hipLaunchKernelGGL(k_input_scales, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s, rows, K,
                        m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
     return check_launch("conv input tiles");
+}
+
+int mf_conv_input_tiles_wide(const mf_config *cfg, const double *x, const mf_conv_geometry *geom,
+                             const double *fixed_scale, int64_t gr, int64_t gc, uint64_t *work,
+                             double *scale, uint32_t *q, double *xscale, uint32_t *status,
+                             void *stream) {
+    int st = check_wide(cfg);
+    if (st) return st;
+    if (!x || !geom || !q || !xscale) return fail(MF_E_INVALID, "invalid conv input-tile arguments");
+    const mf_conv_geometry g = *geom;
+    st = check_conv_geometry(g);
+    if (st) return st;
+    const i64 rows = g.n * g.out_height * g.out_width;
+    const i64 K = g.group_channels * g.kh * g.kw;
+    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (K + R - 1) / R, kp = m * R;
+    const int bits = cfg->activation_bits;
+    const double upper = double((i64(1) << (bits - 1)) - 1);
+    const double lower = cfg->bw_e ? -double(i64(1) << (bits - 1)) : -upper;
+    const u64 mask = bits == 64 ? ~u64(0) : (u64(1) << bits) - 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (fixed_scale) {
+        hipLaunchKernelGGL(k_conv_codes_f64, dim3(grid_for(rows * kp)), dim3(256), 0, s, x, g, K,
+                           kp, fixed_scale, i64(1), i64(1), K, 1, lower, upper, mask, q, status,
+                           u32(MF_STATUS_INPUT));
+        hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s,
+                           rows, K, m * Gr, R, P, Gr, fixed_scale, i64(1), i64(1), K, 1, xscale);
+        return check_launch("wide conv input tiles");
+    }
+    if (!work || !scale || gr < 1 || gc < 1)
+        return fail(MF_E_INVALID, "dynamic conv input tiles need work, scale and group sizes");
+    gr = gr < rows ? gr : rows;
+    gc = gc < K ? gc : K;
+    const i64 nrg = (rows + gr - 1) / gr, ncg = (K + gc - 1) / gc;
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(2 * nrg * ncg)), dim3(256), 0, s,
+                       reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
+    hipLaunchKernelGGL(k_conv_group_max_f64, dim3(grid_for(rows * K)), dim3(256), 0, s, x, g, K,
+                       gr, gc, ncg, work, status, u32(MF_STATUS_INPUT));
+    hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
+                       nrg * ncg, bits, cfg->bw_e, upper, scale);
+    hipLaunchKernelGGL(k_conv_codes_f64, dim3(grid_for(rows * kp)), dim3(256), 0, s, x, g, K, kp,
+                       scale, gr, gc, ncg, 0, lower, upper, mask, q, status, u32(MF_STATUS_INPUT));
+    hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s, rows,
+                       K, m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
+    return check_launch("wide conv input tiles");
 }
 
 static i64 lcm4(i64 gr) { return gr % 4 == 0 ? gr : (gr % 2 == 0 ? 2 * gr : 4 * gr); }
@@ -1140,7 +1192,10 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32
         *bytes = noisy_terms_bytes(cfg, m, p) +
                  noisy_scratch_bytes(cfg, n, m, p, variant_split(variant));
     } else if (wide_plan_ok(cfg, n, m, p)) {
-        *bytes = wide_codes_bytes(n, m, cfg) + (p * cfg->cols + 31) / 32 * wide_block_bytes(cfg, m);
+        // At least the two 32-column blocks the wide read's chunking needs, even for
+        // outputs narrower than 64 columns.
+        const i64 blocks = std::max<i64>(2, (p * cfg->cols + 31) / 32);
+        *bytes = wide_codes_bytes(n, m, cfg) + blocks * wide_block_bytes(cfg, m);
     } else {
         *bytes = 0;
     }

@@ -244,6 +244,12 @@ template <typename I>
 __global__ void k_input_codes4(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
                                i64 gr, i64 gc, i64 ncg, int fixed, float lower, float upper,
                                u32 mask, u8 *q);
+__global__ void k_conv_group_max_f64(const double *x, const mf_conv_geometry g, i64 K, i64 gr,
+                                     i64 gc, i64 ncg, u64 *work, u32 *status, u32 flag);
+__global__ void k_conv_codes_f64(const double *x, const mf_conv_geometry g, i64 K, i64 kp,
+                                 const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
+                                 double lower, double upper, u64 mask, u32 *q, u32 *status,
+                                 u32 flag);
 constexpr int CONV_CHUNK_COLS = 128;   // patch columns per k_conv_codes block
 __global__ void k_conv_codes(const float *x, const mf_conv_geometry g, i64 K, i64 kp,
                              const float *scale, i64 gr, i64 gc, i64 ncg, float lower, float upper,

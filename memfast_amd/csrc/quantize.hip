@@ -1158,4 +1158,66 @@ __global__ void k_weight_scales_f64(i64 k, i64 o, i64 groups, i64 op, int R, int
     }
 }
 
+// ---- implicit im2col for wide configurations ------------------------------
+// The patch matrix of k_conv_codes (same row and column order) gathered from an FP64
+// NCHW image, one element per thread: wide configurations are the rarer case, and
+// their codes are 32-bit words, so the LDS byte tiling of the narrow kernel does not
+// apply.
+
+// Value of patch element (row, col) of the geometry, 0 outside the image.
+__device__ __forceinline__ double conv_value_f64(const double *x, const mf_conv_geometry &g,
+                                                 i64 row, i64 col) {
+    const i64 plane = g.out_height * g.out_width;
+    const i64 b = row / plane, l = row - b * plane;
+    const i64 oh = l / g.out_width, ow = l - oh * g.out_width;
+    const i64 taps = i64(g.kh) * g.kw;
+    const i64 c = col / taps, rem = col - c * taps;
+    const i64 i = rem / g.kw, j = rem - i * g.kw;
+    const i64 ih = oh * g.sh - g.ph + i * g.dh, iw = ow * g.sw - g.pw + j * g.dw;
+    if (ih < 0 || ih >= g.height || iw < 0 || iw >= g.width) return 0.0;
+    return x[((b * g.channels + g.c0 + c) * g.height + ih) * g.width + iw];
+}
+
+// Group maxima |v| of the patch matrix as FP64 bit patterns into work [ceil(rows/gr), ncg]
+// (cleared); a non-finite gathered value sets `flag`.
+__global__ void k_conv_group_max_f64(const double *x, const mf_conv_geometry g, i64 K, i64 gr,
+                                     i64 gc, i64 ncg, u64 *work, u32 *status, u32 flag) {
+    const i64 rows = g.n * g.out_height * g.out_width;
+    bool finite = true;
+    for (i64 e = i64(blockIdx.x) * blockDim.x + threadIdx.x; e < rows * K;
+         e += i64(gridDim.x) * blockDim.x) {
+        const i64 row = e / K, col = e - row * K;
+        const double v = fabs(conv_value_f64(x, g, row, col));
+        finite = finite && v <= DBL_MAX;
+        const u64 bits = u64(__double_as_longlong(v));
+        if (bits)
+            atomicMax(reinterpret_cast<unsigned long long *>(&work[(row / gr) * ncg + col / gc]),
+                      static_cast<unsigned long long>(bits));
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
+// Codes q [rows, kp] (zero past K) with group scales [ceil(rows/gr), ncg], or with a
+// fixed per-column scale [K] (`fixed`); a non-finite gathered value sets `flag`.
+__global__ void k_conv_codes_f64(const double *x, const mf_conv_geometry g, i64 K, i64 kp,
+                                 const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
+                                 double lower, double upper, u64 mask, u32 *q, u32 *status,
+                                 u32 flag) {
+    const i64 rows = g.n * g.out_height * g.out_width;
+    bool finite = true;
+    for (i64 e = i64(blockIdx.x) * blockDim.x + threadIdx.x; e < rows * kp;
+         e += i64(gridDim.x) * blockDim.x) {
+        const i64 row = e / kp, col = e - row * kp;
+        u32 code = 0;
+        if (col < K) {
+            const double v = conv_value_f64(x, g, row, col);
+            finite = finite && fabs(v) <= DBL_MAX;
+            const double s = fixed ? scale[col] : scale[(row / gr) * ncg + col / gc];
+            code = quantize_code_f64(v, s, lower, upper, mask);
+        }
+        q[e] = code;
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
 }  // namespace mf

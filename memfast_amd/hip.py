@@ -160,6 +160,8 @@ SIGNATURES = {
     "mf_quantize_inputs_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                  _P], ct.c_int),
     "mf_input_tiles_wide": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _P, _P], ct.c_int),
+    "mf_conv_input_tiles_wide": ([_CFG, _P, ct.POINTER(MFConvGeometry), _P, _I64, _I64, _P, _P,
+                                  _P, _P, _P, _P], ct.c_int),
     "mf_quantize_weights_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                   _P, _P], ct.c_int),
     "mf_restore_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, ct.c_uint32, ct.c_uint64, _P, _P],
@@ -461,21 +463,22 @@ def conv_input_tiles(x, config, geometry, fixed_scale=None, *, status=None):
     Equals ``input_tiles(F.unfold(x, ...)[:, group block].transpose(1, 2).reshape(-1, K))``
     (memfast/nn/convolution.py:49-54) without building the patch matrix.  ``geometry``
     holds (c0, group_channels, kernel_size, stride, padding, dilation, out_size).
-    Narrow configurations only; a non-finite gathered value raises here without
+    Wide configurations gather from the FP64 image into uint32 codes and FP64 scales,
+    as ``input_tiles`` quantizes them.  A non-finite gathered value raises here without
     ``status``, else sets STATUS_INPUT."""
     supported(config)
     require_device(x)
-    if config.wide:
-        raise BackendError("implicit im2col covers narrow configurations only")
+    wide = config.wide
+    real = torch.float64 if wide else torch.float32
     c0, cg, kernel, stride, padding, dilation, out_size = geometry
-    value = x.to(torch.float32).contiguous()
+    value = x.to(real).contiguous()
     n = value.shape[0]
     rows = n * out_size[0] * out_size[1]
     k = cg * kernel[0] * kernel[1]
     r = config.array_size[0]
     m = math.ceil(k / r)
-    q = torch.empty((rows, m, r), dtype=torch.uint8, device=x.device)
-    xscale = torch.empty((rows, m * config.reads_per_array), dtype=torch.float32, device=x.device)
+    q = torch.empty((rows, m, r), dtype=torch.int32 if wide else torch.uint8, device=x.device)
+    xscale = torch.empty((rows, m * config.reads_per_array), dtype=real, device=x.device)
     geom = MFConvGeometry(n, value.shape[1], value.shape[2], value.shape[3], c0, cg,
                           out_size[0], out_size[1], kernel[0], kernel[1], stride[0], stride[1],
                           padding[0], padding[1], dilation[0], dilation[1])
@@ -485,15 +488,16 @@ def conv_input_tiles(x, config, geometry, fixed_scale=None, *, status=None):
     if fixed_scale is None:
         gr, gc = _group_dims((rows, k), config.input_quant_gran)
         grid = (math.ceil(rows / gr), math.ceil(k / gc))
-        scale = torch.empty(grid, dtype=torch.float32, device=x.device)
-        work = torch.empty(grid, dtype=torch.int32, device=x.device)
+        scale = torch.empty(grid, dtype=real, device=x.device)
+        work = torch.empty(grid, dtype=torch.int64 if wide else torch.int32, device=x.device)
     else:
-        fixed = fixed_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
+        fixed = fixed_scale.to(device=x.device, dtype=real).reshape(-1).contiguous()
         if fixed.numel() != k:
             raise ValueError("fixed input scale must have one entry per input feature")
+    entry = library().mf_conv_input_tiles_wide if wide else library().mf_conv_input_tiles
     with _on(x.device):
         check(
-            library().mf_conv_input_tiles(
+            entry(
                 ct.byref(descriptor(config)), _ptr(value), ct.byref(geom), _ptr(fixed), gr, gc,
                 _ptr(work), _ptr(scale), _ptr(q), _ptr(xscale), _ptr(own_status),
                 _stream(x.device),

@@ -1,11 +1,15 @@
-"""Convolution lowered to one programmed matrix per convolution group.
+"""Convolution on programmed matrices, one per convolution group (memfast/nn/convolution.py).
 
-Restates memfast/nn/convolution.py: each group's [N*L, Cin/g*kh*kw] patch
-matrix (F.unfold's) is read through its own AnalogMatrix; stride, dilation,
-numeric padding, padding modes and groups are preserved.  In default mode a
-narrow configuration never builds the patch matrix: the input quantizer
-gathers each patch element straight from the NCHW image (implicit im2col),
-which yields the same codes and scales.
+Group g's weights [O/groups, Cin/groups*kh*kw] are one programmed matrix, read with the
+group's patch matrix: F.unfold's [N*L, Cin/groups*kh*kw] rows for that group's input
+channels.  Stride, dilation, numeric padding, the padding modes and groups are kept.
+
+The patch matrix itself is never built where it can be avoided: the input quantizer
+gathers each patch element straight from the NCHW image (implicit im2col,
+``hip.conv_input_tiles``), which yields the same codes and scales as quantizing the
+unfolded matrix.  This covers default and tuned mode and narrow and wide
+configurations.  Only inputs that the read itself would reject (and empty outputs) take
+the unfold route, so that the matrix raises its own error.
 """
 
 import math
@@ -20,6 +24,11 @@ _COPIED = ("in_channels", "out_channels", "kernel_size", "stride", "padding", "d
            "groups", "padding_mode")
 
 
+def _output_size(extent, padding, dilation, kernel, stride):
+    return [(size + 2 * pad - dil * (k - 1) - 1) // step + 1
+            for size, pad, dil, k, step in zip(extent, padding, dilation, kernel, stride)]
+
+
 class AnalogConv2d(nn.Module):
     """Conv2d whose groups are independently programmed analog matrices."""
 
@@ -29,67 +38,71 @@ class AnalogConv2d(nn.Module):
             raise TypeError("source must be torch.nn.Conv2d")
         if isinstance(source.padding, str):
             raise ValueError("use numeric Conv2d padding before conversion")
-        for attr in _COPIED:
-            setattr(self, attr, getattr(source, attr))
+        for attribute in _COPIED:
+            setattr(self, attribute, getattr(source, attribute))
+        width = source.out_channels // source.groups
         self.matrices = nn.ModuleList()
-        per_group = source.out_channels // source.groups
         for group in range(source.groups):
-            block = slice(group * per_group, (group + 1) * per_group)
-            bias = None if source.bias is None else source.bias[block]
-            self.matrices.append(
-                simulator.map(source.weight[block].flatten(1), bias=bias, name=f"{name}.group{group}")
-            )
+            rows = slice(group * width, (group + 1) * width)
+            self.matrices.append(simulator.map(
+                source.weight[rows].flatten(1), name=f"{name}.group{group}",
+                bias=None if source.bias is None else source.bias[rows]))
+
+    @property
+    def _patch_width(self):
+        return self.in_channels // self.groups * math.prod(self.kernel_size)
 
     @torch.no_grad()
     def forward(self, x):
         if x.ndim != 4 or x.shape[1] != self.in_channels:
             raise ValueError("expected NCHW input with matching channels")
-        height_in, width_in = x.shape[-2:]
+        spatial = _output_size(x.shape[-2:], self.padding, self.dilation, self.kernel_size,
+                               self.stride)
         padding = self.padding
         if self.padding_mode != "zeros":
+            # Non-zero padding modes pad explicitly; the patches then need none.
             ph, pw = padding
             x = F.pad(x, (pw, pw, ph, ph), mode=self.padding_mode)
             padding = (0, 0)
-        spatial = [
-            (extent + 2 * pad - dil * (kernel - 1) - 1) // step + 1
-            for extent, pad, dil, kernel, step in zip(
-                (height_in, width_in), self.padding, self.dilation, self.kernel_size, self.stride
-            )
-        ]
-        outputs = self._implicit(x, padding, spatial)
-        if outputs is None:
-            patches = F.unfold(x, self.kernel_size, self.dilation, padding, self.stride)
-            size = self.in_channels // self.groups * math.prod(self.kernel_size)
-            outputs = [
-                matrix(patches[:, g * size:(g + 1) * size].transpose(1, 2))
-                for g, matrix in enumerate(self.matrices)
-            ]
-        merged = (outputs[0] if len(outputs) == 1 else torch.cat(outputs, dim=-1)).transpose(1, 2)
-        return merged.reshape(x.shape[0], self.out_channels, *spatial)
+        if self._gathers(x, spatial):
+            groups = self._gathered(x, padding, spatial)
+        else:
+            groups = self._unfolded(x, padding)
+        merged = groups[0] if len(groups) == 1 else torch.cat(groups, dim=-1)
+        return merged.transpose(1, 2).reshape(x.shape[0], self.out_channels, *spatial)
 
-    def _implicit(self, x, padding, spatial):
-        """Per-group outputs [N, L, O/groups] read from implicit-im2col input tiles, or
-        None where the patch matrix path applies (tuned mode, wide configurations, and
-        inputs that AnalogMatrix.forward rejects, so it raises its own error)."""
+    def _unfolded(self, x, padding):
+        """Per-group outputs [N, L, O/groups] read from F.unfold's patch matrix."""
+        patches = F.unfold(x, self.kernel_size, self.dilation, padding, self.stride)
+        width = self._patch_width
+        return [matrix(patches[:, g * width:(g + 1) * width].transpose(1, 2))
+                for g, matrix in enumerate(self.matrices)]
+
+    def _gathers(self, x, spatial):
+        """Whether the input tiles can be gathered from the image: inputs every
+        matrix accepts (AnalogMatrix.forward's checks) and a non-empty output."""
         first = self.matrices[0]
-        config = first.config
-        scale_dtype = torch.float32
-        if (first.simulator.mode != "default" or config.wide or x.numel() == 0
-                or not x.is_floating_point() or min(spatial) < 1
-                or x.device != first.packed.device or x.device != first.simulator.device
-                or any(m.weight_scale.dtype != scale_dtype for m in self.matrices)):
-            return None
+        scale_dtype = torch.float64 if first.config.wide else torch.float32
+        return (x.numel() > 0 and x.is_floating_point() and min(spatial) >= 1
+                and x.device == first.packed.device == first.simulator.device
+                and all(m.weight_scale.dtype == scale_dtype for m in self.matrices))
+
+    def _gathered(self, x, padding, spatial):
+        """Per-group outputs [N, L, O/groups] read from input tiles gathered from ``x``.
+
+        Default mode leaves the finiteness check to the read's status word; tuned mode
+        checks it before the schedule search, as the read of an unfolded matrix does."""
         per_group = self.in_channels // self.groups
-        size = per_group * math.prod(self.kernel_size)
-        rows = spatial[0] * spatial[1]
-        meta = torch.empty((x.shape[0], rows, size), dtype=x.dtype, device="meta")
-        value = x.to(torch.float32).contiguous()
+        # Stands in for the patch rows where only their shape and dtype matter.
+        patch_shape = torch.empty((x.shape[0], spatial[0] * spatial[1], self._patch_width),
+                                  dtype=x.dtype, device="meta")
         outputs = []
         for g, matrix in enumerate(self.matrices):
-            status = hip.status_word(x.device)
             geometry = (g * per_group, per_group, self.kernel_size, self.stride, padding,
                         self.dilation, spatial)
-            q, xscale = hip.conv_input_tiles(value, config, geometry, matrix.input_scale,
+            deferred = matrix.simulator.mode == "default"
+            status = hip.status_word(x.device) if deferred else None
+            q, xscale = hip.conv_input_tiles(x, matrix.config, geometry, matrix.input_scale,
                                              status=status)
-            outputs.append(matrix._run(meta, q, xscale, status=status))
+            outputs.append(matrix._run(patch_shape, q, xscale, status=status))
         return outputs

@@ -724,7 +724,7 @@ class AnalogMatrix(nn.Module):
         if self.simulator.mode == "tuned":
             key = (tuple(x.shape), str(x.dtype))
             if key not in self._prepared:
-                with torch.cuda.device(x.device):
+                with torch.cuda.device(q.device):
                     self._prepared[key] = self.simulator._select(self, x, q, xscale, event)
             schedule = self._prepared[key]
         output, finite = self._execute_checked(

@@ -599,3 +599,89 @@ def test_gru_native_and_python_steps_agree(hip_device, kind, bidirectional, monk
     assert torch.equal(got_h.view(torch.int32), expected_h.view(torch.int32))
     for a, b in zip(native.cells, python.cells):
         assert (a.input._event, a.hidden._event) == (b.input._event, b.hidden._event) == (8, 8)
+
+
+WIDE_CONV = {
+    # BFP16 activations, INT4 weights (BASELINE config 5's slicing) on 64x64 arrays
+    "bfp16": dict(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                  weight_slice=(1, 1, 2), bw_e=8, array_size=(64, 64), adc_bits=(6, 6, 7)),
+    # 12-bit INT activations, 32-row reads, groups of 64 columns
+    "int12": dict(activation_bits=12, weight_bits=8, input_slice=(1, 3, 4, 4),
+                  weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,
+                  adc_bits=8, input_quant_gran=(1, 64)),
+}
+
+
+@pytest.mark.parametrize("name", list(WIDE_CONV))
+@pytest.mark.parametrize("geometry", CONV_GEOMETRIES[:5])
+def test_wide_conv_input_tiles_match_unfold(hip_device, name, geometry):
+    """mf_conv_input_tiles_wide == wide input quantization of F.unfold's patch matrix
+    (uint32 codes, FP64 scales), bit for bit, dynamic and fixed scales; small cases also
+    against the oracle's quantizer."""
+    from memfast_amd import hip
+    n, c, groups, kernel, stride, padding, dilation, out = _conv_case(geometry)
+    cfg = Config(**WIDE_CONV[name], nonidealities=Nonidealities(write_variation=0.0))
+    torch.manual_seed(33)
+    x = torch.randn(n, c, *geometry[2:4]) * 3
+    x[:, :, ::3, 1::2] *= 20.0
+    patches = F.unfold(x, kernel, dilation, padding, stride)
+    per_group = c // groups
+    size = per_group * kernel[0] * kernel[1]
+    xd = x.to(hip_device)
+    for g in range(groups):
+        flat = patches[:, g * size:(g + 1) * size].transpose(1, 2).reshape(-1, size)
+        geom = (g * per_group, per_group, kernel, stride, padding, dilation, out)
+        for fixed in (None, torch.rand(1, size, dtype=torch.float64) * 0.1 + 0.01):
+            fixed_dev = None if fixed is None else fixed.to(hip_device)
+            status = hip.status_word(hip_device)
+            q, xscale = hip.conv_input_tiles(xd, cfg, geom, fixed_dev, status=status)
+            ref_q, ref_scale = hip.input_tiles(flat.to(hip_device), cfg, fixed_dev)
+            assert int(status.item()) == 0
+            assert q.dtype == torch.int32 and xscale.dtype == torch.float64
+            assert torch.equal(q.cpu(), ref_q.cpu()), (name, geometry, g, fixed is None)
+            assert torch.equal(xscale.cpu().view(torch.int64), ref_scale.cpu().view(torch.int64))
+            if fixed is None and flat.shape[0] * size <= 100_000:
+                oq, oscale = oracle.input_tiles(flat, cfg)
+                assert torch.equal(q.cpu().to(oq.dtype), oq)
+                assert torch.equal(xscale.cpu().view(torch.int64), oscale.view(torch.int64))
+
+
+@pytest.mark.parametrize("case", ["wide_default", "narrow_tuned", "wide_tuned"])
+def test_conv_gathered_forward_matches_unfold_in_wide_and_tuned_modes(hip_device, case,
+                                                                      tmp_path):
+    """The gathered forward of wide configurations and of tuned mode equals reading
+    F.unfold's patches through the same matrices (same read events), bit for bit."""
+    wide = case.startswith("wide")
+    mode = "tuned" if case.endswith("tuned") else "default"
+    kwargs = WIDE_CONV["int12"] if wide else BASE
+    cfg = Config(**kwargs, nonidealities=Nonidealities(write_variation=0.02))
+    torch.manual_seed(34)
+    source = nn.Conv2d(6, 8, 3, stride=1, padding=1, groups=2).to(hip_device)
+    sim = Simulator(cfg, device=hip_device, mode=mode, cache_dir=tmp_path)
+    layer = AnalogConv2d(source, sim, name="conv")
+    x = torch.randn(2, 6, 9, 9, device=hip_device)
+    got = layer(x)
+    assert all(matrix._event == 1 for matrix in layer.matrices)
+    for matrix in layer.matrices:
+        matrix.reset_read()
+    expected = torch.cat(layer._unfolded(x, (1, 1)), dim=-1).transpose(1, 2).reshape(2, 8, 9, 9)
+    view = torch.int64 if got.dtype == torch.float64 else torch.int32
+    assert got.dtype == torch.float32
+    assert torch.equal(got.view(view), expected.view(view))
+    if mode == "tuned":
+        assert len(sim.records) >= 2
+
+
+def test_conv_tuned_nonfinite_input_raises_before_search(hip_device, tmp_path):
+    """Tuned mode: a non-finite pixel raises the read's error before any schedule is
+    searched or cached."""
+    cfg = config("write")
+    source = nn.Conv2d(4, 4, 3, padding=1).to(hip_device)
+    sim = Simulator(cfg, device=hip_device, mode="tuned", cache_dir=tmp_path)
+    layer = AnalogConv2d(source, sim, name="conv")
+    x = torch.randn(1, 4, 6, 6, device=hip_device)
+    x[0, 2, 3, 3] = float("nan")
+    with pytest.raises(ValueError, match="finite"):
+        layer(x)
+    assert not sim.records and layer.matrices[0]._event == 0
+    assert not any(tmp_path.rglob("*.json"))
