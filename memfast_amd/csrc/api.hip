@@ -285,7 +285,6 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
                       const char **why) {
     if (cfg->wide) { *why = "wide codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
-    if (cfg->has_vnoise) { *why = "voltage variation"; return false; }
     if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
     if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
@@ -371,6 +370,13 @@ i64 noisy_scratch_bytes(const mf_config *cfg, i64 n, i64 m, i64 p, int requested
     return align256(n * m * cfg->reads * p * cfg->cols * 4);
 }
 
+// Voltage-variation input operands (k_voltage_terms): hi and lo fp16 per input
+// slice, vector and physical row.  They sit at the end of the workspace, so the
+// conductance terms keep their place (and stay reusable) whatever the vector count.
+i64 noisy_voltage_bytes(const mf_config *cfg, i64 n, i64 m) {
+    return cfg->has_vnoise ? align256(2 * i64(cfg->n_in) * n * m * cfg->rows * 2) : 0;
+}
+
 // Fields of the `variant` word (include/memfast_hip.h).
 int variant_tile(int32_t v) { return v & 0xFF; }
 int variant_split(int32_t v) { return (v >> MF_MM_SPLIT_SHIFT) & 0xF; }
@@ -398,6 +404,18 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     if (ocols < 0) ocols = ncols;
     if (g_run < 0) g_run = G;
+    const i64 vbytes = noisy_voltage_bytes(cfg, n, m);
+    if (bytes < vbytes) return fail(MF_E_RESOURCE, "workspace below the voltage operands");
+    const uint4 *volt = nullptr;
+    if (vbytes) {
+        // Aligned down to 256 bytes at the end of the workspace.
+        const i64 at = ((bytes - vbytes) / 256) * 256;
+        uint4 *operands = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + at);
+        hipLaunchKernelGGL(k_voltage_terms, dim3(grid_for(i64(cfg->n_in) * n * (kp / 8))),
+                           dim3(256), 0, s, *cfg, q, n, m, seed, event, operands);
+        volt = operands;
+        bytes = at;
+    }
     const i64 per_block = noisy_block_bytes(cfg, m);
     // Split read (fused output only, when the whole program's terms fit).
     const i64 split = totals ? 1 : noisy_split(cfg, n, m, p, split_request);
@@ -447,6 +465,7 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         args.g_begin = 0;
         args.g_end = g_run;
         args.g_step = g_run;
+        args.volt = volt;
         unsigned gz = 1;
         if (use_split) {
             args.totals = 1;
@@ -460,12 +479,16 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         // Benchmark timing brackets the read kernel alone (not the conductance split).
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
         if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-#define MF_NOISY_LAUNCH(KS, NA)                                                                \
-    {                                                                                          \
-        if (nl)                                                                                \
-            hipLaunchKernelGGL((k_noisy<KS, NA, true>), grid, dim3(256), 0, s, plan, args);    \
-        else                                                                                   \
-            hipLaunchKernelGGL((k_noisy<KS, NA, false>), grid, dim3(256), 0, s, plan, args);   \
+#define MF_NOISY_LAUNCH(KS, NA)                                                                 \
+    {                                                                                           \
+        if (volt && nl)                                                                         \
+            hipLaunchKernelGGL((k_noisy<KS, NA, true, true>), grid, dim3(256), 0, s, plan, args);  \
+        else if (volt)                                                                          \
+            hipLaunchKernelGGL((k_noisy<KS, NA, false, true>), grid, dim3(256), 0, s, plan, args); \
+        else if (nl)                                                                            \
+            hipLaunchKernelGGL((k_noisy<KS, NA, true, false>), grid, dim3(256), 0, s, plan, args); \
+        else                                                                                    \
+            hipLaunchKernelGGL((k_noisy<KS, NA, false, false>), grid, dim3(256), 0, s, plan, args); \
     }
         if (ks == 4) MF_NOISY_LAUNCH(4, 5)
         else if (cfg->n_in <= 5) MF_NOISY_LAUNCH(2, 5)
@@ -501,7 +524,6 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
                            bool *small, const char **why) {
     if (!cfg->wide) { *why = "narrow codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
-    if (cfg->has_vnoise) { *why = "voltage variation"; return false; }
     if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
     if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
@@ -1190,7 +1212,8 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32
         *bytes = xb + wb;
     } else if (build_noisy_plan(cfg, m, p, &noisy, &ks, &why)) {
         *bytes = noisy_terms_bytes(cfg, m, p) +
-                 noisy_scratch_bytes(cfg, n, m, p, variant_split(variant));
+                 noisy_scratch_bytes(cfg, n, m, p, variant_split(variant)) +
+                 noisy_voltage_bytes(cfg, n, m);
     } else if (wide_plan_ok(cfg, n, m, p)) {
         // At least the two 32-column blocks the wide read's chunking needs, even for
         // outputs narrower than 64 columns.
@@ -1293,7 +1316,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
     NoisyPlan noisy;
     if (!g && packed_t && aligned && workspace && ideal_extent_ok(cfg, n, m, p) &&
         noisy_extent_ok(n, m, cfg) && build_noisy_plan(cfg, m, p, &noisy, &ks, &why) &&
-        workspace_bytes >= 2 * noisy_block_bytes(cfg, m)) {
+        workspace_bytes >= noisy_voltage_bytes(cfg, n, m) + 2 * noisy_block_bytes(cfg, m)) {
         return launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p, nullptr, seed,
                             event, out, ldo, workspace, workspace_bytes, 0, status, s,
                             (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run,
@@ -1394,8 +1417,10 @@ int mf_mm_static(const mf_config *cfg, const uint8_t *q, const float *xscale, in
         need = xb + wb;
         what = "digit masks of the ideal-device read";
     } else if (!g && packed_t && build_noisy_plan(cfg, m, p, &noisy, &ks, &why)) {
-        need = 2 * noisy_block_bytes(cfg, m);
-        what = "one 64-column chunk of noisy conductance terms";
+        need = noisy_voltage_bytes(cfg, n, m) + 2 * noisy_block_bytes(cfg, m);
+        what = cfg->has_vnoise ? "voltage-noise operands and one 64-column chunk of noisy "
+                                 "conductance terms"
+                               : "one 64-column chunk of noisy conductance terms";
     }
     if (need > MF_STATIC_SCRATCH_BYTES)
         return fail(MF_E_RESOURCE,
@@ -1809,12 +1834,22 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     if (kernel_id == 1) {
         fn = reinterpret_cast<const void *>(&k_ideal<1, 1>);
     } else if (kernel_id == 2) {
-        if (ks4) fn = nl ? reinterpret_cast<const void *>(&k_noisy<4, 5, true>)
-                         : reinterpret_cast<const void *>(&k_noisy<4, 5, false>);
-        else if (cfg->n_in <= 5) fn = nl ? reinterpret_cast<const void *>(&k_noisy<2, 5, true>)
-                                         : reinterpret_cast<const void *>(&k_noisy<2, 5, false>);
-        else fn = nl ? reinterpret_cast<const void *>(&k_noisy<2, 8, true>)
-                     : reinterpret_cast<const void *>(&k_noisy<2, 8, false>);
+        // [ks][vnoise][nonlinear]; ks index 0: KS 2 with up to 5 slices, 1: KS 2 with 8, 2: KS 4.
+        const void *table[3][2][2] = {
+            {{reinterpret_cast<const void *>(&k_noisy<2, 5, false, false>),
+              reinterpret_cast<const void *>(&k_noisy<2, 5, true, false>)},
+             {reinterpret_cast<const void *>(&k_noisy<2, 5, false, true>),
+              reinterpret_cast<const void *>(&k_noisy<2, 5, true, true>)}},
+            {{reinterpret_cast<const void *>(&k_noisy<2, 8, false, false>),
+              reinterpret_cast<const void *>(&k_noisy<2, 8, true, false>)},
+             {reinterpret_cast<const void *>(&k_noisy<2, 8, false, true>),
+              reinterpret_cast<const void *>(&k_noisy<2, 8, true, true>)}},
+            {{reinterpret_cast<const void *>(&k_noisy<4, 5, false, false>),
+              reinterpret_cast<const void *>(&k_noisy<4, 5, true, false>)},
+             {reinterpret_cast<const void *>(&k_noisy<4, 5, false, true>),
+              reinterpret_cast<const void *>(&k_noisy<4, 5, true, true>)}}};
+        const int which = ks4 ? 2 : (cfg->n_in <= 5 ? 0 : 1);
+        fn = table[which][cfg->has_vnoise ? 1 : 0][nl ? 1 : 0];
     } else if (kernel_id == 3) {
         fn = ks4 ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<4, true, false, WIDE_FRAGS_LARGE>)
                        : reinterpret_cast<const void *>(&k_noisy_wide<4, false, false, WIDE_FRAGS_LARGE>))

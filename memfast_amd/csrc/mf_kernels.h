@@ -132,6 +132,9 @@ struct NoisyArgs {
     i64 g_begin, g_end;   // reads of this launch (blockIdx.z adds g_step)
     i64 g_step;
     int totals;
+    // Voltage variation: input operands [2][A][n][kp] fp16 (hi, lo) of digit * (1 + vv*z)
+    // from k_voltage_terms, read instead of the digits of q.
+    const uint4 *volt;
 };
 
 // Terms are k1[w] * (g - L), so the read's MFMA output is in ADC counts.
@@ -139,8 +142,13 @@ template <int KS>
 __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, const float *g_in,
                                      i64 m, i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin,
                                      i64 CB, const NoisyPlan plan, uint4 *gs);
-template <int KS, int NA, bool NONLINEAR>
+template <int KS, int NA, bool NONLINEAR, bool VNOISE>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
+// Input operands of a read with voltage variation (memfast/reference.py:77-82): per
+// input slice a, vector v and physical row k, digit * (1 + vv * z(address)) split into
+// fp16 hi + lo, layout [2][A][n][kp].
+__global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
+                                u64 event, uint4 *volt);
 // (float(T) * xs) * ws summed over reads in torch's cascade order, from slice
 // totals [n, G, ldt]: the epilogue of a read split across blocks.
 __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, i64 ldt,

@@ -25,6 +25,10 @@
 // k_noisy: block = 4 waves (2 column x 2 vector), wave tile 32 columns x 32
 // vectors, A operand = conductance terms, B operand = input digits built in
 // registers from the codes q.  Per read and pair: 2*KS MFMAs and the ADC.
+// With voltage variation (VNOISE) every input digit carries its own factor
+// (1 + vv*z), so the B operand is real too: k_voltage_terms splits digit*(1 + vv*z)
+// into fp16 hi + lo, and a pair takes 3*KS MFMAs (hi*hi + lo*hi + hi*lo; the lo*lo
+// term is below 2^-21 of the product).
 #include <cfloat>
 
 #include "mf_kernels.h"
@@ -114,7 +118,44 @@ __device__ __forceinline__ v8h digits_f16(uint2 word, int shift, u32 mask4) {
     return __builtin_bit_cast(v8h, packed);
 }
 
-template <int KS, int NA, bool NONLINEAR>
+__global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
+                                u64 event, uint4 *volt) {
+    const int R = cfg.rows, A = cfg.n_in;
+    const i64 kp = m * R, units = kp / 8;
+    const i64 total = i64(A) * n * units;
+    const u64 read_seed = event_seed(seed, event);
+    for (i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += i64(gridDim.x) * blockDim.x) {
+        const i64 u = t % units, rest = t / units;
+        const i64 v = rest % n;
+        const int a = int(rest / n);
+        const i64 k0 = u * 8;
+        const uint2 bytes = *reinterpret_cast<const uint2 *>(q + v * kp + k0);
+        const u32 shift = u32(cfg.in_shift[a]), mask = u32(cfg.in_mask[a]);
+        u32 hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const u32 code = ((j < 4 ? bytes.x : bytes.y) >> (8 * (j & 3))) & 0xFFu;
+            const u32 digit = (code >> shift) & mask;
+            float x = 0.0f;   // a zero digit stays zero whatever its factor
+            if (digit) {
+                const i64 k = k0 + j, i = k / R, r = k - i * R;
+                const u64 address = u64(((v * m + i) * A + a) * R + r);
+                const float z = normal(address, read_seed, 40u, cfg.f_two_pi);
+                x = float(digit) * (1.0f + cfg.f_vnoise * z);
+            }
+            const _Float16 hi = static_cast<_Float16>(x);
+            const _Float16 lo = static_cast<_Float16>(x - static_cast<float>(hi));
+            const int half = 16 * (j & 1);
+            hw[j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << half;
+            lw[j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << half;
+        }
+        volt[(i64(a) * n + v) * units + u] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        volt[((i64(A) + a) * n + v) * units + u] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    }
+}
+
+template <int KS, int NA, bool NONLINEAR, bool VNOISE>
 __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const NoisyArgs args) {
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     constexpr int P = 16 * KS;
@@ -153,10 +194,21 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     uint2 qw[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
+        qw[ks] = make_uint2(0u, 0u);
+        if (VNOISE) continue;
         const u32 x = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + g0 * P + ks * 16, 0, 0);
         const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + g0 * P + ks * 16 + 4, 0, 0);
         qw[ks] = make_uint2(x, y);
     }
+    // Voltage-noise operands of this lane's vector: [term][a] rows of kp/8 uint4.
+    const i64 vunits = kp / 8;
+    const bool vlive = n_out < args.n;
+    auto volt_operand = [&](int term, int a, int g, int ks) -> v8h {
+        if (!vlive) return v8h{};
+        const i64 unit = (g * P + ks * 16 + lhalf * 8) / 8;
+        return __builtin_bit_cast(
+            v8h, args.volt[((i64(term) * A + a) * args.n + n_out) * vunits + unit]);
+    };
 
     // Conductance terms of (read g, weight slice w), double-buffered in registers:
     // the next slice's terms are in flight while the current slice's MFMAs run.
@@ -174,16 +226,19 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     if (KS != 2 && g0 < g1) load_terms(Fa, g0, 0);
 
     for (int g = g0; g < g1; ++g) {
-        // Input digits of this read for every slice (B operands).
-        v8h B[NA][KS];
+        // Input digits of this read for every slice (B operands).  With voltage
+        // variation the operands come from k_voltage_terms where they are used.
+        v8h B[VNOISE ? 1 : NA][KS];
+        if (!VNOISE) {
 #pragma unroll
-        for (int a = 0; a < NA; ++a) {
-            if (a >= A) break;
+            for (int a = 0; a < NA; ++a) {
+                if (a >= A) break;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                B[a][ks] = digits_f16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
+                for (int ks = 0; ks < KS; ++ks)
+                    B[VNOISE ? 0 : a][ks] = digits_f16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
+            }
         }
-        if (g + 1 < g1) {
+        if (!VNOISE && g + 1 < g1) {
             const int next = (g + 1) * P;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -222,11 +277,31 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
             for (int a = 0; a < NA; ++a) {
                 if (a >= A) break;
                 v16f I = {};
+                if (VNOISE) {
+                    v8h hi[KS], lo[KS];
 #pragma unroll
-                for (int term = 0; term < NOISY_TERMS; ++term)
+                    for (int ks = 0; ks < KS; ++ks) {
+                        hi[ks] = volt_operand(0, a, g, ks);
+                        lo[ks] = volt_operand(1, a, g, ks);
+                    }
+#pragma unroll
+                    for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                        for (int ks = 0; ks < KS; ++ks)
+                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], hi[ks], I, 0, 0,
+                                                                       0);
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks)
-                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], B[a][ks], I, 0, 0, 0);
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[0][ks], lo[ks], I, 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                        for (int ks = 0; ks < KS; ++ks)
+                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks],
+                                                                       B[VNOISE ? 0 : a][ks], I, 0,
+                                                                       0, 0);
+                }
                 convert(I, a);
             }
         };
@@ -378,8 +453,10 @@ __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, 
 }
 
 #define MF_NOISY_INST(KS, NA)                                                               \
-    template __global__ void k_noisy<KS, NA, true>(const NoisyPlan, const NoisyArgs);       \
-    template __global__ void k_noisy<KS, NA, false>(const NoisyPlan, const NoisyArgs);
+    template __global__ void k_noisy<KS, NA, true, false>(const NoisyPlan, const NoisyArgs);  \
+    template __global__ void k_noisy<KS, NA, false, false>(const NoisyPlan, const NoisyArgs); \
+    template __global__ void k_noisy<KS, NA, true, true>(const NoisyPlan, const NoisyArgs);   \
+    template __global__ void k_noisy<KS, NA, false, true>(const NoisyPlan, const NoisyArgs);
 MF_NOISY_INST(2, 5)
 MF_NOISY_INST(2, 8)
 MF_NOISY_INST(4, 5)

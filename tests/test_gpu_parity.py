@@ -474,6 +474,16 @@ MFMA_NOISY = {
                 dict(write_variation=0.03, adc_nonlinearity=0.05)),
     "rows64": (dict(array_size=(128, 32), rows_per_read=64, weight_quant_gran=(64, 1),
                     input_quant_gran=(1, 64)), dict(write_variation=0.02, read_variation=0.01)),
+    # Voltage variation: real input operands (hi + lo), 2-bit and binary digits, 32- and
+    # 64-row reads, with shared read noise and the S-curve ADC.
+    "voltage": (dict(), dict(write_variation=0.02, voltage_variation=0.05)),
+    "voltage_binary8": (dict(input_slice=None, weight_slice=(1, 1, 2, 2, 2),
+                             adc_bits=(4, 5, 5, 6, 6)),
+                        dict(write_variation=0.02, voltage_variation=0.03)),
+    "voltage_rows64": (dict(array_size=(128, 32), rows_per_read=64, weight_quant_gran=(64, 1),
+                            input_quant_gran=(1, 64)),
+                       dict(write_variation=0.02, read_variation=0.01, voltage_variation=0.02,
+                            adc_nonlinearity=0.1)),
 }
 NOISY_BASE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
                   weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,

@@ -60,8 +60,14 @@ def test_workspace_need_prices_each_schedule():
     assert tuning.workspace_need(ideal, n, m, p, {}) == (
         -(-(4 * 16 * 8) // 256) * 256 + -(-(32 * 16 * 8) // 256) * 256)
     general = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02,
-                                                          voltage_variation=0.01))
+                                                          read_variation=0.01,
+                                                          read_mode="output"))
     assert tuning.workspace_need(general, n, m, p, {}) == 4 * m * p * 5 * 128 * 128
+    # Voltage variation adds the noisy read's input operands: hi and lo fp16 per input
+    # slice, vector and physical row.
+    voltage = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02,
+                                                          voltage_variation=0.01))
+    assert tuning.workspace_need(voltage, n, m, p, dict(split=1)) == terms + 2 * 5 * n * m * 128 * 2
 
 
 def test_unknown_variant_bits_are_refused():
