@@ -281,11 +281,17 @@ bool fp16_terms_fit(const mf_config *cfg) {
 // conductances that do not depend on the input slice (no slice_pair read
 // noise), no voltage or output-mode read noise, reads of 32 or 64 rows that
 // tile the array, plain cascade columns, FP32-exact totals.
+// Planes of conductance terms of the noisy read: slice_pair read noise gives every
+// input slice its own read of each cell.
+int noisy_term_planes(const mf_config *cfg) {
+    return cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR ? cfg->n_in : 1;
+}
+
 bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *ks,
                       const char **why) {
     if (cfg->wide) { *why = "wide codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
-    if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
+    if (cfg->has_read && cfg->read_mode == MF_READ_OUTPUT) { *why = "output-mode read noise"; return false; }
     if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
         return false;
@@ -303,6 +309,7 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
     memset(plan, 0, sizeof(*plan));
     plan->n_in = cfg->n_in;
     plan->n_w = cfg->n_w;
+    plan->planes = noisy_term_planes(cfg);
     for (int w = 0; w < cfg->n_w; ++w) {
         plan->k1[w] = float(cfg->d_voltage * double(cfg->w_mask[w]) * cfg->d_inv_unit);
         plan->top[w] = float(cfg->adc_max[w]);
@@ -327,9 +334,10 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
     return true;
 }
 
-// Bytes of conductance terms per 32-column block: NOISY_TERMS fp16 terms per cell and slice.
+// Bytes of conductance terms per 32-column block: NOISY_TERMS fp16 terms per cell,
+// weight slice and term plane.
 i64 noisy_block_bytes(const mf_config *cfg, i64 m) {
-    return i64(cfg->n_w) * 32 * m * cfg->rows * NOISY_TERMS * 2;
+    return i64(cfg->n_w) * noisy_term_planes(cfg) * 32 * m * cfg->rows * NOISY_TERMS * 2;
 }
 
 bool noisy_extent_ok(i64 n, i64 m, const mf_config *cfg) {
@@ -476,24 +484,30 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         }
         const dim3 grid{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
         const bool nl = cfg->has_nonlinear != 0;
+        const bool slice = plan.planes > 1;
         // Benchmark timing brackets the read kernel alone (not the conductance split).
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
         if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-#define MF_NOISY_LAUNCH(KS, NA)                                                                 \
-    {                                                                                           \
-        if (volt && nl)                                                                         \
-            hipLaunchKernelGGL((k_noisy<KS, NA, true, true>), grid, dim3(256), 0, s, plan, args);  \
-        else if (volt)                                                                          \
-            hipLaunchKernelGGL((k_noisy<KS, NA, false, true>), grid, dim3(256), 0, s, plan, args); \
-        else if (nl)                                                                            \
-            hipLaunchKernelGGL((k_noisy<KS, NA, true, false>), grid, dim3(256), 0, s, plan, args); \
-        else                                                                                    \
-            hipLaunchKernelGGL((k_noisy<KS, NA, false, false>), grid, dim3(256), 0, s, plan, args); \
+#define MF_NOISY_LAUNCH1(KS, NA, NL, VN, SL) \
+    hipLaunchKernelGGL((k_noisy<KS, NA, NL, VN, SL>), grid, dim3(256), 0, s, plan, args)
+#define MF_NOISY_LAUNCH2(KS, NA, VN, SL)                    \
+    {                                                      \
+        if (nl) MF_NOISY_LAUNCH1(KS, NA, true, VN, SL);    \
+        else MF_NOISY_LAUNCH1(KS, NA, false, VN, SL);      \
+    }
+#define MF_NOISY_LAUNCH(KS, NA)                                         \
+    {                                                                  \
+        if (volt && slice) MF_NOISY_LAUNCH2(KS, NA, true, true)        \
+        else if (volt) MF_NOISY_LAUNCH2(KS, NA, true, false)           \
+        else if (slice) MF_NOISY_LAUNCH2(KS, NA, false, true)          \
+        else MF_NOISY_LAUNCH2(KS, NA, false, false)                    \
     }
         if (ks == 4) MF_NOISY_LAUNCH(4, 5)
         else if (cfg->n_in <= 5) MF_NOISY_LAUNCH(2, 5)
         else MF_NOISY_LAUNCH(2, 8)
 #undef MF_NOISY_LAUNCH
+#undef MF_NOISY_LAUNCH2
+#undef MF_NOISY_LAUNCH1
         if (timing.first) {
             hipEventRecord(timing.second, s);
             g_profile.pending.push_back(timing);
@@ -524,6 +538,7 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
                            bool *small, const char **why) {
     if (!cfg->wide) { *why = "narrow codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
+    if (cfg->has_vnoise) { *why = "voltage variation"; return false; }
     if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
     if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
@@ -1834,22 +1849,20 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     if (kernel_id == 1) {
         fn = reinterpret_cast<const void *>(&k_ideal<1, 1>);
     } else if (kernel_id == 2) {
-        // [ks][vnoise][nonlinear]; ks index 0: KS 2 with up to 5 slices, 1: KS 2 with 8, 2: KS 4.
-        const void *table[3][2][2] = {
-            {{reinterpret_cast<const void *>(&k_noisy<2, 5, false, false>),
-              reinterpret_cast<const void *>(&k_noisy<2, 5, true, false>)},
-             {reinterpret_cast<const void *>(&k_noisy<2, 5, false, true>),
-              reinterpret_cast<const void *>(&k_noisy<2, 5, true, true>)}},
-            {{reinterpret_cast<const void *>(&k_noisy<2, 8, false, false>),
-              reinterpret_cast<const void *>(&k_noisy<2, 8, true, false>)},
-             {reinterpret_cast<const void *>(&k_noisy<2, 8, false, true>),
-              reinterpret_cast<const void *>(&k_noisy<2, 8, true, true>)}},
-            {{reinterpret_cast<const void *>(&k_noisy<4, 5, false, false>),
-              reinterpret_cast<const void *>(&k_noisy<4, 5, true, false>)},
-             {reinterpret_cast<const void *>(&k_noisy<4, 5, false, true>),
-              reinterpret_cast<const void *>(&k_noisy<4, 5, true, true>)}}};
+        // [ks][vnoise][slice][nonlinear]; ks index 0: KS 2 with up to 5 slices, 1: KS 2
+        // with 8, 2: KS 4.
+#define MF_NOISY_FN(KS, NA, NL, VN, SL) reinterpret_cast<const void *>(&k_noisy<KS, NA, NL, VN, SL>)
+#define MF_NOISY_ROW(KS, NA)                                                                  \
+    {{{MF_NOISY_FN(KS, NA, false, false, false), MF_NOISY_FN(KS, NA, true, false, false)},   \
+      {MF_NOISY_FN(KS, NA, false, false, true), MF_NOISY_FN(KS, NA, true, false, true)}},    \
+     {{MF_NOISY_FN(KS, NA, false, true, false), MF_NOISY_FN(KS, NA, true, true, false)},     \
+      {MF_NOISY_FN(KS, NA, false, true, true), MF_NOISY_FN(KS, NA, true, true, true)}}}
+        const void *table[3][2][2][2] = {MF_NOISY_ROW(2, 5), MF_NOISY_ROW(2, 8),
+                                         MF_NOISY_ROW(4, 5)};
+#undef MF_NOISY_ROW
+#undef MF_NOISY_FN
         const int which = ks4 ? 2 : (cfg->n_in <= 5 ? 0 : 1);
-        fn = table[which][cfg->has_vnoise ? 1 : 0][nl ? 1 : 0];
+        fn = table[which][cfg->has_vnoise ? 1 : 0][noisy_term_planes(cfg) > 1 ? 1 : 0][nl ? 1 : 0];
     } else if (kernel_id == 3) {
         fn = ks4 ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<4, true, false, WIDE_FRAGS_LARGE>)
                        : reinterpret_cast<const void *>(&k_noisy_wide<4, false, false, WIDE_FRAGS_LARGE>))

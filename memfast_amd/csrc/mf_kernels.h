@@ -115,6 +115,7 @@ constexpr int NOISY_TERMS = 2;   // fp16 terms per conductance (hi, lo)
 // T += fa[a] * fw[w] * code.
 struct NoisyPlan {
     int n_in, n_w;
+    int planes;        // planes of conductance terms: n_in with slice_pair read noise, else 1
     float k1[8], top[8], alpha[8], fa[8], fw[8];
     int in_shift[8];
     u32 in_mask4[8];   // input slice mask replicated into four bytes
@@ -142,7 +143,7 @@ template <int KS>
 __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, const float *g_in,
                                      i64 m, i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin,
                                      i64 CB, const NoisyPlan plan, uint4 *gs);
-template <int KS, int NA, bool NONLINEAR, bool VNOISE>
+template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
 // Input operands of a read with voltage variation (memfast/reference.py:77-82): per
 // input slice a, vector v and physical row k, digit * (1 + vv * z(address)) split into

@@ -28,7 +28,9 @@
 // With voltage variation (VNOISE) every input digit carries its own factor
 // (1 + vv*z), so the B operand is real too: k_voltage_terms splits digit*(1 + vv*z)
 // into fp16 hi + lo, and a pair takes 3*KS MFMAs (hi*hi + lo*hi + hi*lo; the lo*lo
-// term is below 2^-21 of the product).
+// term is below 2^-21 of the product).  With slice_pair read noise (SLICE) each
+// (weight slice, input slice) pair reads its own conductances: k_split_conductances
+// writes one plane of terms per input slice and a pair loads its plane.
 #include <cfloat>
 
 #include "mf_kernels.h"
@@ -61,7 +63,8 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
         const int lr = lane & 31, h = lane >> 5;
         const i64 c = c_begin + cb * 32 + lr;
         const i64 k0 = g * P + ks * 16 + h * 8;
-        u32 terms[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        float level[8] = {};
+        u64 cells[8] = {};
         if (c < ncols) {
             const uint2 bytes = *reinterpret_cast<const uint2 *>(packed_t + c * kp + k0);
             const i64 i = k0 / R, r0 = k0 - i * R;
@@ -69,22 +72,39 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const u8 code = u8(((j < 4 ? bytes.x : bytes.y) >> (8 * (j & 3))) & 0xFFu);
-                const u64 cell = u64((((i * p + tt) * W + w) * R + r0 + j) * C + cc);
-                const float level = g_in ? g_in[cell]
-                                         : cell_conductance<float>(cfg, code, w, cell, seed, read_seed);
-                const float delta = (level - cfg.f_low) * plan.k1[w];   // ADC counts per digit
-                const _Float16 hi = static_cast<_Float16>(delta);        // round to nearest even
-                const _Float16 lo = static_cast<_Float16>(delta - static_cast<float>(hi));
-                const int shift = 16 * (j & 1);
-                terms[0][j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << shift;
-                terms[1][j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << shift;
+                cells[j] = u64((((i * p + tt) * W + w) * R + r0 + j) * C + cc);
+                level[j] = g_in ? g_in[cells[j]]
+                                : cell_conductance<float>(cfg, code, w, cells[j], seed, read_seed);
             }
         }
-        uint4 *dst = gs + (((w * CB + cb) * G + g) * NOISY_TERMS * KS + ks) * 64 + lane;
+        // slice_pair read noise (memfast/reference.py:86-90): an independent read factor
+        // per (cell, input slice), one plane of terms per input slice.
+        for (int plane = 0; plane < plan.planes; ++plane) {
+            u32 terms[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+            if (c < ncols) {
 #pragma unroll
-        for (int term = 0; term < NOISY_TERMS; ++term)
-            dst[term * KS * 64] = make_uint4(terms[term][0], terms[term][1], terms[term][2],
-                                             terms[term][3]);
+                for (int j = 0; j < 8; ++j) {
+                    float g_read = level[j];
+                    if (plan.planes > 1) {
+                        const u64 address = cells[j] * u64(cfg.n_in) + u64(plane);
+                        g_read = g_read * expf(cfg.f_read * normal(address, read_seed, 20u,
+                                                                    cfg.f_two_pi));
+                    }
+                    const float delta = (g_read - cfg.f_low) * plan.k1[w];   // ADC counts per digit
+                    const _Float16 hi = static_cast<_Float16>(delta);         // round to nearest even
+                    const _Float16 lo = static_cast<_Float16>(delta - static_cast<float>(hi));
+                    const int shift = 16 * (j & 1);
+                    terms[0][j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << shift;
+                    terms[1][j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << shift;
+                }
+            }
+            const i64 vw = i64(w) * plan.planes + plane;   // plane of (weight, input) slices
+            uint4 *dst = gs + (((vw * CB + cb) * G + g) * NOISY_TERMS * KS + ks) * 64 + lane;
+#pragma unroll
+            for (int term = 0; term < NOISY_TERMS; ++term)
+                dst[term * KS * 64] = make_uint4(terms[term][0], terms[term][1], terms[term][2],
+                                                 terms[term][3]);
+        }
     }
 }
 
@@ -155,7 +175,7 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
     }
 }
 
-template <int KS, int NA, bool NONLINEAR, bool VNOISE>
+template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE>
 __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const NoisyArgs args) {
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     constexpr int P = 16 * KS;
@@ -212,6 +232,8 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
 
     // Conductance terms of (read g, weight slice w), double-buffered in registers:
     // the next slice's terms are in flight while the current slice's MFMAs run.
+    // `w` indexes planes of terms: the weight slice, or with SLICE (weight slice, input
+    // slice) as w * A + a.
     auto load_terms = [&](v8h (&F)[NOISY_TERMS][KS], int g, int w) {
         const uint4 *frag = frag_base + i64(g) * NOISY_TERMS * KS * 64 + w * w_stride;
 #pragma unroll
@@ -223,7 +245,7 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     // (With KS == 2 a second buffer would cost the third wave per SIMD: 32-row reads
     // load each slice's terms where they are used.)
     v8h Fa[NOISY_TERMS][KS], Fb[NOISY_TERMS][KS];
-    if (KS != 2 && g0 < g1) load_terms(Fa, g0, 0);
+    if (KS != 2 && !SLICE && g0 < g1) load_terms(Fa, g0, 0);
 
     for (int g = g0; g < g1; ++g) {
         // Input digits of this read for every slice (B operands).  With voltage
@@ -252,7 +274,8 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
         u32 Ti[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) Ti[r] = 0u;
-        auto slice_reads = [&](const v8h (&F)[NOISY_TERMS][KS], int w) {
+        // The reads of weight slice w with input slices [a_lo, a_hi) from terms F.
+        auto slice_reads = [&](const v8h (&F)[NOISY_TERMS][KS], int w, int a_lo, int a_hi) {
             const float top = MAGIC + plan.top[w], alpha = plan.alpha[w];
             const float fw = plan.fw[w];
             auto convert = [&](const v16f &I, int a) {
@@ -276,6 +299,7 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
 #pragma unroll
             for (int a = 0; a < NA; ++a) {
                 if (a >= A) break;
+                if (a < a_lo || a >= a_hi) continue;
                 v16f I = {};
                 if (VNOISE) {
                     v8h hi[KS], lo[KS];
@@ -305,24 +329,30 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
                 convert(I, a);
             }
         };
-        if (KS == 2) {
+        if (SLICE) {
+            for (int w = 0; w < W; ++w)
+                for (int a = 0; a < A; ++a) {
+                    load_terms(Fa, g, w * A + a);
+                    slice_reads(Fa, w, a, a + 1);
+                }
+        } else if (KS == 2) {
             for (int w = 0; w < W; ++w) {
                 load_terms(Fa, g, w);
-                slice_reads(Fa, w);
+                slice_reads(Fa, w, 0, A);
             }
         } else {
             // Fa holds (g, 0) on entry; on exit it holds (g + 1, 0) when that read exists.
             int w = 0;
             for (; w + 1 < W; w += 2) {
                 load_terms(Fb, g, w + 1);
-                slice_reads(Fa, w);
+                slice_reads(Fa, w, 0, A);
                 if (w + 2 < W) load_terms(Fa, g, w + 2);
                 else if (g + 1 < g1) load_terms(Fa, g + 1, 0);
-                slice_reads(Fb, w + 1);
+                slice_reads(Fb, w + 1, 0, A);
             }
             if (w < W) {
                 if (g + 1 < g1) load_terms(Fb, g + 1, 0);
-                slice_reads(Fa, w);
+                slice_reads(Fa, w, 0, A);
 #pragma unroll
                 for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
@@ -452,14 +482,17 @@ __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, 
     if (!finite && status) atomicOr(status, u32(MF_STATUS_OUTPUT));
 }
 
-#define MF_NOISY_INST(KS, NA)                                                               \
-    template __global__ void k_noisy<KS, NA, true, false>(const NoisyPlan, const NoisyArgs);  \
-    template __global__ void k_noisy<KS, NA, false, false>(const NoisyPlan, const NoisyArgs); \
-    template __global__ void k_noisy<KS, NA, true, true>(const NoisyPlan, const NoisyArgs);   \
-    template __global__ void k_noisy<KS, NA, false, true>(const NoisyPlan, const NoisyArgs);
+#define MF_NOISY_INST1(KS, NA, NL, VN, SL) \
+    template __global__ void k_noisy<KS, NA, NL, VN, SL>(const NoisyPlan, const NoisyArgs);
+#define MF_NOISY_INST(KS, NA)                                                      \
+    MF_NOISY_INST1(KS, NA, false, false, false) MF_NOISY_INST1(KS, NA, true, false, false) \
+    MF_NOISY_INST1(KS, NA, false, true, false) MF_NOISY_INST1(KS, NA, true, true, false)   \
+    MF_NOISY_INST1(KS, NA, false, false, true) MF_NOISY_INST1(KS, NA, true, false, true)   \
+    MF_NOISY_INST1(KS, NA, false, true, true) MF_NOISY_INST1(KS, NA, true, true, true)
 MF_NOISY_INST(2, 5)
 MF_NOISY_INST(2, 8)
 MF_NOISY_INST(4, 5)
 #undef MF_NOISY_INST
+#undef MF_NOISY_INST1
 
 }  // namespace mf

@@ -484,6 +484,18 @@ MFMA_NOISY = {
                             input_quant_gran=(1, 64)),
                        dict(write_variation=0.02, read_variation=0.01, voltage_variation=0.02,
                             adc_nonlinearity=0.1)),
+    # slice_pair read noise: one plane of conductance terms per input slice; with binary
+    # digits (8 planes), and at 64-row reads with voltage noise and the S-curve.
+    "slice_pair": (dict(), dict(write_variation=0.02, read_variation=0.02,
+                                read_mode="slice_pair")),
+    "slice_pair_binary8": (dict(input_slice=None, weight_slice=(1, 1, 2, 2, 2),
+                                adc_bits=(4, 5, 5, 6, 6)),
+                           dict(write_variation=0.02, read_variation=0.02,
+                                read_mode="slice_pair")),
+    "slice_pair_rows64": (dict(array_size=(128, 32), rows_per_read=64,
+                               weight_quant_gran=(64, 1), input_quant_gran=(1, 64)),
+                          dict(write_variation=0.02, read_variation=0.01, read_mode="slice_pair",
+                               voltage_variation=0.02, adc_nonlinearity=0.1)),
 }
 NOISY_BASE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
                   weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,

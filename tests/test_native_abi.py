@@ -123,3 +123,30 @@ def test_noisy_mfma_kernels_require_fp16_range():
                        weight_slice=(1, 1, 2), bw_e=8,
                        nonidealities=Nonidealities(read_variation=2.5))
     assert hip.mm_kernel(wide_wild, 64, 4, 4) == 0
+
+
+def test_read_kernel_selection_by_noise_model():
+    """Which read kernel each noise model takes (mf_mm_kernel, host only): the narrow noisy
+    MFMA read covers voltage variation and slice_pair read noise; output-mode read noise
+    stays on the general kernel; the wide MFMA read covers neither voltage
+    variation nor per-slice read noise (it models them not at all, so they must never
+    reach it)."""
+    from memfast_amd import Config, Nonidealities
+    narrow = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                  weight_slice=(1, 1, 2, 2, 2), array_size=(128, 128), rows_per_read=32)
+    wide = dict(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                weight_slice=(1, 1, 2), bw_e=8, array_size=(128, 128), rows_per_read=32)
+    cases = [
+        (narrow, dict(write_variation=0.02), 2),
+        (narrow, dict(write_variation=0.02, voltage_variation=0.01), 2),
+        (narrow, dict(read_variation=0.01, read_mode="slice_pair"), 2),
+        (narrow, dict(read_variation=0.01, read_mode="output"), 0),
+        (narrow, dict(read_variation=0.01, read_mode="slice_pair", voltage_variation=0.01), 2),
+        (wide, dict(read_variation=0.01), 3),
+        (wide, dict(write_variation=0.02, voltage_variation=0.01), 0),
+        (wide, dict(read_variation=0.01, read_mode="slice_pair"), 0),
+        (wide, dict(read_variation=0.01, read_mode="output"), 0),
+    ]
+    for kwargs, effects, kernel in cases:
+        cfg = Config(**kwargs, nonidealities=Nonidealities(**effects))
+        assert hip.mm_kernel(cfg, 64, 4, 4) == kernel, (kwargs["activation_bits"], effects)

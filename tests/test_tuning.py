@@ -25,8 +25,12 @@ def test_grid_follows_the_selected_kernel():
     assert [s["split"] for s in tuning.schedule_grid(noisy, 64, 8, arrays=1)] == [0, 1, 2, 4]
     wide = Config(**CONFIG5, nonidealities=Nonidealities(read_variation=0.01))
     assert [s["tier"] for s in tuning.schedule_grid(wide, 256, 4, arrays=8)] == [0, 1, 2, 3]
+    slice_pair = Config(**INT8, nonidealities=Nonidealities(read_variation=0.01,
+                                                             read_mode="slice_pair"))
+    assert [s["split"] for s in tuning.schedule_grid(slice_pair, 64, 8, arrays=4)] == [
+        0, 1, 2, 4, 8]
     general = Config(**INT8, nonidealities=Nonidealities(read_variation=0.01,
-                                                          read_mode="slice_pair"))
+                                                          read_mode="output"))
     assert tuning.schedule_grid(general, 64, 8, arrays=4) == [tuning.default_schedule(general)]
     # Without the array count (the reference's signature) only the default is declared.
     assert tuning.schedule_grid(noisy, 64, 8) == [tuning.default_schedule(noisy)]
