@@ -169,9 +169,10 @@ def _ideal_input_cases(out, device):
 
 
 def _read_modes(out, device):
-    """Config 2's array shape at 4096^3 with the other noise forms: per-slice-pair and
-    output-mode read noise (the general FP32 kernel) and voltage noise (the noisy MFMA read
-    with real input operands)."""
+    """Config 2's array shape at 4096^3 with the other noise forms, all on the noisy MFMA
+    read: per-slice-pair read noise (a plane of terms per input slice), output-mode read
+    noise (mean and variance sums, a normal per conversion) and voltage noise (real input
+    operands)."""
     import torch
 
     import memfast_amd as memfast

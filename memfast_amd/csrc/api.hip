@@ -284,14 +284,24 @@ bool fp16_terms_fit(const mf_config *cfg) {
 // Planes of conductance terms of the noisy read: slice_pair read noise gives every
 // input slice its own read of each cell.
 int noisy_term_planes(const mf_config *cfg) {
-    return cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR ? cfg->n_in : 1;
+    if (cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR) return cfg->n_in;
+    if (cfg->has_read && cfg->read_mode == MF_READ_OUTPUT) return 2;
+    return 1;
 }
 
 bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *ks,
                       const char **why) {
     if (cfg->wide) { *why = "wide codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
-    if (cfg->has_read && cfg->read_mode == MF_READ_OUTPUT) { *why = "output-mode read noise"; return false; }
+    const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
+    if (output_noise) {
+        // Squared digits must be exact in fp16, the noise addresses of a wave's 32 columns
+        // must share one array tile, and voltage-noise operands are not squared here.
+        if (cfg->has_vnoise) { *why = "output-mode read noise with voltage variation"; return false; }
+        if (cfg->cols % 32) { *why = "output-mode read noise needs array columns in multiples of 32"; return false; }
+        for (int a = 0; a < cfg->n_in; ++a)
+            if (cfg->in_mask[a] > 15) { *why = "output-mode read noise with input digits above 15"; return false; }
+    }
     if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
         return false;
@@ -310,11 +320,18 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
     plan->n_in = cfg->n_in;
     plan->n_w = cfg->n_w;
     plan->planes = noisy_term_planes(cfg);
+    plan->out_noise = output_noise ? 1 : 0;
+    plan->out_mean = cfg->f_out_mean;
+    plan->two_pi = cfg->f_two_pi;
     for (int w = 0; w < cfg->n_w; ++w) {
         plan->k1[w] = float(cfg->d_voltage * double(cfg->w_mask[w]) * cfg->d_inv_unit);
         plan->top[w] = float(cfg->adc_max[w]);
         plan->alpha[w] = cfg->has_nonlinear ? cfg->f_alpha_over_max[w] : 0.0f;
         plan->fw[w] = float(cfg->w_factor[w]);
+        plan->kl[w] = plan->k1[w] * cfg->f_low;
+        plan->qk[w] = float(cfg->d_voltage * cfg->d_inv_unit);
+        const float mw = float(cfg->w_mask[w]);
+        plan->out_var[w] = mw * mw * cfg->f_out_var;
     }
     i64 factor_sum = 0;
     for (int a = 0; a < cfg->n_in; ++a) {
@@ -474,6 +491,8 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         args.g_end = g_run;
         args.g_step = g_run;
         args.volt = volt;
+        args.read_seed = event_seed(seed, event);
+        args.C = cfg->cols;
         unsigned gz = 1;
         if (use_split) {
             args.totals = 1;
@@ -484,23 +503,24 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         }
         const dim3 grid{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
         const bool nl = cfg->has_nonlinear != 0;
-        const bool slice = plan.planes > 1;
+        const bool slice = plan.planes > 1 && !plan.out_noise;
         // Benchmark timing brackets the read kernel alone (not the conductance split).
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
         if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-#define MF_NOISY_LAUNCH1(KS, NA, NL, VN, SL) \
-    hipLaunchKernelGGL((k_noisy<KS, NA, NL, VN, SL>), grid, dim3(256), 0, s, plan, args)
-#define MF_NOISY_LAUNCH2(KS, NA, VN, SL)                    \
-    {                                                      \
-        if (nl) MF_NOISY_LAUNCH1(KS, NA, true, VN, SL);    \
-        else MF_NOISY_LAUNCH1(KS, NA, false, VN, SL);      \
+#define MF_NOISY_LAUNCH1(KS, NA, NL, VN, SL, ON) \
+    hipLaunchKernelGGL((k_noisy<KS, NA, NL, VN, SL, ON>), grid, dim3(256), 0, s, plan, args)
+#define MF_NOISY_LAUNCH2(KS, NA, VN, SL, ON)                    \
+    {                                                          \
+        if (nl) MF_NOISY_LAUNCH1(KS, NA, true, VN, SL, ON);    \
+        else MF_NOISY_LAUNCH1(KS, NA, false, VN, SL, ON);      \
     }
-#define MF_NOISY_LAUNCH(KS, NA)                                         \
-    {                                                                  \
-        if (volt && slice) MF_NOISY_LAUNCH2(KS, NA, true, true)        \
-        else if (volt) MF_NOISY_LAUNCH2(KS, NA, true, false)           \
-        else if (slice) MF_NOISY_LAUNCH2(KS, NA, false, true)          \
-        else MF_NOISY_LAUNCH2(KS, NA, false, false)                    \
+#define MF_NOISY_LAUNCH(KS, NA)                                                \
+    {                                                                         \
+        if (plan.out_noise) MF_NOISY_LAUNCH2(KS, NA, false, false, true)      \
+        else if (volt && slice) MF_NOISY_LAUNCH2(KS, NA, true, true, false)   \
+        else if (volt) MF_NOISY_LAUNCH2(KS, NA, true, false, false)           \
+        else if (slice) MF_NOISY_LAUNCH2(KS, NA, false, true, false)          \
+        else MF_NOISY_LAUNCH2(KS, NA, false, false, false)                    \
     }
         if (ks == 4) MF_NOISY_LAUNCH(4, 5)
         else if (cfg->n_in <= 5) MF_NOISY_LAUNCH(2, 5)
@@ -1849,20 +1869,26 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
     if (kernel_id == 1) {
         fn = reinterpret_cast<const void *>(&k_ideal<1, 1>);
     } else if (kernel_id == 2) {
-        // [ks][vnoise][slice][nonlinear]; ks index 0: KS 2 with up to 5 slices, 1: KS 2
-        // with 8, 2: KS 4.
-#define MF_NOISY_FN(KS, NA, NL, VN, SL) reinterpret_cast<const void *>(&k_noisy<KS, NA, NL, VN, SL>)
-#define MF_NOISY_ROW(KS, NA)                                                                  \
-    {{{MF_NOISY_FN(KS, NA, false, false, false), MF_NOISY_FN(KS, NA, true, false, false)},   \
-      {MF_NOISY_FN(KS, NA, false, false, true), MF_NOISY_FN(KS, NA, true, false, true)}},    \
-     {{MF_NOISY_FN(KS, NA, false, true, false), MF_NOISY_FN(KS, NA, true, true, false)},     \
-      {MF_NOISY_FN(KS, NA, false, true, true), MF_NOISY_FN(KS, NA, true, true, true)}}}
-        const void *table[3][2][2][2] = {MF_NOISY_ROW(2, 5), MF_NOISY_ROW(2, 8),
+        // ks index 0: KS 2 with up to 5 slices, 1: KS 2 with 8, 2: KS 4.
+#define MF_NOISY_FN(KS, NA, NL, VN, SL, ON) \
+    reinterpret_cast<const void *>(&k_noisy<KS, NA, NL, VN, SL, ON>)
+#define MF_NOISY_ROW(KS, NA)                                                                      \
+    {{{MF_NOISY_FN(KS, NA, false, false, false, false), MF_NOISY_FN(KS, NA, true, false, false, false)}, \
+      {MF_NOISY_FN(KS, NA, false, false, true, false), MF_NOISY_FN(KS, NA, true, false, true, false)}},  \
+     {{MF_NOISY_FN(KS, NA, false, true, false, false), MF_NOISY_FN(KS, NA, true, true, false, false)},   \
+      {MF_NOISY_FN(KS, NA, false, true, true, false), MF_NOISY_FN(KS, NA, true, true, true, false)}},    \
+     {{MF_NOISY_FN(KS, NA, false, false, false, true), MF_NOISY_FN(KS, NA, true, false, false, true)},   \
+      {MF_NOISY_FN(KS, NA, false, false, false, true), MF_NOISY_FN(KS, NA, true, false, false, true)}}}
+        // [ks][plain, voltage or output noise][slice_pair][nonlinear]
+        const void *table[3][3][2][2] = {MF_NOISY_ROW(2, 5), MF_NOISY_ROW(2, 8),
                                          MF_NOISY_ROW(4, 5)};
 #undef MF_NOISY_ROW
 #undef MF_NOISY_FN
         const int which = ks4 ? 2 : (cfg->n_in <= 5 ? 0 : 1);
-        fn = table[which][cfg->has_vnoise ? 1 : 0][noisy_term_planes(cfg) > 1 ? 1 : 0][nl ? 1 : 0];
+        const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
+        const int mode = output_noise ? 2 : (cfg->has_vnoise ? 1 : 0);
+        const bool slice = cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR;
+        fn = table[which][mode][slice ? 1 : 0][nl ? 1 : 0];
     } else if (kernel_id == 3) {
         fn = ks4 ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<4, true, false, WIDE_FRAGS_LARGE>)
                        : reinterpret_cast<const void *>(&k_noisy_wide<4, false, false, WIDE_FRAGS_LARGE>))

@@ -115,7 +115,13 @@ constexpr int NOISY_TERMS = 2;   // fp16 terms per conductance (hi, lo)
 // T += fa[a] * fw[w] * code.
 struct NoisyPlan {
     int n_in, n_w;
-    int planes;        // planes of conductance terms: n_in with slice_pair read noise, else 1
+    int planes;        // planes of terms per weight slice: n_in (slice_pair), 2 (output), else 1
+    int out_noise;     // output-mode read noise: plane 1 holds (k1*g/Mw)^2
+    float kl[8];       // k1 * L: the current of a digit at the low conductance (output mode)
+    float qk[8];       // k1 / Mw (output mode)
+    float out_var[8];  // Mw^2 * fp32(exp(s^2) * expm1(s^2)) (output mode)
+    float out_mean;    // fp32(expm1(s^2 / 2)) (output mode)
+    float two_pi;
     float k1[8], top[8], alpha[8], fa[8], fw[8];
     int in_shift[8];
     u32 in_mask4[8];   // input slice mask replicated into four bytes
@@ -136,6 +142,8 @@ struct NoisyArgs {
     // Voltage variation: input operands [2][A][n][kp] fp16 (hi, lo) of digit * (1 + vv*z)
     // from k_voltage_terms, read instead of the digits of q.
     const uint4 *volt;
+    u64 read_seed;        // output-mode read noise: event_seed(seed, event)
+    i64 C;                // array columns (output-mode noise addresses)
 };
 
 // Terms are k1[w] * (g - L), so the read's MFMA output is in ADC counts.
@@ -143,7 +151,7 @@ template <int KS>
 __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, const float *g_in,
                                      i64 m, i64 p, i64 ncols, u32 seed, u64 event, i64 c_begin,
                                      i64 CB, const NoisyPlan plan, uint4 *gs);
-template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE>
+template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
 // Input operands of a read with voltage variation (memfast/reference.py:77-82): per
 // input slice a, vector v and physical row k, digit * (1 + vv * z(address)) split into

@@ -79,13 +79,25 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
         }
         // slice_pair read noise (memfast/reference.py:86-90): an independent read factor
         // per (cell, input slice), one plane of terms per input slice.
+        // Output-mode read noise: plane 1 holds (k1 * g / Mw)^2 for the variance
+        // sum_r d^2 * (k1 * g)^2 (memfast/reference.py:104-108).
         for (int plane = 0; plane < plan.planes; ++plane) {
             u32 terms[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
             if (c < ncols) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     float g_read = level[j];
-                    if (plan.planes > 1) {
+                    if (plan.out_noise && plane == 1) {
+                        const float y = g_read * plan.qk[w];
+                        const float q = y * y;
+                        const _Float16 hi = static_cast<_Float16>(q);
+                        const _Float16 lo = static_cast<_Float16>(q - static_cast<float>(hi));
+                        const int shift = 16 * (j & 1);
+                        terms[0][j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << shift;
+                        terms[1][j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << shift;
+                        continue;
+                    }
+                    if (plan.planes > 1 && !plan.out_noise) {
                         const u64 address = cells[j] * u64(cfg.n_in) + u64(plane);
                         g_read = g_read * expf(cfg.f_read * normal(address, read_seed, 20u,
                                                                     cfg.f_two_pi));
@@ -175,8 +187,19 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
     }
 }
 
-template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE>
-__global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const NoisyArgs args) {
+// normal() for a kernel short of registers: the cosine's argument 2*pi*u (u a uniform in
+// (0, 1)) is told to lie in [0, 6.3], which lets the compiler drop the large-argument
+// reduction of cosf; the value is the same.
+__device__ __forceinline__ float normal_in_range(u64 address, u64 seed, u32 stream, float two_pi) {
+    const float u = uniform(address, seed, stream);
+    const float v = uniform(address, seed, stream + 1u);
+    const float angle = two_pi * v;
+    __builtin_assume(angle >= 0.0f && angle <= 6.3f);
+    return sqrtf(-2.0f * logf(u)) * cosf(angle);
+}
+
+template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
+__device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArgs &args) {
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     constexpr int P = 16 * KS;
     constexpr int BC = 64, BV = 64;
@@ -245,19 +268,27 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     // (With KS == 2 a second buffer would cost the third wave per SIMD: 32-row reads
     // load each slice's terms where they are used.)
     v8h Fa[NOISY_TERMS][KS], Fb[NOISY_TERMS][KS];
-    if (KS != 2 && !SLICE && g0 < g1) load_terms(Fa, g0, 0);
+    if (KS != 2 && !SLICE && !OUTN && g0 < g1) load_terms(Fa, g0, 0);
 
     for (int g = g0; g < g1; ++g) {
         // Input digits of this read for every slice (B operands).  With voltage
         // variation the operands come from k_voltage_terms where they are used.
-        v8h B[VNOISE ? 1 : NA][KS];
-        if (!VNOISE) {
+        v8h B[(VNOISE || OUTN) ? 1 : NA][KS];
+        // Output-mode noise builds each slice's digits where they are used, from the codes
+        // of this read (kept past the next read's prefetch).
+        uint2 qcur[OUTN ? KS : 1];
+        if (OUTN) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) qcur[OUTN ? ks : 0] = qw[ks];
+        }
+        if (!VNOISE && !OUTN) {
 #pragma unroll
             for (int a = 0; a < NA; ++a) {
                 if (a >= A) break;
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
-                    B[VNOISE ? 0 : a][ks] = digits_f16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
+                    B[(VNOISE || OUTN) ? 0 : a][ks] =
+                        digits_f16(qw[ks], plan.in_shift[a], plan.in_mask4[a]);
             }
         }
         if (!VNOISE && g + 1 < g1) {
@@ -322,14 +353,90 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
                     for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
                         for (int ks = 0; ks < KS; ++ks)
-                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks],
-                                                                       B[VNOISE ? 0 : a][ks], I, 0,
-                                                                       0, 0);
+                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                F[term][ks], B[(VNOISE || OUTN) ? 0 : a][ks], I, 0, 0, 0);
                 }
                 convert(I, a);
             }
         };
-        if (SLICE) {
+        // Output-mode read noise (memfast/reference.py:99-112), in ADC counts: the current
+        // z = I (terms k1*(g - L)); the mean's sum k1*sum d*g = I + k1*L*sum d; the
+        // variance's sum Mw^2 * Q with Q = sum d^2 * (k1*g/Mw)^2 (plane 1, digits squared
+        // exactly in fp16); then z += mean + sqrt(variance) * normal(address) with the
+        // reference's per-(vector, read, tile, a, w, column) address, and the ADC.
+        auto output_reads = [&](const v8h (&Fg)[NOISY_TERMS][KS], const v8h (&Fq)[NOISY_TERMS][KS],
+                                int w) {
+            const float top = MAGIC + plan.top[w], alpha = plan.alpha[w];
+            const float fw = plan.fw[w];
+            const float var_scale = plan.out_var[w];
+            const i64 C = args.C;
+            const i64 tile = col_tile / C, cc0 = col_tile - tile * C;
+            const i64 p_tiles = args.ldws / C;
+            // One input slice at a time (not unrolled): the 16 in-kernel normals per slice
+            // need the registers.
+#pragma unroll 1
+            for (int a = 0; a < A; ++a) {
+                v16f I = {}, Q = {};
+                v8h digits[KS];
+                // This lane's vector's digit sum over the read's rows (the two lanes of a
+                // vector hold rows 0-7 and 8-15 of each 16-row block).
+                u32 rowsum = 0u;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const uint2 code = qcur[OUTN ? ks : 0];
+                    digits[ks] = digits_f16(code, plan.in_shift[a], plan.in_mask4[a]);
+                    const u32 sh = u32(plan.in_shift[a]);
+                    rowsum = __builtin_amdgcn_sad_u8((code.x >> sh) & plan.in_mask4[a], 0u, rowsum);
+                    rowsum = __builtin_amdgcn_sad_u8((code.y >> sh) & plan.in_mask4[a], 0u, rowsum);
+                }
+                rowsum += u32(__shfl_xor(int(rowsum), 32));
+#pragma unroll
+                for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks)
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fg[term][ks], digits[ks], I, 0, 0,
+                                                                   0);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const v8h squared = digits[ks] * digits[ks];
+#pragma unroll
+                    for (int term = 0; term < NOISY_TERMS; ++term)
+                        Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fq[term][ks], squared, Q, 0, 0, 0);
+                }
+                const int f = int(plan.fa[a] * fw);
+                const u32 f24 = u32(int(u32(f) << 8) >> 8);
+                const float shift = plan.kl[w] * float(rowsum);
+                const u64 base = u64((((n_out * G + g) * p_tiles + tile) * A + a) * W + w) * u64(C) +
+                                 u64(cc0 + lhalf * 4);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float mean = (I[r] + shift) * plan.out_mean;
+                    const float sd = sqrtf(fmaxf(Q[r] * var_scale, 0.0f));
+                    const u64 address = base + u64((r >> 2) * 8 + (r & 3));
+                    const float z = normal_in_range(address, args.read_seed, 60u, plan.two_pi);
+                    const float current = I[r] + (mean + sd * z);
+                    float y;
+                    if (NONLINEAR)
+                        y = fmaf(current, __builtin_amdgcn_rcpf(fmaf(fabsf(current), alpha, 1.0f)),
+                                 MAGIC);
+                    else
+                        y = current + MAGIC;
+                    y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
+                    const int low = int(__float_as_uint(y) << 8) >> 8;
+                    Ti[r] += u32(low) * f24;
+                    // One output at a time: interleaving the normals of all 16 outputs
+                    // would spill registers.
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        };
+        if (OUTN) {
+            for (int w = 0; w < W; ++w) {
+                load_terms(Fa, g, 2 * w);
+                load_terms(Fb, g, 2 * w + 1);
+                output_reads(Fa, Fb, w);
+            }
+        } else if (SLICE) {
             for (int w = 0; w < W; ++w)
                 for (int a = 0; a < A; ++a) {
                     load_terms(Fa, g, w * A + a);
@@ -441,6 +548,14 @@ __global__ __launch_bounds__(256, 2) void k_noisy(const NoisyPlan plan, const No
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
+// The read kernel.  The output-mode variant (16 in-kernel normals per pair) runs one wave
+// per SIMD, so that it has the whole register file instead of spilling.
+template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
+__global__ __launch_bounds__(256, OUTN ? 1 : 2) void k_noisy(const NoisyPlan plan,
+                                                             const NoisyArgs args) {
+    noisy_read<KS, NA, NONLINEAR, VNOISE, SLICE, OUTN>(plan, args);
+}
+
 __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, i64 ldt,
                                   i64 ncols, const float *xscale, const float *wscale, i64 ldws,
                                   float *out, i64 ldo, int lp, u32 *status) {
@@ -482,13 +597,14 @@ __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, 
     if (!finite && status) atomicOr(status, u32(MF_STATUS_OUTPUT));
 }
 
-#define MF_NOISY_INST1(KS, NA, NL, VN, SL) \
-    template __global__ void k_noisy<KS, NA, NL, VN, SL>(const NoisyPlan, const NoisyArgs);
-#define MF_NOISY_INST(KS, NA)                                                      \
-    MF_NOISY_INST1(KS, NA, false, false, false) MF_NOISY_INST1(KS, NA, true, false, false) \
-    MF_NOISY_INST1(KS, NA, false, true, false) MF_NOISY_INST1(KS, NA, true, true, false)   \
-    MF_NOISY_INST1(KS, NA, false, false, true) MF_NOISY_INST1(KS, NA, true, false, true)   \
-    MF_NOISY_INST1(KS, NA, false, true, true) MF_NOISY_INST1(KS, NA, true, true, true)
+#define MF_NOISY_INST1(KS, NA, NL, VN, SL, ON) \
+    template __global__ void k_noisy<KS, NA, NL, VN, SL, ON>(const NoisyPlan, const NoisyArgs);
+#define MF_NOISY_INST(KS, NA)                                                                    \
+    MF_NOISY_INST1(KS, NA, false, false, false, false) MF_NOISY_INST1(KS, NA, true, false, false, false) \
+    MF_NOISY_INST1(KS, NA, false, true, false, false) MF_NOISY_INST1(KS, NA, true, true, false, false)   \
+    MF_NOISY_INST1(KS, NA, false, false, true, false) MF_NOISY_INST1(KS, NA, true, false, true, false)   \
+    MF_NOISY_INST1(KS, NA, false, true, true, false) MF_NOISY_INST1(KS, NA, true, true, true, false)     \
+    MF_NOISY_INST1(KS, NA, false, false, false, true) MF_NOISY_INST1(KS, NA, true, false, false, true)
 MF_NOISY_INST(2, 5)
 MF_NOISY_INST(2, 8)
 MF_NOISY_INST(4, 5)

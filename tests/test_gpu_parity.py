@@ -496,6 +496,16 @@ MFMA_NOISY = {
                                weight_quant_gran=(64, 1), input_quant_gran=(1, 64)),
                           dict(write_variation=0.02, read_variation=0.01, read_mode="slice_pair",
                                voltage_variation=0.02, adc_nonlinearity=0.1)),
+    # Output-mode read noise: mean and variance sums beside the current, one normal per
+    # conversion; with binary digits, and at 64-row reads with SAF and the S-curve.
+    "output": (dict(), dict(write_variation=0.02, read_variation=0.02, read_mode="output")),
+    "output_binary8": (dict(input_slice=None, weight_slice=(1, 1, 2, 2, 2),
+                            adc_bits=(4, 5, 5, 6, 6)),
+                       dict(write_variation=0.02, read_variation=0.03, read_mode="output")),
+    "output_rows64": (dict(array_size=(128, 32), rows_per_read=64, weight_quant_gran=(64, 1),
+                           input_quant_gran=(1, 64)),
+                      dict(write_variation=0.02, read_variation=0.02, read_mode="output",
+                           stuck_at_low=0.01, stuck_at_high=0.01, adc_nonlinearity=0.1)),
 }
 NOISY_BASE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
                   weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,

@@ -30,7 +30,8 @@ def test_grid_follows_the_selected_kernel():
     assert [s["split"] for s in tuning.schedule_grid(slice_pair, 64, 8, arrays=4)] == [
         0, 1, 2, 4, 8]
     general = Config(**INT8, nonidealities=Nonidealities(read_variation=0.01,
-                                                          read_mode="output"))
+                                                          read_mode="output",
+                                                          voltage_variation=0.01))
     assert tuning.schedule_grid(general, 64, 8, arrays=4) == [tuning.default_schedule(general)]
     # Without the array count (the reference's signature) only the default is declared.
     assert tuning.schedule_grid(noisy, 64, 8) == [tuning.default_schedule(noisy)]
@@ -65,7 +66,8 @@ def test_workspace_need_prices_each_schedule():
         -(-(4 * 16 * 8) // 256) * 256 + -(-(32 * 16 * 8) // 256) * 256)
     general = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02,
                                                           read_variation=0.01,
-                                                          read_mode="output"))
+                                                          read_mode="output",
+                                                          voltage_variation=0.01))
     assert tuning.workspace_need(general, n, m, p, {}) == 4 * m * p * 5 * 128 * 128
     # Voltage variation adds the noisy read's input operands: hi and lo fp16 per input
     # slice, vector and physical row.
