@@ -156,9 +156,11 @@ def test_mfma_kernel_selected_for_baseline(hip_device):
     assert hip.mm_kernel(cfg, 4096, 32, 32) == 1
     noisy = Config(**CONFIG2)   # default write variation
     assert hip.mm_kernel(noisy, 4096, 32, 32) == 2
-    slice_pair = Config(**CONFIG2, nonidealities=Nonidealities(read_variation=0.01,
-                                                              read_mode="slice_pair"))
-    assert hip.mm_kernel(slice_pair, 4096, 32, 32) == 0
+    for mode in ("slice_pair", "output"):
+        other = Config(**CONFIG2, nonidealities=Nonidealities(read_variation=0.01, read_mode=mode))
+        assert hip.mm_kernel(other, 4096, 32, 32) == 2
+    voltage = Config(**CONFIG2, nonidealities=Nonidealities(voltage_variation=0.01))
+    assert hip.mm_kernel(voltage, 4096, 32, 32) == 2
 
 
 @pytest.mark.parametrize("name,cfg,n,k,o", IDEAL_CASES[:4], ids=[c[0] for c in IDEAL_CASES[:4]])
