@@ -342,11 +342,15 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
     }
     plan->bias = u32(0) - u32(u64(factor_sum) * 0x400000u);
     for (int a = 0; a < cfg->n_in; ++a)
-        for (int w = 0; w < cfg->n_w; ++w)
+        for (int w = 0; w < cfg->n_w; ++w) {
             if (std::abs(double(cfg->in_factor[a]) * double(cfg->w_factor[w])) >= 8388608.0) {
                 *why = "slice factor product beyond 24 bits";
                 return false;
             }
+            const int f = int(plan->fa[a] * plan->fw[w]);
+            plan->f24[a][w] = u32(int(u32(f) << 8) >> 8);
+        }
+    for (int w = 0; w < cfg->n_w; ++w) plan->top_magic[w] = 12582912.0f + plan->top[w];
     *ks = cfg->read_rows / 16;
     return true;
 }

@@ -126,6 +126,8 @@ struct NoisyPlan {
     int in_shift[8];
     u32 in_mask4[8];   // input slice mask replicated into four bytes
     u32 bias;          // -0x400000 * sum(fa*fw) modulo 2^32
+    u32 f24[8][8];     // fa*fw as the 24-bit signed operand of v_mad_i32_i24, per (a, w)
+    float top_magic[8];  // 1.5 * 2^23 + adc_max[w] (exact in FP32)
 };
 
 struct NoisyArgs {

@@ -301,17 +301,17 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
             }
         }
 
-        // Integer totals modulo 2^32, offset by 0x400000 * sum(fa*fw) (plan.bias).
+        // Integer totals modulo 2^32.  Every conversion adds fa*fw*(0x400000 + code), so
+        // they start at plan.bias = -0x400000 * sum(fa*fw) and end at the totals themselves.
         u32 Ti[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) Ti[r] = 0u;
+        for (int r = 0; r < 16; ++r) Ti[r] = plan.bias;
         // The reads of weight slice w with input slices [a_lo, a_hi) from terms F.
         auto slice_reads = [&](const v8h (&F)[NOISY_TERMS][KS], int w, int a_lo, int a_hi) {
-            const float top = MAGIC + plan.top[w], alpha = plan.alpha[w];
-            const float fw = plan.fw[w];
+            const float top = plan.top_magic[w], alpha = plan.alpha[w];
             auto convert = [&](const v16f &I, int a) {
-                const int f = int(plan.fa[a] * fw);   // |fa*fw| < 2^23 (plan)
-                const u32 f24 = u32(int(u32(f) << 8) >> 8);
+                // Sign-extended here so the compiler sees a 24-bit operand (v_mad_i32_i24).
+                const u32 f24 = u32(int(plan.f24[a][w] << 8) >> 8);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     // The terms carry k1, so I is already z = I * Ma*Mw / unit.  Rounding
@@ -366,8 +366,7 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
         // reference's per-(vector, read, tile, a, w, column) address, and the ADC.
         auto output_reads = [&](const v8h (&Fg)[NOISY_TERMS][KS], const v8h (&Fq)[NOISY_TERMS][KS],
                                 int w) {
-            const float top = MAGIC + plan.top[w], alpha = plan.alpha[w];
-            const float fw = plan.fw[w];
+            const float top = plan.top_magic[w], alpha = plan.alpha[w];
             const float var_scale = plan.out_var[w];
             const i64 C = args.C;
             const i64 tile = col_tile / C, cc0 = col_tile - tile * C;
@@ -403,8 +402,8 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
                     for (int term = 0; term < NOISY_TERMS; ++term)
                         Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fq[term][ks], squared, Q, 0, 0, 0);
                 }
-                const int f = int(plan.fa[a] * fw);
-                const u32 f24 = u32(int(u32(f) << 8) >> 8);
+                // Sign-extended here so the compiler sees a 24-bit operand (v_mad_i32_i24).
+                const u32 f24 = u32(int(plan.f24[a][w] << 8) >> 8);
                 const float shift = plan.kl[w] * float(rowsum);
                 const u64 base = u64((((n_out * G + g) * p_tiles + tile) * A + a) * W + w) * u64(C) +
                                  u64(cc0 + lhalf * 4);
@@ -468,7 +467,7 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
         }
         float T[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) T[r] = float(int(Ti[r] + plan.bias));
+        for (int r = 0; r < 16; ++r) T[r] = float(int(Ti[r]));
 
         if (args.totals) {
             if (n_out < args.n) {
