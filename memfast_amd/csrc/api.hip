@@ -210,7 +210,7 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
     for (int w = 0; w < cfg->n_w; ++w)
         wf[w] = slice_form(cfg->w_shift[w], cfg->w_mask[w], w == cfg->n_w - 1,
                            cfg->weight_bits);
-    // Clamp-candidate grid: slot ca * 8 + cw.
+    // Clamp-candidate grid: slot cw * 8 + ca (a weight slice's slots are adjacent).
     int ca_of[MF_MAX_SLICES], cw_of[MF_MAX_SLICES];
     for (int a = 0; a < cfg->n_in; ++a) {
         ca_of[a] = -1;
@@ -228,7 +228,6 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
         if (cw_of[w] >= 0) {
             plan->cw_wnat[cw_of[w]] = wf[w].nat;
             plan->cw_limit[cw_of[w]] = int(cfg->w_factor[w] * cfg->adc_max[w]);
-            if (cfg->w_factor[w] < 0) plan->cw_negative |= 1u << cw_of[w];
         }
     }
     memset(xtests, 0, sizeof(*xtests));
@@ -236,8 +235,10 @@ bool build_ideal_plan(const mf_config *cfg, i64 m, i64 p, IdealPlan *plan, SlotT
     for (int a = 0; a < cfg->n_in; ++a)
         for (int w = 0; w < cfg->n_w; ++w) {
             if (is_free[a][w]) continue;
-            const int slot = ca_of[a] * 8 + cw_of[w];
+            const int slot = cw_of[w] * 8 + ca_of[a];
             plan->exists |= uint64_t(1) << slot;
+            if ((cfg->in_factor[a] < 0) != (cfg->w_factor[w] < 0))
+                plan->cw_negative_ca[cw_of[w]] |= 1u << ca_of[a];
             // S <= Mw * sum_r da  and  S <= Ma * sum_r dw.
             xtests->exists |= uint64_t(1) << slot;
             xtests->slice[slot] = a;

@@ -139,32 +139,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, i6
 
 // T += min(Y, lim) - Y for a positive pair (max() for a negative one, lim < 0),
 // skipped when no output of the 32x32 tile crosses lim (the usual case).
+template <bool POSITIVE>
 __device__ __forceinline__ void correct_tile(v16i &T, const v16i &y, int lim) {
-    if (lim >= 0) {
-        int e = max(max(y[0], y[1]), y[2]);
-        e = max(max(e, y[3]), y[4]);
-        e = max(max(e, y[5]), y[6]);
-        e = max(max(e, y[7]), y[8]);
-        e = max(max(e, y[9]), y[10]);
-        e = max(max(e, y[11]), y[12]);
-        e = max(max(e, y[13]), y[14]);
-        e = max(e, y[15]);
-        if (__builtin_amdgcn_ballot_w64(e > lim) == 0) return;
+    int e = y[0];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) T[r] += min(lim - y[r], 0);
-    } else {
-        int e = min(min(y[0], y[1]), y[2]);
-        e = min(min(e, y[3]), y[4]);
-        e = min(min(e, y[5]), y[6]);
-        e = min(min(e, y[7]), y[8]);
-        e = min(min(e, y[9]), y[10]);
-        e = min(min(e, y[11]), y[12]);
-        e = min(min(e, y[13]), y[14]);
-        e = min(e, y[15]);
-        if (__builtin_amdgcn_ballot_w64(e < lim) == 0) return;
+    for (int r = 1; r < 16; ++r) e = POSITIVE ? max(e, y[r]) : min(e, y[r]);
+    if (__builtin_amdgcn_ballot_w64(POSITIVE ? e > lim : e < lim) == 0) return;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) T[r] += max(lim - y[r], 0);
-    }
+    for (int r = 0; r < 16; ++r) T[r] += POSITIVE ? min(lim - y[r], 0) : max(lim - y[r], 0);
 }
 
 template <int TN, int KS>
@@ -270,12 +252,6 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
 
     const uint64_t *xbits = args.xbits + vblock * G;
     const uint64_t *wbits = args.wbits + cblock * G;
-    // Per-slot constants, lane s holding slot s = ca * 8 + cw (read with readlane).
-    const int slot_ca = lane >> 3, slot_cw = lane & 7;
-    const bool slot_live = slot_ca < plan.n_ca && slot_cw < plan.n_cw;
-    const u32 slot_x = slot_live ? plan.ca_xnat[slot_ca] : 0u;
-    const u32 slot_w = slot_live ? plan.cw_wnat[slot_cw] : 0u;
-    const int slot_lim = slot_live ? plan.ca_factor[slot_ca] * plan.cw_limit[slot_cw] : 0;
     const int G_run = int(args.G_run);   // reads past G_run hold only zero padding
     for (int g = 0; g < G_run; ++g) {
         const int cur = g & 1;
@@ -305,21 +281,39 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
         // Clamp candidates (pairs that can exceed max_w) not proven clamp-free
         // by the digit sums are recomputed alone, Y = fa*fw*S; only a tile where
         // some |Y| exceeds the limit lim = fa*fw*max_w pays the per-output
-        // correction min(Y, lim) - Y (max() for negative pairs).
+        // correction min(Y, lim) - Y (max() for negative pairs).  Slots are
+        // numbered cw * 8 + ca, so one weight slice's failing slots share its
+        // masked operand; the slot constants are scalar loads from the plan.
         uint64_t fail = plan.exists & ~(xbits[g] | wbits[g]);
         while (fail) {
-            const int slot = __builtin_ctzll(fail);
-            fail &= fail - 1;
-            const u32 xm = u32(__builtin_amdgcn_readlane(int(slot_x), slot));
-            const u32 wm = u32(__builtin_amdgcn_readlane(int(slot_w), slot));
-            const int lim = __builtin_amdgcn_readlane(slot_lim, slot);
+            const int cw = __builtin_ctzll(fail) >> 3;
+            u32 group = u32(fail >> (cw * 8)) & 0xFFu;
+            fail &= ~(uint64_t(0xFF) << (cw * 8));
+            const u32 wm = plan.cw_wnat[cw];
+            const int wlim = plan.cw_limit[cw];
+            v4i Wm[KS];
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-                v16i y = mfma(and4(Wr[0], wm), and4(Xr[tn][0], xm), v16i{});
+            for (int ks = 0; ks < KS; ++ks) Wm[ks] = and4(Wr[ks], wm);
+            // Positive pairs (fa * fw > 0) first, then negative ones.
+            const u32 negative = plan.cw_negative_ca[cw];
+            auto candidates = [&](u32 set, auto positive) {
+                while (set) {
+                    const int ca = __builtin_ctz(set);
+                    set &= set - 1;
+                    const u32 xm = plan.ca_xnat[ca];
+                    const int lim = plan.ca_factor[ca] * wlim;
 #pragma unroll
-                for (int ks = 1; ks < KS; ++ks) y = mfma(and4(Wr[ks], wm), and4(Xr[tn][ks], xm), y);
-                correct_tile(T[tn], y, lim);
-            }
+                    for (int tn = 0; tn < TN; ++tn) {
+                        v16i y = mfma(Wm[0], and4(Xr[tn][0], xm), v16i{});
+#pragma unroll
+                        for (int ks = 1; ks < KS; ++ks)
+                            y = mfma(Wm[ks], and4(Xr[tn][ks], xm), y);
+                        correct_tile<decltype(positive)::value>(T[tn], y, lim);
+                    }
+                }
+            };
+            candidates(group & ~negative, std::true_type{});
+            candidates(group & negative, std::false_type{});
         }
 
         // Scale restore (float(T) * xs) * ws and cascade accumulation.

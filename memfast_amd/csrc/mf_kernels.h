@@ -50,7 +50,7 @@ struct IdealPlan {
     int ca_factor[IDEAL_MAX_CA];                      // fa
     u32 cw_wnat[IDEAL_MAX_CW];
     int cw_limit[IDEAL_MAX_CW];                       // fw * max_w
-    u32 cw_negative;                                  // bit cw: fw < 0
+    u32 cw_negative_ca[IDEAL_MAX_CW];                 // bit ca: fa * fw < 0
     uint64_t exists;                                  // slots holding a clamp candidate
 };
 
