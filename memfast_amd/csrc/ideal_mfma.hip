@@ -150,7 +150,8 @@ __device__ __forceinline__ void correct_tile(v16i &T, const v16i &y, int lim) {
 }
 
 template <int TN, int KS>
-__global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const IdealArgs args) {
+__global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const IdealPlan plan,
+                                                                           const IdealArgs args) {
     constexpr int BC = 64;                 // output columns per block
     constexpr int BV = 2 * TN * 32;        // vectors per block
     constexpr int KB = 32 * KS;            // code bytes per row and read (= P)
@@ -162,6 +163,9 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
     __shared__ __align__(16) u8 sX[2][BV * STRIDE];
     __shared__ __align__(16) float sWS[2][BC];
     __shared__ __align__(16) float sXS[2][BV];
+    // Level 1 of the cascade, per wave and lane (it changes once per 16 reads;
+    // keeping it out of registers leaves room for a fifth wave per SIMD).
+    __shared__ float sAcc1[4][TN][16][64];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -240,11 +244,11 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
         else if (scale_x) sXS[buf][tid - BC] = rscale;
     };
 
-    float acc0[TN][16], acc1[TN][16];
+    float acc0[TN][16];
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) { acc0[tn][r] = 0.0f; acc1[tn][r] = 0.0f; }
+        for (int r = 0; r < 16; ++r) { acc0[tn][r] = 0.0f; sAcc1[wave][tn][r][lane] = 0.0f; }
 
     fetch(0);
     stash(0);
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    acc1[tn][r] = acc1[tn][r] + acc0[tn][r];
+                    sAcc1[wave][tn][r][lane] = sAcc1[wave][tn][r][lane] + acc0[tn][r];
                     acc0[tn][r] = 0.0f;
                 }
             if ((count & 255) == 0) {
@@ -348,11 +352,12 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const i64 c = c0 + wc * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+                        const float a1 = sAcc1[wave][tn][r][lane];
                         if (n < args.n && c < args.ncols) {
                             float *dst = args.out + n * args.ldo + c;
-                            *dst = count == 256 ? acc1[tn][r] : *dst + acc1[tn][r];
+                            *dst = count == 256 ? a1 : *dst + a1;
                         }
-                        acc1[tn][r] = 0.0f;
+                        sAcc1[wave][tn][r][lane] = 0.0f;
                     }
                 }
             }
@@ -374,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void k_ideal(const IdealPlan plan, const Id
             v4f v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                float s = acc0[tn][qd * 4 + e] + acc1[tn][qd * 4 + e];
+                float s = acc0[tn][qd * 4 + e] + sAcc1[wave][tn][qd * 4 + e][lane];
                 if (G_run >= 256 && c + e < args.ncols) s = s + dst[e];
                 v[e] = s;
                 finite = finite && (c + e >= args.ncols || fabsf(s) <= FLT_MAX);
