@@ -28,12 +28,9 @@ import torch
 
 from .config import Config
 from .nn.training import _SurrogateGradient, _linear_surrogate
-from .simulator import Simulator
+from .simulator import _SINGLE_PASS as _SINGLE_PASS_DTYPES, Simulator
 
 _FLOATING = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
-# Dtypes whose FP32 quantization keeps finiteness, so that the device-side check of the
-# single-pass product raises exactly where a host check would.
-_SINGLE_PASS_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
 def _check_operands(a, b):
@@ -183,7 +180,9 @@ def _matmul(a, b, *, simulator, config, mode, cache_dir, out):
             if _wants_grad(a, b):
                 result = _SurrogateGradient.apply(result, torch.matmul(a.float(), b.float()))
         elif shared:
-            rhs = layout.right.reshape(layout.reduction, layout.columns)
+            # A rank-two B is its own program key; other shapes are read through a view.
+            right = layout.right
+            rhs = right if right.ndim == 2 else right.reshape(layout.reduction, layout.columns)
             inputs = layout.left.expand(layout.batch + layout.left.shape[-2:])
             result = _read(engine, inputs, rhs, b, (), single_pass).reshape(layout.shape)
         else:

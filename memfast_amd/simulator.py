@@ -141,6 +141,11 @@ class _ProgramCache(dict):
         self[key] = _CacheEntry(weakref.ref(owner, forget), _geometry(owner), program)
 
 
+# Dtypes whose FP32 quantization keeps finiteness, so that the device-side check of the
+# single-pass product raises exactly where a host check would.
+_SINGLE_PASS = (torch.float16, torch.bfloat16, torch.float32)
+
+
 class Simulator:
     """Configuration, device, and the choice of fixed defaults or a tuned schedule.
 
@@ -173,6 +178,7 @@ class Simulator:
         self._fingerprint = None
         self._next_id = 0
         self._matrix_cache = _ProgramCache(self)
+        self._status = None   # _product's device status word; replaced once it holds flags
 
     def _next_name(self):
         name = f"matrix.{self._next_id}"
@@ -197,9 +203,24 @@ class Simulator:
 
     def mm(self, input, mat2, *, out=None):
         """Simulate a two-dimensional matrix product, following torch.mm."""
+        if out is None and self._plain_pair(input, mat2):
+            return self._product(input, mat2)[0]
         from .functional import mm
 
         return mm(input, mat2, simulator=self, out=out)
+
+    def _plain_pair(self, a, b):
+        """Whether ``mm(a, b)`` goes straight to the single-pass product: two non-empty
+        dense matrices of one single-pass dtype on this simulator's device, with nothing
+        for the general route's checks, autocast or gradients to do.  Anything else
+        takes that route, which raises the reference's errors."""
+        return (type(a) is torch.Tensor and type(b) is torch.Tensor
+                and a.ndim == 2 and b.ndim == 2 and a.dtype == b.dtype
+                and a.dtype in _SINGLE_PASS and a.layout == b.layout == torch.strided
+                and a.device == b.device == self.device and self.device.type == "cuda"
+                and a.shape[1] == b.shape[0] and a.numel() > 0 and b.numel() > 0
+                and not (a.requires_grad or b.requires_grad)
+                and not torch.is_autocast_enabled("cuda"))
 
     def matmul(self, input, other, *, out=None):
         """Simulate a vector, matrix, or broadcast batch product like torch.matmul."""
@@ -245,7 +266,42 @@ class Simulator:
         """
         config = self.config
         owner = rhs if owner is None else owner
-        status = hip.status_word(self.device)
+        if self._status is None:
+            self._status = hip.status_word(self.device)
+        status = self._status
+        try:
+            flags, tiles, q, xscale, output, kept, fused, event = self._launch(
+                x, rhs, owner, index, status)
+        except BaseException:
+            self._status = None   # kernels may still set flags in this word
+            raise
+        if flags:
+            self._status = None
+        if flags & hip.STATUS_INPUT:
+            raise ValueError("A must be finite")
+        if flags & hip.STATUS_WEIGHT:
+            raise ValueError("B must be finite")
+        if kept is not None:
+            kept._install(tiles)
+            program = kept
+        else:
+            program = self._matrix_for(rhs, tiles=tiles, owner=owner, index=index)
+        if not fused:
+            if program.input_scale is not None:
+                q, xscale = hip.input_tiles(x.reshape(-1, x.shape[-1]), config,
+                                            program.input_scale)
+            return program._run(x, q, xscale), program
+        output = output[:, :program.out_features].contiguous()
+        finite = not flags & hip.STATUS_OUTPUT
+        if not finite and not config.wide:
+            output, finite = program._execute_checked(q, xscale, default_schedule(config), event,
+                                                      stable=True)
+        return program._finish(x, output, finite), program
+
+    def _launch(self, x, rhs, owner, index, status):
+        """The device work of ``_product`` up to its status read: both quantizers and, in
+        default mode, the fused read."""
+        config = self.config
         tiles = hip.weight_tiles(rhs.T, config, status=status)
         flat = x.reshape(-1, x.shape[-1])
         q, xscale = hip.input_tiles(flat, config, status=status)
@@ -265,26 +321,7 @@ class Simulator:
             output = hip.mm(q, xscale, packed, codes_t, wscale.reshape(-1, p * config.array_size[1]),
                             config, config.seed ^ _name_tag(name), event,
                             variant=tuning.DEFAULT_VARIANT, status=status, out_cols=o, k_rows=k)
-        flags = int(status.item())
-        if flags & hip.STATUS_INPUT:
-            raise ValueError("A must be finite")
-        if flags & hip.STATUS_WEIGHT:
-            raise ValueError("B must be finite")
-        if kept is not None:
-            kept._install(tiles)
-            program = kept
-        else:
-            program = self._matrix_for(rhs, tiles=tiles, owner=owner, index=index)
-        if not fused:
-            if program.input_scale is not None:
-                q, xscale = hip.input_tiles(flat, config, program.input_scale)
-            return program._run(x, q, xscale), program
-        output = output[:, :program.out_features].contiguous()
-        finite = not flags & hip.STATUS_OUTPUT
-        if not finite and not config.wide:
-            output, finite = program._execute_checked(q, xscale, default_schedule(config), event,
-                                                      stable=True)
-        return program._finish(x, output, finite), program
+        return int(status.item()), tiles, q, xscale, output, kept, fused, event
 
     # -- tuned mode (memfast_amd/tuning.py) -------------------------------------
     def _key(self, matrix, x, grid):

@@ -11,6 +11,7 @@ memfast/nn/conversion.py:26-243 and docs/user-guide.md:55-81.
 """
 
 import copy
+import dataclasses
 import math
 
 import pytest
@@ -107,6 +108,42 @@ def test_matmul_shapes_and_programs(hip_device, left, right):
     b3 = b2.expand(*batch, *b2.shape[-2:]).reshape(-1, *b2.shape[-2:])
     expected = torch.stack([oracle.mm(a3[i], b3[i], cfg) for i in range(a3.shape[0])])
     assert bits_equal(got.reshape(-1), expected.reshape(-1))
+
+
+@pytest.mark.parametrize("route", ["simulator", "functional"])
+def test_rhs_program_names_follow_tensor_geometry(hip_device, route):
+    """A rank-two RHS is its own program key (memfast/simulator.py:133-171): after an
+    in-place change of its geometry the new program takes over the old one's name and
+    read-event counter.  A vector RHS is read through a view of its tensor
+    (memfast/functional.py:95-127), so the same tensor with a new geometry is a new RHS.
+    Simulator.mm's direct route and the general functional route agree."""
+    cfg = dataclasses.replace(
+        IDEAL, nonidealities=Nonidealities(write_variation=0.02, read_variation=0.01))
+    sim = Simulator(cfg, device=hip_device)
+    gen = torch.Generator().manual_seed(83)
+    a = torch.randn(6, 150, generator=gen).to(hip_device)
+    b = torch.randn(150, 40, generator=gen).to(hip_device)
+    mm = sim.mm if route == "simulator" else (lambda x, y: memfast.mm(x, y, simulator=sim))
+    first, second = mm(a, b), mm(a, b)
+    program = sim._matrix_cache.program(b)
+    assert (program.name, program._event, sim._next_id) == ("matrix.0", 2, 1)
+    b.data = b.data.T.contiguous().T          # same values, new strides
+    assert b.stride() != (40, 1)
+    third = mm(a, b)
+    program = sim._matrix_cache.program(b)
+    assert (program.name, program._event, sim._next_id) == ("matrix.0", 3, 1)
+    # The reads used name matrix.0 at events 0, 1, 2, as a fresh simulator's reads do.
+    fresh, same = Simulator(cfg, device=hip_device), b.contiguous()
+    reads = [fresh.mm(a, same) for _ in range(3)]
+    assert all(bits_equal(got, want) for got, want in zip((first, second, third), reads))
+    assert not bits_equal(reads[1], reads[2])   # read noise follows the event
+    # Vector RHS: a new geometry of the same tensor is a new RHS with a new name.
+    v = torch.randn(150, generator=gen).to(hip_device)
+    sim.matmul(a, v)
+    key = sim._next_id
+    v.data = torch.randn(300, generator=gen).to(hip_device)[::2]
+    sim.matmul(a, v)
+    assert sim._next_id == key + 1
 
 
 def test_mm_out_and_argument_errors(hip_device):
