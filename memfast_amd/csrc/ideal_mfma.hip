@@ -257,8 +257,9 @@ __global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const
     const uint64_t *xbits = args.xbits + vblock * G;
     const uint64_t *wbits = args.wbits + cblock * G;
     const int G_run = int(args.G_run);   // reads past G_run hold only zero padding
-    for (int g = 0; g < G_run; ++g) {
-        const int cur = g & 1;
+    // One read; the LDS buffer index is a constant in each of the two copies.
+    auto read = [&](const int g, auto buffer) {
+        constexpr int cur = decltype(buffer)::value;
         if (g + 1 < G_run) fetch(g + 1);
 
         v4i Wr[KS], Xr[TN][KS];
@@ -365,6 +366,10 @@ __global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const
 
         if (g + 1 < G_run) stash(cur ^ 1);
         __syncthreads();
+    };
+    for (int g = 0; g < G_run; g += 2) {
+        read(g, std::integral_constant<int, 0>{});
+        if (g + 1 < G_run) read(g + 1, std::integral_constant<int, 1>{});
     }
 
     bool finite = true;
