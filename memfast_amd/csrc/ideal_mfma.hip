@@ -200,8 +200,11 @@ __global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const
         const int c = tid + e * 256;
         x_off[e] = (c / CHUNKS) * int(kp) + (c % CHUNKS) * 16;
     }
-    const bool scale_w = tid < BC;
-    const bool scale_x = tid >= BC && tid < BC + BV;
+    // Wave 0 loads the column scales, the next BV / 64 waves the vector scales
+    // (wave-uniform conditions, so the loads need no lane masks).
+    static_assert(BC == 64 && BV % 64 == 0 && BC + BV <= 256, "scale loaders");
+    const bool scale_w = wave == 0;
+    const bool scale_x = wave >= 1 && wave <= BV / 64;
     const int scale_off = scale_w ? tid * 4 : (tid - BC) * G * 4;
 
     v4i rw[W_LOADS], rx[X_LOADS];
@@ -221,11 +224,13 @@ __global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const
             rscale = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
                 xsbuf, scale_off + g * 4, 0, 0));
     };
+    // Tile rows are whole waves (multiples of 64 chunks), so the store conditions are
+    // wave-uniform.
     auto stash = [&](int buf) {
 #pragma unroll
         for (int e = 0; e < W_LOADS; ++e) {
             const int c = tid + e * 256;
-            if (W_LOADS * 256 == BC * CHUNKS || c < BC * CHUNKS) {
+            if (W_LOADS * 256 == BC * CHUNKS || wave + 4 * e < BC * CHUNKS / 64) {
                 v4i v = rw[e];
                 if (args.w_bits < 8) v = sext4(v, args.w_bits);
                 *reinterpret_cast<v4i *>(&sW[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const
 #pragma unroll
         for (int e = 0; e < X_LOADS; ++e) {
             const int c = tid + e * 256;
-            if (X_LOADS * 256 == BV * CHUNKS || c < BV * CHUNKS) {
+            if (X_LOADS * 256 == BV * CHUNKS || wave + 4 * e < BV * CHUNKS / 64) {
                 v4i v = rx[e];
                 if (args.a_bits < 8) v = sext4(v, args.a_bits);
                 *reinterpret_cast<v4i *>(&sX[buf][(c / CHUNKS) * STRIDE + (c % CHUNKS) * 16]) = v;
