@@ -227,9 +227,21 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
     const i64 n_out = v0 + wv * 32 + lrow;
     const i64 col_tile = args.c_begin + c0 + wc * 32;   // absolute first column of the wave
 
-    float acc0[16], acc1[16];
+    // Cascade levels 0 and 1 per output.  The 32-row reads keep them in LDS (each lane
+    // only ever touches its own words), which leaves room for a fourth wave per SIMD.
+    constexpr bool LDS_SUMS = KS == 2 && !OUTN;
+    __shared__ float sums[LDS_SUMS ? 2 : 1][LDS_SUMS ? 4 : 1][16][64];
+    float acc[2][LDS_SUMS ? 1 : 16];
+    auto sum_get = [&](int level, int r) -> float {
+        if constexpr (LDS_SUMS) return sums[level][wave][r][lane];
+        else return acc[level][r];
+    };
+    auto sum_set = [&](int level, int r, float v) {
+        if constexpr (LDS_SUMS) sums[level][wave][r][lane] = v;
+        else acc[level][r] = v;
+    };
 #pragma unroll
-    for (int r = 0; r < 16; ++r) { acc0[r] = 0.0f; acc1[r] = 0.0f; }
+    for (int r = 0; r < 16; ++r) { sum_set(0, r, 0.0f); sum_set(1, r, 0.0f); }
 
     // Reads of this block: [g0, g1) (a read split across blocks writes totals).
     const int g0 = int(args.g_begin + i64(blockIdx.z) * args.g_step);
@@ -497,15 +509,15 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
             for (int e = 0; e < 4; ++e) {
                 float v = T[qd * 4 + e] * xs;
                 v = v * ws[e];
-                acc0[qd * 4 + e] = acc0[qd * 4 + e] + v;
+                sum_set(0, qd * 4 + e, sum_get(0, qd * 4 + e) + v);
             }
         }
         const int count = g + 1;
         if ((count & 15) == 0) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                acc1[r] = acc1[r] + acc0[r];
-                acc0[r] = 0.0f;
+                sum_set(1, r, sum_get(1, r) + sum_get(0, r));
+                sum_set(0, r, 0.0f);
             }
             if ((count & 255) == 0) {
                 // Level 2 of the cascade lives in `out` (more than 255 reads).
@@ -514,9 +526,9 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
                     const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
                     if (n_out < args.n && c < args.ncols) {
                         float *dst = args.out + n_out * args.ldo + c;
-                        *dst = count == 256 ? acc1[r] : *dst + acc1[r];
+                        *dst = count == 256 ? sum_get(1, r) : *dst + sum_get(1, r);
                     }
-                    acc1[r] = 0.0f;
+                    sum_set(1, r, 0.0f);
                 }
             }
         }
@@ -531,7 +543,7 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
         v4fn v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            float s = acc0[qd * 4 + e] + acc1[qd * 4 + e];
+            float s = sum_get(0, qd * 4 + e) + sum_get(1, qd * 4 + e);
             if (g1 >= 256 && c + e < args.ncols) s = s + dst[e];
             v[e] = s;
             finite = finite && (c + e >= args.ncols || fabsf(s) <= FLT_MAX);
@@ -550,7 +562,8 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
 // The read kernel.  The output-mode variant (16 in-kernel normals per pair) runs one wave
 // per SIMD, so that it has the whole register file instead of spilling.
 template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
-__global__ __launch_bounds__(256, OUTN ? 1 : 2) void k_noisy(const NoisyPlan plan,
+__global__ __launch_bounds__(256, OUTN ? 1 : (KS == 2 && NA <= 5 ? 4 : 2)) void k_noisy(
+    const NoisyPlan plan,
                                                              const NoisyArgs args) {
     noisy_read<KS, NA, NONLINEAR, VNOISE, SLICE, OUTN>(plan, args);
 }
