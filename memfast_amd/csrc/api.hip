@@ -1312,9 +1312,13 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         const DigitJob xjob{q, n, 64, xl, xtests, xbits};
         const DigitJob wjob{packed_t, ncols, 32, wl, wtests, wbits};
         const i64 xblocks = (n + 63) / 64;
-        hipLaunchKernelGGL(k_digit_bits, dim3(gblocks, unsigned(xblocks + (ncols + 31) / 32)),
-                           dim3(64 * DIGIT_WAVES), 0, s, xjob, wjob, xblocks, kp, G,
-                           cfg->read_rows);
+        const dim3 dgrid(gblocks, unsigned(xblocks + (ncols + 31) / 32));
+        if (cfg->read_rows == 64)
+            hipLaunchKernelGGL(k_digit_bits<64>, dgrid, dim3(64 * DIGIT_WAVES), 0, s, xjob, wjob,
+                               xblocks, kp, G);
+        else
+            hipLaunchKernelGGL(k_digit_bits<32>, dgrid, dim3(64 * DIGIT_WAVES), 0, s, xjob, wjob,
+                               xblocks, kp, G);
         IdealArgs args{};
         args.q = q;
         args.wt = packed_t;

@@ -61,8 +61,10 @@ __device__ __forceinline__ v16i mfma(v4i a, v4i b, v16i c) {
 // partial maxima.  Digit sums use SWAR: (word >> shift) & mask per byte, then
 // v_sad_u8 adds the four bytes.  Requires P in {32, 64} and reads that start
 // at g * P (R a multiple of P).
+template <int P>
 __global__ __launch_bounds__(64 * DIGIT_WAVES) void k_digit_bits(
-    const DigitJob a, const DigitJob b, i64 first_blocks, i64 kp, i64 G, int P) {
+    const DigitJob a, const DigitJob b, i64 first_blocks, i64 kp, i64 G) {
+    constexpr int CHUNKS = P / 16;
     __shared__ int partial[DIGIT_WAVES][8][64];
     const bool second = i64(blockIdx.y) >= first_blocks;
     const DigitJob &job = second ? b : a;
@@ -81,34 +83,36 @@ __global__ __launch_bounds__(64 * DIGIT_WAVES) void k_digit_bits(
     u32 masks[8];
 #pragma unroll
     for (int sl = 0; sl < 8; ++sl) masks[sl] = sl < S ? u32(layout.mask[sl]) * 0x01010101u : 0u;
-    if (g < G) {
-        for (int i = 0; i < per; ++i) {
-            const i64 row = rb * block + wave * per + i;
-            if (row >= rows) break;
-            const uint4 *src = reinterpret_cast<const uint4 *>(codes + row * kp + g * P);
-            uint4 chunk[4];
-            chunk[0] = src[0];
-            chunk[1] = src[1];
-            if (P == 64) {
-                chunk[2] = src[2];
-                chunk[3] = src[3];
-            }
+    // Every row's loads are issued before the first digit sum.
+    constexpr int MAX_PER = 64 / DIGIT_WAVES;
+    uint4 chunk[MAX_PER][CHUNKS];
+    bool live[MAX_PER];
 #pragma unroll
-            for (int sl = 0; sl < 8; ++sl) {
-                if (sl >= S) break;
-                const int sh = layout.shift[sl];
-                const u32 mk = masks[sl];
-                u32 sum = 0;
+    for (int i = 0; i < MAX_PER; ++i) {
+        const i64 row = rb * block + wave * per + i;
+        live[i] = g < G && i < per && row < rows;
+        const uint4 *src = reinterpret_cast<const uint4 *>(codes + row * kp + g * P);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    if (c >= 2 && P != 64) break;
-                    sum = __builtin_amdgcn_sad_u8((chunk[c].x >> sh) & mk, 0u, sum);
-                    sum = __builtin_amdgcn_sad_u8((chunk[c].y >> sh) & mk, 0u, sum);
-                    sum = __builtin_amdgcn_sad_u8((chunk[c].z >> sh) & mk, 0u, sum);
-                    sum = __builtin_amdgcn_sad_u8((chunk[c].w >> sh) & mk, 0u, sum);
-                }
-                best[sl] = max(best[sl], int(sum));
+        for (int c = 0; c < CHUNKS; ++c)
+            chunk[i][c] = live[i] ? src[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < MAX_PER; ++i) {
+        if (!live[i]) continue;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) {
+            if (sl >= S) break;
+            const int sh = layout.shift[sl];
+            const u32 mk = masks[sl];
+            u32 sum = 0;
+#pragma unroll
+            for (int c = 0; c < CHUNKS; ++c) {
+                sum = __builtin_amdgcn_sad_u8((chunk[i][c].x >> sh) & mk, 0u, sum);
+                sum = __builtin_amdgcn_sad_u8((chunk[i][c].y >> sh) & mk, 0u, sum);
+                sum = __builtin_amdgcn_sad_u8((chunk[i][c].z >> sh) & mk, 0u, sum);
+                sum = __builtin_amdgcn_sad_u8((chunk[i][c].w >> sh) & mk, 0u, sum);
             }
+            best[sl] = max(best[sl], int(sum));
         }
     }
 #pragma unroll
@@ -116,16 +120,19 @@ __global__ __launch_bounds__(64 * DIGIT_WAVES) void k_digit_bits(
     __syncthreads();
     if (wave > 0 || g >= G || rb * block >= rows) return;
 #pragma unroll
-    for (int sl = 0; sl < 8; ++sl)
-        for (int w = 1; w < DIGIT_WAVES; ++w) best[sl] = max(best[sl], partial[w][sl][lane]);
+    for (int sl = 0; sl < 8; ++sl) {
+        if (sl >= S) break;
+        int m = best[sl];
+        for (int w = 1; w < DIGIT_WAVES; ++w) m = max(m, partial[w][sl][lane]);
+        partial[0][sl][lane] = m;
+    }
+    // Only this lane reads back its own words: no barrier needed.
     uint64_t bits = 0;
-    for (int slot = 0; slot < 64; ++slot) {
-        if (!((tests.exists >> slot) & 1)) continue;
-        int v = 0;
-#pragma unroll
-        for (int sl = 0; sl < 8; ++sl)
-            if (sl == tests.slice[slot]) v = best[sl];
-        if (v <= tests.thr[slot]) bits |= uint64_t(1) << slot;
+    uint64_t slots = tests.exists;
+    while (slots) {
+        const int slot = __builtin_ctzll(slots);
+        slots &= slots - 1;
+        if (partial[0][tests.slice[slot]][lane] <= tests.thr[slot]) bits |= uint64_t(1) << slot;
     }
     out[rb * G + g] = bits;
 }
@@ -405,6 +412,9 @@ __global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const
     }
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
+
+template __global__ void k_digit_bits<32>(const DigitJob, const DigitJob, i64, i64, i64);
+template __global__ void k_digit_bits<64>(const DigitJob, const DigitJob, i64, i64, i64);
 
 #define MF_IDEAL_INST(TN, KS) template __global__ void k_ideal<TN, KS>(const IdealPlan, const IdealArgs);
 MF_IDEAL_INST(2, 1)

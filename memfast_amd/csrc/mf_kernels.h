@@ -99,8 +99,8 @@ struct DigitJob {
     SlotTests tests;
     uint64_t *out;     // [ceil(rows / block), G]
 };
-__global__ void k_digit_bits(const DigitJob a, const DigitJob b, i64 first_blocks, i64 kp, i64 G,
-                             int P);
+template <int P>
+__global__ void k_digit_bits(const DigitJob a, const DigitJob b, i64 first_blocks, i64 kp, i64 G);
 
 // ---- conductances (restore.hip) -------------------------------------------
 template <typename Phys, typename Code>
