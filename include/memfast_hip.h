@@ -213,6 +213,25 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
           float *out, int64_t ldo, void *workspace, int64_t workspace_bytes, int32_t variant,
           uint32_t *status, void *stream);
 
+/* Both quantizations and the ideal read in two launches (memfast/functional.py:130-136:
+ * the RHS program of Simulator._matrix_for, memfast/simulator.py:133-171 with
+ * quantization.py:82-137, read by AnalogMatrix.forward, :618-646): x [n, k] FP32 (leading
+ * dimension ldx) and b [k, o] FP32 (ldb) are quantized exactly as mf_quantize_inputs
+ * (groups x_gr x x_gc) and mf_quantize_weights (groups w_gr x w_gc) would, into q
+ * [n, m, R], xscale [n, m*Gr], packed [m, p, R, C], packed_t [p*C, m*R] and wscale
+ * [m*Gr, p, C]; the quantizing workgroups also reduce the digit sums of the codes they
+ * wrote into the workspace's clamp-proof masks; then out [n, ldo] receives mf_mm's
+ * result for all o columns.  Status bits as those three calls set them.  Applies to ideal
+ * devices with 32 rows per read, groups of one read on both sides ((1, 32) and (32, 1)),
+ * R % 128 == 0, C % 64 == 0, k == m*R, o == p*C, 16-byte aligned x, q, packed,
+ * packed_t and out, and a workspace of mf_mm_workspace() bytes; otherwise it launches
+ * nothing and returns MF_E_UNSUPPORTED (the caller takes the three calls). */
+int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ldx,
+                     const float *b, int64_t o, int64_t ldb, int64_t x_gr, int64_t x_gc,
+                     int64_t w_gr, int64_t w_gc, uint8_t *q, float *xscale, uint8_t *packed,
+                     uint8_t *packed_t, float *wscale, float *out, int64_t ldo, void *workspace,
+                     int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream);
+
 /* No counterpart in the reference.  mf_mm for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): the same read, arguments and results, with the scratch that mf_mm

@@ -1265,6 +1265,52 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32
     return MF_OK;
 }
 
+// The ideal read proper once both sides' proven-slot masks are in xbits / wbits.
+static int launch_ideal(const mf_config *cfg, const IdealPlan &plan, int ks, const u8 *q,
+                        const float *xscale, const u8 *packed_t, const float *wscale,
+                        const uint64_t *xbits, const uint64_t *wbits, i64 n, i64 m, i64 p,
+                        i64 out_cols, i64 g_run, float *out, i64 ldo, int32_t variant,
+                        u32 *status, hipStream_t s) {
+    const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
+    IdealArgs args{};
+    args.q = q;
+    args.wt = packed_t;
+    args.xscale = xscale;
+    args.wscale = wscale;
+    args.xbits = xbits;
+    args.wbits = wbits;
+    args.out = out;
+    args.status = status;
+    args.n = n;
+    args.kp = kp;
+    args.G = G;
+    args.G_run = g_run;
+    args.ldo = ldo;
+    args.ldws = ncols;
+    args.ncols = out_cols;
+    args.Gr = cfg->reads;
+    args.R = cfg->rows;
+    args.P = cfg->read_rows;
+    args.a_bits = cfg->activation_bits;
+    args.w_bits = cfg->weight_bits;
+    // Tile variants: 0 default (32 vectors per wave), 1 = 64 vectors per wave,
+    // 2 = 32 vectors per wave.
+    const int tn = (ks == 1 && variant_tile(variant) == 1) ? 2 : 1;
+    const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (out_cols + 63) / 64;
+    if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
+    const dim3 grid{unsigned(gx), unsigned(gy), 1u};
+    std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+    if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+    if (ks == 1 && tn == 2) hipLaunchKernelGGL((k_ideal<2, 1>), grid, dim3(256), 0, s, plan, args);
+    else if (ks == 1) hipLaunchKernelGGL((k_ideal<1, 1>), grid, dim3(256), 0, s, plan, args);
+    else hipLaunchKernelGGL((k_ideal<1, 2>), grid, dim3(256), 0, s, plan, args);
+    if (timing.first) {
+        hipEventRecord(timing.second, s);
+        g_profile.pending.push_back(timing);
+    }
+    return check_launch("ideal MFMA read");
+}
+
 // Reads that hold at least one of the first k_rows rows (reads tile the
 // arrays: R a multiple of P, as the MFMA kernels require).
 static i64 reads_with_rows(const mf_config *cfg, i64 m, i64 k_rows) {
@@ -1319,43 +1365,8 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         else
             hipLaunchKernelGGL(k_digit_bits<32>, dgrid, dim3(64 * DIGIT_WAVES), 0, s, xjob, wjob,
                                xblocks, kp, G);
-        IdealArgs args{};
-        args.q = q;
-        args.wt = packed_t;
-        args.xscale = xscale;
-        args.wscale = wscale;
-        args.xbits = xbits;
-        args.wbits = wbits;
-        args.out = out;
-        args.status = status;
-        args.n = n;
-        args.kp = kp;
-        args.G = G;
-        args.G_run = g_run;
-        args.ldo = ldo;
-        args.ldws = ncols;
-        args.ncols = out_cols;
-        args.Gr = cfg->reads;
-        args.R = cfg->rows;
-        args.P = cfg->read_rows;
-        args.a_bits = cfg->activation_bits;
-        args.w_bits = cfg->weight_bits;
-        // Tile variants: 0 default (32 vectors per wave), 1 = 64 vectors per wave,
-        // 2 = 32 vectors per wave.
-        const int tn = (ks == 1 && variant_tile(variant) == 1) ? 2 : 1;
-        const i64 gy = (n + 64 * tn - 1) / (64 * tn), gx = (out_cols + 63) / 64;
-        if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
-        const dim3 grid{unsigned(gx), unsigned(gy), 1u};
-        std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
-        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-        if (ks == 1 && tn == 2) hipLaunchKernelGGL((k_ideal<2, 1>), grid, dim3(256), 0, s, plan, args);
-        else if (ks == 1) hipLaunchKernelGGL((k_ideal<1, 1>), grid, dim3(256), 0, s, plan, args);
-        else hipLaunchKernelGGL((k_ideal<1, 2>), grid, dim3(256), 0, s, plan, args);
-        if (timing.first) {
-            hipEventRecord(timing.second, s);
-            g_profile.pending.push_back(timing);
-        }
-        return check_launch("ideal MFMA read");
+        return launch_ideal(cfg, plan, ks, q, xscale, packed_t, wscale, xbits, wbits, n, m, p,
+                            out_cols, g_run, out, ldo, variant, status, s);
     }
     NoisyPlan noisy;
     if (!g && packed_t && aligned && workspace && ideal_extent_ok(cfg, n, m, p) &&
@@ -1397,6 +1408,79 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         g_profile.pending.push_back(timing);
     }
     return launched;
+}
+
+int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ldx,
+                     const float *b, int64_t o, int64_t ldb, int64_t x_gr, int64_t x_gc,
+                     int64_t w_gr, int64_t w_gc, uint8_t *q, float *xscale, uint8_t *packed,
+                     uint8_t *packed_t, float *wscale, float *out, int64_t ldo, void *workspace,
+                     int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream) {
+    const int valid = check_narrow(cfg);
+    if (valid) return valid;
+    if (!x || !b || !q || !xscale || !packed || !packed_t || !wscale || !out || n < 1 || k < 1 ||
+        o < 1 || ldx < k || ldb < o || ldo < o)
+        return fail(MF_E_INVALID, "invalid mm_from_float arguments");
+    if (!variant_valid(variant)) return fail(MF_E_INVALID, "unknown kernel variant 0x%x", variant);
+    const int R = cfg->rows, C = cfg->cols, P = cfg->read_rows;
+    const i64 m = (k + R - 1) / R, p = (o + C - 1) / C, G = m * cfg->reads;
+    // Groups of one read on both sides, whole arrays, and the tile and vector layouts the
+    // fused quantizer assumes; anything else takes mf_quantize_inputs/_weights + mf_mm.
+    const bool shapes = P == 32 && R % 128 == 0 && C % 64 == 0 && k == m * R && o == p * C &&
+                        G % 4 == 0 &&
+                        (x_gr < n ? x_gr : n) == 1 && x_gc == P && w_gr == P && w_gc == 1;
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0 &&
+                         reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(packed_t) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(packed) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(out) % 16 == 0 && ldo % 4 == 0;
+    i64 xbytes = 0, wbytes = 0;
+    ideal_workspace(cfg, n, m, p, &xbytes, &wbytes);
+    const bool room = workspace && workspace_bytes >= xbytes + wbytes;
+    IdealPlan plan;
+    SlotTests xtests, wtests;
+    int ks = 0;
+    const char *why = "";
+    const i64 wgrid_x = o / 64, wblocks = wgrid_x * (m * R / 128), xblocks = (n + 63) / 64 * (G / 4);
+    if (!shapes || !aligned || !room || !ideal_extent_ok(cfg, n, m, p) ||
+        wblocks + xblocks > 0x7FFFFFFF || !build_ideal_plan(cfg, m, p, &plan, &xtests, &wtests, &ks, &why))
+        return fail(MF_E_UNSUPPORTED, "mm_from_float not applicable");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint64_t *xbits = static_cast<uint64_t *>(workspace);
+    uint64_t *wbits = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) + xbytes);
+    ReadGroupArgs a{};
+    a.b = b;
+    a.k = k;
+    a.o = o;
+    a.ldb = ldb;
+    a.R = R;
+    a.C = C;
+    a.m = m;
+    a.p = p;
+    const int wbits_n = cfg->weight_bits;
+    a.wupper = float((1 << (wbits_n - (cfg->weight_signed ? 1 : 0))) - 1);
+    a.wlower = cfg->weight_signed ? -a.wupper : 0.0f;
+    a.wmask = (1u << wbits_n) - 1u;
+    a.packed = packed;
+    a.packed_t = packed_t;
+    a.wscale = wscale;
+    a.wgrid_x = wgrid_x;
+    a.wblocks = wblocks;
+    a.x = x;
+    a.n = n;
+    a.ldx = ldx;
+    a.xupper = float((1 << (cfg->activation_bits - 1)) - 1);
+    a.xmask = (1u << cfg->activation_bits) - 1u;
+    a.q = q;
+    a.xscale = xscale;
+    a.G = G;
+    a.wdigits = TileDigits{layout_of(cfg->w_shift, cfg->w_mask, cfg->n_w), wtests, wbits, G};
+    a.xdigits = TileDigits{layout_of(cfg->in_shift, cfg->in_mask, cfg->n_in), xtests, xbits, G};
+    a.status = status;
+    hipLaunchKernelGGL(k_read_groups, dim3(unsigned(wblocks + xblocks)), dim3(256), 0, s, a);
+    const int launched = check_launch("read-group quantization");
+    if (launched) return launched;
+    return launch_ideal(cfg, plan, ks, q, xscale, packed_t, wscale, xbits, wbits, n, m, p, o, G,
+                        out, ldo, variant, status, s);
 }
 
 }  // extern "C"

@@ -36,7 +36,7 @@ constexpr int IDEAL_MAX_CW = 8;     // weight slices with at least one clamped p
 
 // The linear part of every slice pair, sum_aw fa*fw*S_aw, is the plain int8
 // product of the codes.  Pairs that can exceed their ADC limit form a
-// (clamp-a x clamp-w) grid of slots s = ca * 8 + cw.  Per read and wave a slot
+// (clamp-w x clamp-a) grid of slots s = cw * 8 + ca.  Per read and wave a slot
 // is *proven clamp-free* when a digit-sum bound shows S <= max: max_n sum_r da
 // <= floor(max_w / Mw) (input side) or max_c sum_r dw <= floor(max_w / Ma)
 // (weight side).  The pre-pass k_digit_bits evaluates these tests and stores
@@ -101,6 +101,40 @@ struct DigitJob {
 };
 template <int P>
 __global__ void k_digit_bits(const DigitJob a, const DigitJob b, i64 first_blocks, i64 kp, i64 G);
+
+// The same masks produced by the quantizers that wrote the codes (k_read_groups).
+struct TileDigits {
+    SliceLayout layout;
+    SlotTests tests;
+    uint64_t *bits;    // [blocks, G]
+    i64 G;
+};
+
+// k_read_groups: B [k, o] (ld ldb) programmed in 32-row column groups into packed,
+// packed_t and the per-read scale table wscale [G, o]; A [n, k] (ld ldx) quantized in
+// groups of one read into q [n, k] and xscale [n, G]; both sides' digit-sum masks.
+// Requires rows per read 32, k == m*R and o == p*C.
+struct ReadGroupArgs {
+    const float *b;
+    i64 k, o, ldb;
+    int R, C;
+    i64 m, p;
+    float wlower, wupper;
+    u32 wmask;
+    u8 *packed, *packed_t;
+    float *wscale;
+    i64 wgrid_x, wblocks;     // tile grid width (o / 64) and tile workgroups
+    const float *x;
+    i64 n, ldx;
+    float xupper;
+    u32 xmask;
+    u8 *q;
+    float *xscale;
+    i64 G;
+    TileDigits wdigits, xdigits;
+    u32 *status;
+};
+__global__ void k_read_groups(const ReadGroupArgs a);
 
 // ---- conductances (restore.hip) -------------------------------------------
 template <typename Phys, typename Code>

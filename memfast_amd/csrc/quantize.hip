@@ -307,6 +307,18 @@ __global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, in
     }
     if (!finite && status) atomicOr(status, flag);
 }
+// The proven-slot mask of one side from its slices' digit-sum maxima (the test
+// k_digit_bits applies): slot s passes when maxima[tests.slice[s]] <= tests.thr[s].
+__device__ __forceinline__ uint64_t proven_slots(const SlotTests &tests, const int *maxima) {
+    uint64_t bits = 0, slots = tests.exists;
+    while (slots) {
+        const int slot = __builtin_ctzll(slots);
+        slots &= slots - 1;
+        if (maxima[tests.slice[slot]] <= tests.thr[slot]) bits |= uint64_t(1) << slot;
+    }
+    return bits;
+}
+
 // Column groups through an LDS tile: workgroup = 64 physical columns (lanes)
 // x 4 row groups of GR rows (waves), i.e. a [4*GR x 64] code tile.  Each lane
 // holds its group's GR values in registers (coalesced 256-byte row loads),
@@ -316,16 +328,19 @@ __global__ void k_col_groups_reg(const float *b, i64 k, i64 o, i64 ld, int R, in
 // == 0 (row segments stay inside one array tile) and kp % 16 == 0.
 // GIVEN: the group scales [ceil(k/gr), o] are already in `scale` (any gr, from
 // a separate group-maximum pass); each row takes its group's scale.
+// With `digits` (GR == 32 == rows per read), each wave also reduces its read's
+// digit sums over the 32-column blocks of the tile into their proven-slot masks.
 template <int GR, bool GIVEN>
-__global__ __launch_bounds__(256) void k_col_groups_tile(
-    const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m, i64 p, float lower, float upper,
-    u32 mask, u8 *packed, u8 *packed_t, float *scale, i64 gr, u32 *status, u32 flag) {
+__device__ __forceinline__ void col_tile(const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+                                         i64 p, float lower, float upper, u32 mask, u8 *packed,
+                                         u8 *packed_t, float *scale, i64 gr, u32 *status, u32 flag,
+                                         i64 bx, i64 by, const TileDigits *digits) {
     constexpr int ROWS = 4 * GR;
     __shared__ __align__(16) u8 tile_rc[ROWS][64 + 16];   // row-major codes
     __shared__ __align__(16) u8 tile_cr[64][ROWS + 16];   // column-major codes
     const i64 kp = m * R;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const i64 c0 = i64(blockIdx.x) * 64, r_block = i64(blockIdx.y) * ROWS;
+    const i64 c0 = bx * 64, r_block = by * ROWS;
     const i64 col = c0 + lane;
     const i64 r0 = r_block + wave * GR;
     const bool live = col < o;
@@ -389,7 +404,44 @@ __global__ __launch_bounds__(256) void k_col_groups_tile(
                 *reinterpret_cast<const uint4 *>(&tile_cr[cl][chunk * 16]);
         }
     }
+    if (GR == 32 && digits && r0 < kp) {
+        // This wave's rows are one read (g = r0 / 32) of all 64 columns.
+        __shared__ int col_max[4][2][8];
+        const uint4 *mine = reinterpret_cast<const uint4 *>(&tile_cr[lane][wave * GR]);
+        const uint4 lo = mine[0], hi = mine[1];
+        const SliceLayout &layout = digits->layout;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) {
+            if (sl >= layout.count) break;
+            const int sh = layout.shift[sl];
+            const u32 mk = u32(layout.mask[sl]) * 0x01010101u;
+            u32 sum = __builtin_amdgcn_sad_u8((lo.x >> sh) & mk, 0u, 0u);
+            sum = __builtin_amdgcn_sad_u8((lo.y >> sh) & mk, 0u, sum);
+            sum = __builtin_amdgcn_sad_u8((lo.z >> sh) & mk, 0u, sum);
+            sum = __builtin_amdgcn_sad_u8((lo.w >> sh) & mk, 0u, sum);
+            sum = __builtin_amdgcn_sad_u8((hi.x >> sh) & mk, 0u, sum);
+            sum = __builtin_amdgcn_sad_u8((hi.y >> sh) & mk, 0u, sum);
+            sum = __builtin_amdgcn_sad_u8((hi.z >> sh) & mk, 0u, sum);
+            sum = __builtin_amdgcn_sad_u8((hi.w >> sh) & mk, 0u, sum);
+            int best = int(sum);
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) best = max(best, __shfl_xor(best, off, 64));
+            if ((lane & 31) == 0) col_max[wave][lane >> 5][sl] = best;
+        }
+        // Lanes 0 and 32 read back only the words they wrote.
+        if ((lane & 31) == 0)
+            digits->bits[((c0 + lane) / 32) * digits->G + r0 / GR] =
+                proven_slots(digits->tests, col_max[wave][lane >> 5]);
+    }
     if (!finite && status) atomicOr(status, flag);
+}
+
+template <int GR, bool GIVEN>
+__global__ __launch_bounds__(256) void k_col_groups_tile(
+    const float *b, i64 k, i64 o, i64 ld, int R, int C, i64 m, i64 p, float lower, float upper,
+    u32 mask, u8 *packed, u8 *packed_t, float *scale, i64 gr, u32 *status, u32 flag) {
+    col_tile<GR, GIVEN>(b, k, o, ld, R, C, m, p, lower, upper, mask, packed, packed_t, scale, gr,
+                        status, flag, blockIdx.x, blockIdx.y, nullptr);
 }
 #define MF_COL_TILE_INST(GR, GIVEN)                                                             \
     template __global__ void k_col_groups_tile<GR, GIVEN>(const float *, i64, i64, i64, int, int, \
@@ -399,6 +451,94 @@ MF_COL_TILE_INST(16, false)
 MF_COL_TILE_INST(32, false)
 MF_COL_TILE_INST(32, true)
 #undef MF_COL_TILE_INST
+
+// Input row groups of one read (P = 32 values of one vector) for the ideal read, with
+// its digit-sum pre-pass: one workgroup quantizes reads 4j .. 4j+3 of 64 vectors (one
+// (vector, read) group per lane, whole 128-byte lines of q) into q and the per-read
+// scale table xscale [n, G], and reduces each read's digit sums over the 64 vectors into
+// the proven-slot mask of that vector block (what k_digit_bits computes from q).
+// Requires k == m*R, G % 4 == 0, ldx % 4 == 0 and 16-byte aligned x and q.
+__device__ __forceinline__ void input_read_block(const ReadGroupArgs &a, i64 block) {
+    __shared__ int wave_max[4][4][8];
+    __shared__ int block_max[4][8];
+    const i64 G = a.G, quads = G / 4;
+    const i64 vb = block / quads, g0 = (block - vb * quads) * 4;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int rd = t & 3;
+    const i64 row = vb * 64 + (t >> 2), g = g0 + rd;
+    const bool live = row < a.n;
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (live) {
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + row * a.ldx + g * 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = src[i];
+    }
+    bool finite = true;
+    float peak = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float e0 = fabsf(v[i].x), e1 = fabsf(v[i].y), e2 = fabsf(v[i].z), e3 = fabsf(v[i].w);
+        finite = finite && e0 <= FLT_MAX && e1 <= FLT_MAX && e2 <= FLT_MAX && e3 <= FLT_MAX;
+        peak = fmaxf(fmaxf(peak, fmaxf(e0, e1)), fmaxf(e2, e3));
+    }
+    const float s = group_scale(peak, a.xupper);
+    const float lo = -a.xupper, hi = a.xupper;
+    const u32 mk = a.xmask;
+    u32 w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        w[i] = u32(quantize_code(v[i].x, s, lo, hi, mk)) |
+               u32(quantize_code(v[i].y, s, lo, hi, mk)) << 8 |
+               u32(quantize_code(v[i].z, s, lo, hi, mk)) << 16 |
+               u32(quantize_code(v[i].w, s, lo, hi, mk)) << 24;
+    if (live) {
+        a.xscale[row * G + g] = s;
+        uint4 *dst = reinterpret_cast<uint4 *>(a.q + row * a.k + g * 32);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+    // Digit sums of this lane's (vector, read), maximized over the wave's 16 vectors of
+    // the same read and then over the workgroup's 4 waves.  Rows past n hold zero codes.
+    const SliceLayout &layout = a.xdigits.layout;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+        if (sl >= layout.count) break;
+        const int sh = layout.shift[sl];
+        const u32 dm = u32(layout.mask[sl]) * 0x01010101u;
+        u32 sum = 0u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum = __builtin_amdgcn_sad_u8((w[i] >> sh) & dm, 0u, sum);
+        int best = int(sum);
+#pragma unroll
+        for (int off = 4; off < 64; off <<= 1) best = max(best, __shfl_xor(best, off, 64));
+        if (lane < 4) wave_max[wave][lane][sl] = best;
+    }
+    __syncthreads();
+    if (t < 4) {
+        for (int sl = 0; sl < layout.count && sl < 8; ++sl)
+            block_max[t][sl] = max(max(wave_max[0][t][sl], wave_max[1][t][sl]),
+                                   max(wave_max[2][t][sl], wave_max[3][t][sl]));
+        a.xdigits.bits[vb * G + g0 + t] = proven_slots(a.xdigits.tests, block_max[t]);
+    }
+    if (!finite && a.status) atomicOr(a.status, u32(MF_STATUS_INPUT));
+}
+
+// Both operands of the ideal read in read-sized groups, with its digit-sum pre-pass, in
+// one launch: workgroups [0, wblocks) program B through the LDS code tile (32-row column
+// groups), the rest quantize A (one read of 64 vectors each).
+__global__ __launch_bounds__(256) void k_read_groups(const ReadGroupArgs a) {
+    const i64 block = blockIdx.x;
+    if (block < a.wblocks) {
+        const i64 bx = block % a.wgrid_x, by = block / a.wgrid_x;
+        col_tile<32, false>(a.b, a.k, a.o, a.ldb, a.R, a.C, a.m, a.p, a.wlower, a.wupper,
+                            a.wmask, a.packed, a.packed_t, a.wscale, 32, a.status,
+                            u32(MF_STATUS_WEIGHT), bx, by, &a.wdigits);
+    } else {
+        input_read_block(a, block - a.wblocks);
+    }
+}
 
 #define MF_COL_REG_INST(GR, WORD)                                                               \
     template __global__ void k_col_groups_reg<GR, WORD>(const float *, i64, i64, i64, int, int, \

@@ -147,6 +147,8 @@ SIGNATURES = {
                     _P, _P, _P], ct.c_int),
     "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
                ct.c_uint64, _P, _I64, _P, _I64, _I32, _P, _P], ct.c_int),
+    "mf_mm_from_float": ([_CFG, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
+                          _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_static": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
                       ct.c_uint64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
@@ -1050,6 +1052,61 @@ def mm_totals_wide(q, packed, config, seed, event, *, conductance=None):
 
 
 @lru_cache(maxsize=4096)
+def from_float_applies(config, n, k, o):
+    """Whether ``mm_from_float`` can take an [n, k] @ [k, o] product of this configuration
+    (the checks mf_mm_from_float repeats, short of buffer alignment): ideal devices on the
+    MFMA read, 32 rows per read, groups of one read on both sides, whole arrays."""
+    if config.wide or config.read_rows != 32:
+        return False
+    r, c = config.array_size
+    m, p = math.ceil(k / r), math.ceil(o / c)
+    return (r % 128 == 0 and c % 64 == 0 and k == m * r and o == p * c
+            and _group_dims((n, k), config.input_quant_gran) == (1, 32)
+            and _group_dims((k, o), config.weight_quant_gran) == (32, 1)
+            and mm_kernel(config, n, m, p) == 1)
+
+
+def mm_from_float(x, b, config, *, status=None, variant=0, workspace=None, scratch=None):
+    """``x [N, K] @ b [K, O]`` from floating operands in two launches (mf_mm_from_float):
+    (q, xscale, (packed, packed_t, wscale), out), exactly what ``input_tiles``,
+    ``weight_tiles(b.T)`` and ``mm`` return, or None where the fused route does not apply
+    (nothing is launched then).  ``workspace`` (optional, ``mm_workspace_bytes``) receives
+    the digit masks as ``mm`` would.  ``scratch`` (optional) is a (q, xscale, workspace)
+    triple of earlier results to write again, for a caller that has finished with them."""
+    require_device(x)
+    n, k = x.shape
+    o = b.shape[1]
+    device = x.device
+    xf = x if x.dtype == torch.float32 and x.is_contiguous() else x.float().contiguous()
+    bf = b if b.dtype == torch.float32 and b.is_contiguous() else b.detach().float().contiguous()
+    r, c = config.array_size
+    m, p = (k + r - 1) // r, (o + c - 1) // c
+    gr_x, gc_x = _group_dims((n, k), config.input_quant_gran)
+    gr_w, gc_w = _group_dims((k, o), config.weight_quant_gran)
+    reads = m * config.reads_per_array
+    if scratch is not None:
+        q, xscale, workspace = scratch
+    else:
+        q = torch.empty((n, m, r), dtype=torch.uint8, device=device)
+        xscale = torch.empty((n, reads), dtype=torch.float32, device=device)
+        if workspace is None:
+            workspace = _workspace(config, n, m, p, device, variant)
+    packed = torch.empty((m, p, r, c), dtype=torch.uint8, device=device)
+    packed_t = torch.empty((p * c, m * r), dtype=torch.uint8, device=device)
+    wscale = torch.empty((reads, p, c), dtype=torch.float32, device=device)
+    out = torch.empty((n, p * c), dtype=torch.float32, device=device)
+    with _on(device):
+        code = library().mf_mm_from_float(
+            ct.byref(descriptor(config)), xf.data_ptr(), n, k, k, bf.data_ptr(), o, o, gr_x,
+            gc_x, gr_w, gc_w, q.data_ptr(), xscale.data_ptr(), packed.data_ptr(),
+            packed_t.data_ptr(), wscale.data_ptr(), out.data_ptr(), p * c, workspace.data_ptr(),
+            workspace.numel(), variant, _ptr(status), _stream(device))
+    if code == E_UNSUPPORTED:
+        return None
+    check(code, "quantization and read")
+    return q, xscale, (packed, packed_t, wscale), out
+
+
 def mm_kernel(config, n, m, p, has_packed_t=True):
     """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA, 3: noisy-device MFMA for
     wide codes (what ``mm`` launches).

@@ -179,6 +179,10 @@ class Simulator:
         self._next_id = 0
         self._matrix_cache = _ProgramCache(self)
         self._status = None   # _product's device status word; replaced once it holds flags
+        self._from_float = {}   # (n, k, o) -> whether hip.mm_from_float applies
+        # (shape, (q, xscale, workspace)) of the last fused call, written again by the next
+        # call of that shape.
+        self._from_float_scratch = (None, None)
 
     def _next_name(self):
         name = f"matrix.{self._next_id}"
@@ -302,6 +306,10 @@ class Simulator:
         """The device work of ``_product`` up to its status read: both quantizers and, in
         default mode, the fused read."""
         config = self.config
+        if self.mode == "default":
+            fast = self._launch_from_float(x, rhs, owner, index, status)
+            if fast is not None:
+                return fast
         tiles = hip.weight_tiles(rhs.T, config, status=status)
         flat = x.reshape(-1, x.shape[-1])
         q, xscale = hip.input_tiles(flat, config, status=status)
@@ -322,6 +330,37 @@ class Simulator:
                             config, config.seed ^ _name_tag(name), event,
                             variant=tuning.DEFAULT_VARIANT, status=status, out_cols=o, k_rows=k)
         return int(status.item()), tiles, q, xscale, output, kept, fused, event
+
+    def _launch_from_float(self, x, rhs, owner, index, status):
+        """``_launch`` in two launches (``hip.mm_from_float``: both quantizers with the
+        ideal read's digit masks, then the read) where that route applies: what the
+        quantizers and the fused read produce, or None."""
+        flat = x.reshape(-1, x.shape[-1])
+        shape = (flat.shape[0], flat.shape[1], rhs.shape[1])
+        applies = self._from_float.get(shape)
+        if applies is None:
+            applies = self._from_float[shape] = hip.from_float_applies(self.config, *shape)
+        if not applies:
+            return None
+        previous, keepable = self._matrix_cache.previous(rhs, owner, index)
+        event = 0 if previous is None else previous._event
+        if event >= _EVENT_LIMIT or (previous is not None and previous.input_scale is not None):
+            return None
+        # The codes, scales and masks of the last call of this shape are written again: that
+        # call read its status word, so its kernels have finished.
+        last_shape, scratch = self._from_float_scratch
+        fused = hip.mm_from_float(flat, rhs, self.config, status=status,
+                                  scratch=scratch if last_shape == shape else None)
+        if fused is None:
+            self._from_float[shape] = False
+            return None
+        q, xscale, tiles, output = fused
+        if last_shape != shape:
+            workspace = hip._workspace(self.config, shape[0], q.shape[1], tiles[0].shape[1],
+                                       q.device)
+            self._from_float_scratch = (shape, (q, xscale, workspace))
+        kept = previous if keepable and previous._accepts(tiles) else None
+        return int(status.item()), tiles, q, xscale, output, kept, True, event
 
     # -- tuned mode (memfast_amd/tuning.py) -------------------------------------
     def _key(self, matrix, x, grid):

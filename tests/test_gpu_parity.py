@@ -384,6 +384,92 @@ def test_config2_full_size_permutation_equivariance(hip_device):
     assert not torch.equal(permuted.cpu(), out.cpu())   # the permutation moved values
 
 
+FROM_FLOAT_SHAPES = [(1, 128, 128), (37, 256, 128), (64, 128, 256), (200, 384, 256),
+                     (130, 4096, 128)]
+
+
+@pytest.mark.parametrize("data", ["randn", "saturating"])
+@pytest.mark.parametrize("n,k,o", FROM_FLOAT_SHAPES)
+def test_mm_from_float_matches_separate_calls(hip_device, n, k, o, data):
+    """mf_mm_from_float (one launch quantizing both operands and reducing the digit masks,
+    then the read) writes exactly what mf_quantize_inputs, mf_quantize_weights and mf_mm
+    write: codes, scale tables, the digit masks in the workspace and the output, which is
+    the oracle's.  Saturating operands make every clamp candidate real."""
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(n * 7 + k + o)
+    a, b = torch.randn(n, k, generator=gen), torch.randn(k, o, generator=gen)
+    if data == "saturating":
+        a, b = a.sign(), b.sign()
+    ad, bd = a.to(hip_device), b.to(hip_device)
+    assert hip.from_float_applies(cfg, n, k, o)
+    m, p = k // 128, o // 128
+    ws1 = torch.zeros(hip.mm_workspace_bytes(cfg, n, m, p), dtype=torch.uint8, device=hip_device)
+    ws2 = torch.zeros_like(ws1)
+    s1, s2 = hip.status_word(hip_device), hip.status_word(hip_device)
+    q, xscale, (packed, packed_t, wscale), out = hip.mm_from_float(ad, bd, cfg, status=s1,
+                                                                   workspace=ws1)
+    packed2, packed_t2, wscale2 = hip.weight_tiles(bd.T, cfg, status=s2)
+    q2, xscale2 = hip.input_tiles(ad, cfg, status=s2)
+    out2 = hip.mm(q2, xscale2, packed2, packed_t2, wscale2.reshape(-1, o), cfg, 0, 0,
+                  status=s2, workspace=ws2, out_cols=o, k_rows=k)
+    for name, got, want in (("q", q, q2), ("xscale", xscale, xscale2), ("packed", packed, packed2),
+                            ("packed_t", packed_t, packed_t2), ("wscale", wscale, wscale2),
+                            ("out", out, out2)):
+        assert bits_equal(got, want), name
+    G = m * cfg.reads_per_array
+    xwords, wwords = -(-n // 64) * G, (o // 32) * G
+    xbytes = -(-xwords * 8 // 256) * 256
+    for lo, count in ((0, xwords), (xbytes, wwords)):
+        got = ws1[lo:lo + 8 * count].view(torch.int64)
+        want = ws2[lo:lo + 8 * count].view(torch.int64)
+        assert torch.equal(got, want), (lo, count)
+    assert int(s1.item()) == int(s2.item()) == 0
+    assert bits_equal(out, oracle.mm(a, b, cfg))
+
+
+def test_mm_from_float_flags_nonfinite_operands(hip_device):
+    """The fused quantizers set the status bits the separate ones set; Simulator.mm raises
+    the reference's errors from them, A before B."""
+    from memfast_amd import Simulator
+
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(9)
+    a, b = torch.randn(64, 256, generator=gen), torch.randn(256, 128, generator=gen)
+    bad_a, bad_b = a.clone(), b.clone()
+    bad_a[5, 77] = float("nan")
+    bad_b[200, 3] = float("-inf")
+    for left, right, bit in ((bad_a, b, hip.STATUS_INPUT), (a, bad_b, hip.STATUS_WEIGHT),
+                             (bad_a, bad_b, hip.STATUS_INPUT | hip.STATUS_WEIGHT)):
+        status = hip.status_word(hip_device)
+        assert hip.mm_from_float(left.to(hip_device), right.to(hip_device), cfg,
+                                 status=status) is not None
+        assert int(status.item()) & (hip.STATUS_INPUT | hip.STATUS_WEIGHT) == bit
+    sim = Simulator(cfg, device=hip_device)
+    with pytest.raises(ValueError, match="A must be finite"):
+        sim.mm(bad_a.to(hip_device), bad_b.to(hip_device))
+    with pytest.raises(ValueError, match="B must be finite"):
+        sim.mm(a.to(hip_device), bad_b.to(hip_device))
+    assert bits_equal(sim.mm(a.to(hip_device), b.to(hip_device)), oracle.mm(a, b, cfg))
+
+
+def test_mm_from_float_declines_other_shapes(hip_device):
+    """Shapes and configurations outside the fused route launch nothing and return None;
+    Simulator.mm then takes the separate calls (checked against the oracle)."""
+    from memfast_amd import Simulator
+
+    cfg = ideal(**CONFIG2)
+    cases = [(cfg, 8, 150, 128), (cfg, 8, 256, 100),
+             (ideal(**CONFIG2 | dict(input_quant_gran=(1, None))), 8, 256, 128),
+             (Config(**CONFIG2, nonidealities=Nonidealities(write_variation=0.02)), 8, 256, 128)]
+    for config, n, k, o in cases:
+        assert not hip.from_float_applies(config, n, k, o)
+        a, b = torch.randn(n, k), torch.randn(k, o)
+        assert hip.mm_from_float(a.to(hip_device), b.to(hip_device), config) is None
+        if config.nonidealities.write_variation == 0.0:
+            got = Simulator(config, device=hip_device).mm(a.to(hip_device), b.to(hip_device))
+            assert bits_equal(got, oracle.mm(a, b, config))
+
+
 def test_functional_nonfinite_operands_leave_simulator_unchanged(hip_device):
     """The fused product checks finiteness on the device (functional.py:49-53 order)."""
     from memfast_amd import Simulator, mm
