@@ -427,6 +427,27 @@ def test_mm_from_float_matches_separate_calls(hip_device, n, k, o, data):
     assert bits_equal(out, oracle.mm(a, b, cfg))
 
 
+def test_mm_from_float_operand_forms(hip_device):
+    """Simulator.mm on the two-launch route with half-precision operands, a transposed B
+    (an nn.Linear weight read as W.T) and a sliced A: the oracle's result in A's dtype."""
+    from memfast_amd import Simulator
+
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(10)
+    a = torch.randn(96, 512, generator=gen)
+    w = torch.randn(256, 512, generator=gen)          # [O, K]
+    sim = Simulator(cfg, device=hip_device)
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        ad, wd = a.to(hip_device, dtype), w.to(hip_device, dtype)
+        assert hip.from_float_applies(cfg, 96, 512, 256)
+        got = sim.mm(ad, wd.T)
+        assert got.dtype == dtype
+        assert bits_equal(got, oracle.mm(ad.cpu(), wd.T.cpu(), cfg))
+    wide = torch.randn(96, 1024, generator=gen)
+    got = sim.mm(wide.to(hip_device)[:, 256:768], w.to(hip_device).T)
+    assert bits_equal(got, oracle.mm(wide[:, 256:768], w.T, cfg))
+
+
 def test_mm_from_float_flags_nonfinite_operands(hip_device):
     """The fused quantizers set the status bits the separate ones set; Simulator.mm raises
     the reference's errors from them, A before B."""
