@@ -230,7 +230,7 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
     // Cascade levels 0 and 1 per output.  The 32-row reads keep them in LDS (each lane
     // only ever touches its own words), which leaves room for a fourth wave per SIMD
     // (not with voltage noise, whose operand loads run faster at three).
-    constexpr bool LDS_SUMS = KS == 2 && !OUTN && !VNOISE;
+    constexpr bool LDS_SUMS = KS == 2 && !VNOISE;
     __shared__ float sums[LDS_SUMS ? 2 : 1][LDS_SUMS ? 4 : 1][16][64];
     float acc[2][LDS_SUMS ? 1 : 16];
     auto sum_get = [&](int level, int r) -> float {
@@ -563,7 +563,7 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
 // The read kernel.  The output-mode variant (16 in-kernel normals per pair) runs one wave
 // per SIMD, so that it has the whole register file instead of spilling.
 template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
-__global__ __launch_bounds__(256, OUTN ? 1 : (KS == 2 && NA <= 5 && !VNOISE ? 4 : 2)) void k_noisy(
+__global__ __launch_bounds__(256, OUTN ? (KS == 2 ? 2 : 1) : (KS == 2 && NA <= 5 && !VNOISE ? 4 : 2)) void k_noisy(
     const NoisyPlan plan,
                                                              const NoisyArgs args) {
     noisy_read<KS, NA, NONLINEAR, VNOISE, SLICE, OUTN>(plan, args);
