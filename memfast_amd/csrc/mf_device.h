@@ -24,14 +24,23 @@ __host__ __device__ __forceinline__ u32 mix(u32 x) {
     return x ^ (x >> 16);
 }
 
-__device__ __forceinline__ float uniform(u64 address, u64 seed, u32 stream) {
+// uniform() in two parts: uniform_fold() depends on the address's high word, the seed
+// and the stream only, so addresses that share a high word share it.
+__device__ __forceinline__ u32 uniform_fold(u32 hi, u64 seed, u32 stream) {
     const u32 key = mix(u32(seed) ^ (stream * 0x9e3779b9u));
-    const u32 hi = u32(address >> 32);
     u32 fold = mix(hi ^ mix(u32(seed >> 32)));
     if (hi != 0u) fold ^= mix(hi ^ key);
-    const u32 h = mix(u32(address) ^ fold ^ key);
+    return fold ^ key;
+}
+
+__device__ __forceinline__ float uniform_finish(u32 lo, u32 fold) {
+    const u32 h = mix(lo ^ fold);
     // ((h >> 8) + 0.5) / 2^24 is exact in FP32.
     return (float(h >> 8) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+__device__ __forceinline__ float uniform(u64 address, u64 seed, u32 stream) {
+    return uniform_finish(u32(address), uniform_fold(u32(address >> 32), seed, stream));
 }
 
 __device__ __forceinline__ float normal(u64 address, u64 seed, u32 stream, float two_pi) {

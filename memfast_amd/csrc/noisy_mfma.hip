@@ -187,16 +187,32 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
     }
 }
 
-// normal() for a kernel short of registers: the cosine's argument 2*pi*u (u a uniform in
-// (0, 1)) is told to lie in [0, 6.3], which lets the compiler drop the large-argument
-// reduction of cosf; the value is the same.
-__device__ __forceinline__ float normal_in_range(u64 address, u64 seed, u32 stream, float two_pi) {
-    const float u = uniform(address, seed, stream);
-    const float v = uniform(address, seed, stream + 1u);
-    const float angle = two_pi * v;
-    __builtin_assume(angle >= 0.0f && angle <= 6.3f);
-    return sqrtf(-2.0f * logf(u)) * cosf(angle);
-}
+// The normals of normal() at the addresses base + offset (offset < 2^31) for one stream
+// pair, at a few instructions each:
+// * the high-word folds of both streams are computed once for base's high word, and again
+//   only in a lane whose low word carries;
+// * log2 (v_log_f32), cos(2*pi*v) with v in revolutions (v_cos_f32) and sqrt (v_sqrt_f32)
+//   are one instruction each.  Over every uniform value (k + 0.5) / 2^24 they stay within
+//   1.2e-7 relative (log2) and 1.3e-7 absolute (cos), and sqrt(-2 ln u) within 4.8e-7
+//   absolute of the exact value (OCML's sqrtf(-2 logf(u)): 5.9e-7).
+struct NormalRun {
+    u32 lo, hi, fold_u, fold_v;
+    __device__ __forceinline__ NormalRun(u64 base, u64 seed, u32 stream)
+        : lo(u32(base)), hi(u32(base >> 32)), fold_u(uniform_fold(hi, seed, stream)),
+          fold_v(uniform_fold(hi, seed, stream + 1u)) {}
+    __device__ __forceinline__ float at(u32 offset, u64 seed, u32 stream) const {
+        const u32 low = lo + offset;
+        u32 fu = fold_u, fv = fold_v;
+        if (low < offset) {   // the low word carried into the high word
+            fu = uniform_fold(hi + 1u, seed, stream);
+            fv = uniform_fold(hi + 1u, seed, stream + 1u);
+        }
+        const float u = uniform_finish(low, fu), v = uniform_finish(low, fv);
+        // -2 ln u = -2 ln(2) log2(u).
+        return __builtin_amdgcn_sqrtf(-1.38629436f * __builtin_amdgcn_logf(u)) *
+               __builtin_amdgcn_cosf(v);
+    }
+};
 
 template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
 __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArgs &args) {
@@ -420,12 +436,12 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
                 const float shift = plan.kl[w] * float(rowsum);
                 const u64 base = u64((((n_out * G + g) * p_tiles + tile) * A + a) * W + w) * u64(C) +
                                  u64(cc0 + lhalf * 4);
+                const NormalRun normals(base, args.read_seed, 60u);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float mean = (I[r] + shift) * plan.out_mean;
-                    const float sd = sqrtf(fmaxf(Q[r] * var_scale, 0.0f));
-                    const u64 address = base + u64((r >> 2) * 8 + (r & 3));
-                    const float z = normal_in_range(address, args.read_seed, 60u, plan.two_pi);
+                    const float sd = __builtin_amdgcn_sqrtf(fmaxf(Q[r] * var_scale, 0.0f));
+                    const float z = normals.at(u32((r >> 2) * 8 + (r & 3)), args.read_seed, 60u);
                     const float current = I[r] + (mean + sd * z);
                     float y;
                     if (NONLINEAR)
@@ -560,10 +576,11 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
-// The read kernel.  The output-mode variant (16 in-kernel normals per pair) runs one wave
-// per SIMD, so that it has the whole register file instead of spilling.
+// The read kernel.  The output-mode variant (16 in-kernel normals per pair) runs three waves
+// per SIMD at 32-row reads (a few spilled registers cost less than a wave fewer) and one at
+// 64-row reads, which hold two slices' terms.
 template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
-__global__ __launch_bounds__(256, OUTN ? (KS == 2 ? 2 : 1) : (KS == 2 && NA <= 5 && !VNOISE ? 4 : 2)) void k_noisy(
+__global__ __launch_bounds__(256, OUTN ? (KS == 2 ? 3 : 1) : (KS == 2 && NA <= 5 && !VNOISE ? 4 : 2)) void k_noisy(
     const NoisyPlan plan,
                                                              const NoisyArgs args) {
     noisy_read<KS, NA, NONLINEAR, VNOISE, SLICE, OUTN>(plan, args);
