@@ -401,10 +401,12 @@ i64 noisy_scratch_bytes(const mf_config *cfg, i64 n, i64 m, i64 p, int requested
 }
 
 // Voltage-variation input operands (k_voltage_terms): hi and lo fp16 per input
-// slice, vector and physical row.  They sit at the end of the workspace, so the
-// conductance terms keep their place (and stay reusable) whatever the vector count.
+// slice, vector (in blocks of 32) and physical row.  They sit at the end of the
+// workspace, so the conductance terms keep their place (and stay reusable) whatever
+// the vector count.
 i64 noisy_voltage_bytes(const mf_config *cfg, i64 n, i64 m) {
-    return cfg->has_vnoise ? align256(2 * i64(cfg->n_in) * n * m * cfg->rows * 2) : 0;
+    const i64 vectors = (n + 31) / 32 * 32;
+    return cfg->has_vnoise ? align256(2 * i64(cfg->n_in) * vectors * m * cfg->rows * 2) : 0;
 }
 
 // Fields of the `variant` word (include/memfast_hip.h).
@@ -441,7 +443,8 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         // Aligned down to 256 bytes at the end of the workspace.
         const i64 at = ((bytes - vbytes) / 256) * 256;
         uint4 *operands = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + at);
-        hipLaunchKernelGGL(k_voltage_terms, dim3(grid_for(i64(cfg->n_in) * n * (kp / 8))),
+        hipLaunchKernelGGL(k_voltage_terms,
+                           dim3(grid_for(i64(cfg->n_in) * ((n + 31) / 32 * 32) * (kp / 8))),
                            dim3(256), 0, s, *cfg, q, n, m, seed, event, operands);
         volt = operands;
         bytes = at;

@@ -175,8 +175,8 @@ struct NoisyArgs {
     i64 g_begin, g_end;   // reads of this launch (blockIdx.z adds g_step)
     i64 g_step;
     int totals;
-    // Voltage variation: input operands [2][A][n][kp] fp16 (hi, lo) of digit * (1 + vv*z)
-    // from k_voltage_terms, read instead of the digits of q.
+    // Voltage variation: input operands [2][A][ceil(n/32)][kp/8][32] uint4 of 8 fp16 (hi,
+    // lo) of digit * (1 + vv*z) from k_voltage_terms, read instead of the digits of q.
     const uint4 *volt;
     u64 read_seed;        // output-mode read noise: event_seed(seed, event)
     i64 C;                // array columns (output-mode noise addresses)
@@ -191,7 +191,9 @@ template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
 // Input operands of a read with voltage variation (memfast/reference.py:77-82): per
 // input slice a, vector v and physical row k, digit * (1 + vv * z(address)) split into
-// fp16 hi + lo, layout [2][A][n][kp].
+// fp16 hi + lo.  Layout [2][A][ceil(n/32)][kp/8][32] of uint4 (8 rows each): the 32
+// vectors of a block are innermost, so one MFMA operand of a wave (32 vectors, two
+// 8-row units) is 1 KiB contiguous.  Vectors past n hold zeros.
 __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
                                 u64 event, uint4 *volt);
 // (float(T) * xs) * ws summed over reads in torch's cascade order, from slice

@@ -153,14 +153,21 @@ __device__ __forceinline__ v8h digits_f16(uint2 word, int shift, u32 mask4) {
 __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
                                 u64 event, uint4 *volt) {
     const int R = cfg.rows, A = cfg.n_in;
-    const i64 kp = m * R, units = kp / 8;
-    const i64 total = i64(A) * n * units;
+    const i64 kp = m * R, units = kp / 8, vblocks = (n + 31) / 32;
+    const i64 total = i64(A) * vblocks * units * 32;
     const u64 read_seed = event_seed(seed, event);
     for (i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
          t += i64(gridDim.x) * blockDim.x) {
-        const i64 u = t % units, rest = t / units;
-        const i64 v = rest % n;
-        const int a = int(rest / n);
+        // t is the operand's index in [A][vblocks][units][32].
+        const i64 lr = t & 31, rest = t >> 5;
+        const i64 u = rest % units, vb = (rest / units) % vblocks;
+        const int a = int(rest / (units * vblocks));
+        const i64 v = vb * 32 + lr;
+        if (v >= n) {
+            volt[t] = make_uint4(0u, 0u, 0u, 0u);
+            volt[i64(A) * vblocks * units * 32 + t] = make_uint4(0u, 0u, 0u, 0u);
+            continue;
+        }
         const i64 k0 = u * 8;
         const uint2 bytes = *reinterpret_cast<const uint2 *>(q + v * kp + k0);
         const u32 shift = u32(cfg.in_shift[a]), mask = u32(cfg.in_mask[a]);
@@ -182,8 +189,8 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
             hw[j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << half;
             lw[j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << half;
         }
-        volt[(i64(a) * n + v) * units + u] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        volt[((i64(A) + a) * n + v) * units + u] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        volt[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        volt[i64(A) * vblocks * units * 32 + t] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
 }
 
@@ -272,14 +279,16 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
         const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + g0 * P + ks * 16 + 4, 0, 0);
         qw[ks] = make_uint2(x, y);
     }
-    // Voltage-noise operands of this lane's vector: [term][a] rows of kp/8 uint4.
-    const i64 vunits = kp / 8;
-    const bool vlive = n_out < args.n;
+    // Voltage-noise operands of this wave's 32 vectors: [term][a][vector block] runs of
+    // kp/8 units of 32 uint4, so a wave's operand is 1 KiB contiguous.
+    const i64 vunits = kp / 8, vblocks = (args.n + 31) / 32, vblock = (v0 + wv * 32) / 32;
+    const bool vlive = vblock < vblocks;   // wave-uniform; padded vectors hold zeros
+    const i64 vplane = vblocks * vunits * 32;   // one (term, a) plane, in uint4
+    const uint4 *vbase = args.volt + vblock * vunits * 32 + lane;   // lane = lhalf * 32 + lrow
     auto volt_operand = [&](int term, int a, int g, int ks) -> v8h {
         if (!vlive) return v8h{};
-        const i64 unit = (g * P + ks * 16 + lhalf * 8) / 8;
         return __builtin_bit_cast(
-            v8h, args.volt[((i64(term) * A + a) * args.n + n_out) * vunits + unit]);
+            v8h, vbase[(term * A + a) * vplane + (g * (P / 8) + ks * 2) * 32]);
     };
 
     // Conductance terms of (read g, weight slice w), double-buffered in registers:
