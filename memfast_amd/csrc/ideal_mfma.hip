@@ -145,7 +145,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void *base, i6
 }
 
 // T += min(Y, lim) - Y for a positive pair (max() for a negative one, lim < 0),
-// skipped when no output of the 32x32 tile crosses lim (the usual case).
+// skipped when no output of the 32x32 tile crosses lim (the usual case).  A positive
+// pair has Y >= 0 and lim > 0, so min(Y, lim) - Y = -(Y -sat lim), an unsigned
+// saturating subtract (one instruction).
 template <bool POSITIVE>
 __device__ __forceinline__ void correct_tile(v16i &T, const v16i &y, int lim) {
     int e = y[0];
@@ -153,7 +155,12 @@ __device__ __forceinline__ void correct_tile(v16i &T, const v16i &y, int lim) {
     for (int r = 1; r < 16; ++r) e = POSITIVE ? max(e, y[r]) : min(e, y[r]);
     if (__builtin_amdgcn_ballot_w64(POSITIVE ? e > lim : e < lim) == 0) return;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) T[r] += POSITIVE ? min(lim - y[r], 0) : max(lim - y[r], 0);
+    for (int r = 0; r < 16; ++r) {
+        if (POSITIVE)
+            T[r] = int(u32(T[r]) - __builtin_elementwise_sub_sat(u32(y[r]), u32(lim)));
+        else
+            T[r] += max(lim - y[r], 0);
+    }
 }
 
 template <int TN, int KS>

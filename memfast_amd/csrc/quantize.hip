@@ -88,6 +88,29 @@ __device__ __forceinline__ u8 quantize_code(float x, float s, float lower, float
     return u8(u32(int(c)) & mask);
 }
 
+// quantize_code() for many values of one group at the cost of one division.  The
+// quotient is taken as q = x * y with y = RN(1/s): then |q - x/s| <= |x/s| * 2^-23 and the
+// reference's RN(x/s) is within |x/s| * 2^-24 of x/s, so for |x/s| <= 256 the two lie
+// within 2^-14.4 of each other and round to the same integer unless q is within that of
+// a half-integer.  Such values (|q - rint(q)| >= 0.5 - 2^-12), NaN, and every value of a
+// group whose 1/s overflows (s subnormal) take the IEEE division.  Beyond |x/s| = 256 both
+// quotients clamp to the same code, as long as |lower|, upper <= 128 (codes of at most
+// 8 bits).
+struct GroupCodes {
+    float s, y;
+    bool fast;
+    __device__ __forceinline__ explicit GroupCodes(float scale)
+        : s(scale), y(1.0f / scale), fast(y <= FLT_MAX) {}
+    __device__ __forceinline__ u8 operator()(float x, float lower, float upper, u32 mask) const {
+        const float q = x * y;
+        float c = rintf(q);
+        if (!fast || !(fabsf(q - c) < 0.5f - 0x1p-12f)) c = rintf(x / s);
+        c = c < lower ? lower : c;
+        c = c > upper ? upper : c;
+        return u8(u32(int(c)) & mask);
+    }
+};
+
 // scale of one group from its peak |x| (quantization.py:25-31 for INT codes).
 __device__ __forceinline__ float group_scale(float peak, float upper) {
     float s = (peak > 0.0f ? peak : 1.0f) / upper;
@@ -376,9 +399,10 @@ __device__ __forceinline__ void col_tile(const float *b, i64 k, i64 o, i64 ld, i
         }
         const float sc = group_scale(peak, upper);
         if (live && r0 < k) scale[(r0 / GR) * o + col] = sc;
+        const GroupCodes codes(sc);
 #pragma unroll
         for (int i = 0; i < GR; ++i) {
-            const u8 code = (live && r0 + i < k) ? quantize_code(v[i], sc, lower, upper, mask) : u8(0);
+            const u8 code = (live && r0 + i < k) ? codes(v[i], lower, upper, mask) : u8(0);
             tile_rc[wave * GR + i][lane] = code;
             tile_cr[lane][wave * GR + i] = code;
         }
@@ -486,13 +510,12 @@ __device__ __forceinline__ void input_read_block(const ReadGroupArgs &a, i64 blo
     const float s = group_scale(peak, a.xupper);
     const float lo = -a.xupper, hi = a.xupper;
     const u32 mk = a.xmask;
+    const GroupCodes codes(s);
     u32 w[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        w[i] = u32(quantize_code(v[i].x, s, lo, hi, mk)) |
-               u32(quantize_code(v[i].y, s, lo, hi, mk)) << 8 |
-               u32(quantize_code(v[i].z, s, lo, hi, mk)) << 16 |
-               u32(quantize_code(v[i].w, s, lo, hi, mk)) << 24;
+        w[i] = u32(codes(v[i].x, lo, hi, mk)) | u32(codes(v[i].y, lo, hi, mk)) << 8 |
+               u32(codes(v[i].z, lo, hi, mk)) << 16 | u32(codes(v[i].w, lo, hi, mk)) << 24;
     if (live) {
         a.xscale[row * G + g] = s;
         uint4 *dst = reinterpret_cast<uint4 *>(a.q + row * a.k + g * 32);

@@ -427,6 +427,51 @@ def test_mm_from_float_matches_separate_calls(hip_device, n, k, o, data):
     assert bits_equal(out, oracle.mm(a, b, cfg))
 
 
+def near_half_integer_groups(count, seed):
+    """[count, 32] float32 groups whose quotients x / s (s = peak / 127, as the quantizer
+    computes it) sit on or within three ulps of a half-integer: exact ties (power-of-two
+    scales), their neighbours, and groups with subnormal and huge peaks."""
+    rng = np.random.default_rng(seed)
+    groups = np.empty((count, 32), dtype=np.float32)
+    for g in range(count):
+        kind = g % 4
+        if kind == 0:
+            peak = np.float32(127.0 * 2.0 ** rng.integers(-20, 20))   # s a power of two
+        elif kind == 1:
+            peak = np.float32(np.exp(rng.uniform(-8.0, 8.0)))
+        elif kind == 2:
+            peak = np.float32(rng.uniform(1e-43, 1e-39))              # subnormal scale
+        else:
+            peak = np.float32(rng.uniform(1e30, 3e38))
+        s = max(np.float32(peak) / np.float32(127.0), np.float32(1e-45))
+        groups[g, 0] = peak if rng.integers(2) else -peak
+        for r in range(1, 32):
+            x = np.float32((rng.integers(-127, 127) + 0.5) * np.float64(s))
+            for _ in range(abs(step := int(rng.integers(-3, 4)))):
+                x = np.nextafter(x, np.float32(np.inf if step > 0 else -np.inf), dtype=np.float32)
+            groups[g, r] = np.clip(x, -peak, peak)
+    return torch.from_numpy(groups)
+
+
+def test_mm_from_float_codes_at_half_integer_quotients(hip_device):
+    """The fused quantizers divide by multiplying with the group's reciprocal and fall back to
+    the division near half-integer quotients: codes and scales equal the oracle's (torch's
+    true division) on operands built from ties and their ulp neighbours."""
+    cfg = ideal(**CONFIG2)
+    n, k, o = 64, 512, 128
+    a = near_half_integer_groups(n * k // 32, 5).reshape(n, k)
+    b = near_half_integer_groups(k * o // 32, 6).reshape(o, k // 32, 32).permute(1, 2, 0)
+    b = b.reshape(k, o).contiguous()          # column groups of 32 rows
+    assert hip.from_float_applies(cfg, n, k, o)
+    q, xscale, (packed, _, wscale), _ = hip.mm_from_float(a.to(hip_device), b.to(hip_device), cfg)
+    q_ref, xs_ref = oracle.input_tiles(a, cfg)
+    packed_ref, ws_ref = oracle.weight_tiles(b.T, cfg)
+    assert bits_equal(q, q_ref)
+    assert bits_equal(xscale.reshape(xs_ref.shape), xs_ref)
+    assert bits_equal(packed, packed_ref)
+    assert bits_equal(wscale.reshape(ws_ref.shape), ws_ref)
+
+
 def test_mm_from_float_operand_forms(hip_device):
     """Simulator.mm on the two-launch route with half-precision operands, a transposed B
     (an nn.Linear weight read as W.T) and a sliced A: the oracle's result in A's dtype."""
