@@ -52,7 +52,7 @@ __device__ __forceinline__ Phys cell_conductance(const mf_config &cfg, u32 code,
     const int mask = cfg.w_mask[w];
     const int digit = int((code >> cfg.w_shift[w]) & u32(mask));
     Phys raw = nominal_level<Phys>(cfg, digit, mask);
-    if (cfg.has_write) raw = raw * Phys(expf(cfg.f_write * normal(cell, seed, 10u, cfg.f_two_pi)));
+    if (cfg.has_write) raw = raw * Phys(exp_small(cfg.f_write * normal_fast(cell, seed, 10u)));
     raw = raw * drift_of<Phys>(cfg);
     if (cfg.has_saf) {
         const float u = uniform(cell, seed, 30u);
@@ -60,7 +60,7 @@ __device__ __forceinline__ Phys cell_conductance(const mf_config &cfg, u32 code,
         else if (u < cfg.f_saf_band) raw = high_of<Phys>(cfg);
     }
     if (cfg.read_mode == MF_READ_SHARED && cfg.has_read)
-        raw = raw * Phys(expf(cfg.f_read * normal(cell, read_seed, 20u, cfg.f_two_pi)));
+        raw = raw * Phys(exp_small(cfg.f_read * normal_fast(cell, read_seed, 20u)));
     return raw;
 }
 

@@ -99,8 +99,7 @@ __global__ __launch_bounds__(256) void k_split_conductances(const mf_config cfg,
                     }
                     if (plan.planes > 1 && !plan.out_noise) {
                         const u64 address = cells[j] * u64(cfg.n_in) + u64(plane);
-                        g_read = g_read * expf(cfg.f_read * normal(address, read_seed, 20u,
-                                                                    cfg.f_two_pi));
+                        g_read = g_read * exp_small(cfg.f_read * normal_fast(address, read_seed, 20u));
                     }
                     const float delta = (g_read - cfg.f_low) * plan.k1[w];   // ADC counts per digit
                     const _Float16 hi = static_cast<_Float16>(delta);         // round to nearest even
@@ -180,7 +179,7 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
             if (digit) {
                 const i64 k = k0 + j, i = k / R, r = k - i * R;
                 const u64 address = u64(((v * m + i) * A + a) * R + r);
-                const float z = normal(address, read_seed, 40u, cfg.f_two_pi);
+                const float z = normal_fast(address, read_seed, 40u);
                 x = float(digit) * (1.0f + cfg.f_vnoise * z);
             }
             const _Float16 hi = static_cast<_Float16>(x);
@@ -194,14 +193,9 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
     }
 }
 
-// The normals of normal() at the addresses base + offset (offset < 2^31) for one stream
-// pair, at a few instructions each:
-// * the high-word folds of both streams are computed once for base's high word, and again
-//   only in a lane whose low word carries;
-// * log2 (v_log_f32), cos(2*pi*v) with v in revolutions (v_cos_f32) and sqrt (v_sqrt_f32)
-//   are one instruction each.  Over every uniform value (k + 0.5) / 2^24 they stay within
-//   1.2e-7 relative (log2) and 1.3e-7 absolute (cos), and sqrt(-2 ln u) within 4.8e-7
-//   absolute of the exact value (OCML's sqrtf(-2 logf(u)): 5.9e-7).
+// normal_fast() at the addresses base + offset (offset < 2^31) for one stream pair: the
+// high-word folds of both streams are computed once for base's high word, and again only in
+// a lane whose low word carries.
 struct NormalRun {
     u32 lo, hi, fold_u, fold_v;
     __device__ __forceinline__ NormalRun(u64 base, u64 seed, u32 stream)
@@ -214,10 +208,7 @@ struct NormalRun {
             fu = uniform_fold(hi + 1u, seed, stream);
             fv = uniform_fold(hi + 1u, seed, stream + 1u);
         }
-        const float u = uniform_finish(low, fu), v = uniform_finish(low, fv);
-        // -2 ln u = -2 ln(2) log2(u).
-        return __builtin_amdgcn_sqrtf(-1.38629436f * __builtin_amdgcn_logf(u)) *
-               __builtin_amdgcn_cosf(v);
+        return box_muller(uniform_finish(low, fu), uniform_finish(low, fv));
     }
 };
 
