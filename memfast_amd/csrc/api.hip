@@ -933,8 +933,8 @@ int mf_conv_input_tiles_wide(const mf_config *cfg, const double *x, const mf_con
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (fixed_scale) {
         hipLaunchKernelGGL(k_conv_codes_f64, dim3(grid_for(rows * kp)), dim3(256), 0, s, x, g, K,
-                           kp, fixed_scale, i64(1), i64(1), K, 1, lower, upper, mask, q, status,
-                           u32(MF_STATUS_INPUT));
+                           kp, fixed_scale, i64(1), i64(1), K, 1, lower, upper, mask, 0, q,
+                           status, u32(MF_STATUS_INPUT));
         hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s,
                            rows, K, m * Gr, R, P, Gr, fixed_scale, i64(1), i64(1), K, 1, xscale);
         return check_launch("wide conv input tiles");
@@ -948,10 +948,12 @@ int mf_conv_input_tiles_wide(const mf_config *cfg, const double *x, const mf_con
                        reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
     hipLaunchKernelGGL(k_conv_group_max_f64, dim3(grid_for(rows * K)), dim3(256), 0, s, x, g, K,
                        gr, gc, ncg, work, status, u32(MF_STATUS_INPUT));
+    const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
-                       nrg * ncg, bits, cfg->bw_e, upper, scale);
+                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
     hipLaunchKernelGGL(k_conv_codes_f64, dim3(grid_for(rows * kp)), dim3(256), 0, s, x, g, K, kp,
-                       scale, gr, gc, ncg, 0, lower, upper, mask, q, status, u32(MF_STATUS_INPUT));
+                       scale, gr, gc, ncg, 0, lower, upper, mask, narrow, q, status,
+                       u32(MF_STATUS_INPUT));
     hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(rows * m * Gr)), dim3(256), 0, s, rows,
                        K, m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
     return check_launch("wide conv input tiles");
@@ -1728,10 +1730,11 @@ int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, in
     hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(2 * nrg * ncg)), dim3(256), 0, s,
                        reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
     launch_group_max_f64(x, n, k, ld, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT), s);
+    const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
-                       nrg * ncg, bits, cfg->bw_e, upper, scale);
+                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
     hipLaunchKernelGGL(k_input_codes_f64, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
-                       scale, gr, gc, ncg, 0, lower, upper, mask, q);
+                       scale, gr, gc, ncg, 0, lower, upper, mask, narrow, q);
     hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
                        m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
     return check_launch("wide input quantization");
@@ -1751,7 +1754,7 @@ int mf_input_tiles_wide(const mf_config *cfg, const double *x, int64_t n, int64_
     const u64 mask = (u64(1) << bits) - 1;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(k_input_codes_f64, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
-                       scale, i64(1), i64(1), k, 1, lower, upper, mask, q);
+                       scale, i64(1), i64(1), k, 1, lower, upper, mask, 0, q);
     hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
                        m * Gr, R, P, Gr, scale, i64(1), i64(1), k, 1, xscale);
     return check_launch("wide input tiles");
@@ -1780,10 +1783,11 @@ int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, i
     hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(2 * nrg * ncg)), dim3(256), 0, s,
                        reinterpret_cast<u32 *>(work), 2 * nrg * ncg, 0u);
     launch_group_max_f64(b, k, o, ld, gr, gc, ncg, work, status, u32(MF_STATUS_WEIGHT), s);
+    const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
-                       nrg * ncg, bits, cfg->bw_e, upper, scale);
+                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
     hipLaunchKernelGGL(k_weight_codes_f64, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o, ld, R,
-                       C, m, p, scale, gr, gc, ncg, lower, upper, mask, packed, packed32);
+                       C, m, p, scale, gr, gc, ncg, lower, upper, mask, narrow, packed, packed32);
     hipLaunchKernelGGL(k_weight_scales_f64, dim3(grid_for(m * Gr * op)), dim3(256), 0, s, k, o,
                        m * Gr, op, R, P, Gr, scale, gr, gc, ncg, wscale);
     return check_launch("wide weight quantization");

@@ -303,8 +303,8 @@ __global__ void k_conv_group_max_f64(const double *x, const mf_conv_geometry g, 
                                      i64 gc, i64 ncg, u64 *work, u32 *status, u32 flag);
 __global__ void k_conv_codes_f64(const double *x, const mf_conv_geometry g, i64 K, i64 kp,
                                  const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
-                                 double lower, double upper, u64 mask, u32 *q, u32 *status,
-                                 u32 flag);
+                                 double lower, double upper, u64 mask, int narrow, u32 *q,
+                                 u32 *status, u32 flag);
 constexpr int CONV_CHUNK_COLS = 128;   // patch columns per k_conv_codes block
 __global__ void k_conv_codes(const float *x, const mf_conv_geometry g, i64 K, i64 kp,
                              const float *scale, i64 gr, i64 gc, i64 ncg, float lower, float upper,
@@ -337,14 +337,16 @@ template <typename T, typename U>
 __global__ void k_row_group_max(const T *x, i64 rows, i64 cols, i64 ld, i64 gc, i64 ncg, U *work,
                                 u32 *status, u32 flag);
 constexpr int ROW_CHUNK_COLS = 1024;  // columns per k_row_group_max wave
+// `narrow`: an INT operand of at most 8 bits in a wide configuration, quantized in FP32 as
+// the reference does (its dtype follows the operand's own width).
 __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
-                                  double *scale);
+                                  int narrow, double *scale);
 __global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
                                   const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
-                                  double lower, double upper, u64 mask, u32 *q);
+                                  double lower, double upper, u64 mask, int narrow, u32 *q);
 __global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
                                    i64 p, const double *scale, i64 gr, i64 gc, i64 ncg,
-                                   double lower, double upper, u64 mask, i64 *packed,
+                                   double lower, double upper, u64 mask, int narrow, i64 *packed,
                                    u32 *packed32);
 __global__ void k_input_scales_f64(i64 n, i64 k, i64 groups, int R, int P, int Gr,
                                    const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,

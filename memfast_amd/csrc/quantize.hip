@@ -1224,13 +1224,18 @@ __device__ __forceinline__ int floor_log2_rounded(double x) {
 // INT: scale = (max > 0 ? max : 1) / upper, at least the smallest FP64
 // subnormal.  BFP (bw_e > 0): e = clamp(floor(log2(max(max, DBL_MIN))),
 // 1 - L, L) with L = 2^(bw_e-1) - 1, scale = 2^(e + 2 - bits).
+// `narrow`: an INT operand of at most 8 bits in a wide configuration, which the reference
+// quantizes in FP32 (memfast/quantization.py:9-31 picks the dtype per operand): the FP32
+// scale of the FP32 peak, stored exactly as a double.
 __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
-                                  double *scale) {
+                                  int narrow, double *scale) {
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < groups;
          i += i64(gridDim.x) * blockDim.x) {
         const double peak = __longlong_as_double(static_cast<long long>(work[i]));
         double s;
-        if (bw_e) {
+        if (narrow && !bw_e) {
+            s = double(group_scale(float(peak), float(upper)));
+        } else if (bw_e) {
             const int limit = (1 << (bw_e - 1)) - 1;
             int e = floor_log2_rounded(peak > DBL_MIN ? peak : DBL_MIN);
             e = e < 1 - limit ? 1 - limit : (e > limit ? limit : e);
@@ -1244,8 +1249,10 @@ __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_
     }
 }
 
+// `narrow`: the FP32 code of the FP32 value and scale (see k_group_scale_f64).
 __device__ __forceinline__ u32 quantize_code_f64(double x, double s, double lower, double upper,
-                                                 u64 mask) {
+                                                 u64 mask, int narrow) {
+    if (narrow) return quantize_code(float(x), float(s), float(lower), float(upper), u32(mask));
     double c = rint(x / s);
     c = c < lower ? lower : c;
     c = c > upper ? upper : c;
@@ -1255,7 +1262,7 @@ __device__ __forceinline__ u32 quantize_code_f64(double x, double s, double lowe
 // q [n, kp] u32 codes; `scale` is the group grid, or a [k] row when fixed.
 __global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
                                   const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
-                                  double lower, double upper, u64 mask, u32 *q) {
+                                  double lower, double upper, u64 mask, int narrow, u32 *q) {
     const i64 total = n * kp;
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += i64(gridDim.x) * blockDim.x) {
@@ -1263,7 +1270,7 @@ __global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
         u32 code = 0;
         if (col < k) {
             const double s = fixed ? scale[col] : scale[(row / gr) * ncg + col / gc];
-            code = quantize_code_f64(x[row * ld + col], s, lower, upper, mask);
+            code = quantize_code_f64(x[row * ld + col], s, lower, upper, mask, narrow);
         }
         q[i] = code;
     }
@@ -1272,7 +1279,7 @@ __global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
 // packed [m, p, R, C] as int64 (the checkpoint layout) and u32 (kernel copy).
 __global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
                                    i64 p, const double *scale, i64 gr, i64 gc, i64 ncg,
-                                   double lower, double upper, u64 mask, i64 *packed,
+                                   double lower, double upper, u64 mask, int narrow, i64 *packed,
                                    u32 *packed32) {
     const i64 kp = m * R, op = p * C;
     const i64 total = kp * op;
@@ -1287,7 +1294,7 @@ __global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R,
         u32 code = 0;
         if (row < k && col < o)
             code = quantize_code_f64(b[row * ld + col], scale[(row / gr) * ncg + col / gc], lower,
-                                     upper, mask);
+                                     upper, mask, narrow);
         packed[idx] = i64(code);
         packed32[idx] = code;
     }
@@ -1364,8 +1371,8 @@ __global__ void k_conv_group_max_f64(const double *x, const mf_conv_geometry g, 
 // fixed per-column scale [K] (`fixed`); a non-finite gathered value sets `flag`.
 __global__ void k_conv_codes_f64(const double *x, const mf_conv_geometry g, i64 K, i64 kp,
                                  const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
-                                 double lower, double upper, u64 mask, u32 *q, u32 *status,
-                                 u32 flag) {
+                                 double lower, double upper, u64 mask, int narrow, u32 *q,
+                                 u32 *status, u32 flag) {
     const i64 rows = g.n * g.out_height * g.out_width;
     bool finite = true;
     for (i64 e = i64(blockIdx.x) * blockDim.x + threadIdx.x; e < rows * kp;
@@ -1376,7 +1383,7 @@ __global__ void k_conv_codes_f64(const double *x, const mf_conv_geometry g, i64 
             const double v = conv_value_f64(x, g, row, col);
             finite = finite && fabs(v) <= DBL_MAX;
             const double s = fixed ? scale[col] : scale[(row / gr) * ncg + col / gc];
-            code = quantize_code_f64(v, s, lower, upper, mask);
+            code = quantize_code_f64(v, s, lower, upper, mask, narrow);
         }
         q[e] = code;
     }

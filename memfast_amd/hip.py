@@ -405,7 +405,9 @@ def input_error(config, fixed_scale=None):
     grouped scales, :124-125 for fixed scales)."""
     if fixed_scale is not None:
         return "quantized values must be finite"
-    return f"quantized values must be finite in {torch.float64 if config.wide else torch.float32}"
+    # The dtype follows the operand's own width (quantization.py:11).
+    wide = config.activation_bits > 8 or config.bw_e is not None
+    return f"quantized values must be finite in {torch.float64 if wide else torch.float32}"
 
 
 def input_tiles(value, config, fixed_scale=None, *, status=None):
@@ -601,7 +603,10 @@ def _weight_tiles_wide(weight, config, status):
     o, k = weight.shape
     b = weight.detach().T.to(torch.float64).contiguous()  # [K, O]
     if status is None and not torch.isfinite(b).all():
-        raise ValueError("quantized values must be finite in torch.float64")
+        # The reference quantizes an INT operand of at most 8 bits in FP32 (per operand).
+        narrow = config.weight_bits <= 8 and config.bw_e is None
+        raise ValueError("quantized values must be finite in "
+                         f"torch.float{32 if narrow else 64}")
     if not config.weight_signed and (b < 0).any():
         raise ValueError(
             "unsigned floating weights must be nonnegative INT values; "

@@ -1031,6 +1031,42 @@ def test_wide_group_quantizers_bit_exact(hip_device, wgran, igran):
     assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
 
 
+# Wide configurations with an INT operand of at most 8 bits: the reference quantizes each
+# operand in its own dtype (FP32 up to 8 bits without BFP), so that operand's scales and
+# codes are FP32 results even though the configuration restores in FP64.
+MIXED_WIDTHS = [dict(activation_bits=16, weight_bits=4, weight_slice=(1, 1, 2)),
+                dict(activation_bits=12, weight_bits=6),
+                dict(activation_bits=8, weight_bits=12, input_slice=(1, 1, 2, 2, 2))]
+
+
+@pytest.mark.parametrize("widths", MIXED_WIDTHS, ids=["a16w4", "a12w6", "a8w12"])
+def test_mixed_width_operands_quantize_in_their_own_dtype(hip_device, widths):
+    from memfast_amd import Simulator
+
+    cfg = Config(**widths, array_size=(64, 32), rows_per_read=32, adc_bits=6,
+                 weight_quant_gran=(32, 1), input_quant_gran=(1, 32),
+                 nonidealities=Nonidealities(write_variation=0.0))
+    assert cfg.wide
+    gen = torch.Generator().manual_seed(46)
+    a = torch.randn(24, 200, generator=gen)
+    b = torch.randn(200, 70, generator=gen)
+    # 8-bit inputs: quotients on and next to half-integers of their group's FP32 scale
+    # (without the groups of huge peaks, whose products overflow FP32).
+    groups = near_half_integer_groups(24, 7)
+    groups[3::4] = groups[1::4]
+    a[:, :32] = groups
+    q, xs = hip.input_tiles(a.to(hip_device), cfg)
+    packed, _, ws = hip.weight_tiles(b.T.to(hip_device), cfg)
+    q_ref, xs_ref = oracle.input_tiles(a, cfg)
+    packed_ref, ws_ref = oracle.weight_tiles(b.T, cfg)
+    mask = (1 << cfg.activation_bits) - 1
+    assert bits_equal(q.cpu().to(torch.int64) & mask, q_ref & mask)
+    assert bits_equal(xs, xs_ref)
+    assert bits_equal(packed, packed_ref) and bits_equal(ws, ws_ref)
+    got = Simulator(cfg, device=hip_device).mm(a.to(hip_device), b.to(hip_device))
+    assert bits_equal(got, oracle.mm(a, b, cfg))
+
+
 # Narrow (FP32) group quantizers: whole-column and whole-matrix groups, groups that straddle
 # the kernels' 256-row chunks, and 2-D groups (the row-first reduction path).
 NARROW_GROUPS = [((None, 1), (1, None)), ((192, 1), (None, 64)), ((320, 3), (None, None)),

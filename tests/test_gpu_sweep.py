@@ -1,0 +1,119 @@
+"""Seeded sweep over configurations: Simulator.mm on the GPU against the oracle.
+
+Each case draws a valid Config (bit widths, slicings, BFP exponents, array shapes, rows
+per read, quantization groups, ADC widths and, for the noisy half, device effects) and
+operand shapes that are not multiples of the arrays, then checks the product as the
+other parity tests do: bit for bit with ideal devices, flip-aware with device noise
+(``tests/parity.py``).  The draws cover every read kernel (``hip.mm_kernel``); the CPU
+test checks that the generator reaches them all without a GPU.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from memfast_amd import Config, Nonidealities, hip
+from parity import check_product, say
+
+CASES = 24
+
+
+def _slices(rng, bits, signed=True):
+    """None (binary slices) or MSB-first widths summing to ``bits`` (a one-bit sign slice
+    first when signed)."""
+    if rng.random() < 0.2:
+        return None
+    widths = [1] if signed else []
+    left = bits - sum(widths)
+    while left > 0:
+        width = int(min(left, rng.integers(1, 5)))
+        widths.append(width)
+        left -= width
+    return tuple(widths)
+
+
+def _config(rng, noisy):
+    """A valid Config drawn from ``rng`` (redrawn until the constructor accepts it)."""
+    while True:
+        rows = int(rng.choice([32, 64, 128]))
+        cols = int(rng.choice([16, 32, 64]))
+        read_rows = int(rng.choice([d for d in (16, 32, 64, rows) if d <= rows and rows % d == 0]))
+        wide = rng.random() < 0.2
+        abits = int(rng.choice([12, 16])) if wide else int(rng.choice([4, 6, 8]))
+        wbits = int(rng.choice([4, 6, 8]))
+        bw_e = int(rng.integers(3, 9)) if wide and rng.random() < 0.5 else None
+        wslice = _slices(rng, wbits)
+        n_w = len(wslice) if wslice is not None else wbits
+        adc = (tuple(int(rng.integers(4, 10)) for _ in range(n_w)) if rng.random() < 0.5
+               else int(rng.integers(4, 10)))
+        wgran = [(None, 1), (read_rows, 1), (None, None), (rows, 1)][int(rng.integers(4))]
+        igran = [(1, None), (1, read_rows), (None, None), (1, rows)][int(rng.integers(4))]
+        effects = dict(write_variation=0.0)
+        if noisy:
+            effects = dict(write_variation=float(rng.choice([0.01, 0.03])))
+            kind = int(rng.integers(6))
+            if kind == 1:
+                effects.update(read_variation=0.01, adc_nonlinearity=0.1)
+            elif kind == 2:
+                effects.update(read_variation=0.02, read_mode="slice_pair")
+            elif kind == 3:
+                effects.update(read_variation=0.02, read_mode="output")
+            elif kind == 4:
+                effects.update(voltage_variation=0.02)
+            elif kind == 5:
+                effects.update(stuck_at_low=0.02, stuck_at_high=0.01, drift_coefficient=0.05,
+                               drift_time=100.0)
+        try:
+            return Config(activation_bits=abits, weight_bits=wbits,
+                          input_slice=_slices(rng, abits), weight_slice=wslice, bw_e=bw_e,
+                          array_size=(rows, cols), rows_per_read=read_rows,
+                          weight_quant_gran=wgran, input_quant_gran=igran, adc_bits=adc,
+                          seed=int(rng.integers(0, 2**32)),
+                          nonidealities=Nonidealities(**effects))
+        except ValueError:
+            continue
+
+
+def _case(index, noisy):
+    rng = np.random.default_rng(1000 * int(noisy) + index)
+    cfg = _config(rng, noisy)
+    rows, cols = cfg.array_size
+    n = int(rng.integers(1, 25))
+    k = int(rng.integers(1, 3 * rows + 1))
+    o = int(rng.integers(1, 2 * cols + 6))
+    gen = torch.Generator().manual_seed(index)
+    a = torch.randn(n, k, generator=gen)
+    b = torch.randn(k, o, generator=gen)
+    if rng.random() < 0.25:
+        a = a.relu()
+    return cfg, a, b
+
+
+def _kernel(cfg, n, k, o):
+    rows, cols = cfg.array_size
+    return hip.mm_kernel(cfg, n, -(-k // rows), -(-o // cols))
+
+
+def test_sweep_reaches_every_read_kernel():
+    """The draws cover the general kernel and both MFMA reads with noise, and the ideal
+    MFMA read (at the shapes the product runs them)."""
+    kinds = set()
+    for noisy in (False, True):
+        for index in range(CASES):
+            cfg, a, b = _case(index, noisy)
+            kinds.add(_kernel(cfg, a.shape[0], a.shape[1], b.shape[1]))
+    assert {0, 1, 2, 3} <= kinds, kinds
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("noisy", [False, True], ids=["ideal", "noisy"])
+@pytest.mark.parametrize("index", range(CASES))
+def test_sweep_product_matches_oracle(hip_device, index, noisy):
+    from memfast_amd import Simulator
+
+    cfg, a, b = _case(index, noisy)
+    say("sweep", "noisy" if noisy else "ideal", index, tuple(a.shape), tuple(b.shape),
+        "kernel", _kernel(cfg, a.shape[0], a.shape[1], b.shape[1]), cfg)
+    sim = Simulator(cfg, device=hip_device)
+    got = sim.mm(a.to(hip_device), b.to(hip_device))
+    check_product(cfg, got, a, b, hip_device, label=f"sweep {index}")
