@@ -1,8 +1,9 @@
 """Seeded sweep over configurations: Simulator.mm on the GPU against the oracle.
 
-Each case draws a valid Config (bit widths, slicings, BFP exponents, array shapes, rows
-per read, quantization groups, ADC widths and, for the noisy half, device effects) and
-operand shapes that are not multiples of the arrays, then checks the product as the
+Each case draws a valid Config (bit widths, slicings, BFP exponents, signed or unsigned
+weights, array shapes, rows per read, quantization groups, ADC widths and, for the noisy
+half, device effects) and operand shapes that are not multiples of the arrays (up to 150
+vectors), then checks the product as the
 other parity tests do: bit for bit with ideal devices, flip-aware with device noise
 (``tests/parity.py``).  The draws cover every read kernel (``hip.mm_kernel``); the CPU
 test checks that the generator reaches them all without a GPU.
@@ -42,7 +43,8 @@ def _config(rng, noisy):
         abits = int(rng.choice([12, 16])) if wide else int(rng.choice([4, 6, 8]))
         wbits = int(rng.choice([4, 6, 8]))
         bw_e = int(rng.integers(3, 9)) if wide and rng.random() < 0.5 else None
-        wslice = _slices(rng, wbits)
+        signed = bw_e is not None or rng.random() < 0.85
+        wslice = _slices(rng, wbits, signed)
         n_w = len(wslice) if wslice is not None else wbits
         adc = (tuple(int(rng.integers(4, 10)) for _ in range(n_w)) if rng.random() < 0.5
                else int(rng.integers(4, 10)))
@@ -68,7 +70,7 @@ def _config(rng, noisy):
                           input_slice=_slices(rng, abits), weight_slice=wslice, bw_e=bw_e,
                           array_size=(rows, cols), rows_per_read=read_rows,
                           weight_quant_gran=wgran, input_quant_gran=igran, adc_bits=adc,
-                          seed=int(rng.integers(0, 2**32)),
+                          seed=int(rng.integers(0, 2**32)), weight_signed=signed,
                           nonidealities=Nonidealities(**effects))
         except ValueError:
             continue
@@ -78,7 +80,7 @@ def _case(index, noisy):
     rng = np.random.default_rng(1000 * int(noisy) + index)
     cfg = _config(rng, noisy)
     rows, cols = cfg.array_size
-    n = int(rng.integers(1, 25))
+    n = int(rng.integers(1, 25)) if rng.random() < 0.7 else int(rng.integers(25, 150))
     k = int(rng.integers(1, 3 * rows + 1))
     o = int(rng.integers(1, 2 * cols + 6))
     gen = torch.Generator().manual_seed(index)
@@ -86,6 +88,8 @@ def _case(index, noisy):
     b = torch.randn(k, o, generator=gen)
     if rng.random() < 0.25:
         a = a.relu()
+    if not cfg.weight_signed:
+        b = b.abs()   # unsigned weights are nonnegative INT values
     return cfg, a, b
 
 
