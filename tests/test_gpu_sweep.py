@@ -121,3 +121,57 @@ def test_sweep_product_matches_oracle(hip_device, index, noisy):
     sim = Simulator(cfg, device=hip_device)
     got = sim.mm(a.to(hip_device), b.to(hip_device))
     check_product(cfg, got, a, b, hip_device, label=f"sweep {index}")
+
+
+CONV_CASES = 8
+
+
+def _conv(index, noisy):
+    """A drawn configuration with a Conv2d geometry (kernel, stride, padding, dilation,
+    groups) and its input."""
+    rng = np.random.default_rng(5000 + 1000 * int(noisy) + index)
+    cfg = _config(rng, noisy)
+    groups = int(rng.choice([1, 1, 2]))
+    channels = groups * int(rng.integers(1, 5))
+    out_channels = groups * int(rng.integers(1, 4))
+    kernel = (int(rng.integers(1, 5)), int(rng.integers(1, 5)))
+    stride = (int(rng.integers(1, 3)), int(rng.integers(1, 3)))
+    padding = (int(rng.integers(0, 3)), int(rng.integers(0, 3)))
+    dilation = (int(rng.integers(1, 3)), int(rng.integers(1, 3)))
+    size = (int(rng.integers(8, 14)), int(rng.integers(8, 14)))
+    torch.manual_seed(index)
+    source = torch.nn.Conv2d(channels, out_channels, kernel, stride, padding, dilation, groups)
+    if not cfg.weight_signed:
+        with torch.no_grad():
+            source.weight.abs_()
+    x = torch.randn(int(rng.integers(1, 4)), channels, *size)
+    return cfg, source, x
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("noisy", [False, True], ids=["ideal", "noisy"])
+@pytest.mark.parametrize("index", range(CONV_CASES))
+def test_sweep_conv2d_matches_oracle(hip_device, index, noisy):
+    """AnalogConv2d (implicit im2col where it applies) against the oracle's read of
+    F.unfold's patch matrix, group by group."""
+    from torch.nn import functional as F
+
+    from memfast_amd import Simulator
+    from memfast_amd.nn import AnalogConv2d
+
+    cfg, source, x = _conv(index, noisy)
+    say("conv sweep", "noisy" if noisy else "ideal", index, source, tuple(x.shape), cfg)
+    layer = AnalogConv2d(source.to(hip_device), Simulator(cfg, device=hip_device), name="conv")
+    got = layer(x.to(hip_device))
+    source = source.cpu()
+    patches = F.unfold(x, source.kernel_size, source.dilation, source.padding, source.stride)
+    groups, out_channels = source.groups, source.out_channels
+    size = source.in_channels // groups * source.kernel_size[0] * source.kernel_size[1]
+    per_group = out_channels // groups
+    rows = got.flatten(2).transpose(1, 2)            # [N, L, out_channels]
+    for g in range(groups):
+        block = slice(g * per_group, (g + 1) * per_group)
+        check_product(cfg, rows[:, :, block],
+                      patches[:, g * size:(g + 1) * size].transpose(1, 2),
+                      source.weight[block].flatten(1).T, hip_device, name=f"conv.group{g}",
+                      bias=source.bias[block], label=f"conv sweep {index} group {g}")
