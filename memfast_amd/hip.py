@@ -1112,9 +1112,10 @@ def mm_from_float(x, b, config, *, status=None, variant=0, workspace=None, scrat
     return q, xscale, (packed, packed_t, wscale), out
 
 
+@lru_cache(maxsize=4096)
 def mm_kernel(config, n, m, p, has_packed_t=True):
     """0: general kernel, 1: ideal-device MFMA, 2: noisy-device MFMA, 3: noisy-device MFMA for
-    wide codes (what ``mm`` launches).
+    wide codes (what ``mm`` launches; a function of its arguments, cached).
 
     The kernels other than the general one read ``kernel_codes`` of the program."""
     out = ct.c_int32()
