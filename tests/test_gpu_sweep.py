@@ -175,3 +175,39 @@ def test_sweep_conv2d_matches_oracle(hip_device, index, noisy):
                       patches[:, g * size:(g + 1) * size].transpose(1, 2),
                       source.weight[block].flatten(1).T, hip_device, name=f"conv.group{g}",
                       bias=source.bias[block], label=f"conv sweep {index} group {g}")
+
+
+FIXED_CASES = 16
+
+
+def _fixed(index):
+    """A drawn configuration, inputs and a fixed per-feature input scale; a quarter of the
+    inputs sit on or next to half-integer quotients of their scale."""
+    rng = np.random.default_rng(9000 + index)
+    cfg = _config(rng, False)
+    n, k = int(rng.integers(1, 40)), int(rng.integers(1, 3 * cfg.array_size[0] + 1))
+    scale = torch.from_numpy(np.exp(rng.uniform(-6.0, 2.0, (1, k))).astype(np.float32))
+    gen = torch.Generator().manual_seed(index)
+    x = torch.randn(n, k, generator=gen) * 4.0
+    limit = 1 << (cfg.activation_bits - 1)
+    ties = torch.from_numpy(rng.integers(-limit - 1, limit + 1, (n, k)).astype(np.float64) + 0.5)
+    near = (ties * scale.double()).float()
+    pick = torch.from_numpy(rng.random((n, k)) < 0.25)
+    x = torch.where(pick, near, x)
+    return cfg, x, scale
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("index", range(FIXED_CASES))
+def test_sweep_fixed_scale_input_tiles(hip_device, index):
+    """Input codes and per-read scales with a fixed (calibrated) per-feature scale, narrow
+    and wide configurations, bit for bit against the oracle (codes past the range clamp)."""
+    from oracle import oracle
+
+    cfg, x, scale = _fixed(index)
+    say("fixed-scale sweep", index, tuple(x.shape), cfg)
+    q, xs = hip.input_tiles(x.to(hip_device), cfg, scale.to(hip_device))
+    q_ref, xs_ref = oracle.input_tiles(x, cfg, scale)
+    mask = (1 << cfg.activation_bits) - 1
+    assert torch.equal(q.cpu().to(torch.int64) & mask, q_ref.to(torch.int64) & mask)
+    assert torch.equal(xs.cpu(), xs_ref)
