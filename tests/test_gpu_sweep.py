@@ -211,3 +211,21 @@ def test_sweep_fixed_scale_input_tiles(hip_device, index):
     mask = (1 << cfg.activation_bits) - 1
     assert torch.equal(q.cpu().to(torch.int64) & mask, q_ref.to(torch.int64) & mask)
     assert torch.equal(xs.cpu(), xs_ref)
+
+
+TUNED_CASES = 8
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("noisy", [False, True], ids=["ideal", "noisy"])
+@pytest.mark.parametrize("index", range(TUNED_CASES))
+def test_sweep_tuned_product_matches_oracle(hip_device, tmp_path, index, noisy):
+    """Tuned mode (its schedule search, cache write and selected kernel) gives the product
+    default mode gives: the oracle's, as in test_sweep_product_matches_oracle."""
+    from memfast_amd import Simulator
+
+    cfg, a, b = _case(100 + index, noisy)
+    say("tuned sweep", "noisy" if noisy else "ideal", index, tuple(a.shape), tuple(b.shape), cfg)
+    sim = Simulator(cfg, mode="tuned", device=hip_device, cache_dir=tmp_path)
+    got = sim.mm(a.to(hip_device), b.to(hip_device))
+    check_product(cfg, got, a, b, hip_device, label=f"tuned sweep {index}")
