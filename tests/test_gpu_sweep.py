@@ -229,3 +229,34 @@ def test_sweep_tuned_product_matches_oracle(hip_device, tmp_path, index, noisy):
     sim = Simulator(cfg, mode="tuned", device=hip_device, cache_dir=tmp_path)
     got = sim.mm(a.to(hip_device), b.to(hip_device))
     check_product(cfg, got, a, b, hip_device, label=f"tuned sweep {index}")
+
+
+GRU_CASES = 6
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("noisy", [False, True], ids=["ideal", "noisy"])
+@pytest.mark.parametrize("index", range(GRU_CASES))
+def test_sweep_gru_sequence_matches_oracle_steps(hip_device, index, noisy):
+    """AnalogGRU over a sequence (the native sequence call where it applies) against its
+    steps recomputed from PyTorch's gate equations over oracle-checked reads."""
+    from memfast_amd import Simulator
+    from memfast_amd.nn import AnalogGRU
+    from parity import gru_step_parity
+
+    rng = np.random.default_rng(7000 + 1000 * int(noisy) + index)
+    cfg = _config(rng, noisy)
+    hidden = int(rng.choice([16, 48, 64]))
+    inputs = int(rng.integers(4, 41))
+    steps, batch = int(rng.integers(3, 6)), int(rng.integers(1, 5))
+    torch.manual_seed(index)
+    source = torch.nn.GRU(inputs, hidden, num_layers=1)
+    if not cfg.weight_signed:
+        with torch.no_grad():
+            for weight in (source.weight_ih_l0, source.weight_hh_l0):
+                weight.abs_()
+    x = torch.randn(steps, batch, inputs)
+    say("gru sweep", "noisy" if noisy else "ideal", index, source, tuple(x.shape), cfg)
+    layer = AnalogGRU(source.to(hip_device), Simulator(cfg, device=hip_device), name="gru")
+    output, _ = layer(x.to(hip_device))
+    gru_step_parity(layer.cells[0], source.cpu(), x, output, hip_device, label=f"gru sweep {index}")
