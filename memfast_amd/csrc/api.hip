@@ -432,7 +432,8 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
                  const float *xscale, i64 n, i64 m, const u8 *packed_t, const float *wscale, i64 p,
                  const float *g, u32 seed, u64 event, float *out, i64 ldo, void *workspace,
                  i64 bytes, int totals, u32 *status, hipStream_t s, bool reuse = false,
-                 i64 ocols = -1, i64 g_run = -1, int split_request = 0) {
+                 i64 ocols = -1, i64 g_run = -1, int split_request = 0,
+                 const float **split_totals = nullptr) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     if (ocols < 0) ocols = ncols;
     if (g_run < 0) g_run = G;
@@ -541,7 +542,10 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
             g_profile.pending.push_back(timing);
         }
     }
-    if (use_split)
+    // With split_totals the caller restores and sums a split read's totals [n, G, ncols]
+    // itself (null when the read wrote `out`).
+    if (split_totals) *split_totals = use_split ? partial : nullptr;
+    if (use_split && !split_totals)
         hipLaunchKernelGGL(k_restore_sum_f32, dim3(grid_for(n * ocols)), dim3(256), 0, s, partial, n,
                            G, g_run, ncols, ocols, xscale, wscale, ncols, out, ldo, level_power(G),
                            status);
@@ -1325,11 +1329,15 @@ static i64 reads_with_rows(const mf_config *cfg, i64 m, i64 k_rows) {
     return used < G ? used : G;
 }
 
-int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
-          const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
-          int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed, uint64_t event,
-          float *out, int64_t ldo, void *workspace, int64_t workspace_bytes, int32_t variant,
-          uint32_t *status, void *stream) {
+// mf_mm; with `split_totals` a noisy MFMA read split across blocks leaves its totals to the
+// caller (*split_totals, [n, G, p*C]) instead of restoring them into `out` (null otherwise).
+static int mm_read(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n,
+                   int64_t m, const uint8_t *packed, const uint8_t *packed_t, const float *wscale,
+                   int64_t p, int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed,
+                   uint64_t event, float *out, int64_t ldo, void *workspace,
+                   int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream,
+                   const float **split_totals) {
+    if (split_totals) *split_totals = nullptr;
     const int valid = check_narrow(cfg);
     if (valid) return valid;
     if (!q || !xscale || !packed || !wscale || !out || n < 1 || m < 1 || p < 1 ||
@@ -1380,7 +1388,7 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         return launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p, nullptr, seed,
                             event, out, ldo, workspace, workspace_bytes, 0, status, s,
                             (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run,
-                            variant_split(variant));
+                            variant_split(variant), split_totals);
     }
     if (!g && needs_conductances(cfg))
         return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
@@ -1413,6 +1421,15 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
         g_profile.pending.push_back(timing);
     }
     return launched;
+}
+
+int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n, int64_t m,
+          const uint8_t *packed, const uint8_t *packed_t, const float *wscale, int64_t p,
+          int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed, uint64_t event,
+          float *out, int64_t ldo, void *workspace, int64_t workspace_bytes, int32_t variant,
+          uint32_t *status, void *stream) {
+    return mm_read(cfg, q, xscale, n, m, packed, packed_t, wscale, p, out_cols, k_rows, g, seed,
+                   event, out, ldo, workspace, workspace_bytes, variant, status, stream, nullptr);
 }
 
 int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ldx,
@@ -1641,25 +1658,66 @@ int mf_gru_sequence(const mf_config *cfg, int64_t steps, int32_t reverse, int64_
     if (event0 > uint64_t(INT64_MAX) - uint64_t(steps))
         return fail(MF_E_INVALID, "read events of the sequence exceed the signed 64-bit range");
     hipStream_t s = static_cast<hipStream_t>(stream);
+    // With one input group per state row, each step after its read is one k_gru_step: the
+    // split read's restore and sum, the gates, and the next read's input codes.  Otherwise
+    // the step quantizes, reads (restoring its own totals) and runs k_gru_gates.
+    const i64 G = m * cfg->reads, ncols = p * cfg->cols;
+    const bool fused = (gr < batch ? gr : batch) == 1 && (gc < width ? gc : width) == width &&
+                       (scale != xscale || G == 1) && width <= 5120;   // 3H floats of LDS, under 64 KiB
     for (i64 i = 0; i < steps; ++i) {
         const i64 t = reverse ? steps - 1 - i : i;
         const float *hx = i == 0 ? h0 : out + (reverse ? t + 1 : t - 1) * out_step;
         const i64 ldx = i == 0 ? ld_h0 : out_row;
-        int rc = mf_quantize_inputs(cfg, hx, batch, width, ldx, gr, gc, work, scale, q, xscale,
+        int rc = MF_OK;
+        if (i == 0 || !fused) {
+            rc = mf_quantize_inputs(cfg, hx, batch, width, ldx, gr, gc, work, scale, q, xscale,
                                     status, stream);
-        if (rc) return rc;
+            if (rc) return rc;
+        }
         // The first read writes the program's event-independent conductance terms
         // into the workspace (unless the caller's variant says they are there);
         // later reads of the same program reuse them.
         const int32_t v = i == 0 ? variant : (variant | MF_MM_REUSE_TERMS);
-        rc = mf_mm(cfg, q, xscale, batch, m, packed, packed_t, wscale, p, 3 * width, width,
-                   nullptr, seed, event0 + uint64_t(i), hidden, ld_hidden, workspace,
-                   workspace_bytes, v, status, stream);
+        const float *totals = nullptr;
+        rc = mm_read(cfg, q, xscale, batch, m, packed, packed_t, wscale, p, 3 * width, width,
+                     nullptr, seed, event0 + uint64_t(i), hidden, ld_hidden, workspace,
+                     workspace_bytes, v, status, stream, fused ? &totals : nullptr);
         if (rc) return rc;
-        hipLaunchKernelGGL(k_gru_gates, dim3(grid_for(batch * width)), dim3(256), 0, s,
-                           projected + t * proj_step, proj_row, hidden, ld_hidden, hx, ldx,
-                           out + t * out_step, out_row, batch, width, bias, status,
-                           u32(MF_STATUS_OUTPUT));
+        if (fused) {
+            GruStepArgs a{};
+            a.inputs = projected + t * proj_step;
+            a.ldi = proj_row;
+            a.hidden = hidden;
+            a.ldh = ld_hidden;
+            a.totals = totals;
+            a.G = G;
+            a.g_run = reads_with_rows(cfg, m, width);
+            a.ldt = ncols;
+            a.lp = level_power(G);
+            a.xscale_in = xscale;
+            a.wscale = wscale;
+            a.ldws = ncols;
+            a.bias = bias;
+            a.hx = hx;
+            a.ldx = ldx;
+            a.out = out + t * out_step;
+            a.ldo = out_row;
+            a.width = width;
+            a.quantize = i + 1 < steps;
+            a.kp = m * cfg->rows;
+            a.upper = float((1 << (cfg->activation_bits - 1)) - 1);
+            a.mask = (1u << cfg->activation_bits) - 1u;
+            a.q = q;
+            a.scale = scale;
+            a.xscale_out = xscale;
+            a.status = status;
+            hipLaunchKernelGGL(k_gru_step, dim3(unsigned(batch)), dim3(1024), 3 * width * 4, s, a);
+        } else {
+            hipLaunchKernelGGL(k_gru_gates, dim3(grid_for(batch * width)), dim3(256), 0, s,
+                               projected + t * proj_step, proj_row, hidden, ld_hidden, hx, ldx,
+                               out + t * out_step, out_row, batch, width, bias, status,
+                               u32(MF_STATUS_OUTPUT));
+        }
         rc = check_launch("GRU sequence gates");
         if (rc) return rc;
     }

@@ -71,6 +71,23 @@ __device__ __forceinline__ float exp_small(float x) {
     return __builtin_amdgcn_exp2f(x * 1.44269504f);
 }
 
+// INT code of x in a group of scale s (memfast/quantization.py:41: round half to even,
+// clamp, two's complement masked to the code width), FP32 division as torch's.
+__device__ __forceinline__ u8 quantize_code(float x, float s, float lower, float upper,
+                                            u32 mask) {
+    float c = rintf(x / s);
+    c = c < lower ? lower : c;
+    c = c > upper ? upper : c;
+    return u8(u32(int(c)) & mask);
+}
+
+// scale of one group from its peak |x| (quantization.py:25-31 for INT codes).
+__device__ __forceinline__ float group_scale(float peak, float upper) {
+    float s = (peak > 0.0f ? peak : 1.0f) / upper;
+    const float tiny = __uint_as_float(1u);
+    return s < tiny ? tiny : s;
+}
+
 __host__ __device__ __forceinline__ u64 event_seed(u32 seed, u64 event) {
     return u64(seed ^ mix(u32(event))) | (u64(mix(u32(event >> 32))) << 32);
 }

@@ -259,6 +259,38 @@ __global__ void k_gru_gates(const float *inputs, i64 ldi, const float *hidden, i
                             const float *bias, u32 *status, u32 flag);
 __global__ void k_bias_add(float *out, i64 n, i64 o, i64 ldo, const float *bias, u32 *status,
                            u32 flag);
+
+// One GRU step after its hidden read (recurrent.hip): the read's restore and read-order sum
+// from split totals (or its fused output), the gate equations of k_gru_gates, and the
+// quantization of the new state for the next step's hidden read (row groups of the whole
+// state, as k_row_groups_wave writes them).  One workgroup of 1024 threads per batch row,
+// with 3H floats of dynamic LDS.
+struct GruStepArgs {
+    const float *inputs;        // projected inputs of the step [B, 3H] (row stride ldi)
+    i64 ldi;
+    const float *hidden;        // the hidden read's output [B, 3H] (when totals is null)
+    i64 ldh;
+    const float *totals;        // split read: integer totals [B, G, ldt]
+    i64 G, g_run, ldt;
+    int lp;                     // level power of the read-order cascade
+    const float *xscale_in;     // [B, G] scales of the read's input codes
+    const float *wscale;        // [G, ldws]
+    i64 ldws;
+    const float *bias;          // hidden projection bias [3H] or null
+    const float *hx;            // previous state [B, H]
+    i64 ldx;
+    float *out;                 // new state [B, H]
+    i64 ldo, width;
+    int quantize;               // 0: last step (no next read)
+    i64 kp;                     // code row length (>= H, zero past H)
+    float upper;
+    u32 mask;
+    u8 *q;                      // next codes [B, kp]
+    float *scale;               // group scale per row [B]
+    float *xscale_out;          // [B, G] per-read scales of the next read (may be xscale_in)
+    u32 *status;
+};
+__global__ void k_gru_step(const GruStepArgs a);
 __global__ void k_group_max(const float *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,
                             u32 *work, u32 *status, u32 flag);
 template <bool VEC>

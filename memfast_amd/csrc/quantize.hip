@@ -80,14 +80,6 @@ __global__ void k_group_scale(const u32 *work, i64 groups, float upper, float *s
     }
 }
 
-__device__ __forceinline__ u8 quantize_code(float x, float s, float lower, float upper,
-                                            u32 mask) {
-    float c = rintf(x / s);
-    c = c < lower ? lower : c;
-    c = c > upper ? upper : c;
-    return u8(u32(int(c)) & mask);
-}
-
 // quantize_code() for many values of one group at the cost of one division.  The
 // quotient is taken as q = x * y with y = RN(1/s): then |q - x/s| <= |x/s| * 2^-23 and the
 // reference's RN(x/s) is within |x/s| * 2^-24 of x/s, so for |x/s| <= 256 the two lie
@@ -110,13 +102,6 @@ struct GroupCodes {
         return u8(u32(int(c)) & mask);
     }
 };
-
-// scale of one group from its peak |x| (quantization.py:25-31 for INT codes).
-__device__ __forceinline__ float group_scale(float peak, float upper) {
-    float s = (peak > 0.0f ? peak : 1.0f) / upper;
-    const float tiny = __uint_as_float(1u);
-    return s < tiny ? tiny : s;
-}
 
 // Fused grouped quantization of row-local groups (gr == 1, the activation
 // layout): one thread per (row, group of gc columns) computes the group's peak,

@@ -46,4 +46,93 @@ __global__ __launch_bounds__(256) void k_gru_gates(const float *inputs, i64 ldi,
     if (!finite && status) atomicOr(status, flag);
 }
 
+// k_restore_sum_f32, k_gru_gates and k_row_groups_wave of one step in one launch, one
+// workgroup of 1024 threads per batch row, bit for bit their results:
+// 1. each hidden projection value is (float(T) * xs) * ws summed over the reads in torch's
+//    cascade order (Cascade<float>; loads issued a batch of reads at a time), or read from
+//    the fused read's output, into LDS (3H floats, dynamic shared memory);
+// 2. the gates as k_gru_gates (bias first; FP32 in PyTorch's order);
+// 3. the new state's row is one quantization group: its peak (fmaxf, NaN ignored) gives
+//    the scale, every read of the row gets it, codes past H are zero.
+// Flags: a non-finite hidden value (restore) or biased sum sets MF_STATUS_OUTPUT; a
+// non-finite new state sets MF_STATUS_INPUT when it is quantized.
+__global__ __launch_bounds__(1024) void k_gru_step(const GruStepArgs a) {
+    constexpr int BATCH = 8;
+    extern __shared__ float hid[];   // [3H]
+    __shared__ float wave_peak[16];
+    const i64 b = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const i64 H = a.width;
+    bool out_finite = true, state_finite = true;
+    for (i64 c = t; c < 3 * H; c += 1024) {
+        float v;
+        if (!a.totals) {
+            v = a.hidden[b * a.ldh + c];
+        } else {
+            Cascade<float> cascade;
+            cascade.reset();
+            const float *tv = a.totals + b * a.G * a.ldt + c;
+            const float *xv = a.xscale_in + b * a.G;
+            for (i64 g0 = 0; g0 < a.g_run; g0 += BATCH) {
+                float tt[BATCH], xs[BATCH], ws[BATCH];
+#pragma unroll
+                for (int j = 0; j < BATCH; ++j) {
+                    const i64 g = g0 + j < a.g_run ? g0 + j : a.g_run - 1;   // past the end: unused
+                    tt[j] = tv[g * a.ldt];
+                    xs[j] = xv[g];
+                    ws[j] = a.wscale[g * a.ldws + c];
+                }
+#pragma unroll
+                for (int j = 0; j < BATCH; ++j) {
+                    if (g0 + j < a.g_run) {
+                        float x = tt[j] * xs[j];
+                        x = x * ws[j];
+                        cascade.push(x, a.lp);
+                    }
+                }
+            }
+            v = cascade.finish();
+            out_finite = out_finite && fabsf(v) <= FLT_MAX;
+        }
+        if (a.bias) {
+            v = v + a.bias[c];
+            out_finite = out_finite && fabsf(v) <= FLT_MAX;
+        }
+        hid[c] = v;
+    }
+    if (!out_finite && a.status) atomicOr(a.status, u32(MF_STATUS_OUTPUT));
+    // Also orders this row's restore reads of xscale_in before the writes of xscale_out below.
+    __syncthreads();
+    const float *in = a.inputs + b * a.ldi;
+    float peak = 0.0f;
+    for (i64 c = t; c < H; c += 1024) {
+        const float r = gate_sigmoid(in[c] + hid[c]);
+        const float z = gate_sigmoid(in[H + c] + hid[H + c]);
+        const float rn = r * hid[2 * H + c];
+        const float cand = tanhf(in[2 * H + c] + rn);
+        const float keep = (1.0f - z) * cand;
+        const float carry = z * a.hx[b * a.ldx + c];
+        const float h = keep + carry;
+        a.out[b * a.ldo + c] = h;
+        hid[c] = h;   // only this thread reads it back below
+        const float mag = fabsf(h);
+        state_finite = state_finite && mag <= FLT_MAX;
+        peak = fmaxf(peak, mag);
+    }
+    if (!a.quantize) return;
+    for (int off = 1; off < 64; off <<= 1) peak = fmaxf(peak, __shfl_xor(peak, off, 64));
+    if (lane == 0) wave_peak[wave] = peak;
+    __syncthreads();
+    peak = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) peak = fmaxf(peak, wave_peak[w]);
+    const float s = group_scale(peak, a.upper);
+    if (t == 0) a.scale[b] = s;
+    for (i64 g = t; g < a.G; g += 1024) a.xscale_out[b * a.G + g] = s;
+    u8 *dst = a.q + b * a.kp;
+    for (i64 c = t; c < a.kp; c += 1024)
+        dst[c] = c < H ? quantize_code(hid[c], s, -a.upper, a.upper, a.mask) : u8(0);
+    if (!state_finite && a.status) atomicOr(a.status, u32(MF_STATUS_INPUT));
+}
+
 }  // namespace mf
