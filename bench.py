@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # 227.3 MiB read + 64.0 MiB written.  Summary and commands:
 # profiles/k_ideal_config2_pmc.md.  Only valid for the kernel sources it was
 # measured on (hash prefix below); otherwise the bench reports null.
-MEASURED_TRAFFIC = dict(kernels="1c4220b794bceff0", bytes=298352797)
+MEASURED_TRAFFIC = dict(kernels="4ae5c7b0020c4b5f", bytes=298468977)
 
 
 def cpu_model():
