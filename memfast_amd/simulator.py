@@ -381,7 +381,12 @@ class Simulator:
             resource = hip.program(c, schedule["vectors"], schedule["columns"],
                                    self.device.index).resources(
                 c, schedule["vectors"], schedule["columns"], schedule["workers"], kernel=kernel)
-        if resource["local_bytes"]:
+        # The output-noise MFMA read at 32-row reads keeps part of its state in scratch by
+        # design (three waves per SIMD with spills run faster than two without), and its
+        # registers do not depend on the schedule; the policy refuses any other spill.
+        n_read = c.nonidealities.read_variation > 0 and c.nonidealities.read_mode == "output"
+        deliberate = kernel == 2 and n_read and c.read_rows == 32
+        if resource["local_bytes"] and not deliberate:
             raise hip.ResourceError("register spill policy")
         return resource
 

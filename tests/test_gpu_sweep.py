@@ -213,7 +213,7 @@ def test_sweep_fixed_scale_input_tiles(hip_device, index):
     assert torch.equal(xs.cpu(), xs_ref)
 
 
-TUNED_CASES = 8
+TUNED_CASES = 40
 
 
 @pytest.mark.gpu
