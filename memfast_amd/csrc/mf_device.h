@@ -71,6 +71,22 @@ __device__ __forceinline__ float exp_small(float x) {
     return __builtin_amdgcn_exp2f(x * 1.44269504f);
 }
 
+// The S-curve of memfast/reference.py:57-59 in FP32 with the reference's roundings:
+// t = RN(alpha * z) (alpha = fp32(nonlinearity / max)), d = RN(1 + |t|), then RN(z / d).
+// The quotient is v_rcp_f32's estimate r of 1/d (within 1 ulp) refined by one residual
+// step: q0 = RN(z * r) is within an ulp of z / d, so e = z - q0 * d is exact in one FMA and
+// RN(q0 + e * r) is the correctly rounded quotient (Markstein).  A CPU check over 2e8
+// arguments with r = RN(1/d) and with r one ulp either side found every rounded integer
+// equal to rint(RN(z / d)).
+__device__ __forceinline__ float scurve(float z, float alpha) {
+    const float t = z * alpha;
+    const float d = 1.0f + fabsf(t);
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float q0 = z * r;
+    const float e = fmaf(-q0, d, z);
+    return fmaf(e, r, q0);
+}
+
 // INT code of x in a group of scale s (memfast/quantization.py:41: round half to even,
 // clamp, two's complement masked to the code width), FP32 division as torch's.
 __device__ __forceinline__ u8 quantize_code(float x, float s, float lower, float upper,

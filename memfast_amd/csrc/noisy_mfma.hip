@@ -14,8 +14,9 @@
 // accumulation give z to about FP32 accuracy; codes may flip where z lies within
 // that error of a rounding boundary (a few in 10^7 codes on the bench shapes),
 // the same order as FP32 summation-order differences from the CPU reference.
-// ADC: y = z + 1.5*2^23 (fma with the S-curve factor) rounds half-even, med3
-// clamps, and v_mad_i32_i24 accumulates fa*fw*(0x400000 + code) modulo 2^32;
+// ADC: the S-curve in the reference's FP32 roundings (RN(alpha*z), RN(1 + |t|), a
+// correctly rounded quotient: scurve in mf_device.h), then y + 1.5*2^23 rounds half-even,
+// med3 clamps, and v_mad_i32_i24 accumulates fa*fw*(0x400000 + code) modulo 2^32;
 // plan.bias removes the offset (|T| < 2^24, so float(T) is exact).
 //
 // k_split_conductances writes the conductances (programming, drift, stuck-at
@@ -343,14 +344,11 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
                 const u32 f24 = u32(int(plan.f24[a][w] << 8) >> 8);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    // The terms carry k1, so I is already z = I * Ma*Mw / unit.  Rounding
-                    // to an integer happens in the add (fma) to 1.5 * 2^23, then med3
+                    // The terms carry k1, so I is already z = I * Ma*Mw / unit.  The
+                    // S-curve is the reference's rounded arithmetic (scurve); rounding to
+                    // an integer (half-even) happens in the add to 1.5 * 2^23, then med3
                     // clamps in that domain; its low 24 bits are 0x400000 + code.
-                    float y;
-                    if (NONLINEAR)
-                        y = fmaf(I[r], __builtin_amdgcn_rcpf(fmaf(fabsf(I[r]), alpha, 1.0f)), MAGIC);
-                    else
-                        y = I[r] + MAGIC;
+                    float y = (NONLINEAR ? scurve(I[r], alpha) : I[r]) + MAGIC;
                     y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
                     const int low = int(__float_as_uint(y) << 8) >> 8;
                     Ti[r] += u32(low) * f24;
@@ -443,12 +441,7 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
                     const float sd = __builtin_amdgcn_sqrtf(fmaxf(Q[r] * var_scale, 0.0f));
                     const float z = normals.at(u32((r >> 2) * 8 + (r & 3)), args.read_seed, 60u);
                     const float current = I[r] + (mean + sd * z);
-                    float y;
-                    if (NONLINEAR)
-                        y = fmaf(current, __builtin_amdgcn_rcpf(fmaf(fabsf(current), alpha, 1.0f)),
-                                 MAGIC);
-                    else
-                        y = current + MAGIC;
+                    float y = (NONLINEAR ? scurve(current, alpha) : current) + MAGIC;
                     y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
                     const int low = int(__float_as_uint(y) << 8) >> 8;
                     Ti[r] += u32(low) * f24;

@@ -15,7 +15,8 @@
 // within 2^-23 of x relative to its magnitude, so two fp16 MFMAs with FP32
 // accumulation give z to about FP32 accuracy.
 //
-// Integer totals: the rounded, clamped count is formed in the exponent-fixed
+// Integer totals: the S-curve uses the reference's FP32 roundings (scurve in
+// mf_device.h); the rounded, clamped count is formed in the exponent-fixed
 // domain y = z + 1.5*2^23 (one rounding, half-even), med3-clamped to
 // [1.5*2^23, 1.5*2^23 + max_w]; the low 24 bits of y are 0x400000 + code, and
 // v_mad_i32_i24 accumulates fa*fw*(0x400000 + code) modulo 2^32.  The constant
@@ -280,13 +281,7 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
             if (NONLINEAR) alpha = lane_float(w_alpha, w);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                float y;
-                if (NONLINEAR) {
-                    const float z = I[r] * __builtin_amdgcn_rcpf(fmaf(fabsf(I[r]), alpha, 1.0f));
-                    y = z + MAGIC;
-                } else {
-                    y = I[r] + MAGIC;
-                }
+                float y = (NONLINEAR ? scurve(I[r], alpha) : I[r]) + MAGIC;
                 y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
                 const int low = int(__float_as_uint(y) << 8) >> 8;   // 0x400000 + code
                 T[r] += u32(low) * f24;

@@ -22,7 +22,8 @@ import itertools
 
 import torch
 
-from .oracle import input_layout, weight_layout
+from .oracle import (adc_maxima, input_layout, precise_currents, read_rows, reads_per_array,
+                     weight_layout)
 
 
 def pair_factors(cfg):
@@ -109,3 +110,101 @@ def check_noisy(cfg, got, expected, got_totals, ref_totals, *, xscale=None, wsca
         assert not over.any(), (
             f"{label}: {int(over.sum())} flipped outputs move by more than their flips explain")
     return report
+
+
+def adc_arguments(q, packed, cfg, conductance, begin=0, end=None):
+    """Exact ADC arguments y [N, m*Gr, A, W, (end-begin)*C] (FP64) for injected conductances.
+
+    The reference's count argument (memfast/reference.py:54-60, 96-115) in exact arithmetic:
+    value = sum_r da*(g - L)*V*Mw*u with its constants L, V and u = fp32(1 / ((H - L)*V)) (Ma
+    cancels), without the roundings of its accumulation; then the S-curve
+    y = value / (1 + a*|value|) with its FP32 coefficient a = fp32(alpha / max_w).
+    ``conductance`` is the FP32 (or FP64) tensor [m, p, W, R, C] (or with a leading plane
+    of one) that both sides read.  Read modes whose argument carries per-read noise
+    terms (voltage variation, output-mode or slice_pair read noise) are not covered.
+    """
+    ni = cfg.nonidealities
+    if ni.voltage_variation or (ni.read_variation and ni.read_mode != "shared"):
+        raise NotImplementedError("adc_arguments covers write, shared read, drift and SAF noise")
+    g = conductance.double().cpu()
+    if g.dim() == 6:
+        assert g.shape[0] == 1
+        g = g[0]
+    n, m, r = q.shape
+    end = packed.shape[1] if end is None else end
+    g = g[:, : end - begin] if g.shape[1] > end - begin else g
+    # The reference's constants (memfast/reference.py:23-27, 56, 96-101): the low level and
+    # read voltage in the current's dtype, 1 / current_unit rounded to FP32 in the ADC.
+    low, volt = float(cfg.low_conductance), float(cfg.read_voltage)
+    inverse = 1.0 / ((float(cfg.high_conductance) - low) * volt)
+    if not precise_currents(cfg):
+        f32 = lambda x: torch.tensor(x, dtype=torch.float32).double().item()
+        low, volt = f32(low), f32(volt)
+    inverse = torch.tensor(inverse, dtype=torch.float32).double().item()
+    rows, groups = read_rows(cfg), reads_per_array(cfg)
+    width, c = end - begin, cfg.array_size[1]
+    out = torch.zeros((n, m * groups, len(input_layout(cfg)), len(weight_layout(cfg)), width * c),
+                      dtype=torch.float64)
+    for ai, (sa, ma, _) in enumerate(input_layout(cfg)):
+        da = ((q.long() >> sa) & ma).double()                       # [n, m, r]
+        for wi, (_, mw, _) in enumerate(weight_layout(cfg)):
+            effective = (g[:, :, wi] - low) * (volt * mw * inverse)    # [m, t, r, c]
+            maximum = adc_maxima(cfg)[wi]
+            coeff = torch.tensor(ni.adc_nonlinearity / maximum, dtype=torch.float32).item()
+            for j in range(groups):
+                lo, hi = j * rows, min((j + 1) * rows, r)
+                value = torch.einsum("nir,itrc->nitc", da[:, :, lo:hi], effective[:, :, lo:hi])
+                if ni.adc_nonlinearity:
+                    value = value / (1 + coeff * value.abs())
+                out[:, j::groups, ai, wi] = value.reshape(n, m, width * c)
+    return out
+
+
+def boundary_flips(cfg, got_totals, ref_totals, arguments, tolerance):
+    """Explain every differing slice total by rounding-boundary flips.
+
+    ``arguments`` [N, G, A, W, p*C] are the exact ADC arguments (adc_arguments).  A pair
+    may flip only where its argument lies within ``tolerance * max(1, |y|)`` of a
+    rounding boundary: a half-integer inside [0, max_w], where round() changes value.
+    Each differing total must equal a signed sum of at most three such pairs' fa*fw.
+    Returns (differing totals, flips, the largest relative boundary distance of a flipped
+    pair, list of unexplained (index, difference, nearest relative distances))."""
+    diff = (got_totals.double().cpu() - ref_totals.double().cpu())
+    n, groups = diff.shape[0], diff.shape[1]
+    diff = diff.reshape(n, groups, -1)
+    y = arguments
+    maxima = torch.tensor(adc_maxima(cfg), dtype=torch.float64)[None, None, None, :, None]
+    clamped = y.clamp(min=-0.5 * torch.ones_like(y), max=maxima + 0.5)
+    distance = (clamped - clamped.floor() - 0.5).abs()
+    # Boundaries only at half-integers in [0.5, max - 0.5] (the clamp is exact elsewhere).
+    inside = (y > 0) & (y < maxima)
+    near = inside & (distance <= tolerance * y.abs().clamp(min=1.0))
+    factors = [[fa * fw for _, _, fw in weight_layout(cfg)] for _, _, fa in input_layout(cfg)]
+    relative = distance / y.abs().clamp(min=1.0)
+    flips, worst = 0, 0.0
+    unexplained = []
+    for index in diff.nonzero().tolist():
+        v, g_, col = index
+        want = int(diff[v, g_, col])
+        pairs_near = near[v, g_, :, :, col].nonzero().tolist()
+        candidates = [factors[a][w] for a, w in pairs_near]
+        found = None
+        for count in range(1, 4):
+            for chosen in itertools.combinations(range(len(candidates)), count):
+                for signs in itertools.product((1, -1), repeat=count):
+                    if sum(s * candidates[i] for s, i in zip(signs, chosen)) == want:
+                        found = chosen
+                        break
+                if found:
+                    break
+            if found:
+                break
+        if found:
+            flips += len(found)
+            for i in found:
+                a, w = pairs_near[i]
+                worst = max(worst, float(relative[v, g_, a, w, col]))
+        else:
+            unexplained.append((index, want,
+                                sorted(relative[v, g_, :, :, col].flatten().tolist())[:3]))
+    return int((diff != 0).sum()), flips, worst, unexplained

@@ -260,3 +260,49 @@ def test_sweep_gru_sequence_matches_oracle_steps(hip_device, index, noisy):
     layer = AnalogGRU(source.to(hip_device), Simulator(cfg, device=hip_device), name="gru")
     output, _ = layer(x.to(hip_device))
     gru_step_parity(layer.cells[0], source.cpu(), x, output, hip_device, label=f"gru sweep {index}")
+
+
+def _injected_flips(cfg, a, b, device, events, tolerance=2.0**-16):
+    """Per read event, the kernel's slice totals (the one hip.mm runs) against oracle.partial,
+    both given the oracle's own sampled conductances.  Every differing total must be explained
+    by flips of pairs whose exact ADC argument (oracle.flips.adc_arguments) lies within
+    ``tolerance`` (relative) of a rounding boundary.  Returns the flips per event, the codes
+    per event and the largest relative boundary distance of a flipped pair."""
+    from oracle import flips, oracle
+    from parity import gpu_totals
+
+    q, _ = oracle.input_tiles(a, cfg)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    p = packed.shape[1]
+    seed = oracle.name_seed(cfg.seed, "matrix.0")
+    q_dev, packed_dev = q.to(device), packed.to(device)
+    counts, worst = [], 0.0
+    for event in events:
+        raw, _, _ = oracle.restored(packed, cfg, seed, event, 0, p)
+        expected = oracle.partial(q, packed, cfg, seed, event, 0, p, conductance=raw)
+        got = gpu_totals(q_dev, packed_dev, cfg, seed, event, conductance=raw.to(device))
+        arguments = flips.adc_arguments(q, packed, cfg, raw)
+        _, flipped, far, unexplained = flips.boundary_flips(cfg, got, expected, arguments,
+                                                            tolerance)
+        assert not unexplained, (event, unexplained[:3])
+        counts.append(flipped)
+        worst = max(worst, far)
+    codes = expected.numel() * len(cfg.input_layout) * len(cfg.weight_layout)
+    return counts, codes, worst
+
+
+@pytest.mark.gpu
+def test_sweep_draw_1386_injected_conductances(hip_device):
+    """Regression for product draw 1386 with noise (9-bit S-curve ADCs, shared read noise,
+    4-bit inputs, 12 x 54 @ 54 x 57 on 32 x 32 arrays), which once flipped 2 of its 13,824
+    codes against the oracle's sampled conductances, more than 1e-4 of that one read.
+    Given the oracle's own conductances, over 64 read events every flipped code is a
+    rounding-boundary flip (its exact argument within 2^-16 relative of a half-integer)
+    and the flips stay within 1e-4 of all codes."""
+    cfg, a, b = _case(1386, True)
+    assert cfg.nonidealities.adc_nonlinearity and max(cfg.adc_bits) >= 9
+    assert _kernel(cfg, *a.shape, b.shape[1]) == 2
+    counts, codes, worst = _injected_flips(cfg, a, b, hip_device, range(64))
+    say("draw 1386 injected: flips per event", counts, "of", codes, "codes each; largest "
+        "relative boundary distance of a flip", worst)
+    assert sum(counts) <= 1e-4 * codes * len(counts)
