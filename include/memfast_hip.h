@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 7
+#define MF_ABI_VERSION 8
 #define MF_MAX_SLICES 32
 
 enum {
@@ -363,7 +363,8 @@ int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, i
                              void *stream);
 /* mf_restore, mf_partial and mf_mm for wide codes (totals and outputs FP64;
  * the fused read restores with restore_scales in FP64 and sums in torch's
- * FP64 order).  mf_mm_wide uses the noisy-device bf16 MFMA read when the
+ * FP64 order).  mf_mm_wide uses the noisy-device fp16 MFMA read (conductance
+ * terms split into fp16 hi + lo) when the
  * configuration allows it (mf_mm_kernel reports 3) and `workspace` holds at
  * least the 64-column minimum of mf_mm_workspace (smaller than its full
  * figure: column chunks); otherwise the general read. */
@@ -414,15 +415,19 @@ int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
                  float *totals, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Kernel selected by mf_mm (mf_mm_wide) for this shape: 0 = general, 1 = MFMA
- * ideal, 2 = MFMA noisy (bf16 split conductances), 3 = MFMA noisy for wide
+ * ideal, 2 = MFMA noisy (fp16 hi + lo conductance terms), 3 = MFMA noisy for wide
  * codes. */
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
                  int32_t *kernel_id);
 
 /* Resource figures (registers, scratch spill, LDS, resident blocks per CU) of the
- * read kernel mf_mm (mf_mm_wide) launches as `kernel_id` (mf_mm_kernel): 0 general,
- * 1 ideal MFMA, 2 noisy MFMA, 3 wide noisy MFMA (its largest LDS tier). */
-int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *out);
+ * read kernel instance mf_mm (mf_mm_wide) launches as `kernel_id` (mf_mm_kernel: 0
+ * general, 1 ideal MFMA, 2 noisy MFMA, 3 wide noisy MFMA) under the schedule `variant`
+ * (mf_mm's variant word: the ideal read's tile, the wide read's LDS tier).  Replaces the
+ * per-candidate compiled-kernel attributes memfast/simulator.py:230-236 reads
+ * (memfast/cuda.py:376-389). */
+int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int32_t variant,
+                       mf_resources *out);
 
 /* ---- counter-based RNG (memfast/random.py:8-33), for parity tests -------- */
 /* out[i] = uniform(address[i], seed, stream) (FP32) */

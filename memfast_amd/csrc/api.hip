@@ -4,6 +4,7 @@
 // ideal-device MFMA plan, launches on the caller's stream and error strings.
 // Nothing here allocates device memory; the caller owns every buffer.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -31,23 +32,37 @@ __global__ void k_rng(const u64 *address, i64 count, u64 seed, u32 stream, int k
 thread_local char g_error[1024] = "";
 
 // Read-kernel timing for benchmarks: event pairs recorded around the main read
-// kernel of each mf_mm call while enabled (single host thread, as torch's).
+// kernel of each mf_mm call while enabled.  The event lists are guarded by a mutex;
+// a call that must not create events (mf_mm_static) turns timing off for its own
+// thread only.
 struct ProfileState {
-    bool enabled = false;
+    std::atomic<bool> enabled{false};
+    std::mutex lock;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> pending, spare;
 };
 ProfileState g_profile;
+thread_local bool g_profile_off = false;
+
+bool profiling() { return g_profile.enabled.load(std::memory_order_relaxed) && !g_profile_off; }
 
 std::pair<hipEvent_t, hipEvent_t> profile_pair() {
-    if (!g_profile.spare.empty()) {
-        auto pair = g_profile.spare.back();
-        g_profile.spare.pop_back();
-        return pair;
+    {
+        std::lock_guard<std::mutex> guard(g_profile.lock);
+        if (!g_profile.spare.empty()) {
+            auto pair = g_profile.spare.back();
+            g_profile.spare.pop_back();
+            return pair;
+        }
     }
     std::pair<hipEvent_t, hipEvent_t> pair{nullptr, nullptr};
     if (hipEventCreate(&pair.first) != hipSuccess || hipEventCreate(&pair.second) != hipSuccess)
         return {nullptr, nullptr};
     return pair;
+}
+
+void profile_push(std::pair<hipEvent_t, hipEvent_t> pair) {
+    std::lock_guard<std::mutex> guard(g_profile.lock);
+    g_profile.pending.push_back(pair);
 }
 
 int fail(int code, const char *fmt, ...) {
@@ -515,7 +530,7 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         const bool slice = plan.planes > 1 && !plan.out_noise;
         // Benchmark timing brackets the read kernel alone (not the conductance split).
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
-        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+        if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
 #define MF_NOISY_LAUNCH1(KS, NA, NL, VN, SL, ON) \
     hipLaunchKernelGGL((k_noisy<KS, NA, NL, VN, SL, ON>), grid, dim3(256), 0, s, plan, args)
 #define MF_NOISY_LAUNCH2(KS, NA, VN, SL, ON)                    \
@@ -539,7 +554,7 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
 #undef MF_NOISY_LAUNCH1
         if (timing.first) {
             hipEventRecord(timing.second, s);
-            g_profile.pending.push_back(timing);
+            profile_push(timing);
         }
     }
     // With split_totals the caller restores and sums a split read's totals [n, G, ncols]
@@ -1309,13 +1324,13 @@ static int launch_ideal(const mf_config *cfg, const IdealPlan &plan, int ks, con
     if (gy > 65535 || gx > 2147483647) return fail(MF_E_RESOURCE, "grid too large");
     const dim3 grid{unsigned(gx), unsigned(gy), 1u};
     std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
-    if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+    if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
     if (ks == 1 && tn == 2) hipLaunchKernelGGL((k_ideal<2, 1>), grid, dim3(256), 0, s, plan, args);
     else if (ks == 1) hipLaunchKernelGGL((k_ideal<1, 1>), grid, dim3(256), 0, s, plan, args);
     else hipLaunchKernelGGL((k_ideal<1, 2>), grid, dim3(256), 0, s, plan, args);
     if (timing.first) {
         hipEventRecord(timing.second, s);
-        g_profile.pending.push_back(timing);
+        profile_push(timing);
     }
     return check_launch("ideal MFMA read");
 }
@@ -1413,12 +1428,12 @@ static int mm_read(const mf_config *cfg, const uint8_t *q, const float *xscale, 
     args.lp_cascade = level_power(G);
     args.lp_interleaved = level_power(G / 4);
     std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
-    if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+    if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
     const int launched = cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
                                       : launch_general<float>(cfg, args, OUT_FUSED, s);
     if (timing.first) {
         hipEventRecord(timing.second, s);
-        g_profile.pending.push_back(timing);
+        profile_push(timing);
     }
     return launched;
 }
@@ -1583,14 +1598,14 @@ int mf_mm_static(const mf_config *cfg, const uint8_t *q, const float *xscale, in
     if (found) return found;
     // The scratch is shared by every call on this GPU, so it never holds this
     // program's conductance terms from an earlier call: sample them again.
-    // Benchmark timing (hipEventCreate) stays off for the call.
+    // Benchmark timing (hipEventCreate) stays off for this thread's call.
     variant &= ~MF_MM_REUSE_TERMS;
-    const bool profiling = g_profile.enabled;
-    g_profile.enabled = false;
+    const bool was_off = g_profile_off;
+    g_profile_off = true;
     const int launched = mf_mm(cfg, q, xscale, n, m, packed, packed_t, wscale, p, out_cols,
                                k_rows, g, seed, event, out, ldo, ptr, MF_STATIC_SCRATCH_BYTES,
                                variant, status, stream);
-    g_profile.enabled = profiling;
+    g_profile_off = was_off;
     return launched;
 }
 
@@ -1922,14 +1937,14 @@ int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, in
         workspace_bytes >= wide_codes_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m)) {
         hipStream_t s = static_cast<hipStream_t>(stream);
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
-        if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+        if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
         const int launched = launch_noisy_wide(cfg, wplan, ks, small, q, xscale, n, m, packed,
                                                wscale, p, nullptr, seed, event, out, ldo,
                                                workspace, workspace_bytes, 0, status, s,
                                                variant_tier(variant));
         if (timing.first) {
             hipEventRecord(timing.second, s);
-            g_profile.pending.push_back(timing);
+            profile_push(timing);
         }
         return launched;
     }
@@ -1958,12 +1973,12 @@ int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, in
     args.lp_interleaved = level_power(G / 4);
     hipStream_t s = static_cast<hipStream_t>(stream);
     std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
-    if (g_profile.enabled && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
+    if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
     const int launched = cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
                                       : launch_general<float>(cfg, args, OUT_FUSED, s);
     if (timing.first) {
         hipEventRecord(timing.second, s);
-        g_profile.pending.push_back(timing);
+        profile_push(timing);
     }
     return launched;
 }
@@ -1993,7 +2008,7 @@ int mf_mm_totals_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_
 }
 
 int mf_profile_kernels(int32_t enable) {
-    g_profile.enabled = enable != 0;
+    g_profile.enabled.store(enable != 0);
     return MF_OK;
 }
 
@@ -2002,6 +2017,7 @@ int mf_profile_collect(int64_t *launches, double *milliseconds) {
     *launches = 0;
     *milliseconds = 0.0;
     int status = MF_OK;
+    std::lock_guard<std::mutex> guard(g_profile.lock);
     for (auto &pair : g_profile.pending) {
         float ms = 0.0f;
         hipError_t e = hipEventSynchronize(pair.second);
@@ -2016,18 +2032,27 @@ int mf_profile_collect(int64_t *launches, double *milliseconds) {
     return status;
 }
 
-int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *out) {
+int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int32_t variant,
+                       mf_resources *out) {
     int status = check_config(cfg);
     if (status) return status;
     if (!out) return fail(MF_E_INVALID, "resources output is NULL");
-    // The instance of the read kernel mf_mm (mf_mm_wide) launches for this descriptor.
+    if (!variant_valid(variant)) return fail(MF_E_INVALID, "unknown kernel variant 0x%x", variant);
+    // The instance of the read kernel that mf_mm (mf_mm_wide) launches for this descriptor
+    // and schedule (`variant`), chosen as launch_ideal, launch_noisy, launch_noisy_wide and
+    // launch_general choose it.
     const bool nl = cfg->has_nonlinear != 0;
     const bool ks4 = cfg->read_rows == 64;
+    const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
     const void *fn = nullptr;
     if (kernel_id == 1) {
-        fn = reinterpret_cast<const void *>(&k_ideal<1, 1>);
+        // 32-row reads: 32 or (tile field 1) 64 vectors per wave; 64-row reads: KS 2.
+        if (ks4) fn = reinterpret_cast<const void *>(&k_ideal<1, 2>);
+        else if (variant_tile(variant) == 1) fn = reinterpret_cast<const void *>(&k_ideal<2, 1>);
+        else fn = reinterpret_cast<const void *>(&k_ideal<1, 1>);
     } else if (kernel_id == 2) {
-        // ks index 0: KS 2 with up to 5 slices, 1: KS 2 with 8, 2: KS 4.
+        // ks index 0: KS 2 with up to 5 slices, 1: KS 2 with 8, 2: KS 4.  The read split
+        // does not change the instance.
 #define MF_NOISY_FN(KS, NA, NL, VN, SL, ON) \
     reinterpret_cast<const void *>(&k_noisy<KS, NA, NL, VN, SL, ON>)
 #define MF_NOISY_ROW(KS, NA)                                                                      \
@@ -2043,18 +2068,35 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, mf_resources *ou
 #undef MF_NOISY_ROW
 #undef MF_NOISY_FN
         const int which = ks4 ? 2 : (cfg->n_in <= 5 ? 0 : 1);
-        const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
         const int mode = output_noise ? 2 : (cfg->has_vnoise ? 1 : 0);
         const bool slice = cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR;
         fn = table[which][mode][slice ? 1 : 0][nl ? 1 : 0];
     } else if (kernel_id == 3) {
-        fn = ks4 ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<4, true, false, WIDE_FRAGS_LARGE>)
-                       : reinterpret_cast<const void *>(&k_noisy_wide<4, false, false, WIDE_FRAGS_LARGE>))
-                 : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<2, true, false, WIDE_FRAGS_LARGE>)
-                       : reinterpret_cast<const void *>(&k_noisy_wide<2, false, false, WIDE_FRAGS_LARGE>));
+        // The LDS tier: the schedule's (tier field 1-3), else the smallest that holds a read.
+        const int frags = cfg->n_w * NOISY_TERMS * (ks4 ? 4 : 2);
+        int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
+        if (variant_tier(variant) > 0) tier = variant_tier(variant) - 1;
+        bool small = true;   // every input digit of at most 2 bits (build_noisy_wide_plan)
+        for (int a = 0; a < cfg->n_in; ++a) small = small && cfg->in_mask[a] <= 3;
+#define MF_WIDE_FN(KS, FR) \
+    (nl ? (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, true, FR>)           \
+                 : reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR>))         \
+        : (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, false, true, FR>)          \
+                 : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR>)))
+        if (ks4) fn = tier == 2 ? MF_WIDE_FN(4, WIDE_FRAGS_LARGE)
+                      : tier == 1 ? MF_WIDE_FN(4, WIDE_FRAGS_SMALL) : MF_WIDE_FN(4, WIDE_FRAGS_TINY);
+        else fn = tier == 2 ? MF_WIDE_FN(2, WIDE_FRAGS_LARGE)
+                  : tier == 1 ? MF_WIDE_FN(2, WIDE_FRAGS_SMALL) : MF_WIDE_FN(2, WIDE_FRAGS_TINY);
+#undef MF_WIDE_FN
     } else if (kernel_id == 0) {
-        fn = cfg->precise ? reinterpret_cast<const void *>(&k_general<double, 4, false, false>)
-                          : reinterpret_cast<const void *>(&k_general<float, 8, false, false>);
+#define MF_GENERAL_FN(WIDE)                                                                      \
+    (cfg->precise                                                                                \
+         ? (output_noise ? reinterpret_cast<const void *>(&k_general<double, 2, true, WIDE>)      \
+                         : reinterpret_cast<const void *>(&k_general<double, 4, false, WIDE>))    \
+         : (output_noise ? reinterpret_cast<const void *>(&k_general<float, 2, true, WIDE>)       \
+                         : reinterpret_cast<const void *>(&k_general<float, 8, false, WIDE>)))
+        fn = cfg->wide ? MF_GENERAL_FN(true) : MF_GENERAL_FN(false);
+#undef MF_GENERAL_FN
     } else {
         return fail(MF_E_INVALID, "unknown read kernel %d", kernel_id);
     }

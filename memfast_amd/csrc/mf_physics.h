@@ -45,6 +45,20 @@ __device__ __forceinline__ float high_of<float>(const mf_config &cfg) { return c
 template <>
 __device__ __forceinline__ double high_of<double>(const mf_config &cfg) { return cfg.d_high; }
 
+// exp(sigma * n) for a noise sample n at `address`.  FP64 currents resolve conductance
+// differences far below one FP32 ulp of g (high - low down to 1e-4 of high), and one ulp of an
+// FP32 factor near 1 is 2^-23 of g, so they sample with OCML's logf/cosf/sqrtf/expf, which stay
+// within an ulp or two of torch CPU's; FP32 currents use the hardware approximations
+// (normal_fast, exp_small).
+template <typename Phys>
+__device__ __forceinline__ float noise_factor(const mf_config &cfg, float sigma, u64 address,
+                                              u64 seed, u32 stream) {
+    if constexpr (sizeof(Phys) == sizeof(double))
+        return expf(sigma * normal(address, seed, stream, cfg.f_two_pi));
+    else
+        return exp_small(sigma * normal_fast(address, seed, stream));
+}
+
 // Programmed + (shared) read conductance of one cell.
 template <typename Phys>
 __device__ __forceinline__ Phys cell_conductance(const mf_config &cfg, u32 code, int w, u64 cell,
@@ -52,7 +66,7 @@ __device__ __forceinline__ Phys cell_conductance(const mf_config &cfg, u32 code,
     const int mask = cfg.w_mask[w];
     const int digit = int((code >> cfg.w_shift[w]) & u32(mask));
     Phys raw = nominal_level<Phys>(cfg, digit, mask);
-    if (cfg.has_write) raw = raw * Phys(exp_small(cfg.f_write * normal_fast(cell, seed, 10u)));
+    if (cfg.has_write) raw = raw * Phys(noise_factor<Phys>(cfg, cfg.f_write, cell, seed, 10u));
     raw = raw * drift_of<Phys>(cfg);
     if (cfg.has_saf) {
         const float u = uniform(cell, seed, 30u);
@@ -60,7 +74,7 @@ __device__ __forceinline__ Phys cell_conductance(const mf_config &cfg, u32 code,
         else if (u < cfg.f_saf_band) raw = high_of<Phys>(cfg);
     }
     if (cfg.read_mode == MF_READ_SHARED && cfg.has_read)
-        raw = raw * Phys(exp_small(cfg.f_read * normal_fast(cell, read_seed, 20u)));
+        raw = raw * Phys(noise_factor<Phys>(cfg, cfg.f_read, cell, read_seed, 20u));
     return raw;
 }
 

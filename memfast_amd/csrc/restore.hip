@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void k_restore(const mf_config cfg, const Code
         if (planes > 1) {
             // slice_pair: an independent read field per activation slice.
             const u64 address = cell * u64(cfg.n_in) + u64(plane);
-            raw = raw * Phys(exp_small(cfg.f_read * normal_fast(address, read_seed, 20u)));
+            raw = raw * Phys(noise_factor<Phys>(cfg, cfg.f_read, address, read_seed, 20u));
         }
         g[idx] = raw;
     }

@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -178,7 +178,7 @@ SIGNATURES = {
     "mf_profile_collect": ([ct.POINTER(_I64), ct.POINTER(ct.c_double)], ct.c_int),
     "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I64)], ct.c_int),
     "mf_mm_kernel": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I32)], ct.c_int),
-    "mf_resources_query": ([_CFG, _I32, ct.POINTER(MFResources)], ct.c_int),
+    "mf_resources_query": ([_CFG, _I32, _I32, ct.POINTER(MFResources)], ct.c_int),
     "mf_rng_uniform": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
     "mf_rng_normal": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
 }
@@ -367,6 +367,12 @@ def _group_dims(shape, granularity):
 
 
 STATUS_INPUT, STATUS_WEIGHT, STATUS_OUTPUT = 1, 2, 4
+# Set by a torch reduction in weight_tiles, not by a kernel: a negative weight under an
+# unsigned configuration, raised after the finiteness flags as the reference orders them
+# (memfast/functional.py:51-53 before memfast/quantization.py:14-18).
+STATUS_NEGATIVE_WEIGHT = 8
+UNSIGNED_MESSAGE = ("unsigned floating weights must be nonnegative INT values; "
+                    "use map_quantized with zero_points for affine weights")
 
 
 class _Scratch(ct.c_void_p):
@@ -553,13 +559,26 @@ def _input_tiles_wide(value, config, fixed_scale, status):
     return q, xscale
 
 
+def _check_unsigned(b, config, status):
+    """Unsigned weights must be nonnegative (memfast/quantization.py:14-18): raised here, or
+    with a status word flagged as STATUS_NEGATIVE_WEIGHT for the caller's one status read."""
+    if config.weight_signed:
+        return
+    if status is None:
+        if (b < 0).any():
+            raise ValueError(UNSIGNED_MESSAGE)
+    else:
+        status.bitwise_or_((b < 0).any().to(torch.int32) * STATUS_NEGATIVE_WEIGHT)
+
+
 def weight_tiles(weight, config, *, transposed=True, status=None):
     """PyTorch [O,K] weights -> packed [m,p,R,C], packed_t [p*C, m*R], scales [m*Gr,p,C].
 
     Follows quantization.py:82-112 (weights are quantized in physical [K,O]
     coordinates).  ``packed_t`` is the column-major copy read by the MFMA kernel.
-    Without ``status`` a non-finite weight raises here; with a status word the
-    check is deferred (STATUS_WEIGHT on the device).
+    Without ``status`` a non-finite weight (or, for unsigned weights, a negative one)
+    raises here; with a status word the checks are deferred (STATUS_WEIGHT,
+    STATUS_NEGATIVE_WEIGHT).
     """
     supported(config)
     require_device(weight)
@@ -569,11 +588,7 @@ def weight_tiles(weight, config, *, transposed=True, status=None):
     b = weight.detach().T.to(torch.float32).contiguous()  # [K, O]
     if status is None and not torch.isfinite(b).all():
         raise ValueError("quantized values must be finite in torch.float32")
-    if not config.weight_signed and (b < 0).any():
-        raise ValueError(
-            "unsigned floating weights must be nonnegative INT values; "
-            "use map_quantized with zero_points for affine weights"
-        )
+    _check_unsigned(b, config, status)
     r, c = config.array_size
     m, p = math.ceil(k / r), math.ceil(o / c)
     device = b.device
@@ -607,11 +622,7 @@ def _weight_tiles_wide(weight, config, status):
         narrow = config.weight_bits <= 8 and config.bw_e is None
         raise ValueError("quantized values must be finite in "
                          f"torch.float{32 if narrow else 64}")
-    if not config.weight_signed and (b < 0).any():
-        raise ValueError(
-            "unsigned floating weights must be nonnegative INT values; "
-            "use map_quantized with zero_points for affine weights"
-        )
+    _check_unsigned(b, config, status)
     r, c = config.array_size
     m, p = math.ceil(k / r), math.ceil(o / c)
     device = b.device
@@ -1149,14 +1160,15 @@ class Program:
         self.vectors = vectors
         self.columns = columns
 
-    def resources(self, config, vectors, columns, workers, kernel=None):
-        """Resources of the read kernel ``kernel`` (mf_mm_kernel's id; by default the ideal
-        MFMA read for ideal devices, else the general one)."""
+    def resources(self, config, vectors, columns, workers, kernel=None, variant=0):
+        """Resources of the instance of read kernel ``kernel`` (mf_mm_kernel's id; by default
+        the ideal MFMA read for ideal devices, else the general one) that mf_mm launches under
+        the schedule word ``variant`` (variant_word)."""
         info = MFResources()
         if kernel is None:
             kernel = 1 if config.nonidealities.ideal else 0
-        check(library().mf_resources_query(ct.byref(descriptor(config)), kernel, ct.byref(info)),
-              "resources")
+        check(library().mf_resources_query(ct.byref(descriptor(config)), kernel, variant,
+                                           ct.byref(info)), "resources")
         return dict(threads=info.threads, shared=info.shared_bytes, local_bytes=info.local_bytes,
                     registers=info.registers)
 

@@ -285,6 +285,8 @@ class Simulator:
             raise ValueError("A must be finite")
         if flags & hip.STATUS_WEIGHT:
             raise ValueError("B must be finite")
+        if flags & hip.STATUS_NEGATIVE_WEIGHT:
+            raise ValueError(hip.UNSIGNED_MESSAGE)
         if kept is not None:
             kept._install(tiles)
             program = kept
@@ -380,7 +382,8 @@ class Simulator:
         with torch.cuda.device(self.device):
             resource = hip.program(c, schedule["vectors"], schedule["columns"],
                                    self.device.index).resources(
-                c, schedule["vectors"], schedule["columns"], schedule["workers"], kernel=kernel)
+                c, schedule["vectors"], schedule["columns"], schedule["workers"], kernel=kernel,
+                variant=tuning.schedule_variant(schedule))
         # The output-noise MFMA read at 32-row reads keeps part of its state in scratch by
         # design (three waves per SIMD with spills run faster than two without), and its
         # registers do not depend on the schedule; the policy refuses any other spill.

@@ -34,14 +34,19 @@ uint64_t brute_event_seed(uint32_t seed, uint64_t event) {
 }
 
 /*
- * q:      uint8 [n][m][R]     (two's-complement codes masked to activation bits)
- * packed: uint8 [m][p][R][C]  (codes masked to weight bits)
- * totals: int64 [n][m*Gr][p][C]
+ * q:      [n][m][R]     codes (two's complement masked to the activation bits)
+ * packed: [m][p][R][C]  codes (masked to the weight bits)
+ * uint8 codes (brute_ideal_totals) or int64 codes of wide configurations
+ * (brute_ideal_totals_wide); totals: int64 [n][m*Gr][p][C]
  */
-void brute_ideal_totals(const uint8_t *q, const uint8_t *packed, int n, int m, int p,
-                        int R, int C, int P, int na, const int *ashift, const int *amask,
-                        const int64_t *afac, int nw, const int *wshift, const int *wmask,
-                        const int64_t *wfac, const int *maxima, int64_t *totals) {
+static int64_t code_at(const void *codes, int wide, int64_t index) {
+    return wide ? ((const int64_t *)codes)[index] : (int64_t)((const uint8_t *)codes)[index];
+}
+
+static void ideal_totals(const void *q, const void *packed, int wide, int n, int m, int p,
+                         int R, int C, int P, int na, const int *ashift, const int64_t *amask,
+                         const int64_t *afac, int nw, const int *wshift, const int64_t *wmask,
+                         const int64_t *wfac, const int64_t *maxima, int64_t *totals) {
     int gr = (R + P - 1) / P;
     for (int v = 0; v < n; ++v)
         for (int i = 0; i < m; ++i)
@@ -54,9 +59,12 @@ void brute_ideal_totals(const uint8_t *q, const uint8_t *packed, int n, int m, i
                             for (int w = 0; w < nw; ++w) {
                                 int64_t s = 0;
                                 for (int r = lo; r < hi; ++r) {
-                                    int da = (q[((int64_t)v * m + i) * R + r] >> ashift[a]) & amask[a];
-                                    int dw = (packed[(((int64_t)i * p + t) * R + r) * C + c] >> wshift[w]) & wmask[w];
-                                    s += (int64_t)da * dw;
+                                    int64_t da = (code_at(q, wide, ((int64_t)v * m + i) * R + r)
+                                                  >> ashift[a]) & amask[a];
+                                    int64_t dw = (code_at(packed, wide,
+                                                          (((int64_t)i * p + t) * R + r) * C + c)
+                                                  >> wshift[w]) & wmask[w];
+                                    s += da * dw;
                                 }
                                 if (s > maxima[w]) s = maxima[w];
                                 total += afac[a] * wfac[w] * s;
@@ -64,4 +72,21 @@ void brute_ideal_totals(const uint8_t *q, const uint8_t *packed, int n, int m, i
                         totals[(((int64_t)v * m * gr + i * gr + j) * p + t) * C + c] = total;
                     }
             }
+}
+
+void brute_ideal_totals(const uint8_t *q, const uint8_t *packed, int n, int m, int p, int R,
+                        int C, int P, int na, const int *ashift, const int64_t *amask,
+                        const int64_t *afac, int nw, const int *wshift, const int64_t *wmask,
+                        const int64_t *wfac, const int64_t *maxima, int64_t *totals) {
+    ideal_totals(q, packed, 0, n, m, p, R, C, P, na, ashift, amask, afac, nw, wshift, wmask,
+                 wfac, maxima, totals);
+}
+
+void brute_ideal_totals_wide(const int64_t *q, const int64_t *packed, int n, int m, int p,
+                             int R, int C, int P, int na, const int *ashift,
+                             const int64_t *amask, const int64_t *afac, int nw,
+                             const int *wshift, const int64_t *wmask, const int64_t *wfac,
+                             const int64_t *maxima, int64_t *totals) {
+    ideal_totals(q, packed, 1, n, m, p, R, C, P, na, ashift, amask, afac, nw, wshift, wmask,
+                 wfac, maxima, totals);
 }

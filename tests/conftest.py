@@ -1,5 +1,6 @@
 """Shared pytest setup: the `gpu` marker, import paths and golden fixtures."""
 
+import json
 import sys
 from pathlib import Path
 
@@ -29,3 +30,12 @@ def hip_device():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     return torch.device("cuda", 0)
+
+
+def fixture_config(vectors, name):
+    """The Config that make_reference_vectors.py ran case ``name`` with (stored as JSON)."""
+    from memfast_amd import Config, Nonidealities
+
+    stored = json.loads(str(vectors[f"case_{name}_config"]))
+    kwargs = {k: tuple(v) if isinstance(v, list) else v for k, v in stored["config"].items()}
+    return Config(**kwargs, nonidealities=Nonidealities(**stored["nonidealities"]))

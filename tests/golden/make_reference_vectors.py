@@ -12,6 +12,7 @@ The reference never travels: only the vectors in reference_vectors.npz are
 committed.  Run: python tests/golden/make_reference_vectors.py
 """
 
+import json
 import sys
 from pathlib import Path
 
@@ -52,7 +53,26 @@ def cases():
         ("bfp8_binary", dict(activation_bits=8, weight_bits=8, bw_e=4, array_size=(32, 16),
                              rows_per_read=16, adc_bits=6),
          dict(write_variation=0.02, adc_nonlinearity=0.05), 4, 64, 33),
+        # FP64 currents (memfast/config.py:215-224, `precise_currents`): a 9-bit input
+        # slice (mask 511 > 255, wide codes) ...
+        ("precise_slice9_ideal", PRECISE_SLICE9, dict(write_variation=0.0), 3, 70, 24),
+        ("precise_slice9", PRECISE_SLICE9,
+         dict(write_variation=0.02, read_variation=0.01, adc_nonlinearity=0.1), 3, 70, 24),
+        # ... and narrow INT8 codes with high - low < 1e-4 * high, where FP32 conductance
+        # differences lose the count; the noise is scaled to a few percent of high - low.
+        ("precise_close_ideal", PRECISE_CLOSE, dict(write_variation=0.0), 4, 64, 33),
+        ("precise_close", PRECISE_CLOSE,
+         dict(write_variation=2e-6, read_variation=1e-6, adc_nonlinearity=0.1), 4, 64, 33),
     ]
+
+
+PRECISE_SLICE9 = dict(activation_bits=12, weight_bits=8, input_slice=(1, 2, 9),
+                      weight_slice=(1, 1, 2, 2, 2), array_size=(32, 16), rows_per_read=16,
+                      adc_bits=8)
+PRECISE_CLOSE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                     weight_slice=(1, 1, 2, 2, 2), array_size=(32, 16), rows_per_read=16,
+                     weight_quant_gran=(16, 1), input_quant_gran=(1, 16), adc_bits=(6, 7, 7, 8, 8),
+                     high_conductance=1e-5, low_conductance=0.99995e-5)
 
 
 def bfp_edge_values():
@@ -117,6 +137,8 @@ def main():
         raw, _, _ = reference.restored(matrix.packed, config, matrix.seed, 0, 0, matrix.p)
         totals = reference.partial(q, matrix.packed, config, None, matrix.seed, 0, 0, matrix.p)
         prefix = f"case_{name}_"
+        vectors[prefix + "config"] = np.array(json.dumps(dict(config=cfg_kwargs,
+                                                              nonidealities=ni_kwargs)))
         vectors[prefix + "a"] = a.numpy()
         vectors[prefix + "b"] = b.numpy()
         vectors[prefix + "out0"] = out0.numpy()

@@ -559,6 +559,34 @@ def test_functional_nonfinite_operands_leave_simulator_unchanged(hip_device):
     assert bits_equal(sim.mm(a.to(hip_device), b.to(hip_device)), oracle.mm(a, b, cfg))
 
 
+def test_unsigned_weight_error_follows_finiteness_errors(hip_device):
+    """Unsigned configurations: a non-finite A (or B) raises its finiteness error before a
+    negative weight raises the unsigned-weight error, as memfast/functional.py:51-53 checks
+    finiteness before memfast/quantization.py:14-18 quantizes; narrow and wide."""
+    from memfast_amd import Simulator
+
+    for cfg in (ideal(weight_bits=4, weight_signed=False, weight_slice=(2, 2),
+                      array_size=(32, 16), adc_bits=5),
+                ideal(activation_bits=12, weight_bits=10, weight_signed=False,
+                      array_size=(32, 16), adc_bits=8)):
+        gen = torch.Generator().manual_seed(8)
+        a, b = torch.randn(4, 40, generator=gen), torch.randn(40, 20, generator=gen).abs()
+        bad_a, negative_b, bad_b = a.clone(), -b, b.clone()
+        bad_a[1, 3] = float("nan")
+        bad_b[2, 2] = float("inf")
+        negative_bad_b = negative_b.clone()
+        negative_bad_b[2, 2] = float("nan")
+        sim = Simulator(cfg, device=hip_device)
+        cases = [(bad_a, negative_b, "A must be finite"), (a, negative_bad_b, "B must be finite"),
+                 (a, negative_b, "unsigned floating weights must be nonnegative"),
+                 (bad_a, bad_b, "A must be finite")]
+        for left, right, message in cases:
+            with pytest.raises(ValueError, match=message):
+                sim.mm(left.to(hip_device), right.to(hip_device))
+        assert sim._next_id == 0
+        assert bits_equal(sim.mm(a.to(hip_device), b.to(hip_device)), oracle.mm(a, b, cfg))
+
+
 def test_functional_reprogramming_follows_in_place_edits(hip_device):
     """Reused RHS programs take new codes in place and keep name and event counter."""
     from memfast_amd import Simulator
@@ -616,7 +644,7 @@ def test_stable_sum_matches_cpu_restore(hip_device, groups, width, c):
 
 
 # ---------------------------------------------------------------------------
-# Noisy devices on the bf16 MFMA kernel (reads of 32 or 64 rows)
+# Noisy devices on the fp16 MFMA kernel (hi + lo terms; reads of 32 or 64 rows)
 # ---------------------------------------------------------------------------
 MFMA_NOISY = {
     "write": (dict(), dict(write_variation=0.02)),
@@ -859,7 +887,135 @@ def test_bfp_exponent_edges_on_gpu(hip_device, reference_vectors):
 
 
 # ---------------------------------------------------------------------------
-# Wide configurations on the noisy-device bf16 MFMA kernel (mm_kernel 3)
+# FP64 currents (memfast/config.py:215-224 `precise_currents`): k_restore<double> and
+# k_general<double> against the reference's own vectors (tests/golden)
+# ---------------------------------------------------------------------------
+PRECISE = ["precise_slice9_ideal", "precise_slice9", "precise_close_ideal", "precise_close"]
+
+
+def _precise_case(v, name, device):
+    from conftest import fixture_config
+
+    cfg = fixture_config(v, name)
+    assert cfg.precise_currents
+    q = torch.from_numpy(v[f"case_{name}_q"])
+    packed = torch.from_numpy(v[f"case_{name}_packed"])
+    assert hip.mm_kernel(cfg, q.shape[0], q.shape[1], packed.shape[1]) == 0
+    return cfg, q, packed, int(v[f"case_{name}_seed"])
+
+
+def _pair_codes_closed_form(q, packed, cfg):
+    """Ideal ADC counts min(sum_r da*dw, max_w) per pair, [N, m*Gr, A, W, p*C]."""
+    n, m, r = q.shape
+    p, c = packed.shape[1], cfg.array_size[1]
+    rows, groups = cfg.read_rows, cfg.reads_per_array
+    maxima = cfg.adc_maxima
+    out = torch.zeros((n, m * groups, len(cfg.input_layout), len(cfg.weight_layout), p * c),
+                      dtype=torch.int64)
+    for ai, (sa, ma, _) in enumerate(cfg.input_layout):
+        da = (q.long() >> sa) & ma
+        for wi, (sw, mw, _) in enumerate(cfg.weight_layout):
+            dw = (packed.long() >> sw) & mw
+            for j in range(groups):
+                lo, hi = j * rows, min((j + 1) * rows, r)
+                s = torch.einsum("nir,itrc->nitc", da[:, :, lo:hi], dw[:, :, lo:hi])
+                out[:, j::groups, ai, wi] = s.clamp_max(maxima[wi]).reshape(n, m, p * c)
+    return out
+
+
+@pytest.mark.parametrize("name", PRECISE)
+def test_precise_partial_matches_reference_vectors(hip_device, reference_vectors, name):
+    """mf_partial's totals (k_general<double>) against the reference's at its seed and event:
+    bit for bit with ideal devices, where every per-pair ADC count is also the closed form
+    min(sum_r da*dw, max_w); with noise, given the reference's own FP64 conductances, identical
+    except rounding-boundary flips."""
+    v = reference_vectors
+    cfg, q, packed, seed = _precise_case(v, name, hip_device)
+    p = packed.shape[1]
+    reference = torch.from_numpy(v[f"case_{name}_totals"])
+    if cfg.nonidealities.ideal:
+        got, codes = hip.partial(q.to(hip_device), packed.to(hip_device), cfg, None, seed, 0, 0,
+                                 p, codes=True)
+        assert bits_equal(got, reference)
+        assert torch.equal(codes.cpu().long(), _pair_codes_closed_form(q, packed, cfg))
+        return
+    raw = torch.from_numpy(v[f"case_{name}_restored"])
+    assert raw.dtype == torch.float64
+    got = hip.partial(q.to(hip_device), packed.to(hip_device), cfg, None, seed, 0, 0, p,
+                      conductance=raw.to(hip_device))
+    differing, flipped, unexplained, mask = flips.count_flips(cfg, got.cpu(), reference)
+    codes = mask.numel() * len(cfg.input_layout) * len(cfg.weight_layout)
+    say("  precise", name, "injected:", differing, "differing totals,", flipped, "flips of", codes)
+    assert unexplained == 0
+    assert flipped <= max(1, 1e-4 * codes)
+
+
+@pytest.mark.parametrize("name", ["precise_slice9", "precise_close"])
+def test_precise_restore_close_to_reference(hip_device, reference_vectors, name):
+    """k_restore<double>: FP64 conductances with write and shared read noise against the
+    reference's restored tensor (same seed, event 0)."""
+    v = reference_vectors
+    cfg, q, packed, seed = _precise_case(v, name, hip_device)
+    got = hip.restore(packed.to(hip_device), cfg, seed, 0, 0, packed.shape[1])
+    assert got.dtype == torch.float64 and got.shape[0] == 1
+    expected = torch.from_numpy(v[f"case_{name}_restored"])
+    # The noise factors are FP32 (torch.exp of an FP32 normal); OCML's and torch CPU's
+    # transcendentals agree to an ulp or two of the factor (2.4e-7 relative).
+    ratio = got[0].cpu() / expected - 1
+    assert float(ratio.abs().max()) <= 2.4e-7
+
+
+@pytest.mark.parametrize("name", PRECISE)
+def test_precise_mm_matches_reference_vectors(hip_device, reference_vectors, name):
+    """Simulator.mm with FP64 currents for two read events against the reference's outputs:
+    bit for bit with ideal devices, flip-aware with noise (GPU-sampled conductances).
+
+    With high - low = 5e-5 of high (precise_close), one FP32 ulp of a noise factor moves g by
+    0.24% of high - low, so sampled codes are only as reproducible as the host's FP32
+    exp/log/cos: the reference's own restored tensor differs between two x86 hosts (this
+    test's and the fixture's).  There the bar is the injected one
+    (test_precise_partial_matches_reference_vectors), and the sampled product is checked
+    to be that read of its own samples: its totals equal mf_partial's with the GPU's restored
+    conductances injected, and its output is the reference epilogue of those totals."""
+    from memfast_amd import Simulator
+
+    v = reference_vectors
+    cfg, q, packed, seed = _precise_case(v, name, hip_device)
+    a = torch.from_numpy(v[f"case_{name}_a"]).to(hip_device)
+    b = torch.from_numpy(v[f"case_{name}_b"]).to(hip_device)
+    xs = torch.from_numpy(v[f"case_{name}_xscale"])
+    ws = torch.from_numpy(v[f"case_{name}_wscale"])
+    sim = Simulator(cfg, device=hip_device)
+    for event in (0, 1):
+        got = sim.mm(a, b)
+        ref = torch.from_numpy(v[f"case_{name}_out{event}"])
+        if cfg.nonidealities.ideal:
+            assert bits_equal(got, ref)
+            continue
+        totals = gpu_totals(q.to(hip_device), packed.to(hip_device), cfg, seed, event)
+        if name == "precise_close":
+            p = packed.shape[1]
+            own = hip.restore(packed.to(hip_device), cfg, seed, event, 0, p)
+            injected = hip.partial(q.to(hip_device), packed.to(hip_device), cfg, None, seed,
+                                   event, 0, p, conductance=own)
+            assert bits_equal(totals, injected)
+            epilogue = oracle.execute(q, xs, packed, ws, cfg, seed, event, b.shape[1],
+                                      totals=totals.cpu().to(injected.dtype)).to(got.dtype)
+            assert bits_equal(got, epilogue)
+            continue
+        if event == 0:
+            ref_totals = torch.from_numpy(v[f"case_{name}_totals"])
+        else:
+            ref_totals = oracle_totals(q, packed, cfg, seed, event)
+            ref = oracle.execute(q, xs, packed, ws, cfg, seed, event, b.shape[1],
+                                 totals=ref_totals).to(ref.dtype)
+        say("  precise", name, "event", event,
+            flips.check_noisy(cfg, got, ref, totals, ref_totals, xscale=xs, wscale=ws,
+                              label=f"precise {name} event {event}"))
+
+
+# ---------------------------------------------------------------------------
+# Wide configurations on the noisy-device fp16 MFMA kernel (mm_kernel 3)
 # ---------------------------------------------------------------------------
 WIDE_MFMA = {
     # BASELINE config 5's slicing: BFP16 x INT4, 64-row reads, 2-bit digits.

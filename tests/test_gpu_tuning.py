@@ -166,3 +166,30 @@ def test_tuned_layer_reuses_its_selection(hip_device, tmp_path):
         assert bits_equal(tuned(x), plain(x))
     assert len(tuned_sim.records) == 1 and tuned._event == plain._event == 3
     assert tuning.read_kernel(cfg, 96, 3, tuned.p) == 2
+
+
+def test_resources_follow_the_schedule(hip_device):
+    """mf_resources_query reports the instance a schedule launches, as the reference reads
+    each candidate's own compiled kernel (memfast/simulator.py:230-236): the ideal read's
+    64x64 and 128x64 tiles (k_ideal<1,1>, k_ideal<2,1>) and the wide read's LDS tiers."""
+    from memfast_amd import hip
+
+    ideal = Config(**INT8, nonidealities=Nonidealities(write_variation=0.0))
+    program = hip.program(ideal, 64, 64, hip_device.index)
+    tiles = {name: program.resources(ideal, 64, 64, 0, kernel=1,
+                                     variant=tuning.schedule_variant(dict(tile=name)))
+             for name in tuning.TILES}
+    say("ideal tiles", tiles)
+    assert tiles["64x64"]["registers"] != tiles["128x64"]["registers"]
+    assert tiles["64x64"]["shared"] < tiles["128x64"]["shared"]
+    wide = Config(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                  weight_slice=(1, 1, 2), bw_e=8, array_size=(64, 64), rows_per_read=64,
+                  adc_bits=(6, 6, 7), nonidealities=Nonidealities(write_variation=0.02))
+    program = hip.program(wide, 64, 64, hip_device.index)
+    tiers = {tier: program.resources(wide, 64, 64, 0, kernel=3,
+                                     variant=tuning.schedule_variant(dict(tier=tier)))
+             for tier in tuning.TIERS}
+    say("wide tiers", tiers)
+    assert tiers[1]["shared"] < tiers[2]["shared"] < tiers[3]["shared"]
+    # The automatic tier is the smallest that holds a read (3 weight slices x 2 terms x 4).
+    assert program.resources(wide, 64, 64, 0, kernel=3) == tiers[1]

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+from conftest import fixture_config
 from memfast_amd import Config, Nonidealities
 from oracle import oracle
 
@@ -199,7 +200,7 @@ def test_read_starts_and_padding():
 def test_reference_fixture_tiles(reference_vectors):
     v = reference_vectors
     for name in v["case_names"].tolist():
-        cfg = _cfg(name)
+        cfg = fixture_config(v, name)
         a = torch.from_numpy(v[f"case_{name}_a"])
         b = torch.from_numpy(v[f"case_{name}_b"])
         packed, wscale = oracle.weight_tiles(b.T, cfg)
@@ -210,13 +211,27 @@ def test_reference_fixture_tiles(reference_vectors):
         np.testing.assert_array_equal(xscale.numpy(), v[f"case_{name}_xscale"])
 
 
+def test_fixture_configs_match_the_case_table(reference_vectors):
+    """The configurations stored with the vectors are the ones this file's table names."""
+    v = reference_vectors
+    names = v["case_names"].tolist()
+    for name in names:
+        if not name.startswith("precise"):
+            assert repr(fixture_config(v, name)) == repr(_cfg(name)), name
+    precise = [name for name in names if name.startswith("precise")]
+    assert len(precise) == 4
+    for name in precise:
+        cfg = fixture_config(v, name)
+        assert cfg.precise_currents and oracle.precise_currents(cfg), name
+
+
 # ---------------------------------------------------------------------------
 # Array reads
 # ---------------------------------------------------------------------------
 def test_reference_fixture_reads(reference_vectors):
     v = reference_vectors
     for name in v["case_names"].tolist():
-        cfg = _cfg(name)
+        cfg = fixture_config(v, name)
         packed = torch.from_numpy(v[f"case_{name}_packed"])
         q = torch.from_numpy(v[f"case_{name}_q"])
         seed = int(v[f"case_{name}_seed"])
@@ -230,7 +245,7 @@ def test_reference_fixture_reads(reference_vectors):
 def test_reference_fixture_mm(reference_vectors):
     v = reference_vectors
     for name in v["case_names"].tolist():
-        cfg = _cfg(name)
+        cfg = fixture_config(v, name)
         a = torch.from_numpy(v[f"case_{name}_a"])
         b = torch.from_numpy(v[f"case_{name}_b"])
         np.testing.assert_array_equal(oracle.mm(a, b, cfg).numpy(), v[f"case_{name}_out0"])
@@ -244,17 +259,18 @@ def _brute_totals(brute, q, packed, cfg):
     il, wl = oracle.input_layout(cfg), oracle.weight_layout(cfg)
     gr = oracle.reads_per_array(cfg)
     out = np.zeros((n, m * gr, p, c), dtype=np.int64)
-    i32 = ctypes.c_int * len(il)
-    w32 = ctypes.c_int * len(wl)
-    i64a = ctypes.c_int64 * len(il)
-    i64w = ctypes.c_int64 * len(wl)
-    qn = np.ascontiguousarray(q.numpy())
-    pn = np.ascontiguousarray(packed.numpy())
-    brute.brute_ideal_totals(
+    ints = lambda values: (ctypes.c_int * len(values))(*values)
+    longs = lambda values: (ctypes.c_int64 * len(values))(*values)
+    wide = q.dtype != torch.uint8
+    dtype = np.int64 if wide else np.uint8
+    qn = np.ascontiguousarray(q.numpy().astype(dtype))
+    pn = np.ascontiguousarray(packed.numpy().astype(dtype))
+    entry = brute.brute_ideal_totals_wide if wide else brute.brute_ideal_totals
+    entry(
         qn.ctypes.data_as(ctypes.c_void_p), pn.ctypes.data_as(ctypes.c_void_p), n, m, p, r, c,
-        oracle.read_rows(cfg), len(il), i32(*[e[0] for e in il]), i32(*[e[1] for e in il]),
-        i64a(*[e[2] for e in il]), len(wl), w32(*[e[0] for e in wl]), w32(*[e[1] for e in wl]),
-        i64w(*[e[2] for e in wl]), w32(*oracle.adc_maxima(cfg)),
+        oracle.read_rows(cfg), len(il), ints([e[0] for e in il]), longs([e[1] for e in il]),
+        longs([e[2] for e in il]), len(wl), ints([e[0] for e in wl]), longs([e[1] for e in wl]),
+        longs([e[2] for e in wl]), longs(oracle.adc_maxima(cfg)),
         out.ctypes.data_as(ctypes.c_void_p),
     )
     return out
@@ -281,6 +297,24 @@ def test_ideal_partial_matches_closed_form_and_brute(brute, kwargs, shape):
     closed = oracle.ideal_totals_closed_form(q, packed, cfg)
     assert torch.equal(totals.long(), closed)
     assert np.array_equal(_brute_totals(brute, q, packed, cfg), closed.numpy())
+
+
+@pytest.mark.parametrize("name", ["precise_slice9_ideal", "precise_close_ideal"])
+def test_precise_ideal_fixtures_match_closed_form_and_brute(brute, reference_vectors, name):
+    """FP64 currents (a 9-bit slice; high - low < 1e-4 high) with ideal devices: the
+    reference's totals, the oracle's and the C brute force of min(sum da*dw, max) agree."""
+    v = reference_vectors
+    cfg = fixture_config(v, name)
+    q = torch.from_numpy(v[f"case_{name}_q"])
+    packed = torch.from_numpy(v[f"case_{name}_packed"])
+    reference = torch.from_numpy(v[f"case_{name}_totals"])
+    closed = oracle.ideal_totals_closed_form(q, packed, cfg)
+    assert torch.equal(reference.long(), closed) and torch.equal(reference, closed.to(reference.dtype))
+    totals = oracle.partial(q, packed, cfg, int(v[f"case_{name}_seed"]), 0, 0, packed.shape[1])
+    assert totals.dtype == reference.dtype and torch.equal(totals, reference)
+    assert np.array_equal(_brute_totals(brute, q, packed, cfg), closed.numpy())
+    # Clamping happens: the cases reach the ADC limits, so min() is exercised.
+    assert int(closed.abs().max()) > 0
 
 
 def test_dft_known_answer():
@@ -424,3 +458,86 @@ def test_zero_point_correction_closed_form(wide):
     torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-5)
     without = oracle.execute(q, xs, packed, wscale, cfg, 1, 0, o)
     assert (without.double() - expected).abs().max() > 1e-2
+
+
+def _boundary_case(**effects):
+    cfg = Config(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                 weight_slice=(1, 1, 2, 2, 2), array_size=(32, 16), rows_per_read=16,
+                 adc_bits=(6, 7, 7, 9, 9), nonidealities=Nonidealities(**effects))
+    gen = torch.Generator().manual_seed(62)
+    a = torch.randn(12, 70, generator=gen)
+    b = torch.randn(70, 40, generator=gen)
+    q, _ = oracle.input_tiles(a, cfg)
+    packed, _ = oracle.weight_tiles(b.T, cfg)
+    raw, _, _ = oracle.restored(packed, cfg, 11, 2, 0, packed.shape[1])
+    return cfg, q, packed, raw
+
+
+@pytest.mark.parametrize("effects", [
+    dict(write_variation=0.02, read_variation=0.01, adc_nonlinearity=0.1),
+    dict(write_variation=0.02, stuck_at_low=0.05, drift_coefficient=0.05, drift_time=100.0),
+])
+def test_exact_adc_arguments_round_to_the_oracle_codes(effects):
+    """flips.adc_arguments restates the ADC argument (memfast/reference.py:54-60, 96-115)
+    in exact arithmetic: rounding and clamping it gives the oracle's per-pair codes except
+    within FP32 rounding distance of a boundary.  Leaving out the S-curve, the 1/unit
+    scale or the low level moves hundreds of codes."""
+    from oracle import flips
+
+    cfg, q, packed, raw = _boundary_case(**effects)
+    p = packed.shape[1]
+    codes = {}
+    oracle.partial(q, packed, cfg, 11, 2, 0, p, conductance=raw, codes=codes)
+    y = flips.adc_arguments(q, packed, cfg, raw)
+    maxima = torch.tensor(cfg.adc_maxima, dtype=torch.float64)[None, None, None, :, None]
+    exact = torch.minimum(y.clamp(min=0), maxima).round()
+    distance = (y - y.floor() - 0.5).abs() / y.abs().clamp(min=1.0)
+    n, groups = q.shape[0], q.shape[1] * cfg.reads_per_array
+    mismatched = far = 0
+    for (ai, wi), count in codes.items():
+        count = count.reshape(n, groups, -1).double()
+        differs = count != exact[:, :, ai, wi]
+        mismatched += int(differs.sum())
+        far += int((differs & (distance[:, :, ai, wi] > 2.0**-18)).sum())
+    assert far == 0 and mismatched <= 2
+    # Planted mistakes in the restatement (no S-curve, another span or low level; the read
+    # voltage cancels) are caught by the same comparison.
+    for wrong in (dict(adc_nonlinearity=0.0), dict(high_conductance=1.1e-5),
+                  dict(low_conductance=2e-7)):
+        if "adc_nonlinearity" in wrong and not cfg.nonidealities.adc_nonlinearity:
+            continue
+        from dataclasses import replace
+
+        bad = replace(cfg, nonidealities=replace(cfg.nonidealities, **wrong)) \
+            if "adc_nonlinearity" in wrong else replace(cfg, **wrong)
+        moved = (torch.minimum(flips.adc_arguments(q, packed, bad, raw).clamp(min=0),
+                               maxima).round() != exact).sum()
+        assert int(moved) > 100, wrong
+
+
+def test_boundary_flips_accept_only_flips_at_rounding_boundaries():
+    """A planted flip of the pair nearest its rounding boundary is explained; one of a
+    pair far from every boundary is not."""
+    from oracle import flips
+
+    cfg, q, packed, raw = _boundary_case(write_variation=0.02, read_variation=0.01,
+                                         adc_nonlinearity=0.1)
+    p, c = packed.shape[1], cfg.array_size[1]
+    totals = oracle.partial(q, packed, cfg, 11, 2, 0, p, conductance=raw)
+    y = flips.adc_arguments(q, packed, cfg, raw)
+    maxima = torch.tensor(cfg.adc_maxima, dtype=torch.float64)[None, None, None, :, None]
+    inside = (y > 0) & (y < maxima)
+    distance = torch.where(inside, (y - y.floor() - 0.5).abs(), torch.full_like(y, 9.0))
+    n, groups = totals.shape[:2]
+    factors = [[fa * fw for _, _, fw in cfg.weight_layout] for _, _, fa in cfg.input_layout]
+    for pick, expect in ((distance.argmin(), True), ((distance - 0.25).abs().argmin(), False)):
+        v, g, a, w, col = np.unravel_index(int(pick), tuple(distance.shape))
+        moved = totals.clone().reshape(n, groups, -1)
+        moved[v, g, col] += factors[a][w]
+        differing, count, worst, unexplained = flips.boundary_flips(
+            cfg, moved.reshape(totals.shape), totals, y, 2.0**-18)
+        assert differing == 1
+        if expect:
+            assert count == 1 and not unexplained and worst <= 2.0**-18
+        else:
+            assert count == 0 and len(unexplained) == 1
