@@ -422,11 +422,14 @@ int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t 
 
 /* Resource figures (registers, scratch spill, LDS, resident blocks per CU) of the
  * read kernel instance mf_mm (mf_mm_wide) launches as `kernel_id` (mf_mm_kernel: 0
- * general, 1 ideal MFMA, 2 noisy MFMA, 3 wide noisy MFMA) under the schedule `variant`
- * (mf_mm's variant word: the ideal read's tile, the wide read's LDS tier).  Replaces the
- * per-candidate compiled-kernel attributes memfast/simulator.py:230-236 reads
- * (memfast/cuda.py:376-389). */
-int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int32_t variant,
+ * general, 1 ideal MFMA, 2 noisy MFMA, 3 wide noisy MFMA) for `n` input vectors (n <= 0:
+ * the instances of batches above 32) under the schedule `variant` (mf_mm's variant word:
+ * the ideal read's tile, the noisy read's split, the wide read's LDS tier).  A noisy read
+ * of at most 32 vectors is taken as split (the automatic schedule splits reads of fewer
+ * than 32768 output columns), the split the small-batch kernel k_noisy_pairs serves.
+ * Replaces the per-candidate compiled-kernel attributes memfast/simulator.py:230-236
+ * reads (memfast/cuda.py:376-389). */
+int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32_t variant,
                        mf_resources *out);
 
 /* ---- counter-based RNG (memfast/random.py:8-33), for parity tests -------- */

@@ -424,6 +424,16 @@ i64 noisy_voltage_bytes(const mf_config *cfg, i64 n, i64 m) {
     return cfg->has_vnoise ? align256(2 * i64(cfg->n_in) * vectors * m * cfg->rows * 2) : 0;
 }
 
+// Whether a split noisy read runs k_noisy_pairs (one wave per input slice, 32 vectors):
+// batches of at most 32 vectors, where the four-wave tile (64 vectors, the slices one
+// after another) would leave half its waves idle; plain and S-curve reads (no voltage,
+// slice_pair or output-mode noise).
+bool noisy_small_tile(const mf_config *cfg, i64 n) {
+    const bool per_read_noise = cfg->has_vnoise ||
+                                (cfg->has_read && cfg->read_mode != MF_READ_SHARED);
+    return n <= 32 && !per_read_noise;
+}
+
 // Fields of the `variant` word (include/memfast_hip.h).
 int variant_tile(int32_t v) { return v & 0xFF; }
 int variant_split(int32_t v) { return (v >> MF_MM_SPLIT_SHIFT) & 0xF; }
@@ -448,7 +458,7 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
                  const float *g, u32 seed, u64 event, float *out, i64 ldo, void *workspace,
                  i64 bytes, int totals, u32 *status, hipStream_t s, bool reuse = false,
                  i64 ocols = -1, i64 g_run = -1, int split_request = 0,
-                 const float **split_totals = nullptr) {
+                 const float **split_totals = nullptr, bool *split_restored = nullptr) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     if (ocols < 0) ocols = ncols;
     if (g_run < 0) g_run = G;
@@ -525,26 +535,39 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
             args.g_step = (g_run + split - 1) / split;
             gz = unsigned((g_run + args.g_step - 1) / args.g_step);
         }
-        const dim3 grid{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
         const bool nl = cfg->has_nonlinear != 0;
         const bool slice = plan.planes > 1 && !plan.out_noise;
+        // A split read of at most 32 vectors runs k_noisy_pairs: one read per workgroup,
+        // one wave per input slice.
+        const bool pairs = use_split && noisy_small_tile(cfg, n);
+        const dim3 grid = pairs ? dim3{unsigned(CB), unsigned((n + 31) / 32), unsigned(g_run)}
+                                : dim3{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
+        const dim3 block{pairs ? unsigned(64 * cfg->n_in) : 256u};
+        if (pairs) {
+            args.g_step = 1;
+            args.restored = 1;   // the values (float(T) * xs) * ws; consumers only sum them
+        }
         // Benchmark timing brackets the read kernel alone (not the conductance split).
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
         if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
 #define MF_NOISY_LAUNCH1(KS, NA, NL, VN, SL, ON) \
-    hipLaunchKernelGGL((k_noisy<KS, NA, NL, VN, SL, ON>), grid, dim3(256), 0, s, plan, args)
+    hipLaunchKernelGGL((k_noisy<KS, NA, NL, VN, SL, ON>), grid, block, 0, s, plan, args)
 #define MF_NOISY_LAUNCH2(KS, NA, VN, SL, ON)                    \
     {                                                          \
         if (nl) MF_NOISY_LAUNCH1(KS, NA, true, VN, SL, ON);    \
         else MF_NOISY_LAUNCH1(KS, NA, false, VN, SL, ON);      \
     }
-#define MF_NOISY_LAUNCH(KS, NA)                                                \
-    {                                                                         \
-        if (plan.out_noise) MF_NOISY_LAUNCH2(KS, NA, false, false, true)      \
-        else if (volt && slice) MF_NOISY_LAUNCH2(KS, NA, true, true, false)   \
-        else if (volt) MF_NOISY_LAUNCH2(KS, NA, true, false, false)           \
-        else if (slice) MF_NOISY_LAUNCH2(KS, NA, false, true, false)          \
-        else MF_NOISY_LAUNCH2(KS, NA, false, false, false)                    \
+#define MF_NOISY_LAUNCH(KS, NA)                                                                \
+    {                                                                                         \
+        if (pairs && nl)                                                                      \
+            hipLaunchKernelGGL((k_noisy_pairs<KS, NA, true>), grid, block, 0, s, plan, args);  \
+        else if (pairs)                                                                       \
+            hipLaunchKernelGGL((k_noisy_pairs<KS, NA, false>), grid, block, 0, s, plan, args); \
+        else if (plan.out_noise) MF_NOISY_LAUNCH2(KS, NA, false, false, true)                 \
+        else if (volt && slice) MF_NOISY_LAUNCH2(KS, NA, true, true, false)                   \
+        else if (volt) MF_NOISY_LAUNCH2(KS, NA, true, false, false)                           \
+        else if (slice) MF_NOISY_LAUNCH2(KS, NA, false, true, false)                          \
+        else MF_NOISY_LAUNCH2(KS, NA, false, false, false)                                    \
     }
         if (ks == 4) MF_NOISY_LAUNCH(4, 5)
         else if (cfg->n_in <= 5) MF_NOISY_LAUNCH(2, 5)
@@ -559,11 +582,13 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
     }
     // With split_totals the caller restores and sums a split read's totals [n, G, ncols]
     // itself (null when the read wrote `out`).
+    const bool restored = use_split && noisy_small_tile(cfg, n);   // k_noisy_pairs restored
     if (split_totals) *split_totals = use_split ? partial : nullptr;
+    if (split_restored) *split_restored = restored;
     if (use_split && !split_totals)
         hipLaunchKernelGGL(k_restore_sum_f32, dim3(grid_for(n * ocols)), dim3(256), 0, s, partial, n,
                            G, g_run, ncols, ocols, xscale, wscale, ncols, out, ldo, level_power(G),
-                           status);
+                           int(restored), status);
     return check_launch("noisy MFMA read");
 }
 
@@ -1345,13 +1370,14 @@ static i64 reads_with_rows(const mf_config *cfg, i64 m, i64 k_rows) {
 }
 
 // mf_mm; with `split_totals` a noisy MFMA read split across blocks leaves its totals to the
-// caller (*split_totals, [n, G, p*C]) instead of restoring them into `out` (null otherwise).
+// caller (*split_totals, [n, G, p*C]) instead of restoring them into `out` (null otherwise);
+// *split_restored says whether they are already restored ((float(T) * xs) * ws).
 static int mm_read(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n,
                    int64_t m, const uint8_t *packed, const uint8_t *packed_t, const float *wscale,
                    int64_t p, int64_t out_cols, int64_t k_rows, const void *g, uint32_t seed,
                    uint64_t event, float *out, int64_t ldo, void *workspace,
                    int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream,
-                   const float **split_totals) {
+                   const float **split_totals, bool *split_restored = nullptr) {
     if (split_totals) *split_totals = nullptr;
     const int valid = check_narrow(cfg);
     if (valid) return valid;
@@ -1403,7 +1429,7 @@ static int mm_read(const mf_config *cfg, const uint8_t *q, const float *xscale, 
         return launch_noisy(cfg, noisy, ks, q, xscale, n, m, packed_t, wscale, p, nullptr, seed,
                             event, out, ldo, workspace, workspace_bytes, 0, status, s,
                             (variant & MF_MM_REUSE_TERMS) != 0, out_cols, g_run,
-                            variant_split(variant), split_totals);
+                            variant_split(variant), split_totals, split_restored);
     }
     if (!g && needs_conductances(cfg))
         return fail(MF_E_INVALID, "device noise needs restored conductances (g)");
@@ -1694,9 +1720,11 @@ int mf_gru_sequence(const mf_config *cfg, int64_t steps, int32_t reverse, int64_
         // later reads of the same program reuse them.
         const int32_t v = i == 0 ? variant : (variant | MF_MM_REUSE_TERMS);
         const float *totals = nullptr;
+        bool restored = false;
         rc = mm_read(cfg, q, xscale, batch, m, packed, packed_t, wscale, p, 3 * width, width,
                      nullptr, seed, event0 + uint64_t(i), hidden, ld_hidden, workspace,
-                     workspace_bytes, v, status, stream, fused ? &totals : nullptr);
+                     workspace_bytes, v, status, stream, fused ? &totals : nullptr,
+                     fused ? &restored : nullptr);
         if (rc) return rc;
         if (fused) {
             GruStepArgs a{};
@@ -1705,6 +1733,7 @@ int mf_gru_sequence(const mf_config *cfg, int64_t steps, int32_t reverse, int64_
             a.hidden = hidden;
             a.ldh = ld_hidden;
             a.totals = totals;
+            a.restored = restored;
             a.G = G;
             a.g_run = reads_with_rows(cfg, m, width);
             a.ldt = ncols;
@@ -2032,7 +2061,7 @@ int mf_profile_collect(int64_t *launches, double *milliseconds) {
     return status;
 }
 
-int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int32_t variant,
+int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32_t variant,
                        mf_resources *out) {
     int status = check_config(cfg);
     if (status) return status;
@@ -2045,6 +2074,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int32_t variant,
     const bool ks4 = cfg->read_rows == 64;
     const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
     const void *fn = nullptr;
+    int threads = 256;
     if (kernel_id == 1) {
         // 32-row reads: 32 or (tile field 1) 64 vectors per wave; 64-row reads: KS 2.
         if (ks4) fn = reinterpret_cast<const void *>(&k_ideal<1, 2>);
@@ -2071,6 +2101,20 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int32_t variant,
         const int mode = output_noise ? 2 : (cfg->has_vnoise ? 1 : 0);
         const bool slice = cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR;
         fn = table[which][mode][slice ? 1 : 0][nl ? 1 : 0];
+        if (n > 0 && noisy_small_tile(cfg, n) && variant_split(variant) != 1) {
+            // A split read of at most 32 vectors (the automatic split applies below 512
+            // four-wave blocks, 32768 output columns): k_noisy_pairs, one wave per input
+            // slice.
+            const void *pairs[3][2] = {
+                {reinterpret_cast<const void *>(&k_noisy_pairs<2, 5, false>),
+                 reinterpret_cast<const void *>(&k_noisy_pairs<2, 5, true>)},
+                {reinterpret_cast<const void *>(&k_noisy_pairs<2, 8, false>),
+                 reinterpret_cast<const void *>(&k_noisy_pairs<2, 8, true>)},
+                {reinterpret_cast<const void *>(&k_noisy_pairs<4, 5, false>),
+                 reinterpret_cast<const void *>(&k_noisy_pairs<4, 5, true>)}};
+            fn = pairs[which][nl ? 1 : 0];
+            threads = 64 * cfg->n_in;
+        }
     } else if (kernel_id == 3) {
         // The LDS tier: the schedule's (tier field 1-3), else the smallest that holds a read.
         const int frags = cfg->n_w * NOISY_TERMS * (ks4 ? 4 : 2);
@@ -2104,12 +2148,12 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int32_t variant,
     const hipError_t e = hipFuncGetAttributes(&attr, fn);
     if (e != hipSuccess) return fail(MF_E_HIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
     memset(out, 0, sizeof(*out));
-    out->threads = 256;
+    out->threads = threads;
     out->shared_bytes = int32_t(attr.sharedSizeBytes);
     out->registers = attr.numRegs;
     out->local_bytes = int32_t(attr.localSizeBytes);
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) == hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, threads, 0) == hipSuccess)
         out->max_blocks_per_cu = blocks;
     if (blocks == 0) return fail(MF_E_RESOURCE, "zero resident blocks");
     return MF_OK;

@@ -180,6 +180,7 @@ struct NoisyArgs {
     const uint4 *volt;
     u64 read_seed;        // output-mode read noise: event_seed(seed, event)
     i64 C;                // array columns (output-mode noise addresses)
+    int restored;         // k_noisy_pairs: write (float(T) * xs) * ws instead of float(T)
 };
 
 // Terms are k1[w] * (g - L), so the read's MFMA output is in ADC counts.
@@ -189,6 +190,12 @@ __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, co
                                      i64 CB, const NoisyPlan plan, uint4 *gs);
 template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
+// Split read of batches of at most 32 vectors: block = one wave per input slice on 32
+// vectors x 32 columns and one read (grid: column blocks, vector blocks, reads); writes
+// slice totals [n, G, ldo], or with args.restored the restored (float(T) * xs) * ws
+// (plain and S-curve reads).
+template <int KS, int NA, bool NONLINEAR>
+__global__ void k_noisy_pairs(const NoisyPlan plan, const NoisyArgs args);
 // Input operands of a read with voltage variation (memfast/reference.py:77-82): per
 // input slice a, vector v and physical row k, digit * (1 + vv * z(address)) split into
 // fp16 hi + lo.  Layout [2][A][ceil(n/32)][kp/8][32] of uint4 (8 rows each): the 32
@@ -198,9 +205,10 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
                                 u64 event, uint4 *volt);
 // (float(T) * xs) * ws summed over reads in torch's cascade order, from slice
 // totals [n, G, ldt]: the epilogue of a read split across blocks.
+// With `restored` the values are already (float(T) * xs) * ws and are only summed.
 __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, i64 ldt,
                                   i64 ncols, const float *xscale, const float *wscale, i64 ldws,
-                                  float *out, i64 ldo, int lp, u32 *status);
+                                  float *out, i64 ldo, int lp, int restored, u32 *status);
 
 // ---- noisy-device MFMA read, wide configurations (noisy_wide.hip) ----------
 // Same ADC model as NoisyPlan; integer totals accumulate modulo 2^32 as
@@ -270,7 +278,8 @@ struct GruStepArgs {
     i64 ldi;
     const float *hidden;        // the hidden read's output [B, 3H] (when totals is null)
     i64 ldh;
-    const float *totals;        // split read: integer totals [B, G, ldt]
+    const float *totals;        // split read: integer totals [B, G, ldt], or with restored
+    int restored;               // set, the values (float(T) * xs) * ws
     i64 G, g_run, ldt;
     int lp;                     // level power of the read-order cascade
     const float *xscale_in;     // [B, G] scales of the read's input codes

@@ -569,6 +569,112 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
+// Split reads of small batches (at most 32 vectors): one workgroup per (32-column block,
+// read) with one wave per input slice, so a read's 25 pairs (config 3) run on five waves at
+// once instead of one after another.  Each wave builds its slice's digits once and converts
+// its pairs with every weight slice (fa*fw*(0x400000 + code) modulo 2^32, as noisy_read),
+// the waves add their words in LDS (integer sums: any order gives the same totals) and the
+// block writes the read's slice totals [n, G, ldo], or with args.restored their scale
+// restore (float(T) * xs) * ws rounded as the fused epilogue rounds it; k_restore_sum_f32
+// or k_gru_step sums them over the reads in torch's order.  Plain and S-curve reads (terms
+// event-independent or shared read noise).
+template <int KS, int NA, bool NONLINEAR>
+__global__ __launch_bounds__(512) void k_noisy_pairs(const NoisyPlan plan, const NoisyArgs args) {
+    const float MAGIC = 12582912.0f;   // 1.5 * 2^23
+    constexpr int P = 16 * KS;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int a = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's input slice
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int W = plan.n_w, A = plan.n_in;
+    const i64 cb = blockIdx.x;                       // chunk-relative 32-column block
+    const i64 v0 = i64(blockIdx.y) * 32;
+    const int g = int(args.g_begin + blockIdx.z);
+    const i64 G = args.G, kp = args.kp;
+    const i64 vrows = (args.n - v0) < 32 ? (args.n - v0) : 32;
+    const __amdgpu_buffer_rsrc_t qbuf = noisy_buffer(args.q + v0 * kp, vrows * kp);
+    const int q_off = lrow * int(kp) + lhalf * 8 + g * P;
+    // Terms of (weight slice w, column block cb, read g): [w][CB][G][term][KS][64 lanes].
+    const uint4 *frag = args.gs + (cb * G + g) * NOISY_TERMS * KS * 64 + lane;
+    const i64 w_stride = args.CB * G * NOISY_TERMS * KS * 64;
+    auto load_terms = [&](v8h (&F)[NOISY_TERMS][KS], int w) {
+#pragma unroll
+        for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                F[term][ks] = __builtin_bit_cast(v8h, frag[w * w_stride + (term * KS + ks) * 64]);
+    };
+    v8h Fa[NOISY_TERMS][KS], Fb[NOISY_TERMS][KS];
+    load_terms(Fa, 0);
+    v8h digits[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const u32 x = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16, 0, 0);
+        const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16 + 4, 0, 0);
+        digits[ks] = digits_f16(make_uint2(x, y), plan.in_shift[a], plan.in_mask4[a]);
+    }
+    u32 Ti[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Ti[r] = 0u;
+    // The MFMA order of noisy_read (terms outer, row blocks inner), so the totals are its
+    // totals bit for bit.
+    auto pair = [&](const v8h (&F)[NOISY_TERMS][KS], int w) {
+        v16f I = {};
+#pragma unroll
+        for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], digits[ks], I, 0, 0, 0);
+        const float top = plan.top_magic[w], alpha = plan.alpha[w];
+        const u32 f24 = u32(int(plan.f24[a][w] << 8) >> 8);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float y = (NONLINEAR ? scurve(I[r], alpha) : I[r]) + MAGIC;
+            y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
+            const int low = int(__float_as_uint(y) << 8) >> 8;
+            Ti[r] += u32(low) * f24;
+        }
+    };
+    // Weight slices in pairs, the next slice's terms in flight during a slice's pair.
+    int w = 0;
+    for (; w + 1 < W; w += 2) {
+        load_terms(Fb, w + 1);
+        pair(Fa, w);
+        if (w + 2 < W) load_terms(Fa, w + 2);
+        pair(Fb, w + 1);
+    }
+    if (w < W) pair(Fa, w);
+    // Sum the slices' words: wave a writes its plane, then wave a adds outputs r = a, a + A..
+    __shared__ u32 planes[8][16][64];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) planes[a][r][lane] = Ti[r];
+    __syncthreads();
+    const i64 n_out = v0 + lrow;
+    const i64 col_tile = args.c_begin + cb * 32;
+    const float xs = args.restored && n_out < args.n ? args.xscale[n_out * G + g] : 0.0f;
+    for (int r = a; r < 16; r += A) {
+        u32 total = plan.bias;
+        for (int j = 0; j < A; ++j) total += planes[j][r][lane];
+        const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+        if (n_out < args.n && c < args.ncols) {
+            float v = float(int(total));
+            if (args.restored) {
+                v = v * xs;
+                v = v * args.wscale[i64(g) * args.ldws + c];
+            }
+            args.out[(n_out * G + g) * args.ldo + c] = v;
+        }
+    }
+}
+
+#define MF_PAIRS_INST(KS, NA)                                                                  \
+    template __global__ void k_noisy_pairs<KS, NA, false>(const NoisyPlan, const NoisyArgs);  \
+    template __global__ void k_noisy_pairs<KS, NA, true>(const NoisyPlan, const NoisyArgs);
+MF_PAIRS_INST(2, 5)
+MF_PAIRS_INST(2, 8)
+MF_PAIRS_INST(4, 5)
+#undef MF_PAIRS_INST
+
 // The read kernel.  The output-mode variant (16 in-kernel normals per pair) runs three waves
 // per SIMD at 32-row reads (a few spilled registers cost less than a wave fewer) and one at
 // 64-row reads, which hold two slices' terms.
@@ -581,7 +687,7 @@ __global__ __launch_bounds__(256, OUTN ? (KS == 2 ? 3 : 1) : (KS == 2 && NA <= 5
 
 __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, i64 ldt,
                                   i64 ncols, const float *xscale, const float *wscale, i64 ldws,
-                                  float *out, i64 ldo, int lp, u32 *status) {
+                                  float *out, i64 ldo, int lp, int restored, u32 *status) {
     // Reads arrive in batches of RESTORE_BATCH: a batch's loads are all issued before
     // its values enter the cascade, so a thread waits on memory once per batch rather
     // than once per read.  The arithmetic and the summation order are unchanged.
@@ -601,14 +707,19 @@ __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, 
             for (int j = 0; j < RESTORE_BATCH; ++j) {
                 const i64 g = g0 + j < g_run ? g0 + j : g_run - 1;   // past the end: unused
                 t[j] = tv[g * ldt];
-                xs[j] = xv[g];
-                ws[j] = wv[g * ldws];
+                if (!restored) {
+                    xs[j] = xv[g];
+                    ws[j] = wv[g * ldws];
+                }
             }
 #pragma unroll
             for (int j = 0; j < RESTORE_BATCH; ++j) {
                 if (g0 + j < g_run) {
-                    float x = t[j] * xs[j];
-                    x = x * ws[j];
+                    float x = t[j];
+                    if (!restored) {
+                        x = x * xs[j];
+                        x = x * ws[j];
+                    }
                     cascade.push(x, lp);
                 }
             }

@@ -46,59 +46,93 @@ __global__ __launch_bounds__(256) void k_gru_gates(const float *inputs, i64 ldi,
     if (!finite && status) atomicOr(status, flag);
 }
 
+// The hidden projection values of columns c0 and c1 of row b: the split read's values summed
+// over its reads in torch's cascade order, BATCH reads' loads at a time (RESTORED: the
+// values are already (float(T) * xs) * ws; else they are integer totals restored here).
+template <bool RESTORED, int BATCH>
+__device__ __forceinline__ void restore_columns(const GruStepArgs &a, i64 b, i64 c0, i64 c1,
+                                                float (&v)[2]) {
+    Cascade<float> cascade[2];
+    cascade[0].reset();
+    cascade[1].reset();
+    const float *tv = a.totals + b * a.G * a.ldt;
+    const float *xv = a.xscale_in + b * a.G;
+    const i64 cc[2] = {c0, c1};
+    for (i64 g0 = 0; g0 < a.g_run; g0 += BATCH) {
+        float tt[2][BATCH], ws[2][BATCH], xs[BATCH];
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const i64 g = g0 + j < a.g_run ? g0 + j : a.g_run - 1;   // past the end: unused
+            if (!RESTORED) xs[j] = xv[g];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                tt[k][j] = tv[g * a.ldt + cc[k]];
+                if (!RESTORED) ws[k][j] = a.wscale[g * a.ldws + cc[k]];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            if (g0 + j < a.g_run) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    float x = tt[k][j];
+                    if (!RESTORED) {
+                        x = x * xs[j];
+                        x = x * ws[k][j];
+                    }
+                    cascade[k].push(x, a.lp);
+                }
+            }
+        }
+    }
+    v[0] = cascade[0].finish();
+    v[1] = cascade[1].finish();
+}
+
 // k_restore_sum_f32, k_gru_gates and k_row_groups_wave of one step in one launch, one
 // workgroup of 1024 threads per batch row, bit for bit their results:
-// 1. each hidden projection value is (float(T) * xs) * ws summed over the reads in torch's
-//    cascade order (Cascade<float>; loads issued a batch of reads at a time), or read from
-//    the fused read's output, into LDS (3H floats, dynamic shared memory);
+// 1. each hidden projection value is (float(T) * xs) * ws (or the read's already restored
+//    values) summed over the reads in torch's cascade order (Cascade<float>; loads issued a
+//    batch of reads at a time), or read from the fused read's output, into LDS (3H floats,
+//    dynamic shared memory);
 // 2. the gates as k_gru_gates (bias first; FP32 in PyTorch's order);
 // 3. the new state's row is one quantization group: its peak (fmaxf, NaN ignored) gives
 //    the scale, every read of the row gets it, codes past H are zero.
 // Flags: a non-finite hidden value (restore) or biased sum sets MF_STATUS_OUTPUT; a
 // non-finite new state sets MF_STATUS_INPUT when it is quantized.
 __global__ __launch_bounds__(1024) void k_gru_step(const GruStepArgs a) {
-    constexpr int BATCH = 8;
+    // A thread restores columns c and c + 1024 together, so the loads of both columns share
+    // each round trip (config 3: 3H = 1536, 16 restored reads: one).
     extern __shared__ float hid[];   // [3H]
     __shared__ float wave_peak[16];
     const i64 b = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const i64 H = a.width;
     bool out_finite = true, state_finite = true;
-    for (i64 c = t; c < 3 * H; c += 1024) {
-        float v;
+    for (i64 c0 = t; c0 < 3 * H; c0 += 2048) {
+        const i64 c1 = c0 + 1024;
+        const bool two = c1 < 3 * H;
+        float v[2];
         if (!a.totals) {
-            v = a.hidden[b * a.ldh + c];
+            v[0] = a.hidden[b * a.ldh + c0];
+            v[1] = two ? a.hidden[b * a.ldh + c1] : 0.0f;
+        } else if (a.restored) {
+            restore_columns<true, 16>(a, b, c0, two ? c1 : c0, v);   // a missing c1 rereads c0
         } else {
-            Cascade<float> cascade;
-            cascade.reset();
-            const float *tv = a.totals + b * a.G * a.ldt + c;
-            const float *xv = a.xscale_in + b * a.G;
-            for (i64 g0 = 0; g0 < a.g_run; g0 += BATCH) {
-                float tt[BATCH], xs[BATCH], ws[BATCH];
+            restore_columns<false, 8>(a, b, c0, two ? c1 : c0, v);
+        }
 #pragma unroll
-                for (int j = 0; j < BATCH; ++j) {
-                    const i64 g = g0 + j < a.g_run ? g0 + j : a.g_run - 1;   // past the end: unused
-                    tt[j] = tv[g * a.ldt];
-                    xs[j] = xv[g];
-                    ws[j] = a.wscale[g * a.ldws + c];
-                }
-#pragma unroll
-                for (int j = 0; j < BATCH; ++j) {
-                    if (g0 + j < a.g_run) {
-                        float x = tt[j] * xs[j];
-                        x = x * ws[j];
-                        cascade.push(x, a.lp);
-                    }
-                }
+        for (int k = 0; k < 2; ++k) {
+            if (k == 1 && !two) break;
+            const i64 c = k ? c1 : c0;
+            float x = v[k];
+            if (a.totals) out_finite = out_finite && fabsf(x) <= FLT_MAX;
+            if (a.bias) {
+                x = x + a.bias[c];
+                out_finite = out_finite && fabsf(x) <= FLT_MAX;
             }
-            v = cascade.finish();
-            out_finite = out_finite && fabsf(v) <= FLT_MAX;
+            hid[c] = x;
         }
-        if (a.bias) {
-            v = v + a.bias[c];
-            out_finite = out_finite && fabsf(v) <= FLT_MAX;
-        }
-        hid[c] = v;
     }
     if (!out_finite && a.status) atomicOr(a.status, u32(MF_STATUS_OUTPUT));
     // Also orders this row's restore reads of xscale_in before the writes of xscale_out below.

@@ -178,7 +178,7 @@ SIGNATURES = {
     "mf_profile_collect": ([ct.POINTER(_I64), ct.POINTER(ct.c_double)], ct.c_int),
     "mf_mm_workspace": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I64)], ct.c_int),
     "mf_mm_kernel": ([_CFG, _I64, _I64, _I64, _I32, ct.POINTER(_I32)], ct.c_int),
-    "mf_resources_query": ([_CFG, _I32, _I32, ct.POINTER(MFResources)], ct.c_int),
+    "mf_resources_query": ([_CFG, _I32, _I64, _I32, ct.POINTER(MFResources)], ct.c_int),
     "mf_rng_uniform": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
     "mf_rng_normal": ([_P, _I64, ct.c_uint64, ct.c_uint32, _P, _P], ct.c_int),
 }
@@ -1160,15 +1160,17 @@ class Program:
         self.vectors = vectors
         self.columns = columns
 
-    def resources(self, config, vectors, columns, workers, kernel=None, variant=0):
+    def resources(self, config, vectors, columns, workers, kernel=None, variant=0, batch=0):
         """Resources of the instance of read kernel ``kernel`` (mf_mm_kernel's id; by default
-        the ideal MFMA read for ideal devices, else the general one) that mf_mm launches under
-        the schedule word ``variant`` (variant_word)."""
+        the ideal MFMA read for ideal devices, else the general one) that mf_mm launches for
+        ``batch`` input vectors (0: a batch above 32) under the schedule word ``variant``
+        (variant_word).  ``vectors``, ``columns`` and ``workers`` are the reference's launch
+        keys, which the gfx950 kernels do not use."""
         info = MFResources()
         if kernel is None:
             kernel = 1 if config.nonidealities.ideal else 0
-        check(library().mf_resources_query(ct.byref(descriptor(config)), kernel, variant,
-                                           ct.byref(info)), "resources")
+        check(library().mf_resources_query(ct.byref(descriptor(config)), kernel, batch,
+                                           variant, ct.byref(info)), "resources")
         return dict(threads=info.threads, shared=info.shared_bytes, local_bytes=info.local_bytes,
                     registers=info.registers)
 

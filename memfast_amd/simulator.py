@@ -383,7 +383,7 @@ class Simulator:
             resource = hip.program(c, schedule["vectors"], schedule["columns"],
                                    self.device.index).resources(
                 c, schedule["vectors"], schedule["columns"], schedule["workers"], kernel=kernel,
-                variant=tuning.schedule_variant(schedule))
+                variant=tuning.schedule_variant(schedule), batch=n)
         # The output-noise MFMA read at 32-row reads keeps part of its state in scratch by
         # design (three waves per SIMD with spills run faster than two without), and its
         # registers do not depend on the schedule; the policy refuses any other spill.

@@ -704,6 +704,33 @@ def packed_columns(packed):
     return packed.permute(1, 3, 0, 2).reshape(p * c, m * r).contiguous()
 
 
+@pytest.mark.parametrize("mode", ["write", "shared_scurve", "saf_drift", "binary8", "rows64"])
+def test_small_batch_split_read_matches_unsplit_read(hip_device, mode):
+    """Batches of at most 32 vectors split their reads over k_noisy_pairs (one workgroup per
+    read and 32-column block, one wave per input slice; the restored values are summed by
+    the split epilogue).  Every schedule (automatic, unsplit k_noisy, a 2-way split) gives
+    the same output bit for bit: 32- and 64-row reads, 5 and 8 input slices, S-curve ADCs;
+    and the product is the oracle's under the flip accounting."""
+    cfg = noisy_case(mode)
+    gen = torch.Generator().manual_seed(34)
+    for n in (1, 7, 32):
+        a = torch.randn(n, 500, generator=gen)
+        b = torch.randn(500, 300, generator=gen)
+        q, xs = hip.input_tiles(a.to(hip_device), cfg)
+        packed, packed_t, ws = hip.weight_tiles(b.T.to(hip_device), cfg)
+        m, p, c = q.shape[1], packed.shape[1], cfg.array_size[1]
+        assert hip.mm_kernel(cfg, n, m, p) == 2
+        outputs = [hip.mm(q, xs, packed, packed_t, ws.reshape(-1, p * c), cfg, 4242, 3,
+                          variant=hip.variant_word(split=split)) for split in (0, 1, 2)]
+        say("  small batch", mode, n, "automatic, 2-way split vs unsplit",
+            bits_equal(outputs[0], outputs[1]), bits_equal(outputs[2], outputs[1]))
+        assert bits_equal(outputs[0], outputs[1]) and bits_equal(outputs[2], outputs[1])
+    from memfast_amd import Simulator
+
+    got = Simulator(cfg, device=hip_device).mm(a.to(hip_device), b.to(hip_device))
+    check_product(cfg, got, a, b, hip_device, label=f"small batch {mode}")
+
+
 @pytest.mark.parametrize("mode", list(MFMA_NOISY))
 def test_noisy_mfma_totals_with_injected_conductances(hip_device, mode):
     """Same slice totals as the oracle given the same conductances, except ADC flips."""
