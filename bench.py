@@ -32,13 +32,22 @@ INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, tera-ops/s
 FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, TFLOP/s (the noisy read's precision)
 HBM_PEAK_GBS = 8000.0
 
-# HBM bytes per launch of the read kernel on this workload, from two rocprofv3
-# --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the
-# same counters read for a 256 MiB device copy (FETCH x1.99974, WRITE x1.0):
-# 227.3 MiB read + 64.0 MiB written.  Summary and commands:
-# profiles/k_ideal_config2_pmc.md.  Only valid for the kernel sources it was
+# HBM bytes per launch of the read kernels on this workload (ideal: k_ideal; noisy:
+# k_noisy), from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB per
+# dispatch) scaled by what the same counters read for a 256 MiB device copy in the same
+# runs.  Summaries and commands: profiles/k_ideal_config2_pmc.md and
+# profiles/k_noisy_config2_noisy_pmc.md.  Only valid for the kernel sources they were
 # measured on (hash prefix below); otherwise the bench reports null.
-MEASURED_TRAFFIC = dict(kernels="4ae5c7b0020c4b5f", bytes=298468977)
+MEASURED_TRAFFIC = dict(kernels="4ae5c7b0020c4b5f", ideal=298468977, noisy=None)
+
+
+def measured_traffic(leg):
+    """HBM bytes per launch of the leg's read kernel, if measured on these kernel sources."""
+    from memfast_amd import hip
+
+    if MEASURED_TRAFFIC["kernels"] != hip.native_source_hash()[:16]:
+        return None
+    return MEASURED_TRAFFIC[leg]
 
 
 def cpu_model():
@@ -342,6 +351,11 @@ def main():
     from memfast_amd import hip
 
     device = torch.device("cuda", 0)
+    if args.copy_calibration > 0:
+        source = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device=device)
+        torch.empty_like(source).copy_(source)
+        torch.cuda.synchronize()
+        del source
     if args.secondary_only:
         names = set(args.secondary_only.split(","))
         print(json.dumps(dict(secondary=secondary(device, only=names))), flush=True)
@@ -351,11 +365,6 @@ def main():
     b_cpu = torch.randn(SIZE, SIZE)
     a = a_cpu.to(device)
     b = b_cpu.to(device)
-    if args.copy_calibration > 0:
-        source = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device=device)
-        torch.empty_like(source).copy_(source)
-        torch.cuda.synchronize()
-        del source
     ideal_cfg = memfast.Config(**BASE, nonidealities=memfast.Nonidealities(write_variation=0.0))
     sim = memfast.Simulator(ideal_cfg, device=device)
     ms_step, kernel_ms = time_steps(lambda: sim.mm(a, b), args.steps, args.warmup)
@@ -379,7 +388,7 @@ def main():
             config="write_variation=0.02, read_variation=0.01 shared, adc_nonlinearity=0.1",
             roofline=dict(bound="mfma", achieved=round(noisy_achieved, 2), peak=FP16_PEAK_TFLOPS,
                           unit="TFLOP/s", frac=round(noisy_achieved / FP16_PEAK_TFLOPS, 4),
-                          traffic=None,
+                          traffic=measured_traffic("noisy"),
                           note="2 flops per slice-MAC (25 pairs) / k_noisy time (HIP events "
                                "on its stream, the conductance split excluded); the hardware "
                                "issues two fp16 MFMAs (hi and lo conductance terms) per "
@@ -409,7 +418,7 @@ def main():
         )
 
     kernels = hip.native_source_hash()[:16]
-    traffic = MEASURED_TRAFFIC["bytes"] if MEASURED_TRAFFIC["kernels"] == kernels else None
+    traffic = measured_traffic("ideal")
     line = dict(
         metric="effective GMAC/s, Simulator.mm 4096^3 INT8 (1,1,2,2,2)",
         value=round(value, 3),

@@ -227,3 +227,66 @@ def test_config4_resnet18_batch_permutation(hip_device):
         permuted = analog(images[perm])
     assert logits.shape == (64, 1000) and torch.isfinite(logits).all()
     assert bits_equal(permuted, logits[perm])
+
+
+# ---------------------------------------------------------------------------
+# Config 5: LLM decoder linear shapes, BFP16 inputs (bw_e 8) x INT4 weights, drift + read noise
+# ---------------------------------------------------------------------------
+CONFIG5 = dict(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+               weight_slice=(1, 1, 2), bw_e=8, adc_bits=(6, 6, 7))
+CONFIG5_NOISE = Nonidealities(read_variation=0.01, drift_coefficient=0.05, drift_time=100.0)
+
+
+def _config5_tokens(tokens, features, seed):
+    """Activations randn with 1% outlier channels x20."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(tokens, features, generator=gen)
+    x[:, torch.randperm(features, generator=gen)[:features // 100]] *= 20
+    return x
+
+
+@pytest.mark.parametrize("mode", ["default", "tuned"])
+def test_config5_up_proj_full_size_row_permutation(hip_device, tmp_path, mode):
+    """The up/gate projection at full size (2048 tokens, 4096 -> 11008) on the wide MFMA
+    read.  Input groups are per row (input_quant_gran (1, None)) and the read noise is keyed
+    by cell and read event, so permuting the tokens permutes the output rows bit for bit:
+    every row is computed at its new position with the same codes, scales and noise."""
+    cfg = Config(**CONFIG5, nonidealities=CONFIG5_NOISE)
+    x = _config5_tokens(2048, 4096, 55)
+    gen = torch.Generator().manual_seed(56)
+    w = torch.randn(4096, 11008, generator=gen) * 0.02
+    rows, cols = cfg.array_size
+    assert hip.mm_kernel(cfg, 2048, 4096 // rows, 11008 // cols) == 3
+    perm = torch.randperm(2048, generator=gen)
+    x_dev, w_dev = x.to(hip_device), w.to(hip_device)
+    kwargs = dict(mode="tuned", cache_dir=tmp_path) if mode == "tuned" else {}
+    say("config5 up_proj 2048x4096 @ 4096x11008", mode)
+    out = Simulator(cfg, device=hip_device, **kwargs).mm(x_dev, w_dev)
+    permuted = Simulator(cfg, device=hip_device, **kwargs).mm(x_dev[perm.to(hip_device)], w_dev)
+    torch.cuda.synchronize()
+    assert out.shape == (2048, 11008) and bool(torch.isfinite(out).all())
+    assert bits_equal(permuted, out[perm.to(hip_device)])
+    assert not bits_equal(permuted, out)
+
+
+def test_config5_down_proj_rows_against_oracle(hip_device):
+    """The down projection (11008 -> 4096) at full K: sampled rows of the GPU product against
+    the oracle's read of the same rows (its own conductance samples), flip-aware, in the
+    first and last two-tile chunks of columns."""
+    cfg = Config(**CONFIG5, nonidealities=CONFIG5_NOISE)
+    x = _config5_tokens(64, 11008, 57)
+    gen = torch.Generator().manual_seed(58)
+    w = torch.randn(11008, 4096, generator=gen) * 0.02
+    out = Simulator(cfg, device=hip_device).mm(x.to(hip_device), w.to(hip_device))
+    rows = torch.tensor([0, 17, 63])
+    q, xs = oracle.input_tiles(x[rows], cfg)
+    packed, ws = oracle.weight_tiles(w.T, cfg)
+    seed = oracle.name_seed(cfg.seed, "matrix.0")
+    totals = gpu_totals(q.to(hip_device), packed.to(hip_device), cfg, seed, 0)
+    got = out[rows.to(hip_device)].cpu()
+    c = cfg.array_size[1]
+    p = packed.shape[1]
+    for first in (0, p - 2):
+        tiles = (first, first + 2)
+        check_read(cfg, got[:, first * c:(first + 2) * c], q, xs, packed, ws, seed, 0, totals,
+                   tiles=tiles, label=f"config5 down_proj rows, tiles {tiles}")
