@@ -180,8 +180,9 @@ def _ideal_input_cases(out, device):
 def _read_modes(out, device):
     """Config 2's array shape at 4096^3 with the other noise forms, all on the noisy MFMA
     read: per-slice-pair read noise (a plane of terms per input slice), output-mode read
-    noise (mean and variance sums, a normal per conversion) and voltage noise (real input
-    operands)."""
+    noise (mean and variance sums, a normal per conversion), voltage noise (real input
+    operands) and output-mode read noise with voltage noise (real operands and their
+    squares)."""
     import torch
 
     import memfast_amd as memfast
@@ -194,6 +195,8 @@ def _read_modes(out, device):
         "slice_pair": dict(write_variation=0.02, read_variation=0.01, read_mode="slice_pair"),
         "output": dict(write_variation=0.02, read_variation=0.01, read_mode="output"),
         "voltage": dict(write_variation=0.02, voltage_variation=0.01),
+        "output_voltage": dict(write_variation=0.02, read_variation=0.01, read_mode="output",
+                               voltage_variation=0.01),
     }
     for name, effects in modes.items():
         cfg = memfast.Config(**BASE, nonidealities=memfast.Nonidealities(**effects))

@@ -311,9 +311,8 @@ bool build_noisy_plan(const mf_config *cfg, i64 m, i64 p, NoisyPlan *plan, int *
     if (cfg->precise) { *why = "FP64 currents"; return false; }
     const bool output_noise = cfg->has_read && cfg->read_mode == MF_READ_OUTPUT;
     if (output_noise) {
-        // Squared digits must be exact in fp16, the noise addresses of a wave's 32 columns
-        // must share one array tile, and voltage-noise operands are not squared here.
-        if (cfg->has_vnoise) { *why = "output-mode read noise with voltage variation"; return false; }
+        // Squared digits must be exact in fp16 and the noise addresses of a wave's 32
+        // columns must share one array tile.
         if (cfg->cols % 32) { *why = "output-mode read noise needs array columns in multiples of 32"; return false; }
         for (int a = 0; a < cfg->n_in; ++a)
             if (cfg->in_mask[a] > 15) { *why = "output-mode read noise with input digits above 15"; return false; }
@@ -415,13 +414,21 @@ i64 noisy_scratch_bytes(const mf_config *cfg, i64 n, i64 m, i64 p, int requested
     return align256(n * m * cfg->reads * p * cfg->cols * 4);
 }
 
+// Operand terms per input value with voltage variation: x hi and lo, and with output-mode
+// read noise RN(x * x) hi and lo.
+int voltage_terms(const mf_config *cfg) {
+    return cfg->has_read && cfg->read_mode == MF_READ_OUTPUT ? 4 : 2;
+}
+
 // Voltage-variation input operands (k_voltage_terms): hi and lo fp16 per input
 // slice, vector (in blocks of 32) and physical row.  They sit at the end of the
 // workspace, so the conductance terms keep their place (and stay reusable) whatever
 // the vector count.
 i64 noisy_voltage_bytes(const mf_config *cfg, i64 n, i64 m) {
     const i64 vectors = (n + 31) / 32 * 32;
-    return cfg->has_vnoise ? align256(2 * i64(cfg->n_in) * vectors * m * cfg->rows * 2) : 0;
+    return cfg->has_vnoise ? align256(voltage_terms(cfg) * i64(cfg->n_in) * vectors * m *
+                                      cfg->rows * 2)
+                           : 0;
 }
 
 // Whether a split noisy read runs k_noisy_pairs (one wave per input slice, 32 vectors):
@@ -471,7 +478,8 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         uint4 *operands = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + at);
         hipLaunchKernelGGL(k_voltage_terms,
                            dim3(grid_for(i64(cfg->n_in) * ((n + 31) / 32 * 32) * (kp / 8))),
-                           dim3(256), 0, s, *cfg, q, n, m, seed, event, operands);
+                           dim3(256), 0, s, *cfg, q, n, m, seed, event,
+                           int(voltage_terms(cfg) == 4), operands);
         volt = operands;
         bytes = at;
     }
@@ -563,6 +571,7 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
             hipLaunchKernelGGL((k_noisy_pairs<KS, NA, true>), grid, block, 0, s, plan, args);  \
         else if (pairs)                                                                       \
             hipLaunchKernelGGL((k_noisy_pairs<KS, NA, false>), grid, block, 0, s, plan, args); \
+        else if (plan.out_noise && volt) MF_NOISY_LAUNCH2(KS, NA, true, false, true)          \
         else if (plan.out_noise) MF_NOISY_LAUNCH2(KS, NA, false, false, true)                 \
         else if (volt && slice) MF_NOISY_LAUNCH2(KS, NA, true, true, false)                   \
         else if (volt) MF_NOISY_LAUNCH2(KS, NA, true, false, false)                           \
@@ -2091,14 +2100,16 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
      {{MF_NOISY_FN(KS, NA, false, true, false, false), MF_NOISY_FN(KS, NA, true, true, false, false)},   \
       {MF_NOISY_FN(KS, NA, false, true, true, false), MF_NOISY_FN(KS, NA, true, true, true, false)}},    \
      {{MF_NOISY_FN(KS, NA, false, false, false, true), MF_NOISY_FN(KS, NA, true, false, false, true)},   \
-      {MF_NOISY_FN(KS, NA, false, false, false, true), MF_NOISY_FN(KS, NA, true, false, false, true)}}}
-        // [ks][plain, voltage or output noise][slice_pair][nonlinear]
-        const void *table[3][3][2][2] = {MF_NOISY_ROW(2, 5), MF_NOISY_ROW(2, 8),
+      {MF_NOISY_FN(KS, NA, false, false, false, true), MF_NOISY_FN(KS, NA, true, false, false, true)}},  \
+     {{MF_NOISY_FN(KS, NA, false, true, false, true), MF_NOISY_FN(KS, NA, true, true, false, true)},     \
+      {MF_NOISY_FN(KS, NA, false, true, false, true), MF_NOISY_FN(KS, NA, true, true, false, true)}}}
+        // [ks][plain, voltage, output, output and voltage noise][slice_pair][nonlinear]
+        const void *table[3][4][2][2] = {MF_NOISY_ROW(2, 5), MF_NOISY_ROW(2, 8),
                                          MF_NOISY_ROW(4, 5)};
 #undef MF_NOISY_ROW
 #undef MF_NOISY_FN
         const int which = ks4 ? 2 : (cfg->n_in <= 5 ? 0 : 1);
-        const int mode = output_noise ? 2 : (cfg->has_vnoise ? 1 : 0);
+        const int mode = output_noise ? (cfg->has_vnoise ? 3 : 2) : (cfg->has_vnoise ? 1 : 0);
         const bool slice = cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR;
         fn = table[which][mode][slice ? 1 : 0][nl ? 1 : 0];
         if (n > 0 && noisy_small_tile(cfg, n) && variant_split(variant) != 1) {

@@ -197,12 +197,13 @@ __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
 template <int KS, int NA, bool NONLINEAR>
 __global__ void k_noisy_pairs(const NoisyPlan plan, const NoisyArgs args);
 // Input operands of a read with voltage variation (memfast/reference.py:77-82): per
-// input slice a, vector v and physical row k, digit * (1 + vv * z(address)) split into
-// fp16 hi + lo.  Layout [2][A][ceil(n/32)][kp/8][32] of uint4 (8 rows each): the 32
-// vectors of a block are innermost, so one MFMA operand of a wave (32 vectors, two
-// 8-row units) is 1 KiB contiguous.  Vectors past n hold zeros.
+// input slice a, vector v and physical row k, x = digit * (1 + vv * z(address)) split into
+// fp16 hi + lo (terms 0, 1), and with `squares` (output-mode read noise) RN(x * x) split
+// the same way (terms 2, 3).  Layout [terms][A][ceil(n/32)][kp/8][32] of uint4 (8 rows
+// each): the 32 vectors of a block are innermost, so one MFMA operand of a wave (32
+// vectors, two 8-row units) is 1 KiB contiguous.  Vectors past n hold zeros.
 __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
-                                u64 event, uint4 *volt);
+                                u64 event, int squares, uint4 *volt);
 // (float(T) * xs) * ws summed over reads in torch's cascade order, from slice
 // totals [n, G, ldt]: the epilogue of a read split across blocks.
 // With `restored` the values are already (float(T) * xs) * ws and are only summed.

@@ -151,7 +151,7 @@ __device__ __forceinline__ v8h digits_f16(uint2 word, int shift, u32 mask4) {
 }
 
 __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
-                                u64 event, uint4 *volt) {
+                                u64 event, int squares, uint4 *volt) {
     const int R = cfg.rows, A = cfg.n_in;
     const i64 kp = m * R, units = kp / 8, vblocks = (n + 31) / 32;
     const i64 total = i64(A) * vblocks * units * 32;
@@ -163,15 +163,18 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
         const i64 u = rest % units, vb = (rest / units) % vblocks;
         const int a = int(rest / (units * vblocks));
         const i64 v = vb * 32 + lr;
+        const i64 plane = i64(A) * vblocks * units * 32;   // one term of every slice
         if (v >= n) {
-            volt[t] = make_uint4(0u, 0u, 0u, 0u);
-            volt[i64(A) * vblocks * units * 32 + t] = make_uint4(0u, 0u, 0u, 0u);
+            for (int term = 0; term < (squares ? 4 : 2); ++term)
+                volt[term * plane + t] = make_uint4(0u, 0u, 0u, 0u);
             continue;
         }
         const i64 k0 = u * 8;
         const uint2 bytes = *reinterpret_cast<const uint2 *>(q + v * kp + k0);
         const u32 shift = u32(cfg.in_shift[a]), mask = u32(cfg.in_mask[a]);
-        u32 hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+        // Terms 0, 1: hi and lo of x = digit * (1 + vv*z); with `squares` (output-mode read
+        // noise) terms 2, 3: hi and lo of RN(x * x), the variance sum's operand.
+        u32 w4[4][4] = {};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const u32 code = ((j < 4 ? bytes.x : bytes.y) >> (8 * (j & 3))) & 0xFFu;
@@ -183,14 +186,19 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
                 const float z = normal_fast(address, read_seed, 40u);
                 x = float(digit) * (1.0f + cfg.f_vnoise * z);
             }
-            const _Float16 hi = static_cast<_Float16>(x);
-            const _Float16 lo = static_cast<_Float16>(x - static_cast<float>(hi));
+            const float sq = x * x;
+            const float value[2] = {x, sq};
             const int half = 16 * (j & 1);
-            hw[j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << half;
-            lw[j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << half;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const _Float16 hi = static_cast<_Float16>(value[k]);
+                const _Float16 lo = static_cast<_Float16>(value[k] - static_cast<float>(hi));
+                w4[2 * k][j >> 1] |= u32(__builtin_bit_cast(unsigned short, hi)) << half;
+                w4[2 * k + 1][j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << half;
+            }
         }
-        volt[t] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        volt[i64(A) * vblocks * units * 32 + t] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        for (int term = 0; term < (squares ? 4 : 2); ++term)
+            volt[term * plane + t] = make_uint4(w4[term][0], w4[term][1], w4[term][2], w4[term][3]);
     }
 }
 
@@ -403,35 +411,78 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
 #pragma unroll 1
             for (int a = 0; a < A; ++a) {
                 v16f I = {}, Q = {};
-                v8h digits[KS];
-                // This lane's vector's digit sum over the read's rows (the two lanes of a
-                // vector hold rows 0-7 and 8-15 of each 16-row block).
-                u32 rowsum = 0u;
+                float rowsum;   // this lane's vector's input sum over the read's rows
+                if (VNOISE) {
+                    // Voltage variation: real operands x = digit * (1 + vv*z) and RN(x*x), each
+                    // as fp16 hi + lo (3*KS MFMAs each, as the voltage read takes them); the sum
+                    // of x in FP32 from its hi and lo terms.
+                    v8h hi[KS], lo[KS];
+                    float part = 0.0f;
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const uint2 code = qcur[OUTN ? ks : 0];
-                    digits[ks] = digits_f16(code, plan.in_shift[a], plan.in_mask4[a]);
-                    const u32 sh = u32(plan.in_shift[a]);
-                    rowsum = __builtin_amdgcn_sad_u8((code.x >> sh) & plan.in_mask4[a], 0u, rowsum);
-                    rowsum = __builtin_amdgcn_sad_u8((code.y >> sh) & plan.in_mask4[a], 0u, rowsum);
-                }
-                rowsum += u32(__shfl_xor(int(rowsum), 32));
+                    for (int ks = 0; ks < KS; ++ks) {
+                        hi[ks] = volt_operand(0, a, g, ks);
+                        lo[ks] = volt_operand(1, a, g, ks);
 #pragma unroll
-                for (int term = 0; term < NOISY_TERMS; ++term)
-#pragma unroll
-                    for (int ks = 0; ks < KS; ++ks)
-                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fg[term][ks], digits[ks], I, 0, 0,
-                                                                   0);
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const v8h squared = digits[ks] * digits[ks];
+                        for (int j = 0; j < 8; ++j)
+                            part = part + (float(hi[ks][j]) + float(lo[ks][j]));
+                    }
+                    rowsum = part + __shfl_xor(part, 32);
 #pragma unroll
                     for (int term = 0; term < NOISY_TERMS; ++term)
-                        Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fq[term][ks], squared, Q, 0, 0, 0);
+#pragma unroll
+                        for (int ks = 0; ks < KS; ++ks)
+                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fg[term][ks], hi[ks], I, 0,
+                                                                       0, 0);
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks)
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fg[0][ks], lo[ks], I, 0, 0, 0);
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        hi[ks] = volt_operand(2, a, g, ks);
+                        lo[ks] = volt_operand(3, a, g, ks);
+                    }
+#pragma unroll
+                    for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                        for (int ks = 0; ks < KS; ++ks)
+                            Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fq[term][ks], hi[ks], Q, 0,
+                                                                       0, 0);
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks)
+                        Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fq[0][ks], lo[ks], Q, 0, 0, 0);
+                } else {
+                    v8h digits[KS];
+                    // The digit sum over the read's rows (the two lanes of a vector hold
+                    // rows 0-7 and 8-15 of each 16-row block).
+                    u32 count = 0u;
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const uint2 code = qcur[OUTN ? ks : 0];
+                        digits[ks] = digits_f16(code, plan.in_shift[a], plan.in_mask4[a]);
+                        const u32 sh = u32(plan.in_shift[a]);
+                        count = __builtin_amdgcn_sad_u8((code.x >> sh) & plan.in_mask4[a], 0u, count);
+                        count = __builtin_amdgcn_sad_u8((code.y >> sh) & plan.in_mask4[a], 0u, count);
+                    }
+                    count += u32(__shfl_xor(int(count), 32));
+                    rowsum = float(count);
+#pragma unroll
+                    for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                        for (int ks = 0; ks < KS; ++ks)
+                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fg[term][ks], digits[ks], I,
+                                                                       0, 0, 0);
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const v8h squared = digits[ks] * digits[ks];
+#pragma unroll
+                        for (int term = 0; term < NOISY_TERMS; ++term)
+                            Q = __builtin_amdgcn_mfma_f32_32x32x16_f16(Fq[term][ks], squared, Q, 0,
+                                                                       0, 0);
+                    }
                 }
                 // Sign-extended here so the compiler sees a 24-bit operand (v_mad_i32_i24).
                 const u32 f24 = u32(int(plan.f24[a][w] << 8) >> 8);
-                const float shift = plan.kl[w] * float(rowsum);
+                const float shift = plan.kl[w] * rowsum;
                 const u64 base = u64((((n_out * G + g) * p_tiles + tile) * A + a) * W + w) * u64(C) +
                                  u64(cc0 + lhalf * 4);
                 const NormalRun normals(base, args.read_seed, 60u);
@@ -679,7 +730,7 @@ MF_PAIRS_INST(4, 5)
 // per SIMD at 32-row reads (a few spilled registers cost less than a wave fewer) and one at
 // 64-row reads, which hold two slices' terms.
 template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
-__global__ __launch_bounds__(256, OUTN ? (KS == 2 ? 3 : 1) : (KS == 2 && NA <= 5 && !VNOISE ? 4 : 2)) void k_noisy(
+__global__ __launch_bounds__(256, OUTN ? (KS == 2 && !VNOISE ? 3 : KS == 2 ? 2 : 1) : (KS == 2 && NA <= 5 && !VNOISE ? 4 : 2)) void k_noisy(
     const NoisyPlan plan,
                                                              const NoisyArgs args) {
     noisy_read<KS, NA, NONLINEAR, VNOISE, SLICE, OUTN>(plan, args);
@@ -738,7 +789,8 @@ __global__ void k_restore_sum_f32(const float *totals, i64 n, i64 G, i64 g_run, 
     MF_NOISY_INST1(KS, NA, false, true, false, false) MF_NOISY_INST1(KS, NA, true, true, false, false)   \
     MF_NOISY_INST1(KS, NA, false, false, true, false) MF_NOISY_INST1(KS, NA, true, false, true, false)   \
     MF_NOISY_INST1(KS, NA, false, true, true, false) MF_NOISY_INST1(KS, NA, true, true, true, false)     \
-    MF_NOISY_INST1(KS, NA, false, false, false, true) MF_NOISY_INST1(KS, NA, true, false, false, true)
+    MF_NOISY_INST1(KS, NA, false, false, false, true) MF_NOISY_INST1(KS, NA, true, false, false, true)   \
+    MF_NOISY_INST1(KS, NA, false, true, false, true) MF_NOISY_INST1(KS, NA, true, true, false, true)
 MF_NOISY_INST(2, 5)
 MF_NOISY_INST(2, 8)
 MF_NOISY_INST(4, 5)

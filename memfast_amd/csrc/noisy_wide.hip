@@ -283,8 +283,8 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
             for (int r = 0; r < 16; ++r) {
                 float y = (NONLINEAR ? scurve(I[r], alpha) : I[r]) + MAGIC;
                 y = __builtin_amdgcn_fmed3f(y, MAGIC, top);
-                const int low = int(__float_as_uint(y) << 8) >> 8;   // 0x400000 + code
-                T[r] += u32(low) * f24;
+                // 0x400000 + code in the low 24 bits; v_mad_i32_i24 reads only those.
+                asm("v_mad_i32_i24 %0, %1, %2, %0" : "+v"(T[r]) : "v"(y), "s"(f24));
             }
         };
         auto digits = [&](v8h_w (&B)[KS], int a) {

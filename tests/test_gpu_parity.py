@@ -688,6 +688,18 @@ MFMA_NOISY = {
                            input_quant_gran=(1, 64)),
                       dict(write_variation=0.02, read_variation=0.02, read_mode="output",
                            stuck_at_low=0.01, stuck_at_high=0.01, adc_nonlinearity=0.1)),
+    # Output-mode read noise with voltage variation: real operands x and x*x (hi + lo) for
+    # the current and variance sums; 2-bit and binary digits, 32- and 64-row reads.
+    "output_voltage": (dict(), dict(write_variation=0.02, read_variation=0.02,
+                                    read_mode="output", voltage_variation=0.05)),
+    "output_voltage_binary8": (dict(input_slice=None, weight_slice=(1, 1, 2, 2, 2),
+                                    adc_bits=(4, 5, 5, 6, 6)),
+                               dict(write_variation=0.02, read_variation=0.03, read_mode="output",
+                                    voltage_variation=0.03, adc_nonlinearity=0.1)),
+    "output_voltage_rows64": (dict(array_size=(128, 32), rows_per_read=64,
+                                   weight_quant_gran=(64, 1), input_quant_gran=(1, 64)),
+                              dict(write_variation=0.02, read_variation=0.02, read_mode="output",
+                                   voltage_variation=0.02)),
 }
 NOISY_BASE = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
                   weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,

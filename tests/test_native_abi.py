@@ -127,8 +127,8 @@ def test_noisy_mfma_kernels_require_fp16_range():
 
 def test_read_kernel_selection_by_noise_model():
     """Which read kernel each noise model takes (mf_mm_kernel, host only): the narrow noisy
-    MFMA read covers voltage variation, slice_pair and output-mode read noise (output mode
-    without voltage variation); the wide MFMA read covers neither voltage
+    MFMA read covers voltage variation, slice_pair and output-mode read noise (also output
+    mode with voltage variation); the wide MFMA read covers neither voltage
     variation nor per-slice read noise (it models them not at all, so they must never
     reach it)."""
     from memfast_amd import Config, Nonidealities
@@ -141,7 +141,7 @@ def test_read_kernel_selection_by_noise_model():
         (narrow, dict(write_variation=0.02, voltage_variation=0.01), 2),
         (narrow, dict(read_variation=0.01, read_mode="slice_pair"), 2),
         (narrow, dict(read_variation=0.01, read_mode="output"), 2),
-        (narrow, dict(read_variation=0.01, read_mode="output", voltage_variation=0.01), 0),
+        (narrow, dict(read_variation=0.01, read_mode="output", voltage_variation=0.01), 2),
         (narrow, dict(read_variation=0.01, read_mode="slice_pair", voltage_variation=0.01), 2),
         (wide, dict(read_variation=0.01), 3),
         (wide, dict(write_variation=0.02, voltage_variation=0.01), 0),

@@ -29,9 +29,10 @@ def test_grid_follows_the_selected_kernel():
                                                              read_mode="slice_pair"))
     assert [s["split"] for s in tuning.schedule_grid(slice_pair, 64, 8, arrays=4)] == [
         0, 1, 2, 4, 8]
-    general = Config(**INT8, nonidealities=Nonidealities(read_variation=0.01,
-                                                          read_mode="output",
-                                                          voltage_variation=0.01))
+    # FP64 currents (high - low < 1e-4 high) run on the general kernel only.
+    general = Config(**INT8, high_conductance=1e-5, low_conductance=0.99995e-5,
+                     nonidealities=Nonidealities(write_variation=0.02))
+    assert general.precise_currents and hip.mm_kernel(general, 64, 4, 8) == 0
     assert tuning.schedule_grid(general, 64, 8, arrays=4) == [tuning.default_schedule(general)]
     # Without the array count (the reference's signature) only the default is declared.
     assert tuning.schedule_grid(noisy, 64, 8) == [tuning.default_schedule(noisy)]
@@ -64,16 +65,20 @@ def test_workspace_need_prices_each_schedule():
     ideal = Config(**INT8, nonidealities=Nonidealities(write_variation=0.0))
     assert tuning.workspace_need(ideal, n, m, p, {}) == (
         -(-(4 * 16 * 8) // 256) * 256 + -(-(32 * 16 * 8) // 256) * 256)
-    general = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02,
-                                                          read_variation=0.01,
-                                                          read_mode="output",
-                                                          voltage_variation=0.01))
-    assert tuning.workspace_need(general, n, m, p, {}) == 4 * m * p * 5 * 128 * 128
+    # FP64 currents (general kernel): FP64 restored conductances.
+    general = Config(**INT8, high_conductance=1e-5, low_conductance=0.99995e-5,
+                     nonidealities=Nonidealities(write_variation=0.02))
+    assert tuning.workspace_need(general, n, m, p, {}) == 8 * m * p * 5 * 128 * 128
     # Voltage variation adds the noisy read's input operands: hi and lo fp16 per input
-    # slice, vector and physical row.
+    # slice, vector and physical row; with output-mode read noise also hi and lo of their
+    # squares (and two planes of conductance terms).
     voltage = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02,
                                                           voltage_variation=0.01))
     assert tuning.workspace_need(voltage, n, m, p, dict(split=1)) == terms + 2 * 5 * n * m * 128 * 2
+    output = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02, read_variation=0.01,
+                                                         read_mode="output",
+                                                         voltage_variation=0.01))
+    assert tuning.workspace_need(output, n, m, p, dict(split=1)) == 2 * terms + 4 * 5 * n * m * 128 * 2
 
 
 def test_unknown_variant_bits_are_refused():
