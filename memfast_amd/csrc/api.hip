@@ -476,7 +476,7 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         // Aligned down to 256 bytes at the end of the workspace.
         const i64 at = ((bytes - vbytes) / 256) * 256;
         uint4 *operands = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + at);
-        hipLaunchKernelGGL(k_voltage_terms,
+        hipLaunchKernelGGL(k_voltage_terms<u8>,
                            dim3(grid_for(i64(cfg->n_in) * ((n + 31) / 32 * 32) * (kp / 8))),
                            dim3(256), 0, s, *cfg, q, n, m, seed, event,
                            int(voltage_terms(cfg) == 4), operands);
@@ -619,7 +619,6 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
                            bool *small, const char **why) {
     if (!cfg->wide) { *why = "narrow codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
-    if (cfg->has_vnoise) { *why = "voltage variation"; return false; }
     if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
     if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
@@ -675,6 +674,17 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
 // Workspace of the wide MFMA read: 16-bit input codes, then the conductance
 // terms of up to every 32-column block (NOISY_TERMS fp16 terms per cell and slice).
 i64 wide_codes_bytes(i64 n, i64 m, const mf_config *cfg) { return align256(n * m * cfg->rows * 2); }
+// Voltage-variation input operands of the wide read (k_voltage_terms<u32>): hi and lo
+// fp16 per input slice, vector (in blocks of 32) and physical row.
+i64 wide_voltage_bytes(i64 n, i64 m, const mf_config *cfg) {
+    const i64 vectors = (n + 31) / 32 * 32;
+    return cfg->has_vnoise ? align256(2 * i64(cfg->n_in) * vectors * m * cfg->rows * 2) : 0;
+}
+// Workspace of the wide read before its conductance terms: the 16-bit codes, then the
+// voltage operands.
+i64 wide_prefix_bytes(i64 n, i64 m, const mf_config *cfg) {
+    return wide_codes_bytes(n, m, cfg) + wide_voltage_bytes(n, m, cfg);
+}
 i64 wide_block_bytes(const mf_config *cfg, i64 m) {
     return i64(cfg->n_w) * 32 * m * cfg->rows * NOISY_TERMS * 2;
 }
@@ -693,8 +703,9 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
                       hipStream_t s, int tier_request = 0) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     const i64 codes_bytes = wide_codes_bytes(n, m, cfg);
+    const i64 prefix = wide_prefix_bytes(n, m, cfg);
     const i64 per_block = wide_block_bytes(cfg, m);
-    const i64 max_cb = (bytes - codes_bytes) / per_block;
+    const i64 max_cb = (bytes - prefix) / per_block;
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
     const int frags = cfg->n_w * NOISY_TERMS * ks;
     if (frags > WIDE_FRAGS_LARGE) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
@@ -708,8 +719,15 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
         tier = tier_request - 1;
     }
     uint16_t *q16 = static_cast<uint16_t *>(workspace);
-    uint4 *gs = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + codes_bytes);
+    uint4 *volt = cfg->has_vnoise
+                      ? reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + codes_bytes)
+                      : nullptr;
+    uint4 *gs = reinterpret_cast<uint4 *>(static_cast<char *>(workspace) + prefix);
     hipLaunchKernelGGL(k_codes16, dim3(grid_for(n * kp)), dim3(256), 0, s, q, n * kp, q16);
+    if (volt)
+        hipLaunchKernelGGL(k_voltage_terms<u32>,
+                           dim3(grid_for(i64(cfg->n_in) * ((n + 31) / 32 * 32) * (kp / 8))),
+                           dim3(256), 0, s, *cfg, q, n, m, seed, event, 0, volt);
     for (i64 c_begin = 0; c_begin < ncols; c_begin += max_cb * 32) {
         const i64 cols = (ncols - c_begin) < max_cb * 32 ? (ncols - c_begin) : max_cb * 32;
         const i64 CB = (cols + 31) / 32;
@@ -735,19 +753,26 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
         args.ncols = ncols;
         args.c_begin = c_begin;
         args.totals = totals;
+        args.volt = volt;
         const dim3 grid{unsigned(CB), unsigned((n + 127) / 128), 1u};
         const bool nl = cfg->has_nonlinear != 0;
-#define MF_WIDE_LAUNCH(KS, FR)                                                                   \
-    if (nl) {                                                                                    \
-        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, true, true, FR>), grid, dim3(256), 0, s,  \
-                                      plan, args);                                               \
-        else hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR>), grid, dim3(256), 0, s, plan, \
-                                args);                                                           \
-    } else {                                                                                     \
-        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, false, true, FR>), grid, dim3(256), 0, s, \
-                                      plan, args);                                               \
-        else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR>), grid, dim3(256), 0, s,      \
-                                plan, args);                                                     \
+#define MF_WIDE_LAUNCH(KS, FR)                                                                         \
+    if (volt && nl) {                                                                                  \
+        hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, true>), grid, dim3(256), 0, s, plan,      \
+                           args);                                                                      \
+    } else if (volt) {                                                                                 \
+        hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, true>), grid, dim3(256), 0, s, plan,     \
+                           args);                                                                      \
+    } else if (nl) {                                                                                   \
+        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, true, true, FR, false>), grid, dim3(256), 0, s, \
+                                      plan, args);                                                     \
+        else hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, false>), grid, dim3(256), 0, s,      \
+                                plan, args);                                                           \
+    } else {                                                                                           \
+        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, false, true, FR, false>), grid, dim3(256), 0,   \
+                                      s, plan, args);                                                  \
+        else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, false>), grid, dim3(256), 0, s,     \
+                                plan, args);                                                           \
     }
         if (ks == 4) {
             if (tier == 2) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_LARGE) }
@@ -1316,7 +1341,7 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32
         // At least the two 32-column blocks the wide read's chunking needs, even for
         // outputs narrower than 64 columns.
         const i64 blocks = std::max<i64>(2, (p * cfg->cols + 31) / 32);
-        *bytes = wide_codes_bytes(n, m, cfg) + blocks * wide_block_bytes(cfg, m);
+        *bytes = wide_prefix_bytes(n, m, cfg) + blocks * wide_block_bytes(cfg, m);
     } else {
         *bytes = 0;
     }
@@ -1972,7 +1997,7 @@ int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, in
     const char *why = "";
     if (!g && workspace && (reinterpret_cast<uintptr_t>(workspace) % 256) == 0 &&
         wide_extent_ok(n, m, cfg) && build_noisy_wide_plan(cfg, m, p, &wplan, &ks, &small, &why) &&
-        workspace_bytes >= wide_codes_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m)) {
+        workspace_bytes >= wide_prefix_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m)) {
         hipStream_t s = static_cast<hipStream_t>(stream);
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
         if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
@@ -2037,7 +2062,7 @@ int mf_mm_totals_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_
     const char *why = "";
     if (!wide_extent_ok(n, m, cfg) || !build_noisy_wide_plan(cfg, m, p, &plan, &ks, &small, &why))
         return fail(MF_E_UNSUPPORTED, "wide MFMA read not applicable: %s", why);
-    if (workspace_bytes < wide_codes_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m))
+    if (workspace_bytes < wide_prefix_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m))
         return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
     const i64 ncols = p * cfg->cols;
     return launch_noisy_wide(cfg, plan, ks, small, q, nullptr, n, m, packed, nullptr, p, g, seed,
@@ -2133,11 +2158,14 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
         if (variant_tier(variant) > 0) tier = variant_tier(variant) - 1;
         bool small = true;   // every input digit of at most 2 bits (build_noisy_wide_plan)
         for (int a = 0; a < cfg->n_in; ++a) small = small && cfg->in_mask[a] <= 3;
+        const bool vn = cfg->has_vnoise != 0;
 #define MF_WIDE_FN(KS, FR) \
-    (nl ? (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, true, FR>)           \
-                 : reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR>))         \
-        : (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, false, true, FR>)          \
-                 : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR>)))
+    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, true>)       \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, true>))     \
+     : nl ? (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, true, FR, false>)   \
+                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, false>)) \
+          : (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, false, true, FR, false>)  \
+                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, false>)))
         if (ks4) fn = tier == 2 ? MF_WIDE_FN(4, WIDE_FRAGS_LARGE)
                       : tier == 1 ? MF_WIDE_FN(4, WIDE_FRAGS_SMALL) : MF_WIDE_FN(4, WIDE_FRAGS_TINY);
         else fn = tier == 2 ? MF_WIDE_FN(2, WIDE_FRAGS_LARGE)

@@ -202,7 +202,9 @@ __global__ void k_noisy_pairs(const NoisyPlan plan, const NoisyArgs args);
 // the same way (terms 2, 3).  Layout [terms][A][ceil(n/32)][kp/8][32] of uint4 (8 rows
 // each): the 32 vectors of a block are innermost, so one MFMA operand of a wave (32
 // vectors, two 8-row units) is 1 KiB contiguous.  Vectors past n hold zeros.
-__global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
+// Code: u8 (narrow codes) or u32 (wide codes, digits up to 255).
+template <typename Code>
+__global__ void k_voltage_terms(const mf_config cfg, const Code *q, i64 n, i64 m, u32 seed,
                                 u64 event, int squares, uint4 *volt);
 // (float(T) * xs) * ws summed over reads in torch's cascade order, from slice
 // totals [n, G, ldt]: the epilogue of a read split across blocks.
@@ -235,6 +237,9 @@ struct NoisyWideArgs {
     u32 *status;           // optional: MF_STATUS_OUTPUT for a non-finite fused output
     i64 n, kp, G, ldo, ldws, ncols, c_begin;
     int totals;
+    // Voltage variation: input operands [2][A][ceil(n/32)][kp/8][32] uint4 of 8 fp16 (hi,
+    // lo) of digit * (1 + vv*z) from k_voltage_terms<u32>, read instead of the digits.
+    const uint4 *volt;
 };
 
 __global__ void k_codes16(const u32 *q, i64 count, uint16_t *q16);
@@ -253,7 +258,8 @@ constexpr int WIDE_FRAGS_LARGE = 72;
 constexpr int wide_blocks_per_cu(int frmax, bool nonlinear) {
     return frmax <= WIDE_FRAGS_TINY && !nonlinear ? 3 : 2;
 }
-template <int KS, bool NONLINEAR, bool SMALL, int FRMAX>
+// VNOISE: voltage variation (real input operands from args.volt, one input slice a step).
+template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE>
 __global__ void k_noisy_wide(const NoisyWidePlan plan, const NoisyWideArgs args);
 
 // ---- FP64 restore and read sum (stable.hip) --------------------------------

@@ -150,7 +150,21 @@ __device__ __forceinline__ v8h digits_f16(uint2 word, int shift, u32 mask4) {
     return __builtin_bit_cast(v8h, packed);
 }
 
-__global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, u32 seed,
+// Eight consecutive input codes of one vector: bytes (narrow) or 32-bit words (wide).
+__device__ __forceinline__ void codes8(const u8 *q, u32 (&c)[8]) {
+    const uint2 bytes = *reinterpret_cast<const uint2 *>(q);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = ((j < 4 ? bytes.x : bytes.y) >> (8 * (j & 3))) & 0xFFu;
+}
+__device__ __forceinline__ void codes8(const u32 *q, u32 (&c)[8]) {
+    const uint4 a = *reinterpret_cast<const uint4 *>(q);
+    const uint4 b = *reinterpret_cast<const uint4 *>(q + 4);
+    c[0] = a.x; c[1] = a.y; c[2] = a.z; c[3] = a.w;
+    c[4] = b.x; c[5] = b.y; c[6] = b.z; c[7] = b.w;
+}
+
+template <typename Code>
+__global__ void k_voltage_terms(const mf_config cfg, const Code *q, i64 n, i64 m, u32 seed,
                                 u64 event, int squares, uint4 *volt) {
     const int R = cfg.rows, A = cfg.n_in;
     const i64 kp = m * R, units = kp / 8, vblocks = (n + 31) / 32;
@@ -170,15 +184,15 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
             continue;
         }
         const i64 k0 = u * 8;
-        const uint2 bytes = *reinterpret_cast<const uint2 *>(q + v * kp + k0);
+        u32 codes[8];
+        codes8(q + v * kp + k0, codes);
         const u32 shift = u32(cfg.in_shift[a]), mask = u32(cfg.in_mask[a]);
         // Terms 0, 1: hi and lo of x = digit * (1 + vv*z); with `squares` (output-mode read
         // noise) terms 2, 3: hi and lo of RN(x * x), the variance sum's operand.
         u32 w4[4][4] = {};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const u32 code = ((j < 4 ? bytes.x : bytes.y) >> (8 * (j & 3))) & 0xFFu;
-            const u32 digit = (code >> shift) & mask;
+            const u32 digit = (codes[j] >> shift) & mask;
             float x = 0.0f;   // a zero digit stays zero whatever its factor
             if (digit) {
                 const i64 k = k0 + j, i = k / R, r = k - i * R;
@@ -201,6 +215,11 @@ __global__ void k_voltage_terms(const mf_config cfg, const u8 *q, i64 n, i64 m, 
             volt[term * plane + t] = make_uint4(w4[term][0], w4[term][1], w4[term][2], w4[term][3]);
     }
 }
+
+template __global__ void k_voltage_terms<u8>(const mf_config, const u8 *, i64, i64, u32, u64,
+                                            int, uint4 *);
+template __global__ void k_voltage_terms<u32>(const mf_config, const u32 *, i64, i64, u32, u64,
+                                             int, uint4 *);
 
 // normal_fast() at the addresses base + offset (offset < 2^31) for one stream pair: the
 // high-word folds of both streams are computed once for base's high word, and again only in

@@ -196,7 +196,7 @@ template __global__ void k_split_wide<2>(const mf_config, const u32 *, const flo
 template __global__ void k_split_wide<4>(const mf_config, const u32 *, const float *, i64, i64,
                                          i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 
-template <int KS, bool NONLINEAR, bool SMALL, int FRMAX>
+template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE>
 __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_noisy_wide(
     const NoisyWidePlan plan,
                                                        const NoisyWideArgs args) {
@@ -245,6 +245,7 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
 
     const i64 n_out = v0 + lrow;
     const bool live_n = n_out < args.n;
+    const bool live_block = v0 < args.n;   // wave-uniform: the wave holds some vector
     const i64 col_tile = args.c_begin + cb * 32;   // absolute first column of the block
     double acc0[16];
 #pragma unroll
@@ -303,10 +304,44 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
                     F[term][ks] = __builtin_bit_cast(
                         v8h_w, fl[((w * NOISY_TERMS + term) * KS + ks) * 64]);
         };
+        if (VNOISE) {
+            // Voltage variation (memfast/reference.py:77-82): every input value carries its
+            // own factor, x = digit * (1 + vv*z), held as fp16 hi + lo operands; a pair takes
+            // 3*KS MFMAs (hi*hi + lo*hi + hi*lo, the narrow voltage read's order).  One input
+            // slice a step (its two operands take the registers of two slices' digits).
+            const i64 vunits = kp / 8;
+            const uint4 *vbase = args.volt + (v0 / 32) * vunits * 32 + lane;
+            const i64 vplane = ((args.n + 31) / 32) * vunits * 32;
+            for (int a = 0; a < A; ++a) {
+                v8h_w hi[KS], lo[KS];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const i64 at = (g * (P / 8) + ks * 2) * 32;
+                    hi[ks] = __builtin_bit_cast(v8h_w, live_block ? vbase[a * vplane + at] : uint4{});
+                    lo[ks] = __builtin_bit_cast(v8h_w, live_block ? vbase[(A + a) * vplane + at]
+                                                                  : uint4{});
+                }
+                for (int w = 0; w < W; ++w) {
+                    v8h_w F[NOISY_TERMS][KS];
+                    terms(F, w);
+                    v16f_w I = {};
+#pragma unroll
+                    for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                        for (int ks = 0; ks < KS; ++ks)
+                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], hi[ks], I, 0,
+                                                                       0, 0);
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks)
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[0][ks], lo[ks], I, 0, 0, 0);
+                    convert(I, w, a);
+                }
+            }
+        }
         // Input slices in pairs: the digits of a slice are built once per read;
         // per weight slice the two currents are two interleaved MFMA chains.
         int a = 0;
-        for (; a + 1 < A; a += 2) {
+        for (; !VNOISE && a + 1 < A; a += 2) {
             v8h_w B0[KS], B1[KS];
             digits(B0, a);
             digits(B1, a + 1);
@@ -325,7 +360,7 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
                 convert(I1, w, a + 1);
             }
         }
-        if (a < A) {
+        if (!VNOISE && a < A) {
             v8h_w B0[KS];
             digits(B0, a);
             for (int w = 0; w < W; ++w) {
@@ -409,14 +444,16 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
-#define MF_NOISY_WIDE_INST(KS, NL, SMALL, FRMAX)                                            \
-    template __global__ void k_noisy_wide<KS, NL, SMALL, FRMAX>(const NoisyWidePlan,          \
-                                                                const NoisyWideArgs);
-#define MF_NOISY_WIDE_INST4(KS, FRMAX)              \
-    MF_NOISY_WIDE_INST(KS, false, true, FRMAX)      \
-    MF_NOISY_WIDE_INST(KS, true, true, FRMAX)       \
-    MF_NOISY_WIDE_INST(KS, false, false, FRMAX)     \
-    MF_NOISY_WIDE_INST(KS, true, false, FRMAX)
+#define MF_NOISY_WIDE_INST(KS, NL, SMALL, FRMAX, VN)                                           \
+    template __global__ void k_noisy_wide<KS, NL, SMALL, FRMAX, VN>(const NoisyWidePlan,         \
+                                                                    const NoisyWideArgs);
+#define MF_NOISY_WIDE_INST4(KS, FRMAX)                  \
+    MF_NOISY_WIDE_INST(KS, false, true, FRMAX, false)   \
+    MF_NOISY_WIDE_INST(KS, true, true, FRMAX, false)    \
+    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, false)  \
+    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, false)   \
+    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, true)   \
+    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, true)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_TINY)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_SMALL)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_LARGE)

@@ -1075,6 +1075,17 @@ WIDE_MFMA = {
                       weight_slice=(1, 2, 2, 2), array_size=(128, 64), rows_per_read=64,
                       adc_bits=8), dict(write_variation=0.02, drift_coefficient=0.05,
                                         drift_time=100.0), 90, 300, 130),
+    # Voltage variation: real input operands (hi + lo of digit * (1 + vv*z)) instead of
+    # digits; BFP16 x INT4 at 64-row reads with read noise and drift, and 4-bit digits at
+    # 32-row reads with the S-curve ADC.
+    "bfp16_voltage": (WIDE["bfp16_int4"][0],
+                      dict(write_variation=0.02, read_variation=0.01, voltage_variation=0.03,
+                           drift_coefficient=0.05, drift_time=100.0), 70, 300, 150),
+    "int12_voltage": (dict(activation_bits=12, weight_bits=8, input_slice=(1, 3, 4, 4),
+                           weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,
+                           adc_bits=8),
+                      dict(write_variation=0.02, voltage_variation=0.05, adc_nonlinearity=0.05),
+                      45, 200, 70),
 }
 
 
