@@ -612,6 +612,12 @@ bool all_cascade_columns_wide(int C, i64 p) {
     return true;
 }
 
+// Planes of conductance terms per weight slice of the wide read: one per input slice with
+// slice_pair read noise (an independent read factor per cell and input slice), else one.
+int wide_term_planes(const mf_config *cfg) {
+    return cfg->has_read && cfg->read_mode == MF_READ_SLICE_PAIR ? cfg->n_in : 1;
+}
+
 // Wide noisy-device MFMA eligibility and plan (noisy_wide.hip): the narrow
 // kernel's device model, input codes of at most 16 bits with digits up to 255,
 // fewer than 256 reads, exact int32 totals.
@@ -619,7 +625,7 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
                            bool *small, const char **why) {
     if (!cfg->wide) { *why = "narrow codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
-    if (cfg->has_read && cfg->read_mode != MF_READ_SHARED) { *why = "per-slice read noise"; return false; }
+    if (cfg->has_read && cfg->read_mode == MF_READ_OUTPUT) { *why = "output-mode read noise"; return false; }
     if ((cfg->read_rows != 32 && cfg->read_rows != 64) || cfg->rows % cfg->read_rows) {
         *why = "rows_per_read must be 32 or 64 and divide the array rows";
         return false;
@@ -652,6 +658,7 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
     memset(plan, 0, sizeof(*plan));
     plan->n_in = cfg->n_in;
     plan->n_w = cfg->n_w;
+    plan->planes = wide_term_planes(cfg);
     i64 factor_sum = 0;
     for (int w = 0; w < cfg->n_w; ++w) {
         plan->k1[w] = float(cfg->d_voltage * double(cfg->w_mask[w]) * cfg->d_inv_unit);
@@ -686,7 +693,7 @@ i64 wide_prefix_bytes(i64 n, i64 m, const mf_config *cfg) {
     return wide_codes_bytes(n, m, cfg) + wide_voltage_bytes(n, m, cfg);
 }
 i64 wide_block_bytes(const mf_config *cfg, i64 m) {
-    return i64(cfg->n_w) * 32 * m * cfg->rows * NOISY_TERMS * 2;
+    return i64(cfg->n_w) * wide_term_planes(cfg) * 32 * m * cfg->rows * NOISY_TERMS * 2;
 }
 
 bool wide_extent_ok(i64 n, i64 m, const mf_config *cfg) {
@@ -756,22 +763,38 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
         args.volt = volt;
         const dim3 grid{unsigned(CB), unsigned((n + 127) / 128), 1u};
         const bool nl = cfg->has_nonlinear != 0;
+        if (plan.planes > 1) {
+            // slice_pair read noise: every (weight, input) slice pair has its own plane of
+            // terms, read from global memory rather than staged in LDS.
+#define MF_WIDE_SLICE(KS)                                                                          \
+    if (volt && nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, false, 1, true, true>), grid,        \
+                                       dim3(256), 0, s, plan, args);                                \
+    else if (volt) hipLaunchKernelGGL((k_noisy_wide<KS, false, false, 1, true, true>), grid,        \
+                                      dim3(256), 0, s, plan, args);                                 \
+    else if (nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, false, 1, false, true>), grid,          \
+                                    dim3(256), 0, s, plan, args);                                   \
+    else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, 1, false, true>), grid, dim3(256), 0,   \
+                            s, plan, args);
+            if (ks == 4) { MF_WIDE_SLICE(4) } else { MF_WIDE_SLICE(2) }
+#undef MF_WIDE_SLICE
+            continue;
+        }
 #define MF_WIDE_LAUNCH(KS, FR)                                                                         \
     if (volt && nl) {                                                                                  \
-        hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, true>), grid, dim3(256), 0, s, plan,      \
+        hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, true, false>), grid, dim3(256), 0, s, plan,      \
                            args);                                                                      \
     } else if (volt) {                                                                                 \
-        hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, true>), grid, dim3(256), 0, s, plan,     \
+        hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, true, false>), grid, dim3(256), 0, s, plan,     \
                            args);                                                                      \
     } else if (nl) {                                                                                   \
-        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, true, true, FR, false>), grid, dim3(256), 0, s, \
+        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, true, true, FR, false, false>), grid, dim3(256), 0, s, \
                                       plan, args);                                                     \
-        else hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, false>), grid, dim3(256), 0, s,      \
+        else hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, false, false>), grid, dim3(256), 0, s,      \
                                 plan, args);                                                           \
     } else {                                                                                           \
-        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, false, true, FR, false>), grid, dim3(256), 0,   \
+        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, false, true, FR, false, false>), grid, dim3(256), 0,   \
                                       s, plan, args);                                                  \
-        else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, false>), grid, dim3(256), 0, s,     \
+        else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, false, false>), grid, dim3(256), 0, s,     \
                                 plan, args);                                                           \
     }
         if (ks == 4) {
@@ -2159,17 +2182,25 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
         bool small = true;   // every input digit of at most 2 bits (build_noisy_wide_plan)
         for (int a = 0; a < cfg->n_in; ++a) small = small && cfg->in_mask[a] <= 3;
         const bool vn = cfg->has_vnoise != 0;
-#define MF_WIDE_FN(KS, FR) \
-    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, true>)       \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, true>))     \
-     : nl ? (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, true, FR, false>)   \
-                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, false>)) \
-          : (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, false, true, FR, false>)  \
-                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, false>)))
-        if (ks4) fn = tier == 2 ? MF_WIDE_FN(4, WIDE_FRAGS_LARGE)
-                      : tier == 1 ? MF_WIDE_FN(4, WIDE_FRAGS_SMALL) : MF_WIDE_FN(4, WIDE_FRAGS_TINY);
+        const bool sl = wide_term_planes(cfg) > 1;   // slice_pair: planes from global memory
+#define MF_WIDE_FN(KS, FR)                                                                         \
+    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, true, false>)       \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, true, false>))     \
+     : nl ? (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, true, FR, false, false>)   \
+                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, false, false>)) \
+          : (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, false, true, FR, false, false>)  \
+                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, false, false>)))
+#define MF_WIDE_SLICE_FN(KS)                                                                     \
+    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, 1, true, true>)      \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, 1, true, true>))    \
+        : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, 1, false, true>)     \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, 1, false, true>)))
+        if (sl) fn = ks4 ? MF_WIDE_SLICE_FN(4) : MF_WIDE_SLICE_FN(2);
+        else if (ks4) fn = tier == 2 ? MF_WIDE_FN(4, WIDE_FRAGS_LARGE)
+                           : tier == 1 ? MF_WIDE_FN(4, WIDE_FRAGS_SMALL) : MF_WIDE_FN(4, WIDE_FRAGS_TINY);
         else fn = tier == 2 ? MF_WIDE_FN(2, WIDE_FRAGS_LARGE)
                   : tier == 1 ? MF_WIDE_FN(2, WIDE_FRAGS_SMALL) : MF_WIDE_FN(2, WIDE_FRAGS_TINY);
+#undef MF_WIDE_SLICE_FN
 #undef MF_WIDE_FN
     } else if (kernel_id == 0) {
 #define MF_GENERAL_FN(WIDE)                                                                      \

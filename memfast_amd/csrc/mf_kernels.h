@@ -220,6 +220,7 @@ constexpr int WIDE_MFMA_MAX_A = 16;
 constexpr int WIDE_MFMA_MAX_W = 8;
 struct NoisyWidePlan {
     int n_in, n_w;
+    int planes;        // planes of terms per weight slice: n_in (slice_pair read noise), else 1
     float k1[WIDE_MFMA_MAX_W], top[WIDE_MFMA_MAX_W], alpha[WIDE_MFMA_MAX_W];
     int fw[WIDE_MFMA_MAX_W];
     int fa[WIDE_MFMA_MAX_A];
@@ -230,7 +231,7 @@ struct NoisyWidePlan {
 
 struct NoisyWideArgs {
     const uint16_t *q16;   // [n, kp] input codes, 16 bits
-    const uint4 *gs;       // conductance terms [CB][G][W][3][KS][64 lanes] of the column chunk
+    const uint4 *gs;       // conductance terms [CB][G][W*planes][2][KS][64 lanes] of the chunk
     const double *xscale;  // [n, G]
     const double *wscale;  // [G, ldws]
     double *out;           // fused: [n, ldo]; totals: [n, G, ldo]
@@ -259,7 +260,9 @@ constexpr int wide_blocks_per_cu(int frmax, bool nonlinear) {
     return frmax <= WIDE_FRAGS_TINY && !nonlinear ? 3 : 2;
 }
 // VNOISE: voltage variation (real input operands from args.volt, one input slice a step).
-template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE>
+// SLICE: slice_pair read noise (a plane of terms per (weight slice, input slice), read from
+// global memory: FRMAX 1, no LDS staging).
+template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE, bool SLICE>
 __global__ void k_noisy_wide(const NoisyWidePlan plan, const NoisyWideArgs args);
 
 // ---- FP64 restore and read sum (stable.hip) --------------------------------

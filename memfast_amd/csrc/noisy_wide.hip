@@ -147,14 +147,15 @@ __global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u
     constexpr int P = 16 * KS;
     const int R = cfg.rows, C = cfg.cols, W = cfg.n_w;
     const i64 G = m * R / P;
-    const i64 total = CB * G * W * KS * 64;
+    const i64 total = CB * G * W * plan.planes * KS * 64;
     const u64 read_seed = event_seed(seed, event);
     for (i64 t = i64(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
          t += i64(gridDim.x) * blockDim.x) {
         i64 rest = t;
         const int lane = int(rest & 63); rest >>= 6;
         const int ks = int(rest % KS); rest /= KS;
-        const int w = int(rest % W); rest /= W;
+        const int vw = int(rest % (W * plan.planes)); rest /= W * plan.planes;
+        const int w = vw / plan.planes, plane = vw - w * plan.planes;
         const i64 g = rest % G;
         const i64 cb = rest / G;
         const int lr = lane & 31, h = lane >> 5;
@@ -175,6 +176,12 @@ __global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u
                     const u32 code = packed[((i * p + tt) * R + r) * C + cc];
                     level = cell_conductance<float>(cfg, code, w, cell, seed, read_seed);
                 }
+                // slice_pair read noise (memfast/reference.py:86-90): a read factor per
+                // (cell, input slice), one plane of terms per input slice.
+                if (plan.planes > 1)
+                    level = level * exp_small(cfg.f_read *
+                                              normal_fast(cell * u64(cfg.n_in) + u64(plane),
+                                                          read_seed, 20u));
                 const float delta = (level - cfg.f_low) * plan.k1[w];   // ADC counts per digit
                 const _Float16 hi = static_cast<_Float16>(delta);        // round to nearest even
                 const _Float16 lo = static_cast<_Float16>(delta - static_cast<float>(hi));
@@ -183,7 +190,8 @@ __global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u
                 terms[1][j >> 1] |= u32(__builtin_bit_cast(unsigned short, lo)) << shift;
             }
         }
-        uint4 *dst = gs + ((((cb * G + g) * W + w) * NOISY_TERMS) * KS + ks) * 64 + lane;
+        uint4 *dst = gs + ((((cb * G + g) * W * plan.planes + vw) * NOISY_TERMS) * KS + ks) * 64 +
+                     lane;
 #pragma unroll
         for (int term = 0; term < NOISY_TERMS; ++term)
             dst[term * KS * 64] = make_uint4(terms[term][0], terms[term][1], terms[term][2],
@@ -196,7 +204,7 @@ template __global__ void k_split_wide<2>(const mf_config, const u32 *, const flo
 template __global__ void k_split_wide<4>(const mf_config, const u32 *, const float *, i64, i64,
                                          i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 
-template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE>
+template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE, bool SLICE>
 __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_noisy_wide(
     const NoisyWidePlan plan,
                                                        const NoisyWideArgs args) {
@@ -211,7 +219,9 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
     const int lrow = lane & 31, lhalf = lane >> 5;
     const int A = plan.n_in, W = plan.n_w;
     const int G = int(args.G);
-    const int FR = W * NOISY_TERMS * KS;          // fragments per read
+    // Fragments per read staged in LDS (slice_pair reads take their planes from global
+    // memory: none).
+    const int FR = SLICE ? 0 : W * NOISY_TERMS * KS;
     const i64 cb = blockIdx.x;                    // chunk-relative 32-column block
     const i64 v0 = i64(blockIdx.y) * 128 + wave * 32;
     const i64 kp = args.kp;
@@ -304,36 +314,62 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
                     F[term][ks] = __builtin_bit_cast(
                         v8h_w, fl[((w * NOISY_TERMS + term) * KS + ks) * 64]);
         };
-        if (VNOISE) {
-            // Voltage variation (memfast/reference.py:77-82): every input value carries its
-            // own factor, x = digit * (1 + vv*z), held as fp16 hi + lo operands; a pair takes
-            // 3*KS MFMAs (hi*hi + lo*hi + hi*lo, the narrow voltage read's order).  One input
-            // slice a step (its two operands take the registers of two slices' digits).
+        if (VNOISE || SLICE) {
+            // One input slice a step.  Voltage variation (memfast/reference.py:77-82): every
+            // input value carries its own factor, x = digit * (1 + vv*z), held as fp16 hi + lo
+            // operands, and a pair takes 3*KS MFMAs (hi*hi + lo*hi + hi*lo, the narrow voltage
+            // read's order).  slice_pair read noise (memfast/reference.py:86-90): each (weight
+            // slice, input slice) pair reads its own plane of terms, from global memory.
             const i64 vunits = kp / 8;
             const uint4 *vbase = args.volt + (v0 / 32) * vunits * 32 + lane;
             const i64 vplane = ((args.n + 31) / 32) * vunits * 32;
+            const uint4 *planes = args.gs + (cb * G + g) * i64(W * A) * NOISY_TERMS * KS * 64 + lane;
             for (int a = 0; a < A; ++a) {
                 v8h_w hi[KS], lo[KS];
+                if (VNOISE) {
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const i64 at = (g * (P / 8) + ks * 2) * 32;
-                    hi[ks] = __builtin_bit_cast(v8h_w, live_block ? vbase[a * vplane + at] : uint4{});
-                    lo[ks] = __builtin_bit_cast(v8h_w, live_block ? vbase[(A + a) * vplane + at]
-                                                                  : uint4{});
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const i64 at = (g * (P / 8) + ks * 2) * 32;
+                        hi[ks] = __builtin_bit_cast(v8h_w, live_block ? vbase[a * vplane + at]
+                                                                      : uint4{});
+                        lo[ks] = __builtin_bit_cast(v8h_w, live_block ? vbase[(A + a) * vplane + at]
+                                                                      : uint4{});
+                    }
+                } else {
+                    digits(hi, a);
                 }
                 for (int w = 0; w < W; ++w) {
                     v8h_w F[NOISY_TERMS][KS];
-                    terms(F, w);
-                    v16f_w I = {};
+                    if (SLICE) {
+                        const uint4 *plane = planes + i64(w * A + a) * NOISY_TERMS * KS * 64;
 #pragma unroll
-                    for (int term = 0; term < NOISY_TERMS; ++term)
+                        for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                            for (int ks = 0; ks < KS; ++ks)
+                                F[term][ks] = __builtin_bit_cast(v8h_w, plane[(term * KS + ks) * 64]);
+                    } else {
+                        terms(F, w);
+                    }
+                    v16f_w I = {};
+                    if (VNOISE) {
+#pragma unroll
+                        for (int term = 0; term < NOISY_TERMS; ++term)
+#pragma unroll
+                            for (int ks = 0; ks < KS; ++ks)
+                                I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], hi[ks], I,
+                                                                           0, 0, 0);
 #pragma unroll
                         for (int ks = 0; ks < KS; ++ks)
-                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], hi[ks], I, 0,
-                                                                       0, 0);
+                            I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[0][ks], lo[ks], I, 0, 0,
+                                                                       0);
+                    } else {
 #pragma unroll
-                    for (int ks = 0; ks < KS; ++ks)
-                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[0][ks], lo[ks], I, 0, 0, 0);
+                        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                            for (int term = 0; term < NOISY_TERMS; ++term)
+                                I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], hi[ks], I,
+                                                                           0, 0, 0);
+                    }
                     convert(I, w, a);
                 }
             }
@@ -341,7 +377,7 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
         // Input slices in pairs: the digits of a slice are built once per read;
         // per weight slice the two currents are two interleaved MFMA chains.
         int a = 0;
-        for (; !VNOISE && a + 1 < A; a += 2) {
+        for (; !VNOISE && !SLICE && a + 1 < A; a += 2) {
             v8h_w B0[KS], B1[KS];
             digits(B0, a);
             digits(B1, a + 1);
@@ -360,7 +396,7 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
                 convert(I1, w, a + 1);
             }
         }
-        if (!VNOISE && a < A) {
+        if (!VNOISE && !SLICE && a < A) {
             v8h_w B0[KS];
             digits(B0, a);
             for (int w = 0; w < W; ++w) {
@@ -444,16 +480,25 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
-#define MF_NOISY_WIDE_INST(KS, NL, SMALL, FRMAX, VN)                                           \
-    template __global__ void k_noisy_wide<KS, NL, SMALL, FRMAX, VN>(const NoisyWidePlan,         \
-                                                                    const NoisyWideArgs);
-#define MF_NOISY_WIDE_INST4(KS, FRMAX)                  \
-    MF_NOISY_WIDE_INST(KS, false, true, FRMAX, false)   \
-    MF_NOISY_WIDE_INST(KS, true, true, FRMAX, false)    \
-    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, false)  \
-    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, false)   \
-    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, true)   \
-    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, true)
+#define MF_NOISY_WIDE_INST(KS, NL, SMALL, FRMAX, VN, SL)                                       \
+    template __global__ void k_noisy_wide<KS, NL, SMALL, FRMAX, VN, SL>(const NoisyWidePlan,     \
+                                                                        const NoisyWideArgs);
+#define MF_NOISY_WIDE_INST4(KS, FRMAX)                         \
+    MF_NOISY_WIDE_INST(KS, false, true, FRMAX, false, false)   \
+    MF_NOISY_WIDE_INST(KS, true, true, FRMAX, false, false)    \
+    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, false, false)  \
+    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, false, false)   \
+    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, true, false)   \
+    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, true, false)
+// slice_pair read noise: no LDS staging (FRMAX 1), digits of any width, with and without
+// voltage variation.
+#define MF_NOISY_WIDE_SLICE(KS)                                \
+    MF_NOISY_WIDE_INST(KS, false, false, 1, false, true)       \
+    MF_NOISY_WIDE_INST(KS, true, false, 1, false, true)        \
+    MF_NOISY_WIDE_INST(KS, false, false, 1, true, true)        \
+    MF_NOISY_WIDE_INST(KS, true, false, 1, true, true)
+MF_NOISY_WIDE_SLICE(2)
+MF_NOISY_WIDE_SLICE(4)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_TINY)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_SMALL)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_LARGE)

@@ -1086,6 +1086,18 @@ WIDE_MFMA = {
                            adc_bits=8),
                       dict(write_variation=0.02, voltage_variation=0.05, adc_nonlinearity=0.05),
                       45, 200, 70),
+    # slice_pair read noise: one plane of conductance terms per (weight, input) slice pair,
+    # read from global memory; BFP16 x INT4 (nine input planes) with drift, and 4-bit digits
+    # at 32-row reads with voltage variation and the S-curve ADC.
+    "bfp16_slice_pair": (WIDE["bfp16_int4"][0],
+                         dict(write_variation=0.02, read_variation=0.02, read_mode="slice_pair",
+                              drift_coefficient=0.05, drift_time=100.0), 70, 300, 150),
+    "int12_slice_pair_voltage": (dict(activation_bits=12, weight_bits=8, input_slice=(1, 3, 4, 4),
+                                      weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32),
+                                      rows_per_read=32, adc_bits=8),
+                                 dict(write_variation=0.02, read_variation=0.01,
+                                      read_mode="slice_pair", voltage_variation=0.03,
+                                      adc_nonlinearity=0.05), 45, 200, 70),
 }
 
 

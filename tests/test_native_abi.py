@@ -128,8 +128,9 @@ def test_noisy_mfma_kernels_require_fp16_range():
 def test_read_kernel_selection_by_noise_model():
     """Which read kernel each noise model takes (mf_mm_kernel, host only): the narrow noisy
     MFMA read covers voltage variation, slice_pair and output-mode read noise (also output
-    mode with voltage variation); the wide MFMA read covers voltage variation but not
-    per-slice read noise (it models it not at all, so it must never reach it)."""
+    mode with voltage variation); the wide MFMA read covers voltage variation and slice_pair
+    read noise but not output-mode read noise (it models it not at all, so it must never
+    reach it)."""
     from memfast_amd import Config, Nonidealities
     narrow = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
                   weight_slice=(1, 1, 2, 2, 2), array_size=(128, 128), rows_per_read=32)
@@ -144,7 +145,8 @@ def test_read_kernel_selection_by_noise_model():
         (narrow, dict(read_variation=0.01, read_mode="slice_pair", voltage_variation=0.01), 2),
         (wide, dict(read_variation=0.01), 3),
         (wide, dict(write_variation=0.02, voltage_variation=0.01), 3),
-        (wide, dict(read_variation=0.01, read_mode="slice_pair"), 0),
+        (wide, dict(read_variation=0.01, read_mode="slice_pair"), 3),
+        (wide, dict(read_variation=0.01, read_mode="slice_pair", voltage_variation=0.01), 3),
         (wide, dict(read_variation=0.01, read_mode="output"), 0),
     ]
     for kwargs, effects, kernel in cases:
