@@ -207,6 +207,27 @@ def _read_modes(out, device):
         out[f"read_mode_{name}"] = dict(ms_per_step=round(ms, 2), kernel_ms=round(kernel_ms, 2),
                                         gmac_per_s=round(SIZE**3 / (ms * 1e-3) / 1e9, 1),
                                         kernel={0: "general FP32", 2: "noisy MFMA"}[kernel])
+    # Wide codes (config 5's slicing: BFP16 x INT4, nine input and three weight slices,
+    # 64x64 arrays) at the same size, on the wide MFMA read: shared read noise, voltage
+    # variation (real input operands) and slice_pair read noise (a plane of terms per
+    # input slice, read from global memory).
+    wide = dict(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
+                weight_slice=(1, 1, 2), bw_e=8, adc_bits=(6, 6, 7))
+    shared = dict(read_variation=0.01, drift_coefficient=0.05, drift_time=100.0)
+    wide_modes = {
+        "wide_shared": shared,
+        "wide_voltage": shared | dict(voltage_variation=0.01),
+        "wide_slice_pair": shared | dict(read_mode="slice_pair"),
+    }
+    for name, effects in wide_modes.items():
+        cfg = memfast.Config(**wide, nonidealities=memfast.Nonidealities(**effects))
+        kernel = hip.mm_kernel(cfg, SIZE, SIZE // 64, SIZE // 64)
+        assert kernel == 3, (name, kernel)
+        sim = memfast.Simulator(cfg, device=device)
+        ms, kernel_ms = time_steps(lambda: sim.mm(a, b), 3, 1)
+        out[f"read_mode_{name}"] = dict(ms_per_step=round(ms, 2), kernel_ms=round(kernel_ms, 2),
+                                        gmac_per_s=round(SIZE**3 / (ms * 1e-3) / 1e9, 1),
+                                        kernel="wide MFMA")
 
 
 def _config1(out, int8, device):

@@ -134,20 +134,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t noisy_buffer(const void *base,
                                              0x00020000);
 }
 
-// Eight input digits (bytes of `word`, slice (shift, mask)) as eight fp16.
+// Eight input digits (bytes of `word`, slice (shift, mask)) as eight fp16.  Each digit d
+// (at most 8 bits) becomes the low byte of fp16 0x64dd = 1024 + d: one v_perm places two
+// digits beside two 0x64 bytes, and one packed fp16 subtraction of 1024 leaves d exactly
+// (the same fp16 values as a conversion).  Six instructions per four digits.
 __device__ __forceinline__ v8h digits_f16(uint2 word, int shift, u32 mask4) {
+    typedef _Float16 v2f16 __attribute__((ext_vector_type(2)));
+    const v2f16 base = {_Float16(1024.0f), _Float16(1024.0f)};
     const u32 lo = (word.x >> shift) & mask4, hi = (word.y >> shift) & mask4;
-    // (byte of a u32) -> float compiles to v_cvt_f32_ubyte{0..3}; small integers
-    // pack into fp16 exactly (round toward zero is exact here).
-    const float f[8] = {float(lo & 0xFFu), float((lo >> 8) & 0xFFu), float((lo >> 16) & 0xFFu),
-                        float(lo >> 24), float(hi & 0xFFu), float((hi >> 8) & 0xFFu),
-                        float((hi >> 16) & 0xFFu), float(hi >> 24)};
-    typedef __fp16 v2h __attribute__((ext_vector_type(2)));
-    const v2h a = __builtin_amdgcn_cvt_pkrtz(f[0], f[1]), b = __builtin_amdgcn_cvt_pkrtz(f[2], f[3]);
-    const v2h c = __builtin_amdgcn_cvt_pkrtz(f[4], f[5]), d = __builtin_amdgcn_cvt_pkrtz(f[6], f[7]);
-    uint4 packed = make_uint4(__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b),
-                              __builtin_bit_cast(u32, c), __builtin_bit_cast(u32, d));
-    return __builtin_bit_cast(v8h, packed);
+    // Byte pool of v_perm(src0, src1, sel): src1 bytes 0-3 (0x64), src0 bytes 4-7.
+    const u32 k64 = 0x64646464u;
+    const u32 w[4] = {__builtin_amdgcn_perm(lo, k64, 0x00050004u), __builtin_amdgcn_perm(lo, k64, 0x00070006u),
+                      __builtin_amdgcn_perm(hi, k64, 0x00050004u), __builtin_amdgcn_perm(hi, k64, 0x00070006u)};
+    u32 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __builtin_bit_cast(u32, __builtin_bit_cast(v2f16, w[i]) - base);
+    return __builtin_bit_cast(v8h, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
 // Eight consecutive input codes of one vector: bytes (narrow) or 32-bit words (wide).

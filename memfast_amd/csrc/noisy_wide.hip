@@ -88,6 +88,25 @@ __device__ __forceinline__ v8h_w digits_any(uint4 c, int shift, u32 mask2) {
     return __builtin_bit_cast(v8h_w, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
+// Digits of slice (shift, mask2), any width up to 8 bits, of eight 16-bit codes as eight
+// fp16: each field d is OR-ed into the mantissa of fp16 1024 (0x6400, mantissa step 1),
+// and one packed fp16 subtraction of 1024 leaves d exactly (the same fp16 values as a
+// conversion).  Three instructions per two digits: shift, and-or (one v_and_or_b32, the
+// constant held in a VGPR: VOP3 takes no literal), packed subtract.
+__device__ __forceinline__ v8h_w digits_magic(uint4 c, int shift, u32 mask2, u32 magic) {
+    typedef _Float16 v2h_w __attribute__((ext_vector_type(2)));
+    const v2h_w base = {_Float16(1024.0f), _Float16(1024.0f)};
+    const u32 w[4] = {c.x, c.y, c.z, c.w};
+    u32 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u32 x;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(x) : "v"(w[i] >> shift), "s"(mask2), "v"(magic));
+        o[i] = __builtin_bit_cast(u32, __builtin_bit_cast(v2h_w, x) - base);
+    }
+    return __builtin_bit_cast(v8h_w, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
 // One 1 KiB LDS DMA: lane l's 16 bytes at src go to lds_base + 16 * l.  Issued
 // as inline assembly so that the compiler's wait-count analysis does not track
 // it (it would otherwise wait for it at the next loop header); the kernel waits
@@ -205,7 +224,7 @@ template __global__ void k_split_wide<4>(const mf_config, const u32 *, const flo
                                          i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 
 template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE, bool SLICE>
-__global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_noisy_wide(
+__global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, KS)) void k_noisy_wide(
     const NoisyWidePlan plan,
                                                        const NoisyWideArgs args) {
     // Two LDS objects (read g in one, read g+1 arriving in the other) so that the
@@ -273,6 +292,8 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
     __syncthreads();
 
     const u32 sel_bias = 0x04000400u;
+    u32 magic16 = 0x64006400u;   // fp16 1024 in both halves (digits_magic)
+    settle_one(magic16);
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     auto step = [&](int g, const uint4 *sCur, uint4 *sNext) {
         if (g + 1 < G) fetch(g + 1, sNext);
@@ -303,8 +324,7 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_n
             const u32 mask2 = u32(__builtin_amdgcn_readlane(int(slice_mask2), a));
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                B[ks] = SMALL ? digits_small(qc[ks], shift, mask2, sel_bias)
-                              : digits_any(qc[ks], shift, mask2);
+                B[ks] = digits_magic(qc[ks], shift, mask2, magic16);
         };
         auto terms = [&](v8h_w (&F)[NOISY_TERMS][KS], int w) {
 #pragma unroll
