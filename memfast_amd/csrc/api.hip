@@ -431,7 +431,7 @@ i64 noisy_voltage_bytes(const mf_config *cfg, i64 n, i64 m) {
                            : 0;
 }
 
-// Whether a split noisy read runs k_noisy_pairs (one wave per input slice, 32 vectors):
+// Whether a split noisy read runs k_noisy_pairs (one wave per weight slice, 32 vectors):
 // batches of at most 32 vectors, where the four-wave tile (64 vectors, the slices one
 // after another) would leave half its waves idle; plain and S-curve reads (no voltage,
 // slice_pair or output-mode noise).
@@ -546,11 +546,11 @@ int launch_noisy(const mf_config *cfg, const NoisyPlan &plan, int ks, const u8 *
         const bool nl = cfg->has_nonlinear != 0;
         const bool slice = plan.planes > 1 && !plan.out_noise;
         // A split read of at most 32 vectors runs k_noisy_pairs: one read per workgroup,
-        // one wave per input slice.
+        // one wave per weight slice.
         const bool pairs = use_split && noisy_small_tile(cfg, n);
         const dim3 grid = pairs ? dim3{unsigned(CB), unsigned((n + 31) / 32), unsigned(g_run)}
                                 : dim3{unsigned((n + 63) / 64), unsigned(CB / 2), gz};
-        const dim3 block{pairs ? unsigned(64 * cfg->n_in) : 256u};
+        const dim3 block{pairs ? unsigned(64 * cfg->n_w) : 256u};
         if (pairs) {
             args.g_step = 1;
             args.restored = 1;   // the values (float(T) * xs) * ws; consumers only sum them
@@ -1815,7 +1815,9 @@ int mf_gru_sequence(const mf_config *cfg, int64_t steps, int32_t reverse, int64_
             a.scale = scale;
             a.xscale_out = xscale;
             a.status = status;
-            hipLaunchKernelGGL(k_gru_step, dim3(unsigned(batch)), dim3(1024), 3 * width * 4, s, a);
+            // One thread per hidden unit (up to 1024; more units loop).
+            const unsigned threads = unsigned(width >= 1024 ? 1024 : (width + 63) / 64 * 64);
+            hipLaunchKernelGGL(k_gru_step, dim3(unsigned(batch)), dim3(threads), width * 4, s, a);
         } else {
             hipLaunchKernelGGL(k_gru_gates, dim3(grid_for(batch * width)), dim3(256), 0, s,
                                projected + t * proj_step, proj_row, hidden, ld_hidden, hx, ldx,
@@ -2165,7 +2167,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
         fn = table[which][mode][slice ? 1 : 0][nl ? 1 : 0];
         if (n > 0 && noisy_small_tile(cfg, n) && variant_split(variant) != 1) {
             // A split read of at most 32 vectors (the automatic split applies below 512
-            // four-wave blocks, 32768 output columns): k_noisy_pairs, one wave per input
+            // four-wave blocks, 32768 output columns): k_noisy_pairs, one wave per weight
             // slice.
             const void *pairs[3][2] = {
                 {reinterpret_cast<const void *>(&k_noisy_pairs<2, 5, false>),
@@ -2175,7 +2177,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
                 {reinterpret_cast<const void *>(&k_noisy_pairs<4, 5, false>),
                  reinterpret_cast<const void *>(&k_noisy_pairs<4, 5, true>)}};
             fn = pairs[which][nl ? 1 : 0];
-            threads = 64 * cfg->n_in;
+            threads = 64 * cfg->n_w;
         }
     } else if (kernel_id == 3) {
         // The LDS tier: the schedule's (tier field 1-3), else launch_noisy_wide's automatic one.

@@ -190,7 +190,7 @@ __global__ void k_split_conductances(const mf_config cfg, const u8 *packed_t, co
                                      i64 CB, const NoisyPlan plan, uint4 *gs);
 template <int KS, int NA, bool NONLINEAR, bool VNOISE, bool SLICE, bool OUTN>
 __global__ void k_noisy(const NoisyPlan plan, const NoisyArgs args);
-// Split read of batches of at most 32 vectors: block = one wave per input slice on 32
+// Split read of batches of at most 32 vectors: block = one wave per weight slice on 32
 // vectors x 32 columns and one read (grid: column blocks, vector blocks, reads); writes
 // slice totals [n, G, ldo], or with args.restored the restored (float(T) * xs) * ws
 // (plain and S-curve reads).

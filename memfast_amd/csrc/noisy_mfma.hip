@@ -642,21 +642,22 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
 }
 
 // Split reads of small batches (at most 32 vectors): one workgroup per (32-column block,
-// read) with one wave per input slice, so a read's 25 pairs (config 3) run on five waves at
-// once instead of one after another.  Each wave builds its slice's digits once and converts
-// its pairs with every weight slice (fa*fw*(0x400000 + code) modulo 2^32, as noisy_read),
-// the waves add their words in LDS (integer sums: any order gives the same totals) and the
-// block writes the read's slice totals [n, G, ldo], or with args.restored their scale
-// restore (float(T) * xs) * ws rounded as the fused epilogue rounds it; k_restore_sum_f32
-// or k_gru_step sums them over the reads in torch's order.  Plain and S-curve reads (terms
-// event-independent or shared read noise).
+// read) with one wave per weight slice, so a read's 25 pairs (config 3) run on five waves
+// at once instead of one after another.  Each wave loads its weight slice's terms once (a
+// block reads every term of its read once) and converts its pairs with every input slice,
+// whose digits it builds from the read's codes (fa*fw*(0x400000 + code) modulo 2^32, as
+// noisy_read); the waves add their words in LDS (integer sums: any order gives the same
+// totals) and the block writes the read's slice totals [n, G, ldo], or with args.restored
+// their scale restore (float(T) * xs) * ws rounded as the fused epilogue rounds it;
+// k_restore_sum_f32 or k_gru_step sums them over the reads in torch's order.  Plain and
+// S-curve reads (terms event-independent or shared read noise).
 template <int KS, int NA, bool NONLINEAR>
 __global__ __launch_bounds__(512) void k_noisy_pairs(const NoisyPlan plan, const NoisyArgs args) {
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     constexpr int P = 16 * KS;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int a = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's input slice
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's weight slice
     const int lrow = lane & 31, lhalf = lane >> 5;
     const int W = plan.n_w, A = plan.n_in;
     const i64 cb = blockIdx.x;                       // chunk-relative 32-column block
@@ -667,37 +668,62 @@ __global__ __launch_bounds__(512) void k_noisy_pairs(const NoisyPlan plan, const
     const __amdgpu_buffer_rsrc_t qbuf = noisy_buffer(args.q + v0 * kp, vrows * kp);
     const int q_off = lrow * int(kp) + lhalf * 8 + g * P;
     // Terms of (weight slice w, column block cb, read g): [w][CB][G][term][KS][64 lanes].
-    const uint4 *frag = args.gs + (cb * G + g) * NOISY_TERMS * KS * 64 + lane;
-    const i64 w_stride = args.CB * G * NOISY_TERMS * KS * 64;
-    auto load_terms = [&](v8h (&F)[NOISY_TERMS][KS], int w) {
+    const uint4 *frag = args.gs + (cb * G + g) * NOISY_TERMS * KS * 64 + lane +
+                        w * (args.CB * G * NOISY_TERMS * KS * 64);
+    v8h F[NOISY_TERMS][KS];
 #pragma unroll
-        for (int term = 0; term < NOISY_TERMS; ++term)
+    for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                F[term][ks] = __builtin_bit_cast(v8h, frag[w * w_stride + (term * KS + ks) * 64]);
-    };
-    v8h Fa[NOISY_TERMS][KS], Fb[NOISY_TERMS][KS];
-    load_terms(Fa, 0);
-    v8h digits[KS];
+        for (int ks = 0; ks < KS; ++ks)
+            F[term][ks] = __builtin_bit_cast(v8h, frag[(term * KS + ks) * 64]);
+    uint2 codes[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const u32 x = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16, 0, 0);
-        const u32 y = __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16 + 4, 0, 0);
-        digits[ks] = digits_f16(make_uint2(x, y), plan.in_shift[a], plan.in_mask4[a]);
+    for (int ks = 0; ks < KS; ++ks)
+        codes[ks] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16, 0, 0),
+                               __builtin_amdgcn_raw_buffer_load_b32(qbuf, q_off + ks * 16 + 4, 0, 0));
+    // LDS: first the digits of every input slice (wave w builds slices w, w + W, ..), then
+    // the waves' total words.
+    __shared__ u32 shared_words[8 * 16 * 64];
+    uint4 *sdigits = reinterpret_cast<uint4 *>(shared_words);   // [a][ks][64 lanes]
+    for (int a = w; a < A; a += W)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            sdigits[(a * KS + ks) * 64 + lane] = __builtin_bit_cast(
+                uint4, digits_f16(codes[ks], plan.in_shift[a], plan.in_mask4[a]));
+    __syncthreads();
+    // The epilogue's scales (outputs r = w, w + W, ..: the first four) are loaded now, so
+    // their latency overlaps the pairs.
+    const i64 n_out = v0 + lrow;
+    const i64 col_tile = args.c_begin + cb * 32;
+    auto column = [&](int r) { return col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3); };
+    const float xs = args.restored && n_out < args.n ? args.xscale[n_out * G + g] : 0.0f;
+    float ws_first[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = w + j * W;
+        if (args.restored && r < 16 && column(r) < args.ncols)
+            ws_first[j] = args.wscale[i64(g) * args.ldws + column(r)];
     }
     u32 Ti[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) Ti[r] = 0u;
+    const float top = plan.top_magic[w], alpha = plan.alpha[w];
     // The MFMA order of noisy_read (terms outer, row blocks inner), so the totals are its
-    // totals bit for bit.
-    auto pair = [&](const v8h (&F)[NOISY_TERMS][KS], int w) {
+    // totals bit for bit.  Unrolled over the input slices (at most NA), so that a slice's
+    // MFMAs can issue while the previous slice's currents are converted.
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+        if (a >= A) break;
+        v8h digits[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            digits[ks] = __builtin_bit_cast(v8h, sdigits[(a * KS + ks) * 64 + lane]);
         v16f I = {};
 #pragma unroll
         for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
                 I = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[term][ks], digits[ks], I, 0, 0, 0);
-        const float top = plan.top_magic[w], alpha = plan.alpha[w];
         const u32 f24 = u32(int(plan.f24[a][w] << 8) >> 8);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -706,33 +732,26 @@ __global__ __launch_bounds__(512) void k_noisy_pairs(const NoisyPlan plan, const
             const int low = int(__float_as_uint(y) << 8) >> 8;
             Ti[r] += u32(low) * f24;
         }
-    };
-    // Weight slices in pairs, the next slice's terms in flight during a slice's pair.
-    int w = 0;
-    for (; w + 1 < W; w += 2) {
-        load_terms(Fb, w + 1);
-        pair(Fa, w);
-        if (w + 2 < W) load_terms(Fa, w + 2);
-        pair(Fb, w + 1);
     }
-    if (w < W) pair(Fa, w);
-    // Sum the slices' words: wave a writes its plane, then wave a adds outputs r = a, a + A..
-    __shared__ u32 planes[8][16][64];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) planes[a][r][lane] = Ti[r];
+    // Sum the slices' words: wave w writes its plane, then wave w adds outputs r = w, w + W..
+    // (in the digits' LDS, once every wave has read them).
+    u32 (*planes)[16][64] = reinterpret_cast<u32 (*)[16][64]>(shared_words);
     __syncthreads();
-    const i64 n_out = v0 + lrow;
-    const i64 col_tile = args.c_begin + cb * 32;
-    const float xs = args.restored && n_out < args.n ? args.xscale[n_out * G + g] : 0.0f;
-    for (int r = a; r < 16; r += A) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) planes[w][r][lane] = Ti[r];
+    __syncthreads();
+    for (int j = 0, r = w; r < 16; ++j, r += W) {
         u32 total = plan.bias;
-        for (int j = 0; j < A; ++j) total += planes[j][r][lane];
-        const i64 c = col_tile + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+        for (int k = 0; k < W; ++k) total += planes[k][r][lane];
+        const i64 c = column(r);
         if (n_out < args.n && c < args.ncols) {
             float v = float(int(total));
             if (args.restored) {
                 v = v * xs;
-                v = v * args.wscale[i64(g) * args.ldws + c];
+                // (selects, not an index: a dynamic index would put ws_first in scratch)
+                const float ws = j == 0 ? ws_first[0] : j == 1 ? ws_first[1] : j == 2 ? ws_first[2]
+                                 : j == 3 ? ws_first[3] : args.wscale[i64(g) * args.ldws + c];
+                v = v * ws;
             }
             args.out[(n_out * G + g) * args.ldo + c] = v;
         }

@@ -719,7 +719,7 @@ def packed_columns(packed):
 @pytest.mark.parametrize("mode", ["write", "shared_scurve", "saf_drift", "binary8", "rows64"])
 def test_small_batch_split_read_matches_unsplit_read(hip_device, mode):
     """Batches of at most 32 vectors split their reads over k_noisy_pairs (one workgroup per
-    read and 32-column block, one wave per input slice; the restored values are summed by
+    read and 32-column block, one wave per weight slice; the restored values are summed by
     the split epilogue).  Every schedule (automatic, unsplit k_noisy, a 2-way split) gives
     the same output bit for bit: 32- and 64-row reads, 5 and 8 input slices, S-curve ADCs;
     and the product is the oracle's under the flip accounting."""

@@ -194,7 +194,7 @@ def test_resources_follow_the_schedule(hip_device):
     # The automatic tier is the smallest that holds a read (3 weight slices x 2 terms x 4),
     # but at least the 36-fragment one for 64-row reads.
     assert program.resources(wide, 64, 64, 0, kernel=3) == tiers[2]
-    # The noisy read of at most 32 vectors runs k_noisy_pairs (one wave per input slice)
+    # The noisy read of at most 32 vectors runs k_noisy_pairs (one wave per weight slice)
     # unless the schedule never splits.
     noisy = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02))
     program = hip.program(noisy, 64, 64, hip_device.index)
@@ -203,5 +203,5 @@ def test_resources_follow_the_schedule(hip_device):
                                 variant=tuning.schedule_variant(dict(split=1)))
     large = program.resources(noisy, 64, 64, 0, kernel=2, batch=33)
     say("noisy small batch", small, "unsplit", unsplit, "large", large)
-    assert small["threads"] == 64 * len(noisy.input_layout)
+    assert small["threads"] == 64 * len(noisy.weight_layout)
     assert unsplit == large and large["threads"] == 256
