@@ -187,9 +187,8 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
  *              restores and sums them); MF_E_RESOURCE when the workspace cannot
  *              hold the chunks' totals (mf_mm_workspace prices them).
  *   bits 16-19 wide noisy-device read: LDS capacity per read, 0 automatic (the
- *              smallest holding a read's conductance terms, at least 36 fragments
- *              for 64-row reads), 1..3: 24, 36 or 72 fragments; MF_E_RESOURCE when
- *              it cannot hold them. */
+ *              smallest holding a read's conductance terms), 1..3: 24, 36 or 72
+ *              fragments; MF_E_RESOURCE when it cannot hold them. */
 #define MF_MM_SPLIT_SHIFT 12
 #define MF_MM_TIER_SHIFT 16
 

@@ -716,10 +716,8 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
     if (max_cb < 2) return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
     const int frags = cfg->n_w * NOISY_TERMS * ks;
     if (frags > WIDE_FRAGS_LARGE) return fail(MF_E_RESOURCE, "too many weight slices for LDS");
-    // Automatic: the smallest capacity that holds a read, but at least the 36-fragment one
-    // for 64-row reads, whose kernels run faster at two blocks per CU than at three (config 5,
-    // 2048 x 4096 x 4096: 3.45 against 3.59 ms).
-    int tier = frags > WIDE_FRAGS_SMALL ? 2 : (frags > WIDE_FRAGS_TINY || ks == 4) ? 1 : 0;
+    // Automatic: the smallest capacity that holds a read.
+    int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
     if (tier_request > 0) {
         // A tuned schedule's LDS capacity: 24, 36 or 72 fragments per read.
         const int capacity[3] = {WIDE_FRAGS_TINY, WIDE_FRAGS_SMALL, WIDE_FRAGS_LARGE};
@@ -2182,7 +2180,7 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
     } else if (kernel_id == 3) {
         // The LDS tier: the schedule's (tier field 1-3), else launch_noisy_wide's automatic one.
         const int frags = cfg->n_w * NOISY_TERMS * (ks4 ? 4 : 2);
-        int tier = frags > WIDE_FRAGS_SMALL ? 2 : (frags > WIDE_FRAGS_TINY || ks4) ? 1 : 0;
+        int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
         if (variant_tier(variant) > 0) tier = variant_tier(variant) - 1;
         bool small = true;   // every input digit of at most 2 bits (build_noisy_wide_plan)
         for (int a = 0; a < cfg->n_in; ++a) small = small && cfg->in_mask[a] <= 3;

@@ -191,9 +191,8 @@ def test_resources_follow_the_schedule(hip_device):
              for tier in tuning.TIERS}
     say("wide tiers", tiers)
     assert tiers[1]["shared"] < tiers[2]["shared"] < tiers[3]["shared"]
-    # The automatic tier is the smallest that holds a read (3 weight slices x 2 terms x 4),
-    # but at least the 36-fragment one for 64-row reads.
-    assert program.resources(wide, 64, 64, 0, kernel=3) == tiers[2]
+    # The automatic tier is the smallest that holds a read (3 weight slices x 2 terms x 4).
+    assert program.resources(wide, 64, 64, 0, kernel=3) == tiers[1]
     # The noisy read of at most 32 vectors runs k_noisy_pairs (one wave per weight slice)
     # unless the schedule never splits.
     noisy = Config(**INT8, nonidealities=Nonidealities(write_variation=0.02))
