@@ -622,7 +622,7 @@ int wide_term_planes(const mf_config *cfg) {
 // kernel's device model, input codes of at most 16 bits with digits up to 255,
 // fewer than 256 reads, exact int32 totals.
 bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *plan, int *ks,
-                           bool *small, const char **why) {
+                           const char **why) {
     if (!cfg->wide) { *why = "narrow codes"; return false; }
     if (cfg->precise) { *why = "FP64 currents"; return false; }
     if (cfg->has_read && cfg->read_mode == MF_READ_OUTPUT) { *why = "output-mode read noise"; return false; }
@@ -640,11 +640,9 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
     const i64 G = m * cfg->reads;
     if (G >= 256) { *why = "256 or more reads per output"; return false; }
     if (!all_cascade_columns_wide(cfg->cols, p)) { *why = "interleaved summation columns"; return false; }
-    bool all_small = true;
     double fa_sum = 0.0, fw_sum = 0.0;
     for (int a = 0; a < cfg->n_in; ++a) {
         if (cfg->in_mask[a] > 255) { *why = "input digits above 255"; return false; }
-        all_small = all_small && cfg->in_mask[a] <= 3;
         fa_sum += std::fabs(double(cfg->in_factor[a]));
     }
     for (int w = 0; w < cfg->n_w; ++w) fw_sum += std::fabs(double(cfg->w_factor[w])) * cfg->adc_max[w];
@@ -674,7 +672,6 @@ bool build_noisy_wide_plan(const mf_config *cfg, i64 m, i64 p, NoisyWidePlan *pl
     }
     plan->bias = u32(0) - u32(u64(factor_sum) * 0x400000u);
     *ks = cfg->read_rows / 16;
-    *small = all_small;
     return true;
 }
 
@@ -703,7 +700,7 @@ bool wide_extent_ok(i64 n, i64 m, const mf_config *cfg) {
 
 // Repack codes to 16 bits, split conductances and run k_noisy_wide over column
 // chunks that fit the workspace.  g: optional injected conductances.
-int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, bool small,
+int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks,
                       const u32 *q, const double *xscale, i64 n, i64 m, const u32 *packed,
                       const double *wscale, i64 p, const float *g, u32 seed, u64 event,
                       double *out, i64 ldo, void *workspace, i64 bytes, int totals, u32 *status,
@@ -768,36 +765,31 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks, b
             // slice_pair read noise: every (weight, input) slice pair has its own plane of
             // terms, read from global memory rather than staged in LDS.
 #define MF_WIDE_SLICE(KS)                                                                          \
-    if (volt && nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, false, 1, true, true>), grid,        \
+    if (volt && nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, 1, true, true>), grid,        \
                                        dim3(256), 0, s, plan, args);                                \
-    else if (volt) hipLaunchKernelGGL((k_noisy_wide<KS, false, false, 1, true, true>), grid,        \
+    else if (volt) hipLaunchKernelGGL((k_noisy_wide<KS, false, 1, true, true>), grid,        \
                                       dim3(256), 0, s, plan, args);                                 \
-    else if (nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, false, 1, false, true>), grid,          \
+    else if (nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, 1, false, true>), grid,          \
                                     dim3(256), 0, s, plan, args);                                   \
-    else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, 1, false, true>), grid, dim3(256), 0,   \
+    else hipLaunchKernelGGL((k_noisy_wide<KS, false, 1, false, true>), grid, dim3(256), 0,   \
                             s, plan, args);
             if (ks == 4) { MF_WIDE_SLICE(4) } else { MF_WIDE_SLICE(2) }
 #undef MF_WIDE_SLICE
             continue;
         }
-#define MF_WIDE_LAUNCH(KS, FR)                                                                         \
-    if (volt && nl) {                                                                                  \
-        hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, true, false>), grid, dim3(256), 0, s, plan,      \
-                           args);                                                                      \
-    } else if (volt) {                                                                                 \
-        hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, true, false>), grid, dim3(256), 0, s, plan,     \
-                           args);                                                                      \
-    } else if (nl) {                                                                                   \
-        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, true, true, FR, false, false>), grid, dim3(256), 0, s, \
-                                      plan, args);                                                     \
-        else hipLaunchKernelGGL((k_noisy_wide<KS, true, false, FR, false, false>), grid, dim3(256), 0, s,      \
-                                plan, args);                                                           \
-    } else {                                                                                           \
-        if (small) hipLaunchKernelGGL((k_noisy_wide<KS, false, true, FR, false, false>), grid, dim3(256), 0,   \
-                                      s, plan, args);                                                  \
-        else hipLaunchKernelGGL((k_noisy_wide<KS, false, false, FR, false, false>), grid, dim3(256), 0, s,     \
-                                plan, args);                                                           \
-    }
+#define MF_WIDE_LAUNCH(KS, FR)                                                                   \
+    if (volt && nl)                                                                              \
+        hipLaunchKernelGGL((k_noisy_wide<KS, true, FR, true, false>), grid, dim3(256), 0, s, plan,  \
+                           args);                                                                \
+    else if (volt)                                                                               \
+        hipLaunchKernelGGL((k_noisy_wide<KS, false, FR, true, false>), grid, dim3(256), 0, s, plan, \
+                           args);                                                                \
+    else if (nl)                                                                                 \
+        hipLaunchKernelGGL((k_noisy_wide<KS, true, FR, false, false>), grid, dim3(256), 0, s, plan, \
+                           args);                                                                \
+    else                                                                                         \
+        hipLaunchKernelGGL((k_noisy_wide<KS, false, FR, false, false>), grid, dim3(256), 0, s,      \
+                           plan, args);
         if (ks == 4) {
             if (tier == 2) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_LARGE) }
             else if (tier == 1) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_SMALL) }
@@ -1314,9 +1306,8 @@ static bool ideal_extent_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
 static bool wide_plan_ok(const mf_config *cfg, i64 n, i64 m, i64 p) {
     NoisyWidePlan plan;
     int ks = 0;
-    bool small = false;
     const char *why = "";
-    return wide_extent_ok(n, m, cfg) && build_noisy_wide_plan(cfg, m, p, &plan, &ks, &small, &why);
+    return wide_extent_ok(n, m, cfg) && build_noisy_wide_plan(cfg, m, p, &plan, &ks, &why);
 }
 
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
@@ -2019,15 +2010,14 @@ int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, in
         return fail(MF_E_INVALID, "invalid mm arguments");
     NoisyWidePlan wplan;
     int ks = 0;
-    bool small = false;
     const char *why = "";
     if (!g && workspace && (reinterpret_cast<uintptr_t>(workspace) % 256) == 0 &&
-        wide_extent_ok(n, m, cfg) && build_noisy_wide_plan(cfg, m, p, &wplan, &ks, &small, &why) &&
+        wide_extent_ok(n, m, cfg) && build_noisy_wide_plan(cfg, m, p, &wplan, &ks, &why) &&
         workspace_bytes >= wide_prefix_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m)) {
         hipStream_t s = static_cast<hipStream_t>(stream);
         std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
         if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-        const int launched = launch_noisy_wide(cfg, wplan, ks, small, q, xscale, n, m, packed,
+        const int launched = launch_noisy_wide(cfg, wplan, ks, q, xscale, n, m, packed,
                                                wscale, p, nullptr, seed, event, out, ldo,
                                                workspace, workspace_bytes, 0, status, s,
                                                variant_tier(variant));
@@ -2084,14 +2074,13 @@ int mf_mm_totals_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_
         return fail(MF_E_INVALID, "workspace must be 256-byte aligned");
     NoisyWidePlan plan;
     int ks = 0;
-    bool small = false;
     const char *why = "";
-    if (!wide_extent_ok(n, m, cfg) || !build_noisy_wide_plan(cfg, m, p, &plan, &ks, &small, &why))
+    if (!wide_extent_ok(n, m, cfg) || !build_noisy_wide_plan(cfg, m, p, &plan, &ks, &why))
         return fail(MF_E_UNSUPPORTED, "wide MFMA read not applicable: %s", why);
     if (workspace_bytes < wide_prefix_bytes(n, m, cfg) + 2 * wide_block_bytes(cfg, m))
         return fail(MF_E_RESOURCE, "workspace below one 64-column chunk");
     const i64 ncols = p * cfg->cols;
-    return launch_noisy_wide(cfg, plan, ks, small, q, nullptr, n, m, packed, nullptr, p, g, seed,
+    return launch_noisy_wide(cfg, plan, ks, q, nullptr, n, m, packed, nullptr, p, g, seed,
                              event, totals, ncols, workspace, workspace_bytes, 1, nullptr,
                              static_cast<hipStream_t>(stream));
 }
@@ -2182,22 +2171,18 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
         const int frags = cfg->n_w * NOISY_TERMS * (ks4 ? 4 : 2);
         int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
         if (variant_tier(variant) > 0) tier = variant_tier(variant) - 1;
-        bool small = true;   // every input digit of at most 2 bits (build_noisy_wide_plan)
-        for (int a = 0; a < cfg->n_in; ++a) small = small && cfg->in_mask[a] <= 3;
         const bool vn = cfg->has_vnoise != 0;
         const bool sl = wide_term_planes(cfg) > 1;   // slice_pair: planes from global memory
-#define MF_WIDE_FN(KS, FR)                                                                         \
-    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, true, false>)       \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, true, false>))     \
-     : nl ? (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, true, FR, false, false>)   \
-                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, FR, false, false>)) \
-          : (small ? reinterpret_cast<const void *>(&k_noisy_wide<KS, false, true, FR, false, false>)  \
-                   : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, FR, false, false>)))
+#define MF_WIDE_FN(KS, FR)                                                                       \
+    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, FR, true, false>)          \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, FR, true, false>))        \
+        : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, FR, false, false>)         \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, FR, false, false>)))
 #define MF_WIDE_SLICE_FN(KS)                                                                     \
-    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, 1, true, true>)      \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, 1, true, true>))    \
-        : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, false, 1, false, true>)     \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, false, 1, false, true>)))
+    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, 1, true, true>)            \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, 1, true, true>))          \
+        : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, 1, false, true>)           \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, 1, false, true>)))
         if (sl) fn = ks4 ? MF_WIDE_SLICE_FN(4) : MF_WIDE_SLICE_FN(2);
         else if (ks4) fn = tier == 2 ? MF_WIDE_FN(4, WIDE_FRAGS_LARGE)
                            : tier == 1 ? MF_WIDE_FN(4, WIDE_FRAGS_SMALL) : MF_WIDE_FN(4, WIDE_FRAGS_TINY);

@@ -263,7 +263,7 @@ constexpr int wide_blocks_per_cu(int frmax, bool nonlinear, bool vnoise, int ks)
 // VNOISE: voltage variation (real input operands from args.volt, one input slice a step).
 // SLICE: slice_pair read noise (a plane of terms per (weight slice, input slice), read from
 // global memory: FRMAX 1, no LDS staging).
-template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE, bool SLICE>
+template <int KS, bool NONLINEAR, int FRMAX, bool VNOISE, bool SLICE>
 __global__ void k_noisy_wide(const NoisyWidePlan plan, const NoisyWideArgs args);
 
 // ---- FP64 restore and read sum (stable.hip) --------------------------------

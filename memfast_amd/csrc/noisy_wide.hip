@@ -51,43 +51,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wide_buffer(const void *base, 
                                              0x00020000);
 }
 
-// x * 0x101 + bias in one v_mad_u32_u24 (x < 2^24); the compiler otherwise
-// emits a shift-add and an add.  `bias` is kept in a VGPR (one SGPR operand).
-__device__ __forceinline__ u32 mad_u24(u32 x, u32 mul, u32 bias) {
-    u32 r;
-    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mul), "v"(bias));
-    return r;
-}
-
-// Digits of slice (shift, mask <= 3) of eight 16-bit codes (rows 0..7, two per
-// word, low half first) as eight fp16.  x = d0 | d1 << 16 selects, per output
-// byte, the low or high byte of fp16(d) from two 4-entry byte tables with one
-// v_perm: selector bytes (d0, 4 + d0, d1, 4 + d1) = x * 0x101 + 0x04000400.
-__device__ __forceinline__ v8h_w digits_small(uint4 c, int shift, u32 mask2, u32 sel_bias) {
-    constexpr u32 LO = 0x00000000u;   // low bytes of fp16(0), fp16(1), fp16(2), fp16(3)
-    constexpr u32 HI = 0x42403C00u;   // high bytes
-    uint4 r;
-    r.x = __builtin_amdgcn_perm(HI, LO, mad_u24((c.x >> shift) & mask2, 0x101u, sel_bias));
-    r.y = __builtin_amdgcn_perm(HI, LO, mad_u24((c.y >> shift) & mask2, 0x101u, sel_bias));
-    r.z = __builtin_amdgcn_perm(HI, LO, mad_u24((c.z >> shift) & mask2, 0x101u, sel_bias));
-    r.w = __builtin_amdgcn_perm(HI, LO, mad_u24((c.w >> shift) & mask2, 0x101u, sel_bias));
-    return __builtin_bit_cast(v8h_w, r);
-}
-
-// Same for digits up to 255 (exact in fp16): convert each half to FP32 and pack
-// the pair (round toward zero, exact for these integers).
-__device__ __forceinline__ v8h_w digits_any(uint4 c, int shift, u32 mask2) {
-    typedef __fp16 v2h_w __attribute__((ext_vector_type(2)));
-    const u32 w[4] = {(c.x >> shift) & mask2, (c.y >> shift) & mask2, (c.z >> shift) & mask2,
-                      (c.w >> shift) & mask2};
-    u32 o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        o[i] = __builtin_bit_cast(u32, __builtin_amdgcn_cvt_pkrtz(float(w[i] & 0xFFFFu),
-                                                                  float(w[i] >> 16)));
-    return __builtin_bit_cast(v8h_w, make_uint4(o[0], o[1], o[2], o[3]));
-}
-
 // Digits of slice (shift, mask2), any width up to 8 bits, of eight 16-bit codes as eight
 // fp16: each field d is OR-ed into the mantissa of fp16 1024 (0x6400, mantissa step 1),
 // and one packed fp16 subtraction of 1024 leaves d exactly (the same fp16 values as a
@@ -223,7 +186,7 @@ template __global__ void k_split_wide<2>(const mf_config, const u32 *, const flo
 template __global__ void k_split_wide<4>(const mf_config, const u32 *, const float *, i64, i64,
                                          i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 
-template <int KS, bool NONLINEAR, bool SMALL, int FRMAX, bool VNOISE, bool SLICE>
+template <int KS, bool NONLINEAR, int FRMAX, bool VNOISE, bool SLICE>
 __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, KS)) void k_noisy_wide(
     const NoisyWidePlan plan,
                                                        const NoisyWideArgs args) {
@@ -291,7 +254,6 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
     settle_one(w_factor);
     __syncthreads();
 
-    const u32 sel_bias = 0x04000400u;
     u32 magic16 = 0x64006400u;   // fp16 1024 in both halves (digits_magic)
     settle_one(magic16);
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
@@ -500,23 +462,21 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
 }
 
-#define MF_NOISY_WIDE_INST(KS, NL, SMALL, FRMAX, VN, SL)                                       \
-    template __global__ void k_noisy_wide<KS, NL, SMALL, FRMAX, VN, SL>(const NoisyWidePlan,     \
-                                                                        const NoisyWideArgs);
-#define MF_NOISY_WIDE_INST4(KS, FRMAX)                         \
-    MF_NOISY_WIDE_INST(KS, false, true, FRMAX, false, false)   \
-    MF_NOISY_WIDE_INST(KS, true, true, FRMAX, false, false)    \
-    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, false, false)  \
-    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, false, false)   \
-    MF_NOISY_WIDE_INST(KS, false, false, FRMAX, true, false)   \
-    MF_NOISY_WIDE_INST(KS, true, false, FRMAX, true, false)
-// slice_pair read noise: no LDS staging (FRMAX 1), digits of any width, with and without
-// voltage variation.
-#define MF_NOISY_WIDE_SLICE(KS)                                \
-    MF_NOISY_WIDE_INST(KS, false, false, 1, false, true)       \
-    MF_NOISY_WIDE_INST(KS, true, false, 1, false, true)        \
-    MF_NOISY_WIDE_INST(KS, false, false, 1, true, true)        \
-    MF_NOISY_WIDE_INST(KS, true, false, 1, true, true)
+#define MF_NOISY_WIDE_INST(KS, NL, FRMAX, VN, SL)                                             \
+    template __global__ void k_noisy_wide<KS, NL, FRMAX, VN, SL>(const NoisyWidePlan,            \
+                                                                 const NoisyWideArgs);
+// LDS-staged terms: linear or S-curve ADC, digits or voltage operands.
+#define MF_NOISY_WIDE_INST4(KS, FRMAX)                  \
+    MF_NOISY_WIDE_INST(KS, false, FRMAX, false, false)  \
+    MF_NOISY_WIDE_INST(KS, true, FRMAX, false, false)   \
+    MF_NOISY_WIDE_INST(KS, false, FRMAX, true, false)   \
+    MF_NOISY_WIDE_INST(KS, true, FRMAX, true, false)
+// slice_pair read noise: no LDS staging (FRMAX 1), with and without voltage variation.
+#define MF_NOISY_WIDE_SLICE(KS)                         \
+    MF_NOISY_WIDE_INST(KS, false, 1, false, true)       \
+    MF_NOISY_WIDE_INST(KS, true, 1, false, true)        \
+    MF_NOISY_WIDE_INST(KS, false, 1, true, true)        \
+    MF_NOISY_WIDE_INST(KS, true, 1, true, true)
 MF_NOISY_WIDE_SLICE(2)
 MF_NOISY_WIDE_SLICE(4)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_TINY)
