@@ -50,6 +50,11 @@ def measured_traffic(leg):
     return MEASURED_TRAFFIC[leg]
 
 
+def progress(message):
+    """One line per finished leg on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -137,18 +142,16 @@ def secondary(device, only=None):
     out = {}
     int8 = dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
                 weight_slice=(1, 1, 2, 2, 2))
-    if want("config1_readme_mm"):
-        _config1(out, int8, device)
-    if want("config3_gru"):
-        _config3(out, int8, device)
-    if want("config4_resnet18"):
-        _config4(out, int8, device)
-    if want("config5_llm_q_proj"):
-        _config5(out, device)
-    if want("ideal_input_cases"):
-        _ideal_input_cases(out, device)
-    if want("read_modes_general"):
-        _read_modes(out, device)
+    legs = [("config1_readme_mm", lambda: _config1(out, int8, device)),
+            ("config3_gru", lambda: _config3(out, int8, device)),
+            ("config4_resnet18", lambda: _config4(out, int8, device)),
+            ("config5_llm_q_proj", lambda: _config5(out, device)),
+            ("ideal_input_cases", lambda: _ideal_input_cases(out, device)),
+            ("read_modes_general", lambda: _read_modes(out, device))]
+    for name, run in legs:
+        if want(name):
+            run()
+            progress(f"{name} done")
     return out
 
 
@@ -392,6 +395,7 @@ def main():
     ideal_cfg = memfast.Config(**BASE, nonidealities=memfast.Nonidealities(write_variation=0.0))
     sim = memfast.Simulator(ideal_cfg, device=device)
     ms_step, kernel_ms = time_steps(lambda: sim.mm(a, b), args.steps, args.warmup)
+    progress(f"ideal leg: {ms_step:.3f} ms per step")
 
     macs = SIZE**3
     pairs = len(ideal_cfg.input_layout) * len(ideal_cfg.weight_layout)
@@ -405,6 +409,7 @@ def main():
             write_variation=0.02, read_variation=0.01, adc_nonlinearity=0.1))
         noisy_sim = memfast.Simulator(noisy_cfg, device=device)
         noisy_ms, noisy_kernel_ms = time_steps(lambda: noisy_sim.mm(a, b), args.noisy_steps, 1)
+        progress(f"noisy leg: {noisy_ms:.3f} ms per step")
         noisy_achieved = 2 * slice_macs / (noisy_kernel_ms * 1e-3) / 1e12
         noisy = dict(
             ms_per_step=round(noisy_ms, 3), kernel_ms=round(noisy_kernel_ms, 3),
@@ -431,6 +436,7 @@ def main():
         start = time.perf_counter()
         oracle.mm(a_cpu[:rows], b_cpu[:, :cols], ideal_cfg)
         seconds = time.perf_counter() - start
+        progress(f"cpu baseline: {seconds:.1f} s")
         cpu = dict(
             value=rows * cols * SIZE / seconds / 1e9,
             unit="GMAC/s",
