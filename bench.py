@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # runs.  Summaries and commands: profiles/k_ideal_config2_pmc.md and
 # profiles/k_noisy_config2_noisy_pmc.md.  Only valid for the kernel sources they were
 # measured on (hash prefix below); otherwise the bench reports null.
-MEASURED_TRAFFIC = dict(kernels="4ae5c7b0020c4b5f", ideal=298468977, noisy=None)
+MEASURED_TRAFFIC = dict(kernels="ed526d122608fdb1", ideal=298307009, noisy=3077628803)
 
 
 def measured_traffic(leg):
@@ -432,7 +432,7 @@ def main():
 
         threads = os.cpu_count()
         torch.set_num_threads(threads)
-        rows, cols = 1024, 256
+        rows, cols = 4096, 256   # about 10 s on 16 threads
         start = time.perf_counter()
         oracle.mm(a_cpu[:rows], b_cpu[:, :cols], ideal_cfg)
         seconds = time.perf_counter() - start
@@ -443,7 +443,7 @@ def main():
             cores=torch.get_num_threads(),
             kind="port",
             sample=(f"oracle.mm(A[:{rows}], B[:, :{cols}]) at K={SIZE} (one two-tile chunk of "
-                    f"a quarter of the rows), ideal devices, {seconds:.2f} s on "
+                    f"every row), ideal devices, {seconds:.2f} s on "
                     f"{threads} threads of {cpu_model()}"),
         )
 
