@@ -87,6 +87,19 @@ __device__ __forceinline__ float scurve(float z, float alpha) {
     return fmaf(e, r, q0);
 }
 
+// Tile (x, y) of workgroup L (its linear id) in a grid of nx (fast) by ny tiles, arranged so
+// that the workgroups one XCD runs take one contiguous run of tiles in x-fastest order. The
+// dispatcher deals workgroup L to XCD L % 8 (MI355X: 8 XCDs, one L2 each), so with the plain
+// order neighbouring tiles, which share the operand indexed by y, land on eight different L2s;
+// here the tiles in flight on an XCD share it.  A bijection of [0, nx*ny): the last
+// (nx*ny) % 8 workgroups keep their own index.
+__device__ __forceinline__ void xcd_tile(u32 L, u32 nx, u32 ny, u32 &x, u32 &y) {
+    const u32 per = (nx * ny) / 8;
+    const u32 P = L < per * 8 ? (L % 8) * per + L / 8 : L;
+    x = P % nx;
+    y = P / nx;
+}
+
 // INT code of x in a group of scale s (memfast/quantization.py:41: round half to even,
 // clamp, two's complement masked to the code width), FP32 division as torch's.
 __device__ __forceinline__ u8 quantize_code(float x, float s, float lower, float upper,

@@ -252,10 +252,14 @@ __device__ __forceinline__ void noisy_read(const NoisyPlan &plan, const NoisyArg
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wc = wave & 1, wv = wave >> 1;
     const int lrow = lane & 31, lhalf = lane >> 5;
-    // Vector blocks are the fast grid axis, so the blocks that share a column
-    // block's conductance terms run together (on one XCD's L2).
-    const i64 c0 = i64(blockIdx.y) * BC;              // chunk-relative first column
-    const i64 v0 = i64(blockIdx.x) * BV;
+    // Vector blocks are the fast tile axis and each XCD takes a contiguous run of tiles, so
+    // the blocks in flight on an XCD share a column block's conductance terms in its L2
+    // (FETCH_SIZE at config 2: -34%, slice_pair -77%).  Voltage operands are as large as the
+    // terms and indexed by the vector block; there the plain order fetches 3.5 times less.
+    u32 vtile = blockIdx.x, ctile = blockIdx.y;
+    if (!VNOISE) xcd_tile(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x, gridDim.y, vtile, ctile);
+    const i64 c0 = i64(ctile) * BC;                   // chunk-relative first column
+    const i64 v0 = i64(vtile) * BV;
     const int G = int(args.G);
     const int A = plan.n_in, W = plan.n_w;
     const i64 kp = args.kp;

@@ -204,6 +204,11 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
     // Fragments per read staged in LDS (slice_pair reads take their planes from global
     // memory: none).
     const int FR = SLICE ? 0 : W * NOISY_TERMS * KS;
+    // Column blocks are the fast grid axis: the dispatcher deals neighbouring workgroups to
+    // different XCDs, so each XCD holds every eighth column block's terms for the vector
+    // blocks in flight, and the 16-bit codes of those vector blocks are shared by all of
+    // them.  (Giving each XCD a contiguous run with vector blocks fastest cut FETCH_SIZE by
+    // 19% at the q_proj shape but re-read the codes at 4096 vectors: 8% slower there.)
     const i64 cb = blockIdx.x;                    // chunk-relative 32-column block
     const i64 v0 = i64(blockIdx.y) * 128 + wave * 32;
     const i64 kp = args.kp;
