@@ -142,3 +142,51 @@ def test_order_probe_rejects_planted_orders():
     for block in blocks:
         eights = eights + block
     assert not torch.equal(eights, expected)
+
+
+@pytest.mark.parametrize("capability", ["avx2", "default"])
+def test_order_does_not_depend_on_torch_cpu_capability(capability):
+    """torch's CPU kernels forced to another vector ISA (ATEN_CPU_CAPABILITY, in a fresh
+    process) reduce in the same order: FP32 and FP64 chunks with cascade and interleaved
+    columns equal the kernels' order bit for bit."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    script = """
+import sys
+import torch
+from memfast_amd import host_order
+assert torch.backends.cpu.get_cpu_capability() == sys.argv[1].upper(), torch.backends.cpu.get_cpu_capability()
+assert host_order.sum_order_matches()
+for dtype, view in ((torch.float32, torch.int32), (torch.float64, torch.int64)):
+    for reads in (3, 17, 64, 300):
+        for columns in (4, 7, 24, 40, 72, 100):
+            values = host_order.probe_values(reads=reads, columns=columns, dtype=dtype)
+            got = host_order.kernel_order_sum(values[0])
+            assert torch.equal(values.sum(1)[0].view(view), got.view(view)), (dtype, reads, columns)
+print("ok", torch.backends.cpu.get_cpu_capability())
+"""
+    root = Path(__file__).resolve().parents[1]
+    env = dict(os.environ, ATEN_CPU_CAPABILITY=capability, PYTHONPATH=str(root))
+    result = subprocess.run([sys.executable, "-c", script, capability], env=env,
+                            capture_output=True, text=True, timeout=600)
+    assert result.returncode == 0, result.stderr[-2000:]
+    assert result.stdout.strip() == f"ok {capability.upper()}"
+
+
+def test_product_model_matches_this_restatement_and_rejects_other_spans():
+    """host_order.kernel_order_sum (the product's guard) equals this file's incremental
+    restatement on FP32 chunks with interleaved columns; and an FP64 chunk classified with
+    the FP32 span (32 instead of 16) differs from torch's sum."""
+    from memfast_amd import host_order
+
+    values = host_order.probe_values(reads=100, columns=72)[0]
+    np.testing.assert_array_equal(host_order.kernel_order_sum(values).numpy().view(np.int32),
+                                  kernel_sum(values.numpy()).view(np.int32))
+    wide = host_order.probe_values(reads=100, columns=24, dtype=torch.float64)[0]
+    expected = wide[None].sum(1)[0]
+    assert torch.equal(host_order.kernel_order_sum(wide), expected)
+    # With a 32-column span all 24 columns would be interleaved; the first 16 are not.
+    assert not torch.equal(host_order.interleaved_sum(wide)[:16], expected[:16])
