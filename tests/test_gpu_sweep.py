@@ -60,6 +60,10 @@ def _config(rng, noisy):
                 effects.update(read_variation=0.02, read_mode="slice_pair")
             elif kind == 3:
                 effects.update(read_variation=0.02, read_mode="output")
+                # Half of them with voltage variation too, chosen from values already drawn
+                # so that every other draw stays as it was.
+                if (rows // 32 + cols // 16 + read_rows // 16) % 2:
+                    effects.update(voltage_variation=0.02)
             elif kind == 4:
                 effects.update(voltage_variation=0.02)
             elif kind == 5:
