@@ -761,35 +761,24 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks,
         args.volt = volt;
         const dim3 grid{unsigned(CB), unsigned((n + 127) / 128), 1u};
         const bool nl = cfg->has_nonlinear != 0;
-        if (plan.planes > 1) {
-            // slice_pair read noise: every (weight, input) slice pair has its own plane of
-            // terms, read from global memory rather than staged in LDS.
-#define MF_WIDE_SLICE(KS)                                                                          \
-    if (volt && nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, 1, true, true>), grid,        \
-                                       dim3(256), 0, s, plan, args);                                \
-    else if (volt) hipLaunchKernelGGL((k_noisy_wide<KS, false, 1, true, true>), grid,        \
-                                      dim3(256), 0, s, plan, args);                                 \
-    else if (nl) hipLaunchKernelGGL((k_noisy_wide<KS, true, 1, false, true>), grid,          \
-                                    dim3(256), 0, s, plan, args);                                   \
-    else hipLaunchKernelGGL((k_noisy_wide<KS, false, 1, false, true>), grid, dim3(256), 0,   \
-                            s, plan, args);
-            if (ks == 4) { MF_WIDE_SLICE(4) } else { MF_WIDE_SLICE(2) }
-#undef MF_WIDE_SLICE
-            continue;
-        }
-#define MF_WIDE_LAUNCH(KS, FR)                                                                   \
+        // slice_pair read noise: a plane of terms per (weight, input) slice pair, staged in
+        // LDS one input slice at a time (the kernel's SLICE form).
+        const bool sl = plan.planes > 1;
+#define MF_WIDE_LAUNCH2(KS, FR, SL)                                                              \
     if (volt && nl)                                                                              \
-        hipLaunchKernelGGL((k_noisy_wide<KS, true, FR, true, false>), grid, dim3(256), 0, s, plan,  \
+        hipLaunchKernelGGL((k_noisy_wide<KS, true, FR, true, SL>), grid, dim3(256), 0, s, plan,     \
                            args);                                                                \
     else if (volt)                                                                               \
-        hipLaunchKernelGGL((k_noisy_wide<KS, false, FR, true, false>), grid, dim3(256), 0, s, plan, \
+        hipLaunchKernelGGL((k_noisy_wide<KS, false, FR, true, SL>), grid, dim3(256), 0, s, plan,    \
                            args);                                                                \
     else if (nl)                                                                                 \
-        hipLaunchKernelGGL((k_noisy_wide<KS, true, FR, false, false>), grid, dim3(256), 0, s, plan, \
+        hipLaunchKernelGGL((k_noisy_wide<KS, true, FR, false, SL>), grid, dim3(256), 0, s, plan,    \
                            args);                                                                \
     else                                                                                         \
-        hipLaunchKernelGGL((k_noisy_wide<KS, false, FR, false, false>), grid, dim3(256), 0, s,      \
-                           plan, args);
+        hipLaunchKernelGGL((k_noisy_wide<KS, false, FR, false, SL>), grid, dim3(256), 0, s, plan,   \
+                           args);
+#define MF_WIDE_LAUNCH(KS, FR)                                                                   \
+    if (sl) { MF_WIDE_LAUNCH2(KS, FR, true) } else { MF_WIDE_LAUNCH2(KS, FR, false) }
         if (ks == 4) {
             if (tier == 2) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_LARGE) }
             else if (tier == 1) { MF_WIDE_LAUNCH(4, WIDE_FRAGS_SMALL) }
@@ -800,6 +789,7 @@ int launch_noisy_wide(const mf_config *cfg, const NoisyWidePlan &plan, int ks,
             else { MF_WIDE_LAUNCH(2, WIDE_FRAGS_TINY) }
         }
 #undef MF_WIDE_LAUNCH
+#undef MF_WIDE_LAUNCH2
     }
     return check_launch("wide noisy MFMA read");
 }
@@ -2172,24 +2162,19 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
         int tier = frags > WIDE_FRAGS_SMALL ? 2 : frags > WIDE_FRAGS_TINY ? 1 : 0;
         if (variant_tier(variant) > 0) tier = variant_tier(variant) - 1;
         const bool vn = cfg->has_vnoise != 0;
-        const bool sl = wide_term_planes(cfg) > 1;   // slice_pair: planes from global memory
-#define MF_WIDE_FN(KS, FR)                                                                       \
-    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, FR, true, false>)          \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, FR, true, false>))        \
-        : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, FR, false, false>)         \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, FR, false, false>)))
-#define MF_WIDE_SLICE_FN(KS)                                                                     \
-    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, 1, true, true>)            \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, 1, true, true>))          \
-        : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, 1, false, true>)           \
-              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, 1, false, true>)))
-        if (sl) fn = ks4 ? MF_WIDE_SLICE_FN(4) : MF_WIDE_SLICE_FN(2);
-        else if (ks4) fn = tier == 2 ? MF_WIDE_FN(4, WIDE_FRAGS_LARGE)
-                           : tier == 1 ? MF_WIDE_FN(4, WIDE_FRAGS_SMALL) : MF_WIDE_FN(4, WIDE_FRAGS_TINY);
+        const bool sl = wide_term_planes(cfg) > 1;   // slice_pair: an LDS unit per input slice
+#define MF_WIDE_FN2(KS, FR, SL)                                                                  \
+    (vn ? (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, FR, true, SL>)             \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, FR, true, SL>))           \
+        : (nl ? reinterpret_cast<const void *>(&k_noisy_wide<KS, true, FR, false, SL>)            \
+              : reinterpret_cast<const void *>(&k_noisy_wide<KS, false, FR, false, SL>)))
+#define MF_WIDE_FN(KS, FR) (sl ? MF_WIDE_FN2(KS, FR, true) : MF_WIDE_FN2(KS, FR, false))
+        if (ks4) fn = tier == 2 ? MF_WIDE_FN(4, WIDE_FRAGS_LARGE)
+                      : tier == 1 ? MF_WIDE_FN(4, WIDE_FRAGS_SMALL) : MF_WIDE_FN(4, WIDE_FRAGS_TINY);
         else fn = tier == 2 ? MF_WIDE_FN(2, WIDE_FRAGS_LARGE)
                   : tier == 1 ? MF_WIDE_FN(2, WIDE_FRAGS_SMALL) : MF_WIDE_FN(2, WIDE_FRAGS_TINY);
-#undef MF_WIDE_SLICE_FN
 #undef MF_WIDE_FN
+#undef MF_WIDE_FN2
     } else if (kernel_id == 0) {
 #define MF_GENERAL_FN(WIDE)                                                                      \
     (cfg->precise                                                                                \

@@ -255,10 +255,11 @@ constexpr int WIDE_FRAGS_TINY = 24;
 constexpr int WIDE_FRAGS_SMALL = 36;
 constexpr int WIDE_FRAGS_LARGE = 72;
 // Blocks per CU the wide read is compiled for: three (at most 168 VGPRs) where
-// the LDS allows it and the linear converter leaves the registers to spare (not with
-// voltage operands on 64-row reads).
-constexpr int wide_blocks_per_cu(int frmax, bool nonlinear, bool vnoise, int ks) {
-    return frmax <= WIDE_FRAGS_TINY && !nonlinear && !(vnoise && ks == 4) ? 3 : 2;
+// the LDS allows it and the linear converter leaves the registers to spare.  (Voltage
+// operands on 64-row reads spill two VGPRs at three blocks; two blocks without the spill
+// ran 4.6% slower at 4096^3.)
+constexpr int wide_blocks_per_cu(int frmax, bool nonlinear) {
+    return frmax <= WIDE_FRAGS_TINY && !nonlinear ? 3 : 2;
 }
 // VNOISE: voltage variation (real input operands from args.volt, one input slice a step).
 // SLICE: slice_pair read noise (a plane of terms per (weight slice, input slice), read from

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256) void k_split_wide(const mf_config cfg, const u
         const int lane = int(rest & 63); rest >>= 6;
         const int ks = int(rest % KS); rest /= KS;
         const int vw = int(rest % (W * plan.planes)); rest /= W * plan.planes;
-        const int w = vw / plan.planes, plane = vw - w * plan.planes;
+        const int plane = vw / W, w = vw - plane * W;   // planes outermost: [plane][w]
         const i64 g = rest % G;
         const i64 cb = rest / G;
         const int lr = lane & 31, h = lane >> 5;
@@ -187,7 +187,7 @@ template __global__ void k_split_wide<4>(const mf_config, const u32 *, const flo
                                          i64, u32, u64, i64, i64, const NoisyWidePlan, uint4 *);
 
 template <int KS, bool NONLINEAR, int FRMAX, bool VNOISE, bool SLICE>
-__global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, KS)) void k_noisy_wide(
+__global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR)) void k_noisy_wide(
     const NoisyWidePlan plan,
                                                        const NoisyWideArgs args) {
     // Two LDS objects (read g in one, read g+1 arriving in the other) so that the
@@ -201,9 +201,10 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
     const int lrow = lane & 31, lhalf = lane >> 5;
     const int A = plan.n_in, W = plan.n_w;
     const int G = int(args.G);
-    // Fragments per read staged in LDS (slice_pair reads take their planes from global
-    // memory: none).
-    const int FR = SLICE ? 0 : W * NOISY_TERMS * KS;
+    // Fragments per LDS unit: one read's terms [w][term][ks], or with slice_pair read noise
+    // one (read, input slice) plane set: a read is A units, each staged in turn.
+    const int FR = W * NOISY_TERMS * KS;
+    const int UNITS = SLICE ? A : 1;   // LDS units per read
     // Column blocks are the fast grid axis: the dispatcher deals neighbouring workgroups to
     // different XCDs, so each XCD holds every eighth column block's terms for the vector
     // blocks in flight, and the 16-bit codes of those vector blocks are shared by all of
@@ -213,10 +214,10 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
     const i64 v0 = i64(blockIdx.y) * 128 + wave * 32;
     const i64 kp = args.kp;
 
-    // Conductance terms of this column block: [g][w][term][ks][lane].
-    const uint4 *frag = args.gs + cb * i64(G) * FR * 64 + lane;
-    auto fetch = [&](int g, uint4 *dst) {
-        const uint4 *src = frag + i64(g) * FR * 64;
+    // Conductance terms of this column block: [g][unit][w][term][ks][lane].
+    const uint4 *frag = args.gs + cb * i64(G) * UNITS * FR * 64 + lane;
+    auto fetch = [&](int u, uint4 *dst) {   // unit u = g * UNITS + a
+        const uint4 *src = frag + i64(u) * FR * 64;
         const u32 base = u32(reinterpret_cast<uintptr_t>((lds_void *)dst));
         for (int f = wave; f < FR; f += 4)
             lds_dma_16(src + f * 64, __builtin_amdgcn_readfirstlane(base + u32(f) * 1024u));
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
     settle_one(magic16);
     const float MAGIC = 12582912.0f;   // 1.5 * 2^23
     auto step = [&](int g, const uint4 *sCur, uint4 *sNext) {
-        if (g + 1 < G) fetch(g + 1, sNext);
+        if (!SLICE && g + 1 < G) fetch(g + 1, sNext);
         u32 T[16];   // modulo 2^32, offset by 0x400000 * sum(fa*fw) (plan.bias undoes it)
 #pragma unroll
         for (int r = 0; r < 16; ++r) T[r] = 0u;
@@ -306,12 +307,15 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
             // input value carries its own factor, x = digit * (1 + vv*z), held as fp16 hi + lo
             // operands, and a pair takes 3*KS MFMAs (hi*hi + lo*hi + hi*lo, the narrow voltage
             // read's order).  slice_pair read noise (memfast/reference.py:86-90): each (weight
-            // slice, input slice) pair reads its own plane of terms, from global memory.
+            // slice, input slice) pair reads its own plane of terms; input slice a's planes are
+            // LDS unit g*A + a, in the buffer of its parity, the next unit's DMA in flight.
             const i64 vunits = kp / 8;
             const uint4 *vbase = args.volt + (v0 / 32) * vunits * 32 + lane;
             const i64 vplane = ((args.n + 31) / 32) * vunits * 32;
-            const uint4 *planes = args.gs + (cb * G + g) * i64(W * A) * NOISY_TERMS * KS * 64 + lane;
             for (int a = 0; a < A; ++a) {
+                const int u = g * A + a;
+                if (SLICE && u + 1 < G * A) fetch(u + 1, ((u + 1) & 1) ? sF1 : sF0);
+                const uint4 *fu = (SLICE ? ((u & 1) ? sF1 : sF0) : sCur) + lane;
                 v8h_w hi[KS], lo[KS];
                 if (VNOISE) {
 #pragma unroll
@@ -327,16 +331,12 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
                 }
                 for (int w = 0; w < W; ++w) {
                     v8h_w F[NOISY_TERMS][KS];
-                    if (SLICE) {
-                        const uint4 *plane = planes + i64(w * A + a) * NOISY_TERMS * KS * 64;
 #pragma unroll
-                        for (int term = 0; term < NOISY_TERMS; ++term)
+                    for (int term = 0; term < NOISY_TERMS; ++term)
 #pragma unroll
-                            for (int ks = 0; ks < KS; ++ks)
-                                F[term][ks] = __builtin_bit_cast(v8h_w, plane[(term * KS + ks) * 64]);
-                    } else {
-                        terms(F, w);
-                    }
+                        for (int ks = 0; ks < KS; ++ks)
+                            F[term][ks] = __builtin_bit_cast(
+                                v8h_w, fu[((w * NOISY_TERMS + term) * KS + ks) * 64]);
                     v16f_w I = {};
                     if (VNOISE) {
 #pragma unroll
@@ -358,6 +358,12 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
                                                                            0, 0, 0);
                     }
                     convert(I, w, a);
+                }
+                // slice_pair: the next unit is in LDS and every wave is done with this one
+                // (the read's last unit waits at the end of the step).
+                if (SLICE && a + 1 < A) {
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __syncthreads();
                 }
             }
         }
@@ -470,20 +476,17 @@ __global__ __launch_bounds__(256, wide_blocks_per_cu(FRMAX, NONLINEAR, VNOISE, K
 #define MF_NOISY_WIDE_INST(KS, NL, FRMAX, VN, SL)                                             \
     template __global__ void k_noisy_wide<KS, NL, FRMAX, VN, SL>(const NoisyWidePlan,            \
                                                                  const NoisyWideArgs);
-// LDS-staged terms: linear or S-curve ADC, digits or voltage operands.
+// Linear or S-curve ADC; digits or voltage operands; shared (one LDS unit per read) or
+// slice_pair read noise (one LDS unit per read and input slice).
 #define MF_NOISY_WIDE_INST4(KS, FRMAX)                  \
     MF_NOISY_WIDE_INST(KS, false, FRMAX, false, false)  \
     MF_NOISY_WIDE_INST(KS, true, FRMAX, false, false)   \
     MF_NOISY_WIDE_INST(KS, false, FRMAX, true, false)   \
-    MF_NOISY_WIDE_INST(KS, true, FRMAX, true, false)
-// slice_pair read noise: no LDS staging (FRMAX 1), with and without voltage variation.
-#define MF_NOISY_WIDE_SLICE(KS)                         \
-    MF_NOISY_WIDE_INST(KS, false, 1, false, true)       \
-    MF_NOISY_WIDE_INST(KS, true, 1, false, true)        \
-    MF_NOISY_WIDE_INST(KS, false, 1, true, true)        \
-    MF_NOISY_WIDE_INST(KS, true, 1, true, true)
-MF_NOISY_WIDE_SLICE(2)
-MF_NOISY_WIDE_SLICE(4)
+    MF_NOISY_WIDE_INST(KS, true, FRMAX, true, false)    \
+    MF_NOISY_WIDE_INST(KS, false, FRMAX, false, true)   \
+    MF_NOISY_WIDE_INST(KS, true, FRMAX, false, true)    \
+    MF_NOISY_WIDE_INST(KS, false, FRMAX, true, true)    \
+    MF_NOISY_WIDE_INST(KS, true, FRMAX, true, true)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_TINY)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_SMALL)
 MF_NOISY_WIDE_INST4(2, WIDE_FRAGS_LARGE)
