@@ -262,8 +262,8 @@ constexpr int wide_blocks_per_cu(int frmax, bool nonlinear) {
     return frmax <= WIDE_FRAGS_TINY && !nonlinear ? 3 : 2;
 }
 // VNOISE: voltage variation (real input operands from args.volt, one input slice a step).
-// SLICE: slice_pair read noise (a plane of terms per (weight slice, input slice), read from
-// global memory: FRMAX 1, no LDS staging).
+// SLICE: slice_pair read noise (a plane of terms per (weight slice, input slice), staged in
+// LDS one (read, input slice) unit at a time).
 template <int KS, bool NONLINEAR, int FRMAX, bool VNOISE, bool SLICE>
 __global__ void k_noisy_wide(const NoisyWidePlan plan, const NoisyWideArgs args);
 

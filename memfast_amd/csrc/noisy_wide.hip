@@ -25,10 +25,11 @@
 //
 // Layout: k_split_wide writes the conductance terms of each 32-column block
 // and read as one contiguous run [w][term][ks] of 1 KiB fragments (MFMA lane
-// order).  Block = 4 waves on the same 32 columns and 128 vectors (32 per
-// wave); per read the block copies the run into LDS with global_load_lds
-// (double-buffered in two LDS objects, one barrier per read) and every wave
-// reads it from there.  FRMAX bounds the fragments per read (W * 2 * KS); the
+// order); with slice_pair read noise one such run per input slice.  Block = 4
+// waves on the same 32 columns and 128 vectors (32 per wave); per read (or per
+// read and input slice) the block copies the run into LDS with global_load_lds
+// (double-buffered in two LDS objects, one barrier per run) and every wave
+// reads it from there.  FRMAX bounds the fragments per run (W * 2 * KS); the
 // smallest capacity is compiled for three blocks per CU.
 // Input codes are repacked to 16 bits (k_codes16) so a lane's 8 rows of a
 // 16-row step are one 16-byte load.  Bound: VALU (digit expansion + ADC per
