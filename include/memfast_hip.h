@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 8
+#define MF_ABI_VERSION 9
 #define MF_MAX_SLICES 32
 
 enum {
@@ -47,8 +47,13 @@ enum { MF_READ_SHARED = 0, MF_READ_SLICE_PAIR = 1, MF_READ_OUTPUT = 2 };
 enum {
     MF_STATUS_INPUT = 1,   /* non-finite activation value */
     MF_STATUS_WEIGHT = 2,  /* non-finite weight value */
-    MF_STATUS_OUTPUT = 4   /* non-finite FP32 output of mf_mm */
+    MF_STATUS_OUTPUT = 4,  /* non-finite FP32 output of mf_mm */
+    MF_STATUS_RANGE = 16   /* mf_mm_from_float: a group scale above the bound that keeps
+                            * every FP32 output finite; MF_STATUS_OUTPUT is then known
+                            * only once the read has finished */
 };
+/* Set in a mailbox word (mf_mm_from_float) beside the status bits it carries. */
+#define MF_STATUS_PUBLISHED 0x80000000u
 
 /* Physical configuration (memfast/config.py:21-224), derived on the host.
  * f_* members are the FP32 values the reference's torch CPU ops use (Python
@@ -225,12 +230,30 @@ int mf_mm(const mf_config *cfg, const uint8_t *q, const float *xscale, int64_t n
  * devices with 32 rows per read, groups of one read on both sides ((1, 32) and (32, 1)),
  * R % 128 == 0, C % 64 == 0, k == m*R, o == p*C, 16-byte aligned x, q, packed,
  * packed_t and out, and a workspace of mf_mm_workspace() bytes; otherwise it launches
- * nothing and returns MF_E_UNSUPPORTED (the caller takes the three calls). */
+ * nothing and returns MF_E_UNSUPPORTED (the caller takes the three calls).
+ * The quantizers set MF_STATUS_RANGE when a group scale exceeds
+ * sqrt(FLT_MAX / (2 * G * Tmax)) (G reads, Tmax the largest |count total| of one read):
+ * below it no product, restore or sum of the read can overflow, so MF_STATUS_OUTPUT
+ * cannot be set.  mailbox (may be NULL): a host word of pinned memory (hipHostMalloc),
+ * cleared by the call before it launches, that the read's first workgroup sets when it
+ * ends to MF_STATUS_PUBLISHED | the status bits (the quantizers' are final by then, as
+ * they finished before the read began); mf_status_wait reads it.  A caller that finds no
+ * bit but MF_STATUS_PUBLISHED there has every status bit of the call without waiting for
+ * the rest of the read, which then overlaps the caller's next work on the stream. */
 int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k, int64_t ldx,
                      const float *b, int64_t o, int64_t ldb, int64_t x_gr, int64_t x_gc,
                      int64_t w_gr, int64_t w_gc, uint8_t *q, float *xscale, uint8_t *packed,
                      uint8_t *packed_t, float *wscale, float *out, int64_t ldo, void *workspace,
-                     int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream);
+                     int64_t workspace_bytes, int32_t variant, uint32_t *status,
+                     uint32_t *mailbox, void *stream);
+
+/* No counterpart in the reference (which checks its operands with host scans that
+ * synchronize).  Waits until the mailbox word of mf_mm_from_float holds
+ * MF_STATUS_PUBLISHED or timeout_us microseconds have passed (spinning, then sleeping
+ * in short steps); *flags receives the word without that bit and *published whether
+ * it was set.  A caller that times out reads the device status word instead. */
+int mf_status_wait(const uint32_t *mailbox, int64_t timeout_us, uint32_t *flags,
+                   int32_t *published);
 
 /* No counterpart in the reference.  mf_mm for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid

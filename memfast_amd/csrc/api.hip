@@ -5,11 +5,14 @@
 // Nothing here allocates device memory; the caller owns every buffer.
 #include <algorithm>
 #include <atomic>
+#include <cfloat>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -1354,11 +1357,28 @@ int mf_mm_workspace(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32
 }
 
 // The ideal read proper once both sides' proven-slot masks are in xbits / wbits.
+// The largest group scale for which no FP32 step of the ideal read's restore can overflow:
+// each read's total obeys |T| <= Tmax = sum over slice pairs of |fa*fw| * P * mask_a * mask_w,
+// so with every scale <= s, |(T*xs)*ws| <= Tmax*s^2*(1+2^-24)^2 and a sum of G such terms in
+// any order stays below G*Tmax*s^2*1.07 (G < 2^20).  s = sqrt(FLT_MAX / (2*G*Tmax)), rounded
+// down to FP32.
+static float finite_output_scale_bound(const mf_config *cfg, i64 G) {
+    double tmax = 0.0;
+    for (int a = 0; a < cfg->n_in; ++a)
+        for (int w = 0; w < cfg->n_w; ++w)
+            tmax += std::fabs(double(cfg->in_factor[a]) * double(cfg->w_factor[w])) *
+                    double(cfg->read_rows) * double(cfg->in_mask[a]) * double(cfg->w_mask[w]);
+    const double bound = std::sqrt(double(FLT_MAX) / (2.0 * double(G) * std::max(tmax, 1.0)));
+    float f = float(bound);
+    if (double(f) > bound) f = std::nextafter(f, 0.0f);
+    return f;
+}
+
 static int launch_ideal(const mf_config *cfg, const IdealPlan &plan, int ks, const u8 *q,
                         const float *xscale, const u8 *packed_t, const float *wscale,
                         const uint64_t *xbits, const uint64_t *wbits, i64 n, i64 m, i64 p,
                         i64 out_cols, i64 g_run, float *out, i64 ldo, int32_t variant,
-                        u32 *status, hipStream_t s) {
+                        u32 *status, hipStream_t s, u32 *mailbox = nullptr) {
     const i64 kp = m * cfg->rows, ncols = p * cfg->cols, G = m * cfg->reads;
     IdealArgs args{};
     args.q = q;
@@ -1369,6 +1389,7 @@ static int launch_ideal(const mf_config *cfg, const IdealPlan &plan, int ks, con
     args.wbits = wbits;
     args.out = out;
     args.status = status;
+    args.mailbox = mailbox;
     args.n = n;
     args.kp = kp;
     args.G = G;
@@ -1516,7 +1537,8 @@ int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k,
                      const float *b, int64_t o, int64_t ldb, int64_t x_gr, int64_t x_gc,
                      int64_t w_gr, int64_t w_gc, uint8_t *q, float *xscale, uint8_t *packed,
                      uint8_t *packed_t, float *wscale, float *out, int64_t ldo, void *workspace,
-                     int64_t workspace_bytes, int32_t variant, uint32_t *status, void *stream) {
+                     int64_t workspace_bytes, int32_t variant, uint32_t *status,
+                     uint32_t *mailbox, void *stream) {
     const int valid = check_narrow(cfg);
     if (valid) return valid;
     if (!x || !b || !q || !xscale || !packed || !packed_t || !wscale || !out || n < 1 || k < 1 ||
@@ -1546,9 +1568,18 @@ int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k,
     if (!shapes || !aligned || !room || !ideal_extent_ok(cfg, n, m, p) ||
         wblocks + xblocks > 0x7FFFFFFF || !build_ideal_plan(cfg, m, p, &plan, &xtests, &wtests, &ks, &why))
         return fail(MF_E_UNSUPPORTED, "mm_from_float not applicable");
+    u32 *device_mailbox = nullptr;
+    if (mailbox) {
+        __atomic_store_n(mailbox, 0u, __ATOMIC_RELAXED);
+        const hipError_t e =
+            hipHostGetDevicePointer(reinterpret_cast<void **>(&device_mailbox), mailbox, 0);
+        if (e != hipSuccess)
+            return fail(MF_E_INVALID, "mailbox is not pinned host memory: %s", hipGetErrorString(e));
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint64_t *xbits = static_cast<uint64_t *>(workspace);
     uint64_t *wbits = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) + xbytes);
+    const float bound = finite_output_scale_bound(cfg, G);
     ReadGroupArgs a{};
     a.b = b;
     a.k = k;
@@ -1575,14 +1606,46 @@ int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k,
     a.q = q;
     a.xscale = xscale;
     a.G = G;
-    a.wdigits = TileDigits{layout_of(cfg->w_shift, cfg->w_mask, cfg->n_w), wtests, wbits, G};
-    a.xdigits = TileDigits{layout_of(cfg->in_shift, cfg->in_mask, cfg->n_in), xtests, xbits, G};
+    a.wdigits = TileDigits{layout_of(cfg->w_shift, cfg->w_mask, cfg->n_w), wtests, wbits, G, bound};
+    a.xdigits = TileDigits{layout_of(cfg->in_shift, cfg->in_mask, cfg->n_in), xtests, xbits, G,
+                           bound};
     a.status = status;
     hipLaunchKernelGGL(k_read_groups, dim3(unsigned(wblocks + xblocks)), dim3(256), 0, s, a);
     const int launched = check_launch("read-group quantization");
     if (launched) return launched;
     return launch_ideal(cfg, plan, ks, q, xscale, packed_t, wscale, xbits, wbits, n, m, p, o, G,
-                        out, ldo, variant, status, s);
+                        out, ldo, variant, status, s, device_mailbox);
+}
+
+int mf_status_wait(const uint32_t *mailbox, int64_t timeout_us, uint32_t *flags,
+                   int32_t *published) {
+    if (!mailbox || !flags || !published || timeout_us < 0)
+        return fail(MF_E_INVALID, "invalid status_wait arguments");
+    using clock = std::chrono::steady_clock;
+    const auto start = clock::now();
+    for (int64_t i = 0;; ++i) {
+        const uint32_t word = __atomic_load_n(mailbox, __ATOMIC_ACQUIRE);
+        if (word & MF_STATUS_PUBLISHED) {
+            *flags = word & ~MF_STATUS_PUBLISHED;
+            *published = 1;
+            return MF_OK;
+        }
+        if (i % 64 == 0) {
+            const int64_t waited =
+                std::chrono::duration_cast<std::chrono::microseconds>(clock::now() - start).count();
+            if (waited >= timeout_us) {
+                *flags = 0;
+                *published = 0;
+                return MF_OK;
+            }
+            // Spin for the first 2 ms (a read's quantizers take tens of microseconds), then
+            // poll in short sleeps behind longer queued work.
+            if (waited >= 2000) std::this_thread::sleep_for(std::chrono::microseconds(20));
+        }
+#if defined(__x86_64__)
+        __builtin_ia32_pause();
+#endif
+    }
 }
 
 }  // extern "C"

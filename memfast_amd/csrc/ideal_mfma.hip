@@ -418,6 +418,10 @@ __global__ __launch_bounds__(256, TN == 1 && KS == 1 ? 5 : 2) void k_ideal(const
         }
     }
     if (!finite && args.status) atomicOr(args.status, u32(MF_STATUS_OUTPUT));
+    // The quantizers finished before this read began, so their status bits are final: the
+    // first workgroup hands them to the caller, which then need not wait for the whole read.
+    if (args.mailbox && blockIdx.x == 0 && blockIdx.y == 0 && tid == 0)
+        publish_status(args.status, args.mailbox);
 }
 
 template __global__ void k_digit_bits<32>(const DigitJob, const DigitJob, i64, i64, i64);

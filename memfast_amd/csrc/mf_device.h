@@ -100,6 +100,18 @@ __device__ __forceinline__ void xcd_tile(u32 L, u32 nx, u32 ny, u32 &x, u32 &y) 
     y = P / nx;
 }
 
+// Copy a status word to a caller's pinned host word, marked MF_STATUS_PUBLISHED.  Called by
+// one lane of a kernel that started after the kernels setting those bits had finished: the
+// device-scope load sees their atomics, and the system-scope store writes through to host
+// memory.  Call it after the kernel's last load of read-only inputs: the compiler counts this
+// store as a possible write to them, and loads after it become vector loads.
+__device__ __forceinline__ void publish_status(u32 *status, u32 *mailbox) {
+    const u32 flags = status ? __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : 0u;
+    __hip_atomic_store(mailbox, flags | MF_STATUS_PUBLISHED, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // INT code of x in a group of scale s (memfast/quantization.py:41: round half to even,
 // clamp, two's complement masked to the code width), FP32 division as torch's.
 __device__ __forceinline__ u8 quantize_code(float x, float s, float lower, float upper,

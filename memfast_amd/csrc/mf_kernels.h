@@ -71,6 +71,8 @@ struct IdealArgs {
     const uint64_t *wbits;  // [ceil(ncols/32), G] weight-side proven slots per 32 columns
     float *out;             // [n, ldo]
     u32 *status;            // optional: MF_STATUS_OUTPUT for a non-finite output
+    u32 *mailbox;           // optional: pinned host word; the first workgroup copies the
+                            // status bits there (with MF_STATUS_PUBLISHED) when it ends
     i64 n, kp, G, ldo, ldws, ncols;
     i64 G_run;              // reads executed: [0, G_run) (the rest is zero padding)
     int Gr, R, P;
@@ -108,6 +110,7 @@ struct TileDigits {
     SlotTests tests;
     uint64_t *bits;    // [blocks, G]
     i64 G;
+    float scale_bound; // group scales above it set MF_STATUS_RANGE
 };
 
 // k_read_groups: B [k, o] (ld ldb) programmed in 32-row column groups into packed,

@@ -358,7 +358,7 @@ __device__ __forceinline__ void col_tile(const float *b, i64 k, i64 o, i64 ld, i
         const i64 row = r0 + i;
         v[i] = (live && row < k) ? b[row * ld + col] : 0.0f;
     }
-    bool finite = true;
+    bool finite = true, large = false;
     if (GIVEN) {
         i64 g = r0 / gr, boundary = (g + 1) * gr;
         float sc = (live && r0 < k) ? scale[g * o + col] : 1.0f;
@@ -384,6 +384,7 @@ __device__ __forceinline__ void col_tile(const float *b, i64 k, i64 o, i64 ld, i
         }
         const float sc = group_scale(peak, upper);
         if (live && r0 < k) scale[(r0 / GR) * o + col] = sc;
+        large = digits && live && r0 < k && sc > digits->scale_bound;
         const GroupCodes codes(sc);
 #pragma unroll
         for (int i = 0; i < GR; ++i) {
@@ -443,6 +444,7 @@ __device__ __forceinline__ void col_tile(const float *b, i64 k, i64 o, i64 ld, i
                 proven_slots(digits->tests, col_max[wave][lane >> 5]);
     }
     if (!finite && status) atomicOr(status, flag);
+    if (large && status) atomicOr(status, u32(MF_STATUS_RANGE));
 }
 
 template <int GR, bool GIVEN>
@@ -531,6 +533,7 @@ __device__ __forceinline__ void input_read_block(const ReadGroupArgs &a, i64 blo
         a.xdigits.bits[vb * G + g0 + t] = proven_slots(a.xdigits.tests, block_max[t]);
     }
     if (!finite && a.status) atomicOr(a.status, u32(MF_STATUS_INPUT));
+    if (live && s > a.xdigits.scale_bound && a.status) atomicOr(a.status, u32(MF_STATUS_RANGE));
 }
 
 // Both operands of the ideal read in read-sized groups, with its digit-sum pre-pass, in

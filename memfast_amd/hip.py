@@ -22,7 +22,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libmemfast_hip.so"
 MAX_SLICES = 32
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 OK, E_INVALID, E_UNSUPPORTED, E_RESOURCE, E_HIP = 0, 1, 2, 3, 4
 
@@ -148,7 +148,8 @@ SIGNATURES = {
     "mf_mm": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
                ct.c_uint64, _P, _I64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_from_float": ([_CFG, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
-                          _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P], ct.c_int),
+                          _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _P], ct.c_int),
+    "mf_status_wait": ([_P, _I64, ct.POINTER(ct.c_uint32), ct.POINTER(_I32)], ct.c_int),
     "mf_mm_static": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
                       ct.c_uint64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
@@ -367,6 +368,9 @@ def _group_dims(shape, granularity):
 
 
 STATUS_INPUT, STATUS_WEIGHT, STATUS_OUTPUT = 1, 2, 4
+# mm_from_float: a group scale above the bound that keeps every FP32 output finite, so
+# STATUS_OUTPUT is known only after the read (MF_STATUS_RANGE).
+STATUS_RANGE = 16
 # Set by a torch reduction in weight_tiles, not by a kernel: a negative weight under an
 # unsigned configuration, raised after the finiteness flags as the reference orders them
 # (memfast/functional.py:51-53 before memfast/quantization.py:14-18).
@@ -404,6 +408,21 @@ def _group_scratch(groups, device):
 def status_word(device):
     """Zeroed device status word (int32) that kernels OR their MF_STATUS_* bits into."""
     return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+def mailbox():
+    """A pinned host word for ``mm_from_float`` to publish its quantizers' status bits into."""
+    return torch.zeros(1, dtype=torch.int32, pin_memory=True)
+
+
+def status_wait(box, timeout_s=10.0):
+    """The status bits ``mm_from_float`` published into ``box`` (mf_status_wait), or None
+    when nothing was published within ``timeout_s`` (the caller then reads its device
+    status word, which waits for the whole call)."""
+    flags, published = ct.c_uint32(), _I32()
+    check(library().mf_status_wait(box.data_ptr(), int(timeout_s * 1e6), ct.byref(flags),
+                                   ct.byref(published)), "status wait")
+    return int(flags.value) if published.value else None
 
 
 def input_error(config, fixed_scale=None):
@@ -1082,13 +1101,16 @@ def from_float_applies(config, n, k, o):
             and mm_kernel(config, n, m, p) == 1)
 
 
-def mm_from_float(x, b, config, *, status=None, variant=0, workspace=None, scratch=None):
+def mm_from_float(x, b, config, *, status=None, variant=0, workspace=None, scratch=None,
+                  mailbox=None):
     """``x [N, K] @ b [K, O]`` from floating operands in two launches (mf_mm_from_float):
     (q, xscale, (packed, packed_t, wscale), out), exactly what ``input_tiles``,
     ``weight_tiles(b.T)`` and ``mm`` return, or None where the fused route does not apply
     (nothing is launched then).  ``workspace`` (optional, ``mm_workspace_bytes``) receives
     the digit masks as ``mm`` would.  ``scratch`` (optional) is a (q, xscale, workspace)
-    triple of earlier results to write again, for a caller that has finished with them."""
+    triple of earlier results to write again, whose earlier readers are queued on the current
+    stream.  ``mailbox`` (optional, from ``mailbox()``, zeroed by the caller) receives the
+    quantizers' status bits when the read starts (``status_wait``)."""
     require_device(x)
     n, k = x.shape
     o = b.shape[1]
@@ -1116,7 +1138,7 @@ def mm_from_float(x, b, config, *, status=None, variant=0, workspace=None, scrat
             ct.byref(descriptor(config)), xf.data_ptr(), n, k, k, bf.data_ptr(), o, o, gr_x,
             gc_x, gr_w, gc_w, q.data_ptr(), xscale.data_ptr(), packed.data_ptr(),
             packed_t.data_ptr(), wscale.data_ptr(), out.data_ptr(), p * c, workspace.data_ptr(),
-            workspace.numel(), variant, _ptr(status), _stream(device))
+            workspace.numel(), variant, _ptr(status), _ptr(mailbox), _stream(device))
     if code == E_UNSUPPORTED:
         return None
     check(code, "quantization and read")

@@ -179,10 +179,11 @@ class Simulator:
         self._next_id = 0
         self._matrix_cache = _ProgramCache(self)
         self._status = None   # _product's device status word; replaced once it holds flags
+        self._mailbox = None  # pinned host word the fused route publishes its status bits to
         self._from_float = {}   # (n, k, o) -> whether hip.mm_from_float applies
-        # (shape, (q, xscale, workspace)) of the last fused call, written again by the next
-        # call of that shape.
-        self._from_float_scratch = (None, None)
+        # (shape, stream, (q, xscale, workspace)) of the last fused call, written again by the
+        # next call of that shape on that stream.
+        self._from_float_scratch = (None, None, None)
 
     def _next_name(self):
         name = f"matrix.{self._next_id}"
@@ -348,21 +349,31 @@ class Simulator:
         event = 0 if previous is None else previous._event
         if event >= _EVENT_LIMIT or (previous is not None and previous.input_scale is not None):
             return None
-        # The codes, scales and masks of the last call of this shape are written again: that
-        # call read its status word, so its kernels have finished.
-        last_shape, scratch = self._from_float_scratch
+        # The codes, scales and masks of the last call of this shape are written again when
+        # that call ran on the current stream: its read is queued before these writes.
+        last_shape, last_stream, scratch = self._from_float_scratch
+        stream = hip._stream(self.device).value
+        reuse = last_shape == shape and last_stream == stream
+        if self._mailbox is None:
+            self._mailbox = hip.mailbox()
         fused = hip.mm_from_float(flat, rhs, self.config, status=status,
-                                  scratch=scratch if last_shape == shape else None)
+                                  scratch=scratch if reuse else None, mailbox=self._mailbox)
         if fused is None:
             self._from_float[shape] = False
             return None
         q, xscale, tiles, output = fused
-        if last_shape != shape:
+        if not reuse:
             workspace = hip._workspace(self.config, shape[0], q.shape[1], tiles[0].shape[1],
                                        q.device)
-            self._from_float_scratch = (shape, (q, xscale, workspace))
+            self._from_float_scratch = (shape, stream, (q, xscale, workspace))
         kept = previous if keepable and previous._accepts(tiles) else None
-        return int(status.item()), tiles, q, xscale, output, kept, True, event
+        # The read publishes the quantizers' status bits when it starts.  Unless a scale is
+        # large enough for an FP32 output to overflow, they are every bit of the call, and
+        # the read finishes behind the caller's next work on the stream.
+        flags = hip.status_wait(self._mailbox)
+        if flags is None or flags & hip.STATUS_RANGE:
+            flags = int(status.item())
+        return flags, tiles, q, xscale, output, kept, True, event
 
     # -- tuned mode (memfast_amd/tuning.py) -------------------------------------
     def _key(self, matrix, x, grid):

@@ -518,6 +518,124 @@ def test_mm_from_float_flags_nonfinite_operands(hip_device):
     assert bits_equal(sim.mm(a.to(hip_device), b.to(hip_device)), oracle.mm(a, b, cfg))
 
 
+def test_mm_from_float_publishes_status_when_the_read_starts(hip_device):
+    """The read's first workgroup copies the quantizers' status bits to a pinned host word
+    (hip.status_wait, mf_status_wait): the bits the device status word holds afterwards."""
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(11)
+    a, b = torch.randn(64, 256, generator=gen), torch.randn(256, 128, generator=gen)
+    bad_a, bad_b = a.clone(), b.clone()
+    bad_a[5, 77] = float("nan")
+    bad_b[200, 3] = float("-inf")
+    box = hip.mailbox()
+    checks = hip.STATUS_INPUT | hip.STATUS_WEIGHT
+    for left, right, bits in ((a, b, 0), (bad_a, b, hip.STATUS_INPUT),
+                              (a, bad_b, hip.STATUS_WEIGHT)):
+        status = hip.status_word(hip_device)
+        assert hip.mm_from_float(left.to(hip_device), right.to(hip_device), cfg, status=status,
+                                 mailbox=box) is not None
+        flags = hip.status_wait(box)
+        assert flags is not None and flags & checks == bits
+        if not bits:
+            assert flags == 0
+        torch.cuda.synchronize()
+        assert int(status.item()) & checks == bits
+
+
+def range_flag(cfg, peak, device, box, n=64, k=256, o=128):
+    """STATUS_RANGE of mm_from_float on saturating operands (every code at its extreme, every
+    group scale peak / 127; row 0 of A and column 0 of B all positive, so output (0, 0) is
+    the largest product the codes allow), and the call's output."""
+    signs_a = torch.randn(n, k, generator=torch.Generator().manual_seed(1)).sign()
+    signs_b = torch.randn(k, o, generator=torch.Generator().manual_seed(2)).sign()
+    signs_a[0], signs_b[:, 0] = 1.0, 1.0
+    a, b = signs_a * peak, signs_b * peak
+    fused = hip.mm_from_float(a.to(device), b.to(device), cfg, status=hip.status_word(device),
+                              mailbox=box)
+    flags = hip.status_wait(box)
+    assert flags is not None and not flags & (hip.STATUS_INPUT | hip.STATUS_WEIGHT)
+    return bool(flags & hip.STATUS_RANGE), a, b, fused[3]
+
+
+def test_range_flag_bounds_the_fp32_restore(hip_device):
+    """Below the scale at which the quantizers set STATUS_RANGE no FP32 step of the read's
+    restore can overflow: worst-case operands (every code saturated, the largest |total| of
+    every read) just below it give finite outputs equal to the oracle's.  The threshold is
+    found by bisection on the device; it is far above ordinary data, and Simulator.mm above
+    it reads the status word after the read (FP64 retry or the reference's error)."""
+    from memfast_amd import Simulator
+
+    cfg = ideal(**CONFIG2)
+    box = hip.mailbox()
+    lo, hi = 1.0, 1e38                     # no flag at lo, flag at hi
+    assert not range_flag(cfg, lo, hip_device, box)[0] and range_flag(cfg, hi, hip_device, box)[0]
+    while hi / lo > 1.0001:
+        mid = math.sqrt(lo * hi)
+        if range_flag(cfg, mid, hip_device, box)[0]:
+            hi = mid
+        else:
+            lo = mid
+    say("range threshold (peak)", lo)
+    flagged, a, b, out = range_flag(cfg, lo, hip_device, box)
+    assert not flagged
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert bits_equal(out, oracle.mm(a, b, cfg))
+    # The worst-case output at the threshold is within 2^8 of FP32's range: the bound
+    # leaves no needless fallback for data that fits.
+    assert float(out.abs().max()) > torch.finfo(torch.float32).max / 256
+    sim = Simulator(cfg, device=hip_device)
+    for scale in (hi * 1.01, 1e30):
+        flagged, a, b, _ = range_flag(cfg, scale, hip_device, box)
+        assert flagged
+        expected = None
+        try:
+            expected = oracle.mm(a, b, cfg)
+        except FloatingPointError:
+            pass
+        if expected is None or not torch.isfinite(expected).all():
+            with pytest.raises(FloatingPointError):
+                sim.mm(a.to(hip_device), b.to(hip_device))
+        else:
+            assert bits_equal(sim.mm(a.to(hip_device), b.to(hip_device)), expected)
+
+
+def test_pipelined_products_keep_their_results(hip_device):
+    """Simulator.mm on the fused route returns once the quantizers' status is published, and
+    the read finishes behind the caller's next work.  Consecutive products of one shape (each
+    writes the codes and scales of the last one again), one on a side stream (which gets its
+    own scratch), one with a bf16 output and one that overflows FP32 (full status read, FP64
+    retry) all equal the oracle's."""
+    from memfast_amd import Simulator
+
+    cfg = ideal(**CONFIG2)
+    gen = torch.Generator().manual_seed(12)
+    n, k, o = 256, 1024, 512
+    pairs = [(torch.randn(n, k, generator=gen), torch.randn(k, o, generator=gen))
+             for _ in range(4)]
+    big = (torch.randn(n, k, generator=gen) * 1e37, torch.randn(k, o, generator=gen) * 1e-8)
+    sim = Simulator(cfg, device=hip_device)
+    assert hip.from_float_applies(cfg, n, k, o)
+    outs = [sim.mm(a.to(hip_device), b.to(hip_device)) for a, b in pairs[:2]]
+    main = torch.cuda.current_stream(hip_device)
+    side = torch.cuda.Stream(device=hip_device)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        a, b = pairs[2]
+        outs.append(sim.mm(a.to(hip_device), b.to(hip_device)))
+    main.wait_stream(side)
+    a, b = pairs[3]
+    outs.append(sim.mm(a.to(hip_device).bfloat16(), b.to(hip_device).bfloat16()))
+    overflow = sim.mm(big[0].to(hip_device), big[1].to(hip_device))
+    torch.cuda.synchronize()
+    for i, ((a, b), got) in enumerate(zip(pairs, outs)):
+        if i == 3:
+            a, b = a.bfloat16(), b.bfloat16()
+        assert bits_equal(got, oracle.mm(a, b, cfg)), i
+    expected = oracle.mm(*big, cfg)
+    assert torch.isfinite(expected).all() and bits_equal(overflow, expected)
+
+
 def test_mm_from_float_declines_other_shapes(hip_device):
     """Shapes and configurations outside the fused route launch nothing and return None;
     Simulator.mm then takes the separate calls (checked against the oracle)."""

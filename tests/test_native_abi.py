@@ -40,6 +40,22 @@ def test_ctypes_signatures_cover_header():
     assert set(hip.SIGNATURES) == set(declared_functions())
 
 
+def test_status_wait_reads_a_published_word():
+    """mf_status_wait (host code only) returns the bits of a mailbox word that holds
+    MF_STATUS_PUBLISHED and reports a word without it as unpublished after the timeout."""
+    lib = hip.library()
+    word = (ctypes.c_uint32 * 1)(0x80000000 | hip.STATUS_INPUT | hip.STATUS_RANGE)
+    flags, published = ctypes.c_uint32(), ctypes.c_int32()
+    assert lib.mf_status_wait(ctypes.addressof(word), 0, ctypes.byref(flags),
+                              ctypes.byref(published)) == 0
+    assert published.value == 1 and flags.value == hip.STATUS_INPUT | hip.STATUS_RANGE
+    word[0] = hip.STATUS_WEIGHT   # bits without the published mark: not yet published
+    assert lib.mf_status_wait(ctypes.addressof(word), 3000, ctypes.byref(flags),
+                              ctypes.byref(published)) == 0
+    assert published.value == 0 and flags.value == 0
+    assert lib.mf_status_wait(None, 0, ctypes.byref(flags), ctypes.byref(published)) != 0
+
+
 def test_abi_version_and_hash():
     lib = hip.library()
     assert lib.mf_abi_version() == hip.ABI_VERSION
