@@ -127,6 +127,64 @@ def test_sweep_product_matches_oracle(hip_device, index, noisy):
     check_product(cfg, got, a, b, hip_device, label=f"sweep {index}")
 
 
+FUSED_CASES = 12
+
+
+def _fused_case(index):
+    """A configuration and shapes that the two-launch route (hip.mm_from_float) takes: ideal
+    devices, 32 rows per read, groups of one read on both sides, whole arrays; slicings,
+    widths and ADC bits drawn.  Three operand pairs whose magnitudes range over 10^-12 to
+    10^12, and sometimes A's far above the bound under which no FP32 restore can overflow
+    (with B small enough that the product stays finite)."""
+    rng = np.random.default_rng(7000 + index)
+    while True:
+        rows, cols = int(rng.choice([128, 256])), int(rng.choice([64, 128]))
+        abits, wbits = int(rng.choice([4, 6, 8])), int(rng.choice([4, 6, 8]))
+        wslice = _slices(rng, wbits)
+        n_w = len(wslice) if wslice is not None else wbits
+        adc = (tuple(int(rng.integers(4, 10)) for _ in range(n_w)) if rng.random() < 0.5
+               else int(rng.integers(4, 10)))
+        try:
+            cfg = Config(activation_bits=abits, weight_bits=wbits, input_slice=_slices(rng, abits),
+                         weight_slice=wslice, array_size=(rows, cols), rows_per_read=32,
+                         weight_quant_gran=(32, 1), input_quant_gran=(1, 32), adc_bits=adc,
+                         seed=int(rng.integers(0, 2**32)),
+                         nonidealities=Nonidealities(write_variation=0.0))
+        except ValueError:
+            continue
+        n = int(rng.integers(1, 200))
+        k, o = rows * int(rng.integers(1, 5)), cols * int(rng.integers(1, 5))
+        if hip.from_float_applies(cfg, n, k, o):
+            break
+    gen = torch.Generator().manual_seed(7000 + index)
+    pairs = []
+    for _ in range(3):
+        a, b = torch.randn(n, k, generator=gen), torch.randn(k, o, generator=gen)
+        if rng.random() < 0.3:
+            a, b = a * 1e18, b * 1e-12
+        else:
+            a, b = a * 10.0 ** rng.uniform(-12, 12), b * 10.0 ** rng.uniform(-12, 12)
+        pairs.append((a, b))
+    return cfg, pairs
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("index", range(FUSED_CASES))
+def test_sweep_fused_products_back_to_back(hip_device, index):
+    """Three products of one shape on one simulator with no synchronization between them:
+    each call returns once its quantizers' status is published (or, above the overflow
+    bound, after its read), and each output equals the oracle's bit for bit."""
+    from memfast_amd import Simulator
+
+    cfg, pairs = _fused_case(index)
+    a0, b0 = pairs[0]
+    say("fused sweep", index, tuple(a0.shape), tuple(b0.shape), cfg)
+    sim = Simulator(cfg, device=hip_device)
+    outs = [sim.mm(a.to(hip_device), b.to(hip_device)) for a, b in pairs]
+    for call, ((a, b), got) in enumerate(zip(pairs, outs)):
+        check_product(cfg, got, a, b, hip_device, label=f"fused {index}.{call}")
+
+
 CONV_CASES = 8
 
 
