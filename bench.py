@@ -185,7 +185,7 @@ def _read_modes(out, device):
     read: per-slice-pair read noise (a plane of terms per input slice), output-mode read
     noise (mean and variance sums, a normal per conversion), voltage noise (real input
     operands) and output-mode read noise with voltage noise (real operands and their
-    squares)."""
+    squares); then config 5's wide slicing, and FP64 currents."""
     import torch
 
     import memfast_amd as memfast
@@ -231,6 +231,17 @@ def _read_modes(out, device):
         out[f"read_mode_{name}"] = dict(ms_per_step=round(ms, 2), kernel_ms=round(kernel_ms, 2),
                                         gmac_per_s=round(SIZE**3 / (ms * 1e-3) / 1e9, 1),
                                         kernel="wide MFMA")
+    # FP64 currents (precise_currents: high - low = 5e-5 of high) at config 2's slicing and
+    # size, on the FP64 MFMA read, with write and shared read noise.
+    cfg = memfast.Config(**BASE, high_conductance=1e-5, low_conductance=9.9995e-6,
+                         nonidealities=memfast.Nonidealities(write_variation=2e-6,
+                                                             read_variation=1e-6))
+    assert cfg.precise_currents and hip.mm_kernel(cfg, SIZE, SIZE // 128, SIZE // 128) == 0
+    sim = memfast.Simulator(cfg, device=device)
+    ms, kernel_ms = time_steps(lambda: sim.mm(a, b), 3, 1)
+    out["read_mode_precise"] = dict(ms_per_step=round(ms, 2), kernel_ms=round(kernel_ms, 2),
+                                    gmac_per_s=round(SIZE**3 / (ms * 1e-3) / 1e9, 1),
+                                    kernel="FP64 MFMA")
 
 
 def _config1(out, int8, device):

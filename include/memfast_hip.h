@@ -437,9 +437,11 @@ int mf_mm_totals(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m,
                  const uint8_t *packed_t, int64_t p, const float *g, uint32_t seed, uint64_t event,
                  float *totals, void *workspace, int64_t workspace_bytes, void *stream);
 
-/* Kernel selected by mf_mm (mf_mm_wide) for this shape: 0 = general, 1 = MFMA
- * ideal, 2 = MFMA noisy (fp16 hi + lo conductance terms), 3 = MFMA noisy for wide
- * codes. */
+/* Kernel selected by mf_mm (mf_mm_wide) for this shape: 0 = general (FP64 currents,
+ * precise_currents, run on FP64 MFMA unless voltage variation or output-mode read
+ * noise needs the FMA kernel; so do mf_partial's totals without per-pair codes),
+ * 1 = MFMA ideal, 2 = MFMA noisy (fp16 hi + lo conductance terms), 3 = MFMA noisy
+ * for wide codes. */
 int mf_mm_kernel(const mf_config *cfg, int64_t n, int64_t m, int64_t p, int32_t has_packed_t,
                  int32_t *kernel_id);
 

@@ -838,6 +838,45 @@ int launch_general(const mf_config *cfg, const GeneralArgs &args, int out_kind, 
     return check_launch("general read");
 }
 
+// Precise currents run on FP64 MFMA (k_general_mfma64) unless voltage variation or
+// output-mode read noise needs the general kernel.
+static bool precise_mfma_ok(const mf_config *cfg) {
+    return cfg->precise && !cfg->has_vnoise &&
+           !(cfg->has_read && cfg->read_mode == MF_READ_OUTPUT);
+}
+
+static int launch_general_mfma64(const mf_config *cfg, const GeneralArgs &args, int out_kind,
+                                 hipStream_t s) {
+    const i64 ncols = args.width * cfg->cols;
+    const i64 col_blocks = (ncols + 15) / 16;
+    const i64 vec_blocks = (args.n + 15) / 16;
+    if (col_blocks > 65535) return fail(MF_E_RESOURCE, "too many output columns for one launch");
+    if (vec_blocks > 2147483647) return fail(MF_E_RESOURCE, "too many input vectors");
+    const dim3 grid{unsigned(vec_blocks), unsigned(col_blocks), 1u};
+    const bool staged = args.planes == 1 && cfg->n_w <= MFMA64_STAGED_MAX_W;
+#define MF_MFMA64_LAUNCH(WIDE, STAGED)                                                           \
+    hipLaunchKernelGGL((k_general_mfma64<WIDE, STAGED>), grid, dim3(256), 0, s, *cfg, args,     \
+                       out_kind)
+    if (cfg->wide) {
+        if (staged) MF_MFMA64_LAUNCH(true, true);
+        else MF_MFMA64_LAUNCH(true, false);
+    } else {
+        if (staged) MF_MFMA64_LAUNCH(false, true);
+        else MF_MFMA64_LAUNCH(false, false);
+    }
+#undef MF_MFMA64_LAUNCH
+    return check_launch("precise MFMA read");
+}
+
+// The general read (fused or to totals): FP32 currents on k_general, precise ones on FP64
+// MFMA where that applies and no per-pair codes are asked for, else k_general in FP64.
+static int launch_general_read(const mf_config *cfg, const GeneralArgs &args, int out_kind,
+                               hipStream_t s) {
+    if (!cfg->precise) return launch_general<float>(cfg, args, out_kind, s);
+    return precise_mfma_ok(cfg) && !args.codes ? launch_general_mfma64(cfg, args, out_kind, s)
+                                               : launch_general<double>(cfg, args, out_kind, s);
+}
+
 // Group maxima |x| into work[row group][col group] (cleared): column groups and
 // wide row groups by chunked reductions with few atomics, others elementwise.
 static void launch_input_codes(const float *x, i64 n, i64 k, i64 ld, i64 kp, const float *scale,
@@ -1283,8 +1322,7 @@ int mf_partial(const mf_config *cfg, const uint8_t *q, int64_t n, int64_t m, con
     args.lp_cascade = level_power(G);
     args.lp_interleaved = level_power(G / 4);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    return cfg->precise ? launch_general<double>(cfg, args, OUT_TOTALS, s)
-                        : launch_general<float>(cfg, args, OUT_TOTALS, s);
+    return launch_general_read(cfg, args, OUT_TOTALS, s);
 }
 
 // Extents the MFMA kernel addresses with 32-bit buffer offsets (a block's code
@@ -1515,8 +1553,7 @@ static int mm_read(const mf_config *cfg, const uint8_t *q, const float *xscale, 
     args.lp_interleaved = level_power(G / 4);
     std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
     if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-    const int launched = cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
-                                      : launch_general<float>(cfg, args, OUT_FUSED, s);
+    const int launched = launch_general_read(cfg, args, OUT_FUSED, s);
     if (timing.first) {
         hipEventRecord(timing.second, s);
         profile_push(timing);
@@ -2047,8 +2084,7 @@ int mf_partial_wide(const mf_config *cfg, const uint32_t *q, int64_t n, int64_t 
     args.lp_cascade = level_power(G);
     args.lp_interleaved = level_power(G / 4);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    return cfg->precise ? launch_general<double>(cfg, args, OUT_TOTALS, s)
-                        : launch_general<float>(cfg, args, OUT_TOTALS, s);
+    return launch_general_read(cfg, args, OUT_TOTALS, s);
 }
 
 int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, int64_t n, int64_t m,
@@ -2106,8 +2142,7 @@ int mf_mm_wide(const mf_config *cfg, const uint32_t *q, const double *xscale, in
     hipStream_t s = static_cast<hipStream_t>(stream);
     std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
     if (profiling() && (timing = profile_pair()).first) hipEventRecord(timing.first, s);
-    const int launched = cfg->precise ? launch_general<double>(cfg, args, OUT_FUSED, s)
-                                      : launch_general<float>(cfg, args, OUT_FUSED, s);
+    const int launched = launch_general_read(cfg, args, OUT_FUSED, s);
     if (timing.first) {
         hipEventRecord(timing.second, s);
         profile_push(timing);
@@ -2241,7 +2276,11 @@ int mf_resources_query(const mf_config *cfg, int32_t kernel_id, int64_t n, int32
     } else if (kernel_id == 0) {
 #define MF_GENERAL_FN(WIDE)                                                                      \
     (cfg->precise                                                                                \
-         ? (output_noise ? reinterpret_cast<const void *>(&k_general<double, 2, true, WIDE>)      \
+         ? (precise_mfma_ok(cfg)                                                                 \
+                ? (restore_planes(cfg) == 1 && cfg->n_w <= MFMA64_STAGED_MAX_W                   \
+                       ? reinterpret_cast<const void *>(&k_general_mfma64<WIDE, true>)           \
+                       : reinterpret_cast<const void *>(&k_general_mfma64<WIDE, false>))         \
+            : output_noise ? reinterpret_cast<const void *>(&k_general<double, 2, true, WIDE>)    \
                          : reinterpret_cast<const void *>(&k_general<double, 4, false, WIDE>))    \
          : (output_noise ? reinterpret_cast<const void *>(&k_general<float, 2, true, WIDE>)       \
                          : reinterpret_cast<const void *>(&k_general<float, 8, false, WIDE>)))

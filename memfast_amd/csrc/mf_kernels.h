@@ -29,6 +29,11 @@ struct GeneralArgs {
 
 template <typename Phys, int WG, bool OUTPUT_NOISE, bool WIDE>
 __global__ void k_general(const mf_config cfg, const GeneralArgs args, int out_kind);
+// The read of precise currents on FP64 MFMA (no voltage variation, no output-mode read
+// noise), fused or to totals as k_general.
+template <bool WIDE, bool STAGED>
+__global__ void k_general_mfma64(const mf_config cfg, const GeneralArgs args, int out_kind);
+constexpr int MFMA64_STAGED_MAX_W = 8;   // weight slices of the LDS-staged variant
 
 // ---- ideal MFMA read (ideal_mfma.hip) -------------------------------------
 constexpr int IDEAL_MAX_CA = 8;     // input slices with at least one clamped pair

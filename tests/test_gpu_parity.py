@@ -1171,6 +1171,88 @@ def test_precise_mm_matches_reference_vectors(hip_device, reference_vectors, nam
                               label=f"precise {name} event {event}"))
 
 
+PRECISE_MFMA = {
+    # A 9-bit input digit (mask 511 > 255): FP64 currents.  Write and shared read noise with
+    # the S-curve ADC; ideal devices; slice_pair read noise (one plane per input slice).
+    "slice9": (dict(activation_bits=12, weight_bits=8, input_slice=(1, 2, 9),
+                    weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=16,
+                    adc_bits=8), dict(write_variation=0.02, read_variation=0.01,
+                                      adc_nonlinearity=0.1)),
+    "slice9_ideal": (dict(activation_bits=12, weight_bits=8, input_slice=(1, 2, 9),
+                          weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=32,
+                          adc_bits=8), dict(write_variation=0.0)),
+    "slice9_pair": (dict(activation_bits=12, weight_bits=8, input_slice=(1, 2, 9),
+                         weight_slice=(1, 1, 2, 2, 2), array_size=(64, 32), rows_per_read=64,
+                         adc_bits=8), dict(write_variation=0.02, read_variation=0.02,
+                                           read_mode="slice_pair")),
+    # High - low = 5e-5 of high, narrow codes; drift and stuck-at faults; 128-row reads.
+    "close": (dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                   weight_slice=(1, 1, 2, 2, 2), array_size=(128, 64), rows_per_read=128,
+                   adc_bits=(6, 7, 7, 8, 8), high_conductance=1e-5, low_conductance=9.9995e-6),
+              dict(write_variation=2e-6, stuck_at_low=0.01, stuck_at_high=0.01,
+                   drift_coefficient=0.05, drift_time=100.0)),
+    "close_ideal": (dict(activation_bits=8, weight_bits=8, input_slice=(1, 1, 2, 2, 2),
+                         weight_slice=(1, 1, 2, 2, 2), array_size=(32, 16), rows_per_read=16,
+                         adc_bits=(6, 7, 7, 8, 8), high_conductance=1e-5,
+                         low_conductance=9.9995e-6), dict(write_variation=0.0)),
+}
+
+
+@pytest.mark.parametrize("name", list(PRECISE_MFMA))
+def test_precise_mfma_read_matches_general_kernel(hip_device, name):
+    """FP64 currents on FP64 MFMA (k_general_mfma64, what Simulator.mm and mf_partial's totals
+    run) against k_general<double> (mf_partial with per-pair codes, the reference's
+    arithmetic order) on the same conductances: bit for bit with ideal devices, else
+    identical but for rounding-boundary flips.  Simulator.mm's fused output is the oracle's
+    epilogue of the MFMA totals, bit for bit, and the oracle checks the product as the other
+    parity tests do."""
+    from memfast_amd import Simulator
+
+    kwargs, effects = PRECISE_MFMA[name]
+    cfg = Config(**kwargs, nonidealities=Nonidealities(**effects))
+    assert cfg.precise_currents
+    gen = torch.Generator().manual_seed(len(name))
+    n, k, o = 37, 2 * cfg.array_size[0] + 9, cfg.array_size[1] + 7
+    a, b = torch.randn(n, k, generator=gen), torch.randn(k, o, generator=gen)
+    dev = hip_device
+    q, xs = hip.input_tiles(a.to(dev), cfg)
+    packed, _, ws = hip.weight_tiles(b.T.contiguous().to(dev), cfg)
+    m, p = q.shape[1], packed.shape[1]
+    assert hip.mm_kernel(cfg, n, m, p) == 0
+    seed = oracle.name_seed(cfg.seed, "matrix.0")
+    g = None if cfg.nonidealities.ideal else hip.restore(packed, cfg, seed, 0, 0, p)
+    mfma = hip.partial(q, packed, cfg, None, seed, 0, 0, p, conductance=g)
+    general, _ = hip.partial(q, packed, cfg, None, seed, 0, 0, p, conductance=g, codes=True)
+    if cfg.nonidealities.ideal:
+        assert bits_equal(mfma, general)
+    else:
+        differing, flipped, unexplained, mask = flips.count_flips(cfg, mfma.cpu().double(),
+                                                                  general.cpu().double())
+        codes = mask.numel() * len(cfg.input_layout) * len(cfg.weight_layout)
+        say("  precise mfma", name, differing, "differing totals,", flipped, "flips of", codes)
+        assert unexplained == 0 and flipped <= max(1, 1e-4 * codes)
+    got = Simulator(cfg, device=dev).mm(a.to(dev), b.to(dev))
+    q_cpu, xs_cpu = oracle.input_tiles(a, cfg)
+    packed_cpu, ws_cpu = oracle.weight_tiles(b.T, cfg)
+    epilogue = oracle.execute(q_cpu, xs_cpu, packed_cpu, ws_cpu, cfg, seed, 0, o,
+                              totals=mfma.cpu().to(mfma.dtype)).to(got.dtype)
+    assert bits_equal(got, epilogue)
+    check_product(cfg, got, a, b, dev, label=f"precise mfma {name}")
+
+
+def test_precise_mfma_resources(hip_device):
+    """mf_resources_query reports the FP64 MFMA read for precise currents, and k_general
+    where voltage variation keeps them there."""
+    cfg = Config(**PRECISE_MFMA["slice9"][0], nonidealities=Nonidealities(write_variation=0.02))
+    volt = Config(**PRECISE_MFMA["slice9"][0],
+                  nonidealities=Nonidealities(write_variation=0.02, voltage_variation=0.02))
+    plain = hip.program(cfg, 64, 64, hip_device.index).resources(cfg, 64, 64, 0, kernel=0)
+    general = hip.program(volt, 64, 64, hip_device.index).resources(volt, 64, 64, 0, kernel=0)
+    say("precise resources", plain, general)
+    assert plain["threads"] == general["threads"] == 256
+    assert plain != general
+
+
 # ---------------------------------------------------------------------------
 # Wide configurations on the noisy-device fp16 MFMA kernel (mm_kernel 3)
 # ---------------------------------------------------------------------------
