@@ -248,10 +248,17 @@ int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k,
                      uint32_t *mailbox, void *stream);
 
 /* No counterpart in the reference (which checks its operands with host scans that
- * synchronize).  Waits until the mailbox word of mf_mm_from_float holds
- * MF_STATUS_PUBLISHED or timeout_us microseconds have passed (spinning, then sleeping
- * in short steps); *flags receives the word without that bit and *published whether
- * it was set.  A caller that times out reads the device status word instead. */
+ * synchronize).  Queues, on `stream`, a copy of the device status word into the mailbox
+ * (pinned host memory; cleared here first), marked MF_STATUS_PUBLISHED: what the kernels
+ * queued before it have set.  A caller that launches it between a quantizer and the read
+ * learns the quantizer's bits without waiting for the read. */
+int mf_status_publish(const uint32_t *status, uint32_t *mailbox, void *stream);
+
+/* No counterpart in the reference (which checks its operands with host scans that
+ * synchronize).  Waits until the mailbox word of mf_mm_from_float or mf_status_publish
+ * holds MF_STATUS_PUBLISHED or timeout_us microseconds have passed (spinning, then
+ * sleeping in short steps); *flags receives the word without that bit and *published
+ * whether it was set.  A caller that times out reads the device status word instead. */
 int mf_status_wait(const uint32_t *mailbox, int64_t timeout_us, uint32_t *flags,
                    int32_t *published);
 

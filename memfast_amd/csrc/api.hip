@@ -949,6 +949,9 @@ static int check_conv_geometry(const mf_conv_geometry &g) {
     return MF_OK;
 }
 
+// One lane: the status word as the kernels queued before it left it, to the mailbox.
+__global__ void k_publish_status(u32 *status, u32 *mailbox) { publish_status(status, mailbox); }
+
 extern "C" {
 
 int32_t mf_abi_version(void) { return MF_ABI_VERSION; }
@@ -1652,6 +1655,19 @@ int mf_mm_from_float(const mf_config *cfg, const float *x, int64_t n, int64_t k,
     if (launched) return launched;
     return launch_ideal(cfg, plan, ks, q, xscale, packed_t, wscale, xbits, wbits, n, m, p, o, G,
                         out, ldo, variant, status, s, device_mailbox);
+}
+
+int mf_status_publish(const uint32_t *status, uint32_t *mailbox, void *stream) {
+    if (!status || !mailbox) return fail(MF_E_INVALID, "invalid status_publish arguments");
+    __atomic_store_n(mailbox, 0u, __ATOMIC_RELAXED);
+    u32 *device_mailbox = nullptr;
+    const hipError_t e =
+        hipHostGetDevicePointer(reinterpret_cast<void **>(&device_mailbox), mailbox, 0);
+    if (e != hipSuccess)
+        return fail(MF_E_INVALID, "mailbox is not pinned host memory: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(k_publish_status, dim3(1), dim3(1), 0, static_cast<hipStream_t>(stream),
+                       const_cast<u32 *>(status), device_mailbox);
+    return check_launch("status publish");
 }
 
 int mf_status_wait(const uint32_t *mailbox, int64_t timeout_us, uint32_t *flags,

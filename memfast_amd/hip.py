@@ -150,6 +150,7 @@ SIGNATURES = {
     "mf_mm_from_float": ([_CFG, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
                           _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _P], ct.c_int),
     "mf_status_wait": ([_P, _I64, ct.POINTER(ct.c_uint32), ct.POINTER(_I32)], ct.c_int),
+    "mf_status_publish": ([_P, _P, _P], ct.c_int),
     "mf_mm_static": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
                       ct.c_uint64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
@@ -413,6 +414,14 @@ def status_word(device):
 def mailbox():
     """A pinned host word for ``mm_from_float`` to publish its quantizers' status bits into."""
     return torch.zeros(1, dtype=torch.int32, pin_memory=True)
+
+
+def status_publish(status, box):
+    """Queue a copy of ``status`` into the pinned ``box`` (mf_status_publish): the bits the
+    kernels queued so far set, for ``status_wait``."""
+    with _on(status.device):
+        check(library().mf_status_publish(_ptr(status), _ptr(box), _stream(status.device)),
+              "status publish")
 
 
 def status_wait(box, timeout_s=10.0):

@@ -35,6 +35,8 @@ from .tuning import default_schedule, schedule_grid
 
 _CODE_DTYPES = (torch.uint8, torch.int8, torch.int16, torch.int32, torch.int64)
 _EVENT_LIMIT = 1 << 63
+# _execute_checked's `finite` for an output that the scales bound below FLT_MAX / 2.
+_BOUNDED = "bounded"
 
 
 def source_hash():
@@ -180,10 +182,18 @@ class Simulator:
         self._matrix_cache = _ProgramCache(self)
         self._status = None   # _product's device status word; replaced once it holds flags
         self._mailbox = None  # pinned host word the fused route publishes its status bits to
+        self._mailbox_layers = None   # the same for layer reads (_layer_mailbox)
         self._from_float = {}   # (n, k, o) -> whether hip.mm_from_float applies
         # (shape, stream, (q, xscale, workspace)) of the last fused call, written again by the
         # next call of that shape on that stream.
         self._from_float_scratch = (None, None, None)
+
+    def _layer_mailbox(self):
+        """The pinned word that layer reads of this simulator publish their quantizers'
+        status bits to (one call at a time, as the device status words)."""
+        if self._mailbox_layers is None:
+            self._mailbox_layers = hip.mailbox()
+        return self._mailbox_layers
 
     def _next_name(self):
         name = f"matrix.{self._next_id}"
@@ -675,12 +685,18 @@ class AnalogMatrix(nn.Module):
         packed = self.packed
         if not config.wide and packed.dtype != torch.uint8:
             packed = packed.to(torch.uint8)
+        box = None
         if stable:
             output = self._execute_stable(q, xscale, packed, event)
         else:
             kernel = hip.mm_kernel(config, q.shape[0], q.shape[1], self.p)
             codes_t = self._column_codes() if config.wide or kernel else None
             status = hip.status_word(q.device) if status is None else status
+            if not defer and self._output_bounded(q.shape[1]):
+                # The quantizer's bits are the only ones this read can leave: publish them
+                # now, and the read runs on behind the caller's next work.
+                box = self.simulator._layer_mailbox()
+                hip.status_publish(status, box)
             variant = tuning.schedule_variant(schedule)
             workspace, reuse, source = None, False, None
             if kernel == 2 and hip.terms_event_independent(config):
@@ -706,6 +722,12 @@ class AnalogMatrix(nn.Module):
             hip.bias_add(output, self.bias, status)
         if defer:
             return output, True
+        if box is not None:
+            flags = hip.status_wait(box)
+            if flags is not None and flags & hip.STATUS_INPUT:
+                raise ValueError(input_error or "quantized values must be finite")
+            if flags == 0:
+                return output, _BOUNDED
         flags = int(status.item())   # the one status read: deferred input check, then outputs
         if flags & hip.STATUS_INPUT:
             raise ValueError(input_error or "quantized values must be finite")
@@ -719,6 +741,33 @@ class AnalogMatrix(nn.Module):
         if not retry:
             return None, False
         return self._execute_checked(q, xscale, schedule, event, stable=True)
+
+    def _host_max(self, name, tensor):
+        """max |tensor| as a Python float, read from the device once per version of the
+        tensor (its storage, shape and in-place modification count)."""
+        key = (tensor.data_ptr(), tuple(tensor.shape), tensor._version)
+        cache = self.__dict__.setdefault("_host_maxima", {})
+        hit = cache.get(name)
+        if hit is None or hit[0] != key:
+            value = float(tensor.detach().abs().max()) if tensor.numel() else 0.0
+            hit = cache[name] = (key, value)
+        return hit[1]
+
+    def _output_bounded(self, arrays):
+        """Whether the default-mode read of fixed-scale inputs cannot leave a non-finite
+        output: every read's total obeys |T| <= Config.reconstruction_bound, so with the
+        largest fixed input scale xs, weight scale ws and bias b, every FP32 product, sum and
+        bias add stays below G * bound * xs * ws * 1.07 + |b| (G reads), asked here to be
+        below FLT_MAX / 2.  Those maxima are read once per version of their tensors."""
+        if (self.simulator.mode != "default" or self.input_scale is None
+                or self.config.bw_e is not None or self.zero_correction is not None):
+            return False
+        reads = arrays * self.config.reads_per_array
+        xs = self._host_max("input_scale", self.input_scale)
+        ws = self._host_max("weight_scale", self.weight_scale)
+        bias = 0.0 if self.bias is None else self._host_max("bias", self.bias)
+        bound = reads * self.config.reconstruction_bound * xs * ws * 1.07 + bias
+        return math.isfinite(bound) and bound < torch.finfo(torch.float32).max / 2
 
     def _terms_workspace(self, rows, arrays, device, codes_t, variant=tuning.DEFAULT_VARIANT):
         """Workspace of the noisy MFMA read kept across calls, and whether it still holds
@@ -829,9 +878,12 @@ class AnalogMatrix(nn.Module):
 
     def _finish(self, x, output, finite):
         """Cast to the input dtype, check finiteness, advance the read event
-        (memfast/simulator.py:632-646)."""
+        (memfast/simulator.py:632-646).  A _BOUNDED output is below FLT_MAX / 2, so it is
+        finite in every input dtype with FP32's range."""
         converted = output.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
-        if not (finite and output.dtype == x.dtype) and not bool(torch.isfinite(converted).all()):
+        known = finite is _BOUNDED and x.dtype != torch.float16
+        if not (known or (finite and output.dtype == x.dtype)) and \
+                not bool(torch.isfinite(converted).all()):
             raise FloatingPointError("nonfinite analog output")
         self._event += 1
         return converted

@@ -1658,6 +1658,73 @@ def test_layer_input_and_bias_checks_in_one_status_read(hip_device):
     assert layer._event == 2
 
 
+def test_bounded_fixed_scale_reads_publish_their_input_check(hip_device, monkeypatch):
+    """With fixed input scales whose restore cannot leave FP32 (every read's slice total
+    is at most Config.reconstruction_bound), a layer read publishes its quantizer's status
+    bits before the read and returns on them: the outputs equal the full status read's bit
+    for bit (linear and convolution, FP32 and bfloat16 inputs); a non-finite input still
+    raises before the event advances; an in-place bias change or a huge scale turns the
+    bound off."""
+    from torch import nn
+
+    from memfast_amd import Simulator
+    from memfast_amd.nn import AnalogConv2d, AnalogLinear
+    from memfast_amd.simulator import AnalogMatrix
+
+    cfg = noisy_case("write")
+    torch.manual_seed(47)
+    linear = nn.Linear(300, 90).to(hip_device)
+    conv = nn.Conv2d(8, 16, 3, padding=1).to(hip_device)
+    x = torch.randn(33, 300, device=hip_device)
+    image = torch.randn(2, 8, 12, 12, device=hip_device)
+
+    def build(source, kind):
+        layer = kind(source, Simulator(cfg, device=hip_device), name="bounded")
+        for matrix in getattr(layer, "matrices", [layer]):
+            matrix.set_input_scale(0.03)
+        return layer
+
+    def read(source, kind, value, bounded):
+        layer = build(source, kind)
+        matrix = getattr(layer, "matrices", [layer])[0]
+        seen = []
+        original = AnalogMatrix._output_bounded
+
+        def spy(self, arrays):
+            seen.append(original(self, arrays) if bounded else False)
+            return seen[-1]
+
+        monkeypatch.setattr(AnalogMatrix, "_output_bounded", spy)
+        with torch.no_grad():
+            out = layer(value)
+        monkeypatch.setattr(AnalogMatrix, "_output_bounded", original)
+        assert seen and all(s == bounded for s in seen) and matrix._event == 1
+        return out, layer
+
+    for source, kind, value in ((linear, AnalogLinear, x), (conv, AnalogConv2d, image),
+                                (linear, AnalogLinear, x.to(torch.bfloat16))):
+        early, _ = read(source, kind, value, True)
+        full, _ = read(source, kind, value, False)
+        # bfloat16 widens to float32 exactly, so the float32 bits compare the bfloat16 bits.
+        assert early.dtype == value.dtype and bits_equal(early.float(), full.float())
+
+    layer = build(linear, AnalogLinear)
+    bad = x.clone()
+    bad[4, 7] = float("inf")
+    assert layer._output_bounded(-(-300 // cfg.array_size[0]))
+    with pytest.raises(ValueError, match=r"^quantized values must be finite$"):
+        layer(bad)
+    assert layer._event == 0
+    with torch.no_grad():
+        layer.bias.fill_(torch.finfo(torch.float32).max)
+    assert not layer._output_bounded(-(-300 // cfg.array_size[0]))
+    layer.set_input_scale(1e37)
+    with torch.no_grad():
+        layer.bias.zero_()
+    assert not layer._output_bounded(-(-300 // cfg.array_size[0]))
+    assert torch.isfinite(layer(x[:3])).all() and layer._event == 1
+
+
 EXTENT_CASES = [
     ("ideal", ideal(**CONFIG2 | dict(array_size=(64, 32))), 9, 200, 70),
     ("ideal_258_reads", ideal(**CONFIG2 | dict(array_size=(64, 32))), 3, 8200, 40),
