@@ -284,6 +284,14 @@ int mf_mm_static(const mf_config *cfg, const uint8_t *q, const float *xscale, in
                  uint64_t event, float *out, int64_t ldo, int32_t variant, uint32_t *status,
                  void *stream);
 
+/* The cast of a wide read's FP64 output to FP32 inputs' dtype and its finiteness check
+ * (memfast/simulator.py:642-644, `.to(x.dtype)` then a host `isfinite` scan):
+ * out[v * cols + c] = (float) in[v * ld + c] for c < cols (round to nearest even), and a
+ * non-finite result sets MF_STATUS_OUTPUT in status (may be NULL), so the call's one
+ * status read also answers the scan. */
+int mf_narrow_output(const double *in, int64_t n, int64_t cols, int64_t ld, float *out,
+                     uint32_t *status, void *stream);
+
 /* Bias of an FP32 read (memfast/simulator.py:612-613, `out + bias`): out[v, c]
  * += bias[c] for c < o, one FP32 add each; a non-finite sum sets
  * MF_STATUS_OUTPUT in status (may be NULL), which replaces the host-side

@@ -1820,6 +1820,16 @@ int mf_bias_add(float *out, int64_t n, int64_t o, int64_t ldo, const float *bias
     return check_launch("bias add");
 }
 
+int mf_narrow_output(const double *in, int64_t n, int64_t cols, int64_t ld, float *out,
+                     uint32_t *status, void *stream) {
+    if (!in || !out || n < 1 || cols < 1 || ld < cols)
+        return fail(MF_E_INVALID, "invalid output cast arguments");
+    hipLaunchKernelGGL(k_narrow_f64, dim3(grid_for(n * cols)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), in, n, cols, ld, out, status,
+                       u32(MF_STATUS_OUTPUT));
+    return check_launch("output cast");
+}
+
 int mf_gru_gates(const float *inputs, int64_t ldi, const float *hidden, int64_t ldh,
                  const float *hx, int64_t ldx, float *out, int64_t ldo, int64_t n, int64_t width,
                  void *stream) {

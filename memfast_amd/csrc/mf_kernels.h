@@ -287,6 +287,8 @@ __global__ void k_gru_gates(const float *inputs, i64 ldi, const float *hidden, i
                             const float *bias, u32 *status, u32 flag);
 __global__ void k_bias_add(float *out, i64 n, i64 o, i64 ldo, const float *bias, u32 *status,
                            u32 flag);
+__global__ void k_narrow_f64(const double *in, i64 n, i64 cols, i64 ld, float *out, u32 *status,
+                             u32 flag);
 
 // One GRU step after its hidden read (recurrent.hip): the read's restore and read-order sum
 // from split totals (or its fused output), the gate equations of k_gru_gates, and the

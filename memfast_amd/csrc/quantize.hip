@@ -27,6 +27,21 @@ __global__ void k_bias_add(float *out, i64 n, i64 o, i64 ldo, const float *bias,
     if (!finite && status) atomicOr(status, flag);
 }
 
+// out[v, c] = float(in[v * ld + c]) for c < cols (round to nearest even, as torch's cast
+// of an FP64 tensor to FP32), flagging a non-finite result in the status word.
+__global__ void k_narrow_f64(const double *in, i64 n, i64 cols, i64 ld, float *out, u32 *status,
+                             u32 flag) {
+    bool finite = true;
+    for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < n * cols;
+         i += i64(gridDim.x) * blockDim.x) {
+        const i64 v = i / cols, c = i - v * cols;
+        const float f = float(in[v * ld + c]);
+        out[i] = f;
+        finite = finite && fabsf(f) <= FLT_MAX;
+    }
+    if (!finite && status) atomicOr(status, flag);
+}
+
 __global__ void k_fill_u32(u32 *p, i64 count, u32 value) {
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
          i += i64(gridDim.x) * blockDim.x)

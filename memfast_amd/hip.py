@@ -151,6 +151,7 @@ SIGNATURES = {
                           _P, _P, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _P], ct.c_int),
     "mf_status_wait": ([_P, _I64, ct.POINTER(ct.c_uint32), ct.POINTER(_I32)], ct.c_int),
     "mf_status_publish": ([_P, _P, _P], ct.c_int),
+    "mf_narrow_output": ([_P, _I64, _I64, _I64, _P, _P, _P], ct.c_int),
     "mf_mm_static": ([_CFG, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, ct.c_uint32,
                       ct.c_uint64, _P, _I64, _I32, _P, _P], ct.c_int),
     "mf_mm_totals": ([_CFG, _P, _I64, _I64, _P, _I64, _P, ct.c_uint32, ct.c_uint64, _P, _P, _I64,
@@ -414,6 +415,21 @@ def status_word(device):
 def mailbox():
     """A pinned host word for ``mm_from_float`` to publish its quantizers' status bits into."""
     return torch.zeros(1, dtype=torch.int32, pin_memory=True)
+
+
+def narrow_output(output, cols, status):
+    """FP32 copy [n, cols] of a wide read's FP64 output [n, >= cols] (mf_narrow_output):
+    torch's cast, with a non-finite result flagged as STATUS_OUTPUT in ``status``."""
+    if output.dtype != torch.float64 or output.dim() != 2 or output.stride(1) != 1:
+        raise ValueError("narrow_output takes a row-major FP64 matrix")
+    n = output.shape[0]
+    out = torch.empty((n, cols), dtype=torch.float32, device=output.device)
+    if n and cols:
+        with _on(output.device):
+            check(library().mf_narrow_output(_ptr(output), n, cols, output.stride(0), _ptr(out),
+                                             _ptr(status), _stream(output.device)),
+                  "output cast")
+    return out
 
 
 def status_publish(status, box):

@@ -342,6 +342,10 @@ class Simulator:
             output = hip.mm(q, xscale, packed, codes_t, wscale.reshape(-1, p * config.array_size[1]),
                             config, config.seed ^ _name_tag(name), event,
                             variant=tuning.DEFAULT_VARIANT, status=status, out_cols=o, k_rows=k)
+            if config.wide and x.dtype == torch.float32:
+                # The cast to FP32 flags a non-finite result in the status word, so the one
+                # status read below also stands for the host scan of the cast output.
+                output = hip.narrow_output(output, o, status)
         return int(status.item()), tiles, q, xscale, output, kept, fused, event
 
     def _launch_from_float(self, x, rhs, owner, index, status):
@@ -671,7 +675,7 @@ class AnalogMatrix(nn.Module):
         return term
 
     def _execute_checked(self, q, xscale, schedule, event, stable=False, status=None,
-                         input_error=None, retry=True, defer=False):
+                         input_error=None, retry=True, defer=False, narrow=False):
         """(output, finite) where ``finite`` is True when the output is known finite.
 
         ``status`` may carry STATUS_INPUT from a deferred input quantization; the one
@@ -679,7 +683,9 @@ class AnalogMatrix(nn.Module):
         False, a non-finite FP32 result returns (None, False) instead of the FP64 retry
         (which changes every row's rounding).  With ``defer`` the status word is not
         read: the FP32 output returns as it is and the caller reads ``status`` later
-        (``_forward_deferred``)."""
+        (``_forward_deferred``).  With ``narrow`` a wide read's FP64 output returns cast to
+        FP32 on the device, its non-finite values flagged in the status word
+        (hip.narrow_output), so that the caller's FP32 output needs no host scan."""
         config = self.config
         columns = self.p * config.array_size[1]
         packed = self.packed
@@ -722,6 +728,9 @@ class AnalogMatrix(nn.Module):
             hip.bias_add(output, self.bias, status)
         if defer:
             return output, True
+        narrowed = narrow and config.wide
+        if narrowed:
+            output = hip.narrow_output(output, self.out_features, status)
         if box is not None:
             flags = hip.status_wait(box)
             if flags is not None and flags & hip.STATUS_INPUT:
@@ -732,7 +741,8 @@ class AnalogMatrix(nn.Module):
         if flags & hip.STATUS_INPUT:
             raise ValueError(input_error or "quantized values must be finite")
         flagged = bool(flags & hip.STATUS_OUTPUT)
-        host_scan = self.zero_correction is not None or (config.wide and self.bias is not None)
+        host_scan = not narrowed and (self.zero_correction is not None or
+                                      (config.wide and self.bias is not None))
         finite = bool(torch.isfinite(output).all()) if host_scan else not flagged
         if finite or config.wide:
             # A wide read is already an FP64 restore; the reference's retry
@@ -873,7 +883,8 @@ class AnalogMatrix(nn.Module):
             schedule = self._prepared[key]
         output, finite = self._execute_checked(
             q, xscale, schedule, event, status=status,
-            input_error=hip.input_error(self.config, self.input_scale), retry=retry)
+            input_error=hip.input_error(self.config, self.input_scale), retry=retry,
+            narrow=x.dtype == torch.float32)
         return None if output is None else self._finish(x, output, finite)
 
     def _finish(self, x, output, finite):

@@ -742,6 +742,46 @@ def test_fp32_overflow_retries_in_fp64(hip_device):
         sim.mm(a.float().to(hip_device), b.float().to(hip_device))
 
 
+@pytest.mark.parametrize("name", ["int12_ideal", "bfp16_int4"])
+def test_wide_product_cast_flags_nonfinite_outputs(hip_device, name):
+    """A wide product of FP32 operands casts its FP64 restore to FP32 on the device
+    (mf_narrow_output) and flags a non-finite result in the status word: the outputs equal
+    torch's cast of the same product of the FP64 operands bit for bit, and a cast that
+    overflows raises FloatingPointError (memfast/simulator.py:642-644) where the FP64
+    product stays finite.  Layer reads of FP32 inputs cast the same way."""
+    from memfast_amd import Simulator
+
+    cfg = wide_case(name)
+    gen = torch.Generator().manual_seed(48)
+    a = torch.randn(37, 150, generator=gen)
+    b = torch.randn(150, 70, generator=gen)
+    got = Simulator(cfg, device=hip_device).mm(a.to(hip_device), b.to(hip_device))
+    wide = Simulator(cfg, device=hip_device).mm(a.double().to(hip_device),
+                                                 b.double().to(hip_device))
+    assert got.dtype == torch.float32 and wide.dtype == torch.float64
+    assert bits_equal(got, wide.float())
+    big_a, big_b = (a * 1e30).to(hip_device), (b * 1e30).to(hip_device)
+    sim = Simulator(cfg, device=hip_device)
+    assert torch.isfinite(sim.mm(big_a.double(), big_b.double())).all()
+    with pytest.raises(FloatingPointError):
+        sim.mm(big_a, big_b)
+    again = sim.mm(a.to(hip_device), b.to(hip_device))
+    # (noise is keyed by the program's name and event, which the earlier calls moved on)
+    assert torch.isfinite(again).all() and (name != "int12_ideal" or bits_equal(again, got))
+    # A layer read (bias included) casts the same way.
+    from torch import nn
+
+    from memfast_amd.nn import AnalogLinear
+
+    source = nn.Linear(150, 70).to(hip_device)
+    layers = [AnalogLinear(source, Simulator(cfg, device=hip_device), name="cast")
+              for _ in range(2)]
+    x = a.to(hip_device)
+    with torch.no_grad():
+        narrow, full = layers[0](x), layers[1](x.double())
+    assert narrow.dtype == torch.float32 and bits_equal(narrow, full.float())
+
+
 @pytest.mark.parametrize("groups,width,c", [(5, 1, 4), (17, 2, 12), (128, 2, 128), (300, 1, 36),
                                             (40, 2, 4)])
 def test_stable_sum_matches_cpu_restore(hip_device, groups, width, c):
