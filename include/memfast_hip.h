@@ -378,6 +378,12 @@ int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t 
 int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k,
                             int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
                             uint32_t *q, double *xscale, uint32_t *status, void *stream);
+/* The same quantization of FP32 activations (memfast/quantization.py:9-31 takes them in
+ * FP64): each value is widened exactly as it is read, so the codes and scales are those
+ * of the FP64 copy, which the caller need not make. */
+int mf_quantize_inputs_wide_f32(const mf_config *cfg, const float *x, int64_t n, int64_t k,
+                                int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                                uint32_t *q, double *xscale, uint32_t *status, void *stream);
 /* Fixed-scale input tiles (scale [k]). */
 int mf_input_tiles_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k, int64_t ld,
                         const double *scale, uint32_t *q, double *xscale, void *stream);
@@ -399,6 +405,11 @@ int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, i
                              int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
                              int64_t *packed, uint32_t *packed32, double *wscale, uint32_t *status,
                              void *stream);
+/* The same programming of FP32 weights, widened exactly as they are read. */
+int mf_quantize_weights_wide_f32(const mf_config *cfg, const float *b, int64_t k, int64_t o,
+                                 int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                                 int64_t *packed, uint32_t *packed32, double *wscale,
+                                 uint32_t *status, void *stream);
 /* mf_restore, mf_partial and mf_mm for wide codes (totals and outputs FP64;
  * the fused read restores with restore_scales in FP64 and sums in torch's
  * FP64 order).  mf_mm_wide uses the noisy-device fp16 MFMA read (conductance

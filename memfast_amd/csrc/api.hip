@@ -1950,38 +1950,46 @@ int mf_stable_sum(const mf_config *cfg, const float *totals, int64_t n, int64_t 
     return check_launch("stable sum");
 }
 
-// Group maxima |x| of an FP64 matrix into work[row group][col group] (cleared).
-static void launch_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
+}  // extern "C"
+
+// Group maxima |x| of an FP64 matrix (S = float: FP32 values, widened exactly) into
+// work[row group][col group] (cleared).
+template <typename S>
+static void launch_group_max_f64(const S *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
                                  i64 ncg, u64 *work, u32 *status, u32 flag, hipStream_t s) {
+    constexpr int V = 16 / sizeof(S);   // columns per lane of the vector path
     const i64 chunks = (rows + COL_CHUNK_ROWS - 1) / COL_CHUNK_ROWS;
     const i64 row_chunks = (cols + ROW_CHUNK_COLS - 1) / ROW_CHUNK_COLS;
     unsigned long long *w = reinterpret_cast<unsigned long long *>(work);
-    const bool vec_ok = cols % 2 == 0 && ld % 2 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    const bool vec_ok = cols % V == 0 && ld % V == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
     if (gr == 1 && gc >= 64 && (rows + 3) / 4 <= 65535 && row_chunks <= 2147483647) {
-        hipLaunchKernelGGL((k_row_group_max<double, unsigned long long>),
+        hipLaunchKernelGGL((k_row_group_max<double, unsigned long long, S>),
                            dim3(unsigned(row_chunks), unsigned((rows + 3) / 4)), dim3(256), 0, s, x,
                            rows, cols, ld, gc, ncg, w, status, flag);
-    } else if ((gr > 1 || gc == 1) && vec_ok && (cols + 63) / 64 <= 2147483647 &&
+    } else if ((gr > 1 || gc == 1) && vec_ok && (cols + 64 * V - 1) / (64 * V) <= 2147483647 &&
                (rows + COL_CHUNK_ROWS_VEC - 1) / COL_CHUNK_ROWS_VEC <= 65535) {
-        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long, 2>),
-                           dim3(unsigned((cols + 127) / 128),
+        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long, V, S>),
+                           dim3(unsigned((cols + 64 * V - 1) / (64 * V)),
                                 unsigned((rows + COL_CHUNK_ROWS_VEC - 1) / COL_CHUNK_ROWS_VEC)),
                            dim3(256), 0, s, x, rows, cols, ld, gr, gc, ncg, i64(COL_CHUNK_ROWS_VEC),
                            w, status, flag);
     } else if ((gr > 1 || gc == 1) && (cols + 63) / 64 <= 2147483647 && chunks <= 65535) {
-        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long, 1>),
+        hipLaunchKernelGGL((k_col_group_max<double, unsigned long long, 1, S>),
                            dim3(unsigned((cols + 63) / 64), unsigned(chunks)), dim3(256), 0, s, x,
                            rows, cols, ld, gr, gc, ncg, i64(COL_CHUNK_ROWS), w, status, flag);
     } else {
-        hipLaunchKernelGGL(k_group_max_f64, dim3(grid_for(rows * cols)), dim3(256), 0, s, x, rows,
-                           cols, ld, gr, gc, ncg, work, status, flag);
+        hipLaunchKernelGGL(k_group_max_f64<S>, dim3(grid_for(rows * cols)), dim3(256), 0, s, x,
+                           rows, cols, ld, gr, gc, ncg, work, status, flag);
     }
 }
 
 // ---- wide configurations (u32 codes, FP64 scales and outputs) -------------
-int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k,
-                            int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
-                            uint32_t *q, double *xscale, uint32_t *status, void *stream) {
+// The wide quantizers over FP64 operands, or FP32 ones (S = float) widened exactly as they
+// are read, which gives the codes and scales of the FP64 copy without making it.
+template <typename S>
+static int quantize_inputs_wide(const mf_config *cfg, const S *x, int64_t n, int64_t k,
+                                int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                                uint32_t *q, double *xscale, uint32_t *status, void *stream) {
     const int valid = check_wide(cfg);
     if (valid) return valid;
     if (!x || !work || !scale || !q || !xscale || n < 1 || k < 1 || ld < k || gr < 1 || gc < 1)
@@ -2002,37 +2010,18 @@ int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, in
     const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
                        nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
-    hipLaunchKernelGGL(k_input_codes_f64, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
-                       scale, gr, gc, ncg, 0, lower, upper, mask, narrow, q);
+    hipLaunchKernelGGL(k_input_codes_f64<S>, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld,
+                       kp, scale, gr, gc, ncg, 0, lower, upper, mask, narrow, q);
     hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
                        m * Gr, R, P, Gr, scale, gr, gc, ncg, 0, xscale);
     return check_launch("wide input quantization");
 }
 
-int mf_input_tiles_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k, int64_t ld,
-                        const double *scale, uint32_t *q, double *xscale, void *stream) {
-    const int valid = check_wide(cfg);
-    if (valid) return valid;
-    if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k)
-        return fail(MF_E_INVALID, "invalid input-tile arguments");
-    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
-    const i64 m = (k + R - 1) / R, kp = m * R;
-    const int bits = cfg->activation_bits;
-    const double upper = double((i64(1) << (bits - 1)) - 1);
-    const double lower = cfg->bw_e ? -double(i64(1) << (bits - 1)) : -upper;
-    const u64 mask = (u64(1) << bits) - 1;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(k_input_codes_f64, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
-                       scale, i64(1), i64(1), k, 1, lower, upper, mask, 0, q);
-    hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
-                       m * Gr, R, P, Gr, scale, i64(1), i64(1), k, 1, xscale);
-    return check_launch("wide input tiles");
-}
-
-int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, int64_t o,
-                             int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
-                             int64_t *packed, uint32_t *packed32, double *wscale, uint32_t *status,
-                             void *stream) {
+template <typename S>
+static int quantize_weights_wide(const mf_config *cfg, const S *b, int64_t k, int64_t o,
+                                 int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                                 int64_t *packed, uint32_t *packed32, double *wscale,
+                                 uint32_t *status, void *stream) {
     const int valid = check_wide(cfg);
     if (valid) return valid;
     if (!b || !work || !scale || !packed || !packed32 || !wscale || k < 1 || o < 1 || ld < o ||
@@ -2055,11 +2044,62 @@ int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, i
     const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
                        nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
-    hipLaunchKernelGGL(k_weight_codes_f64, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o, ld, R,
-                       C, m, p, scale, gr, gc, ncg, lower, upper, mask, narrow, packed, packed32);
+    hipLaunchKernelGGL(k_weight_codes_f64<S>, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o,
+                       ld, R, C, m, p, scale, gr, gc, ncg, lower, upper, mask, narrow, packed,
+                       packed32);
     hipLaunchKernelGGL(k_weight_scales_f64, dim3(grid_for(m * Gr * op)), dim3(256), 0, s, k, o,
                        m * Gr, op, R, P, Gr, scale, gr, gc, ncg, wscale);
     return check_launch("wide weight quantization");
+}
+
+extern "C" {
+
+int mf_quantize_inputs_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k,
+                            int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                            uint32_t *q, double *xscale, uint32_t *status, void *stream) {
+    return quantize_inputs_wide(cfg, x, n, k, ld, gr, gc, work, scale, q, xscale, status, stream);
+}
+
+int mf_quantize_inputs_wide_f32(const mf_config *cfg, const float *x, int64_t n, int64_t k,
+                                int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                                uint32_t *q, double *xscale, uint32_t *status, void *stream) {
+    return quantize_inputs_wide(cfg, x, n, k, ld, gr, gc, work, scale, q, xscale, status, stream);
+}
+
+int mf_input_tiles_wide(const mf_config *cfg, const double *x, int64_t n, int64_t k, int64_t ld,
+                        const double *scale, uint32_t *q, double *xscale, void *stream) {
+    const int valid = check_wide(cfg);
+    if (valid) return valid;
+    if (!x || !scale || !q || !xscale || n < 1 || k < 1 || ld < k)
+        return fail(MF_E_INVALID, "invalid input-tile arguments");
+    const int R = cfg->rows, P = cfg->read_rows, Gr = cfg->reads;
+    const i64 m = (k + R - 1) / R, kp = m * R;
+    const int bits = cfg->activation_bits;
+    const double upper = double((i64(1) << (bits - 1)) - 1);
+    const double lower = cfg->bw_e ? -double(i64(1) << (bits - 1)) : -upper;
+    const u64 mask = (u64(1) << bits) - 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(k_input_codes_f64<double>, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld, kp,
+                       scale, i64(1), i64(1), k, 1, lower, upper, mask, 0, q);
+    hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
+                       m * Gr, R, P, Gr, scale, i64(1), i64(1), k, 1, xscale);
+    return check_launch("wide input tiles");
+}
+
+int mf_quantize_weights_wide(const mf_config *cfg, const double *b, int64_t k, int64_t o,
+                             int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                             int64_t *packed, uint32_t *packed32, double *wscale, uint32_t *status,
+                             void *stream) {
+    return quantize_weights_wide(cfg, b, k, o, ld, gr, gc, work, scale, packed, packed32, wscale,
+                                 status, stream);
+}
+
+int mf_quantize_weights_wide_f32(const mf_config *cfg, const float *b, int64_t k, int64_t o,
+                                 int64_t ld, int64_t gr, int64_t gc, uint64_t *work, double *scale,
+                                 int64_t *packed, uint32_t *packed32, double *wscale,
+                                 uint32_t *status, void *stream) {
+    return quantize_weights_wide(cfg, b, k, o, ld, gr, gc, work, scale, packed, packed32, wscale,
+                                 status, stream);
 }
 
 int mf_restore_wide(const mf_config *cfg, const uint32_t *packed, int64_t m, int64_t p,

@@ -386,28 +386,31 @@ __global__ void k_col_codes(const float *b, i64 k, i64 o, i64 ld, i64 gr, i64 sp
                             i64 m, i64 p, const float *scale, float lower, float upper, u32 mask,
                             u8 *packed, u8 *packed_t);
 __global__ void k_transpose_packed(const u8 *packed, int R, int C, i64 m, i64 p, u8 *packed_t);
-__global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
+template <typename S>
+__global__ void k_group_max_f64(const S *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
                                 i64 ncg, u64 *work, u32 *status, u32 flag);
 // Group maxima of |x| as bit patterns (U = u32 for float, unsigned long long for
 // double): reduced along rows first (any gr, gc; V adjacent columns per lane),
-// or along a row (gr == 1).
-template <typename T, typename U, int V>
-__global__ void k_col_group_max(const T *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,
+// or along a row (gr == 1).  S is the stored type (float values widened to T = double).
+template <typename T, typename U, int V, typename S = T>
+__global__ void k_col_group_max(const S *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc, i64 ncg,
                                 i64 chunk, U *work, u32 *status, u32 flag);
 constexpr int COL_CHUNK_ROWS = 256;   // rows per k_col_group_max block, one column per lane
 constexpr int COL_CHUNK_ROWS_VEC = 64;  // rows per block, 16 bytes of columns per lane
-template <typename T, typename U>
-__global__ void k_row_group_max(const T *x, i64 rows, i64 cols, i64 ld, i64 gc, i64 ncg, U *work,
+template <typename T, typename U, typename S = T>
+__global__ void k_row_group_max(const S *x, i64 rows, i64 cols, i64 ld, i64 gc, i64 ncg, U *work,
                                 u32 *status, u32 flag);
 constexpr int ROW_CHUNK_COLS = 1024;  // columns per k_row_group_max wave
 // `narrow`: an INT operand of at most 8 bits in a wide configuration, quantized in FP32 as
 // the reference does (its dtype follows the operand's own width).
 __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
                                   int narrow, double *scale);
-__global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
+template <typename S>
+__global__ void k_input_codes_f64(const S *x, i64 n, i64 k, i64 ld, i64 kp,
                                   const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
                                   double lower, double upper, u64 mask, int narrow, u32 *q);
-__global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+template <typename S>
+__global__ void k_weight_codes_f64(const S *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
                                    i64 p, const double *scale, i64 gr, i64 gc, i64 ncg,
                                    double lower, double upper, u64 mask, int narrow, i64 *packed,
                                    u32 *packed32);

@@ -1018,15 +1018,17 @@ __global__ void k_transpose_packed(const u8 *packed, int R, int C, i64 m, i64 p,
 // ---------------------------------------------------------------------------
 namespace mf {
 
-// Group max |x| of FP64 values via atomicMax on the bit pattern.
-__global__ void k_group_max_f64(const double *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
+// Group max |x| of FP64 values (S = float: FP32 values, widened exactly) via atomicMax on
+// the bit pattern.
+template <typename S>
+__global__ void k_group_max_f64(const S *x, i64 rows, i64 cols, i64 ld, i64 gr, i64 gc,
                                 i64 ncg, u64 *work, u32 *status, u32 flag) {
     const i64 total = rows * cols;
     bool finite = true;
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += i64(gridDim.x) * blockDim.x) {
         const i64 r = i / cols, c = i - r * cols;
-        const double v = fabs(x[r * ld + c]);
+        const double v = fabs(double(x[r * ld + c]));
         finite = finite && v <= DBL_MAX;
         const u64 bits = u64(__double_as_longlong(v));
         if (bits) atomicMax(reinterpret_cast<unsigned long long *>(&work[(r / gr) * ncg + c / gc]),
@@ -1059,12 +1061,14 @@ template <> struct AbsBits<double> {
 // when all its columns lie in one group, else a shuffle maximum over aligned
 // segments of `seg` columns (the largest power of two dividing gc, at most 64:
 // such a segment never crosses a group boundary) and one atomicMax per
-// segment.  work [ceil(rows/gr), ncg].
+// segment.  work [ceil(rows/gr), ncg].  S: the stored type (FP32 values widened exactly to
+// T = double for the wide quantizers' FP32 operands).
 template <typename T> struct __align__(16) Vec16 { T e[16 / sizeof(T)]; };
-template <typename T, typename U, int V>
-__global__ __launch_bounds__(256) void k_col_group_max(const T *x, i64 rows, i64 cols, i64 ld,
+template <typename T, typename U, int V, typename S>
+__global__ __launch_bounds__(256) void k_col_group_max(const S *x, i64 rows, i64 cols, i64 ld,
                                                        i64 gr, i64 gc, i64 ncg, i64 chunk,
                                                        U *work, u32 *status, u32 flag) {
+    static_assert(V == 1 || V * sizeof(S) == 16, "V columns per lane fill one 16-byte load");
     constexpr int BC = 64 * V;   // columns per block
     __shared__ U part[4][BC];
     __shared__ U wave_max[4];
@@ -1089,18 +1093,18 @@ __global__ __launch_bounds__(256) void k_col_group_max(const T *x, i64 rows, i64
             i64 r = lo + ty;
             // Four rows per step: independent loads in flight.
             for (; r + 12 < hi; r += 16) {
-                Vec16<T> v[4];
-                T w[4];
+                Vec16<S> v[4];
+                S w[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    if (V > 1) v[u] = *reinterpret_cast<const Vec16<T> *>(x + (r + 4 * u) * ld + c);
+                    if (V > 1) v[u] = *reinterpret_cast<const Vec16<S> *>(x + (r + 4 * u) * ld + c);
                     else w[u] = x[(r + 4 * u) * ld + c];
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
 #pragma unroll
                     for (int j = 0; j < V; ++j) {
-                        const T a = fabs(V > 1 ? v[u].e[j] : w[u]);
+                        const T a = fabs(T(V > 1 ? v[u].e[j] : w[u]));
                         finite = finite && a <= AbsBits<T>::LARGEST;
                         const U bits = U(AbsBits<T>::of(a));
                         best[j] = bits > best[j] ? bits : best[j];
@@ -1108,13 +1112,13 @@ __global__ __launch_bounds__(256) void k_col_group_max(const T *x, i64 rows, i64
                 }
             }
             for (; r < hi; r += 4) {
-                Vec16<T> v;
-                T w = 0;
-                if (V > 1) v = *reinterpret_cast<const Vec16<T> *>(x + r * ld + c);
+                Vec16<S> v;
+                S w = 0;
+                if (V > 1) v = *reinterpret_cast<const Vec16<S> *>(x + r * ld + c);
                 else w = x[r * ld + c];
 #pragma unroll
                 for (int j = 0; j < V; ++j) {
-                    const T a = fabs(V > 1 ? v.e[j] : w);
+                    const T a = fabs(T(V > 1 ? v.e[j] : w));
                     finite = finite && a <= AbsBits<T>::LARGEST;
                     const U bits = U(AbsBits<T>::of(a));
                     best[j] = bits > best[j] ? bits : best[j];
@@ -1166,8 +1170,8 @@ __global__ __launch_bounds__(256) void k_col_group_max(const T *x, i64 rows, i64
 // columns (coalesced); per group in the chunk a lane maximum, a wave maximum by
 // shuffles, and one atomicMax per (row, group, chunk).  work [rows, ncg].
 constexpr int ROW_CHUNK = ROW_CHUNK_COLS;
-template <typename T, typename U>
-__global__ __launch_bounds__(256) void k_row_group_max(const T *x, i64 rows, i64 cols, i64 ld,
+template <typename T, typename U, typename S>
+__global__ __launch_bounds__(256) void k_row_group_max(const S *x, i64 rows, i64 cols, i64 ld,
                                                        i64 gc, i64 ncg, U *work, u32 *status,
                                                        u32 flag) {
     const int lane = threadIdx.x & 63;
@@ -1175,14 +1179,14 @@ __global__ __launch_bounds__(256) void k_row_group_max(const T *x, i64 rows, i64
     const i64 c0 = i64(blockIdx.x) * ROW_CHUNK;
     if (row >= rows) return;
     const i64 c1 = (c0 + ROW_CHUNK) < cols ? (c0 + ROW_CHUNK) : cols;
-    const T *src = x + row * ld;
+    const S *src = x + row * ld;
     bool finite = true;
     for (i64 g = c0 / gc; g * gc < c1; ++g) {
         const i64 lo = (g * gc) > c0 ? (g * gc) : c0;
         const i64 hi = ((g + 1) * gc) < c1 ? ((g + 1) * gc) : c1;
         U best = 0;
         for (i64 c = lo + lane; c < hi; c += 64) {
-            const T v = fabs(src[c]);
+            const T v = fabs(T(src[c]));
             finite = finite && v <= AbsBits<T>::LARGEST;
             const U bits = U(AbsBits<T>::of(v));
             best = bits > best ? bits : best;
@@ -1197,20 +1201,29 @@ __global__ __launch_bounds__(256) void k_row_group_max(const T *x, i64 rows, i64
     if (!finite && status) atomicOr(status, flag);
 }
 
-template __global__ void k_col_group_max<float, u32, 1>(const float *, i64, i64, i64, i64, i64,
-                                                        i64, i64, u32 *, u32 *, u32);
-template __global__ void k_col_group_max<float, u32, 4>(const float *, i64, i64, i64, i64, i64,
-                                                        i64, i64, u32 *, u32 *, u32);
-template __global__ void k_col_group_max<double, unsigned long long, 1>(
-    const double *, i64, i64, i64, i64, i64, i64, i64, unsigned long long *, u32 *, u32);
-template __global__ void k_col_group_max<double, unsigned long long, 2>(
-    const double *, i64, i64, i64, i64, i64, i64, i64, unsigned long long *, u32 *, u32);
-template __global__ void k_row_group_max<float, u32>(const float *, i64, i64, i64, i64, i64, u32 *,
-                                                     u32 *, u32);
-template __global__ void k_row_group_max<double, unsigned long long>(const double *, i64, i64, i64,
-                                                                     i64, i64,
-                                                                     unsigned long long *, u32 *,
-                                                                     u32);
+typedef unsigned long long ull;
+template __global__ void k_col_group_max<float, u32, 1, float>(const float *, i64, i64, i64, i64,
+                                                               i64, i64, i64, u32 *, u32 *, u32);
+template __global__ void k_col_group_max<float, u32, 4, float>(const float *, i64, i64, i64, i64,
+                                                               i64, i64, i64, u32 *, u32 *, u32);
+template __global__ void k_col_group_max<double, ull, 1, double>(const double *, i64, i64, i64, i64,
+                                                                 i64, i64, i64, ull *, u32 *, u32);
+template __global__ void k_col_group_max<double, ull, 2, double>(const double *, i64, i64, i64, i64,
+                                                                 i64, i64, i64, ull *, u32 *, u32);
+template __global__ void k_col_group_max<double, ull, 1, float>(const float *, i64, i64, i64, i64,
+                                                                i64, i64, i64, ull *, u32 *, u32);
+template __global__ void k_col_group_max<double, ull, 4, float>(const float *, i64, i64, i64, i64,
+                                                                i64, i64, i64, ull *, u32 *, u32);
+template __global__ void k_row_group_max<float, u32, float>(const float *, i64, i64, i64, i64, i64,
+                                                            u32 *, u32 *, u32);
+template __global__ void k_row_group_max<double, ull, double>(const double *, i64, i64, i64, i64,
+                                                              i64, ull *, u32 *, u32);
+template __global__ void k_row_group_max<double, ull, float>(const float *, i64, i64, i64, i64,
+                                                             i64, ull *, u32 *, u32);
+template __global__ void k_group_max_f64<double>(const double *, i64, i64, i64, i64, i64, i64,
+                                                 u64 *, u32 *, u32);
+template __global__ void k_group_max_f64<float>(const float *, i64, i64, i64, i64, i64, i64, u64 *,
+                                                u32 *, u32);
 
 // floor() of the correctly rounded log2(x) for normal x > 0: ilogb(x), or one
 // more when log2(x) lies within half a unit in the last place below the next
@@ -1263,7 +1276,8 @@ __device__ __forceinline__ u32 quantize_code_f64(double x, double s, double lowe
 }
 
 // q [n, kp] u32 codes; `scale` is the group grid, or a [k] row when fixed.
-__global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
+template <typename S>
+__global__ void k_input_codes_f64(const S *x, i64 n, i64 k, i64 ld, i64 kp,
                                   const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,
                                   double lower, double upper, u64 mask, int narrow, u32 *q) {
     const i64 total = n * kp;
@@ -1273,14 +1287,15 @@ __global__ void k_input_codes_f64(const double *x, i64 n, i64 k, i64 ld, i64 kp,
         u32 code = 0;
         if (col < k) {
             const double s = fixed ? scale[col] : scale[(row / gr) * ncg + col / gc];
-            code = quantize_code_f64(x[row * ld + col], s, lower, upper, mask, narrow);
+            code = quantize_code_f64(double(x[row * ld + col]), s, lower, upper, mask, narrow);
         }
         q[i] = code;
     }
 }
 
 // packed [m, p, R, C] as int64 (the checkpoint layout) and u32 (kernel copy).
-__global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
+template <typename S>
+__global__ void k_weight_codes_f64(const S *b, i64 k, i64 o, i64 ld, int R, int C, i64 m,
                                    i64 p, const double *scale, i64 gr, i64 gc, i64 ncg,
                                    double lower, double upper, u64 mask, int narrow, i64 *packed,
                                    u32 *packed32) {
@@ -1296,12 +1311,23 @@ __global__ void k_weight_codes_f64(const double *b, i64 k, i64 o, i64 ld, int R,
         const i64 row = i * R + r, col = t * C + c;
         u32 code = 0;
         if (row < k && col < o)
-            code = quantize_code_f64(b[row * ld + col], scale[(row / gr) * ncg + col / gc], lower,
+            code = quantize_code_f64(double(b[row * ld + col]), scale[(row / gr) * ncg + col / gc], lower,
                                      upper, mask, narrow);
         packed[idx] = i64(code);
         packed32[idx] = code;
     }
 }
+
+#define MF_CODES_F64_INST(S)                                                                   \
+    template __global__ void k_input_codes_f64<S>(const S *, i64, i64, i64, i64, const double *,  \
+                                                  i64, i64, i64, int, double, double, u64, int,  \
+                                                  u32 *);                                        \
+    template __global__ void k_weight_codes_f64<S>(const S *, i64, i64, i64, int, int, i64, i64, \
+                                                   const double *, i64, i64, i64, double, double, \
+                                                   u64, int, i64 *, u32 *);
+MF_CODES_F64_INST(double)
+MF_CODES_F64_INST(float)
+#undef MF_CODES_F64_INST
 
 // Per-read scales gathered at each read's first row, replicate-padded
 // (memfast/quantization.py:76-79, :104-111, :133-136), for FP64 scales.

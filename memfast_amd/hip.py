@@ -164,11 +164,15 @@ SIGNATURES = {
     "mf_stable_sum": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P], ct.c_int),
     "mf_quantize_inputs_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                  _P], ct.c_int),
+    "mf_quantize_inputs_wide_f32": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
+                                     _P, _P], ct.c_int),
     "mf_input_tiles_wide": ([_CFG, _P, _I64, _I64, _I64, _P, _P, _P, _P], ct.c_int),
     "mf_conv_input_tiles_wide": ([_CFG, _P, ct.POINTER(MFConvGeometry), _P, _I64, _I64, _P, _P,
                                   _P, _P, _P, _P], ct.c_int),
     "mf_quantize_weights_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P,
                                   _P, _P], ct.c_int),
+    "mf_quantize_weights_wide_f32": ([_CFG, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
+                                      _P, _P, _P], ct.c_int),
     "mf_restore_wide": ([_CFG, _P, _I64, _I64, _I64, _I64, ct.c_uint32, ct.c_uint64, _P, _P],
                         ct.c_int),
     "mf_partial_wide": ([_CFG, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, ct.c_uint32, ct.c_uint64,
@@ -566,7 +570,9 @@ def conv_input_tiles(x, config, geometry, fixed_scale=None, *, status=None):
 def _input_tiles_wide(value, config, fixed_scale, status):
     """Wide input tiles: q [N, m, R] uint32 codes (int32 storage), FP64 scales [N, m*Gr]."""
     n, k = value.shape
-    x = value.to(torch.float64).contiguous()
+    # FP32 activations are widened inside the dynamic quantizer as it reads them.
+    fp32 = value.dtype == torch.float32 and fixed_scale is None
+    x = value.contiguous() if fp32 else value.to(torch.float64).contiguous()
     if status is None and not torch.isfinite(x).all():
         raise ValueError(input_error(config, fixed_scale))
     r = config.array_size[0]
@@ -580,8 +586,10 @@ def _input_tiles_wide(value, config, fixed_scale, status):
             grid = (math.ceil(n / gr), math.ceil(k / gc))
             scale = torch.empty(grid, dtype=torch.float64, device=value.device)
             work = torch.empty(grid, dtype=torch.int64, device=value.device)
+            quantize = (library().mf_quantize_inputs_wide_f32 if fp32
+                        else library().mf_quantize_inputs_wide)
             check(
-                library().mf_quantize_inputs_wide(
+                quantize(
                     descr, _ptr(x), n, k, k, gr, gc, _ptr(work), _ptr(scale), _ptr(q),
                     _ptr(xscale), _ptr(status), _stream(value.device),
                 ),
@@ -660,7 +668,10 @@ def weight_tiles(weight, config, *, transposed=True, status=None):
 def _weight_tiles_wide(weight, config, status):
     """Wide programming: packed int64 [m,p,R,C], its uint32 kernel copy, FP64 scales."""
     o, k = weight.shape
-    b = weight.detach().T.to(torch.float64).contiguous()  # [K, O]
+    # [K, O]; FP32 weights are widened inside the quantizer as it reads them.
+    source = weight.detach().T
+    fp32 = source.dtype == torch.float32
+    b = source.contiguous() if fp32 else source.to(torch.float64).contiguous()
     if status is None and not torch.isfinite(b).all():
         # The reference quantizes an INT operand of at most 8 bits in FP32 (per operand).
         narrow = config.weight_bits <= 8 and config.bw_e is None
@@ -679,7 +690,8 @@ def _weight_tiles_wide(weight, config, status):
     wscale = torch.empty((m * config.reads_per_array, p, c), dtype=torch.float64, device=device)
     with _on(device):
         check(
-            library().mf_quantize_weights_wide(
+            (library().mf_quantize_weights_wide_f32 if fp32
+             else library().mf_quantize_weights_wide)(
                 ct.byref(descriptor(config)), _ptr(b), k, o, o, gr, gc, _ptr(work), _ptr(scale),
                 _ptr(packed), _ptr(packed32), _ptr(wscale), _ptr(status), _stream(device),
             ),

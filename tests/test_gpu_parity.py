@@ -1468,17 +1468,19 @@ WIDE_GROUPS = [((None, 1), (1, None)), ((64, 1), (1, 64)), ((192, 1), (1, 192)),
                ((320, 1), (1, 1088)), ((64, 3), (2, 64))]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["f32", "f64"])
 @pytest.mark.parametrize("wgran,igran", WIDE_GROUPS, ids=[f"{w}-{i}" for w, i in WIDE_GROUPS])
-def test_wide_group_quantizers_bit_exact(hip_device, wgran, igran):
+def test_wide_group_quantizers_bit_exact(hip_device, wgran, igran, dtype):
     """FP64 group maxima (column, row and 2-D groups, chunk-straddling groups) -> codes and
-    scales identical to the oracle's."""
+    scales identical to the oracle's, from FP64 operands and from FP32 ones (widened inside
+    the quantizers; 72 weight columns take the 16-byte loads of the column-group path)."""
     cfg = Config(activation_bits=16, weight_bits=4, input_slice=(1, 1, 2, 2, 2, 2, 2, 2, 2),
                  weight_slice=(1, 1, 2), bw_e=8, array_size=(64, 64), adc_bits=(6, 6, 7),
                  weight_quant_gran=wgran, input_quant_gran=igran)
     gen = torch.Generator().manual_seed(45)
-    a = torch.randn(9, 1500, generator=gen)
+    a = torch.randn(9, 1500, generator=gen).to(dtype)
     a[:, 700] = 50.0
-    b = torch.randn(1500, 70, generator=gen) * 0.02
+    b = (torch.randn(1500, 72, generator=gen) * 0.02).to(dtype)
     b[513, :] = -3.0
     q, xs = hip.input_tiles(a.to(hip_device), cfg)
     packed, _, ws = hip.weight_tiles(b.T.to(hip_device), cfg)
