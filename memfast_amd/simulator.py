@@ -754,14 +754,14 @@ class AnalogMatrix(nn.Module):
 
     def _host_max(self, name, tensor):
         """max |tensor| as a Python float, read from the device once per version of the
-        tensor (its storage, shape and in-place modification count)."""
-        key = (tensor.data_ptr(), tuple(tensor.shape), tensor._version)
+        tensor: the same tensor object (a replaced buffer may reuse the old one's storage)
+        with the same in-place modification count."""
         cache = self.__dict__.setdefault("_host_maxima", {})
         hit = cache.get(name)
-        if hit is None or hit[0] != key:
+        if hit is None or hit[0]() is not tensor or hit[1] != tensor._version:
             value = float(tensor.detach().abs().max()) if tensor.numel() else 0.0
-            hit = cache[name] = (key, value)
-        return hit[1]
+            hit = cache[name] = (weakref.ref(tensor), tensor._version, value)
+        return hit[2]
 
     def _output_bounded(self, arrays):
         """Whether the default-mode read of fixed-scale inputs cannot leave a non-finite
