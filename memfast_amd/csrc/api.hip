@@ -1079,7 +1079,8 @@ int mf_conv_input_tiles_wide(const mf_config *cfg, const double *x, const mf_con
                        gr, gc, ncg, work, status, u32(MF_STATUS_INPUT));
     const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
-                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
+                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale, HUGE_VAL,
+                       static_cast<u32 *>(nullptr));
     hipLaunchKernelGGL(k_conv_codes_f64, dim3(grid_for(rows * kp)), dim3(256), 0, s, x, g, K, kp,
                        scale, gr, gc, ncg, 0, lower, upper, mask, narrow, q, status,
                        u32(MF_STATUS_INPUT));
@@ -1983,6 +1984,20 @@ static void launch_group_max_f64(const S *x, i64 rows, i64 cols, i64 ld, i64 gr,
     }
 }
 
+// Largest group scale of a wide operand below which no read of G reads can leave an output
+// beyond FLT_MAX / 2 once cast to FP32: every read's slice total obeys
+// |T| <= sum|fa| * sum|fw| * adc_max (the ADC clamps each count), so with input and weight
+// scales below s the FP64 sum of G restores is at most G * Tmax * s^2 (times 1 + 2^-50 for
+// its roundings).  Scales above it flag MF_STATUS_RANGE (the caller then reads the status
+// word after the read instead of returning on the quantizers' bits).
+static double wide_scale_bound(const mf_config *cfg, i64 G) {
+    double fa = 0.0, fw = 0.0;
+    for (int a = 0; a < cfg->n_in; ++a) fa += std::fabs(double(cfg->in_factor[a]));
+    for (int w = 0; w < cfg->n_w; ++w)
+        fw += std::fabs(double(cfg->w_factor[w])) * double(cfg->adc_max[w]);
+    return std::sqrt(double(FLT_MAX) / (2.0 * double(G) * std::max(fa * fw, 1.0)));
+}
+
 // ---- wide configurations (u32 codes, FP64 scales and outputs) -------------
 // The wide quantizers over FP64 operands, or FP32 ones (S = float) widened exactly as they
 // are read, which gives the codes and scales of the FP64 copy without making it.
@@ -2009,7 +2024,8 @@ static int quantize_inputs_wide(const mf_config *cfg, const S *x, int64_t n, int
     launch_group_max_f64(x, n, k, ld, gr, gc, ncg, work, status, u32(MF_STATUS_INPUT), s);
     const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
-                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
+                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale,
+                       wide_scale_bound(cfg, ((k) + R - 1) / R * Gr), status);
     hipLaunchKernelGGL(k_input_codes_f64<S>, dim3(grid_for(n * kp)), dim3(256), 0, s, x, n, k, ld,
                        kp, scale, gr, gc, ncg, 0, lower, upper, mask, narrow, q);
     hipLaunchKernelGGL(k_input_scales_f64, dim3(grid_for(n * m * Gr)), dim3(256), 0, s, n, k,
@@ -2043,7 +2059,8 @@ static int quantize_weights_wide(const mf_config *cfg, const S *b, int64_t k, in
     launch_group_max_f64(b, k, o, ld, gr, gc, ncg, work, status, u32(MF_STATUS_WEIGHT), s);
     const int narrow = bits <= 8 && !cfg->bw_e;   // FP32 quantization, as the reference's
     hipLaunchKernelGGL(k_group_scale_f64, dim3(grid_for(nrg * ncg)), dim3(256), 0, s, work,
-                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale);
+                       nrg * ncg, bits, cfg->bw_e, upper, narrow, scale,
+                       wide_scale_bound(cfg, ((k) + R - 1) / R * Gr), status);
     hipLaunchKernelGGL(k_weight_codes_f64<S>, dim3(grid_for(kp * op)), dim3(256), 0, s, b, k, o,
                        ld, R, C, m, p, scale, gr, gc, ncg, lower, upper, mask, narrow, packed,
                        packed32);

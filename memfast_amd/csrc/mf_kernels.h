@@ -404,7 +404,7 @@ constexpr int ROW_CHUNK_COLS = 1024;  // columns per k_row_group_max wave
 // `narrow`: an INT operand of at most 8 bits in a wide configuration, quantized in FP32 as
 // the reference does (its dtype follows the operand's own width).
 __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
-                                  int narrow, double *scale);
+                                  int narrow, double *scale, double bound, u32 *status);
 template <typename S>
 __global__ void k_input_codes_f64(const S *x, i64 n, i64 k, i64 ld, i64 kp,
                                   const double *scale, i64 gr, i64 gc, i64 ncg, int fixed,

@@ -1243,8 +1243,10 @@ __device__ __forceinline__ int floor_log2_rounded(double x) {
 // `narrow`: an INT operand of at most 8 bits in a wide configuration, which the reference
 // quantizes in FP32 (memfast/quantization.py:9-31 picks the dtype per operand): the FP32
 // scale of the FP32 peak, stored exactly as a double.
+// A scale above `bound` sets MF_STATUS_RANGE in *status (may be null).
 __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_e, double upper,
-                                  int narrow, double *scale) {
+                                  int narrow, double *scale, double bound, u32 *status) {
+    bool large = false;
     for (i64 i = i64(blockIdx.x) * blockDim.x + threadIdx.x; i < groups;
          i += i64(gridDim.x) * blockDim.x) {
         const double peak = __longlong_as_double(static_cast<long long>(work[i]));
@@ -1262,7 +1264,9 @@ __global__ void k_group_scale_f64(const u64 *work, i64 groups, int bits, int bw_
             s = s < tiny ? tiny : s;
         }
         scale[i] = s;
+        large = large || s > bound;
     }
+    if (large && status) atomicOr(status, u32(MF_STATUS_RANGE));
 }
 
 // `narrow`: the FP32 code of the FP32 value and scale (see k_group_scale_f64).

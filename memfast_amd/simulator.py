@@ -339,6 +339,15 @@ class Simulator:
             packed, codes_t, wscale = tiles
             if not (config.wide or hip.mm_kernel(config, q.shape[0], q.shape[1], p)):
                 codes_t = None
+            # A wide read's quantizers flag STATUS_RANGE for group scales that could take the
+            # output past FLT_MAX / 2; without it their bits are all the read can leave, and
+            # they are published to the mailbox before the read runs.
+            box = None
+            if config.wide and x.dtype in (torch.float32, torch.float64):
+                if self._mailbox is None:
+                    self._mailbox = hip.mailbox()
+                box = self._mailbox
+                hip.status_publish(status, box)
             output = hip.mm(q, xscale, packed, codes_t, wscale.reshape(-1, p * config.array_size[1]),
                             config, config.seed ^ _name_tag(name), event,
                             variant=tuning.DEFAULT_VARIANT, status=status, out_cols=o, k_rows=k)
@@ -346,6 +355,8 @@ class Simulator:
                 # The cast to FP32 flags a non-finite result in the status word, so the one
                 # status read below also stands for the host scan of the cast output.
                 output = hip.narrow_output(output, o, status)
+            if box is not None and hip.status_wait(box) == 0:
+                return 0, tiles, q, xscale, output, kept, fused, event
         return int(status.item()), tiles, q, xscale, output, kept, fused, event
 
     def _launch_from_float(self, x, rhs, owner, index, status):

@@ -782,6 +782,48 @@ def test_wide_product_cast_flags_nonfinite_outputs(hip_device, name):
     assert narrow.dtype == torch.float32 and bits_equal(narrow, full.float())
 
 
+def test_wide_range_flag_and_early_status(hip_device, monkeypatch):
+    """Wide quantizers flag STATUS_RANGE for a group scale above
+    s = sqrt(FLT_MAX / (2 * G * Config.reconstruction_bound)) (G reads), the bound under
+    which the FP64 restore cast to FP32 stays below FLT_MAX / 2.  Without the flag, a wide
+    product returns on the quantizers' bits, published before the read: its outputs equal
+    the full status read's bit for bit; with it the product reads the device word and
+    raises FloatingPointError where the cast overflows."""
+    from memfast_amd import Simulator
+
+    cfg = wide_case("int12_ideal")
+    k = 150
+    G = -(-k // cfg.array_size[0]) * cfg.reads_per_array
+    s = math.sqrt(torch.finfo(torch.float32).max / (2 * G * cfg.reconstruction_bound))
+    upper = 2 ** (cfg.activation_bits - 1) - 1
+    for factor, flagged in ((0.99, False), (1.01, True)):
+        a = torch.zeros(3, k, device=hip_device)
+        a[:, 5] = s * factor * upper   # group scale = peak / upper
+        status = hip.status_word(hip_device)
+        hip.input_tiles(a, cfg, status=status)
+        assert bool(int(status.item()) & hip.STATUS_RANGE) == flagged, factor
+    gen = torch.Generator().manual_seed(49)
+    a = torch.randn(37, k, generator=gen).to(hip_device)
+    b = torch.randn(k, 70, generator=gen).to(hip_device)
+    seen = []
+    wait = hip.status_wait
+
+    def spy(box, timeout_s=10.0):
+        seen.append(wait(box, timeout_s))
+        return seen[-1]
+
+    monkeypatch.setattr(hip, "status_wait", spy)
+    early = Simulator(cfg, device=hip_device).mm(a, b)
+    assert seen == [0]
+    monkeypatch.setattr(hip, "status_wait", lambda box, timeout_s=10.0: None)
+    full = Simulator(cfg, device=hip_device).mm(a, b)
+    assert bits_equal(early, full)
+    monkeypatch.setattr(hip, "status_wait", spy)
+    with pytest.raises(FloatingPointError):
+        Simulator(cfg, device=hip_device).mm(a * 1e30, b * 1e30)
+    assert seen[-1] is not None and seen[-1] & hip.STATUS_RANGE
+
+
 @pytest.mark.parametrize("groups,width,c", [(5, 1, 4), (17, 2, 12), (128, 2, 128), (300, 1, 36),
                                             (40, 2, 4)])
 def test_stable_sum_matches_cpu_restore(hip_device, groups, width, c):
