@@ -48,9 +48,11 @@ enum {
     MF_STATUS_INPUT = 1,   /* non-finite activation value */
     MF_STATUS_WEIGHT = 2,  /* non-finite weight value */
     MF_STATUS_OUTPUT = 4,  /* non-finite FP32 output of mf_mm */
-    MF_STATUS_RANGE = 16   /* mf_mm_from_float: a group scale above the bound that keeps
-                            * every FP32 output finite; MF_STATUS_OUTPUT is then known
-                            * only once the read has finished */
+    MF_STATUS_RANGE = 16   /* mf_mm_from_float and the wide dynamic quantizers: a group
+                            * scale above the bound that keeps every FP32 output (for
+                            * wide reads, the FP32 cast of the FP64 output) finite;
+                            * MF_STATUS_OUTPUT is then known only once the read has
+                            * finished */
 };
 /* Set in a mailbox word (mf_mm_from_float) beside the status bits it carries. */
 #define MF_STATUS_PUBLISHED 0x80000000u
