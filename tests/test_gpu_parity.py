@@ -1792,6 +1792,16 @@ def test_bounded_fixed_scale_reads_publish_their_input_check(hip_device, monkeyp
         # bfloat16 widens to float32 exactly, so the float32 bits compare the bfloat16 bits.
         assert early.dtype == value.dtype and bits_equal(early.float(), full.float())
 
+    # float16 outputs keep the host scan of the cast: a bounded FP32 output past float16's
+    # range still raises.
+    layer = build(linear, AnalogLinear)
+    with torch.no_grad():
+        layer.bias.fill_(1e5)
+    assert layer._output_bounded(-(-300 // cfg.array_size[0]))
+    with pytest.raises(FloatingPointError):
+        layer(x.half())
+    assert layer._event == 0
+
     layer = build(linear, AnalogLinear)
     bad = x.clone()
     bad[4, 7] = float("inf")
